@@ -1,0 +1,224 @@
+"""Benchmark of the Prometheus hot path on one MI355X.
+
+A *step* is one launch of the fp32 MFMA SGEMM C = A @ B at 4096^3 (BASELINE.json
+configs[1], the configuration the headline metric is quoted on) with A, B
+already resident in HBM.  ``value`` is TFLOP/s from the wall clock around
+exactly ``--steps`` launches bracketed by device synchronisation;
+``roofline.achieved`` is from HIP events recorded on the reactor's own stream
+around the same launches.  Secondary figures (reductions in GB/s, the 1024^3
+case, bf16, GEMV) ride along under ``"secondary"``.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_BF16_MFMA_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def _timed_launches(rt, launch, steps: int, warmup: int):
+    """Returns (wall_ms_per_step, event_ms_per_step)."""
+    for _ in range(warmup):
+        launch()
+    rt.synchronize()
+    t0 = time.perf_counter()
+    rt.event_record(0)
+    for _ in range(steps):
+        launch()
+    rt.event_record(1)
+    rt.synchronize()
+    t1 = time.perf_counter()
+    ev = rt.event_elapsed_ms(0, 1)
+    return (t1 - t0) * 1e3 / steps, ev / steps
+
+
+def _traffic_from_profiles(name: str):
+    path = REPO / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline_sgemm(n: int, seconds: float):
+    """Oct's compiled CPU `@` (__octMatMulMM restatement, binary64 ijk, one thread) on a row sample."""
+    import oracle
+
+    a = oracle.uniform(11, (n, n)).astype(np.float64)
+    b = oracle.uniform(12, (n, n)).astype(np.float64)
+    rows = 0
+    t0 = time.perf_counter()
+    while rows < n:
+        oracle.matmul_compiled_f64(a, b, rows=(rows, rows + 1))
+        rows += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    flops = 2.0 * rows * n * n
+    return {
+        "value": round(flops / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"rows 0..{rows - 1} of the {n}^3 product ({rows}/{n} rows, {dt:.1f} s): "
+                  f"__octMatMulMM (emit_go_runtime.go:168-205) restated in C, binary64 ijk, 1 thread; "
+                  f"host has {os.cpu_count()} logical CPUs",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: this build runs every configuration on a single GPU "
+              "(no collectives); run it with --gpus 1", file=sys.stderr)
+        return 2
+
+    from oct_amd import prometheus as p
+    import oracle
+
+    rt = p.NativeRuntime()
+    rt.require_hardware_gpu()
+    diag = rt.device_diagnostics()
+
+    # ---- headline: fp32 SGEMM 4096^3 ------------------------------------------
+    n = 4096
+    a = oracle.uniform(11, (n, n))
+    b = oracle.uniform(12, (n, n))
+    da, db, dc = rt.alloc(a.nbytes), rt.alloc(b.nbytes), rt.alloc(a.nbytes)
+    rt.upload(da, a)
+    rt.upload(db, b)
+    wall_ms, ev_ms = _timed_launches(rt, lambda: rt.sgemm_device(da, db, dc, n, n, n), args.steps, args.warmup)
+    flops = 2.0 * n * n * n
+    value = flops / (wall_ms * 1e-3) / 1e12
+    achieved = flops / (ev_ms * 1e-3) / 1e12
+    line = {
+        "metric": "SGEMM fp32 TFLOP/s @4096^3 (% MFMA peak)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: A,B ~ U[-1,1] (SplitMix64/xoshiro256** seeds 11,12), fp32 row-major, resident in HBM",
+        "config": {"workload": "sgemm_f32 C=A@B M=N=K=4096 row-major (BASELINE configs[1])", "m": n, "n": n, "k": n,
+                   "kernel": "sgemm_f32_mfma_kernel (v_mfma_f32_32x32x2_f32, 128x128x16 tiles)"},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": _traffic_from_profiles("sgemm_f32_4096"),
+            "algorithmic_flop_per_launch": flops,
+            "event_ms_per_launch": round(ev_ms, 5),
+        },
+        "device": {"name": diag.device_name.decode(), "arch": diag.gcn_arch_name.decode(),
+                   "cus": diag.compute_units, "clock_mhz": diag.clock_khz // 1000},
+    }
+    # verify the measured output once (outside the timed region)
+    out_rows = rt.download(np.empty((n, n), np.float32), dc)
+    chk_rows = [0, 1777, n - 1]
+    errs = [oracle.normwise_rel_err(out_rows[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r]) for r in chk_rows]
+    line["parity_rows_normwise_max"] = float(max(errs))
+    for d in (da, db, dc):
+        rt.free(d)
+
+    if not args.no_secondary:
+        sec = {}
+        # fp32 1024^3
+        m1 = 1024
+        a1, b1 = oracle.uniform(1, (m1, m1)), oracle.uniform(2, (m1, m1))
+        d1 = [rt.alloc(a1.nbytes) for _ in range(3)]
+        rt.upload(d1[0], a1)
+        rt.upload(d1[1], b1)
+        _, ev = _timed_launches(rt, lambda: rt.sgemm_device(d1[0], d1[1], d1[2], m1, m1, m1), 50, 5)
+        sec["sgemm_f32_1024_tflops"] = round(2.0 * m1 ** 3 / (ev * 1e-3) / 1e12, 3)
+        for d in d1:
+            rt.free(d)
+        # ragged and GEMV
+        for (m, nn, k, key) in ((1000, 1000, 1000, "sgemm_f32_1000_tflops"),
+                                (4097, 3001, 513, "sgemm_f32_4097x3001x513_tflops")):
+            aa, bb = oracle.uniform(3, (m, k)), oracle.uniform(4, (k, nn))
+            dd = [rt.alloc(aa.nbytes), rt.alloc(bb.nbytes), rt.alloc(m * nn * 4)]
+            rt.upload(dd[0], aa)
+            rt.upload(dd[1], bb)
+            _, ev = _timed_launches(rt, lambda: rt.sgemm_device(dd[0], dd[1], dd[2], m, nn, k), 30, 5)
+            sec[key] = round(2.0 * m * nn * k / (ev * 1e-3) / 1e12, 3)
+            for d in dd:
+                rt.free(d)
+        m, k = 8192, 4096
+        aa, xx = oracle.uniform(7, (m, k)), oracle.uniform(8, (k, 1))
+        dd = [rt.alloc(aa.nbytes), rt.alloc(xx.nbytes), rt.alloc(m * 4)]
+        rt.upload(dd[0], aa)
+        rt.upload(dd[1], xx)
+        _, ev = _timed_launches(rt, lambda: rt.sgemm_device(dd[0], dd[1], dd[2], m, 1, k), 100, 10)
+        sec["gemv_f32_8192x4096_gbs"] = round((m * k + k + m) * 4 / (ev * 1e-3) / 1e9, 1)
+        for d in dd:
+            rt.free(d)
+        # bf16 4096^3
+        ab, bbf = oracle.to_bf16(oracle.uniform(41, (n, n))), oracle.to_bf16(oracle.uniform(42, (n, n)))
+        dd = [rt.alloc(ab.nbytes), rt.alloc(bbf.nbytes), rt.alloc(n * n * 4)]
+        rt.upload(dd[0], ab)
+        rt.upload(dd[1], bbf)
+        _, ev = _timed_launches(rt, lambda: rt.gemm_bf16_device(dd[0], dd[1], dd[2], n, n, n), 30, 5)
+        tf = flops / (ev * 1e-3) / 1e12
+        sec["gemm_bf16_4096_tflops"] = round(tf, 2)
+        sec["gemm_bf16_4096_frac"] = round(tf / PEAK_BF16_MFMA_TFLOPS, 4)
+        for d in dd:
+            rt.free(d)
+        # reductions on [8192, 4096]
+        rows, width = 8192, 4096
+        x = oracle.normal(77, (rows, width))
+        dx, dy = rt.alloc(x.nbytes), rt.alloc(x.nbytes)
+        rt.upload(dx, x)
+        for op, name, nbytes in ((p.OP_SOFTMAX, "softmax", 2 * x.nbytes), (p.OP_SUM, "row_sum", x.nbytes + rows * 4),
+                                 (p.OP_MAX, "row_max", x.nbytes + rows * 4)):
+            _, ev = _timed_launches(rt, lambda: rt.reduction_device(dx, dy, rows, width, op), 100, 10)
+            gbs = nbytes / (ev * 1e-3) / 1e9
+            sec[f"{name}_8192x4096_gbs"] = round(gbs, 1)
+            sec[f"{name}_8192x4096_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+        w = (1.0 + oracle.normal(89, (width,), 0.0, 0.02)).astype(np.float32)
+        dw, dinv = rt.alloc(w.nbytes), rt.alloc(rows * 4)
+        rt.upload(dw, w)
+        _, ev = _timed_launches(rt, lambda: rt.rmsnorm_device(dx, dw, dy, dinv, rows, width, width, 1e-6), 100, 10)
+        gbs = (2 * x.nbytes + w.nbytes + rows * 4) / (ev * 1e-3) / 1e9
+        sec["rmsnorm_8192x4096_gbs"] = round(gbs, 1)
+        sec["rmsnorm_8192x4096_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+        for d in (dx, dy, dw, dinv):
+            rt.free(d)
+        line["secondary"] = sec
+
+    rt.close()
+    line["cpu_baseline"] = cpu_baseline_sgemm(n, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

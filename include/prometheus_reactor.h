@@ -1,0 +1,536 @@
+/*
+ * prometheus_reactor.h -- C ABI of the MI355X (gfx950) Prometheus reactor.
+ *
+ * A drop-in for the subset of Oct's `libprometheus_reactor.so` that the
+ * north-star hot path uses: runtime lifecycle, FP32 SGEMM (the `@` operator
+ * inside PROMETHEUS { }), row reductions (sum / max / stable softmax) and
+ * RMSNorm.  Struct layouts, enum values and status conventions of those entry
+ * points are kept identical to the reference so an unmodified Go loader binds
+ * this library.  Entry points the reference does not have (bf16 GEMM,
+ * generic RMSNorm, device-resident variants, transformer blocks) follow the
+ * same conventions and are marked NEW.
+ *
+ * Conventions (reference: internal/prometheus/native/reactor_api.h:55-83,227-324):
+ *   return PROM_OK / PROM_ERROR / PROM_INVALID_HANDLE / PROM_INTERNAL_ERROR;
+ *   out_stage reports the phase reached (TRANSFER_OUT on success);
+ *   out_detail is a positive path code on success, negative on failure.
+ *   Host-pointer entry points are synchronous: inputs are copied in, the
+ *   result copied out before return; outputs are written only on success.
+ */
+#ifndef OCT_AMD_PROMETHEUS_REACTOR_H
+#define OCT_AMD_PROMETHEUS_REACTOR_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define PROM_REACTOR_API __attribute__((visibility("default")))
+#else
+#define PROM_REACTOR_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* reactor_api.h:22-25 */
+enum { PROM_REACTOR_ABI_V1 = 1u };
+
+/* reactor_api.h:55-60 */
+enum { PROM_OK = 0, PROM_ERROR = 1, PROM_INVALID_HANDLE = 2, PROM_INTERNAL_ERROR = 3 };
+
+/* reactor_api.h:62-67.  Value 2 is "hardware GPU" to the Go loader
+   (internal/prometheus/fft.go:50-55 requires it); this library reports 2 on a
+   HIP device and exposes the real device via ..._hip_device_diagnostics. */
+enum {
+  PROM_BACKEND_UNKNOWN = 0,
+  PROM_BACKEND_STUB = 1,
+  PROM_BACKEND_VULKAN = 2,
+  PROM_BACKEND_HARDWARE_GPU = 2,
+  PROM_BACKEND_VULKAN_SOFTWARE = 3,
+};
+
+/* reactor_api.h:69-73 */
+enum { PROM_REASON_NONE = 0, PROM_REASON_STUB_UNAVAILABLE = 1, PROM_REASON_VULKAN_UNAVAILABLE = 2 };
+
+/* reactor_api.h:76-83 */
+enum {
+  PROM_STAGE_NONE = 0,
+  PROM_STAGE_INIT = 1,
+  PROM_STAGE_TRANSFER_IN = 2,
+  PROM_STAGE_SUBMIT = 3,
+  PROM_STAGE_TRANSFER_OUT = 4,
+  PROM_STAGE_CLEANUP = 5,
+};
+
+/* reactor_api.h:131-166 (the fault-injection bits this library honours). */
+enum {
+  PROM_TESTCFG_FAIL_DEVICE_CREATE = 1u << 0,
+  PROM_TESTCFG_FAIL_BUFFER_ALLOC = 1u << 2,
+  PROM_TESTCFG_FAIL_UPLOAD = 1u << 3,
+  PROM_TESTCFG_FAIL_DISPATCH = 1u << 4,
+  PROM_TESTCFG_FAIL_DOWNLOAD = 1u << 5,
+  PROM_TESTCFG_SKIP_VULKAN_INIT = 1u << 7,
+};
+
+/* reactor_api.h:227-324 (subset) */
+enum {
+  PROM_DETAIL_INJECTED_UPLOAD_FAILURE = -6001,
+  PROM_DETAIL_INJECTED_DISPATCH_FAILURE = -6002,
+  PROM_DETAIL_INJECTED_DOWNLOAD_FAILURE = -6003,
+  PROM_DETAIL_SIZE_OVERFLOW = -6004,
+  PROM_DETAIL_PATH_DIRECT = 6101,
+  /* NEW success path codes (no Vulkan counterpart). */
+  PROM_DETAIL_PATH_HIP_MFMA_F32 = 6120,
+  PROM_DETAIL_PATH_HIP_GEMV_F32 = 6121,
+  PROM_DETAIL_PATH_HIP_MFMA_BF16 = 6122,
+  PROM_DETAIL_PATH_HIP_SIMT_F32 = 6123,
+  /* NEW failure detail codes. */
+  PROM_DETAIL_HIP_ALLOC_FAILED = -6901,
+  PROM_DETAIL_HIP_COPY_FAILED = -6902,
+  PROM_DETAIL_HIP_LAUNCH_FAILED = -6903,
+  PROM_DETAIL_HIP_SYNC_FAILED = -6904,
+  PROM_DETAIL_HIP_UNAVAILABLE = -6905,
+  PROM_DETAIL_INVALID_ARGUMENT = -6906,
+};
+
+/* reactor_api.h:386-390 */
+enum {
+  PROM_REDUCTION_OPERATION_SUM = 1u,
+  PROM_REDUCTION_OPERATION_MAX = 2u,
+  PROM_REDUCTION_OPERATION_SOFTMAX = 3u,
+};
+/* reactor_api.h:392-395 */
+enum { PROM_REDUCTION_FINALIZATION_NONE = 0u, PROM_REDUCTION_FINALIZATION_STABLE_SOFTMAX = 1u };
+/* reactor_api.h:397-402 */
+enum {
+  PROM_REDUCTION_STRATEGY_AUTO = 0u,
+  PROM_REDUCTION_STRATEGY_FUSED_SINGLE_WORKGROUP = 1u,
+  PROM_REDUCTION_STRATEGY_COMPOSED = 2u,
+  PROM_REDUCTION_STRATEGY_PACKED_SHORT_ROWS = 3u,
+};
+/* reactor_api.h:404-412 */
+enum {
+  PROM_REDUCTION_STAGE_ROW_SUM = 1u,
+  PROM_REDUCTION_STAGE_ROW_MAX = 2u,
+  PROM_REDUCTION_STAGE_SOFTMAX_EXP_SUM = 3u,
+  PROM_REDUCTION_STAGE_SOFTMAX_NORMALIZE = 4u,
+  PROM_REDUCTION_STAGE_SOFTMAX_FUSED = 5u,
+  PROM_REDUCTION_STAGE_ROW_SUM_PACKED_SHORT = 6u,
+  PROM_REDUCTION_STAGE_SOFTMAX_PACKED_SHORT = 7u,
+};
+/* reactor_api.h:414-419 */
+enum {
+  PROM_REDUCTION_TEMPORARY_NONE = 0u,
+  PROM_REDUCTION_TEMPORARY_PARTIALS = 1u,
+  PROM_REDUCTION_TEMPORARY_ROW_MAX = 2u,
+  PROM_REDUCTION_TEMPORARY_ROW_SUM = 3u,
+};
+/* reactor_api.h:421-424 */
+enum { PROM_REDUCTION_FLAG_FORCE_FUSED = 1u << 0u, PROM_REDUCTION_FLAG_FORCE_COMPOSED = 1u << 1u };
+
+/* reactor_api.h:426-452 */
+enum {
+  PROM_REDUCTION_DETAIL_INVALID_REQUEST = -6801,
+  PROM_REDUCTION_DETAIL_NULL_INPUT = -6802,
+  PROM_REDUCTION_DETAIL_NULL_OUTPUT = -6803,
+  PROM_REDUCTION_DETAIL_ZERO_ROW_COUNT = -6804,
+  PROM_REDUCTION_DETAIL_ZERO_ROW_WIDTH = -6805,
+  PROM_REDUCTION_DETAIL_UNSUPPORTED_OPERATION = -6806,
+  PROM_REDUCTION_DETAIL_INVALID_FINALIZATION = -6807,
+  PROM_REDUCTION_DETAIL_SIZE_OVERFLOW = -6808,
+  PROM_REDUCTION_DETAIL_INPUT_SIZE_MISMATCH = -6809,
+  PROM_REDUCTION_DETAIL_OUTPUT_SIZE_MISMATCH = -6810,
+  PROM_REDUCTION_DETAIL_ROW_LIMIT = -6811,
+  PROM_REDUCTION_DETAIL_WIDTH_LIMIT = -6812,
+  PROM_REDUCTION_DETAIL_ELEMENT_LIMIT = -6813,
+  PROM_REDUCTION_DETAIL_NONFINITE_INPUT = -6814,
+  PROM_REDUCTION_DETAIL_UNSUPPORTED_STRATEGY = -6815,
+  PROM_REDUCTION_DETAIL_MALFORMED_PLAN = -6816,
+  PROM_REDUCTION_DETAIL_TEMPORARY_UNDERSIZED = -6817,
+  PROM_REDUCTION_DETAIL_RESOURCE_CREATE_FAILED = -6818,
+  PROM_REDUCTION_DETAIL_PIPELINE_CREATE_FAILED = -6819,
+  PROM_REDUCTION_DETAIL_COMMAND_RECORD_FAILED = -6820,
+  PROM_REDUCTION_DETAIL_QUEUE_SUBMIT_FAILED = -6821,
+  PROM_REDUCTION_DETAIL_COMPLETION_UNCERTAIN = -6822,
+  PROM_REDUCTION_DETAIL_QUERY_FAILED = -6823,
+  PROM_REDUCTION_DETAIL_READBACK_FAILED = -6824,
+  PROM_REDUCTION_DETAIL_RUNTIME_UNAVAILABLE = -6825,
+};
+
+/* reactor_api.h:456-470 */
+enum {
+  PROM_SOFTMAX_DETAIL_INVALID_REQUEST = -6851,
+  PROM_SOFTMAX_DETAIL_NULL_INPUT = -6852,
+  PROM_SOFTMAX_DETAIL_NULL_OUTPUT = -6853,
+  PROM_SOFTMAX_DETAIL_COUNT_MISMATCH = -6854,
+  PROM_SOFTMAX_DETAIL_SIZE_OVERFLOW = -6855,
+  PROM_SOFTMAX_DETAIL_ROW_LIMIT = -6856,
+  PROM_SOFTMAX_DETAIL_WIDTH_LIMIT = -6857,
+  PROM_SOFTMAX_DETAIL_ELEMENT_LIMIT = -6858,
+  PROM_SOFTMAX_DETAIL_PARTIAL_ALIAS = -6859,
+  PROM_SOFTMAX_DETAIL_NONFINITE_INPUT = -6860,
+  PROM_SOFTMAX_DETAIL_RUNTIME_UNAVAILABLE = -6861,
+  PROM_SOFTMAX_DETAIL_SUBGROUP_UNSUPPORTED = -6862,
+  PROM_SOFTMAX_DETAIL_TOPOLOGY_UNSUPPORTED = -6863,
+};
+
+/* reactor_api.h:472-490 (plan vocabulary; kept so plans serialise identically) */
+enum {
+  PROM_REDUCTION_SHADER_ROW_SUM = 16u,
+  PROM_REDUCTION_SHADER_ROW_MAX = 17u,
+  PROM_REDUCTION_SHADER_SOFTMAX_EXP_SUM = 18u,
+  PROM_REDUCTION_SHADER_SOFTMAX_NORMALIZE = 19u,
+  PROM_REDUCTION_SHADER_SOFTMAX_FUSED = 20u,
+  PROM_REDUCTION_SHADER_ROW_SUM_PACKED_SHORT = 21u,
+  PROM_REDUCTION_SHADER_SOFTMAX_PACKED_SHORT = 22u,
+};
+enum {
+  PROM_REDUCTION_IMPLEMENTATION_ROW_SUM = 1001u,
+  PROM_REDUCTION_IMPLEMENTATION_ROW_MAX = 1002u,
+  PROM_REDUCTION_IMPLEMENTATION_SOFTMAX_EXP_SUM = 1003u,
+  PROM_REDUCTION_IMPLEMENTATION_SOFTMAX_NORMALIZE = 1004u,
+  PROM_REDUCTION_IMPLEMENTATION_SOFTMAX_FUSED = 1005u,
+  PROM_REDUCTION_IMPLEMENTATION_ROW_SUM_PACKED_SHORT = 1006u,
+  PROM_REDUCTION_IMPLEMENTATION_SOFTMAX_PACKED_SHORT = 1007u,
+};
+
+/* reactor_api.h:492-510 -- the reference admission envelope.  The reference
+   entry points (..._reduction, ..._reduction_plan, ..._row_wise_softmax) keep
+   it unchanged; the NEW ..._reduction_v2 admits the lifted envelope below. */
+#define PROM_REDUCTION_MAX_STAGES 8u
+#define PROM_REDUCTION_MAX_ROWS 1024u
+#define PROM_REDUCTION_MAX_ELEMENTS_PER_ROW 1048576u
+#define PROM_REDUCTION_MAX_TOTAL_ELEMENTS 16777216u
+#define PROM_REDUCTION_LOCAL_SIZE 256u
+#define PROM_REDUCTION_ELEMENTS_PER_PARTIAL 1024u
+#define PROM_REDUCTION_SINGLE_STAGE_THRESHOLD 1024u
+#define PROM_REDUCTION_FORCE_FUSED_MAX_ELEMENTS_PER_ROW 1056u
+#define PROM_REDUCTION_PACKED_SHORT_WIDTH_MAX 128u
+#define PROM_REDUCTION_PACKED_SHORT_SUM_MIN_ROWS 512u
+#define PROM_REDUCTION_PACKED_SHORT_SUM_WIDE_MIN_ROWS 1024u
+#define PROM_REDUCTION_PACKED_SHORT_ROWS_PER_GROUP 8u
+#define PROM_REDUCTION_PACKED_SHORT_LANES_PER_ROW 32u
+#define PROM_ROW_WISE_SOFTMAX_MAX_ROWS PROM_REDUCTION_MAX_ROWS
+#define PROM_ROW_WISE_SOFTMAX_MAX_ELEMENTS_PER_ROW PROM_REDUCTION_FORCE_FUSED_MAX_ELEMENTS_PER_ROW
+#define PROM_ROW_WISE_SOFTMAX_MAX_TOTAL_ELEMENTS PROM_REDUCTION_MAX_TOTAL_ELEMENTS
+
+/* NEW: lifted envelope of ..._reduction_v2 (rows fit uint32; 4 Gi elements = 16 GiB
+   of fp32, well inside one MI355X's 288 GB). */
+#define PROM_REDUCTION_V2_MAX_ROWS 0xFFFFFFFFu
+#define PROM_REDUCTION_V2_MAX_ELEMENTS_PER_ROW 1048576u
+#define PROM_REDUCTION_V2_MAX_TOTAL_ELEMENTS 4294967296ull
+
+/* reactor_api.h:512-539 */
+typedef struct PrometheusRowWiseSoftmaxRequest {
+  uint32_t struct_size;
+  const float* input;
+  float* output;
+  uint32_t row_count;
+  uint32_t elements_per_row;
+  uint64_t input_element_count;
+  uint64_t output_element_count;
+} PrometheusRowWiseSoftmaxRequest;
+
+typedef struct PrometheusRowWiseSoftmaxResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint32_t output_written;
+  uint32_t physical_dispatch_count;
+  uint32_t physical_submission_count;
+  uint32_t gpu_timestamp_valid;
+  uint64_t gpu_duration_ns;
+  uint64_t end_to_end_ns;
+  uint64_t first_nonfinite_index;
+} PrometheusRowWiseSoftmaxResult;
+
+/* reactor_api.h:541-552 */
+typedef struct PrometheusReductionRequest {
+  uint32_t struct_size;
+  const float* input;
+  float* output;
+  uint32_t row_count;
+  uint32_t elements_per_row;
+  uint64_t input_element_count;
+  uint64_t output_element_count;
+  uint32_t operation;
+  uint32_t finalization;
+  uint32_t flags;
+} PrometheusReductionRequest;
+
+/* reactor_api.h:554-565 */
+typedef struct PrometheusReductionStageDispatch {
+  uint32_t stage_role;
+  uint32_t shader_id;
+  uint32_t implementation_id;
+  uint32_t groups_x;
+  uint32_t groups_y;
+  uint32_t groups_z;
+  uint32_t input_elements_per_row;
+  uint32_t output_partials_per_row;
+  uint32_t temporary_role;
+  uint64_t temporary_bytes_written;
+} PrometheusReductionStageDispatch;
+
+/* reactor_api.h:567-581 */
+typedef struct PrometheusReductionPlan {
+  uint32_t struct_size;
+  uint32_t operation;
+  uint32_t row_count;
+  uint32_t elements_per_row;
+  uint32_t strategy;
+  uint32_t local_size;
+  uint32_t elements_per_partial;
+  uint32_t partial_count;
+  uint32_t stage_count;
+  uint32_t temporary_alignment_bytes;
+  uint64_t temporary_bytes;
+  uint64_t replay_id;
+  PrometheusReductionStageDispatch stages[PROM_REDUCTION_MAX_STAGES];
+} PrometheusReductionPlan;
+
+/* reactor_api.h:583-598 */
+typedef struct PrometheusReductionExecutionResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint64_t logical_request_id;
+  uint32_t physical_slot_id;
+  uint32_t physical_slot_generation;
+  uint32_t physical_slot_recyclable;
+  uint32_t gpu_timestamp_valid;
+  uint64_t gpu_duration_ns;
+  uint64_t end_to_end_ns;
+  uint64_t first_nonfinite_index;
+  uint32_t validation_error_count_before;
+  uint32_t validation_error_count_after;
+  PrometheusReductionPlan plan;
+} PrometheusReductionExecutionResult;
+
+/* reactor_api.h:1582-1586 */
+typedef struct PrometheusCaps {
+  uint32_t available;
+  uint32_t backend_type;
+  uint32_t reason_code;
+} PrometheusCaps;
+
+/* reactor_api.h:1596-1606 (filled from the HIP device; api_version = HIP runtime version). */
+typedef struct PrometheusVulkanDeviceDiagnostics {
+  char device_name[256];
+  uint32_t vendor_id;
+  uint32_t device_id;
+  uint32_t device_type;
+  uint32_t driver_version;
+  uint32_t api_version;
+  uint32_t software_vulkan;
+  uint32_t compute_queue_family;
+  uint32_t transfer_queue_family;
+} PrometheusVulkanDeviceDiagnostics;
+
+/* reactor_api.h:1751-1769.  struct_size gates the tail field. */
+typedef struct PrometheusReactorConfig {
+  uint32_t struct_size;
+  uint32_t test_flags;
+  uint32_t p15_shadow_disabled;
+  uint32_t async_test_flags;
+  uint32_t batch_ring_depth;
+  uint32_t reduction_test_flags;
+  uint32_t reduction_ring_depth;
+  const char* shader_package_root;
+} PrometheusReactorConfig;
+
+/* reactor_api.h:1781-1825 */
+typedef struct PrometheusGemma4E2BM1InputRmsNormRequest {
+  uint32_t struct_size;
+  const float* input;
+  const float* weight;
+  float* output;
+  float* inv_rms_output;
+  uint64_t input_element_count;
+  uint64_t weight_element_count;
+  uint64_t output_element_count;
+  uint64_t inv_rms_output_element_count;
+  uint32_t tokens;
+  uint32_t model_width;
+  uint32_t input_row_stride;
+  float epsilon;
+  uint64_t input_generation;
+  uint64_t weight_generation;
+  uint64_t exact_source_hash;
+} PrometheusGemma4E2BM1InputRmsNormRequest;
+
+typedef struct PrometheusGemma4E2BM1InputRmsNormResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint32_t output_written;
+  uint32_t matched_input;
+  uint64_t input_hash;
+  uint64_t weight_hash;
+  uint64_t output_hash;
+  uint64_t inv_rms_hash;
+  uint32_t submit_count;
+  uint32_t final_readback_count;
+  uint32_t no_product_intermediate_readback_change;
+  uint32_t reserved0;
+  uint64_t retained_bytes;
+  uint64_t buffer_allocation_count;
+  uint64_t buffer_reuse_count;
+  uint64_t descriptor_update_count;
+  uint64_t pipeline_create_count;
+  uint64_t command_buffer_reuse_count;
+  uint64_t reduction_gpu_ns;
+  uint64_t final_reduction_gpu_ns;
+  uint64_t inv_rms_gpu_ns;
+  uint64_t apply_gpu_ns;
+  uint64_t end_to_end_ns;
+} PrometheusGemma4E2BM1InputRmsNormResult;
+
+/* RMSNorm detail codes: internal/prometheus/native/reactor_vulkan.h:1870-1888 (subset).
+   The Gemma entry keeps the reference's admission envelope
+   (tokens <= 1024, width <= 4096: reactor_vulkan.h:10-11); the generic
+   ..._rmsnorm entry lifts it. */
+enum {
+  PROM_M46_DETAIL_INVALID_REQUEST = -7401,
+  PROM_M46_DETAIL_SHAPE = -7403,
+  PROM_M46_DETAIL_STRIDE = -7404,
+  PROM_M46_DETAIL_EPSILON = -7407,
+  PROM_M46_DETAIL_SIZE_OVERFLOW = -7409,
+  PROM_M46_DETAIL_NONFINITE_INPUT = -7418,
+};
+#define PROM_M42_MAX_TOKENS 1024u
+#define PROM_M42_MAX_MODEL_WIDTH 4096u
+
+/* NEW: generic RMSNorm request (no generation/hash bookkeeping). */
+typedef struct PrometheusRmsNormRequest {
+  uint32_t struct_size;
+  const float* input;     /* [tokens, input_row_stride] */
+  const float* weight;    /* [width] */
+  float* output;          /* [tokens, width] */
+  float* inv_rms_output;  /* [tokens], may be NULL */
+  uint32_t tokens;
+  uint32_t width;
+  uint32_t input_row_stride;
+  float epsilon;
+} PrometheusRmsNormRequest;
+
+typedef struct PrometheusRmsNormResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint32_t output_written;
+  uint64_t gpu_duration_ns;
+  uint64_t end_to_end_ns;
+} PrometheusRmsNormResult;
+
+/* ------------------------------------------------------------------------ */
+/* Reference entry points (reactor_api.h:2557-2699)                          */
+/* ------------------------------------------------------------------------ */
+
+/* reactor_api.h:2557 -- returns PROM_REACTOR_ABI_V1. */
+PROM_REACTOR_API uint32_t prometheus_reactor_abi_version(void);
+/* reactor_api.h:2558 -- config may be NULL (defaults). */
+PROM_REACTOR_API int prometheus_reactor_runtime_create(void* config, void** out_handle);
+/* reactor_api.h:2559 -- second destroy of a handle returns PROM_INVALID_HANDLE. */
+PROM_REACTOR_API int prometheus_reactor_runtime_destroy(void* handle);
+/* reactor_api.h:2560 -- available=1, backend 2 on a HIP device; else
+   available=0, backend UNKNOWN, reason VULKAN_UNAVAILABLE (no device). */
+PROM_REACTOR_API int prometheus_reactor_runtime_probe(void* handle, PrometheusCaps* out_caps);
+/* reactor_api.h:2561-2562 */
+PROM_REACTOR_API int prometheus_reactor_runtime_vulkan_device_diagnostics(void* handle,
+                                                                           PrometheusVulkanDeviceDiagnostics* out_diag);
+/* reactor_api.h:2587-2595 -- C[m,n] = A[m,k] @ B[k,n], row-major fp32,
+   synchronous, host pointers.  Validation order and codes follow
+   reactor_sgemm.cpp:4152-4191 (invalid handle -> INIT/PROM_INVALID_HANDLE;
+   NULL operand -> TRANSFER_IN/PROM_ERROR; zero dimension -> INIT/PROM_ERROR;
+   no device -> INIT).  The reference rejects m*n*k >= 2^32 with
+   PROM_DETAIL_SIZE_OVERFLOW, which excludes 4096^3; here the limit is that
+   each of m*k, k*n and m*n is below 2^32 elements (16 GiB of fp32). */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm(void* handle, const float* a, const float* b, float* c,
+                                                      uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
+                                                      int* out_detail_code);
+/* reactor_api.h:2671-2672 -- reference planner, reference envelope. */
+PROM_REACTOR_API int prometheus_reactor_reduction_plan(const PrometheusReductionRequest* request,
+                                                        PrometheusReductionPlan* out_plan);
+/* reactor_api.h:2673-2675 -- reference envelope (rows <= 1024, total <= 2^24). */
+PROM_REACTOR_API int prometheus_reactor_runtime_reduction(void* handle, const PrometheusReductionRequest* request,
+                                                          PrometheusReductionExecutionResult* out_result);
+/* reactor_api.h:2682-2685 -- rows <= 1024, width <= 1056, exact in-place allowed. */
+PROM_REACTOR_API int prometheus_reactor_runtime_row_wise_softmax(void* handle,
+                                                                 const PrometheusRowWiseSoftmaxRequest* request,
+                                                                 PrometheusRowWiseSoftmaxResult* out_result);
+/* reactor_api.h:2686-2689; reactor_api.c:250-359 */
+PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm(
+    void* handle, const PrometheusGemma4E2BM1InputRmsNormRequest* request,
+    PrometheusGemma4E2BM1InputRmsNormResult* out_result);
+
+/* ------------------------------------------------------------------------ */
+/* NEW entry points (same conventions; no reference counterpart)             */
+/* ------------------------------------------------------------------------ */
+
+/* HIP device identity: name, gfx arch, CU count, clock, HBM bytes. */
+typedef struct PrometheusHipDeviceDiagnostics {
+  uint32_t struct_size;
+  char device_name[256];
+  char gcn_arch_name[64];
+  uint32_t compute_units;
+  uint32_t clock_khz;
+  uint32_t memory_clock_khz;
+  uint32_t memory_bus_width;
+  uint64_t total_global_mem;
+  uint32_t lds_bytes_per_workgroup;
+  uint32_t wavefront_size;
+  int32_t hip_runtime_version;
+  int32_t device_ordinal;
+} PrometheusHipDeviceDiagnostics;
+PROM_REACTOR_API int prometheus_reactor_runtime_hip_device_diagnostics(void* handle,
+                                                                        PrometheusHipDeviceDiagnostics* out_diag);
+
+/* The reduction entry of the reference with the admission envelope lifted to
+   PROM_REDUCTION_V2_* (C3's [8192, 4096] does not fit the reference's). */
+PROM_REACTOR_API int prometheus_reactor_runtime_reduction_v2(void* handle, const PrometheusReductionRequest* request,
+                                                             PrometheusReductionExecutionResult* out_result);
+/* Generic RMSNorm: y = x * rsqrt(mean(x^2) + eps) * w, inv_rms optional. */
+PROM_REACTOR_API int prometheus_reactor_runtime_rmsnorm(void* handle, const PrometheusRmsNormRequest* request,
+                                                        PrometheusRmsNormResult* out_result);
+/* bf16 GEMM: A[m,k], B[k,n] as bf16 bit patterns (uint16), C fp32, row-major,
+   fp32 accumulate; synchronous, host pointers. */
+PROM_REACTOR_API int prometheus_reactor_runtime_gemm_bf16(void* handle, const uint16_t* a, const uint16_t* b, float* c,
+                                                          uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
+                                                          int* out_detail_code);
+
+/* Device-resident operation.  Buffers come from ..._device_alloc (or any
+   device pointer of the same HIP device); work is queued on the runtime's
+   single stream and these calls return without waiting. */
+PROM_REACTOR_API int prometheus_reactor_runtime_device_alloc(void* handle, uint64_t bytes, void** out_device_ptr);
+PROM_REACTOR_API int prometheus_reactor_runtime_device_free(void* handle, void* device_ptr);
+PROM_REACTOR_API int prometheus_reactor_runtime_device_upload(void* handle, void* device_dst, const void* host_src,
+                                                              uint64_t bytes);
+PROM_REACTOR_API int prometheus_reactor_runtime_device_download(void* handle, void* host_dst, const void* device_src,
+                                                                uint64_t bytes);
+PROM_REACTOR_API int prometheus_reactor_runtime_synchronize(void* handle);
+/* Event timing on the runtime stream: record into one of 64 slots; elapsed
+   waits for the end event. */
+PROM_REACTOR_API int prometheus_reactor_runtime_event_record(void* handle, uint32_t slot);
+PROM_REACTOR_API int prometheus_reactor_runtime_event_elapsed_ms(void* handle, uint32_t start_slot, uint32_t end_slot,
+                                                                 float* out_ms);
+
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device(void* handle, const float* a, const float* b, float* c,
+                                                             uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
+                                                             int* out_detail_code);
+PROM_REACTOR_API int prometheus_reactor_runtime_gemm_bf16_device(void* handle, const uint16_t* a, const uint16_t* b,
+                                                                 float* c, uint32_t m, uint32_t n, uint32_t k,
+                                                                 uint32_t* out_stage, int* out_detail_code);
+/* operation as PrometheusReductionRequest; softmax writes rows*width, sum/max rows. */
+PROM_REACTOR_API int prometheus_reactor_runtime_reduction_device(void* handle, const float* input, float* output,
+                                                                 uint32_t rows, uint32_t width, uint32_t operation,
+                                                                 uint32_t* out_stage, int* out_detail_code);
+PROM_REACTOR_API int prometheus_reactor_runtime_rmsnorm_device(void* handle, const float* input, const float* weight,
+                                                               float* output, float* inv_rms, uint32_t tokens,
+                                                               uint32_t width, uint32_t input_row_stride, float epsilon,
+                                                               uint32_t* out_stage, int* out_detail_code);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

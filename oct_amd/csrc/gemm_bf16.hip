@@ -1,0 +1,203 @@
+// bf16 GEMM with fp32 accumulate on CDNA4 MFMA (v_mfma_f32_32x32x16_bf16).
+//
+// C[m,n] (fp32) = A[m,k] (bf16) @ B[k,n] (bf16), row-major.  The reference has
+// no bf16 GEMM (its closest is fp16 storage / fp32 accumulate,
+// internal/prometheus/shaders/sdslv/production/sgemm/sgemm_fp16_storage_fp32_accum.sdslv);
+// the bf16 bit patterns and their fp32 widening follow
+// internal/prometheus/gemma4e2b_m1_rtx.go:1005-1014.
+//
+//   * workgroup = 4 wave64, macro tile 128x128, K tile 64, LDS double-buffered;
+//   * each wave owns 64x64 = 2x2 MFMA 32x32x16 blocks;
+//   * MFMA operands want 8 consecutive k per lane, so A is stored [m][k] and
+//     B is transposed into [n][k] on the way into LDS (pairs of k packed into
+//     one 32-bit LDS store); operand reads are 128-bit;
+//   * exact tails by zero-filled loads and masked stores; the 128-bit global
+//     path needs k % 8 == 0 and n % 8 == 0, other shapes use 16-bit loads.
+#include "reactor_internal.h"
+
+namespace prom {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 64;
+constexpr int kLds = kBK + 8;  // row pitch in bf16 elements (144 bytes, 16-byte aligned)
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int num_tiles = tiles_m * tiles_n;
+  int pid = (int)blockIdx.x;
+  if ((num_tiles & 7) == 0) pid = (pid & 7) * (num_tiles >> 3) + (pid >> 3);
+  const int per_group = kGroupM * tiles_n;
+  const int group = pid / per_group;
+  const int first_m = group * kGroupM;
+  const int group_m = min(tiles_m - first_m, kGroupM);
+  const int in_group = pid - group * per_group;
+  *tm = first_m + in_group % group_m;
+  *tn = in_group / group_m;
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_mfma_kernel(const uint16_t* __restrict__ A,
+                                                                const uint16_t* __restrict__ B,
+                                                                float* __restrict__ C, int M, int N, int K,
+                                                                int tiles_m, int tiles_n) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM][kLds];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kBN][kLds];
+
+  int tm, tn;
+  map_tile(tiles_m, tiles_n, &tm, &tn);
+  const int row0 = tm * kBM;
+  const int col0 = tn * kBN;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+
+  // A: thread -> (row = tid/2, 32 consecutive k starting at (tid%2)*32): 4 x 16 bytes.
+  const int a_row = tid >> 1;
+  const int a_k = (tid & 1) * 32;
+  // B: unit u in {tid, tid+256}: k pair = u/16 (0..31), 8 consecutive n at (u%16)*8.
+  u32x4 ra[4];
+  u32x4 rb[4];  // [unit][row of pair]
+
+  auto load_tile = [&](int k0) {
+    const int gr = row0 + a_row;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int gk = k0 + a_k + 8 * h;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if constexpr (kVec) {
+        if (gr < M && gk < K) v = *reinterpret_cast<const u32x4*>(A + (size_t)gr * K + gk);
+      } else {
+        uint16_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = (gr < M && gk + j < K) ? A[(size_t)gr * K + gk + j] : (uint16_t)0;
+        v.x = (uint32_t)e[0] | ((uint32_t)e[1] << 16);
+        v.y = (uint32_t)e[2] | ((uint32_t)e[3] << 16);
+        v.z = (uint32_t)e[4] | ((uint32_t)e[5] << 16);
+        v.w = (uint32_t)e[6] | ((uint32_t)e[7] << 16);
+      }
+      ra[h] = v;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int unit = tid + 256 * u;
+      const int kp = unit >> 4;
+      const int gn = col0 + (unit & 15) * 8;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int gk = k0 + 2 * kp + p;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if constexpr (kVec) {
+          if (gk < K && gn < N) v = *reinterpret_cast<const u32x4*>(B + (size_t)gk * N + gn);
+        } else {
+          uint16_t e[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) e[j] = (gk < K && gn + j < N) ? B[(size_t)gk * N + gn + j] : (uint16_t)0;
+          v.x = (uint32_t)e[0] | ((uint32_t)e[1] << 16);
+          v.y = (uint32_t)e[2] | ((uint32_t)e[3] << 16);
+          v.z = (uint32_t)e[4] | ((uint32_t)e[5] << 16);
+          v.w = (uint32_t)e[6] | ((uint32_t)e[7] << 16);
+        }
+        rb[2 * u + p] = v;
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) *reinterpret_cast<u32x4*>(&As[buf][a_row][a_k + 8 * h]) = ra[h];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int unit = tid + 256 * u;
+      const int kp = unit >> 4;
+      const int n0 = (unit & 15) * 8;
+      const u32x4 lo = rb[2 * u + 0];  // row k = 2kp
+      const u32x4 hi = rb[2 * u + 1];  // row k = 2kp + 1
+      const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
+      const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // element n0+2j: low halves; element n0+2j+1: high halves
+        const uint32_t even = (lw[j] & 0xFFFFu) | (hw[j] << 16);
+        const uint32_t odd = (lw[j] >> 16) | (hw[j] & 0xFFFF0000u);
+        *reinterpret_cast<uint32_t*>(&Bs[buf][n0 + 2 * j][2 * kp]) = even;
+        *reinterpret_cast<uint32_t*>(&Bs[buf][n0 + 2 * j + 1][2 * kp]) = odd;
+      }
+    }
+  };
+
+  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+  const int k_tiles = (K + kBK - 1) / kBK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int lrow = lane & 31;
+  const int lk = (lane >> 5) * 8;
+  const int am = wm * 64 + lrow;
+  const int bn = wn * 64 + lrow;
+
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < k_tiles;
+    if (more) load_tile((kt + 1) * kBK);
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s) {
+      const int kc = 16 * s + lk;
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(&As[cur][am][kc]);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(&As[cur][am + 32][kc]);
+      const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(&Bs[cur][bn][kc]);
+      const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(&Bs[cur][bn + 32][kc]);
+      acc00 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc00, 0, 0, 0);
+      acc01 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc01, 0, 0, 0);
+      acc10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc10, 0, 0, 0);
+      acc11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc11, 0, 0, 0);
+    }
+    if (more) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  const int lgrp = (lane >> 5) * 4;
+  auto store_block = [&](const floatx16& acc, int mi, int ni) {
+    const int col = col0 + wn * 64 + ni * 32 + lrow;
+    if (col >= N) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + wm * 64 + mi * 32 + 8 * (r >> 2) + lgrp + (r & 3);
+      if (row < M) C[(size_t)row * N + col] = acc[r];
+    }
+  };
+  store_block(acc00, 0, 0);
+  store_block(acc01, 0, 1);
+  store_block(acc10, 1, 0);
+  store_block(acc11, 1, 1);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                            hipStream_t stream, int* path_detail) {
+  const int tiles_m = (int)((m + kBM - 1) / kBM);
+  const int tiles_n = (int)((n + kBN - 1) / kBN);
+  const dim3 grid((unsigned)(tiles_m * tiles_n));
+  const bool vec = (k % 8 == 0) && (n % 8 == 0) && aligned16(a) && aligned16(b);
+  if (vec)
+    hipLaunchKernelGGL(gemm_bf16_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
+                       tiles_m, tiles_n);
+  else
+    hipLaunchKernelGGL(gemm_bf16_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
+                       tiles_m, tiles_n);
+  if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_BF16;
+  return hipGetLastError();
+}
+
+}  // namespace prom

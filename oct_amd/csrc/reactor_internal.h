@@ -1,0 +1,71 @@
+// Internal declarations shared by the reactor's translation units.
+//
+// One process-wide device context owns the HIP device, a single stream on
+// which every launch is queued, grow-only staging buffers for host-pointer
+// calls and a ring of timing events.  Runtime handles are cheap records in a
+// registry (the reference keeps a global handle registry too:
+// internal/prometheus/native/reactor_sgemm.cpp:1370-1565).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+
+#include "../../include/prometheus_reactor.h"
+
+namespace prom {
+
+constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
+constexpr uint32_t kEventSlots = 64;
+constexpr uint32_t kStagingSlots = 4;
+
+struct Runtime {
+  uint64_t magic;
+  uint32_t test_flags;
+  uint32_t reduction_test_flags;
+  uint32_t available;       // 1 when a HIP device is usable by this handle
+  int32_t init_detail;      // reason when unavailable
+  uint64_t requests;
+  uint64_t successes;
+};
+
+struct DeviceContext {
+  std::mutex mu;            // serialises host-pointer calls and staging reuse
+  bool probed = false;
+  bool available = false;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t events[kEventSlots] = {};
+  hipEvent_t op_begin = nullptr, op_end = nullptr;
+  void* staging[kStagingSlots] = {};
+  size_t staging_bytes[kStagingSlots] = {};
+  hipDeviceProp_t props{};
+};
+
+DeviceContext& ctx();
+// Initialises the device context once; returns true when a device is usable.
+bool ensure_device();
+// Validates a handle against the registry; returns nullptr when invalid.
+Runtime* lookup(void* handle);
+// Grow-only device staging buffer `slot` of at least `bytes`.
+void* staging(uint32_t slot, size_t bytes);
+
+inline void set_status(uint32_t* stage, int* detail, uint32_t s, int d) {
+  if (stage) *stage = s;
+  if (detail) *detail = d;
+}
+
+uint64_t wall_ns();
+
+// ---- kernel launchers (enqueue on `stream`; return hipSuccess or the launch error)
+hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                            hipStream_t stream, int* path_detail);
+hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                            hipStream_t stream, int* path_detail);
+hipError_t launch_row_reduction(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,
+                                hipStream_t stream);
+hipError_t launch_rmsnorm(const float* in, const float* w, float* out, float* inv_rms, uint32_t tokens,
+                          uint32_t width, uint32_t stride, float eps, hipStream_t stream);
+
+}  // namespace prom

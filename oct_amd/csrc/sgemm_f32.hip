@@ -1,0 +1,248 @@
+// FP32 SGEMM on CDNA4 MFMA (v_mfma_f32_32x32x2_f32) and the HBM-bound GEMV.
+//
+// Computes C[m,n] = A[m,k] @ B[k,n], row-major fp32: the arithmetic of Oct's
+// `@` inside PROMETHEUS { } (internal/prometheus/runtime.go:298-331, C ABI
+// internal/prometheus/native/reactor_api.h:2587-2595).  The reference's
+// Vulkan kernels (e.g. sgemm_reg2x2_tile16x16_exacttail_fp32.sdslv:49-190)
+// are FMA loops on 8x8 threads; this is a different design built for the
+// matrix cores:
+//
+//   * workgroup = 256 threads = 4 wave64, macro tile 128x128, K tile 16;
+//     each wave owns a 64x64 sub-tile = 2x2 MFMA 32x32 blocks (64 fp32
+//     accumulators per lane);
+//   * A and B are staged through LDS, double-buffered: the next K tile is
+//     fetched into registers while the current one feeds the MFMAs, then
+//     written to the other LDS buffer; one barrier per K tile;
+//   * A is transposed on its way into LDS (k-major) so that every MFMA
+//     operand read is 32 consecutive floats per half-wave;
+//   * exact tails: out-of-range rows/columns/k are zero-filled on load and
+//     masked on store, no host padding.  Shapes whose k and n are multiples
+//     of 4 use 128-bit global loads; others use predicated 32-bit loads;
+//   * workgroup -> tile mapping is XCD-aware: hardware deals workgroups to
+//     the 8 XCDs round-robin, so consecutive ids are remapped to contiguous
+//     chunks of a grouped (GROUP_M) tile order, keeping each XCD's L2 on a
+//     compact block of A rows and B columns.
+#include "reactor_internal.h"
+
+namespace prom {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 16;
+constexpr int kLdsA = kBM + 2;  // k-major A rows; +2 keeps the transposing stores conflict-free
+constexpr int kLdsB = kBN + 4;  // k-major B rows; multiple of 4 for 128-bit stores
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int num_tiles = tiles_m * tiles_n;
+  int pid = (int)blockIdx.x;
+  if ((num_tiles & 7) == 0) pid = (pid & 7) * (num_tiles >> 3) + (pid >> 3);
+  const int per_group = kGroupM * tiles_n;
+  const int group = pid / per_group;
+  const int first_m = group * kGroupM;
+  const int group_m = min(tiles_m - first_m, kGroupM);
+  const int in_group = pid - group * per_group;
+  *tm = first_m + in_group % group_m;
+  *tn = in_group / group_m;
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __restrict__ A,
+                                                                const float* __restrict__ B,
+                                                                float* __restrict__ C, int M, int N, int K,
+                                                                int tiles_m, int tiles_n) {
+  __shared__ float As[2][kBK][kLdsA];
+  __shared__ float Bs[2][kBK][kLdsB];
+
+  int tm, tn;
+  map_tile(tiles_m, tiles_n, &tm, &tn);
+  const int row0 = tm * kBM;
+  const int col0 = tn * kBN;
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+
+  // Global->register assignment: A: one row, 8 consecutive k; B: two k rows, 4 consecutive n.
+  const int a_row = tid >> 1;
+  const int a_k = (tid & 1) * 8;
+  const int b_k = tid >> 5;
+  const int b_n = (tid & 31) * 4;
+
+  float ra[8];
+  float rb[8];
+
+  auto load_tile = [&](int k0) {
+    const int gr = row0 + a_row;
+    const int gn = col0 + b_n;
+    if constexpr (kVec) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int gk = k0 + a_k + 4 * h;
+        floatx4 v = {0.f, 0.f, 0.f, 0.f};
+        if (gr < M && gk < K) v = *reinterpret_cast<const floatx4*>(A + (size_t)gr * K + gk);
+        ra[4 * h + 0] = v.x;
+        ra[4 * h + 1] = v.y;
+        ra[4 * h + 2] = v.z;
+        ra[4 * h + 3] = v.w;
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int gk = k0 + b_k + 8 * h;
+        floatx4 v = {0.f, 0.f, 0.f, 0.f};
+        if (gk < K && gn < N) v = *reinterpret_cast<const floatx4*>(B + (size_t)gk * N + gn);
+        rb[4 * h + 0] = v.x;
+        rb[4 * h + 1] = v.y;
+        rb[4 * h + 2] = v.z;
+        rb[4 * h + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int gk = k0 + a_k + j;
+        ra[j] = (gr < M && gk < K) ? A[(size_t)gr * K + gk] : 0.f;
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int gk = k0 + b_k + 8 * h;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          rb[4 * h + j] = (gk < K && gn + j < N) ? B[(size_t)gk * N + gn + j] : 0.f;
+        }
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) As[buf][a_k + j][a_row] = ra[j];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      floatx4 v = {rb[4 * h + 0], rb[4 * h + 1], rb[4 * h + 2], rb[4 * h + 3]};
+      *reinterpret_cast<floatx4*>(&Bs[buf][b_k + 8 * h][b_n]) = v;
+    }
+  };
+
+  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+
+  const int k_tiles = (K + kBK - 1) / kBK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int lrow = lane & 31;
+  const int lk = lane >> 5;
+  const int am = wm * 64 + lrow;
+  const int bn = wn * 64 + lrow;
+
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < k_tiles;
+    if (more) load_tile((kt + 1) * kBK);
+#pragma unroll
+    for (int s = 0; s < kBK / 2; ++s) {
+      const int kr = 2 * s + lk;
+      const float a0 = As[cur][kr][am];
+      const float a1 = As[cur][kr][am + 32];
+      const float b0 = Bs[cur][kr][bn];
+      const float b1 = Bs[cur][kr][bn + 32];
+      acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc00, 0, 0, 0);
+      acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc01, 0, 0, 0);
+      acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc10, 0, 0, 0);
+      acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc11, 0, 0, 0);
+    }
+    if (more) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Accumulator layout of a 32x32 MFMA block: lane l, register r holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  auto store_block = [&](const floatx16& acc, int mi, int ni) {
+    const int col = col0 + wn * 64 + ni * 32 + lrow;
+    if (col >= N) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+      if (row < M) C[(size_t)row * N + col] = acc[r];
+    }
+  };
+  store_block(acc00, 0, 0);
+  store_block(acc01, 0, 1);
+  store_block(acc10, 1, 0);
+  store_block(acc11, 1, 1);
+}
+
+// y[m] = A[m,:] . x : one wave per row, 4 rows per workgroup.  HBM-bound:
+// every byte of A is read once with 128-bit loads, x stays in L2.
+template <bool kVec>
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ A, const float* __restrict__ x,
+                                                       float* __restrict__ y, int M, int K) {
+  const int wave = (int)(threadIdx.x >> 6);
+  const int lane = (int)(threadIdx.x & 63);
+  const int row = (int)blockIdx.x * 4 + wave;
+  if (row >= M) return;
+  const float* a = A + (size_t)row * K;
+  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+  if constexpr (kVec) {
+    const int k4 = K >> 2;
+    const floatx4* a4 = reinterpret_cast<const floatx4*>(a);
+    const floatx4* x4 = reinterpret_cast<const floatx4*>(x);
+    int i = lane;
+    for (; i + 192 < k4; i += 256) {
+      const floatx4 p0 = a4[i], p1 = a4[i + 64], p2 = a4[i + 128], p3 = a4[i + 192];
+      const floatx4 q0 = x4[i], q1 = x4[i + 64], q2 = x4[i + 128], q3 = x4[i + 192];
+      acc0 += p0.x * q0.x + p0.y * q0.y + p0.z * q0.z + p0.w * q0.w;
+      acc1 += p1.x * q1.x + p1.y * q1.y + p1.z * q1.z + p1.w * q1.w;
+      acc2 += p2.x * q2.x + p2.y * q2.y + p2.z * q2.z + p2.w * q2.w;
+      acc3 += p3.x * q3.x + p3.y * q3.y + p3.z * q3.z + p3.w * q3.w;
+    }
+    for (; i < k4; i += 64) {
+      const floatx4 p = a4[i], q = x4[i];
+      acc0 += p.x * q.x + p.y * q.y + p.z * q.z + p.w * q.w;
+    }
+  } else {
+    for (int i = lane; i < K; i += 64) acc0 += a[i] * x[i];
+  }
+  float acc = (acc0 + acc1) + (acc2 + acc3);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) y[row] = acc;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                            hipStream_t stream, int* path_detail) {
+  if (n == 1) {
+    const bool vec = (k % 4 == 0) && aligned16(a) && aligned16(b);
+    const dim3 grid((m + 3) / 4);
+    if (vec)
+      hipLaunchKernelGGL(gemv_f32_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)k);
+    else
+      hipLaunchKernelGGL(gemv_f32_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)k);
+    if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_GEMV_F32;
+    return hipGetLastError();
+  }
+  const int tiles_m = (int)((m + kBM - 1) / kBM);
+  const int tiles_n = (int)((n + kBN - 1) / kBN);
+  const dim3 grid((unsigned)(tiles_m * tiles_n));
+  const bool vec = (k % 4 == 0) && (n % 4 == 0) && aligned16(a) && aligned16(b);
+  if (vec)
+    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
+                       tiles_m, tiles_n);
+  else
+    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
+                       tiles_m, tiles_n);
+  if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_F32;
+  return hipGetLastError();
+}
+
+}  // namespace prom

@@ -1,0 +1,660 @@
+"""Host-side bridge to the MI355X Prometheus reactor.
+
+This module mirrors the reference's Go bridge (``internal/prometheus``) over the
+same C ABI, using ``ctypes``: library discovery (``bridge.go:552-601``), ABI
+check / create / probe (``bridge.go:276-394``), ``nativeRuntime.SGEMM``
+(``bridge.go:410-436``), status mapping (``status.go``, ``bridge.go:535-550``)
+and the strict ``@`` path that never substitutes the CPU
+(``strict.go:11-32``).  The Go toolchain is absent from this image, so the
+host side is Python; ``INTEGRATION.md`` shows the cgo binding a maintainer adds.
+
+Everything here calls the HIP library.  There is no CPU fallback: a missing
+library or device raises :class:`ReactorIssue`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, Structure, byref, c_char, c_float, c_int, c_uint16, c_uint32, c_uint64, c_void_p
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+
+REACTOR_ENV_VAR = "OCT_PROMETHEUS_REACTOR"
+REACTOR_TEST_FLAGS_ENV_VAR = "OCT_PROMETHEUS_REACTOR_TEST_FLAGS"
+REACTOR_EXPECTED_ABI_VERSION = 1
+LIBRARY_BASENAME = "libprometheus_reactor.so"
+PACKAGE_DIR = Path(__file__).resolve().parent
+
+# ---- ABI constants (include/prometheus_reactor.h) --------------------------
+PROM_OK, PROM_ERROR, PROM_INVALID_HANDLE, PROM_INTERNAL_ERROR = 0, 1, 2, 3
+PROM_BACKEND_UNKNOWN, PROM_BACKEND_STUB, PROM_BACKEND_HARDWARE_GPU, PROM_BACKEND_SOFTWARE = 0, 1, 2, 3
+PROM_REASON_NONE, PROM_REASON_STUB_UNAVAILABLE, PROM_REASON_VULKAN_UNAVAILABLE = 0, 1, 2
+STAGE_NONE, STAGE_INIT, STAGE_TRANSFER_IN, STAGE_SUBMIT, STAGE_TRANSFER_OUT, STAGE_CLEANUP = range(6)
+OP_SUM, OP_MAX, OP_SOFTMAX = 1, 2, 3
+FINALIZATION_NONE, FINALIZATION_STABLE_SOFTMAX = 0, 1
+FLAG_FORCE_FUSED, FLAG_FORCE_COMPOSED = 1, 2
+TESTCFG_FAIL_DEVICE_CREATE = 1 << 0
+TESTCFG_FAIL_BUFFER_ALLOC = 1 << 2
+TESTCFG_FAIL_UPLOAD = 1 << 3
+TESTCFG_FAIL_DISPATCH = 1 << 4
+TESTCFG_FAIL_DOWNLOAD = 1 << 5
+TESTCFG_SKIP_VULKAN_INIT = 1 << 7
+DETAIL_INJECTED_UPLOAD_FAILURE = -6001
+DETAIL_INJECTED_DISPATCH_FAILURE = -6002
+DETAIL_INJECTED_DOWNLOAD_FAILURE = -6003
+DETAIL_SIZE_OVERFLOW = -6004
+DETAIL_PATH_HIP_MFMA_F32 = 6120
+DETAIL_PATH_HIP_GEMV_F32 = 6121
+DETAIL_PATH_HIP_MFMA_BF16 = 6122
+DETAIL_HIP_UNAVAILABLE = -6905
+
+
+# ---- ABI structs -----------------------------------------------------------
+class PrometheusCaps(Structure):
+    _fields_ = [("available", c_uint32), ("backend_type", c_uint32), ("reason_code", c_uint32)]
+
+
+class PrometheusReactorConfig(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("test_flags", c_uint32),
+        ("p15_shadow_disabled", c_uint32),
+        ("async_test_flags", c_uint32),
+        ("batch_ring_depth", c_uint32),
+        ("reduction_test_flags", c_uint32),
+        ("reduction_ring_depth", c_uint32),
+        ("shader_package_root", ctypes.c_char_p),
+    ]
+
+
+class PrometheusVulkanDeviceDiagnostics(Structure):
+    _fields_ = [
+        ("device_name", c_char * 256),
+        ("vendor_id", c_uint32),
+        ("device_id", c_uint32),
+        ("device_type", c_uint32),
+        ("driver_version", c_uint32),
+        ("api_version", c_uint32),
+        ("software_vulkan", c_uint32),
+        ("compute_queue_family", c_uint32),
+        ("transfer_queue_family", c_uint32),
+    ]
+
+
+class PrometheusHipDeviceDiagnostics(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("device_name", c_char * 256),
+        ("gcn_arch_name", c_char * 64),
+        ("compute_units", c_uint32),
+        ("clock_khz", c_uint32),
+        ("memory_clock_khz", c_uint32),
+        ("memory_bus_width", c_uint32),
+        ("total_global_mem", c_uint64),
+        ("lds_bytes_per_workgroup", c_uint32),
+        ("wavefront_size", c_uint32),
+        ("hip_runtime_version", ctypes.c_int32),
+        ("device_ordinal", ctypes.c_int32),
+    ]
+
+
+class PrometheusReductionRequest(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("input", c_void_p),
+        ("output", c_void_p),
+        ("row_count", c_uint32),
+        ("elements_per_row", c_uint32),
+        ("input_element_count", c_uint64),
+        ("output_element_count", c_uint64),
+        ("operation", c_uint32),
+        ("finalization", c_uint32),
+        ("flags", c_uint32),
+    ]
+
+
+class PrometheusReductionStageDispatch(Structure):
+    _fields_ = [
+        ("stage_role", c_uint32),
+        ("shader_id", c_uint32),
+        ("implementation_id", c_uint32),
+        ("groups_x", c_uint32),
+        ("groups_y", c_uint32),
+        ("groups_z", c_uint32),
+        ("input_elements_per_row", c_uint32),
+        ("output_partials_per_row", c_uint32),
+        ("temporary_role", c_uint32),
+        ("temporary_bytes_written", c_uint64),
+    ]
+
+
+class PrometheusReductionPlan(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("operation", c_uint32),
+        ("row_count", c_uint32),
+        ("elements_per_row", c_uint32),
+        ("strategy", c_uint32),
+        ("local_size", c_uint32),
+        ("elements_per_partial", c_uint32),
+        ("partial_count", c_uint32),
+        ("stage_count", c_uint32),
+        ("temporary_alignment_bytes", c_uint32),
+        ("temporary_bytes", c_uint64),
+        ("replay_id", c_uint64),
+        ("stages", PrometheusReductionStageDispatch * 8),
+    ]
+
+
+class PrometheusReductionExecutionResult(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("stage", c_uint32),
+        ("detail_code", ctypes.c_int32),
+        ("logical_request_id", c_uint64),
+        ("physical_slot_id", c_uint32),
+        ("physical_slot_generation", c_uint32),
+        ("physical_slot_recyclable", c_uint32),
+        ("gpu_timestamp_valid", c_uint32),
+        ("gpu_duration_ns", c_uint64),
+        ("end_to_end_ns", c_uint64),
+        ("first_nonfinite_index", c_uint64),
+        ("validation_error_count_before", c_uint32),
+        ("validation_error_count_after", c_uint32),
+        ("plan", PrometheusReductionPlan),
+    ]
+
+
+class PrometheusRowWiseSoftmaxRequest(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("input", c_void_p),
+        ("output", c_void_p),
+        ("row_count", c_uint32),
+        ("elements_per_row", c_uint32),
+        ("input_element_count", c_uint64),
+        ("output_element_count", c_uint64),
+    ]
+
+
+class PrometheusRowWiseSoftmaxResult(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("stage", c_uint32),
+        ("detail_code", ctypes.c_int32),
+        ("output_written", c_uint32),
+        ("physical_dispatch_count", c_uint32),
+        ("physical_submission_count", c_uint32),
+        ("gpu_timestamp_valid", c_uint32),
+        ("gpu_duration_ns", c_uint64),
+        ("end_to_end_ns", c_uint64),
+        ("first_nonfinite_index", c_uint64),
+    ]
+
+
+class PrometheusGemma4E2BM1InputRmsNormRequest(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("input", c_void_p),
+        ("weight", c_void_p),
+        ("output", c_void_p),
+        ("inv_rms_output", c_void_p),
+        ("input_element_count", c_uint64),
+        ("weight_element_count", c_uint64),
+        ("output_element_count", c_uint64),
+        ("inv_rms_output_element_count", c_uint64),
+        ("tokens", c_uint32),
+        ("model_width", c_uint32),
+        ("input_row_stride", c_uint32),
+        ("epsilon", c_float),
+        ("input_generation", c_uint64),
+        ("weight_generation", c_uint64),
+        ("exact_source_hash", c_uint64),
+    ]
+
+
+class PrometheusGemma4E2BM1InputRmsNormResult(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("stage", c_uint32),
+        ("detail_code", ctypes.c_int32),
+        ("output_written", c_uint32),
+        ("matched_input", c_uint32),
+        ("input_hash", c_uint64),
+        ("weight_hash", c_uint64),
+        ("output_hash", c_uint64),
+        ("inv_rms_hash", c_uint64),
+        ("submit_count", c_uint32),
+        ("final_readback_count", c_uint32),
+        ("no_product_intermediate_readback_change", c_uint32),
+        ("reserved0", c_uint32),
+        ("retained_bytes", c_uint64),
+        ("buffer_allocation_count", c_uint64),
+        ("buffer_reuse_count", c_uint64),
+        ("descriptor_update_count", c_uint64),
+        ("pipeline_create_count", c_uint64),
+        ("command_buffer_reuse_count", c_uint64),
+        ("reduction_gpu_ns", c_uint64),
+        ("final_reduction_gpu_ns", c_uint64),
+        ("inv_rms_gpu_ns", c_uint64),
+        ("apply_gpu_ns", c_uint64),
+        ("end_to_end_ns", c_uint64),
+    ]
+
+
+class PrometheusRmsNormRequest(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("input", c_void_p),
+        ("weight", c_void_p),
+        ("output", c_void_p),
+        ("inv_rms_output", c_void_p),
+        ("tokens", c_uint32),
+        ("width", c_uint32),
+        ("input_row_stride", c_uint32),
+        ("epsilon", c_float),
+    ]
+
+
+class PrometheusRmsNormResult(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("stage", c_uint32),
+        ("detail_code", ctypes.c_int32),
+        ("output_written", c_uint32),
+        ("gpu_duration_ns", c_uint64),
+        ("end_to_end_ns", c_uint64),
+    ]
+
+
+# ---- errors and status (status.go, bridge.go) ------------------------------
+class ReactorIssue(RuntimeError):
+    """Structured reactor failure (reference ``ReactorIssue``, bridge.go:33-66)."""
+
+    def __init__(self, code: str, message: str):
+        super().__init__(f"{code}: {message}")
+        self.code = code
+
+
+def stage_name(stage: int) -> str:
+    """bridge.go:535-550 (stageFromNativeCode)."""
+    return {1: "init", 2: "transfer_in", 3: "submit", 4: "transfer_out", 5: "cleanup"}.get(stage, "unknown")
+
+
+@dataclass
+class RunStatus:
+    """status.go:30-59."""
+
+    kind: str
+    error_stage: str = ""
+    error_code: int = 0
+    fallback_reason: str = ""
+
+    def __str__(self) -> str:
+        if self.kind == "ok":
+            return "ok"
+        if self.kind == "fallback":
+            return f"fallback({self.fallback_reason})"
+        return f"error({self.error_stage},{self.error_code})"
+
+
+@dataclass
+class CallStatus:
+    stage: int
+    detail: int
+
+
+# ---- library loading --------------------------------------------------------
+_SIGNATURES = {
+    "prometheus_reactor_abi_version": (c_uint32, []),
+    "prometheus_reactor_runtime_create": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "prometheus_reactor_runtime_destroy": (c_int, [c_void_p]),
+    "prometheus_reactor_runtime_probe": (c_int, [c_void_p, POINTER(PrometheusCaps)]),
+    "prometheus_reactor_runtime_vulkan_device_diagnostics": (c_int, [c_void_p, POINTER(PrometheusVulkanDeviceDiagnostics)]),
+    "prometheus_reactor_runtime_hip_device_diagnostics": (c_int, [c_void_p, POINTER(PrometheusHipDeviceDiagnostics)]),
+    "prometheus_reactor_runtime_sgemm": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_sgemm_device": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_gemm_bf16": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_gemm_bf16_device": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_reduction_plan": (
+        c_int, [POINTER(PrometheusReductionRequest), POINTER(PrometheusReductionPlan)]),
+    "prometheus_reactor_runtime_reduction": (
+        c_int, [c_void_p, POINTER(PrometheusReductionRequest), POINTER(PrometheusReductionExecutionResult)]),
+    "prometheus_reactor_runtime_reduction_v2": (
+        c_int, [c_void_p, POINTER(PrometheusReductionRequest), POINTER(PrometheusReductionExecutionResult)]),
+    "prometheus_reactor_runtime_reduction_device": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_row_wise_softmax": (
+        c_int, [c_void_p, POINTER(PrometheusRowWiseSoftmaxRequest), POINTER(PrometheusRowWiseSoftmaxResult)]),
+    "prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm": (
+        c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1InputRmsNormRequest),
+                POINTER(PrometheusGemma4E2BM1InputRmsNormResult)]),
+    "prometheus_reactor_runtime_rmsnorm": (
+        c_int, [c_void_p, POINTER(PrometheusRmsNormRequest), POINTER(PrometheusRmsNormResult)]),
+    "prometheus_reactor_runtime_rmsnorm_device": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_float,
+                POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_device_alloc": (c_int, [c_void_p, c_uint64, POINTER(c_void_p)]),
+    "prometheus_reactor_runtime_device_free": (c_int, [c_void_p, c_void_p]),
+    "prometheus_reactor_runtime_device_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64]),
+    "prometheus_reactor_runtime_device_download": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64]),
+    "prometheus_reactor_runtime_synchronize": (c_int, [c_void_p]),
+    "prometheus_reactor_runtime_event_record": (c_int, [c_void_p, c_uint32]),
+    "prometheus_reactor_runtime_event_elapsed_ms": (c_int, [c_void_p, c_uint32, c_uint32, POINTER(c_float)]),
+}
+
+MANDATORY_SYMBOLS = (
+    "prometheus_reactor_abi_version",
+    "prometheus_reactor_runtime_create",
+    "prometheus_reactor_runtime_destroy",
+    "prometheus_reactor_runtime_probe",
+    "prometheus_reactor_runtime_sgemm",
+)
+
+
+def discover_reactor_candidates() -> list:
+    """bridge.go:552-582: $OCT_PROMETHEUS_REACTOR wins; else the package's build."""
+    explicit = os.environ.get(REACTOR_ENV_VAR, "")
+    if explicit:
+        return [explicit]
+    return [str(PACKAGE_DIR / LIBRARY_BASENAME)]
+
+
+def load_library(path: Optional[str] = None) -> ctypes.CDLL:
+    """dlopen the reactor and bind every known symbol (bridge.go:276-340)."""
+    candidates = [path] if path else discover_reactor_candidates()
+    last_err = None
+    for cand in candidates:
+        if not Path(cand).exists():
+            last_err = f"{cand} not found"
+            continue
+        try:
+            lib = ctypes.CDLL(cand, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        except OSError as exc:
+            last_err = str(exc)
+            continue
+        for name in MANDATORY_SYMBOLS:
+            if not hasattr(lib, name):
+                raise ReactorIssue("symbol_missing", f"{name} missing from {cand}")
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            if hasattr(lib, name):
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+        version = lib.prometheus_reactor_abi_version()
+        if version != REACTOR_EXPECTED_ABI_VERSION:
+            raise ReactorIssue("abi_mismatch", f"expected ABI {REACTOR_EXPECTED_ABI_VERSION}, got {version}")
+        lib._oct_path = cand  # type: ignore[attr-defined]
+        return lib
+    raise ReactorIssue("library_unavailable", last_err or "no reactor candidates")
+
+
+_SHARED_LIB: Optional[ctypes.CDLL] = None
+
+
+def shared_library() -> ctypes.CDLL:
+    global _SHARED_LIB
+    if _SHARED_LIB is None:
+        _SHARED_LIB = load_library()
+    return _SHARED_LIB
+
+
+def _ptr(arr: Optional[np.ndarray]) -> Optional[int]:
+    return None if arr is None else arr.ctypes.data
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+class NativeRuntime:
+    """A reactor runtime handle (reference ``nativeRuntime``, bridge.go:238-516).
+
+    Unlike the reference's strict path, which opens a private runtime per call,
+    a process-wide device context is shared by every handle; creating one is cheap.
+    """
+
+    def __init__(self, lib: Optional[ctypes.CDLL] = None, test_flags: Optional[int] = None,
+                 reduction_test_flags: int = 0):
+        self.lib = lib or shared_library()
+        if test_flags is None:
+            env = os.environ.get(REACTOR_TEST_FLAGS_ENV_VAR, "")
+            test_flags = int(env, 0) if env else 0
+        cfg = PrometheusReactorConfig()
+        cfg.struct_size = ctypes.sizeof(cfg)
+        cfg.test_flags = test_flags
+        cfg.reduction_test_flags = reduction_test_flags
+        handle = c_void_p()
+        rc = self.lib.prometheus_reactor_runtime_create(byref(cfg), byref(handle))
+        if rc != PROM_OK or not handle.value:
+            raise ReactorIssue("create_failed", f"runtime_create returned {rc}")
+        self.handle = handle
+        caps = PrometheusCaps()
+        rc = self.lib.prometheus_reactor_runtime_probe(self.handle, byref(caps))
+        if rc != PROM_OK:
+            self.close()
+            raise ReactorIssue("probe_failed", f"runtime_probe returned {rc}")
+        self.caps = caps
+
+    # -- lifecycle --------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.lib.prometheus_reactor_runtime_destroy(self.handle)
+            self.handle = c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def available(self) -> bool:
+        return bool(self.caps.available)
+
+    def require_hardware_gpu(self) -> None:
+        """fft.go:50-55: strict execution requires a hardware device (backend 2)."""
+        if not self.caps.available or self.caps.backend_type != PROM_BACKEND_HARDWARE_GPU:
+            raise ReactorIssue("unavailable", f"hardware GPU unavailable (backend={self.caps.backend_type}, "
+                                              f"reason={self.caps.reason_code})")
+
+    def environment(self) -> str:
+        return "hardware_gpu_hip" if self.caps.backend_type == PROM_BACKEND_HARDWARE_GPU else "unknown"
+
+    def device_diagnostics(self) -> PrometheusHipDeviceDiagnostics:
+        d = PrometheusHipDeviceDiagnostics()
+        d.struct_size = ctypes.sizeof(d)
+        rc = self.lib.prometheus_reactor_runtime_hip_device_diagnostics(self.handle, byref(d))
+        if rc != PROM_OK:
+            raise ReactorIssue("diagnostics_failed", f"hip_device_diagnostics returned {rc}")
+        return d
+
+    # -- host-pointer operations -------------------------------------------
+    def sgemm_with_status(self, m: int, n: int, k: int, a, b) -> Tuple[Optional[np.ndarray], CallStatus, int]:
+        a = _f32(a).reshape(-1)
+        b = _f32(b).reshape(-1)
+        if a.size != m * k or b.size != k * n:
+            return None, CallStatus(STAGE_INIT, -2), PROM_ERROR
+        out = np.empty(m * n, dtype=np.float32)
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_sgemm(self.handle, _ptr(a), _ptr(b), _ptr(out), m, n, k,
+                                                       byref(stage), byref(detail))
+        status = CallStatus(stage.value, detail.value)
+        return (out if rc == PROM_OK else None), status, rc
+
+    def sgemm(self, m: int, n: int, k: int, a, b) -> Tuple[np.ndarray, RunStatus]:
+        """bridge.go:410-422 (nativeRuntime.SGEMM)."""
+        out, st, rc = self.sgemm_with_status(m, n, k, a, b)
+        if rc != PROM_OK:
+            status = RunStatus("error", stage_name(st.stage), st.detail)
+            raise ReactorIssue("sgemm_failed", f"native sgemm failed: {status}")
+        return out, RunStatus("ok")
+
+    def gemm_bf16(self, m: int, n: int, k: int, a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+        a = np.ascontiguousarray(a_bits, dtype=np.uint16).reshape(-1)
+        b = np.ascontiguousarray(b_bits, dtype=np.uint16).reshape(-1)
+        if a.size != m * k or b.size != k * n:
+            raise ValueError("invalid matrix lengths")
+        out = np.empty(m * n, dtype=np.float32)
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_gemm_bf16(self.handle, _ptr(a), _ptr(b), _ptr(out), m, n, k,
+                                                           byref(stage), byref(detail))
+        if rc != PROM_OK:
+            raise ReactorIssue("gemm_bf16_failed", f"error({stage_name(stage.value)},{detail.value})")
+        return out
+
+    def reduction(self, x, operation: int, flags: int = 0, lifted: bool = True, output=None):
+        """Row reduction through ..._reduction_v2 (lifted limits) or the reference entry."""
+        x = _f32(x)
+        rows, width = x.shape
+        req = PrometheusReductionRequest()
+        req.struct_size = ctypes.sizeof(req)
+        req.input = _ptr(x)
+        out_count = rows * width if operation == OP_SOFTMAX else rows
+        if output is None:
+            output = np.empty((rows, width) if operation == OP_SOFTMAX else (rows,), dtype=np.float32)
+        req.output = _ptr(output)
+        req.row_count, req.elements_per_row = rows, width
+        req.input_element_count, req.output_element_count = rows * width, out_count
+        req.operation = operation
+        req.finalization = FINALIZATION_STABLE_SOFTMAX if operation == OP_SOFTMAX else FINALIZATION_NONE
+        req.flags = flags
+        res = PrometheusReductionExecutionResult()
+        fn = (self.lib.prometheus_reactor_runtime_reduction_v2 if lifted
+              else self.lib.prometheus_reactor_runtime_reduction)
+        rc = fn(self.handle, byref(req), byref(res))
+        return rc, res, output
+
+    def rmsnorm(self, x, weight, epsilon: float, stride: Optional[int] = None):
+        x = _f32(x)
+        w = _f32(weight)
+        tokens = x.shape[0]
+        width = w.size
+        stride = stride or x.shape[1]
+        out = np.empty((tokens, width), dtype=np.float32)
+        inv = np.empty(tokens, dtype=np.float32)
+        req = PrometheusRmsNormRequest()
+        req.struct_size = ctypes.sizeof(req)
+        req.input, req.weight, req.output, req.inv_rms_output = _ptr(x), _ptr(w), _ptr(out), _ptr(inv)
+        req.tokens, req.width, req.input_row_stride, req.epsilon = tokens, width, stride, epsilon
+        res = PrometheusRmsNormResult()
+        rc = self.lib.prometheus_reactor_runtime_rmsnorm(self.handle, byref(req), byref(res))
+        return rc, res, out, inv
+
+    # -- device-resident operations ----------------------------------------
+    def alloc(self, nbytes: int) -> int:
+        p = c_void_p()
+        rc = self.lib.prometheus_reactor_runtime_device_alloc(self.handle, nbytes, byref(p))
+        if rc != PROM_OK:
+            raise ReactorIssue("alloc_failed", f"device_alloc({nbytes}) returned {rc}")
+        return p.value
+
+    def free(self, ptr: int) -> None:
+        self.lib.prometheus_reactor_runtime_device_free(self.handle, c_void_p(ptr))
+
+    def upload(self, dptr: int, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        rc = self.lib.prometheus_reactor_runtime_device_upload(self.handle, c_void_p(dptr), _ptr(arr), arr.nbytes)
+        if rc != PROM_OK:
+            raise ReactorIssue("upload_failed", f"device_upload returned {rc}")
+
+    def download(self, arr: np.ndarray, dptr: int) -> np.ndarray:
+        rc = self.lib.prometheus_reactor_runtime_device_download(self.handle, _ptr(arr), c_void_p(dptr), arr.nbytes)
+        if rc != PROM_OK:
+            raise ReactorIssue("download_failed", f"device_download returned {rc}")
+        return arr
+
+    def synchronize(self) -> None:
+        rc = self.lib.prometheus_reactor_runtime_synchronize(self.handle)
+        if rc != PROM_OK:
+            raise ReactorIssue("sync_failed", f"synchronize returned {rc}")
+
+    def event_record(self, slot: int) -> None:
+        if self.lib.prometheus_reactor_runtime_event_record(self.handle, slot) != PROM_OK:
+            raise ReactorIssue("event_failed", "event_record failed")
+
+    def event_elapsed_ms(self, start: int, end: int) -> float:
+        ms = c_float(0.0)
+        if self.lib.prometheus_reactor_runtime_event_elapsed_ms(self.handle, start, end, byref(ms)) != PROM_OK:
+            raise ReactorIssue("event_failed", "event_elapsed_ms failed")
+        return ms.value
+
+    def _check(self, rc: int, stage: c_uint32, detail: c_int, what: str) -> int:
+        if rc != PROM_OK:
+            raise ReactorIssue(f"{what}_failed", f"error({stage_name(stage.value)},{detail.value})")
+        return detail.value
+
+    def sgemm_device(self, da: int, db: int, dc: int, m: int, n: int, k: int) -> int:
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_sgemm_device(self.handle, c_void_p(da), c_void_p(db), c_void_p(dc),
+                                                              m, n, k, byref(stage), byref(detail))
+        return self._check(rc, stage, detail, "sgemm_device")
+
+    def gemm_bf16_device(self, da: int, db: int, dc: int, m: int, n: int, k: int) -> int:
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_gemm_bf16_device(self.handle, c_void_p(da), c_void_p(db),
+                                                                  c_void_p(dc), m, n, k, byref(stage), byref(detail))
+        return self._check(rc, stage, detail, "gemm_bf16_device")
+
+    def reduction_device(self, din: int, dout: int, rows: int, width: int, operation: int) -> int:
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_reduction_device(self.handle, c_void_p(din), c_void_p(dout), rows,
+                                                                  width, operation, byref(stage), byref(detail))
+        return self._check(rc, stage, detail, "reduction_device")
+
+    def rmsnorm_device(self, din: int, dw: int, dout: int, dinv: Optional[int], tokens: int, width: int,
+                       stride: int, eps: float) -> int:
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_rmsnorm_device(
+            self.handle, c_void_p(din), c_void_p(dw), c_void_p(dout), c_void_p(dinv) if dinv else None,
+            tokens, width, stride, eps, byref(stage), byref(detail))
+        return self._check(rc, stage, detail, "rmsnorm_device")
+
+
+# ---- the strict `@` path (strict.go:11-32, runtime.go:251-317) -------------
+def compiled_matmul_request(left: Sequence[Sequence[float]], right: Sequence[Sequence[float]]):
+    """runtime.go:251-306: shape checks and float64 -> float32 (RNE) flattening."""
+    if len(left) == 0 or len(right) == 0:
+        raise ValueError("compiled Prometheus matmul requires non-empty matrices")
+    k = len(left[0])
+    if any(len(r) != k for r in left):
+        raise ValueError("compiled Prometheus matmul requires rectangular matrices")
+    if k == 0:
+        raise ValueError("compiled Prometheus matmul requires matrices with at least one column")
+    n = len(right[0])
+    if any(len(r) != n for r in right):
+        raise ValueError("compiled Prometheus matmul requires rectangular matrices")
+    if n == 0:
+        raise ValueError("compiled Prometheus matmul requires matrices with at least one column")
+    if k != len(right):
+        raise ValueError(f"compiled Prometheus matmul shape mismatch: left columns={k} right rows={len(right)}")
+    a = np.asarray(left, dtype=np.float64).astype(np.float32)
+    b = np.asarray(right, dtype=np.float64).astype(np.float32)
+    return len(left), n, k, a, b
+
+
+def run_compiled_matmul_mm_strict(left, right) -> Tuple[list, str]:
+    """strict.go:11-32: GPU or error, never a CPU substitute."""
+    m, n, k, a, b = compiled_matmul_request(left, right)
+    try:
+        rt = NativeRuntime()
+    except ReactorIssue as exc:
+        raise ReactorIssue("strict", f"PROMETHEUS requires GPU matrix execution: {exc}") from exc
+    with rt:
+        try:
+            rt.require_hardware_gpu()
+        except ReactorIssue as exc:
+            raise ReactorIssue("strict", f"PROMETHEUS requires GPU matrix execution: {exc}") from exc
+        try:
+            out, status = rt.sgemm(m, n, k, a, b)
+        except ReactorIssue as exc:
+            raise ReactorIssue("strict", f"PROMETHEUS requires GPU matrix execution: {exc}") from exc
+        env = rt.environment()
+    return out.reshape(m, n).astype(np.float64).tolist(), env

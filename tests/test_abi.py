@@ -1,0 +1,315 @@
+"""CPU-side checks of the C ABI: exports, struct layouts, validation semantics.
+
+These run without a GPU: the library loads, every declared entry point is
+exported, ctypes layouts equal the C header's, and the reference's
+device-less and argument-validation behaviour is reproduced
+(Marionette/reactor_stub_tests.cpp:144-203; reactor_reduction_tests.cpp:206-364).
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oct_amd import prometheus as p
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "prometheus_reactor.h"
+LIB = REPO / "oct_amd" / "libprometheus_reactor.so"
+
+
+def declared_entry_points():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"PROM_REACTOR_API\s+[\w\s\*]+?\b(prometheus_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_entry_points()
+    assert len(names) >= 25
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    # nothing beyond the declared ABI leaks out
+    extra = sorted(e for e in exported if e.startswith("prometheus_") and e not in names)
+    assert not extra, extra
+    lib = ctypes.CDLL(str(LIB))
+    for n in names:
+        assert hasattr(lib, n)
+
+
+def test_library_has_gfx950_code_object():
+    # The HIP fat binary embedded in our own build names its offload target.
+    data = LIB.read_bytes()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+STRUCTS = {
+    "PrometheusCaps": p.PrometheusCaps,
+    "PrometheusReactorConfig": p.PrometheusReactorConfig,
+    "PrometheusVulkanDeviceDiagnostics": p.PrometheusVulkanDeviceDiagnostics,
+    "PrometheusHipDeviceDiagnostics": p.PrometheusHipDeviceDiagnostics,
+    "PrometheusReductionRequest": p.PrometheusReductionRequest,
+    "PrometheusReductionStageDispatch": p.PrometheusReductionStageDispatch,
+    "PrometheusReductionPlan": p.PrometheusReductionPlan,
+    "PrometheusReductionExecutionResult": p.PrometheusReductionExecutionResult,
+    "PrometheusRowWiseSoftmaxRequest": p.PrometheusRowWiseSoftmaxRequest,
+    "PrometheusRowWiseSoftmaxResult": p.PrometheusRowWiseSoftmaxResult,
+    "PrometheusGemma4E2BM1InputRmsNormRequest": p.PrometheusGemma4E2BM1InputRmsNormRequest,
+    "PrometheusGemma4E2BM1InputRmsNormResult": p.PrometheusGemma4E2BM1InputRmsNormResult,
+    "PrometheusRmsNormRequest": p.PrometheusRmsNormRequest,
+    "PrometheusRmsNormResult": p.PrometheusRmsNormResult,
+}
+
+
+def test_ctypes_layouts_match_c_header(tmp_path):
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){"]
+    for name, cls in STRUCTS.items():
+        lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{name}.{field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    c_layout = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                                    check=True).stdout.splitlines())
+    for name, cls in STRUCTS.items():
+        assert int(c_layout[name]) == ctypes.sizeof(cls), name
+        for field, _ in cls._fields_:
+            assert int(c_layout[f"{name}.{field}"]) == getattr(cls, field).offset, f"{name}.{field}"
+
+
+def test_reference_struct_sizes_unchanged():
+    # Layouts fixed by the reference header (x86-64): reactor_api.h:512-598, 1582-1586, 1751-1769.
+    assert ctypes.sizeof(p.PrometheusCaps) == 12
+    assert ctypes.sizeof(p.PrometheusReductionRequest) == 64
+    assert ctypes.sizeof(p.PrometheusReactorConfig) == 40
+    assert ctypes.sizeof(p.PrometheusRowWiseSoftmaxRequest) == 48
+    assert ctypes.sizeof(p.PrometheusGemma4E2BM1InputRmsNormRequest) == 112
+
+
+@pytest.fixture
+def lib():
+    return p.load_library(str(LIB))
+
+
+def test_abi_version(lib):
+    assert lib.prometheus_reactor_abi_version() == 1
+
+
+def test_create_destroy_lifecycle(lib):
+    h = ctypes.c_void_p()
+    assert lib.prometheus_reactor_runtime_create(None, ctypes.byref(h)) == p.PROM_OK
+    assert h.value
+    assert lib.prometheus_reactor_runtime_destroy(h) == p.PROM_OK
+    assert lib.prometheus_reactor_runtime_destroy(h) == p.PROM_INVALID_HANDLE
+
+
+def test_invalid_usage(lib):
+    assert lib.prometheus_reactor_runtime_create(None, None) == p.PROM_ERROR
+    caps = p.PrometheusCaps()
+    assert lib.prometheus_reactor_runtime_probe(None, ctypes.byref(caps)) == p.PROM_INVALID_HANDLE
+    h = ctypes.c_void_p()
+    assert lib.prometheus_reactor_runtime_create(None, ctypes.byref(h)) == p.PROM_OK
+    assert lib.prometheus_reactor_runtime_probe(h, None) == p.PROM_ERROR
+    lib.prometheus_reactor_runtime_destroy(h)
+
+
+def test_forced_unavailable_runtime_reports_reference_caps():
+    # PROM_TESTCFG_SKIP_VULKAN_INIT forces the device-less runtime on any machine.
+    with p.NativeRuntime(test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        assert rt.caps.available == 0
+        assert rt.caps.backend_type == p.PROM_BACKEND_UNKNOWN
+        assert rt.caps.reason_code == p.PROM_REASON_VULKAN_UNAVAILABLE
+        out, st, rc = rt.sgemm_with_status(1, 1, 1, [1.0], [1.0])
+        assert rc == p.PROM_ERROR and st.stage == p.STAGE_INIT and out is None
+        with pytest.raises(p.ReactorIssue):
+            rt.require_hardware_gpu()
+
+
+def test_sgemm_argument_validation_order(lib):
+    h = ctypes.c_void_p()
+    lib.prometheus_reactor_runtime_create(None, ctypes.byref(h))
+    st, d = ctypes.c_uint32(), ctypes.c_int()
+    a = np.ones(4, np.float32)
+    ptr = a.ctypes.data
+    # invalid handle -> INIT / PROM_INVALID_HANDLE (reactor_sgemm.cpp:4152-4155)
+    assert lib.prometheus_reactor_runtime_sgemm(None, ptr, ptr, ptr, 1, 1, 1, ctypes.byref(st), ctypes.byref(d)) == 2
+    assert (st.value, d.value) == (p.STAGE_INIT, p.PROM_INVALID_HANDLE)
+    # NULL operand -> TRANSFER_IN / PROM_ERROR
+    assert lib.prometheus_reactor_runtime_sgemm(h, None, ptr, ptr, 1, 1, 1, ctypes.byref(st), ctypes.byref(d)) == 1
+    assert (st.value, d.value) == (p.STAGE_TRANSFER_IN, p.PROM_ERROR)
+    # zero dimension -> INIT / PROM_ERROR
+    assert lib.prometheus_reactor_runtime_sgemm(h, ptr, ptr, ptr, 0, 1, 1, ctypes.byref(st), ctypes.byref(d)) == 1
+    assert (st.value, d.value) == (p.STAGE_INIT, p.PROM_ERROR)
+    lib.prometheus_reactor_runtime_destroy(h)
+
+
+def _request(rows, width, op, flags=0, fin=None, in_count=None, out_count=None):
+    r = p.PrometheusReductionRequest()
+    r.struct_size = ctypes.sizeof(r)
+    r.row_count, r.elements_per_row = rows, width
+    r.operation = op
+    r.finalization = (1 if op == p.OP_SOFTMAX else 0) if fin is None else fin
+    r.flags = flags
+    r.input_element_count = rows * width if in_count is None else in_count
+    r.output_element_count = (rows * width if op == p.OP_SOFTMAX else rows) if out_count is None else out_count
+    return r
+
+
+def _plan(lib, req):
+    plan = p.PrometheusReductionPlan()
+    rc = lib.prometheus_reactor_reduction_plan(ctypes.byref(req), ctypes.byref(plan))
+    return rc, plan
+
+
+def test_reduction_plan_reference_schedule(lib):
+    # PrometheusReduction.concept:128-164 via reactor_vulkan_fused_reduction.c:101-148
+    rc, plan = _plan(lib, _request(128, 4096, p.OP_SUM))
+    assert rc == 0 and plan.strategy == 2 and plan.partial_count == 4 and plan.stage_count == 2
+    assert [plan.stages[i].stage_role for i in range(2)] == [1, 1]
+    assert plan.stages[0].groups_x == 128 * 4 and plan.stages[0].temporary_role == 1
+    assert plan.temporary_bytes == 128 * 4 * 4
+    rc, plan = _plan(lib, _request(16, 4096, p.OP_SOFTMAX))
+    assert rc == 0 and plan.stage_count == 5
+    assert [plan.stages[i].stage_role for i in range(5)] == [2, 2, 3, 1, 4]
+    assert plan.stages[4].groups_x == (16 * 4096 + 255) // 256
+    assert plan.temporary_bytes == 16 * 4 * 4 + 2 * 16 * 4
+    rc, plan = _plan(lib, _request(1024, 512, p.OP_SOFTMAX))
+    assert rc == 0 and plan.strategy == 1 and plan.stage_count == 1 and plan.stages[0].stage_role == 5
+    rc, plan = _plan(lib, _request(4, 64, p.OP_SOFTMAX))
+    assert plan.strategy == 3 and plan.stages[0].stage_role == 7 and plan.stages[0].groups_x == 1
+    rc, plan = _plan(lib, _request(1024, 100, p.OP_SUM))
+    assert plan.strategy == 3 and plan.stages[0].stage_role == 6
+    rc, plan = _plan(lib, _request(1024, 100, p.OP_MAX))
+    assert plan.strategy == 2
+    # forced composed softmax at narrow width
+    rc, plan = _plan(lib, _request(8, 512, p.OP_SOFTMAX, flags=2))
+    assert plan.strategy == 2 and plan.stage_count == 3
+    # replay ids distinguish plans and are stable
+    a = _plan(lib, _request(8, 512, p.OP_SOFTMAX))[1].replay_id
+    assert a == _plan(lib, _request(8, 512, p.OP_SOFTMAX))[1].replay_id
+    assert a != _plan(lib, _request(8, 513, p.OP_SOFTMAX))[1].replay_id
+
+
+@pytest.mark.parametrize("req,detail", [
+    (dict(rows=0, width=4, op=1), -6804),
+    (dict(rows=4, width=0, op=1), -6805),
+    (dict(rows=1025, width=4, op=1), -6811),
+    (dict(rows=1, width=1048577, op=1), -6812),
+    (dict(rows=1024, width=16385, op=1), -6813),
+    (dict(rows=4, width=4, op=4), -6806),
+    (dict(rows=4, width=4, op=1, fin=1), -6807),
+    (dict(rows=4, width=4, op=3, fin=0), -6807),
+    (dict(rows=4, width=4, op=1, flags=1), -6815),
+    (dict(rows=4, width=1057, op=3, flags=1), -6815),
+    (dict(rows=4, width=4, op=1, in_count=15), -6809),
+    (dict(rows=4, width=4, op=1, out_count=16), -6810),
+])
+def test_reduction_validation_codes(lib, req, detail):
+    r = _request(req["rows"], req["width"], req["op"], req.get("flags", 0), req.get("fin"), req.get("in_count"),
+                 req.get("out_count"))
+    x = np.zeros(max(1, req["rows"] * req["width"]), np.float32)
+    r.input = x.ctypes.data
+    r.output = x.ctypes.data
+    assert _plan(lib, r)[0] == p.PROM_ERROR
+    with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        res = p.PrometheusReductionExecutionResult()
+        rc = lib.prometheus_reactor_runtime_reduction(rt.handle, ctypes.byref(r), ctypes.byref(res))
+        assert rc == p.PROM_ERROR and res.stage == p.STAGE_INIT and res.detail_code == detail
+
+
+def test_reduction_v2_lifts_the_envelope_but_keeps_codes(lib):
+    with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        x = np.ones((8192, 4), np.float32)
+        rc, res, _ = rt.reduction(x, p.OP_SUM, lifted=False)
+        assert rc == 1 and res.detail_code == -6811
+        rc, res, _ = rt.reduction(x, p.OP_SUM, lifted=True)
+        # admitted, then refused only because this runtime has no device
+        assert rc == 1 and res.detail_code == -6825 and res.stage == p.STAGE_INIT
+
+
+def test_reduction_nonfinite_is_transfer_in(lib):
+    with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        x = np.ones((3, 5), np.float32)
+        x[2, 1] = np.nan
+        rc, res, _ = rt.reduction(x, p.OP_MAX)
+        assert rc == 1 and res.stage == p.STAGE_TRANSFER_IN and res.detail_code == -6814
+        assert res.first_nonfinite_index == 11
+
+
+def test_row_wise_softmax_validation(lib):
+    with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        x = np.zeros(64, np.float32)
+        req = p.PrometheusRowWiseSoftmaxRequest()
+        req.struct_size = ctypes.sizeof(req)
+        res = p.PrometheusRowWiseSoftmaxResult()
+        call = lambda: lib.prometheus_reactor_runtime_row_wise_softmax(rt.handle, ctypes.byref(req), ctypes.byref(res))
+        # zero rows, zero counts: synchronous no-op
+        assert call() == 0 and res.stage == 0
+        req.row_count, req.elements_per_row, req.input_element_count, req.output_element_count = 2, 4, 8, 7
+        assert call() == 1 and res.detail_code == -6854
+        req.output_element_count = 8
+        assert call() == 1 and res.detail_code == -6852
+        req.input = x.ctypes.data
+        req.output = x.ctypes.data + 4  # partial overlap
+        assert call() == 1 and res.detail_code == -6859
+        req.output = x.ctypes.data  # exact in-place is allowed -> reaches the device check
+        assert call() == 1 and res.detail_code == -6861
+        req.row_count, req.input_element_count, req.output_element_count = 1025, 1025 * 4, 1025 * 4
+        assert call() == 1 and res.detail_code == -6856
+        req.row_count, req.elements_per_row = 1, 1057
+        req.input_element_count = req.output_element_count = 1057
+        assert call() == 1 and res.detail_code == -6857
+
+
+def test_gemma_rmsnorm_validation(lib):
+    with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        x = np.ones((2, 8), np.float32)
+        w = np.ones(8, np.float32)
+        y = np.zeros((2, 8), np.float32)
+        inv = np.zeros(2, np.float32)
+        req = p.PrometheusGemma4E2BM1InputRmsNormRequest()
+        req.struct_size = ctypes.sizeof(req)
+        res = p.PrometheusGemma4E2BM1InputRmsNormResult()
+        call = lambda: lib.prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm(rt.handle, ctypes.byref(req),
+                                                                                   ctypes.byref(res))
+        assert call() == 1 and res.detail_code == -7401
+        req.input, req.weight, req.output, req.inv_rms_output = (x.ctypes.data, w.ctypes.data, y.ctypes.data,
+                                                                 inv.ctypes.data)
+        req.input_element_count, req.weight_element_count, req.output_element_count = 16, 8, 16
+        req.inv_rms_output_element_count = 2
+        req.tokens, req.model_width, req.input_row_stride, req.epsilon = 2, 8, 8, 1e-6
+        req.input_generation = req.weight_generation = req.exact_source_hash = 1
+        assert call() == 1 and res.stage == p.STAGE_INIT and res.detail_code == p.DETAIL_HIP_UNAVAILABLE
+        req.epsilon = 0.0
+        assert call() == 1 and res.detail_code == -7407
+        req.epsilon, req.tokens = 1e-6, 1025
+        assert call() == 1 and res.detail_code == -7403
+
+
+def test_strict_path_raises_without_device(monkeypatch):
+    monkeypatch.setenv(p.REACTOR_TEST_FLAGS_ENV_VAR, str(p.TESTCFG_SKIP_VULKAN_INIT))
+    with pytest.raises(p.ReactorIssue, match="PROMETHEUS requires GPU matrix execution"):
+        p.run_compiled_matmul_mm_strict([[1.0, 2.0], [3.0, 4.0]], [[1.0, 2.0], [3.0, 4.0]])
+
+
+def test_strict_path_missing_library_is_an_error(monkeypatch, tmp_path):
+    # Language/Prometheus/unavailable/matrix.octfail: no CPU substitute when the reactor is absent
+    monkeypatch.setenv(p.REACTOR_ENV_VAR, str(tmp_path / "missing" / p.LIBRARY_BASENAME))
+    monkeypatch.setattr(p, "_SHARED_LIB", None)
+    with pytest.raises(p.ReactorIssue, match="PROMETHEUS requires GPU matrix execution"):
+        p.run_compiled_matmul_mm_strict([[1.0]], [[1.0]])
+
+
+def test_compiled_matmul_request_shape_checks():
+    with pytest.raises(ValueError, match="shape mismatch"):
+        p.compiled_matmul_request([[1.0, 2.0]], [[1.0, 2.0]])
+    with pytest.raises(ValueError, match="rectangular"):
+        p.compiled_matmul_request([[1.0, 2.0], [1.0]], [[1.0], [2.0]])
+    m, n, k, a, b = p.compiled_matmul_request([[0.1, 2.0]], [[1.0], [3.0]])
+    assert (m, n, k) == (1, 1, 2) and a.dtype == np.float32 and a[0, 0] == np.float32(0.1)

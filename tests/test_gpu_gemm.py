@@ -1,0 +1,202 @@
+"""GPU parity of the MFMA SGEMM / GEMV / bf16 GEMM against the CPU oracle.
+
+Bar: normwise relative error <= 1e-5 for fp32
+against Oct's binary64 `@` on the same fp32 operands; <= 2e-2 for bf16
+(against binary64 on the bf16 operands).  The reference's own tolerance
+(abs 1e-4 and rel 1e-4, runtime.go:12-15) is checked on its corpora.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oct_amd import prometheus as p
+
+pytestmark = pytest.mark.gpu
+
+FP32_NORMWISE = 1e-5
+BF16_NORMWISE = 2e-2
+
+
+def _sgemm(rt, a, b):
+    m, k = a.shape
+    n = b.shape[1]
+    out, status = rt.sgemm(m, n, k, a, b)
+    assert str(status) == "ok"
+    return out.reshape(m, n)
+
+
+def test_kat_2x2(gpu_runtime):
+    out = _sgemm(gpu_runtime, np.array([[1, 2], [3, 4]], np.float32), np.array([[5, 6], [7, 8]], np.float32))
+    np.testing.assert_array_equal(out, [[19, 22], [43, 50]])
+
+
+def test_strict_path_a_at_a(gpu_runtime):
+    # Language/Prometheus/gpu/matrix.octest:3-9
+    out, env = p.run_compiled_matmul_mm_strict([[1.0, 2.0], [3.0, 4.0]], [[1.0, 2.0], [3.0, 4.0]])
+    assert out[0][0] == 7.0 and env == "hardware_gpu_hip"
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (4, 4, 4), (16, 16, 16), (32, 32, 32), (3, 5, 7), (3, 7, 5),
+                                   (1, 9, 4), (11, 1, 3), (2, 13, 3)])
+def test_reference_corpora(gpu_runtime, m, n, k):
+    # runtime.go:83-89 and reactor_stub_tests.cpp:205-253
+    a = oracle.deterministic_matrix(m, k)
+    b = oracle.deterministic_matrix(k, n)
+    out, st, rc = gpu_runtime.sgemm_with_status(m, n, k, a, b)
+    assert rc == p.PROM_OK and st.stage == p.STAGE_TRANSFER_OUT and st.detail > 0
+    res = oracle.compare_against_oracle(oracle.cpu_sgemm_f32(a, b), out)
+    assert res.pass_ == 1, (res.first_failing_index, res.first_expected, res.first_actual)
+    assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
+
+
+def test_concept_corpus_binary64(gpu_runtime):
+    # reactor_concept_sgemm_tests.cpp:17-29: 37x29x13 against binary64 within 1e-4
+    m, n, k = 37, 29, 13
+    a = oracle.concept_sgemm_matrix(m * k, 3).reshape(m, k)
+    b = oracle.concept_sgemm_matrix(k * n, 5).reshape(k, n)
+    out = _sgemm(gpu_runtime, a, b)
+    assert np.max(np.abs(out - oracle.matmul_f64(a, b))) <= 1e-4
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 3, 1), (5, 3, 2), (7, 9, 3), (129, 127, 17), (128, 128, 16), (257, 130, 33),
+                                   (64, 256, 4), (300, 200, 100), (1, 513, 257), (513, 1, 255), (130, 5, 1025)])
+def test_exact_tail_shapes(gpu_runtime, m, n, k):
+    a = oracle.uniform(100 + m, (m, k))
+    b = oracle.uniform(200 + n, (k, n))
+    out = _sgemm(gpu_runtime, a, b)
+    assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
+
+
+def test_c1_1024_full(gpu_runtime):
+    # M=N=K=1024, U[-1,1] seeded
+    a = oracle.uniform(1, (1024, 1024))
+    b = oracle.uniform(2, (1024, 1024))
+    out = _sgemm(gpu_runtime, a, b)
+    err = oracle.normwise_rel_err(out, oracle.matmul_f64(a, b))
+    print(f"C1 1024^3 normwise rel err {err:.3e}")
+    assert err <= FP32_NORMWISE
+
+
+def test_c2_1000_full(gpu_runtime):
+    a = oracle.uniform(3, (1000, 1000))
+    b = oracle.uniform(4, (1000, 1000))
+    out = _sgemm(gpu_runtime, a, b)
+    assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
+
+
+def _rows_subset(m, count=64):
+    rows = sorted(set(np.linspace(0, m - 1, count).astype(int).tolist()) | {m - 1, m - 2})
+    return rows
+
+
+def test_c2_ragged_4097_3001_513(gpu_runtime):
+    m, n, k = 4097, 3001, 513
+    a = oracle.uniform(5, (m, k))
+    b = oracle.uniform(6, (k, n))
+    out = _sgemm(gpu_runtime, a, b)
+    # the last 129 rows (one full tile plus the ragged one) and a spread of others, exactly
+    tail = oracle.matmul_f64(a, b, rows=(m - 129, m))
+    assert oracle.normwise_rel_err(out[m - 129:], tail[m - 129:]) <= FP32_NORMWISE
+    for r in _rows_subset(m, 32):
+        ref = oracle.matmul_f64(a, b, rows=(r, r + 1))[r]
+        assert oracle.normwise_rel_err(out[r], ref) <= FP32_NORMWISE
+    # full-size property: C x = A (B x) for a random x (Freivalds)
+    x = np.random.default_rng(0).standard_normal(n)
+    lhs = out.astype(np.float64) @ x
+    rhs = a.astype(np.float64) @ (b.astype(np.float64) @ x)
+    assert np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs) <= FP32_NORMWISE
+
+
+def test_c2_gemv_8192x1x4096(gpu_runtime):
+    m, n, k = 8192, 1, 4096
+    a = oracle.uniform(7, (m, k))
+    b = oracle.uniform(8, (k, n))
+    out, st, rc = gpu_runtime.sgemm_with_status(m, n, k, a, b)
+    assert rc == 0 and st.detail == p.DETAIL_PATH_HIP_GEMV_F32
+    assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
+
+
+@pytest.mark.parametrize("m,k", [(1, 1), (3, 5), (7, 4097), (1000, 1000), (65, 3)])
+def test_gemv_ragged(gpu_runtime, m, k):
+    a = oracle.uniform(9 + m, (m, k))
+    b = oracle.uniform(10 + k, (k, 1))
+    out = _sgemm(gpu_runtime, a, b)
+    assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
+
+
+def test_c2_4096_cubed_device_resident(gpu_runtime):
+    """Full-size 4096^3 via the device-resident entry: subset rows exactly + Freivalds."""
+    rt = gpu_runtime
+    n = 4096
+    a = oracle.uniform(11, (n, n))
+    b = oracle.uniform(12, (n, n))
+    da, db, dc = rt.alloc(a.nbytes), rt.alloc(b.nbytes), rt.alloc(a.nbytes)
+    try:
+        rt.upload(da, a)
+        rt.upload(db, b)
+        assert rt.sgemm_device(da, db, dc, n, n, n) == p.DETAIL_PATH_HIP_MFMA_F32
+        rt.synchronize()
+        out = rt.download(np.empty((n, n), np.float32), dc)
+        # the host-pointer path gives bit-identical results (same kernel, deterministic)
+        out2 = _sgemm(rt, a, b)
+        np.testing.assert_array_equal(out, out2)
+    finally:
+        for d in (da, db, dc):
+            rt.free(d)
+    rows = _rows_subset(n, 24)
+    for r in rows:
+        ref = oracle.matmul_f64(a, b, rows=(r, r + 1))[r]
+        assert oracle.normwise_rel_err(out[r], ref) <= FP32_NORMWISE, r
+    x = np.random.default_rng(1).standard_normal(n)
+    rhs = a.astype(np.float64) @ (b.astype(np.float64) @ x)
+    assert np.linalg.norm(out.astype(np.float64) @ x - rhs) / np.linalg.norm(rhs) <= FP32_NORMWISE
+
+
+def test_sgemm_deterministic(gpu_runtime):
+    a = oracle.uniform(13, (300, 257))
+    b = oracle.uniform(14, (257, 190))
+    np.testing.assert_array_equal(_sgemm(gpu_runtime, a, b), _sgemm(gpu_runtime, a, b))
+
+
+def test_injected_faults_report_reference_stages():
+    # reactor_stub_tests.cpp:842-913: injected upload/dispatch/download failures
+    for flag, stage, detail in ((p.TESTCFG_FAIL_UPLOAD, p.STAGE_TRANSFER_IN, p.DETAIL_INJECTED_UPLOAD_FAILURE),
+                                (p.TESTCFG_FAIL_DISPATCH, p.STAGE_SUBMIT, p.DETAIL_INJECTED_DISPATCH_FAILURE),
+                                (p.TESTCFG_FAIL_DOWNLOAD, p.STAGE_TRANSFER_OUT, p.DETAIL_INJECTED_DOWNLOAD_FAILURE)):
+        with p.NativeRuntime(test_flags=flag) as rt:
+            assert rt.available
+            out, st, rc = rt.sgemm_with_status(2, 2, 2, np.ones(4), np.ones(4))
+            assert rc == p.PROM_ERROR and (st.stage, st.detail) == (stage, detail) and out is None
+
+
+# ------------------------------------------------------------------ bf16
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (5, 7, 3), (128, 128, 64), (129, 130, 65), (257, 513, 200),
+                                   (1000, 1000, 1000), (64, 8, 8)])
+def test_bf16_shapes(gpu_runtime, m, n, k):
+    a = oracle.to_bf16(oracle.uniform(20 + m, (m, k)))
+    b = oracle.to_bf16(oracle.uniform(30 + n, (k, n)))
+    out = gpu_runtime.gemm_bf16(m, n, k, a, b).reshape(m, n)
+    err = oracle.normwise_rel_err(out, oracle.matmul_f64(a, b))
+    # products of bf16 values are exact in fp32; only fp32 accumulation rounds
+    assert err <= 1e-5 and err <= BF16_NORMWISE
+
+
+def test_bf16_4096_cubed(gpu_runtime):
+    rt = gpu_runtime
+    n = 4096
+    a = oracle.to_bf16(oracle.uniform(41, (n, n)))
+    b = oracle.to_bf16(oracle.uniform(42, (n, n)))
+    da, db, dc = rt.alloc(a.nbytes), rt.alloc(b.nbytes), rt.alloc(n * n * 4)
+    try:
+        rt.upload(da, a)
+        rt.upload(db, b)
+        assert rt.gemm_bf16_device(da, db, dc, n, n, n) == p.DETAIL_PATH_HIP_MFMA_BF16
+        rt.synchronize()
+        out = rt.download(np.empty((n, n), np.float32), dc)
+    finally:
+        for d in (da, db, dc):
+            rt.free(d)
+    for r in _rows_subset(n, 16):
+        ref = oracle.matmul_f64(a, b, rows=(r, r + 1))[r]
+        assert oracle.normwise_rel_err(out[r], ref) <= BF16_NORMWISE
+        assert oracle.normwise_rel_err(out[r], ref) <= 1e-5
