@@ -88,6 +88,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (10 launches) so that rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE can be scaled against known bytes")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -97,6 +101,16 @@ def main() -> int:
 
     from oct_amd import prometheus as p
     import oracle
+
+    if args.copy_calibration_mib:
+        import torch
+
+        src = torch.ones(args.copy_calibration_mib << 18, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy calibration: 10 x {args.copy_calibration_mib} MiB read + written", file=sys.stderr)
 
     rt = p.NativeRuntime()
     rt.require_hardware_gpu()
@@ -215,7 +229,7 @@ def main() -> int:
         line["secondary"] = sec
 
     rt.close()
-    line["cpu_baseline"] = cpu_baseline_sgemm(n, args.cpu_seconds)
+    line["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline_sgemm(n, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -49,6 +49,9 @@ bool ensure_device() {
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   if (hipSetDevice(dev) != hipSuccess) return false;
   if (hipGetDeviceProperties(&c.props, dev) != hipSuccess) return false;
+  if (c.props.name[0] == '\0' && hipDeviceGetName(c.props.name, (int)sizeof(c.props.name), dev) != hipSuccess) {
+    c.props.name[0] = '\0';
+  }
   // One non-blocking stream at the default priority carries every launch.
   if (hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking) != hipSuccess) return false;
   for (uint32_t i = 0; i < kEventSlots; ++i) {
