@@ -530,6 +530,121 @@ PROM_REACTOR_API int prometheus_reactor_runtime_rmsnorm_device(void* handle, con
                                                                uint32_t width, uint32_t input_row_stride, float epsilon,
                                                                uint32_t* out_stage, int* out_detail_code);
 
+/* ------------------------------------------------------------------------ */
+/* NEW: transformer-block dispatch.  The reference's block ABI is closed and   */
+/* shape-locked (Z-Image main transformer, reactor_api.h:800-1244, 2713-2821); */
+/* these entries carry explicit shape fields instead.  Weights are [in, out]   */
+/* row-major as canonicalLinear (zimage/canonical_reference.go:156-175).       */
+/* ------------------------------------------------------------------------ */
+
+enum {
+  PROM_BLOCK_DETAIL_INVALID_REQUEST = -7501,
+  PROM_BLOCK_DETAIL_SHAPE = -7502,
+  PROM_BLOCK_DETAIL_UNSUPPORTED = -7503,
+};
+
+/* Gemma-style decoder layer in fp32:
+     n1 = RMSNorm(x; attn_norm_weight, eps)          y = x * rsqrt(mean(x^2)+eps) * w
+     q,k,v = n1 @ w_qkv   (columns: q_heads*head_dim | head_dim | head_dim)
+     rotate-half RoPE on q and k at positions position_offset + t, base rope_base
+     attention: softmax(q k^T / sqrt(head_dim)) v, causal, every query head on KV head 0
+     h = x + attn @ w_o
+     n2 = RMSNorm(h; ffn_norm_weight, eps)
+     g|u = n2 @ w_gate_up (columns: ffn_hidden gate | ffn_hidden up)
+     out = h + (gelu_tanh(g) * u) @ w_down
+   kv_heads must be 1 (multi-query attention, as Gemma-2B). */
+typedef struct PrometheusDecoderLayerF32Request {
+  uint32_t struct_size;
+  uint32_t tokens;
+  uint32_t hidden;
+  uint32_t q_heads;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t ffn_hidden;
+  uint32_t position_offset;
+  float rms_epsilon;
+  float rope_base;
+  const float* input;            /* [tokens, hidden] */
+  const float* attn_norm_weight; /* [hidden] */
+  const float* w_qkv;            /* [hidden, (q_heads + 2*kv_heads) * head_dim] */
+  const float* w_o;              /* [q_heads * head_dim, hidden] */
+  const float* ffn_norm_weight;  /* [hidden] */
+  const float* w_gate_up;        /* [hidden, 2 * ffn_hidden] */
+  const float* w_down;           /* [ffn_hidden, hidden] */
+  float* output;                 /* [tokens, hidden] */
+} PrometheusDecoderLayerF32Request;
+
+/* Z-Image-style single-stream DiT block in bf16;
+   the per-stage definition follows zimage/canonical_reference.go:315-480 and
+   tools/python/zimage/zimage_main_transformer_canonical.py:178-277:
+     m = condition @ w_adaln + b_adaln  -> scaleA = 1+m0, gateA = tanh(m1),
+                                          scaleM = 1+m2, gateM = tanh(m3)
+     a = RMSNorm(x; attn_norm1) * scaleA          (eps rms_epsilon)
+     q|k|v = a @ w_qkv;  q,k = per-head RMSNorm(q_norm / k_norm)
+     3-axis interleaved-pair RoPE on q,k (axes rope_axes, theta rope_theta,
+     per-token coordinates [frame,row,col])
+     o = softmax(q k^T / sqrt(head_dim)) v  (full attention, per head)
+     r = x + gateA * RMSNorm(o @ w_out; attn_norm2)
+     f = RMSNorm(r; ffn_norm1) * scaleM
+     out = r + gateM * RMSNorm((silu(f @ w1) * (f @ w3)) @ w2; ffn_norm2)
+   GEMM operands are bf16 (weights as given; activations rounded to nearest
+   even), accumulation and norms fp32; x and out are fp32. */
+typedef struct PrometheusDitBlockBf16Request {
+  uint32_t struct_size;
+  uint32_t tokens;
+  uint32_t hidden;
+  uint32_t heads;
+  uint32_t head_dim;
+  uint32_t ffn_hidden;
+  uint32_t cond_dim;
+  uint32_t rope_axes[3];
+  float rope_theta;
+  float rms_epsilon;
+  const float* input;        /* [tokens, hidden] fp32 */
+  const float* coordinates;  /* [tokens, 3] fp32 */
+  const float* condition;    /* [cond_dim] fp32 */
+  const uint16_t* w_adaln;   /* bf16 [cond_dim, 4*hidden] */
+  const float* b_adaln;      /* [4*hidden] */
+  const float* attn_norm1;   /* [hidden] */
+  const float* attn_norm2;   /* [hidden] */
+  const float* ffn_norm1;    /* [hidden] */
+  const float* ffn_norm2;    /* [hidden] */
+  const float* q_norm;       /* [head_dim] */
+  const float* k_norm;       /* [head_dim] */
+  const uint16_t* w_qkv;     /* bf16 [hidden, 3*hidden] */
+  const uint16_t* w_out;     /* bf16 [hidden, hidden] */
+  const uint16_t* w_13;      /* bf16 [hidden, 2*ffn_hidden]: w1 columns then w3 columns */
+  const uint16_t* w_2;       /* bf16 [ffn_hidden, hidden] */
+  float* output;             /* [tokens, hidden] fp32 */
+} PrometheusDitBlockBf16Request;
+
+typedef struct PrometheusBlockResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint32_t output_written;
+  uint32_t kernel_launches;
+  uint32_t reserved0;
+  uint64_t gpu_duration_ns;
+  uint64_t end_to_end_ns;
+  uint64_t workspace_bytes;
+} PrometheusBlockResult;
+
+/* Host-pointer forms copy weights and activations in and the output out
+   (synchronous).  _device forms take device pointers for every array, enqueue
+   on the runtime stream and return; the workspace is owned by the runtime's
+   device context (grow-only, reused across calls). */
+PROM_REACTOR_API int prometheus_reactor_runtime_decoder_layer_f32(void* handle,
+                                                                  const PrometheusDecoderLayerF32Request* request,
+                                                                  PrometheusBlockResult* out_result);
+PROM_REACTOR_API int prometheus_reactor_runtime_decoder_layer_f32_device(
+    void* handle, const PrometheusDecoderLayerF32Request* request, PrometheusBlockResult* out_result);
+PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16(void* handle, const PrometheusDitBlockBf16Request* request,
+                                                               PrometheusBlockResult* out_result);
+PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16_device(void* handle,
+                                                                      const PrometheusDitBlockBf16Request* request,
+                                                                      PrometheusBlockResult* out_result);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,221 @@
+// Flash-style bf16 attention on CDNA4 MFMA (v_mfma_f32_32x32x16_bf16).
+//
+// O = softmax(Q K^T * scale) V per head, full (non-causal) attention, head_dim
+// 128; Q, K, V, O are bf16 [T, ld] with head h at column h*128.  The
+// reference's attention (main_transformer_joint_attention_streaming.sdslv:23-86)
+// keeps a whole score row in LDS, one workgroup per (token, head), and caps the
+// sequence at 1056 keys; this kernel streams K/V tiles with an online softmax
+// so the sequence length is unbounded.
+//
+//   * workgroup = 4 wave64 = 128 queries of one head; each wave owns 32 queries;
+//   * per 64-key tile: K [64][128] and V^T [128][64] are staged in LDS (V is
+//     transposed on the way in, k pairs packed into 32-bit stores);
+//   * scores are computed transposed, S^T = K Q^T, so that a lane owns one
+//     query and 32 of its scores: the row max / row sum need one cross-lane
+//     step (lanes l and l^32), not a 32-lane reduction;
+//   * O^T = V^T P^T accumulates in 4 MFMA blocks (128 d x 32 queries); P
+//     stays in registers: the key order inside each 16-key MFMA step is the
+//     permutation the S^T accumulator layout hands out, and V^T is read in the
+//     same permuted order (two 64-bit LDS reads per operand);
+//   * softmax runs in the log2 domain (exp2), running max/sum in fp32;
+//   * the output tile is staged through LDS for 128-bit coalesced stores.
+#include "reactor_internal.h"
+
+namespace prom {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kD = 128;     // head dim
+constexpr int kQW = 32;     // queries per wave
+constexpr int kKB = 64;     // keys per tile
+constexpr int kKP = kD + 8;   // Ks row pitch (bf16)
+constexpr int kVP = kKB + 8;  // Vt row pitch (bf16)
+constexpr float kNegBig = -1.0e30f;
+
+__device__ __forceinline__ uint16_t f2bf(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+__global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t* __restrict__ Q,
+                                                                 const uint16_t* __restrict__ K,
+                                                                 const uint16_t* __restrict__ V,
+                                                                 uint16_t* __restrict__ O, int T, int ldq, int ldk,
+                                                                 int ldv, int ldo, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKB][kKP];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD][kVP];
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int head = (int)blockIdx.y;
+  const int q0 = (int)blockIdx.x * (4 * kQW) + wave * kQW;
+  const int lq = lane & 31;
+  const int hi = lane >> 5;  // lane half
+  const int qi = q0 + lq;
+
+  // Q^T operand (B of S^T = K Q^T): lane holds Q[qi][16s + 8*hi .. +7] for s = 0..7.
+  bf16x8 qf[8];
+  {
+    const uint16_t* qrow = Q + (size_t)qi * ldq + head * kD;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (qi < T) v = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * hi);
+      qf[s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  floatx16 o[4] = {};  // O^T blocks: d = 32*db + 8*(r/4) + 4*hi + r%4, query lq
+  float m_run = kNegBig;
+  float l_run = 0.0f;
+
+  const int n_tiles = (T + kKB - 1) / kKB;
+  for (int kt = 0; kt < n_tiles; ++kt) {
+    const int k0 = kt * kKB;
+    __syncthreads();  // previous tile fully consumed
+    // K tile: 64 keys x 128 d = 1024 16-byte chunks, 4 per thread.
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 256 * u;
+      const int key = c >> 4;
+      const int dc = (c & 15) * 8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (k0 + key < T) v = *reinterpret_cast<const u32x4*>(K + (size_t)(k0 + key) * ldk + head * kD + dc);
+      *reinterpret_cast<u32x4*>(&Ks[key][dc]) = v;
+    }
+    // V tile transposed: units of (key pair, 8 d): 32 pairs x 16 d-chunks = 512, 2 per thread.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + 256 * u;
+      const int kp = c >> 4;
+      const int dc = (c & 15) * 8;
+      u32x4 lo = {0u, 0u, 0u, 0u}, hv = {0u, 0u, 0u, 0u};
+      const int key = k0 + 2 * kp;
+      if (key < T) lo = *reinterpret_cast<const u32x4*>(V + (size_t)key * ldv + head * kD + dc);
+      if (key + 1 < T) hv = *reinterpret_cast<const u32x4*>(V + (size_t)(key + 1) * ldv + head * kD + dc);
+      const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
+      const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        *reinterpret_cast<uint32_t*>(&Vt[dc + 2 * j][2 * kp]) = (lw[j] & 0xFFFFu) | (hw[j] << 16);
+        *reinterpret_cast<uint32_t*>(&Vt[dc + 2 * j + 1][2 * kp]) = (lw[j] >> 16) | (hw[j] & 0xFFFF0000u);
+      }
+    }
+    __syncthreads();
+
+    // S^T for two 32-key blocks.
+    floatx16 s0 = {}, s1 = {};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[lq][16 * s + 8 * hi]);
+      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[32 + lq][16 * s + 8 * hi]);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[s], s1, 0, 0, 0);
+    }
+    // scale to the log2 domain, mask keys past T, tile max
+    float mt = kNegBig;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = 8 * (r >> 2) + 4 * hi + (r & 3);
+      float a = s0[r] * scale_log2;
+      float b = s1[r] * scale_log2;
+      if (k0 + kr >= T) a = kNegBig;
+      if (k0 + 32 + kr >= T) b = kNegBig;
+      s0[r] = a;
+      s1[r] = b;
+      mt = fmaxf(mt, fmaxf(a, b));
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = exp2f(m_run - m_new);
+    float lt = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = exp2f(s0[r] - m_new);
+      s1[r] = exp2f(s1[r] - m_new);
+      lt += s0[r] + s1[r];
+    }
+    lt += __shfl_xor(lt, 32, 64);
+    l_run = l_run * alpha + lt;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    }
+    // P^T operands: chunk c covers keys 16c..16c+15 of the tile in the
+    // accumulator's order; registers 8*(c%2)..+7 of block c/2.
+    bf16x8 pc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const floatx16& sb = (c < 2) ? s0 : s1;
+      const int base = 8 * (c & 1);
+      u32x4 w;
+      w.x = pack2(sb[base + 0], sb[base + 1]);
+      w.y = pack2(sb[base + 2], sb[base + 3]);
+      w.z = pack2(sb[base + 4], sb[base + 5]);
+      w.w = pack2(sb[base + 6], sb[base + 7]);
+      pc[c] = __builtin_bit_cast(bf16x8, w);
+    }
+    // O^T += V^T P^T; V^T operand in the same key order: keys 16c + 4*hi + 0..3
+    // and 16c + 8 + 4*hi + 0..3 of the tile.
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int dr = 32 * db + lq;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x2 va = *reinterpret_cast<const u32x2*>(&Vt[dr][16 * c + 4 * hi]);
+        const u32x2 vb = *reinterpret_cast<const u32x2*>(&Vt[dr][16 * c + 8 + 4 * hi]);
+        u32x4 w = {va.x, va.y, vb.x, vb.y};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pc[c], o[db], 0, 0, 0);
+      }
+    }
+  }
+
+  // Normalise and stage the wave's [32 q][128 d] output through LDS.
+  __shared__ __attribute__((aligned(16))) uint16_t Ostage[4][kQW][kD + 8];
+  const float inv_l = 1.0f / l_run;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * db + 8 * (r >> 2) + 4 * hi + (r & 3);
+      Ostage[wave][lq][d] = f2bf(o[db][r] * inv_l);
+    }
+  }
+  __syncthreads();
+  // 32 rows x 128 d = 512 16-byte chunks per wave, 8 per lane.
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int c = lane + 64 * u;
+    const int row = c >> 4;
+    const int dc = (c & 15) * 8;
+    const int q = q0 + row;
+    if (q < T)
+      *reinterpret_cast<u32x4*>(O + (size_t)q * ldo + head * kD + dc) =
+          *reinterpret_cast<const u32x4*>(&Ostage[wave][row][dc]);
+  }
+}
+
+}  // namespace
+
+// Q/K/V/O bf16 [T, ld*] with `heads` heads of 128 columns each.
+hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v, int ldv,
+                                  uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream) {
+  const dim3 grid((unsigned)((T + 4 * kQW - 1) / (4 * kQW)), (unsigned)heads);
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(flash_attn_bf16_kernel, grid, dim3(256), 0, stream, q, k, v, o, T, ldq, ldk, ldv, ldo,
+                     scale_log2);
+  return hipGetLastError();
+}
+
+}  // namespace prom

@@ -1,0 +1,353 @@
+// Gemma-style fp32 decoder layer on one HIP stream.
+//
+// The reference has no Gemma-2B layer; its Gemma-4-E2B pieces fix
+// the conventions used here: RMSNorm y = x*inv*w with no mean subtraction
+// (reactor_vulkan_gemma4e2b.c:286-319), half-split RoPE pairing
+// (gemma4e2b_m1_rtx.go:834-861), multi-query scores with every query head on
+// KV head 0 and scale 1/sqrt(head_dim) = 0.0625 (gemma4e2b_m1_rtx.go:863-883).
+// GeGLU uses the tanh-approximate GELU Gemma uses; the causal mask is textbook.
+//
+// MI355X design: every matrix product is the fp32 MFMA SGEMM
+// (sgemm_f32.hip) on row-major operands with strides:
+//   1 RMSNorm                       x -> n1                        (reduction.hip)
+//   2 QKV projection, fused         n1 @ Wqkv -> qkv [T, (Hq+2)d]
+//   3 RoPE + split                  qkv -> Q [T, Hq*d] (scaled by 1/sqrt d, exact
+//                                   power of two), K^T [d, T], V [T, d]
+//   4 scores, all heads in one GEMM Q viewed as [T*Hq, d] @ K^T -> S [T*Hq, T]
+//     (multi-query: all query heads share K, so rows (t, h) stack into one
+//     matrix; S is 8 MB at T=512 and stays in MALL)
+//   5 causal softmax rows           row (t, h) keeps keys 0..t
+//   6 P @ V                         [T*Hq, T] @ [T, d] -> O viewed as [T, Hq*d]
+//   7 output projection + residual  x + O @ Wo -> h   (residual fused in the epilogue)
+//   8 RMSNorm                       h -> n2
+//   9 gate|up projection, fused     n2 @ Wgu -> G [T, 2F]
+//  10 GeGLU                         gelu_tanh(G[:, :F]) * G[:, F:] -> A [T, F]
+//  11 down projection + residual    h + A @ Wdown -> out
+#include <math.h>
+#include <string.h>
+
+#include "reactor_internal.h"
+
+namespace prom {
+namespace {
+
+// qkv [T, ldq]: Q heads at column h*d, K at Hq*d, V at (Hq+1)*d.
+__global__ __launch_bounds__(256) void gemma_rope_split_kernel(const float* __restrict__ qkv, int ldq, int T, int Hq,
+                                                               int d, int pos0, float base, float q_scale,
+                                                               float* __restrict__ Q, float* __restrict__ Kt,
+                                                               float* __restrict__ V) {
+  const int half = d >> 1;
+  const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (idx < T * half) {
+    const int t = idx / half;
+    const int i = idx - t * half;
+    // angle = position * base^(-2i/d), evaluated in binary64 then rounded.
+    const double inv_freq = pow((double)base, -2.0 * (double)i / (double)d);
+    const double angle = (double)(pos0 + t) * inv_freq;
+    const float c = (float)cos(angle);
+    const float s = (float)sin(angle);
+    const float* row = qkv + (size_t)t * ldq;
+    for (int h = 0; h < Hq; ++h) {
+      const float x1 = row[h * d + i];
+      const float x2 = row[h * d + i + half];
+      Q[(size_t)t * Hq * d + h * d + i] = (x1 * c - x2 * s) * q_scale;
+      Q[(size_t)t * Hq * d + h * d + i + half] = (x2 * c + x1 * s) * q_scale;
+    }
+    const float k1 = row[Hq * d + i];
+    const float k2 = row[Hq * d + i + half];
+    Kt[(size_t)i * T + t] = k1 * c - k2 * s;
+    Kt[(size_t)(i + half) * T + t] = k2 * c + k1 * s;
+  }
+  if (idx < T * d) {
+    const int t = idx / d;
+    const int j = idx - t * d;
+    V[(size_t)t * d + j] = qkv[(size_t)t * ldq + (Hq + 1) * d + j];
+  }
+}
+
+// Row r of S [rows, width] belongs to query token t = r / heads_per_token at
+// position t; it keeps columns 0..t and zeroes the rest.  Stable softmax with
+// expf and a binary64 row sum, as the fused softmax kernel.
+__global__ __launch_bounds__(256) void causal_softmax_kernel(float* __restrict__ S, int rows, int width,
+                                                             int heads_per_token) {
+  const int wave = (int)(threadIdx.x >> 6);
+  const int lane = (int)(threadIdx.x & 63);
+  const int r = (int)blockIdx.x * 4 + wave;
+  if (r >= rows) return;
+  float* row = S + (size_t)r * width;
+  const int valid = min(width, r / heads_per_token + 1);
+  float m = row[0];
+  for (int j = lane; j < valid; j += 64) m = row[j] > m ? row[j] : m;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(m, off, 64);
+    m = o > m ? o : m;
+  }
+  double sum = 0.0;
+  for (int j = lane; j < valid; j += 64) sum += (double)expf(row[j] - m);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  const float denom = (float)sum;
+  for (int j = lane; j < width; j += 64) row[j] = j < valid ? expf(row[j] - m) / denom : 0.0f;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
+}
+
+// G [T, 2F] (gate | up) -> A [T, F]
+__global__ __launch_bounds__(256) void geglu_kernel(const float* __restrict__ G, float* __restrict__ A, int T, int F) {
+  const size_t total = (size_t)T * F;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = idx / F;
+    const size_t i = idx - t * F;
+    const float g = G[t * 2 * F + i];
+    const float u = G[t * 2 * F + F + i];
+    A[idx] = gelu_tanh(g) * u;
+  }
+}
+
+struct LayerShape {
+  int T, D, Hq, d, F, nqkv;
+};
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Workspace layout (floats): n1 [T,D] | qkv [T,nqkv] | Q [T,Hq*d] | Kt [d,T] | V [T,d]
+// | S [T*Hq,T] | O [T,Hq*d] | h [T,D] | n2 [T,D] | G [T,2F] | A [T,F]
+size_t layer_workspace_bytes(const LayerShape& s, size_t offsets[11]) {
+  const size_t sizes[11] = {(size_t)s.T * s.D,        (size_t)s.T * s.nqkv, (size_t)s.T * s.Hq * s.d,
+                            (size_t)s.d * s.T,        (size_t)s.T * s.d,    (size_t)s.T * s.Hq * s.T,
+                            (size_t)s.T * s.Hq * s.d, (size_t)s.T * s.D,    (size_t)s.T * s.D,
+                            (size_t)s.T * 2 * s.F,    (size_t)s.T * s.F};
+  size_t off = 0;
+  for (int i = 0; i < 11; ++i) {
+    offsets[i] = off;
+    off += align_up(sizes[i] * sizeof(float));
+  }
+  return off;
+}
+
+int32_t validate_layer(const PrometheusDecoderLayerF32Request* r) {
+  if (r == nullptr || r->struct_size < sizeof(*r)) return PROM_BLOCK_DETAIL_INVALID_REQUEST;
+  if (!r->input || !r->attn_norm_weight || !r->w_qkv || !r->w_o || !r->ffn_norm_weight || !r->w_gate_up ||
+      !r->w_down || !r->output)
+    return PROM_BLOCK_DETAIL_INVALID_REQUEST;
+  if (r->tokens == 0 || r->hidden == 0 || r->q_heads == 0 || r->head_dim == 0 || r->ffn_hidden == 0 ||
+      (r->head_dim & 1u) != 0)
+    return PROM_BLOCK_DETAIL_SHAPE;
+  if (r->kv_heads != 1) return PROM_BLOCK_DETAIL_UNSUPPORTED;
+  if (!isfinite(r->rms_epsilon) || r->rms_epsilon <= 0.f || !isfinite(r->rope_base) || r->rope_base <= 0.f)
+    return PROM_BLOCK_DETAIL_INVALID_REQUEST;
+  const uint64_t lim = 1ull << 31;
+  if ((uint64_t)r->tokens * r->q_heads * r->tokens >= lim || (uint64_t)r->tokens * 2 * r->ffn_hidden >= lim ||
+      (uint64_t)r->hidden * 2 * r->ffn_hidden >= lim || (uint64_t)r->tokens * r->hidden >= lim)
+    return PROM_BLOCK_DETAIL_SHAPE;
+  return 0;
+}
+
+// Enqueues the whole layer; all pointers are device pointers.
+hipError_t enqueue_layer(const PrometheusDecoderLayerF32Request* r, char* ws, const size_t off[11], hipStream_t st,
+                         uint32_t* launches) {
+  const LayerShape s{(int)r->tokens, (int)r->hidden, (int)r->q_heads, (int)r->head_dim, (int)r->ffn_hidden,
+                     (int)((r->q_heads + 2) * r->head_dim)};
+  float* n1 = reinterpret_cast<float*>(ws + off[0]);
+  float* qkv = reinterpret_cast<float*>(ws + off[1]);
+  float* Q = reinterpret_cast<float*>(ws + off[2]);
+  float* Kt = reinterpret_cast<float*>(ws + off[3]);
+  float* V = reinterpret_cast<float*>(ws + off[4]);
+  float* S = reinterpret_cast<float*>(ws + off[5]);
+  float* O = reinterpret_cast<float*>(ws + off[6]);
+  float* h = reinterpret_cast<float*>(ws + off[7]);
+  float* n2 = reinterpret_cast<float*>(ws + off[8]);
+  float* G = reinterpret_cast<float*>(ws + off[9]);
+  float* A = reinterpret_cast<float*>(ws + off[10]);
+  hipError_t e;
+  uint32_t n = 0;
+#define PROM_STEP(call)             \
+  do {                              \
+    e = (call);                     \
+    if (e != hipSuccess) return e;  \
+    ++n;                            \
+  } while (0)
+  PROM_STEP(launch_rmsnorm(r->input, r->attn_norm_weight, n1, nullptr, s.T, s.D, s.D, r->rms_epsilon, st));
+  PROM_STEP(launch_sgemm_f32_ex(n1, s.D, r->w_qkv, s.nqkv, qkv, s.nqkv, s.T, s.nqkv, s.D, nullptr, 0, st, nullptr));
+  {
+    const int threads = s.T * s.d;  // covers T*d/2 rope pairs and T*d V elements
+    const float q_scale = 1.0f / sqrtf((float)s.d);
+    hipLaunchKernelGGL(gemma_rope_split_kernel, dim3((threads + 255) / 256), dim3(256), 0, st, qkv, s.nqkv, s.T, s.Hq,
+                       s.d, (int)r->position_offset, r->rope_base, q_scale, Q, Kt, V);
+    PROM_STEP(hipGetLastError());
+  }
+  PROM_STEP(launch_sgemm_f32_ex(Q, s.d, Kt, s.T, S, s.T, s.T * s.Hq, s.T, s.d, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(causal_softmax_kernel, dim3((s.T * s.Hq + 3) / 4), dim3(256), 0, st, S, s.T * s.Hq, s.T, s.Hq);
+  PROM_STEP(hipGetLastError());
+  PROM_STEP(launch_sgemm_f32_ex(S, s.T, V, s.d, O, s.d, s.T * s.Hq, s.d, s.T, nullptr, 0, st, nullptr));
+  PROM_STEP(launch_sgemm_f32_ex(O, s.Hq * s.d, r->w_o, s.D, h, s.D, s.T, s.D, s.Hq * s.d, r->input, s.D, st, nullptr));
+  PROM_STEP(launch_rmsnorm(h, r->ffn_norm_weight, n2, nullptr, s.T, s.D, s.D, r->rms_epsilon, st));
+  PROM_STEP(launch_sgemm_f32_ex(n2, s.D, r->w_gate_up, 2 * s.F, G, 2 * s.F, s.T, 2 * s.F, s.D, nullptr, 0, st, nullptr));
+  {
+    const size_t total = (size_t)s.T * s.F;
+    const unsigned blocks = (unsigned)min((size_t)65536, (total + 255) / 256);
+    hipLaunchKernelGGL(geglu_kernel, dim3(blocks), dim3(256), 0, st, G, A, s.T, s.F);
+    PROM_STEP(hipGetLastError());
+  }
+  PROM_STEP(launch_sgemm_f32_ex(A, s.F, r->w_down, s.D, r->output, s.D, s.T, s.D, s.F, h, s.D, st, nullptr));
+#undef PROM_STEP
+  if (launches) *launches = n;
+  return hipSuccess;
+}
+
+LayerShape shape_of(const PrometheusDecoderLayerF32Request* r) {
+  return LayerShape{(int)r->tokens, (int)r->hidden, (int)r->q_heads, (int)r->head_dim, (int)r->ffn_hidden,
+                    (int)((r->q_heads + 2) * r->head_dim)};
+}
+
+void result_init(PrometheusBlockResult* res) {
+  memset(res, 0, sizeof(*res));
+  res->struct_size = sizeof(*res);
+}
+
+}  // namespace
+}  // namespace prom
+
+using namespace prom;
+
+extern "C" {
+
+PROM_REACTOR_API int prometheus_reactor_runtime_decoder_layer_f32_device(
+    void* handle, const PrometheusDecoderLayerF32Request* request, PrometheusBlockResult* out_result) {
+  PrometheusBlockResult local;
+  PrometheusBlockResult* res = out_result ? out_result : &local;
+  result_init(res);
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = PROM_INVALID_HANDLE;
+    return PROM_INVALID_HANDLE;
+  }
+  const int32_t d = validate_layer(request);
+  if (d != 0) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = d;
+    return PROM_ERROR;
+  }
+  if (!rt->available) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = rt->init_detail;
+    return PROM_ERROR;
+  }
+  size_t off[11];
+  const size_t ws_bytes = layer_workspace_bytes(shape_of(request), off);
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  char* ws = static_cast<char*>(staging(4, ws_bytes));
+  if (ws == nullptr) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = PROM_DETAIL_HIP_ALLOC_FAILED;
+    return PROM_ERROR;
+  }
+  res->workspace_bytes = ws_bytes;
+  uint32_t launches = 0;
+  if (enqueue_layer(request, ws, off, cx.stream, &launches) != hipSuccess) {
+    res->stage = PROM_STAGE_SUBMIT;
+    res->detail_code = PROM_DETAIL_HIP_LAUNCH_FAILED;
+    return PROM_ERROR;
+  }
+  res->kernel_launches = launches;
+  res->stage = PROM_STAGE_SUBMIT;
+  res->detail_code = PROM_DETAIL_PATH_HIP_MFMA_F32;
+  return PROM_OK;
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_decoder_layer_f32(void* handle,
+                                                                  const PrometheusDecoderLayerF32Request* request,
+                                                                  PrometheusBlockResult* out_result) {
+  PrometheusBlockResult local;
+  PrometheusBlockResult* res = out_result ? out_result : &local;
+  result_init(res);
+  const uint64_t t0 = wall_ns();
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = PROM_INVALID_HANDLE;
+    return PROM_INVALID_HANDLE;
+  }
+  const int32_t d = validate_layer(request);
+  if (d != 0) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = d;
+    return PROM_ERROR;
+  }
+  if (!rt->available) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = rt->init_detail;
+    return PROM_ERROR;
+  }
+  const PrometheusDecoderLayerF32Request& r = *request;
+  const LayerShape s = shape_of(request);
+  // Device copies of every host array, packed into one staging buffer.
+  const size_t sizes[8] = {(size_t)s.T * s.D, (size_t)s.D, (size_t)s.D * s.nqkv, (size_t)s.Hq * s.d * s.D,
+                           (size_t)s.D,       (size_t)s.D * 2 * s.F, (size_t)s.F * s.D, (size_t)s.T * s.D};
+  const float* srcs[7] = {r.input, r.attn_norm_weight, r.w_qkv, r.w_o, r.ffn_norm_weight, r.w_gate_up, r.w_down};
+  size_t offs[8], total = 0;
+  for (int i = 0; i < 8; ++i) {
+    offs[i] = total;
+    total += align_up(sizes[i] * sizeof(float));
+  }
+  size_t woff[11];
+  const size_t ws_bytes = layer_workspace_bytes(s, woff);
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  char* dev = static_cast<char*>(staging(5, total));
+  char* ws = static_cast<char*>(staging(4, ws_bytes));
+  if (dev == nullptr || ws == nullptr) {
+    res->stage = PROM_STAGE_TRANSFER_IN;
+    res->detail_code = PROM_DETAIL_HIP_ALLOC_FAILED;
+    return PROM_ERROR;
+  }
+  res->stage = PROM_STAGE_TRANSFER_IN;
+  for (int i = 0; i < 7; ++i) {
+    if (hipMemcpyAsync(dev + offs[i], srcs[i], sizes[i] * sizeof(float), hipMemcpyHostToDevice, cx.stream) !=
+        hipSuccess) {
+      res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
+      return PROM_ERROR;
+    }
+  }
+  PrometheusDecoderLayerF32Request dr = r;
+  dr.input = reinterpret_cast<const float*>(dev + offs[0]);
+  dr.attn_norm_weight = reinterpret_cast<const float*>(dev + offs[1]);
+  dr.w_qkv = reinterpret_cast<const float*>(dev + offs[2]);
+  dr.w_o = reinterpret_cast<const float*>(dev + offs[3]);
+  dr.ffn_norm_weight = reinterpret_cast<const float*>(dev + offs[4]);
+  dr.w_gate_up = reinterpret_cast<const float*>(dev + offs[5]);
+  dr.w_down = reinterpret_cast<const float*>(dev + offs[6]);
+  dr.output = reinterpret_cast<float*>(dev + offs[7]);
+  res->stage = PROM_STAGE_SUBMIT;
+  uint32_t launches = 0;
+  (void)hipEventRecord(cx.op_begin, cx.stream);
+  if (enqueue_layer(&dr, ws, woff, cx.stream, &launches) != hipSuccess) {
+    (void)hipStreamSynchronize(cx.stream);
+    res->detail_code = PROM_DETAIL_HIP_LAUNCH_FAILED;
+    return PROM_ERROR;
+  }
+  (void)hipEventRecord(cx.op_end, cx.stream);
+  res->stage = PROM_STAGE_TRANSFER_OUT;
+  if (hipMemcpyAsync(r.output, dr.output, sizes[7] * sizeof(float), hipMemcpyDeviceToHost, cx.stream) != hipSuccess ||
+      hipStreamSynchronize(cx.stream) != hipSuccess) {
+    res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
+    return PROM_ERROR;
+  }
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, cx.op_begin, cx.op_end) == hipSuccess) res->gpu_duration_ns = (uint64_t)(ms * 1.0e6);
+  res->kernel_launches = launches;
+  res->workspace_bytes = ws_bytes;
+  res->detail_code = PROM_DETAIL_PATH_HIP_MFMA_F32;
+  res->output_written = 1;
+  res->end_to_end_ns = wall_ns() - t0;
+  return PROM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,532 @@
+// Z-Image-style single-stream DiT block in bf16.
+//
+// Stage definitions follow the reference's canonical block
+// (internal/prometheus/zimage/canonical_reference.go:315-480) and its joint
+// main-transformer variant (tools/python/zimage/zimage_main_transformer_canonical.py:178-277):
+// adaLN chunks (scaleA, gateA, scaleM, gateM) with 1+scale and tanh(gate),
+// RMSNorm without mean subtraction, fused QKV with [Q|K|V] column order, per-head
+// Q/K RMSNorm, 3-axis interleaved-pair RoPE, full softmax attention, gated
+// residuals with a second RMSNorm, SwiGLU FFN.
+//
+// MI355X design: the four projections are bf16 MFMA GEMMs (gemm_bf16.hip) with
+// fp32 accumulation; attention is the flash kernel (attention_bf16.hip); the
+// per-row work between them is fused into four one-pass row kernels (one wave
+// per row, the row held in registers, 128-bit loads):
+//   adaln          m = c @ Wada + b -> modulation vectors       (one thread per column)
+//   norm_mod       a = RMSNorm(x; n1) * scaleA                   -> bf16
+//   qk_norm_rope   per (token, head): RMSNorm(q), RMSNorm(k), RoPE, V copy -> bf16
+//   resid_norm_mod r = x + gateA * RMSNorm(proj; n2)             -> fp32
+//                  f = RMSNorm(r; n3) * scaleM                   -> bf16
+//   swiglu         h = silu(g) * u                                -> bf16
+//   final_resid    out = r + gateM * RMSNorm(w2; n4)              -> fp32
+#include <math.h>
+#include <string.h>
+
+#include "reactor_internal.h"
+
+namespace prom {
+
+hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v, int ldv,
+                                  uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream);
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kRowChunks = 16;  // rows up to 16 * 64 * 4 = 4096 floats stay in registers
+
+__device__ __forceinline__ uint16_t f2bf(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ void store_bf16x4(uint16_t* dst, floatx4 v) {
+  u32x2 w;
+  w.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
+  w.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
+  *reinterpret_cast<u32x2*>(dst) = w;
+}
+
+// mod[j] = b[j] + sum_k c[k] * W[k][j]; chunk 0 and 2 -> 1 + m, chunk 1 and 3 -> tanh(m)
+// (canonical_reference.go:373-383).
+__global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ cond, const uint16_t* __restrict__ W,
+                                                    const float* __restrict__ b, float* __restrict__ mod, int C,
+                                                    int D) {
+  const int j = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (j >= 4 * D) return;
+  float acc = 0.0f;
+  for (int k = 0; k < C; ++k) acc += cond[k] * bf2f(W[(size_t)k * 4 * D + j]);
+  acc += b[j];
+  const int chunk = j / D;
+  mod[j] = (chunk == 0 || chunk == 2) ? 1.0f + acc : tanhf(acc);
+}
+
+// a = RMSNorm(x; w) * scale  -> bf16.  One wave per row, D % 4 == 0, D <= 4096.
+__global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                       const float* __restrict__ scale, uint16_t* __restrict__ out,
+                                                       int T, int D, float eps) {
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int t = (int)blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const int d4 = D >> 2;
+  const floatx4* row = reinterpret_cast<const floatx4*>(x + (size_t)t * D);
+  floatx4 v[kRowChunks];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = c * 64 + lane;
+    if (i < d4) {
+      v[c] = row[i];
+      ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  const floatx4* w4 = reinterpret_cast<const floatx4*>(w);
+  const floatx4* s4 = reinterpret_cast<const floatx4*>(scale);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = c * 64 + lane;
+    if (i < d4) {
+      const floatx4 g = w4[i], sc = s4[i];
+      floatx4 o;
+      o.x = v[c].x * inv * g.x * sc.x;
+      o.y = v[c].y * inv * g.y * sc.y;
+      o.z = v[c].z * inv * g.z * sc.z;
+      o.w = v[c].w * inv * g.w * sc.w;
+      store_bf16x4(out + (size_t)t * D + 4 * i, o);
+    }
+  }
+}
+
+// Per (token, head): q and k RMSNorm over 128 channels, then RoPE on the
+// interleaved pairs (2p, 2p+1); pair p belongs to axis a with local pair
+// index p - offset(a), frequency theta^(-2*pair/width_a), angle coord[t][a]*freq
+// (zimage/canonical_contract.go:66-87, zimage_main_transformer_canonical.py:124-140).
+// One wave per (token, head); lane l owns pair l.  V is copied to bf16.
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ coords,
+                                                           const float* __restrict__ qn, const float* __restrict__ kn,
+                                                           uint16_t* __restrict__ Q, uint16_t* __restrict__ K,
+                                                           uint16_t* __restrict__ V, int T, int H, float eps,
+                                                           float theta, int ax0, int ax1, int ax2) {
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int unit = (int)blockIdx.x * 4 + wave;
+  if (unit >= T * H) return;
+  const int t = unit / H;
+  const int h = unit - t * H;
+  const int D = H * 128;
+  const float* row = qkv + (size_t)t * 3 * D;
+  const int c0 = h * 128 + 2 * lane;
+  // RoPE angle for pair `lane`
+  int axis, width, pair;
+  if (lane < ax0 / 2) {
+    axis = 0; width = ax0; pair = lane;
+  } else if (lane < (ax0 + ax1) / 2) {
+    axis = 1; width = ax1; pair = lane - ax0 / 2;
+  } else {
+    axis = 2; width = ax2; pair = lane - (ax0 + ax1) / 2;
+  }
+  const double freq = pow((double)theta, -2.0 * (double)pair / (double)width);
+  const double angle = (double)coords[(size_t)t * 3 + axis] * freq;
+  const float cs = (float)cos(angle), sn = (float)sin(angle);
+  const float qw0 = qn[2 * lane], qw1 = qn[2 * lane + 1];
+  const float kw0 = kn[2 * lane], kw1 = kn[2 * lane + 1];
+  {
+    const float e = row[c0], o = row[c0 + 1];
+    const float inv = 1.0f / sqrtf(wave_sum(e * e + o * o) / 128.0f + eps);
+    const float ne = e * inv * qw0, no = o * inv * qw1;
+    const uint32_t w = (uint32_t)f2bf(ne * cs - no * sn) | ((uint32_t)f2bf(ne * sn + no * cs) << 16);
+    *reinterpret_cast<uint32_t*>(Q + (size_t)t * D + c0) = w;
+  }
+  {
+    const float e = row[D + c0], o = row[D + c0 + 1];
+    const float inv = 1.0f / sqrtf(wave_sum(e * e + o * o) / 128.0f + eps);
+    const float ne = e * inv * kw0, no = o * inv * kw1;
+    const uint32_t w = (uint32_t)f2bf(ne * cs - no * sn) | ((uint32_t)f2bf(ne * sn + no * cs) << 16);
+    *reinterpret_cast<uint32_t*>(K + (size_t)t * D + c0) = w;
+  }
+  {
+    const float e = row[2 * D + c0], o = row[2 * D + c0 + 1];
+    *reinterpret_cast<uint32_t*>(V + (size_t)t * D + c0) = (uint32_t)f2bf(e) | ((uint32_t)f2bf(o) << 16);
+  }
+}
+
+// r = x + gateA * RMSNorm(proj; n2)  (fp32 out), f = RMSNorm(r; n3) * scaleM (bf16 out)
+__global__ __launch_bounds__(256) void resid_norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ proj,
+                                                             const float* __restrict__ n2, const float* __restrict__ gate,
+                                                             const float* __restrict__ n3, const float* __restrict__ scale,
+                                                             float* __restrict__ r_out, uint16_t* __restrict__ f_out,
+                                                             int T, int D, float eps) {
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int t = (int)blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const int d4 = D >> 2;
+  const floatx4* p4 = reinterpret_cast<const floatx4*>(proj + (size_t)t * D);
+  const floatx4* x4 = reinterpret_cast<const floatx4*>(x + (size_t)t * D);
+  floatx4 v[kRowChunks];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = c * 64 + lane;
+    if (i < d4) {
+      v[c] = p4[i];
+      ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  const floatx4* g4 = reinterpret_cast<const floatx4*>(gate);
+  const floatx4* w4 = reinterpret_cast<const floatx4*>(n2);
+  float ss2 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = c * 64 + lane;
+    if (i < d4) {
+      const floatx4 xv = x4[i], g = g4[i], w = w4[i];
+      floatx4 r;
+      r.x = xv.x + g.x * (v[c].x * inv * w.x);
+      r.y = xv.y + g.y * (v[c].y * inv * w.y);
+      r.z = xv.z + g.z * (v[c].z * inv * w.z);
+      r.w = xv.w + g.w * (v[c].w * inv * w.w);
+      v[c] = r;
+      reinterpret_cast<floatx4*>(r_out + (size_t)t * D)[i] = r;
+      ss2 += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
+    }
+  }
+  ss2 = wave_sum(ss2);
+  const float inv2 = 1.0f / sqrtf(ss2 / (float)D + eps);
+  const floatx4* w3 = reinterpret_cast<const floatx4*>(n3);
+  const floatx4* s4 = reinterpret_cast<const floatx4*>(scale);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = c * 64 + lane;
+    if (i < d4) {
+      const floatx4 w = w3[i], sc = s4[i];
+      floatx4 o;
+      o.x = v[c].x * inv2 * w.x * sc.x;
+      o.y = v[c].y * inv2 * w.y * sc.y;
+      o.z = v[c].z * inv2 * w.z * sc.z;
+      o.w = v[c].w * inv2 * w.w * sc.w;
+      store_bf16x4(f_out + (size_t)t * D + 4 * i, o);
+    }
+  }
+}
+
+// out = r + gateM * RMSNorm(w2; n4)
+__global__ __launch_bounds__(256) void final_resid_kernel(const float* __restrict__ r, const float* __restrict__ w2,
+                                                          const float* __restrict__ n4, const float* __restrict__ gate,
+                                                          float* __restrict__ out, int T, int D, float eps) {
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int t = (int)blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const int d4 = D >> 2;
+  const floatx4* y4 = reinterpret_cast<const floatx4*>(w2 + (size_t)t * D);
+  floatx4 v[kRowChunks];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = c * 64 + lane;
+    if (i < d4) {
+      v[c] = y4[i];
+      ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  const floatx4* r4 = reinterpret_cast<const floatx4*>(r + (size_t)t * D);
+  const floatx4* w4 = reinterpret_cast<const floatx4*>(n4);
+  const floatx4* g4 = reinterpret_cast<const floatx4*>(gate);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = c * 64 + lane;
+    if (i < d4) {
+      const floatx4 rv = r4[i], w = w4[i], g = g4[i];
+      floatx4 o;
+      o.x = rv.x + g.x * (v[c].x * inv * w.x);
+      o.y = rv.y + g.y * (v[c].y * inv * w.y);
+      o.z = rv.z + g.z * (v[c].z * inv * w.z);
+      o.w = rv.w + g.w * (v[c].w * inv * w.w);
+      reinterpret_cast<floatx4*>(out + (size_t)t * D)[i] = o;
+    }
+  }
+}
+
+// G [T, 2F] (w1 | w3) -> h [T, F] bf16: silu(g) * u (canonical_reference.go:457-460)
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ G, uint16_t* __restrict__ Hb, int T,
+                                                     int F) {
+  const int f4 = F >> 2;
+  const size_t total = (size_t)T * f4;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = idx / f4;
+    const size_t i = idx - t * f4;
+    const floatx4 g = reinterpret_cast<const floatx4*>(G + t * 2 * F)[i];
+    const floatx4 u = reinterpret_cast<const floatx4*>(G + t * 2 * F + F)[i];
+    floatx4 o;
+    o.x = g.x / (1.0f + expf(-g.x)) * u.x;
+    o.y = g.y / (1.0f + expf(-g.y)) * u.y;
+    o.z = g.z / (1.0f + expf(-g.z)) * u.z;
+    o.w = g.w / (1.0f + expf(-g.w)) * u.w;
+    store_bf16x4(Hb + t * F + 4 * i, o);
+  }
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+enum { kWsMod, kWsA, kWsQkv, kWsQ, kWsK, kWsV, kWsO, kWsProj, kWsR, kWsF, kWsG, kWsH, kWsW2, kWsCount };
+
+size_t dit_workspace(const PrometheusDitBlockBf16Request* r, size_t off[kWsCount]) {
+  const size_t T = r->tokens, D = r->hidden, F = r->ffn_hidden;
+  const size_t sizes[kWsCount] = {4 * D * 4,  T * D * 2, T * 3 * D * 4, T * D * 2, T * D * 2, T * D * 2, T * D * 2,
+                                  T * D * 4,  T * D * 4, T * D * 2,     T * 2 * F * 4, T * F * 2, T * D * 4};
+  size_t o = 0;
+  for (int i = 0; i < kWsCount; ++i) {
+    off[i] = o;
+    o += align_up(sizes[i]);
+  }
+  return o;
+}
+
+int32_t validate_dit(const PrometheusDitBlockBf16Request* r) {
+  if (r == nullptr || r->struct_size < sizeof(*r)) return PROM_BLOCK_DETAIL_INVALID_REQUEST;
+  if (!r->input || !r->coordinates || !r->condition || !r->w_adaln || !r->b_adaln || !r->attn_norm1 ||
+      !r->attn_norm2 || !r->ffn_norm1 || !r->ffn_norm2 || !r->q_norm || !r->k_norm || !r->w_qkv || !r->w_out ||
+      !r->w_13 || !r->w_2 || !r->output)
+    return PROM_BLOCK_DETAIL_INVALID_REQUEST;
+  if (r->tokens == 0 || r->heads == 0 || r->cond_dim == 0 || r->ffn_hidden == 0) return PROM_BLOCK_DETAIL_SHAPE;
+  if (r->head_dim != 128 || r->hidden != r->heads * 128 || r->hidden > 4096 || (r->ffn_hidden % 8) != 0)
+    return PROM_BLOCK_DETAIL_UNSUPPORTED;
+  if (r->rope_axes[0] + r->rope_axes[1] + r->rope_axes[2] != r->head_dim || (r->rope_axes[0] & 1) ||
+      (r->rope_axes[1] & 1) || (r->rope_axes[2] & 1) || r->rope_axes[0] == 0 || r->rope_axes[1] == 0 ||
+      r->rope_axes[2] == 0)
+    return PROM_BLOCK_DETAIL_SHAPE;
+  if (!isfinite(r->rms_epsilon) || r->rms_epsilon <= 0.f || !isfinite(r->rope_theta) || r->rope_theta <= 0.f)
+    return PROM_BLOCK_DETAIL_INVALID_REQUEST;
+  const uint64_t lim = 1ull << 31;
+  if ((uint64_t)r->tokens * 2 * r->ffn_hidden >= lim || (uint64_t)r->tokens * 3 * r->hidden >= lim)
+    return PROM_BLOCK_DETAIL_SHAPE;
+  return 0;
+}
+
+hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const size_t off[kWsCount], hipStream_t st,
+                       uint32_t* launches) {
+  const int T = (int)r->tokens, D = (int)r->hidden, H = (int)r->heads, F = (int)r->ffn_hidden, C = (int)r->cond_dim;
+  const float eps = r->rms_epsilon;
+  float* mod = reinterpret_cast<float*>(ws + off[kWsMod]);
+  uint16_t* A = reinterpret_cast<uint16_t*>(ws + off[kWsA]);
+  float* qkv = reinterpret_cast<float*>(ws + off[kWsQkv]);
+  uint16_t* Q = reinterpret_cast<uint16_t*>(ws + off[kWsQ]);
+  uint16_t* K = reinterpret_cast<uint16_t*>(ws + off[kWsK]);
+  uint16_t* V = reinterpret_cast<uint16_t*>(ws + off[kWsV]);
+  uint16_t* O = reinterpret_cast<uint16_t*>(ws + off[kWsO]);
+  float* proj = reinterpret_cast<float*>(ws + off[kWsProj]);
+  float* R = reinterpret_cast<float*>(ws + off[kWsR]);
+  uint16_t* Fb = reinterpret_cast<uint16_t*>(ws + off[kWsF]);
+  float* G = reinterpret_cast<float*>(ws + off[kWsG]);
+  uint16_t* Hb = reinterpret_cast<uint16_t*>(ws + off[kWsH]);
+  float* W2 = reinterpret_cast<float*>(ws + off[kWsW2]);
+  const float* scaleA = mod;
+  const float* gateA = mod + D;
+  const float* scaleM = mod + 2 * D;
+  const float* gateM = mod + 3 * D;
+  hipError_t e;
+  uint32_t n = 0;
+#define PROM_STEP(call)            \
+  do {                             \
+    e = (call);                    \
+    if (e != hipSuccess) return e; \
+    ++n;                           \
+  } while (0)
+  const dim3 rows((T + 3) / 4), blk(256);
+  hipLaunchKernelGGL(adaln_kernel, dim3((4 * D + 255) / 256), blk, 0, st, r->condition, r->w_adaln, r->b_adaln, mod, C, D);
+  PROM_STEP(hipGetLastError());
+  hipLaunchKernelGGL(norm_mod_kernel, rows, blk, 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
+  PROM_STEP(hipGetLastError());
+  PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, qkv, nullptr, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, r->coordinates, r->q_norm, r->k_norm,
+                     Q, K, V, T, H, eps, r->rope_theta, (int)r->rope_axes[0], (int)r->rope_axes[1],
+                     (int)r->rope_axes[2]);
+  PROM_STEP(hipGetLastError());
+  PROM_STEP(launch_flash_attn_bf16(Q, D, K, D, V, D, O, D, T, H, 1.0f / sqrtf(128.0f), st));
+  PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, proj, nullptr, D, T, D, D, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(resid_norm_mod_kernel, rows, blk, 0, st, r->input, proj, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
+                     R, Fb, T, D, eps);
+  PROM_STEP(hipGetLastError());
+  PROM_STEP(launch_gemm_bf16_ex(Fb, D, r->w_13, 2 * F, G, nullptr, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
+  {
+    const size_t total = (size_t)T * (F / 4);
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)std::min((size_t)65536, (total + 255) / 256)), blk, 0, st, G, Hb,
+                       T, F);
+    PROM_STEP(hipGetLastError());
+  }
+  PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, W2, nullptr, D, T, D, F, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(final_resid_kernel, rows, blk, 0, st, R, W2, r->ffn_norm2, gateM, r->output, T, D, eps);
+  PROM_STEP(hipGetLastError());
+#undef PROM_STEP
+  if (launches) *launches = n;
+  return hipSuccess;
+}
+
+void result_init(PrometheusBlockResult* res) {
+  memset(res, 0, sizeof(*res));
+  res->struct_size = sizeof(*res);
+}
+
+}  // namespace
+}  // namespace prom
+
+using namespace prom;
+
+extern "C" {
+
+PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16_device(void* handle,
+                                                                      const PrometheusDitBlockBf16Request* request,
+                                                                      PrometheusBlockResult* out_result) {
+  PrometheusBlockResult local;
+  PrometheusBlockResult* res = out_result ? out_result : &local;
+  result_init(res);
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = PROM_INVALID_HANDLE;
+    return PROM_INVALID_HANDLE;
+  }
+  const int32_t d = validate_dit(request);
+  if (d != 0) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = d;
+    return PROM_ERROR;
+  }
+  if (!rt->available) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = rt->init_detail;
+    return PROM_ERROR;
+  }
+  size_t off[kWsCount];
+  const size_t ws_bytes = dit_workspace(request, off);
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  char* ws = static_cast<char*>(staging(4, ws_bytes));
+  if (ws == nullptr) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = PROM_DETAIL_HIP_ALLOC_FAILED;
+    return PROM_ERROR;
+  }
+  res->workspace_bytes = ws_bytes;
+  uint32_t launches = 0;
+  if (enqueue_dit(request, ws, off, cx.stream, &launches) != hipSuccess) {
+    res->stage = PROM_STAGE_SUBMIT;
+    res->detail_code = PROM_DETAIL_HIP_LAUNCH_FAILED;
+    return PROM_ERROR;
+  }
+  res->kernel_launches = launches;
+  res->stage = PROM_STAGE_SUBMIT;
+  res->detail_code = PROM_DETAIL_PATH_HIP_MFMA_BF16;
+  return PROM_OK;
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16(void* handle, const PrometheusDitBlockBf16Request* request,
+                                                               PrometheusBlockResult* out_result) {
+  PrometheusBlockResult local;
+  PrometheusBlockResult* res = out_result ? out_result : &local;
+  result_init(res);
+  const uint64_t t0 = wall_ns();
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = PROM_INVALID_HANDLE;
+    return PROM_INVALID_HANDLE;
+  }
+  const int32_t d = validate_dit(request);
+  if (d != 0) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = d;
+    return PROM_ERROR;
+  }
+  if (!rt->available) {
+    res->stage = PROM_STAGE_INIT;
+    res->detail_code = rt->init_detail;
+    return PROM_ERROR;
+  }
+  const PrometheusDitBlockBf16Request& r = *request;
+  const size_t T = r.tokens, D = r.hidden, F = r.ffn_hidden, C = r.cond_dim;
+  // Host arrays: byte sizes in request order.
+  const void* srcs[16] = {r.input,     r.coordinates, r.condition, r.w_adaln, r.b_adaln, r.attn_norm1,
+                          r.attn_norm2, r.ffn_norm1,  r.ffn_norm2, r.q_norm,  r.k_norm,  r.w_qkv,
+                          r.w_out,     r.w_13,        r.w_2,       nullptr};
+  const size_t bytes[16] = {T * D * 4, T * 3 * 4, C * 4, C * 4 * D * 2, 4 * D * 4, D * 4, D * 4, D * 4, D * 4,
+                            128 * 4,   128 * 4,   D * 3 * D * 2, D * D * 2, D * 2 * F * 2, F * D * 2, T * D * 4};
+  size_t offs[16], total = 0;
+  for (int i = 0; i < 16; ++i) {
+    offs[i] = total;
+    total += align_up(bytes[i]);
+  }
+  size_t woff[kWsCount];
+  const size_t ws_bytes = dit_workspace(request, woff);
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  char* dev = static_cast<char*>(staging(5, total));
+  char* ws = static_cast<char*>(staging(4, ws_bytes));
+  if (dev == nullptr || ws == nullptr) {
+    res->stage = PROM_STAGE_TRANSFER_IN;
+    res->detail_code = PROM_DETAIL_HIP_ALLOC_FAILED;
+    return PROM_ERROR;
+  }
+  res->stage = PROM_STAGE_TRANSFER_IN;
+  for (int i = 0; i < 15; ++i) {
+    if (hipMemcpyAsync(dev + offs[i], srcs[i], bytes[i], hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+      res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
+      return PROM_ERROR;
+    }
+  }
+  PrometheusDitBlockBf16Request dr = r;
+  dr.input = reinterpret_cast<const float*>(dev + offs[0]);
+  dr.coordinates = reinterpret_cast<const float*>(dev + offs[1]);
+  dr.condition = reinterpret_cast<const float*>(dev + offs[2]);
+  dr.w_adaln = reinterpret_cast<const uint16_t*>(dev + offs[3]);
+  dr.b_adaln = reinterpret_cast<const float*>(dev + offs[4]);
+  dr.attn_norm1 = reinterpret_cast<const float*>(dev + offs[5]);
+  dr.attn_norm2 = reinterpret_cast<const float*>(dev + offs[6]);
+  dr.ffn_norm1 = reinterpret_cast<const float*>(dev + offs[7]);
+  dr.ffn_norm2 = reinterpret_cast<const float*>(dev + offs[8]);
+  dr.q_norm = reinterpret_cast<const float*>(dev + offs[9]);
+  dr.k_norm = reinterpret_cast<const float*>(dev + offs[10]);
+  dr.w_qkv = reinterpret_cast<const uint16_t*>(dev + offs[11]);
+  dr.w_out = reinterpret_cast<const uint16_t*>(dev + offs[12]);
+  dr.w_13 = reinterpret_cast<const uint16_t*>(dev + offs[13]);
+  dr.w_2 = reinterpret_cast<const uint16_t*>(dev + offs[14]);
+  dr.output = reinterpret_cast<float*>(dev + offs[15]);
+  res->stage = PROM_STAGE_SUBMIT;
+  uint32_t launches = 0;
+  (void)hipEventRecord(cx.op_begin, cx.stream);
+  if (enqueue_dit(&dr, ws, woff, cx.stream, &launches) != hipSuccess) {
+    (void)hipStreamSynchronize(cx.stream);
+    res->detail_code = PROM_DETAIL_HIP_LAUNCH_FAILED;
+    return PROM_ERROR;
+  }
+  (void)hipEventRecord(cx.op_end, cx.stream);
+  res->stage = PROM_STAGE_TRANSFER_OUT;
+  if (hipMemcpyAsync(r.output, dr.output, bytes[15], hipMemcpyDeviceToHost, cx.stream) != hipSuccess ||
+      hipStreamSynchronize(cx.stream) != hipSuccess) {
+    res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
+    return PROM_ERROR;
+  }
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, cx.op_begin, cx.op_end) == hipSuccess) res->gpu_duration_ns = (uint64_t)(ms * 1.0e6);
+  res->kernel_launches = launches;
+  res->workspace_bytes = ws_bytes;
+  res->detail_code = PROM_DETAIL_PATH_HIP_MFMA_BF16;
+  res->output_written = 1;
+  res->end_to_end_ns = wall_ns() - t0;
+  return PROM_OK;
+}
+
+}  // extern "C"

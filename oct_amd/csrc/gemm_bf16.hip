@@ -28,6 +28,12 @@ constexpr int kBK = 64;
 constexpr int kLds = kBK + 8;  // row pitch in bf16 elements (144 bytes, 16-byte aligned)
 constexpr int kGroupM = 8;
 
+// Round-to-nearest-even fp32 -> bf16, as gemma4e2b_m1_rtx.go:1009-1014 (finite inputs).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+}
+
 __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int* tn) {
   const int num_tiles = tiles_m * tiles_n;
   int pid = (int)blockIdx.x;
@@ -41,11 +47,15 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int*
   *tn = in_group / group_m;
 }
 
+// Strides are leading dimensions in elements.  Epilogue: v = A@B (+ R when R is
+// non-null, R may alias C); stored as fp32 into C, or as bf16 (round to nearest
+// even) into Cb when Cb is non-null.
 template <bool kVec>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma_kernel(const uint16_t* __restrict__ A,
-                                                                const uint16_t* __restrict__ B,
-                                                                float* __restrict__ C, int M, int N, int K,
-                                                                int tiles_m, int tiles_n) {
+                                                                const uint16_t* __restrict__ B, float* C,
+                                                                int M, int N, int K, int tiles_m, int tiles_n,
+                                                                int lda, int ldb, int ldc, const float* R, int ldr,
+                                                                uint16_t* Cb) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM][kLds];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kBN][kLds];
 
@@ -73,11 +83,11 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma_kernel(const uint16_t* 
       const int gk = k0 + a_k + 8 * h;
       u32x4 v = {0u, 0u, 0u, 0u};
       if constexpr (kVec) {
-        if (gr < M && gk < K) v = *reinterpret_cast<const u32x4*>(A + (size_t)gr * K + gk);
+        if (gr < M && gk < K) v = *reinterpret_cast<const u32x4*>(A + (size_t)gr * lda + gk);
       } else {
         uint16_t e[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) e[j] = (gr < M && gk + j < K) ? A[(size_t)gr * K + gk + j] : (uint16_t)0;
+        for (int j = 0; j < 8; ++j) e[j] = (gr < M && gk + j < K) ? A[(size_t)gr * lda + gk + j] : (uint16_t)0;
         v.x = (uint32_t)e[0] | ((uint32_t)e[1] << 16);
         v.y = (uint32_t)e[2] | ((uint32_t)e[3] << 16);
         v.z = (uint32_t)e[4] | ((uint32_t)e[5] << 16);
@@ -95,11 +105,11 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma_kernel(const uint16_t* 
         const int gk = k0 + 2 * kp + p;
         u32x4 v = {0u, 0u, 0u, 0u};
         if constexpr (kVec) {
-          if (gk < K && gn < N) v = *reinterpret_cast<const u32x4*>(B + (size_t)gk * N + gn);
+          if (gk < K && gn < N) v = *reinterpret_cast<const u32x4*>(B + (size_t)gk * ldb + gn);
         } else {
           uint16_t e[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) e[j] = (gk < K && gn + j < N) ? B[(size_t)gk * N + gn + j] : (uint16_t)0;
+          for (int j = 0; j < 8; ++j) e[j] = (gk < K && gn + j < N) ? B[(size_t)gk * ldb + gn + j] : (uint16_t)0;
           v.x = (uint32_t)e[0] | ((uint32_t)e[1] << 16);
           v.y = (uint32_t)e[2] | ((uint32_t)e[3] << 16);
           v.z = (uint32_t)e[4] | ((uint32_t)e[5] << 16);
@@ -171,7 +181,14 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma_kernel(const uint16_t* 
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = row0 + wm * 64 + mi * 32 + 8 * (r >> 2) + lgrp + (r & 3);
-      if (row < M) C[(size_t)row * N + col] = acc[r];
+      if (row < M) {
+        float v = acc[r];
+        if (R != nullptr) v += R[(size_t)row * ldr + col];
+        if (Cb != nullptr)
+          Cb[(size_t)row * ldc + col] = f32_to_bf16_rne(v);
+        else
+          C[(size_t)row * ldc + col] = v;
+      }
     }
   };
   store_block(acc00, 0, 0);
@@ -184,20 +201,26 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 }  // namespace
 
-hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
-                            hipStream_t stream, int* path_detail) {
+hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, int ldb, float* c, uint16_t* cb,
+                               int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
+                               hipStream_t stream, int* path_detail) {
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const dim3 grid((unsigned)(tiles_m * tiles_n));
-  const bool vec = (k % 8 == 0) && (n % 8 == 0) && aligned16(a) && aligned16(b);
+  const bool vec = (k % 8 == 0) && (n % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(a) && aligned16(b);
   if (vec)
     hipLaunchKernelGGL(gemm_bf16_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n);
+                       tiles_m, tiles_n, lda, ldb, ldc, residual, ldr, cb);
   else
     hipLaunchKernelGGL(gemm_bf16_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n);
+                       tiles_m, tiles_n, lda, ldb, ldc, residual, ldr, cb);
   if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_BF16;
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                            hipStream_t stream, int* path_detail) {
+  return launch_gemm_bf16_ex(a, (int)k, b, (int)n, c, nullptr, (int)n, m, n, k, nullptr, 0, stream, path_detail);
 }
 
 }  // namespace prom

@@ -18,7 +18,7 @@ namespace prom {
 
 constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
-constexpr uint32_t kStagingSlots = 4;
+constexpr uint32_t kStagingSlots = 8;  // 0-3 operand staging, 4 block workspace, 5 block host staging
 
 struct Runtime {
   uint64_t magic;
@@ -61,6 +61,14 @@ uint64_t wall_ns();
 // ---- kernel launchers (enqueue on `stream`; return hipSuccess or the launch error)
 hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
                             hipStream_t stream, int* path_detail);
+// Strided forms used by the transformer blocks (leading dimensions in elements;
+// residual may be null or alias c; gemm_bf16 writes bf16 to cb when non-null).
+hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
+                               uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
+                               int* path_detail);
+hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, int ldb, float* c, uint16_t* cb,
+                               int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
+                               hipStream_t stream, int* path_detail);
 hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
                             hipStream_t stream, int* path_detail);
 hipError_t launch_row_reduction(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,

@@ -50,11 +50,14 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int*
   *tn = in_group / group_m;
 }
 
+// Strides are leading dimensions in elements.  R (may be null) is added in the
+// epilogue: C = A @ B + R; R may alias C (each element is read, then written,
+// by the same lane).
 template <bool kVec>
 __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __restrict__ A,
-                                                                const float* __restrict__ B,
-                                                                float* __restrict__ C, int M, int N, int K,
-                                                                int tiles_m, int tiles_n) {
+                                                                const float* __restrict__ B, float* C, int M,
+                                                                int N, int K, int tiles_m, int tiles_n, int lda,
+                                                                int ldb, int ldc, const float* R, int ldr) {
   __shared__ float As[2][kBK][kLdsA];
   __shared__ float Bs[2][kBK][kLdsB];
 
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
       for (int h = 0; h < 2; ++h) {
         const int gk = k0 + a_k + 4 * h;
         floatx4 v = {0.f, 0.f, 0.f, 0.f};
-        if (gr < M && gk < K) v = *reinterpret_cast<const floatx4*>(A + (size_t)gr * K + gk);
+        if (gr < M && gk < K) v = *reinterpret_cast<const floatx4*>(A + (size_t)gr * lda + gk);
         ra[4 * h + 0] = v.x;
         ra[4 * h + 1] = v.y;
         ra[4 * h + 2] = v.z;
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
       for (int h = 0; h < 2; ++h) {
         const int gk = k0 + b_k + 8 * h;
         floatx4 v = {0.f, 0.f, 0.f, 0.f};
-        if (gk < K && gn < N) v = *reinterpret_cast<const floatx4*>(B + (size_t)gk * N + gn);
+        if (gk < K && gn < N) v = *reinterpret_cast<const floatx4*>(B + (size_t)gk * ldb + gn);
         rb[4 * h + 0] = v.x;
         rb[4 * h + 1] = v.y;
         rb[4 * h + 2] = v.z;
@@ -106,14 +109,14 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int gk = k0 + a_k + j;
-        ra[j] = (gr < M && gk < K) ? A[(size_t)gr * K + gk] : 0.f;
+        ra[j] = (gr < M && gk < K) ? A[(size_t)gr * lda + gk] : 0.f;
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int gk = k0 + b_k + 8 * h;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          rb[4 * h + j] = (gk < K && gn + j < N) ? B[(size_t)gk * N + gn + j] : 0.f;
+          rb[4 * h + j] = (gk < K && gn + j < N) ? B[(size_t)gk * ldb + gn + j] : 0.f;
         }
       }
     }
@@ -169,7 +172,11 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = row0 + wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-      if (row < M) C[(size_t)row * N + col] = acc[r];
+      if (row < M) {
+        float v = acc[r];
+        if (R != nullptr) v += R[(size_t)row * ldr + col];
+        C[(size_t)row * ldc + col] = v;
+      }
     }
   };
   store_block(acc00, 0, 0);
@@ -219,9 +226,10 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 }  // namespace
 
-hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
-                            hipStream_t stream, int* path_detail) {
-  if (n == 1) {
+hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
+                               uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
+                               int* path_detail) {
+  if (n == 1 && residual == nullptr && ldb == 1 && lda == (int)k) {
     const bool vec = (k % 4 == 0) && aligned16(a) && aligned16(b);
     const dim3 grid((m + 3) / 4);
     if (vec)
@@ -234,15 +242,20 @@ hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const dim3 grid((unsigned)(tiles_m * tiles_n));
-  const bool vec = (k % 4 == 0) && (n % 4 == 0) && aligned16(a) && aligned16(b);
+  const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && aligned16(a) && aligned16(b);
   if (vec)
     hipLaunchKernelGGL(sgemm_f32_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n);
+                       tiles_m, tiles_n, lda, ldb, ldc, residual, ldr);
   else
     hipLaunchKernelGGL(sgemm_f32_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n);
+                       tiles_m, tiles_n, lda, ldb, ldc, residual, ldr);
   if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_F32;
   return hipGetLastError();
+}
+
+hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                            hipStream_t stream, int* path_detail) {
+  return launch_sgemm_f32_ex(a, (int)k, b, (int)n, c, (int)n, m, n, k, nullptr, 0, stream, path_detail);
 }
 
 }  // namespace prom

@@ -270,6 +270,74 @@ class PrometheusRmsNormResult(Structure):
     ]
 
 
+class PrometheusDecoderLayerF32Request(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("tokens", c_uint32),
+        ("hidden", c_uint32),
+        ("q_heads", c_uint32),
+        ("kv_heads", c_uint32),
+        ("head_dim", c_uint32),
+        ("ffn_hidden", c_uint32),
+        ("position_offset", c_uint32),
+        ("rms_epsilon", c_float),
+        ("rope_base", c_float),
+        ("input", c_void_p),
+        ("attn_norm_weight", c_void_p),
+        ("w_qkv", c_void_p),
+        ("w_o", c_void_p),
+        ("ffn_norm_weight", c_void_p),
+        ("w_gate_up", c_void_p),
+        ("w_down", c_void_p),
+        ("output", c_void_p),
+    ]
+
+
+class PrometheusDitBlockBf16Request(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("tokens", c_uint32),
+        ("hidden", c_uint32),
+        ("heads", c_uint32),
+        ("head_dim", c_uint32),
+        ("ffn_hidden", c_uint32),
+        ("cond_dim", c_uint32),
+        ("rope_axes", c_uint32 * 3),
+        ("rope_theta", c_float),
+        ("rms_epsilon", c_float),
+        ("input", c_void_p),
+        ("coordinates", c_void_p),
+        ("condition", c_void_p),
+        ("w_adaln", c_void_p),
+        ("b_adaln", c_void_p),
+        ("attn_norm1", c_void_p),
+        ("attn_norm2", c_void_p),
+        ("ffn_norm1", c_void_p),
+        ("ffn_norm2", c_void_p),
+        ("q_norm", c_void_p),
+        ("k_norm", c_void_p),
+        ("w_qkv", c_void_p),
+        ("w_out", c_void_p),
+        ("w_13", c_void_p),
+        ("w_2", c_void_p),
+        ("output", c_void_p),
+    ]
+
+
+class PrometheusBlockResult(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("stage", c_uint32),
+        ("detail_code", ctypes.c_int32),
+        ("output_written", c_uint32),
+        ("kernel_launches", c_uint32),
+        ("reserved0", c_uint32),
+        ("gpu_duration_ns", c_uint64),
+        ("end_to_end_ns", c_uint64),
+        ("workspace_bytes", c_uint64),
+    ]
+
+
 # ---- errors and status (status.go, bridge.go) ------------------------------
 class ReactorIssue(RuntimeError):
     """Structured reactor failure (reference ``ReactorIssue``, bridge.go:33-66)."""
@@ -341,6 +409,14 @@ _SIGNATURES = {
     "prometheus_reactor_runtime_rmsnorm_device": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_float,
                 POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_decoder_layer_f32": (
+        c_int, [c_void_p, POINTER(PrometheusDecoderLayerF32Request), POINTER(PrometheusBlockResult)]),
+    "prometheus_reactor_runtime_decoder_layer_f32_device": (
+        c_int, [c_void_p, POINTER(PrometheusDecoderLayerF32Request), POINTER(PrometheusBlockResult)]),
+    "prometheus_reactor_runtime_dit_block_bf16": (
+        c_int, [c_void_p, POINTER(PrometheusDitBlockBf16Request), POINTER(PrometheusBlockResult)]),
+    "prometheus_reactor_runtime_dit_block_bf16_device": (
+        c_int, [c_void_p, POINTER(PrometheusDitBlockBf16Request), POINTER(PrometheusBlockResult)]),
     "prometheus_reactor_runtime_device_alloc": (c_int, [c_void_p, c_uint64, POINTER(c_void_p)]),
     "prometheus_reactor_runtime_device_free": (c_int, [c_void_p, c_void_p]),
     "prometheus_reactor_runtime_device_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64]),
@@ -547,6 +623,64 @@ class NativeRuntime:
         res = PrometheusRmsNormResult()
         rc = self.lib.prometheus_reactor_runtime_rmsnorm(self.handle, byref(req), byref(res))
         return rc, res, out, inv
+
+    # -- transformer blocks ----------------------------------------------------
+    def decoder_layer_request(self, tokens, hidden, q_heads, head_dim, ffn, ptrs: dict, eps=1e-6,
+                              rope_base=10000.0, position_offset=0, kv_heads=1) -> PrometheusDecoderLayerF32Request:
+        req = PrometheusDecoderLayerF32Request()
+        req.struct_size = ctypes.sizeof(req)
+        req.tokens, req.hidden, req.q_heads, req.kv_heads = tokens, hidden, q_heads, kv_heads
+        req.head_dim, req.ffn_hidden, req.position_offset = head_dim, ffn, position_offset
+        req.rms_epsilon, req.rope_base = eps, rope_base
+        for name, ptr in ptrs.items():
+            setattr(req, name, ptr)
+        return req
+
+    def decoder_layer_f32(self, x, w, q_heads: int, head_dim: int, eps=1e-6, rope_base=10000.0,
+                          position_offset=0) -> Tuple[int, PrometheusBlockResult, np.ndarray]:
+        """Host-pointer Gemma-style layer; ``w`` has attn_norm, w_qkv, w_o, ffn_norm, w_gate_up, w_down."""
+        x = _f32(x)
+        tokens, hidden = x.shape
+        arrs = {"input": x, "attn_norm_weight": _f32(w.attn_norm), "w_qkv": _f32(w.w_qkv), "w_o": _f32(w.w_o),
+                "ffn_norm_weight": _f32(w.ffn_norm), "w_gate_up": _f32(w.w_gate_up), "w_down": _f32(w.w_down)}
+        out = np.empty_like(x)
+        arrs["output"] = out
+        req = self.decoder_layer_request(tokens, hidden, q_heads, head_dim, arrs["w_down"].shape[0],
+                                         {k: _ptr(v) for k, v in arrs.items()}, eps, rope_base, position_offset)
+        res = PrometheusBlockResult()
+        rc = self.lib.prometheus_reactor_runtime_decoder_layer_f32(self.handle, byref(req), byref(res))
+        return rc, res, out
+
+    def dit_block_request(self, tokens, hidden, heads, ffn, cond_dim, ptrs: dict, eps=1e-5, theta=256.0,
+                          axes=(32, 48, 48), head_dim=128) -> PrometheusDitBlockBf16Request:
+        req = PrometheusDitBlockBf16Request()
+        req.struct_size = ctypes.sizeof(req)
+        req.tokens, req.hidden, req.heads, req.head_dim = tokens, hidden, heads, head_dim
+        req.ffn_hidden, req.cond_dim = ffn, cond_dim
+        req.rope_axes[0], req.rope_axes[1], req.rope_axes[2] = axes
+        req.rope_theta, req.rms_epsilon = theta, eps
+        for name, ptr in ptrs.items():
+            setattr(req, name, ptr)
+        return req
+
+    def dit_block_bf16(self, x, coords, condition, w, heads: int, eps=1e-5, theta=256.0,
+                       axes=(32, 48, 48)) -> Tuple[int, PrometheusBlockResult, np.ndarray]:
+        """Host-pointer DiT block; ``w`` carries bf16 bit patterns for the projections."""
+        x = _f32(x)
+        tokens, hidden = x.shape
+        u16 = lambda a: np.ascontiguousarray(a, dtype=np.uint16)
+        arrs = {"input": x, "coordinates": _f32(coords), "condition": _f32(condition), "w_adaln": u16(w.w_adaln),
+                "b_adaln": _f32(w.b_adaln), "attn_norm1": _f32(w.attn_norm1), "attn_norm2": _f32(w.attn_norm2),
+                "ffn_norm1": _f32(w.ffn_norm1), "ffn_norm2": _f32(w.ffn_norm2), "q_norm": _f32(w.q_norm),
+                "k_norm": _f32(w.k_norm), "w_qkv": u16(w.w_qkv), "w_out": u16(w.w_out), "w_13": u16(w.w_13),
+                "w_2": u16(w.w_2)}
+        out = np.empty_like(x)
+        arrs["output"] = out
+        req = self.dit_block_request(tokens, hidden, heads, arrs["w_2"].shape[0], arrs["condition"].size,
+                                     {k: _ptr(v) for k, v in arrs.items()}, eps, theta, axes)
+        res = PrometheusBlockResult()
+        rc = self.lib.prometheus_reactor_runtime_dit_block_bf16(self.handle, byref(req), byref(res))
+        return rc, res, out
 
     # -- device-resident operations ----------------------------------------
     def alloc(self, nbytes: int) -> int:

@@ -72,28 +72,80 @@ static uint64_t xoshiro_next(xoshiro256* g) {
 /* 53-bit uniform in [0,1). */
 static double xoshiro_unit(xoshiro256* g) { return (double)(xoshiro_next(g) >> 11) * 0x1.0p-53; }
 
-void oct_gen_uniform_f32(uint64_t seed, float* out, uint64_t count, float lo, float hi) {
-  xoshiro256 g;
-  xoshiro_seed(&g, seed);
-  const double span = (double)hi - (double)lo;
-  for (uint64_t i = 0; i < count; ++i) out[i] = (float)((double)lo + xoshiro_unit(&g) * span);
-}
+/* The stream is cut into blocks of 2^20 values; block b draws from xoshiro256**
+   seeded with seed ^ (b * 0x9E3779B97F4A7C15).  Blocks are generated in
+   parallel, and the values do not depend on the thread count. */
+#define OCT_GEN_BLOCK (1ull << 20)
 
-void oct_gen_normal_f32(uint64_t seed, float* out, uint64_t count, float mean, float stddev) {
+typedef struct gen_job {
+  uint64_t seed;
+  float* out;
+  uint64_t count;
+  float a, b;  /* uniform: lo, hi; normal: mean, stddev */
+  int normal;
+  uint64_t first_block, block_stride;
+} gen_job;
+
+static void gen_block(const gen_job* j, uint64_t blk) {
   xoshiro256 g;
-  xoshiro_seed(&g, seed);
+  xoshiro_seed(&g, j->seed ^ (blk * 0x9E3779B97F4A7C15ull));
+  const uint64_t begin = blk * OCT_GEN_BLOCK;
+  uint64_t end = begin + OCT_GEN_BLOCK;
+  if (end > j->count) end = j->count;
+  if (!j->normal) {
+    const double span = (double)j->b - (double)j->a;
+    for (uint64_t i = begin; i < end; ++i) j->out[i] = (float)((double)j->a + xoshiro_unit(&g) * span);
+    return;
+  }
   const double two_pi = 6.283185307179586476925286766559;
-  uint64_t i = 0;
-  while (i < count) {
+  uint64_t i = begin;
+  while (i < end) {
     /* Box-Muller on (0,1] x [0,1). */
     const double u1 = 1.0 - xoshiro_unit(&g);
     const double u2 = xoshiro_unit(&g);
     const double r = sqrt(-2.0 * log(u1));
-    const double z0 = r * cos(two_pi * u2);
-    const double z1 = r * sin(two_pi * u2);
-    out[i++] = (float)((double)mean + (double)stddev * z0);
-    if (i < count) out[i++] = (float)((double)mean + (double)stddev * z1);
+    j->out[i++] = (float)((double)j->a + (double)j->b * r * cos(two_pi * u2));
+    if (i < end) j->out[i++] = (float)((double)j->a + (double)j->b * r * sin(two_pi * u2));
   }
+}
+
+static void* gen_worker(void* raw) {
+  const gen_job* j = (const gen_job*)raw;
+  const uint64_t blocks = (j->count + OCT_GEN_BLOCK - 1) / OCT_GEN_BLOCK;
+  for (uint64_t b = j->first_block; b < blocks; b += j->block_stride) gen_block(j, b);
+  return NULL;
+}
+
+static void gen_dispatch(uint64_t seed, float* out, uint64_t count, float a, float b, int normal) {
+  const uint64_t blocks = (count + OCT_GEN_BLOCK - 1) / OCT_GEN_BLOCK;
+  uint64_t threads = blocks < 16 ? blocks : 16;
+  if (threads < 1) threads = 1;
+  gen_job jobs[16];
+  pthread_t tids[16];
+  for (uint64_t t = 0; t < threads; ++t) {
+    jobs[t].seed = seed;
+    jobs[t].out = out;
+    jobs[t].count = count;
+    jobs[t].a = a;
+    jobs[t].b = b;
+    jobs[t].normal = normal;
+    jobs[t].first_block = t;
+    jobs[t].block_stride = threads;
+  }
+  if (threads == 1) {
+    gen_worker(&jobs[0]);
+    return;
+  }
+  for (uint64_t t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, gen_worker, &jobs[t]);
+  for (uint64_t t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+}
+
+void oct_gen_uniform_f32(uint64_t seed, float* out, uint64_t count, float lo, float hi) {
+  gen_dispatch(seed, out, count, lo, hi, 0);
+}
+
+void oct_gen_normal_f32(uint64_t seed, float* out, uint64_t count, float mean, float stddev) {
+  gen_dispatch(seed, out, count, mean, stddev, 1);
 }
 
 void oct_deterministic_matrix(float* out, uint64_t count) {

@@ -1,16 +1,23 @@
-"""Reader for the Octagon text fixtures (``Type { Field: [..] ... }``)."""
+"""Reader for the Octagon text fixtures: ``Type { Field: [..]  Field: Sub { A: x B: y } }``.
+
+Arrays become float64 numpy arrays; scalars inside nested records are keyed
+``Record.Field`` (e.g. ``QNormPair.Even``)."""
 import re
 from pathlib import Path
 
 import numpy as np
 
 GOLDEN = Path(__file__).resolve().parent
+_NUM = r"-?\d+(?:\.\d*)?(?:[eE][-+]?\d+)?"
 
 
 def load(name: str) -> dict:
     text = (GOLDEN / name).read_text()
     fields = {}
     for m in re.finditer(r"(\w+):\s*\[([^\]]*)\]", text):
-        values = [v for v in m.group(1 + 1).replace("\n", " ").split(",") if v.strip()]
+        values = [v for v in m.group(2).replace("\n", " ").split(",") if v.strip()]
         fields[m.group(1)] = np.array([float(v) for v in values], dtype=np.float64)
+    for m in re.finditer(r"(\w+):\s*\w+\s*\{([^{}]*)\}", text):
+        for s in re.finditer(rf"(\w+):\s*({_NUM})", m.group(2)):
+            fields[f"{m.group(1)}.{s.group(1)}"] = float(s.group(2))
     return fields

@@ -61,6 +61,9 @@ STRUCTS = {
     "PrometheusGemma4E2BM1InputRmsNormResult": p.PrometheusGemma4E2BM1InputRmsNormResult,
     "PrometheusRmsNormRequest": p.PrometheusRmsNormRequest,
     "PrometheusRmsNormResult": p.PrometheusRmsNormResult,
+    "PrometheusDecoderLayerF32Request": p.PrometheusDecoderLayerF32Request,
+    "PrometheusDitBlockBf16Request": p.PrometheusDitBlockBf16Request,
+    "PrometheusBlockResult": p.PrometheusBlockResult,
 }
 
 

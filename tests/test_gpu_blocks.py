@@ -1,0 +1,114 @@
+"""GPU parity of the transformer blocks against the binary64 oracles.
+
+Bars: normwise relative error <= 1e-3 for the fp32
+Gemma-style layer, <= 2e-2 for the bf16 DiT block.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import blocks
+from oct_amd import prometheus as p
+
+pytestmark = pytest.mark.gpu
+
+F32_BLOCK = 1e-3
+
+
+@pytest.mark.parametrize("T,D,Hq,d,F", [(5, 64, 2, 32, 96), (33, 256, 4, 64, 512), (130, 512, 8, 64, 1024),
+                                        (64, 384, 3, 128, 640)])
+def test_decoder_layer_small_shapes(gpu_runtime, T, D, Hq, d, F):
+    x, w = blocks.make_decoder_layer(T + D, T, D, Hq, d, F)
+    rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
+    assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)
+    ref = blocks.decoder_layer_f32(x, w, Hq, d)
+    err = oracle.normwise_rel_err(out, ref)
+    assert err <= F32_BLOCK, err
+
+
+def test_decoder_layer_c4_gemma2b(gpu_runtime):
+    """hidden 2048, 8 query heads, 1 KV head, head_dim 256, FFN 16384, T=512."""
+    T, D, Hq, d, F = 512, 2048, 8, 256, 16384
+    x, w = blocks.make_decoder_layer(4, T, D, Hq, d, F)
+    rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
+    assert rc == p.PROM_OK, (res.stage, res.detail_code)
+    ref = blocks.decoder_layer_f32(x, w, Hq, d)
+    err = oracle.normwise_rel_err(out, ref)
+    print(f"C4 layer normwise rel err {err:.3e}, gpu {res.gpu_duration_ns / 1e6:.3f} ms")
+    assert err <= F32_BLOCK
+    # causality at full size: the first half of the sequence ignores the second
+    x2 = x.copy()
+    x2[T // 2:] = oracle.normal(99, (T - T // 2, D))
+    rc, res, out2 = gpu_runtime.decoder_layer_f32(x2, w, q_heads=Hq, head_dim=d)
+    np.testing.assert_array_equal(out2[:T // 2], out[:T // 2])
+
+
+def test_decoder_layer_position_offset(gpu_runtime):
+    T, D, Hq, d, F = 16, 128, 2, 64, 256
+    x, w = blocks.make_decoder_layer(8, T, D, Hq, d, F)
+    rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d, position_offset=37)
+    assert rc == 0
+    assert oracle.normwise_rel_err(out, blocks.decoder_layer_f32(x, w, Hq, d, position_offset=37)) <= F32_BLOCK
+
+
+def test_decoder_layer_rejects_gqa(gpu_runtime):
+    x, w = blocks.make_decoder_layer(1, 4, 32, 2, 8, 16)
+    req = gpu_runtime.decoder_layer_request(4, 32, 2, 8, 16, {"input": 1, "attn_norm_weight": 1, "w_qkv": 1,
+                                                              "w_o": 1, "ffn_norm_weight": 1, "w_gate_up": 1,
+                                                              "w_down": 1, "output": 1}, kv_heads=2)
+    res = p.PrometheusBlockResult()
+    import ctypes
+    rc = gpu_runtime.lib.prometheus_reactor_runtime_decoder_layer_f32(gpu_runtime.handle, ctypes.byref(req),
+                                                                      ctypes.byref(res))
+    assert rc == p.PROM_ERROR and res.detail_code == -7503
+
+
+# ------------------------------------------------------------------ DiT block
+BF16_BLOCK = 2e-2
+
+
+@pytest.mark.parametrize("grid,text,heads,F,C", [((3, 5), 7, 2, 256, 32), ((8, 16), 40, 4, 1024, 64),
+                                                 ((10, 13), 0, 1, 384, 16)])
+def test_dit_block_small_shapes(gpu_runtime, grid, text, heads, F, C):
+    T = grid[0] * grid[1] + text
+    D = heads * 128
+    x, cond, w = blocks.make_dit_block(T + F, T, D, F, C)
+    coords = blocks.joint_coordinates(grid[0], grid[1], text)
+    rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
+    assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads)
+    err = oracle.normwise_rel_err(out, ref)
+    print(f"DiT T={T} D={D} normwise rel err {err:.3e}")
+    assert err <= BF16_BLOCK
+
+
+def test_dit_block_attention_is_not_trivial(gpu_runtime):
+    """Strong projections make attention and the FFN dominate the residual path."""
+    T, heads, F, C = 96, 2, 512, 32
+    D = heads * 128
+    x, cond, w = blocks.make_dit_block(77, T, D, F, C)
+    for name in ("w_qkv", "w_out", "w_13", "w_2"):
+        setattr(w, name, oracle.to_bf16(oracle.from_bf16(getattr(w, name)) * 10))
+    coords = blocks.joint_coordinates(8, 8, 32)
+    rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
+    assert rc == 0
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads)
+    assert np.linalg.norm(ref - x) / np.linalg.norm(x) > 0.05  # the block does move x
+    assert oracle.normwise_rel_err(out, ref) <= BF16_BLOCK
+
+
+def test_dit_block_c5_full(gpu_runtime):
+    """hidden 3840, 30 x 128 heads, FFN 10240, 4096 image + 128 text tokens."""
+    grid, text, heads, F, C = (64, 64), 128, 30, 10240, 256
+    T = grid[0] * grid[1] + text
+    D = heads * 128
+    x, cond, w = blocks.make_dit_block(5, T, D, F, C)
+    coords = blocks.joint_coordinates(grid[0], grid[1], text)
+    rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
+    assert rc == p.PROM_OK, (res.stage, res.detail_code)
+    rows = sorted(set(np.linspace(0, T - 1, 48).astype(int).tolist()) | {0, 4095, 4096, T - 1})
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads, rows=rows)
+    err = oracle.normwise_rel_err(out[rows], ref)
+    print(f"C5 DiT block normwise rel err {err:.3e} on {len(rows)} rows, gpu {res.gpu_duration_ns / 1e6:.3f} ms")
+    assert err <= BF16_BLOCK
+    assert np.all(np.isfinite(out))
