@@ -226,6 +226,39 @@ def main() -> int:
         sec["rmsnorm_8192x4096_frac"] = round(gbs / PEAK_HBM_GBS, 4)
         for d in (dx, dy, dw, dinv):
             rt.free(d)
+        # transformer layers, weights resident
+        from oracle import blocks
+
+        T, D, Hq, hd, F = 512, 2048, 8, 256, 16384
+        x, w = blocks.make_decoder_layer(4, T, D, Hq, hd, F)
+        ptrs = {"input": x, "attn_norm_weight": w.attn_norm, "w_qkv": w.w_qkv, "w_o": w.w_o,
+                "ffn_norm_weight": w.ffn_norm, "w_gate_up": w.w_gate_up, "w_down": w.w_down}
+        dptr = {k: rt.upload_new(np.ascontiguousarray(v, np.float32)) for k, v in ptrs.items()}
+        dptr["output"] = rt.alloc(T * D * 4)
+        req = rt.decoder_layer_request(T, D, Hq, hd, F, dptr)
+        _, ev = _timed_launches(rt, lambda: rt.decoder_layer_f32_device(req), 10, 3)
+        sec["gemma2b_layer_f32_t512_ms"] = round(ev, 4)
+        sec["gemma2b_layer_f32_t512_tflops"] = round(1.149e11 / (ev * 1e-3) / 1e12, 2)
+        for d in dptr.values():
+            rt.free(d)
+        del x, w
+        grid, text, heads, F5, C = (64, 64), 128, 30, 10240, 256
+        T5 = grid[0] * grid[1] + text
+        D5 = heads * 128
+        x, cond, w = blocks.make_dit_block(5, T5, D5, F5, C)
+        coords = blocks.joint_coordinates(grid[0], grid[1], text)
+        arrs = {"input": x, "coordinates": coords, "condition": cond, "w_adaln": w.w_adaln, "b_adaln": w.b_adaln,
+                "attn_norm1": w.attn_norm1, "attn_norm2": w.attn_norm2, "ffn_norm1": w.ffn_norm1,
+                "ffn_norm2": w.ffn_norm2, "q_norm": w.q_norm, "k_norm": w.k_norm, "w_qkv": w.w_qkv,
+                "w_out": w.w_out, "w_13": w.w_13, "w_2": w.w_2}
+        dptr = {k: rt.upload_new(v) for k, v in arrs.items()}
+        dptr["output"] = rt.alloc(T5 * D5 * 4)
+        req = rt.dit_block_request(T5, D5, heads, F5, C, dptr)
+        _, ev = _timed_launches(rt, lambda: rt.dit_block_bf16_device(req), 10, 3)
+        sec["dit_block_bf16_t4224_ms"] = round(ev, 4)
+        sec["dit_block_bf16_t4224_tflops"] = round(1.769e12 / (ev * 1e-3) / 1e12, 2)
+        for d in dptr.values():
+            rt.free(d)
         line["secondary"] = sec
 
     rt.close()

@@ -197,6 +197,163 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma_kernel(const uint16_t* 
   store_block(acc11, 1, 1);
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile kernel: 512 threads = 8 wave64, macro tile 256x256, K tile 64.
+// Waves are 2 (m) x 4 (n); each owns 128x64 = 4x2 MFMA 32x32x16 blocks (128
+// fp32 accumulators per lane).  A stays [m][k] in LDS (operands are 128-bit
+// reads); B stays row-major [k][n] as it arrives from HBM, and each B operand
+// is assembled with two ds_read_b64_tr_b16 transpose reads: within a 16-lane
+// group, lane L points at row (L/4) and column 4*(L%4) of a 4x16 sub-block and
+// receives the 4 k-consecutive values of column L.  No transposing stores.
+// Requires k % 8 == 0, n % 8 == 0 (whole 16-byte chunks are in or out of range).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr int kBM2 = 256;
+constexpr int kBN2 = 256;
+constexpr int kBK2 = 64;
+constexpr int kLdsA2 = kBK2 + 8;   // 144-byte A rows
+constexpr int kLdsB2 = kBN2 + 16;  // 544-byte B rows: 4 consecutive rows land on distinct banks
+
+__device__ __forceinline__ void map_tile2(int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int num_tiles = tiles_m * tiles_n;
+  int pid = (int)blockIdx.x;
+  if ((num_tiles & 7) == 0) pid = (pid & 7) * (num_tiles >> 3) + (pid >> 3);
+  const int per_group = kGroupM * tiles_n;
+  const int group = pid / per_group;
+  const int first_m = group * kGroupM;
+  const int group_m = min(tiles_m - first_m, kGroupM);
+  const int in_group = pid - group * per_group;
+  *tm = first_m + in_group % group_m;
+  *tn = in_group / group_m;
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16_t* __restrict__ A,
+                                                                   const uint16_t* __restrict__ B, float* C, int M,
+                                                                   int N, int K, int tiles_m, int tiles_n, int lda,
+                                                                   int ldb, int ldc, const float* R, int ldr,
+                                                                   uint16_t* Cb) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM2][kLdsA2];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kBK2][kLdsB2];
+
+  int tm, tn;
+  map_tile2(tiles_m, tiles_n, &tm, &tn);
+  const int row0 = tm * kBM2;
+  const int col0 = tn * kBN2;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2;  // 0..1
+  const int wn = wave & 3;   // 0..3
+
+  u32x4 ra[4], rb[4];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 512 * u;  // A: 256 rows x 8 chunks
+      const int r = c >> 3;
+      const int kc = (c & 7) * 8;
+      const int gr = row0 + r, gk = k0 + kc;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (gr < M && gk < K) v = *reinterpret_cast<const u32x4*>(A + (size_t)gr * lda + gk);
+      ra[u] = v;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 512 * u;  // B: 64 k rows x 32 chunks
+      const int kr = c >> 5;
+      const int nc = (c & 31) * 8;
+      const int gk = k0 + kr, gn = col0 + nc;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (gk < K && gn < N) v = *reinterpret_cast<const u32x4*>(B + (size_t)gk * ldb + gn);
+      rb[u] = v;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 512 * u;
+      *reinterpret_cast<u32x4*>(&As[buf][c >> 3][(c & 7) * 8]) = ra[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 512 * u;
+      *reinterpret_cast<u32x4*>(&Bs[buf][c >> 5][(c & 31) * 8]) = rb[u];
+    }
+  };
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[i][0] = floatx16{};
+    acc[i][1] = floatx16{};
+  }
+
+  const int k_tiles = (K + kBK2 - 1) / kBK2;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int lrow = lane & 31;
+  const int lk = (lane >> 5) * 8;
+  // transpose-read coordinates inside a 16(k) x 32(n) operand block
+  const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < k_tiles;
+    if (more) load_tile((kt + 1) * kBK2);
+#pragma unroll
+    for (int s = 0; s < kBK2 / 16; ++s) {
+      bf16x8 af[4], bfr[2];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        af[mi] = *reinterpret_cast<const bf16x8*>(&As[cur][wm * 128 + mi * 32 + lrow][16 * s + lk]);
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const int col = wn * 64 + ni * 32 + tr_col;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(&Bs[cur][16 * s + tr_row][col]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(&Bs[cur][16 * s + tr_row + 4][col]));
+        const short w8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        bfr[ni] = __builtin_bit_cast(bf16x8, w8);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
+      }
+    }
+    if (more) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  const int lgrp = (lane >> 5) * 4;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int col = col0 + wn * 64 + ni * 32 + lrow;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row0 + wm * 128 + mi * 32 + 8 * (r >> 2) + lgrp + (r & 3);
+        if (row < M) {
+          float v = acc[mi][ni][r];
+          if (R != nullptr) v += R[(size_t)row * ldr + col];
+          if (Cb != nullptr)
+            Cb[(size_t)row * ldc + col] = f32_to_bf16_rne(v);
+          else
+            C[(size_t)row * ldc + col] = v;
+        }
+      }
+    }
+  }
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -204,10 +361,18 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, int ldb, float* c, uint16_t* cb,
                                int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
                                hipStream_t stream, int* path_detail) {
+  const bool vec = (k % 8 == 0) && (n % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(a) && aligned16(b);
+  const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
+  const int tiles_n2 = (int)((n + kBN2 - 1) / kBN2);
+  if (vec && tiles_m2 * tiles_n2 >= 128) {
+    hipLaunchKernelGGL(gemm_bf16_mfma_256_kernel, dim3((unsigned)(tiles_m2 * tiles_n2)), dim3(512), 0, stream, a, b, c,
+                       (int)m, (int)n, (int)k, tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
+    if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_BF16;
+    return hipGetLastError();
+  }
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const dim3 grid((unsigned)(tiles_m * tiles_n));
-  const bool vec = (k % 8 == 0) && (n % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(a) && aligned16(b);
   if (vec)
     hipLaunchKernelGGL(gemm_bf16_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
                        tiles_m, tiles_n, lda, ldb, ldc, residual, ldr, cb);

@@ -121,6 +121,8 @@ int gemm_device(void* handle, const TIn* a, const TIn* b, float* c, uint32_t m, 
   const int v = gemm_validate(rt, a, b, c, m, n, k, out_stage, out_detail);
   if (v != PROM_OK) return v;
   int path = 0;
+  // The lock covers the launcher's use of runtime-owned workspace (split-K partials).
+  std::lock_guard<std::mutex> lock(ctx().mu);
   if (launch(a, b, c, m, n, k, ctx().stream, &path) != hipSuccess) {
     set_status(out_stage, out_detail, PROM_STAGE_SUBMIT, PROM_DETAIL_HIP_LAUNCH_FAILED);
     return PROM_ERROR;

@@ -22,6 +22,8 @@
 //     the 8 XCDs round-robin, so consecutive ids are remapped to contiguous
 //     chunks of a grouped (GROUP_M) tile order, keeping each XCD's L2 on a
 //     compact block of A rows and B columns.
+#include <algorithm>
+
 #include "reactor_internal.h"
 
 namespace prom {
@@ -57,7 +59,8 @@ template <bool kVec>
 __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __restrict__ A,
                                                                 const float* __restrict__ B, float* C, int M,
                                                                 int N, int K, int tiles_m, int tiles_n, int lda,
-                                                                int ldb, int ldc, const float* R, int ldr) {
+                                                                int ldb, int ldc, const float* R, int ldr,
+                                                                int k_len) {
   __shared__ float As[2][kBK][kLdsA];
   __shared__ float Bs[2][kBK][kLdsB];
 
@@ -65,6 +68,15 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
   map_tile(tiles_m, tiles_n, &tm, &tn);
   const int row0 = tm * kBM;
   const int col0 = tn * kBN;
+  // Split-K: slice blockIdx.y covers k in [y*k_len, y*k_len + k_len) and writes
+  // its partial product to slab y of C (slabs M*ldc apart); R is then null.
+  if (gridDim.y > 1) {
+    const int kb = (int)blockIdx.y * k_len;
+    A += kb;
+    B += (size_t)kb * ldb;
+    C += (size_t)blockIdx.y * M * ldc;
+    K = min(k_len, K - kb);
+  }
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -222,7 +234,32 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__
   if (lane == 0) y[row] = acc;
 }
 
+// C = sum over `splits` slabs of P (fixed order: deterministic) + R.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, float* C, int M, int N,
+                                                            int ldc, int splits, const float* R, int ldr) {
+  const size_t total = (size_t)M * N;
+  const size_t slab = (size_t)M * N;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = idx / N;
+    const size_t col = idx - row * N;
+    float v = P[idx];
+    for (int s = 1; s < splits; ++s) v += P[(size_t)s * slab + idx];
+    if (R != nullptr) v += R[row * ldr + col];
+    C[row * ldc + col] = v;
+  }
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Number of K slices for an under-filled launch: aim for >= 2 workgroups per
+// CU (512 on 256 CUs) while keeping every slice >= 256 deep.
+int choose_splits(int tiles, uint32_t k) {
+  if (tiles >= 512 || k < 512) return 1;
+  int s = (512 + tiles - 1) / tiles;
+  s = std::min(s, (int)(k / 256));
+  s = std::min(s, 16);
+  return std::max(s, 1);
+}
 
 }  // namespace
 
@@ -241,14 +278,38 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
   }
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
-  const dim3 grid((unsigned)(tiles_m * tiles_n));
   const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && aligned16(a) && aligned16(b);
+  int splits = choose_splits(tiles_m * tiles_n, k);
+  int k_len = (int)k;
+  float* partial = nullptr;
+  if (splits > 1) {
+    // slices are whole K tiles (multiples of 16 keep 128-bit loads aligned)
+    k_len = (int)((((k + splits - 1) / splits) + kBK - 1) / kBK * kBK);
+    splits = (int)((k + k_len - 1) / k_len);
+    partial = splits > 1 ? static_cast<float*>(staging(6, (size_t)splits * m * n * sizeof(float))) : nullptr;
+    if (partial == nullptr) {
+      splits = 1;
+      k_len = (int)k;
+    }
+  }
+  const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits);
+  float* out = splits > 1 ? partial : c;
+  const int ldo = splits > 1 ? (int)n : ldc;
+  const float* res = splits > 1 ? nullptr : residual;
   if (vec)
-    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n, lda, ldb, ldc, residual, ldr);
+    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+                       tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
   else
-    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n, lda, ldb, ldc, residual, ldr);
+    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+                       tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
+  if (splits > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t total = (size_t)m * n;
+    const unsigned blocks = (unsigned)std::min((size_t)8192, (total + 255) / 256);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, c, (int)m, (int)n, ldc,
+                       splits, residual, ldr);
+  }
   if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_F32;
   return hipGetLastError();
 }

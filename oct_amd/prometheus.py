@@ -682,6 +682,27 @@ class NativeRuntime:
         rc = self.lib.prometheus_reactor_runtime_dit_block_bf16(self.handle, byref(req), byref(res))
         return rc, res, out
 
+    def decoder_layer_f32_device(self, req: PrometheusDecoderLayerF32Request) -> PrometheusBlockResult:
+        res = PrometheusBlockResult()
+        rc = self.lib.prometheus_reactor_runtime_decoder_layer_f32_device(self.handle, byref(req), byref(res))
+        if rc != PROM_OK:
+            raise ReactorIssue("decoder_layer_failed", f"error({stage_name(res.stage)},{res.detail_code})")
+        return res
+
+    def dit_block_bf16_device(self, req: PrometheusDitBlockBf16Request) -> PrometheusBlockResult:
+        res = PrometheusBlockResult()
+        rc = self.lib.prometheus_reactor_runtime_dit_block_bf16_device(self.handle, byref(req), byref(res))
+        if rc != PROM_OK:
+            raise ReactorIssue("dit_block_failed", f"error({stage_name(res.stage)},{res.detail_code})")
+        return res
+
+    def upload_new(self, arr: np.ndarray) -> int:
+        """Allocates a device buffer holding a copy of ``arr``; returns its address."""
+        arr = np.ascontiguousarray(arr)
+        ptr = self.alloc(max(arr.nbytes, 1))
+        self.upload(ptr, arr)
+        return ptr
+
     # -- device-resident operations ----------------------------------------
     def alloc(self, nbytes: int) -> int:
         p = c_void_p()

@@ -200,3 +200,16 @@ def test_bf16_4096_cubed(gpu_runtime):
         ref = oracle.matmul_f64(a, b, rows=(r, r + 1))[r]
         assert oracle.normwise_rel_err(out[r], ref) <= BF16_NORMWISE
         assert oracle.normwise_rel_err(out[r], ref) <= 1e-5
+
+
+@pytest.mark.parametrize("m,n,k", [(4224, 2056, 72), (600, 8200, 136), (1024, 4096, 8)])
+def test_bf16_large_tile_kernel_ragged(gpu_runtime, m, n, k):
+    """Shapes with >= 128 256x256 tiles take the large-tile kernel; ragged m/n/k tails."""
+    a = oracle.to_bf16(oracle.uniform(50 + m, (m, k)))
+    b = oracle.to_bf16(oracle.uniform(60 + n, (k, n)))
+    out = gpu_runtime.gemm_bf16(m, n, k, a, b).reshape(m, n)
+    ref = oracle.from_bf16(a).astype(np.float64) @ oracle.from_bf16(b).astype(np.float64)
+    assert oracle.normwise_rel_err(out, ref) <= 1e-5
+    rows = [0, m // 2, m - 1]
+    for r in rows:
+        np.testing.assert_allclose(out[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r], rtol=1e-4, atol=1e-5)
