@@ -8,15 +8,16 @@
 // so the sequence length is unbounded.
 //
 //   * workgroup = 4 wave64 = 128 queries of one head; each wave owns 32 queries;
-//   * per 64-key tile: K [64][128] and V^T [128][64] are staged in LDS (V is
-//     transposed on the way in, k pairs packed into 32-bit stores);
+//   * per 64-key tile: K and V [64][128] are staged in LDS in their HBM layout,
+//     double-buffered (the next tile is fetched into registers during the
+//     current tile's MFMAs);
 //   * scores are computed transposed, S^T = K Q^T, so that a lane owns one
 //     query and 32 of its scores: the row max / row sum need one cross-lane
 //     step (lanes l and l^32), not a 32-lane reduction;
 //   * O^T = V^T P^T accumulates in 4 MFMA blocks (128 d x 32 queries); P
 //     stays in registers: the key order inside each 16-key MFMA step is the
-//     permutation the S^T accumulator layout hands out, and V^T is read in the
-//     same permuted order (two 64-bit LDS reads per operand);
+//     permutation the S^T accumulator layout hands out, and the V^T operand is
+//     built in the same key order by two ds_read_b64_tr_b16 transpose reads;
 //   * softmax runs in the log2 domain (exp2), running max/sum in fp32;
 //   * the output tile is staged through LDS for 128-bit coalesced stores.
 #include "reactor_internal.h"
@@ -28,12 +29,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr int kD = 128;     // head dim
 constexpr int kQW = 32;     // queries per wave
 constexpr int kKB = 64;     // keys per tile
-constexpr int kKP = kD + 8;   // Ks row pitch (bf16)
-constexpr int kVP = kKB + 8;  // Vt row pitch (bf16)
+constexpr int kKP = kD + 8;   // K row pitch (bf16): 68 words, 16 rows on distinct 16-byte bank groups
+constexpr int kVP = kD + 16;  // V row pitch (bf16): 72 words, 4 consecutive rows on distinct banks
 constexpr float kNegBig = -1.0e30f;
 
 __device__ __forceinline__ uint16_t f2bf(float v) {
@@ -50,8 +53,10 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
                                                                  const uint16_t* __restrict__ V,
                                                                  uint16_t* __restrict__ O, int T, int ldq, int ldk,
                                                                  int ldv, int ldo, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKB][kKP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD][kVP];
+  // K and V tiles are [64 keys][128 d], double-buffered; V keeps its HBM
+  // layout and its operand is assembled with LDS transpose reads.
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKB][kKP];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kKB][kVP];
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -74,50 +79,58 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
     }
   }
 
-  floatx16 o[4] = {};  // O^T blocks: d = 32*db + 8*(r/4) + 4*hi + r%4, query lq
-  float m_run = kNegBig;
-  float l_run = 0.0f;
-
-  const int n_tiles = (T + kKB - 1) / kKB;
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    const int k0 = kt * kKB;
-    __syncthreads();  // previous tile fully consumed
-    // K tile: 64 keys x 128 d = 1024 16-byte chunks, 4 per thread.
+  // global -> register staging for one K tile and one V tile: 1024 + 1024
+  // 16-byte chunks, 4 + 4 per thread
+  u32x4 rk[4], rv[4];
+  auto load_tile = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int c = tid + 256 * u;
       const int key = c >> 4;
       const int dc = (c & 15) * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (k0 + key < T) v = *reinterpret_cast<const u32x4*>(K + (size_t)(k0 + key) * ldk + head * kD + dc);
-      *reinterpret_cast<u32x4*>(&Ks[key][dc]) = v;
-    }
-    // V tile transposed: units of (key pair, 8 d): 32 pairs x 16 d-chunks = 512, 2 per thread.
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int c = tid + 256 * u;
-      const int kp = c >> 4;
-      const int dc = (c & 15) * 8;
-      u32x4 lo = {0u, 0u, 0u, 0u}, hv = {0u, 0u, 0u, 0u};
-      const int key = k0 + 2 * kp;
-      if (key < T) lo = *reinterpret_cast<const u32x4*>(V + (size_t)key * ldv + head * kD + dc);
-      if (key + 1 < T) hv = *reinterpret_cast<const u32x4*>(V + (size_t)(key + 1) * ldv + head * kD + dc);
-      const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
-      const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        *reinterpret_cast<uint32_t*>(&Vt[dc + 2 * j][2 * kp]) = (lw[j] & 0xFFFFu) | (hw[j] << 16);
-        *reinterpret_cast<uint32_t*>(&Vt[dc + 2 * j + 1][2 * kp]) = (lw[j] >> 16) | (hw[j] & 0xFFFF0000u);
+      u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+      if (k0 + key < T) {
+        kv = *reinterpret_cast<const u32x4*>(K + (size_t)(k0 + key) * ldk + head * kD + dc);
+        vv = *reinterpret_cast<const u32x4*>(V + (size_t)(k0 + key) * ldv + head * kD + dc);
       }
+      rk[u] = kv;
+      rv[u] = vv;
     }
-    __syncthreads();
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 256 * u;
+      *reinterpret_cast<u32x4*>(&Ks[buf][c >> 4][(c & 15) * 8]) = rk[u];
+      *reinterpret_cast<u32x4*>(&Vs[buf][c >> 4][(c & 15) * 8]) = rv[u];
+    }
+  };
+
+  floatx16 o[4] = {};  // O^T blocks: d = 32*db + 8*(r/4) + 4*hi + r%4, query lq
+  float m_run = kNegBig;
+  float l_run = 0.0f;
+
+  // transpose-read coordinates: lane's 4 keys start at row 4*hi + (lane&15)/4
+  // (+8 for the second half), its 4 d values at column 16*((lane>>4)&1) + 4*(lane&3)
+  const int tr_row = 4 * hi + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  const int n_tiles = (T + kKB - 1) / kKB;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int kt = 0; kt < n_tiles; ++kt) {
+    const int k0 = kt * kKB;
+    const int cur = kt & 1;
+    const bool more = kt + 1 < n_tiles;
+    if (more) load_tile(k0 + kKB);
 
     // S^T for two 32-key blocks.
     floatx16 s0 = {}, s1 = {};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[lq][16 * s + 8 * hi]);
-      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[32 + lq][16 * s + 8 * hi]);
+      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[cur][lq][16 * s + 8 * hi]);
+      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[cur][32 + lq][16 * s + 8 * hi]);
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[s], s1, 0, 0, 0);
     }
@@ -153,7 +166,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
       for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
     }
     // P^T operands: chunk c covers keys 16c..16c+15 of the tile in the
-    // accumulator's order; registers 8*(c%2)..+7 of block c/2.
+    // accumulator's order: lane half hi holds keys 16c + 4*hi + 0..3 (regs
+    // 8*(c%2)+0..3 of block c/2) and 16c + 8 + 4*hi + 0..3 (regs +4..7).
     bf16x8 pc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -166,30 +180,34 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
       w.w = pack2(sb[base + 6], sb[base + 7]);
       pc[c] = __builtin_bit_cast(bf16x8, w);
     }
-    // O^T += V^T P^T; V^T operand in the same key order: keys 16c + 4*hi + 0..3
-    // and 16c + 8 + 4*hi + 0..3 of the tile.
+    // O^T += V^T P^T.  The V^T operand for chunk c needs, for d = 32*db + lq,
+    // the same 8 keys in the same order: two transpose reads of 4 keys each.
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const int dr = 32 * db + lq;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const u32x2 va = *reinterpret_cast<const u32x2*>(&Vt[dr][16 * c + 4 * hi]);
-        const u32x2 vb = *reinterpret_cast<const u32x2*>(&Vt[dr][16 * c + 8 + 4 * hi]);
-        u32x4 w = {va.x, va.y, vb.x, vb.y};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pc[c], o[db], 0, 0, 0);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(&Vs[cur][16 * c + tr_row][32 * db + tr_col]));
+        const s16x4 hv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(&Vs[cur][16 * c + 8 + tr_row][32 * db + tr_col]));
+        const short w8[8] = {lo[0], lo[1], lo[2], lo[3], hv[0], hv[1], hv[2], hv[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w8), pc[c], o[db], 0, 0, 0);
       }
     }
+    if (more) store_tile(cur ^ 1);
+    __syncthreads();
   }
 
-  // Normalise and stage the wave's [32 q][128 d] output through LDS.
-  __shared__ __attribute__((aligned(16))) uint16_t Ostage[4][kQW][kD + 8];
+  // Normalise and stage the wave's [32 q][128 d] output through LDS (K buffer 0
+  // is free after the final barrier: 4 waves x 32 rows x 136 fit in 2 x 64 x 136).
+  uint16_t* stage = &Ks[0][0][0] + wave * (kQW * kKP);
   const float inv_l = 1.0f / l_run;
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int d = 32 * db + 8 * (r >> 2) + 4 * hi + (r & 3);
-      Ostage[wave][lq][d] = f2bf(o[db][r] * inv_l);
+      stage[lq * kKP + d] = f2bf(o[db][r] * inv_l);
     }
   }
   __syncthreads();
@@ -202,7 +220,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
     const int q = q0 + row;
     if (q < T)
       *reinterpret_cast<u32x4*>(O + (size_t)q * ldo + head * kD + dc) =
-          *reinterpret_cast<const u32x4*>(&Ostage[wave][row][dc]);
+          *reinterpret_cast<const u32x4*>(&stage[row * kKP + dc]);
   }
 }
 

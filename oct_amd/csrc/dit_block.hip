@@ -12,7 +12,8 @@
 // fp32 accumulation; attention is the flash kernel (attention_bf16.hip); the
 // per-row work between them is fused into four one-pass row kernels (one wave
 // per row, the row held in registers, 128-bit loads):
-//   adaln          m = c @ Wada + b -> modulation vectors       (one thread per column)
+//   adaln          m = c @ Wada + b -> modulation vectors       (k split over 4 waves)
+//   rope_table     (cos, sin) per token and pair, binary64 angles
 //   norm_mod       a = RMSNorm(x; n1) * scaleA                   -> bf16
 //   qk_norm_rope   per (token, head): RMSNorm(q), RMSNorm(k), RoPE, V copy -> bf16
 //   resid_norm_mod r = x + gateA * RMSNorm(proj; n2)             -> fp32
@@ -57,17 +58,48 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* dst, floatx4 v) {
 }
 
 // mod[j] = b[j] + sum_k c[k] * W[k][j]; chunk 0 and 2 -> 1 + m, chunk 1 and 3 -> tanh(m)
-// (canonical_reference.go:373-383).
+// (canonical_reference.go:373-383).  A workgroup owns 64 columns; its 4 waves
+// take every 4th k (coalesced 128-byte row segments) and combine through LDS.
 __global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ cond, const uint16_t* __restrict__ W,
                                                     const float* __restrict__ b, float* __restrict__ mod, int C,
                                                     int D) {
-  const int j = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (j >= 4 * D) return;
+  __shared__ float part[4][64];
+  const int lane = (int)(threadIdx.x & 63);
+  const int kg = (int)(threadIdx.x >> 6);
+  const int j = (int)blockIdx.x * 64 + lane;
   float acc = 0.0f;
-  for (int k = 0; k < C; ++k) acc += cond[k] * bf2f(W[(size_t)k * 4 * D + j]);
-  acc += b[j];
-  const int chunk = j / D;
-  mod[j] = (chunk == 0 || chunk == 2) ? 1.0f + acc : tanhf(acc);
+  if (j < 4 * D) {
+    for (int k = kg; k < C; k += 4) acc += cond[k] * bf2f(W[(size_t)k * 4 * D + j]);
+  }
+  part[kg][lane] = acc;
+  __syncthreads();
+  if (kg == 0 && j < 4 * D) {
+    const float m = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]) + b[j];
+    const int chunk = j / D;
+    mod[j] = (chunk == 0 || chunk == 2) ? 1.0f + m : tanhf(m);
+  }
+}
+
+// RoPE table: tab[t][p] = (cos, sin) of coord[t][axis(p)] * theta^(-2*pair/width)
+// for the 64 pairs of a 128-wide head; angles in binary64 (once per token,
+// shared by every head).
+__global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict__ coords, float2* __restrict__ tab,
+                                                         int T, float theta, int ax0, int ax1) {
+  const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (idx >= T * 64) return;
+  const int t = idx >> 6;
+  const int p = idx & 63;
+  int axis, width, pair;
+  if (p < ax0 / 2) {
+    axis = 0; width = ax0; pair = p;
+  } else if (p < (ax0 + ax1) / 2) {
+    axis = 1; width = ax1; pair = p - ax0 / 2;
+  } else {
+    axis = 2; width = 128 - ax0 - ax1; pair = p - (ax0 + ax1) / 2;
+  }
+  const double freq = pow((double)theta, -2.0 * (double)pair / (double)width);
+  const double angle = (double)coords[(size_t)t * 3 + axis] * freq;
+  tab[idx] = make_float2((float)cos(angle), (float)sin(angle));
 }
 
 // a = RMSNorm(x; w) * scale  -> bf16.  One wave per row, D % 4 == 0, D <= 4096.
@@ -109,15 +141,13 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
 }
 
 // Per (token, head): q and k RMSNorm over 128 channels, then RoPE on the
-// interleaved pairs (2p, 2p+1); pair p belongs to axis a with local pair
-// index p - offset(a), frequency theta^(-2*pair/width_a), angle coord[t][a]*freq
-// (zimage/canonical_contract.go:66-87, zimage_main_transformer_canonical.py:124-140).
+// interleaved pairs (2p, 2p+1) with the token's (cos, sin) table entry for
+// pair p (zimage/canonical_contract.go:66-87, zimage_main_transformer_canonical.py:124-140).
 // One wave per (token, head); lane l owns pair l.  V is copied to bf16.
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ coords,
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restrict__ qkv, const float2* __restrict__ tab,
                                                            const float* __restrict__ qn, const float* __restrict__ kn,
                                                            uint16_t* __restrict__ Q, uint16_t* __restrict__ K,
-                                                           uint16_t* __restrict__ V, int T, int H, float eps,
-                                                           float theta, int ax0, int ax1, int ax2) {
+                                                           uint16_t* __restrict__ V, int T, int H, float eps) {
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
   const int unit = (int)blockIdx.x * 4 + wave;
   if (unit >= T * H) return;
@@ -126,18 +156,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restri
   const int D = H * 128;
   const float* row = qkv + (size_t)t * 3 * D;
   const int c0 = h * 128 + 2 * lane;
-  // RoPE angle for pair `lane`
-  int axis, width, pair;
-  if (lane < ax0 / 2) {
-    axis = 0; width = ax0; pair = lane;
-  } else if (lane < (ax0 + ax1) / 2) {
-    axis = 1; width = ax1; pair = lane - ax0 / 2;
-  } else {
-    axis = 2; width = ax2; pair = lane - (ax0 + ax1) / 2;
-  }
-  const double freq = pow((double)theta, -2.0 * (double)pair / (double)width);
-  const double angle = (double)coords[(size_t)t * 3 + axis] * freq;
-  const float cs = (float)cos(angle), sn = (float)sin(angle);
+  const float2 cs2 = tab[(size_t)t * 64 + lane];
+  const float cs = cs2.x, sn = cs2.y;
   const float qw0 = qn[2 * lane], qw1 = qn[2 * lane + 1];
   const float kw0 = kn[2 * lane], kw1 = kn[2 * lane + 1];
   {
@@ -281,12 +301,13 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ G
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
-enum { kWsMod, kWsA, kWsQkv, kWsQ, kWsK, kWsV, kWsO, kWsProj, kWsR, kWsF, kWsG, kWsH, kWsW2, kWsCount };
+enum { kWsMod, kWsA, kWsQkv, kWsQ, kWsK, kWsV, kWsO, kWsProj, kWsR, kWsF, kWsG, kWsH, kWsW2, kWsRope, kWsCount };
 
 size_t dit_workspace(const PrometheusDitBlockBf16Request* r, size_t off[kWsCount]) {
   const size_t T = r->tokens, D = r->hidden, F = r->ffn_hidden;
-  const size_t sizes[kWsCount] = {4 * D * 4,  T * D * 2, T * 3 * D * 4, T * D * 2, T * D * 2, T * D * 2, T * D * 2,
-                                  T * D * 4,  T * D * 4, T * D * 2,     T * 2 * F * 4, T * F * 2, T * D * 4};
+  const size_t sizes[kWsCount] = {4 * D * 4, T * D * 2, T * 3 * D * 4, T * D * 2,     T * D * 2, T * D * 2,
+                                  T * D * 2, T * D * 4, T * D * 4,     T * D * 2,     T * 2 * F * 4, T * F * 2,
+                                  T * D * 4, T * 64 * 8};
   size_t o = 0;
   for (int i = 0; i < kWsCount; ++i) {
     off[i] = o;
@@ -333,6 +354,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   float* G = reinterpret_cast<float*>(ws + off[kWsG]);
   uint16_t* Hb = reinterpret_cast<uint16_t*>(ws + off[kWsH]);
   float* W2 = reinterpret_cast<float*>(ws + off[kWsW2]);
+  float2* rope = reinterpret_cast<float2*>(ws + off[kWsRope]);
   const float* scaleA = mod;
   const float* gateA = mod + D;
   const float* scaleM = mod + 2 * D;
@@ -346,14 +368,16 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     ++n;                           \
   } while (0)
   const dim3 rows((T + 3) / 4), blk(256);
-  hipLaunchKernelGGL(adaln_kernel, dim3((4 * D + 255) / 256), blk, 0, st, r->condition, r->w_adaln, r->b_adaln, mod, C, D);
+  hipLaunchKernelGGL(adaln_kernel, dim3((4 * D + 63) / 64), blk, 0, st, r->condition, r->w_adaln, r->b_adaln, mod, C, D);
+  PROM_STEP(hipGetLastError());
+  hipLaunchKernelGGL(rope_table_kernel, dim3((T * 64 + 255) / 256), blk, 0, st, r->coordinates, rope, T, r->rope_theta,
+                     (int)r->rope_axes[0], (int)r->rope_axes[1]);
   PROM_STEP(hipGetLastError());
   hipLaunchKernelGGL(norm_mod_kernel, rows, blk, 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, qkv, nullptr, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, r->coordinates, r->q_norm, r->k_norm,
-                     Q, K, V, T, H, eps, r->rope_theta, (int)r->rope_axes[0], (int)r->rope_axes[1],
-                     (int)r->rope_axes[2]);
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, Q, K, V,
+                     T, H, eps);
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_flash_attn_bf16(Q, D, K, D, V, D, O, D, T, H, 1.0f / sqrtf(128.0f), st));
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, proj, nullptr, D, T, D, D, nullptr, 0, st, nullptr));

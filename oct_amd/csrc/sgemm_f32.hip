@@ -7,9 +7,9 @@
 // are FMA loops on 8x8 threads; this is a different design built for the
 // matrix cores:
 //
-//   * workgroup = 256 threads = 4 wave64, macro tile 128x128, K tile 16;
-//     each wave owns a 64x64 sub-tile = 2x2 MFMA 32x32 blocks (64 fp32
-//     accumulators per lane);
+//   * workgroup = 256 threads = 4 wave64, macro tile 128x256, K tile 16;
+//     each wave owns a 64x128 sub-tile = 2x4 MFMA 32x32 blocks (128 fp32
+//     accumulators per lane; 6 LDS reads per 8 MFMAs);
 //   * A and B are staged through LDS, double-buffered: the next K tile is
 //     fetched into registers while the current one feeds the MFMAs, then
 //     written to the other LDS buffer; one barrier per K tile;
@@ -33,7 +33,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128;
-constexpr int kBN = 128;
+constexpr int kBN = 256;
 constexpr int kBK = 16;
 constexpr int kLdsA = kBM + 2;  // k-major A rows; +2 keeps the transposing stores conflict-free
 constexpr int kLdsB = kBN + 4;  // k-major B rows; multiple of 4 for 128-bit stores
@@ -84,14 +84,15 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
   const int wm = wave >> 1;
   const int wn = wave & 1;
 
-  // Global->register assignment: A: one row, 8 consecutive k; B: two k rows, 4 consecutive n.
+  // Global->register assignment: A: one row, 8 consecutive k;
+  // B: k rows tid/64 + {0,4,8,12}, 4 consecutive n at (tid%64)*4.
   const int a_row = tid >> 1;
   const int a_k = (tid & 1) * 8;
-  const int b_k = tid >> 5;
-  const int b_n = (tid & 31) * 4;
+  const int b_k = tid >> 6;
+  const int b_n = (tid & 63) * 4;
 
   float ra[8];
-  float rb[8];
+  float rb[16];
 
   auto load_tile = [&](int k0) {
     const int gr = row0 + a_row;
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
         ra[4 * h + 3] = v.w;
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int gk = k0 + b_k + 8 * h;
+      for (int h = 0; h < 4; ++h) {
+        const int gk = k0 + b_k + 4 * h;
         floatx4 v = {0.f, 0.f, 0.f, 0.f};
         if (gk < K && gn < N) v = *reinterpret_cast<const floatx4*>(B + (size_t)gk * ldb + gn);
         rb[4 * h + 0] = v.x;
@@ -124,8 +125,8 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
         ra[j] = (gr < M && gk < K) ? A[(size_t)gr * lda + gk] : 0.f;
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int gk = k0 + b_k + 8 * h;
+      for (int h = 0; h < 4; ++h) {
+        const int gk = k0 + b_k + 4 * h;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           rb[4 * h + j] = (gk < K && gn + j < N) ? B[(size_t)gk * ldb + gn + j] : 0.f;
@@ -138,13 +139,17 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 #pragma unroll
     for (int j = 0; j < 8; ++j) As[buf][a_k + j][a_row] = ra[j];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 4; ++h) {
       floatx4 v = {rb[4 * h + 0], rb[4 * h + 1], rb[4 * h + 2], rb[4 * h + 3]};
-      *reinterpret_cast<floatx4*>(&Bs[buf][b_k + 8 * h][b_n]) = v;
+      *reinterpret_cast<floatx4*>(&Bs[buf][b_k + 4 * h][b_n]) = v;
     }
   };
 
-  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+  floatx16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
 
   const int k_tiles = (K + kBK - 1) / kBK;
   load_tile(0);
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
   const int lrow = lane & 31;
   const int lk = lane >> 5;
   const int am = wm * 64 + lrow;
-  const int bn = wn * 64 + lrow;
+  const int bn = wn * 128 + lrow;
 
   for (int kt = 0; kt < k_tiles; ++kt) {
     const int cur = kt & 1;
@@ -163,14 +168,15 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 #pragma unroll
     for (int s = 0; s < kBK / 2; ++s) {
       const int kr = 2 * s + lk;
-      const float a0 = As[cur][kr][am];
-      const float a1 = As[cur][kr][am + 32];
-      const float b0 = Bs[cur][kr][bn];
-      const float b1 = Bs[cur][kr][bn + 32];
-      acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc00, 0, 0, 0);
-      acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc01, 0, 0, 0);
-      acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc10, 0, 0, 0);
-      acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc11, 0, 0, 0);
+      float a[2], b[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = As[cur][kr][am + 32 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[cur][kr][bn + 32 * j];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
     if (more) store_tile(cur ^ 1);
     __syncthreads();
@@ -179,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
   // Accumulator layout of a 32x32 MFMA block: lane l, register r holds
   // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
   auto store_block = [&](const floatx16& acc, int mi, int ni) {
-    const int col = col0 + wn * 64 + ni * 32 + lrow;
+    const int col = col0 + wn * 128 + ni * 32 + lrow;
     if (col >= N) return;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -191,10 +197,10 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
       }
     }
   };
-  store_block(acc00, 0, 0);
-  store_block(acc01, 0, 1);
-  store_block(acc10, 1, 0);
-  store_block(acc11, 1, 1);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_block(acc[i][j], i, j);
 }
 
 // y[m] = A[m,:] . x : one wave per row, 4 rows per workgroup.  HBM-bound:
@@ -252,11 +258,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Number of K slices for an under-filled launch: aim for >= 2 workgroups per
-// CU (512 on 256 CUs) while keeping every slice >= 256 deep.
+// CU (512 on 256 CUs) while keeping every slice >= 128 deep.
 int choose_splits(int tiles, uint32_t k) {
   if (tiles >= 512 || k < 512) return 1;
   int s = (512 + tiles - 1) / tiles;
-  s = std::min(s, (int)(k / 256));
+  s = std::min(s, (int)(k / 128));
   s = std::min(s, 16);
   return std::max(s, 1);
 }
