@@ -27,6 +27,10 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kOpSum = 1, kOpMax = 2, kOpSoftmax = 3, kOpRms = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Hardware base-2 exponential (v_exp_f32).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -96,30 +100,35 @@ __global__ __launch_bounds__(256) void row_resident_kernel(const float* __restri
       }
     }
     m = wave_max_f32(m);
+    // exp(x - m) = exp2((x - m) * log2 e) on the hardware exp2; the row sum
+    // stays binary64; the normalisation multiplies by one correctly rounded
+    // reciprocal.  Relative error per element is a few fp32 ulps.
+    // (x - m) is formed first: it is exact when x and m are close, so rows of
+    // large nearby values (e.g. 1e4 +- 8) keep full relative accuracy.
     double acc = 0.0;
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
       const uint32_t i = (uint32_t)c * 64u + lane;
       if (i < w4) {
-        v[c].x = expf(v[c].x - m);
-        v[c].y = expf(v[c].y - m);
-        v[c].z = expf(v[c].z - m);
-        v[c].w = expf(v[c].w - m);
+        v[c].x = exp2_hw((v[c].x - m) * kLog2e);
+        v[c].y = exp2_hw((v[c].y - m) * kLog2e);
+        v[c].z = exp2_hw((v[c].z - m) * kLog2e);
+        v[c].w = exp2_hw((v[c].w - m) * kLog2e);
         acc += ((double)v[c].x + (double)v[c].y) + ((double)v[c].z + (double)v[c].w);
       }
     }
     acc = wave_sum_f64(acc);
-    const float denom = (float)acc;
+    const float rden = (float)(1.0 / acc);
     floatx4* dst = reinterpret_cast<floatx4*>(out + (size_t)row * width);
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
       const uint32_t i = (uint32_t)c * 64u + lane;
       if (i < w4) {
         floatx4 o;
-        o.x = v[c].x / denom;
-        o.y = v[c].y / denom;
-        o.z = v[c].z / denom;
-        o.w = v[c].w / denom;
+        o.x = v[c].x * rden;
+        o.y = v[c].y * rden;
+        o.z = v[c].z * rden;
+        o.w = v[c].w * rden;
         dst[i] = o;
       }
     }
