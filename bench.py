@@ -81,6 +81,61 @@ def cpu_baseline_sgemm(n: int, seconds: float):
     }
 
 
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        return max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
+    except Exception:  # noqa: BLE001 - informational only
+        return 1
+
+
+def cpu_baseline_secondary(seconds: float):
+    """CPU timings of the oracles for the secondary rows (bounded samples).
+
+    Reductions: the reference's prom_reduction_cpu_reference / RMSNorm CPU
+    oracle restated in C (scalar, one thread) over the full [8192, 4096]
+    input.  Decoder layer: the binary64 numpy restatement of the C4 layer
+    (BLAS threads as reported)."""
+    import oracle
+    from oracle import blocks
+
+    out = {}
+    rows, width = 8192, 4096
+    x = oracle.normal(77, (rows, width))
+    for op, name, nbytes in ((3, "softmax", 2 * x.nbytes), (1, "row_sum", x.nbytes + rows * 4),
+                             (2, "row_max", x.nbytes + rows * 4)):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle.reduction_reference(x, op)
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= min(2.0, seconds / 4) or reps >= 20:
+                break
+        out[f"{name}_8192x4096_gbs"] = round(nbytes * reps / dt / 1e9, 3)
+    w = (1.0 + oracle.normal(89, (width,), 0.0, 0.02)).astype(np.float32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.rmsnorm_reference(x, w, 1e-6)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min(2.0, seconds / 4) or reps >= 20:
+            break
+    out["rmsnorm_8192x4096_gbs"] = round((2 * x.nbytes + w.nbytes + rows * 4) * reps / dt / 1e9, 3)
+    out["reductions_cores"] = 1
+    del x
+    T, D, Hq, hd, F = 512, 2048, 8, 256, 16384
+    xx, wl = blocks.make_decoder_layer(4, T, D, Hq, hd, F)
+    t0 = time.perf_counter()
+    blocks.decoder_layer_f32(xx, wl, Hq, hd)
+    out["gemma2b_layer_f64_t512_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+    out["gemma2b_layer_cores"] = _blas_threads()
+    out["kind"] = "port"
+    out["sample"] = ("reductions: one full [8192,4096] pass per repetition (C oracle, fp32 data, binary64 sums); "
+                     "layer: one full T=512 Gemma-2B-shaped layer in binary64 numpy")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,7 +196,7 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: A,B ~ U[-1,1] (SplitMix64/xoshiro256** seeds 11,12), fp32 row-major, resident in HBM",
         "config": {"workload": "sgemm_f32 C=A@B M=N=K=4096 row-major (BASELINE configs[1])", "m": n, "n": n, "k": n,
-                   "kernel": "sgemm_f32_mfma_kernel (v_mfma_f32_32x32x2_f32, 128x128x16 tiles)"},
+                   "kernel": "sgemm_f32_mfma_kernel (v_mfma_f32_32x32x2_f32, 128x256x16 tiles, 64x128 per wave)"},
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 3),
@@ -263,6 +318,8 @@ def main() -> int:
 
     rt.close()
     line["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline_sgemm(n, args.cpu_seconds)
+    if not args.no_cpu_baseline and not args.no_secondary:
+        line["secondary_cpu_baseline"] = cpu_baseline_secondary(args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 
