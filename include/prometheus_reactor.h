@@ -70,6 +70,8 @@ enum {
   PROM_TESTCFG_FAIL_DISPATCH = 1u << 4,
   PROM_TESTCFG_FAIL_DOWNLOAD = 1u << 5,
   PROM_TESTCFG_SKIP_VULKAN_INIT = 1u << 7,
+  /* An async query observes a failure for every submitted task. */
+  PROM_TESTCFG_FAIL_ASYNC_POLL = 1u << 15,
 };
 
 /* reactor_api.h:227-324 (subset) */
@@ -644,6 +646,347 @@ PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16(void* handle, con
 PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16_device(void* handle,
                                                                       const PrometheusDitBlockBf16Request* request,
                                                                       PrometheusBlockResult* out_result);
+
+/* ------------------------------------------------------------------------ */
+/* Asynchronous and batched SGEMM (reference lifecycle, HIP execution)       */
+/* ------------------------------------------------------------------------ */
+
+/* reactor_api.h:84-114 */
+enum {
+  PROM_ASYNC_STATE_IDLE = 0,
+  PROM_ASYNC_STATE_SUBMITTED = 1,
+  PROM_ASYNC_STATE_READY = 2,
+  PROM_ASYNC_STATE_FAILED = 3,
+  PROM_ASYNC_STATE_CONSUMED = 4,
+};
+
+enum {
+  PROM_ASYNC_FAILURE_NONE = 0,
+  PROM_ASYNC_FAILURE_PRE_SUBMIT = 1,
+  PROM_ASYNC_FAILURE_OBSERVATION = 2,
+  PROM_ASYNC_FAILURE_QUERY = 3,
+  PROM_ASYNC_FAILURE_SUBMISSION = 4,
+  PROM_ASYNC_FAILURE_DEVICE_LOST = 5,
+};
+
+enum {
+  PROM_ASYNC_PHYSICAL_EMPTY = 0,
+  PROM_ASYNC_PHYSICAL_PREPARING = 1,
+  PROM_ASYNC_PHYSICAL_RECORDED = 2,
+  PROM_ASYNC_PHYSICAL_SUBMITTED = 3,
+  PROM_ASYNC_PHYSICAL_COMPLETE = 4,
+  PROM_ASYNC_PHYSICAL_READY = 5,
+  PROM_ASYNC_PHYSICAL_FAILED = 6,
+  PROM_ASYNC_PHYSICAL_QUARANTINED = 7,
+  PROM_ASYNC_PHYSICAL_FAILED_FATAL = 8,
+};
+
+/* reactor_api.h:250-260, 282-295 */
+enum {
+  PROM_DETAIL_ASYNC_NOT_READY = -6108,
+  PROM_DETAIL_ASYNC_NO_TASK = -6109,
+  PROM_DETAIL_ASYNC_ALREADY_CONSUMED = -6110,
+  PROM_DETAIL_ASYNC_INVALID_TASK = -6111,
+  PROM_DETAIL_ASYNC_SUBMIT_REJECTED = -6112,
+  PROM_DETAIL_ASYNC_SOFTWARE_SUPPRESSED = -6113,
+  PROM_DETAIL_ASYNC_FAILED = -6114,
+  PROM_DETAIL_ASYNC_UNCONSUMED = -6115,
+  PROM_DETAIL_INJECTED_ASYNC_POLL_FAILURE = -6116,
+  PROM_DETAIL_ASYNC_QUEUE_FULL = -6117,
+  PROM_DETAIL_BATCH_ZERO_WORKERS = -6601,
+  PROM_DETAIL_BATCH_PLAN_INVALID = -6602,
+  PROM_DETAIL_BATCH_EVENT_RING_OVERFLOW = -6603,
+  PROM_DETAIL_BATCH_EXECUTION_FAILED = -6604,
+  PROM_DETAIL_BATCH_RESOURCE_OWNERSHIP_VIOLATION = -6605,
+  PROM_DETAIL_BATCH_COMMAND_RESOURCE_CREATE_FAILED = -6606,
+  PROM_DETAIL_BATCH_COMMAND_RECORD_FAILED = -6607,
+  PROM_DETAIL_BATCH_FENCE_RESET_FAILED = -6608,
+  PROM_DETAIL_BATCH_FENCE_WAIT_FAILED = -6609,
+  PROM_DETAIL_BATCH_QUEUE_SUBMIT_FAILED = -6610,
+  PROM_DETAIL_BATCH_DEVICE_LOST = -6611,
+  PROM_DETAIL_BATCH_DRAIN_TIMEOUT = -6612,
+  PROM_DETAIL_BATCH_UNSUPPORTED_OPTION = -6613,
+};
+
+/* reactor_api.h:1448-1474.  Bits 0..7 of the batch flags are the requested
+   logical width (0 means 1); PARTITION_CONTIGUOUS selects the contiguous lane
+   map.  The other bits are test seams that only ..._sgemm_batch_m31_test
+   accepts; the public entry rejects them with BATCH_UNSUPPORTED_OPTION. */
+enum {
+  PROM_BATCH_FLAG_PARTITION_CONTIGUOUS = 1u << 8,
+  PROM_BATCH_FLAG_FAIL_AFTER_FIRST_SUBMIT = 1u << 9,
+  PROM_BATCH_FLAG_TEST_HW_CAP_SHIFT = 10u,
+  PROM_BATCH_FLAG_TEST_HW_CAP_MASK = 0xFu << 10u,
+  PROM_BATCH_FLAG_TEST_SEPARATE_COMPUTE_FAMILY = 1u << 10u,
+  PROM_BATCH_FLAG_TEST_ARENA_SCALE_SHIFT = 14u,
+  PROM_BATCH_FLAG_TEST_ARENA_SCALE_MASK = 0x3u << 14u,
+  PROM_BATCH_FLAG_TEST_EVENT_CAPACITY_SHIFT = 16u,
+  PROM_BATCH_FLAG_TEST_EVENT_CAPACITY_MASK = 0x3Fu << 16u,
+  PROM_BATCH_FLAG_TEST_DUAL_FAIL_FIRST_TWO = 1u << 22,
+  PROM_BATCH_FLAG_TEST_DELAY_ENTRY0 = 1u << 23,
+  PROM_BATCH_FLAG_TEST_FAIL_ENTRY_SHIFT = 24u,
+  PROM_BATCH_FLAG_TEST_FAIL_ENTRY_MASK = 0xFFu << 24u,
+};
+
+/* reactor_api.h:1476-1545 (the values this library reports) */
+enum { PROM_BATCH_PARTITION_ROUND_ROBIN = 1u, PROM_BATCH_PARTITION_CONTIGUOUS = 2u };
+enum {
+  PROM_BATCH_STATE_PENDING = 1u,
+  PROM_BATCH_STATE_RUNNING = 2u,
+  PROM_BATCH_STATE_FAILING = 3u,
+  PROM_BATCH_STATE_DRAINING = 4u,
+  PROM_BATCH_STATE_FAILED = 5u,
+  PROM_BATCH_STATE_SUCCEEDED = 6u,
+};
+enum { PROM_BATCH_EXECUTION_SINGLE_WORKER = 1u };
+enum { PROM_BATCH_WORKER_RESOURCE_SHARED = 2u };
+enum { PROM_BATCH_QUEUE_TOPOLOGY_SINGLE_QUEUE = 1u };
+enum { PROM_BATCH_QUEUE_MAPPING_SINGLE_QUEUE_SERIALIZED = 1u };
+
+/* reactor_api.h:1771-1779 */
+typedef struct PrometheusAsyncStatus {
+  uint32_t lifecycle_state;
+  uint32_t stage;
+  int detail_code;
+  uint32_t ready;
+  uint32_t failed;
+  uint32_t consumed;
+  uint32_t outstanding_tasks;
+} PrometheusAsyncStatus;
+
+/* reactor_api.h:1307-1314 */
+typedef struct PrometheusSgemmBatchEntry {
+  const float* a;
+  const float* b;
+  float* c;
+  uint32_t m;
+  uint32_t n;
+  uint32_t k;
+} PrometheusSgemmBatchEntry;
+
+/* reactor_api.h:1316-1447.  Field order and sizes are the reference's so a
+   caller compiled against it reads the same bytes.  This library fills the
+   plan, state, failure, lane, ring and per-entry (m31_*) fields; fields that
+   describe Vulkan worker threads, command pools, fences and slot leases have no
+   HIP counterpart and stay zero. */
+typedef struct PrometheusSgemmBatchDiagnostics {
+  uint32_t last_batch_entry_count;
+  uint32_t requested_workers;
+  uint32_t effective_workers;
+  uint32_t hardware_queue_cap;
+  uint32_t memory_worker_cap;
+  uint32_t worker_cap_reason;
+  uint32_t partition_policy;
+  uint32_t batch_state;
+  uint32_t failed_entry_id;
+  uint32_t failed_worker_id;
+  uint32_t failure_stage;
+  int32_t failure_detail;
+  uint32_t failure_count;
+  uint32_t first_failure_stable;
+  uint32_t event_overflow_count;
+  uint32_t event_drain_count;
+  uint32_t output_committed;
+  uint32_t plan_generation;
+  uint32_t worker_judgment_count;
+  uint32_t execution_mode;
+  uint32_t worker_resource_mode;
+  uint32_t queue_topology_classification;
+  uint32_t queue_mapping_mode;
+  uint32_t lane_worker_count;
+  uint32_t real_worker_thread_count;
+  uint32_t serialized_vulkan;
+  uint32_t serialized_bridge_enter_count;
+  uint32_t serialized_execution_count;
+  uint32_t serialized_wait_count;
+  uint32_t max_concurrent_serialized_entries;
+  uint32_t hardware_parallelism_claimed;
+  uint32_t resource_ownership_violation_count;
+  uint32_t resource_creation_failure_count;
+  uint32_t worker_active_mask;
+  uint32_t worker_assigned_count[8];
+  uint32_t worker_completed_count[8];
+  uint32_t worker_event_count[8];
+  uint32_t worker_queue_index[8];
+  uint32_t worker_submit_count[8];
+  uint32_t worker_wait_count[8];
+  uint32_t worker_in_flight[8];
+  uint32_t worker_slot_id[8];
+  uint32_t worker_output_staging_id[8];
+  uint32_t worker_arena_bank_id[8];
+  uint32_t worker_command_pool_id[8];
+  uint32_t worker_command_buffer_id[8];
+  uint32_t worker_fence_id[8];
+  uint32_t worker_command_pool_valid[8];
+  uint32_t worker_command_buffer_valid[8];
+  uint32_t worker_fence_valid[8];
+  uint32_t worker_reset_count[8];
+  uint32_t worker_record_count[8];
+  uint32_t worker_failure_stage[8];
+  int32_t worker_failure_detail[8];
+  uint32_t reported_compute_queue_count;
+  uint32_t independent_compute_queue_count;
+  uint32_t true_multi_queue_selected;
+  uint32_t hardware_parallelism_eligible;
+  uint32_t serialized_fallback_reason;
+  uint32_t per_worker_queue_family[8];
+  uint32_t per_worker_fence_state[8];
+  uint32_t queue_drain_count;
+  uint32_t drain_timeout_count;
+  uint32_t queue_family_ownership_handoff_count;
+  uint32_t transfer_compute_sync_wait_count;
+  uint32_t unsafe_to_reuse;
+  uint32_t slots_per_worker_target;
+  uint32_t effective_slots_per_worker;
+  uint32_t total_slot_count;
+  uint32_t slot_cap_reason;
+  uint32_t slot_refill_count;
+  uint32_t slot_full_scan_poll_count;
+  uint32_t slot_attention_poll_count;
+  uint32_t slot_polling_avoided_count;
+  uint32_t slot_failure_count;
+  uint32_t slot_drain_count;
+  uint32_t slot_boundary_generation;
+  uint32_t slot_dirty_mask;
+  uint32_t slot_ready_mask;
+  uint32_t slot_failed_mask;
+  uint32_t slot_invalidated_mask;
+  uint32_t slot_attention_mask;
+  uint32_t slot_owner_worker_id[16];
+  uint32_t slot_state[16];
+  uint32_t slot_generation[16];
+  uint32_t slot_entry_id[16];
+  uint32_t slot_queue_id[16];
+  uint32_t slot_command_resource_id[16];
+  uint32_t slot_arena_id[16];
+  uint32_t slot_output_staging_id[16];
+  uint32_t slot_in_flight[16];
+  uint32_t slot_ready[16];
+  uint32_t slot_invalidated[16];
+  uint32_t slot_failure_stage[16];
+  int32_t slot_failure_detail[16];
+  uint64_t p13_m10_lease_request_count;
+  uint64_t p13_m10_lease_grant_count;
+  uint64_t p13_m10_lease_deny_count;
+  uint64_t p13_m10_lease_yield_count;
+  uint32_t p13_m10_lease_last_state;
+  uint32_t p13_m10_lease_last_deny_reason;
+  uint32_t p13_m10_lookahead_requested;
+  uint32_t p13_m10_lookahead_allowed;
+  uint32_t p13_m10_lookahead_blocked_reason;
+  uint32_t p13_m10_selected_recipe_variant;
+  uint32_t physical_ring_depth_configured;
+  uint32_t physical_ring_depth_effective;
+  uint32_t current_in_flight;
+  uint32_t max_in_flight;
+  uint64_t total_submits;
+  uint64_t total_polls;
+  uint64_t total_forced_waits;
+  uint64_t ring_full_count;
+  uint64_t refill_count;
+  uint64_t query_harvest_count;
+  uint64_t quarantine_count;
+  uint64_t reap_count;
+  uint64_t feedback_committed_count;
+  uint64_t feedback_skipped_count;
+  uint32_t m31_completion_count;
+  uint32_t m31_commit_count;
+  uint64_t m31_submission_sequence[64];
+  uint32_t m31_physical_slot_id[64];
+  uint32_t m31_completion_status[64];
+  uint64_t m31_gpu_duration_ns[64];
+  uint32_t m31_completion_order[64];
+  uint32_t m31_commit_order[64];
+} PrometheusSgemmBatchDiagnostics;
+
+/* reactor_api.h:1987-2006 */
+typedef struct PrometheusSgemmAsyncTaskDiagnostics {
+  int32_t task_id;
+  uint32_t generation;
+  uint32_t lifecycle_state;
+  uint32_t physical_slot_id;
+  uint32_t physical_slot_generation;
+  uint64_t submission_sequence;
+  uint32_t timing_valid;
+  uint64_t gpu_duration_ns;
+  uint32_t feedback_pending;
+  uint32_t feedback_committed;
+  int32_t failure_detail;
+  uint32_t failure_class;
+  uint32_t abandoned;
+  uint32_t physical_slot_state;
+  uint32_t quarantined;
+  uint32_t physical_completion_confirmed;
+  uint32_t reap_pending;
+  uint32_t reap_completed;
+} PrometheusSgemmAsyncTaskDiagnostics;
+
+/* reactor_api.h:2008-2032 */
+typedef struct PrometheusSgemmAsyncDiagnostics {
+  uint32_t task_capacity;
+  uint32_t active_task_count;
+  uint32_t submitted_count;
+  uint32_t ready_count;
+  uint32_t failed_count;
+  uint32_t consumed_count;
+  uint32_t abandoned_count;
+  uint64_t queue_full_count;
+  uint64_t stale_id_rejection_count;
+  uint32_t max_in_flight;
+  uint32_t feedback_pending_count;
+  uint64_t feedback_committed_count;
+  uint64_t feedback_skipped_count;
+  uint64_t next_feedback_sequence;
+  uint32_t quarantined_slot_count;
+  uint64_t quarantine_event_count;
+  uint64_t reap_poll_count;
+  uint64_t reap_success_count;
+  uint64_t reap_wait_count;
+  uint64_t reap_failure_count;
+  uint32_t max_quarantine_depth;
+  uint32_t runtime_unsafe_to_reuse;
+  PrometheusSgemmAsyncTaskDiagnostics tasks[4];
+} PrometheusSgemmAsyncDiagnostics;
+
+/* reactor_api.h:2610-2615; reactor_sgemm.cpp:5984-6009, reactor_batch.c:244-560.
+   Runs every entry C_i = A_i @ B_i (host pointers, row-major fp32) and commits
+   all outputs in entry order only when every entry succeeded; a failure leaves
+   every caller output untouched.  Entries are validated before any work is
+   enqueued (BATCH_PLAN_INVALID names the first bad entry in the diagnostics).
+   Any number of entries; the device arena is reused across calls. */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_batch(void* handle, const PrometheusSgemmBatchEntry* entries,
+                                                            uint32_t entry_count, uint32_t flags, uint32_t* out_stage,
+                                                            int* out_detail_code);
+/* reactor_api.h:2617-2622 -- the same with the test seams of the flag word
+   enabled (FAIL_AFTER_FIRST_SUBMIT, TEST_FAIL_ENTRY, TEST_DUAL_FAIL_FIRST_TWO). */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_batch_m31_test(void* handle,
+                                                                     const PrometheusSgemmBatchEntry* entries,
+                                                                     uint32_t entry_count, uint32_t flags,
+                                                                     uint32_t* out_stage, int* out_detail_code);
+/* reactor_api.h:2649-2650 -- the last batch's diagnostics. */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_batch_diagnostics(void* handle,
+                                                                        PrometheusSgemmBatchDiagnostics* out_diag);
+/* reactor_api.h:2623-2631; reactor_sgemm.cpp:6298-6342.  Copies A and B into
+   pinned staging, enqueues upload, SGEMM and download on the runtime stream
+   and returns a task id (4-entry task table, ids carry a generation; two
+   submission slots, so a third unconsumed task is QUEUE_FULL).  While any task
+   is unconsumed the synchronous ..._sgemm is rejected with ASYNC_UNCONSUMED. */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_submit_async(void* handle, const float* a, const float* b,
+                                                                   uint32_t m, uint32_t n, uint32_t k,
+                                                                   int* out_task_id, uint32_t* out_stage,
+                                                                   int* out_detail_code);
+/* reactor_api.h:2632-2634; reactor_sgemm.cpp:6344-6364 -- non-blocking. */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_query_async(void* handle, int task_id,
+                                                                  PrometheusAsyncStatus* out_status);
+/* reactor_api.h:2635-2636; reactor_sgemm.cpp:6366-6416 */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_async_diagnostics(void* handle,
+                                                                         PrometheusSgemmAsyncDiagnostics* out_diag);
+/* reactor_api.h:2637-2642; reactor_sgemm.cpp:6418-6471 -- c_len >= m*n. */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_consume_async(void* handle, int task_id, float* c,
+                                                                    uint32_t c_len, uint32_t* out_stage,
+                                                                    int* out_detail_code);
+/* reactor_api.h:2643; reactor_sgemm.cpp:6473-6502 -- rejected while running. */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_abandon_async(void* handle, int task_id);
 
 #ifdef __cplusplus
 }

@@ -505,6 +505,11 @@ extern "C" {
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm(void* handle, const float* a, const float* b, float* c,
                                                       uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
                                                       int* out_detail_code) {
+  // reactor_sgemm.cpp:4204-4211: no synchronous SGEMM while async tasks are unconsumed.
+  if (Runtime* rt = lookup(handle); rt != nullptr && async_outstanding(rt) != 0u) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_SUBMIT, PROM_DETAIL_ASYNC_UNCONSUMED);
+    return PROM_ERROR;
+  }
   return gemm_host<float>(handle, a, b, c, m, n, k, out_stage, out_detail_code, launch_sgemm_f32);
 }
 

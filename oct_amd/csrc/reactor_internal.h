@@ -20,6 +20,8 @@ constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
 constexpr uint32_t kStagingSlots = 8;  // 0-3 operand staging, 4 block workspace, 5 block host staging
 
+struct AsyncState;  // async task table, submission slots and batch arenas (sgemm_async.hip)
+
 struct Runtime {
   uint64_t magic;
   uint32_t test_flags;
@@ -28,6 +30,8 @@ struct Runtime {
   int32_t init_detail;      // reason when unavailable
   uint64_t requests;
   uint64_t successes;
+  uint32_t batch_ring_depth;  // 1..4 (config batch_ring_depth; 0 selects 2)
+  AsyncState* async;          // created on first async or batch call
 };
 
 struct DeviceContext {
@@ -50,6 +54,12 @@ bool ensure_device();
 Runtime* lookup(void* handle);
 // Grow-only device staging buffer `slot` of at least `bytes`.
 void* staging(uint32_t slot, size_t bytes);
+
+// Unconsumed async tasks of a runtime (READY and FAILED count until consumed
+// or abandoned); the synchronous SGEMM is rejected while this is non-zero.
+uint32_t async_outstanding(Runtime* rt);
+// Waits for the runtime's queued work and frees its async/batch resources.
+void async_release(Runtime* rt);
 
 inline void set_status(uint32_t* stage, int* detail, uint32_t s, int d) {
   if (stage) *stage = s;

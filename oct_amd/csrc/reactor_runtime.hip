@@ -106,10 +106,11 @@ PROM_REACTOR_API uint32_t prometheus_reactor_abi_version(void) { return PROM_REA
 PROM_REACTOR_API int prometheus_reactor_runtime_create(void* config, void** out_handle) {
   if (out_handle == nullptr) return PROM_ERROR;
   *out_handle = nullptr;
-  uint32_t test_flags = 0, reduction_flags = 0;
+  uint32_t test_flags = 0, reduction_flags = 0, ring_depth = 0;
   if (config != nullptr) {
     const PrometheusReactorConfig* cfg = static_cast<const PrometheusReactorConfig*>(config);
     if (cfg->struct_size >= offsetof(PrometheusReactorConfig, p15_shadow_disabled)) test_flags = cfg->test_flags;
+    if (cfg->struct_size >= offsetof(PrometheusReactorConfig, reduction_test_flags)) ring_depth = cfg->batch_ring_depth;
     if (cfg->struct_size >= offsetof(PrometheusReactorConfig, reduction_ring_depth))
       reduction_flags = cfg->reduction_test_flags;
   }
@@ -119,6 +120,8 @@ PROM_REACTOR_API int prometheus_reactor_runtime_create(void* config, void** out_
   rt->magic = kRuntimeMagic;
   rt->test_flags = test_flags;
   rt->reduction_test_flags = reduction_flags;
+  // reactor_api.h:1759-1760: zero keeps the default depth of two; at most four.
+  rt->batch_ring_depth = ring_depth == 0u ? 2u : (ring_depth > 4u ? 4u : ring_depth);
   if ((test_flags & (PROM_TESTCFG_SKIP_VULKAN_INIT | PROM_TESTCFG_FAIL_DEVICE_CREATE)) != 0u) {
     rt->available = 0;
     rt->init_detail = PROM_DETAIL_HIP_UNAVAILABLE;
@@ -150,6 +153,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_destroy(void* handle) {
     std::lock_guard<std::mutex> lock(c.mu);
     (void)hipStreamSynchronize(c.stream);
   }
+  async_release(rt);
   rt->magic = 0;
   delete rt;
   return PROM_OK;

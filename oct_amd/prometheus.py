@@ -42,6 +42,7 @@ TESTCFG_FAIL_UPLOAD = 1 << 3
 TESTCFG_FAIL_DISPATCH = 1 << 4
 TESTCFG_FAIL_DOWNLOAD = 1 << 5
 TESTCFG_SKIP_VULKAN_INIT = 1 << 7
+TESTCFG_FAIL_ASYNC_POLL = 1 << 15
 DETAIL_INJECTED_UPLOAD_FAILURE = -6001
 DETAIL_INJECTED_DISPATCH_FAILURE = -6002
 DETAIL_INJECTED_DOWNLOAD_FAILURE = -6003
@@ -50,6 +51,27 @@ DETAIL_PATH_HIP_MFMA_F32 = 6120
 DETAIL_PATH_HIP_GEMV_F32 = 6121
 DETAIL_PATH_HIP_MFMA_BF16 = 6122
 DETAIL_HIP_UNAVAILABLE = -6905
+# async and batch (reactor_api.h:84-114, 250-260, 282-295, 1448-1545)
+ASYNC_IDLE, ASYNC_SUBMITTED, ASYNC_READY, ASYNC_FAILED, ASYNC_CONSUMED = range(5)
+DETAIL_ASYNC_NOT_READY = -6108
+DETAIL_ASYNC_NO_TASK = -6109
+DETAIL_ASYNC_ALREADY_CONSUMED = -6110
+DETAIL_ASYNC_INVALID_TASK = -6111
+DETAIL_ASYNC_FAILED = -6114
+DETAIL_ASYNC_UNCONSUMED = -6115
+DETAIL_INJECTED_ASYNC_POLL_FAILURE = -6116
+DETAIL_ASYNC_QUEUE_FULL = -6117
+DETAIL_BATCH_PLAN_INVALID = -6602
+DETAIL_BATCH_EXECUTION_FAILED = -6604
+DETAIL_BATCH_UNSUPPORTED_OPTION = -6613
+BATCH_FLAG_PARTITION_CONTIGUOUS = 1 << 8
+BATCH_FLAG_FAIL_AFTER_FIRST_SUBMIT = 1 << 9
+BATCH_FLAG_TEST_SEPARATE_COMPUTE_FAMILY = 1 << 10
+BATCH_FLAG_TEST_DUAL_FAIL_FIRST_TWO = 1 << 22
+BATCH_FLAG_TEST_FAIL_ENTRY_SHIFT = 24
+BATCH_PARTITION_ROUND_ROBIN, BATCH_PARTITION_CONTIGUOUS = 1, 2
+BATCH_STATE_FAILED, BATCH_STATE_SUCCEEDED = 5, 6
+BATCH_EXECUTION_SINGLE_WORKER = 1
 
 
 # ---- ABI structs -----------------------------------------------------------
@@ -338,6 +360,97 @@ class PrometheusBlockResult(Structure):
     ]
 
 
+class PrometheusAsyncStatus(Structure):
+    _fields_ = [("lifecycle_state", c_uint32), ("stage", c_uint32), ("detail_code", c_int),
+                ("ready", c_uint32), ("failed", c_uint32), ("consumed", c_uint32), ("outstanding_tasks", c_uint32)]
+
+
+class PrometheusSgemmBatchEntry(Structure):
+    _fields_ = [("a", c_void_p), ("b", c_void_p), ("c", c_void_p), ("m", c_uint32), ("n", c_uint32), ("k", c_uint32)]
+
+
+def _u32(name, count=None):
+    return (name, c_uint32 * count) if count else (name, c_uint32)
+
+
+class PrometheusSgemmBatchDiagnostics(Structure):
+    """reactor_api.h:1316-1447, field for field."""
+    _fields_ = (
+        [_u32(f) for f in (
+            "last_batch_entry_count", "requested_workers", "effective_workers", "hardware_queue_cap",
+            "memory_worker_cap", "worker_cap_reason", "partition_policy", "batch_state", "failed_entry_id",
+            "failed_worker_id", "failure_stage")]
+        + [("failure_detail", ctypes.c_int32)]
+        + [_u32(f) for f in (
+            "failure_count", "first_failure_stable", "event_overflow_count", "event_drain_count", "output_committed",
+            "plan_generation", "worker_judgment_count", "execution_mode", "worker_resource_mode",
+            "queue_topology_classification", "queue_mapping_mode", "lane_worker_count", "real_worker_thread_count",
+            "serialized_vulkan", "serialized_bridge_enter_count", "serialized_execution_count",
+            "serialized_wait_count", "max_concurrent_serialized_entries", "hardware_parallelism_claimed",
+            "resource_ownership_violation_count", "resource_creation_failure_count", "worker_active_mask")]
+        + [_u32(f, 8) for f in (
+            "worker_assigned_count", "worker_completed_count", "worker_event_count", "worker_queue_index",
+            "worker_submit_count", "worker_wait_count", "worker_in_flight", "worker_slot_id",
+            "worker_output_staging_id", "worker_arena_bank_id", "worker_command_pool_id",
+            "worker_command_buffer_id", "worker_fence_id", "worker_command_pool_valid",
+            "worker_command_buffer_valid", "worker_fence_valid", "worker_reset_count", "worker_record_count",
+            "worker_failure_stage")]
+        + [("worker_failure_detail", ctypes.c_int32 * 8)]
+        + [_u32(f) for f in (
+            "reported_compute_queue_count", "independent_compute_queue_count", "true_multi_queue_selected",
+            "hardware_parallelism_eligible", "serialized_fallback_reason")]
+        + [_u32(f, 8) for f in ("per_worker_queue_family", "per_worker_fence_state")]
+        + [_u32(f) for f in (
+            "queue_drain_count", "drain_timeout_count", "queue_family_ownership_handoff_count",
+            "transfer_compute_sync_wait_count", "unsafe_to_reuse", "slots_per_worker_target",
+            "effective_slots_per_worker", "total_slot_count", "slot_cap_reason", "slot_refill_count",
+            "slot_full_scan_poll_count", "slot_attention_poll_count", "slot_polling_avoided_count",
+            "slot_failure_count", "slot_drain_count", "slot_boundary_generation", "slot_dirty_mask",
+            "slot_ready_mask", "slot_failed_mask", "slot_invalidated_mask", "slot_attention_mask")]
+        + [_u32(f, 16) for f in (
+            "slot_owner_worker_id", "slot_state", "slot_generation", "slot_entry_id", "slot_queue_id",
+            "slot_command_resource_id", "slot_arena_id", "slot_output_staging_id", "slot_in_flight", "slot_ready",
+            "slot_invalidated", "slot_failure_stage")]
+        + [("slot_failure_detail", ctypes.c_int32 * 16)]
+        + [(f, c_uint64) for f in (
+            "p13_m10_lease_request_count", "p13_m10_lease_grant_count", "p13_m10_lease_deny_count",
+            "p13_m10_lease_yield_count")]
+        + [_u32(f) for f in (
+            "p13_m10_lease_last_state", "p13_m10_lease_last_deny_reason", "p13_m10_lookahead_requested",
+            "p13_m10_lookahead_allowed", "p13_m10_lookahead_blocked_reason", "p13_m10_selected_recipe_variant",
+            "physical_ring_depth_configured", "physical_ring_depth_effective", "current_in_flight", "max_in_flight")]
+        + [(f, c_uint64) for f in (
+            "total_submits", "total_polls", "total_forced_waits", "ring_full_count", "refill_count",
+            "query_harvest_count", "quarantine_count", "reap_count", "feedback_committed_count",
+            "feedback_skipped_count")]
+        + [_u32("m31_completion_count"), _u32("m31_commit_count"), ("m31_submission_sequence", c_uint64 * 64),
+           _u32("m31_physical_slot_id", 64), _u32("m31_completion_status", 64), ("m31_gpu_duration_ns", c_uint64 * 64),
+           _u32("m31_completion_order", 64), _u32("m31_commit_order", 64)]
+    )
+
+
+class PrometheusSgemmAsyncTaskDiagnostics(Structure):
+    _fields_ = [("task_id", ctypes.c_int32), ("generation", c_uint32), ("lifecycle_state", c_uint32),
+                ("physical_slot_id", c_uint32), ("physical_slot_generation", c_uint32),
+                ("submission_sequence", c_uint64), ("timing_valid", c_uint32), ("gpu_duration_ns", c_uint64),
+                ("feedback_pending", c_uint32), ("feedback_committed", c_uint32), ("failure_detail", ctypes.c_int32),
+                ("failure_class", c_uint32), ("abandoned", c_uint32), ("physical_slot_state", c_uint32),
+                ("quarantined", c_uint32), ("physical_completion_confirmed", c_uint32), ("reap_pending", c_uint32),
+                ("reap_completed", c_uint32)]
+
+
+class PrometheusSgemmAsyncDiagnostics(Structure):
+    _fields_ = [("task_capacity", c_uint32), ("active_task_count", c_uint32), ("submitted_count", c_uint32),
+                ("ready_count", c_uint32), ("failed_count", c_uint32), ("consumed_count", c_uint32),
+                ("abandoned_count", c_uint32), ("queue_full_count", c_uint64), ("stale_id_rejection_count", c_uint64),
+                ("max_in_flight", c_uint32), ("feedback_pending_count", c_uint32),
+                ("feedback_committed_count", c_uint64), ("feedback_skipped_count", c_uint64),
+                ("next_feedback_sequence", c_uint64), ("quarantined_slot_count", c_uint32),
+                ("quarantine_event_count", c_uint64), ("reap_poll_count", c_uint64), ("reap_success_count", c_uint64),
+                ("reap_wait_count", c_uint64), ("reap_failure_count", c_uint64), ("max_quarantine_depth", c_uint32),
+                ("runtime_unsafe_to_reuse", c_uint32), ("tasks", PrometheusSgemmAsyncTaskDiagnostics * 4)]
+
+
 # ---- errors and status (status.go, bridge.go) ------------------------------
 class ReactorIssue(RuntimeError):
     """Structured reactor failure (reference ``ReactorIssue``, bridge.go:33-66)."""
@@ -424,6 +537,21 @@ _SIGNATURES = {
     "prometheus_reactor_runtime_synchronize": (c_int, [c_void_p]),
     "prometheus_reactor_runtime_event_record": (c_int, [c_void_p, c_uint32]),
     "prometheus_reactor_runtime_event_elapsed_ms": (c_int, [c_void_p, c_uint32, c_uint32, POINTER(c_float)]),
+    "prometheus_reactor_runtime_sgemm_submit_async": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_int), POINTER(c_uint32),
+                POINTER(c_int)]),
+    "prometheus_reactor_runtime_sgemm_query_async": (c_int, [c_void_p, c_int, POINTER(PrometheusAsyncStatus)]),
+    "prometheus_reactor_runtime_sgemm_async_diagnostics": (
+        c_int, [c_void_p, POINTER(PrometheusSgemmAsyncDiagnostics)]),
+    "prometheus_reactor_runtime_sgemm_consume_async": (
+        c_int, [c_void_p, c_int, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_sgemm_abandon_async": (c_int, [c_void_p, c_int]),
+    "prometheus_reactor_runtime_sgemm_batch": (
+        c_int, [c_void_p, POINTER(PrometheusSgemmBatchEntry), c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_sgemm_batch_m31_test": (
+        c_int, [c_void_p, POINTER(PrometheusSgemmBatchEntry), c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_sgemm_batch_diagnostics": (
+        c_int, [c_void_p, POINTER(PrometheusSgemmBatchDiagnostics)]),
 }
 
 MANDATORY_SYMBOLS = (
@@ -498,7 +626,7 @@ class NativeRuntime:
     """
 
     def __init__(self, lib: Optional[ctypes.CDLL] = None, test_flags: Optional[int] = None,
-                 reduction_test_flags: int = 0):
+                 reduction_test_flags: int = 0, batch_ring_depth: int = 0):
         self.lib = lib or shared_library()
         if test_flags is None:
             env = os.environ.get(REACTOR_TEST_FLAGS_ENV_VAR, "")
@@ -507,6 +635,7 @@ class NativeRuntime:
         cfg.struct_size = ctypes.sizeof(cfg)
         cfg.test_flags = test_flags
         cfg.reduction_test_flags = reduction_test_flags
+        cfg.batch_ring_depth = batch_ring_depth
         handle = c_void_p()
         rc = self.lib.prometheus_reactor_runtime_create(byref(cfg), byref(handle))
         if rc != PROM_OK or not handle.value:
@@ -771,6 +900,80 @@ class NativeRuntime:
             self.handle, c_void_p(din), c_void_p(dw), c_void_p(dout), c_void_p(dinv) if dinv else None,
             tokens, width, stride, eps, byref(stage), byref(detail))
         return self._check(rc, stage, detail, "rmsnorm_device")
+
+    # -- asynchronous SGEMM (bridge.go:438-470) ------------------------------
+    def submit_async(self, m: int, n: int, k: int, a, b) -> Tuple[int, int, CallStatus]:
+        """Returns (rc, task_id, status); A and B may be reused as soon as this returns."""
+        a, b = _f32(a), _f32(b)
+        task, stage, detail = c_int(-1), c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_sgemm_submit_async(
+            self.handle, _ptr(a), _ptr(b), m, n, k, byref(task), byref(stage), byref(detail))
+        return rc, task.value, CallStatus(stage.value, detail.value)
+
+    def query_async(self, task_id: int) -> Tuple[int, PrometheusAsyncStatus]:
+        st = PrometheusAsyncStatus()
+        rc = self.lib.prometheus_reactor_runtime_sgemm_query_async(self.handle, task_id, byref(st))
+        return rc, st
+
+    def wait_async(self, task_id: int, timeout_s: float = 30.0) -> PrometheusAsyncStatus:
+        """Polls query_async until the task leaves SUBMITTED (bounded by timeout_s)."""
+        import time
+
+        deadline = time.monotonic() + timeout_s
+        while True:
+            rc, st = self.query_async(task_id)
+            if rc != PROM_OK or st.lifecycle_state != ASYNC_SUBMITTED or time.monotonic() > deadline:
+                return st
+            time.sleep(0.0005)
+
+    def consume_async(self, task_id: int, out: Optional[np.ndarray], c_len: Optional[int] = None):
+        stage, detail = c_uint32(0), c_int(0)
+        if c_len is None:
+            c_len = out.size if out is not None else 0
+        rc = self.lib.prometheus_reactor_runtime_sgemm_consume_async(
+            self.handle, task_id, _ptr(out), c_len, byref(stage), byref(detail))
+        return rc, CallStatus(stage.value, detail.value)
+
+    def abandon_async(self, task_id: int) -> int:
+        return self.lib.prometheus_reactor_runtime_sgemm_abandon_async(self.handle, task_id)
+
+    def async_diagnostics(self) -> PrometheusSgemmAsyncDiagnostics:
+        d = PrometheusSgemmAsyncDiagnostics()
+        rc = self.lib.prometheus_reactor_runtime_sgemm_async_diagnostics(self.handle, byref(d))
+        if rc != PROM_OK:
+            raise ReactorIssue("diagnostics_failed", f"async_diagnostics returned {rc}")
+        return d
+
+    # -- batched SGEMM (reactor_api.h:2610-2622) -----------------------------
+    def sgemm_batch(self, problems, flags: int = 0, test_entry: bool = False):
+        """problems: list of (a[m,k], b[k,n]).  Outputs start at -1 so that a
+        failed batch's untouched outputs are visible.  Returns (rc, status, outputs)."""
+        entries = (PrometheusSgemmBatchEntry * max(1, len(problems)))()
+        keep, outs = [], []
+        for i, (a, b) in enumerate(problems):
+            a, b = _f32(a), _f32(b)
+            m, k = a.shape
+            n = b.shape[1]
+            c = np.full((m, n), -1.0, np.float32)
+            keep.append((a, b))
+            outs.append(c)
+            entries[i] = PrometheusSgemmBatchEntry(_ptr(a), _ptr(b), _ptr(c), m, n, k)
+        rc, status = self.sgemm_batch_raw(entries, len(problems), flags, test_entry)
+        return rc, status, outs
+
+    def sgemm_batch_raw(self, entries, count: int, flags: int = 0, test_entry: bool = False):
+        stage, detail = c_uint32(0), c_int(0)
+        fn = (self.lib.prometheus_reactor_runtime_sgemm_batch_m31_test if test_entry
+              else self.lib.prometheus_reactor_runtime_sgemm_batch)
+        rc = fn(self.handle, entries, count, flags, byref(stage), byref(detail))
+        return rc, CallStatus(stage.value, detail.value)
+
+    def batch_diagnostics(self) -> PrometheusSgemmBatchDiagnostics:
+        d = PrometheusSgemmBatchDiagnostics()
+        rc = self.lib.prometheus_reactor_runtime_sgemm_batch_diagnostics(self.handle, byref(d))
+        if rc != PROM_OK:
+            raise ReactorIssue("diagnostics_failed", f"batch_diagnostics returned {rc}")
+        return d
 
 
 # ---- the strict `@` path (strict.go:11-32, runtime.go:251-317) -------------

@@ -64,7 +64,49 @@ STRUCTS = {
     "PrometheusDecoderLayerF32Request": p.PrometheusDecoderLayerF32Request,
     "PrometheusDitBlockBf16Request": p.PrometheusDitBlockBf16Request,
     "PrometheusBlockResult": p.PrometheusBlockResult,
+    "PrometheusAsyncStatus": p.PrometheusAsyncStatus,
+    "PrometheusSgemmBatchEntry": p.PrometheusSgemmBatchEntry,
+    "PrometheusSgemmBatchDiagnostics": p.PrometheusSgemmBatchDiagnostics,
+    "PrometheusSgemmAsyncTaskDiagnostics": p.PrometheusSgemmAsyncTaskDiagnostics,
+    "PrometheusSgemmAsyncDiagnostics": p.PrometheusSgemmAsyncDiagnostics,
 }
+
+# Structs whose layout the reference header fixes (a drop-in caller compiled
+# against it must read the same bytes).
+REFERENCE_STRUCTS = (
+    "PrometheusCaps", "PrometheusReactorConfig", "PrometheusVulkanDeviceDiagnostics", "PrometheusReductionRequest",
+    "PrometheusReductionStageDispatch", "PrometheusReductionPlan", "PrometheusReductionExecutionResult",
+    "PrometheusRowWiseSoftmaxRequest", "PrometheusRowWiseSoftmaxResult", "PrometheusGemma4E2BM1InputRmsNormRequest",
+    "PrometheusGemma4E2BM1InputRmsNormResult", "PrometheusAsyncStatus", "PrometheusSgemmBatchEntry",
+    "PrometheusSgemmBatchDiagnostics", "PrometheusSgemmAsyncTaskDiagnostics", "PrometheusSgemmAsyncDiagnostics",
+)
+REFERENCE_HEADER = Path("/root/reference/internal/prometheus/native/reactor_api.h")
+
+
+def _layout(tmp_path, header: Path, names, tag: str) -> dict:
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{header}"', "int main(void){"]
+    for name in names:
+        cls = STRUCTS[name]
+        lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{name}.{field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0;}")
+    src = tmp_path / f"layout_{tag}.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / f"layout_{tag}"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    return dict(line.rsplit(" ", 1) for line in out.splitlines())
+
+
+@pytest.mark.skipif(not REFERENCE_HEADER.exists(), reason="reference tree not present on this machine")
+def test_layouts_equal_the_reference_header(tmp_path):
+    """Every shared struct has the reference's size and field offsets
+    (compiled against internal/prometheus/native/reactor_api.h itself)."""
+    ours = _layout(tmp_path, HEADER, REFERENCE_STRUCTS, "ours")
+    ref = _layout(tmp_path, REFERENCE_HEADER, REFERENCE_STRUCTS, "ref")
+    diff = {k: (ours[k], ref[k]) for k in ours if ours[k] != ref[k]}
+    assert not diff, diff
 
 
 def test_ctypes_layouts_match_c_header(tmp_path):
@@ -93,6 +135,12 @@ def test_reference_struct_sizes_unchanged():
     assert ctypes.sizeof(p.PrometheusReactorConfig) == 40
     assert ctypes.sizeof(p.PrometheusRowWiseSoftmaxRequest) == 48
     assert ctypes.sizeof(p.PrometheusGemma4E2BM1InputRmsNormRequest) == 112
+    # reactor_api.h:1307-1447, 1771-1779, 1987-2032
+    assert ctypes.sizeof(p.PrometheusSgemmBatchEntry) == 40
+    assert ctypes.sizeof(p.PrometheusSgemmBatchDiagnostics) == 3984
+    assert ctypes.sizeof(p.PrometheusAsyncStatus) == 28
+    assert ctypes.sizeof(p.PrometheusSgemmAsyncTaskDiagnostics) == 88
+    assert ctypes.sizeof(p.PrometheusSgemmAsyncDiagnostics) == 488
 
 
 @pytest.fixture
