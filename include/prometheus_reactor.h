@@ -988,6 +988,37 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_consume_async(void* handle
 /* reactor_api.h:2643; reactor_sgemm.cpp:6473-6502 -- rejected while running. */
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_abandon_async(void* handle, int task_id);
 
+/* ------------------------------------------------------------------------ */
+/* Binary64 FFT                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* reactor_api.h:361-379 */
+enum {
+  PROM_FFT_DETAIL_UNAVAILABLE = -6701,
+  PROM_FFT_DETAIL_INVALID_REQUEST = -6702,
+  PROM_FFT_DETAIL_VULKAN_UNAVAILABLE = -6712,
+  PROM_FFT_DETAIL_UNSUPPORTED_SIZE = -6713,
+  PROM_FFT_DETAIL_ALLOCATION_FAILED = -6714,
+  PROM_FFT_DETAIL_UPLOAD_FAILED = -6715,
+  PROM_FFT_DETAIL_DISPATCH_FAILED = -6716,
+  PROM_FFT_DETAIL_READBACK_FAILED = -6717,
+};
+
+/* reactor_api.h:2652-2655; reactor_concept_fft.cpp:97-104.  Interleaved
+   binary64 complex pairs, forward, unnormalised, count a power of two in
+   [1, 2^20]; input and output each hold count pairs and may be the same
+   array.  Invalid requests -> INIT / PROM_FFT_DETAIL_INVALID_REQUEST; no
+   device -> INIT / PROM_FFT_DETAIL_VULKAN_UNAVAILABLE (no CPU fallback);
+   success -> TRANSFER_OUT / 0.  Result agrees with internal/fft/fft.go's CPU
+   transform within 1e-12 * max|X| per component (fft.go:176-192) and is
+   bit-identical to it for count <= 4096 given the same twiddle table. */
+PROM_REACTOR_API int prometheus_reactor_runtime_fft64(void* handle, const double* input, double* output,
+                                                      uint32_t count, uint32_t* stage, int* detail);
+/* NEW: the same transform on device pointers, enqueued on the runtime stream
+   (success -> SUBMIT / 0; synchronise before reading output). */
+PROM_REACTOR_API int prometheus_reactor_runtime_fft64_device(void* handle, const double* input, double* output,
+                                                             uint32_t count, uint32_t* stage, int* detail);
+
 #ifdef __cplusplus
 }
 #endif

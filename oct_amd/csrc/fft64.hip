@@ -1,0 +1,286 @@
+// Binary64 complex FFT (forward, unnormalised, power-of-two lengths <= 2^20).
+//
+// Contract: internal/fft/fft.go:206-258 (bit-reversal permutation, then
+// iterative radix-2 decimation-in-time butterflies with the n/2 roots
+// w_j = cos(-2*pi/n*j) + i sin(-2*pi/n*j)); entry validation and status codes:
+// internal/prometheus/native/reactor_concept_fft.cpp:97-104 and :36-76; the
+// host-side twiddle table, cached per length, follows :50-57.
+//
+// MI355X design.  A length L <= 4096 transform is held entirely in LDS by one
+// workgroup (64 KiB of double2): the bit-reversed load, log2(L) butterfly
+// stages separated by barriers, and the store.  It performs exactly the
+// reference's butterflies with its twiddles and no contraction, so its output
+// is bit-identical to the CPU contract.  Longer transforms use the four-step
+// factorisation N = N1 * N2 (N1, N2 <= 1024 for N <= 2^20), with n = N2*n1 + n2
+// and k = k1 + N1*k2:
+//   pass 1: for every column n2, an N1-point transform over x[N2*n1 + n2],
+//           multiplied by W_N^(n2*k1) on the way out and stored as T[k1*N2 + n2];
+//   pass 2: for every row k1, an N2-point transform over T[k1*N2 + n2], stored
+//           to X[k1 + N1*k2].
+// Each workgroup takes several adjacent columns (rows) so that its strided
+// loads and stores touch contiguous runs; the whole 16 MiB working set of a
+// 2^20-point transform stays resident in the MI355X's 256 MiB Infinity Cache
+// between the passes.
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "reactor_internal.h"
+
+namespace prom {
+
+namespace {
+
+constexpr uint32_t kFftThreads = 256;
+constexpr uint32_t kFftMaxLds = 4096;  // double2 elements per workgroup (64 KiB)
+constexpr uint32_t kFftMaxLog2 = 20;
+
+// Go's complex product (xu - yv) + (xv + yu)i with every operation rounded.
+__device__ __forceinline__ double2 cmul(double2 w, double2 v) {
+#pragma clang fp contract(off)
+  double2 t;
+  t.x = w.x * v.x - w.y * v.y;
+  t.y = w.x * v.y + w.y * v.x;
+  return t;
+}
+
+// One workgroup transforms `seqs` sequences of length L = 2^log2l.  Global
+// sequence q = blockIdx.x * seqs + s reads element i at
+// in[q * in_seq + i * in_elem] and writes element k at out[q * out_seq + k * out_elem].
+// seq_fast_in / seq_fast_out pick the thread order of the global accesses
+// (adjacent threads on adjacent sequences when the sequences are adjacent in
+// memory).  post multiplies output k of sequence q by W_N^(q*k).
+__global__ __launch_bounds__(256) void fft_lds_kernel(const double2* __restrict__ in, double2* __restrict__ out,
+                                                      const double2* __restrict__ roots, uint32_t n_total,
+                                                      uint32_t log2l, uint32_t log2seqs, uint64_t in_seq,
+                                                      uint64_t in_elem, uint64_t out_seq, uint64_t out_elem,
+                                                      int post, int seq_fast_in, int seq_fast_out) {
+#pragma clang fp contract(off)
+  extern __shared__ double2 buf[];
+  const uint32_t L = 1u << log2l;
+  const uint32_t seqs = 1u << log2seqs;
+  const uint32_t total = L << log2seqs;
+  const uint64_t q0 = (uint64_t)blockIdx.x << log2seqs;
+  for (uint32_t e = threadIdx.x; e < total; e += blockDim.x) {
+    uint32_t s, i;
+    if (seq_fast_in) {
+      s = e & (seqs - 1);
+      i = e >> log2seqs;
+    } else {
+      s = e >> log2l;
+      i = e & (L - 1);
+    }
+    const double2 v = in[(q0 + s) * in_seq + (uint64_t)i * in_elem];
+    const uint32_t r = log2l == 0 ? 0u : (__brev(i) >> (32u - log2l));
+    buf[(s << log2l) + r] = v;
+  }
+  __syncthreads();
+  const uint32_t butterflies = total >> 1;
+  for (uint32_t lg = 1; lg <= log2l; ++lg) {
+    const uint32_t half = 1u << (lg - 1);
+    const uint32_t stride = n_total >> lg;  // N / span
+    for (uint32_t b = threadIdx.x; b < butterflies; b += blockDim.x) {
+      const uint32_t s = b >> (log2l - 1);
+      const uint32_t bb = b & ((L >> 1) - 1);
+      const uint32_t j = bb & (half - 1);
+      const uint32_t base = (bb >> (lg - 1)) << lg;
+      const uint32_t p = (s << log2l) + base + j;
+      const uint32_t q = p + half;
+      const double2 t = cmul(roots[(size_t)j * stride], buf[q]);
+      const double2 a = buf[p];
+      buf[p] = make_double2(a.x + t.x, a.y + t.y);
+      buf[q] = make_double2(a.x - t.x, a.y - t.y);
+    }
+    __syncthreads();
+  }
+  const uint32_t half_n = n_total >> 1;
+  for (uint32_t e = threadIdx.x; e < total; e += blockDim.x) {
+    uint32_t s, k;
+    if (seq_fast_out) {
+      s = e & (seqs - 1);
+      k = e >> log2seqs;
+    } else {
+      s = e >> log2l;
+      k = e & (L - 1);
+    }
+    double2 v = buf[(s << log2l) + k];
+    if (post) {
+      const uint64_t p = (q0 + s) * (uint64_t)k;  // < N
+      double2 w;
+      if (p < half_n) {
+        w = roots[p];
+      } else {
+        const double2 r = roots[p - half_n];
+        w = make_double2(-r.x, -r.y);
+      }
+      v = cmul(w, v);
+    }
+    out[(q0 + s) * out_seq + (uint64_t)k * out_elem] = v;
+  }
+}
+
+uint32_t ilog2(uint32_t v) {
+  uint32_t r = 0;
+  while ((1u << r) < v) ++r;
+  return r;
+}
+
+// Sequences per workgroup: enough to fill the chip with >= 512 workgroups when
+// possible, within the LDS budget.
+uint32_t pick_log2seqs(uint32_t log2l, uint32_t log2count) {
+  uint32_t best = 0;
+  while (best < log2count && ((1u << (best + 1)) << log2l) <= kFftMaxLds &&
+         (log2count - (best + 1)) >= 9u)
+    ++best;
+  return best;
+}
+
+hipError_t launch_pass(const double2* in, double2* out, const double2* roots, uint32_t n, uint32_t log2l,
+                       uint32_t log2count, uint64_t in_seq, uint64_t in_elem, uint64_t out_seq, uint64_t out_elem,
+                       int post, int fast_in, int fast_out, hipStream_t stream) {
+  const uint32_t log2seqs = pick_log2seqs(log2l, log2count);
+  const uint32_t blocks = 1u << (log2count - log2seqs);
+  const size_t lds = ((size_t)1 << (log2l + log2seqs)) * sizeof(double2);
+  hipLaunchKernelGGL(fft_lds_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l, log2seqs,
+                     in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Twiddles for length n (reactor_concept_fft.cpp:50-57 computes the same
+// table on the host and caches it per length).  Caller holds ctx().mu.
+const double2* fft64_roots(uint32_t n) {
+  DeviceContext& c = ctx();
+  if (c.fft_roots_n == n && c.fft_roots != nullptr) return static_cast<const double2*>(c.fft_roots);
+  const uint32_t count = n / 2 > 0 ? n / 2 : 1;
+  std::vector<double> host(2 * (size_t)count, 0.0);
+  host[0] = 1.0;
+  const double pi = 3.14159265358979323846;
+  for (uint32_t j = 0; j < n / 2; ++j) {
+    const double angle = -2.0 * pi / (double)n * (double)j;
+    host[2 * j] = cos(angle);
+    host[2 * j + 1] = sin(angle);
+  }
+  void* dev = staging(7, host.size() * sizeof(double));
+  if (dev == nullptr) return nullptr;
+  if (hipMemcpyAsync(dev, host.data(), host.size() * sizeof(double), hipMemcpyHostToDevice, c.stream) != hipSuccess ||
+      hipStreamSynchronize(c.stream) != hipSuccess) {
+    (void)hipGetLastError();
+    c.fft_roots_n = 0;
+    return nullptr;
+  }
+  c.fft_roots = dev;
+  c.fft_roots_n = n;
+  return static_cast<const double2*>(dev);
+}
+
+hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,
+                        hipStream_t stream) {
+  const uint32_t log2n = ilog2(n);
+  if ((1u << log2n) != n || log2n > kFftMaxLog2) return hipErrorInvalidValue;
+  if (n <= kFftMaxLds) return launch_pass(in, out, roots, n, log2n, 0, 0, 1, 0, 1, 0, 0, 0, stream);
+  const uint32_t log2n1 = (log2n + 1) / 2, log2n2 = log2n - log2n1;
+  const uint64_t n1 = 1ull << log2n1, n2 = 1ull << log2n2;
+  // pass 1: N2 columns of length N1 (stride N2), twiddled, to T[k1*N2 + n2]
+  hipError_t e = launch_pass(in, temp, roots, n, log2n1, log2n2, 1, n2, 1, n2, 1, 1, 1, stream);
+  if (e != hipSuccess) return e;
+  // pass 2: N1 rows of length N2 (contiguous), to X[k1 + N1*k2]
+  return launch_pass(temp, out, roots, n, log2n2, log2n1, n2, 1, 1, n1, 0, 0, 1, stream);
+}
+
+}  // namespace prom
+
+using namespace prom;
+
+namespace {
+
+bool fft64_request_valid(const void* input, const void* output, uint32_t count) {
+  return input != nullptr && output != nullptr && count != 0u && (count & (count - 1u)) == 0u &&
+         count <= (1u << kFftMaxLog2);
+}
+
+}  // namespace
+
+extern "C" {
+
+PROM_REACTOR_API int prometheus_reactor_runtime_fft64(void* handle, const double* input, double* output,
+                                                      uint32_t count, uint32_t* stage, int* detail) {
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    set_status(stage, detail, PROM_STAGE_INIT, PROM_INVALID_HANDLE);
+    return PROM_INVALID_HANDLE;
+  }
+  if (!fft64_request_valid(input, output, count)) {
+    set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_INVALID_REQUEST);
+    return PROM_ERROR;
+  }
+  set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_VULKAN_UNAVAILABLE);
+  if (!rt->available) return PROM_ERROR;
+  rt->requests++;
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  const size_t bytes = (size_t)count * 2 * sizeof(double);
+  const double2* roots = fft64_roots(count);
+  double2* din = static_cast<double2*>(staging(0, bytes));
+  double2* dout = static_cast<double2*>(staging(1, bytes));
+  double2* dtmp = count > kFftMaxLds ? static_cast<double2*>(staging(3, bytes)) : nullptr;
+  if (roots == nullptr || din == nullptr || dout == nullptr || (count > kFftMaxLds && dtmp == nullptr)) {
+    set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_ALLOCATION_FAILED);
+    return PROM_ERROR;
+  }
+  if (hipMemcpyAsync(din, input, bytes, hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+    (void)hipGetLastError();
+    set_status(stage, detail, PROM_STAGE_TRANSFER_IN, PROM_FFT_DETAIL_UPLOAD_FAILED);
+    return PROM_ERROR;
+  }
+  if (launch_fft64(din, dout, dtmp, roots, count, cx.stream) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipStreamSynchronize(cx.stream);
+    set_status(stage, detail, PROM_STAGE_SUBMIT, PROM_FFT_DETAIL_DISPATCH_FAILED);
+    return PROM_ERROR;
+  }
+  if (hipMemcpyAsync(output, dout, bytes, hipMemcpyDeviceToHost, cx.stream) != hipSuccess ||
+      hipStreamSynchronize(cx.stream) != hipSuccess) {
+    (void)hipGetLastError();
+    set_status(stage, detail, PROM_STAGE_TRANSFER_OUT, PROM_FFT_DETAIL_READBACK_FAILED);
+    return PROM_ERROR;
+  }
+  rt->successes++;
+  set_status(stage, detail, PROM_STAGE_TRANSFER_OUT, 0);
+  return PROM_OK;
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_fft64_device(void* handle, const double* input, double* output,
+                                                             uint32_t count, uint32_t* stage, int* detail) {
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    set_status(stage, detail, PROM_STAGE_INIT, PROM_INVALID_HANDLE);
+    return PROM_INVALID_HANDLE;
+  }
+  if (!fft64_request_valid(input, output, count)) {
+    set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_INVALID_REQUEST);
+    return PROM_ERROR;
+  }
+  set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_VULKAN_UNAVAILABLE);
+  if (!rt->available) return PROM_ERROR;
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  const double2* roots = fft64_roots(count);
+  double2* dtmp = count > kFftMaxLds ? static_cast<double2*>(staging(3, (size_t)count * sizeof(double2))) : nullptr;
+  if (roots == nullptr || (count > kFftMaxLds && dtmp == nullptr)) {
+    set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_ALLOCATION_FAILED);
+    return PROM_ERROR;
+  }
+  if (launch_fft64(reinterpret_cast<const double2*>(input), reinterpret_cast<double2*>(output), dtmp, roots, count,
+                   cx.stream) != hipSuccess) {
+    (void)hipGetLastError();
+    set_status(stage, detail, PROM_STAGE_SUBMIT, PROM_FFT_DETAIL_DISPATCH_FAILED);
+    return PROM_ERROR;
+  }
+  set_status(stage, detail, PROM_STAGE_SUBMIT, 0);
+  return PROM_OK;
+}
+
+}  // extern "C"

@@ -18,7 +18,9 @@ namespace prom {
 
 constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
-constexpr uint32_t kStagingSlots = 8;  // 0-3 operand staging, 4 block workspace, 5 block host staging
+// Staging slots: 0-3 operand staging, 4 block workspace, 5 block host staging,
+// 6 split-K partials, 7 FFT twiddle table.
+constexpr uint32_t kStagingSlots = 8;
 
 struct AsyncState;  // async task table, submission slots and batch arenas (sgemm_async.hip)
 
@@ -44,6 +46,8 @@ struct DeviceContext {
   hipEvent_t op_begin = nullptr, op_end = nullptr;
   void* staging[kStagingSlots] = {};
   size_t staging_bytes[kStagingSlots] = {};
+  void* fft_roots = nullptr;  // twiddle table in staging slot 7 for length fft_roots_n
+  uint32_t fft_roots_n = 0;
   hipDeviceProp_t props{};
 };
 
@@ -81,6 +85,12 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
                                hipStream_t stream, int* path_detail);
 hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
                             hipStream_t stream, int* path_detail);
+// Binary64 FFT of n = 2^k <= 2^20 points (interleaved complex); temp holds n
+// points and is used when n > 4096.  roots comes from fft64_roots(n).
+hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,
+                        hipStream_t stream);
+// Device twiddle table for length n (cached; caller holds ctx().mu).
+const double2* fft64_roots(uint32_t n);
 hipError_t launch_row_reduction(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,
                                 hipStream_t stream);
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, float* inv_rms, uint32_t tokens,

@@ -72,6 +72,9 @@ BATCH_FLAG_TEST_FAIL_ENTRY_SHIFT = 24
 BATCH_PARTITION_ROUND_ROBIN, BATCH_PARTITION_CONTIGUOUS = 1, 2
 BATCH_STATE_FAILED, BATCH_STATE_SUCCEEDED = 5, 6
 BATCH_EXECUTION_SINGLE_WORKER = 1
+# FFT (reactor_api.h:361-379)
+DETAIL_FFT_INVALID_REQUEST = -6702
+DETAIL_FFT_VULKAN_UNAVAILABLE = -6712
 
 
 # ---- ABI structs -----------------------------------------------------------
@@ -552,6 +555,10 @@ _SIGNATURES = {
         c_int, [c_void_p, POINTER(PrometheusSgemmBatchEntry), c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_sgemm_batch_diagnostics": (
         c_int, [c_void_p, POINTER(PrometheusSgemmBatchDiagnostics)]),
+    "prometheus_reactor_runtime_fft64": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_fft64_device": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
 }
 
 MANDATORY_SYMBOLS = (
@@ -967,6 +974,23 @@ class NativeRuntime:
               else self.lib.prometheus_reactor_runtime_sgemm_batch)
         rc = fn(self.handle, entries, count, flags, byref(stage), byref(detail))
         return rc, CallStatus(stage.value, detail.value)
+
+    # -- binary64 FFT (fft.go:33-40, reactor_concept_fft.cpp:97-104) ----------
+    def fft64(self, values, output: Optional[np.ndarray] = None):
+        """Forward unnormalised FFT of complex128 values; returns (rc, status, spectrum)."""
+        x = np.ascontiguousarray(values, dtype=np.complex128)
+        out = np.empty_like(x) if output is None else output
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_fft64(self.handle, _ptr(x) if x.size else None,
+                                                       _ptr(out) if out.size else None, x.size,
+                                                       byref(stage), byref(detail))
+        return rc, CallStatus(stage.value, detail.value), out
+
+    def fft64_device(self, din: int, dout: int, count: int) -> int:
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_fft64_device(self.handle, c_void_p(din), c_void_p(dout), count,
+                                                              byref(stage), byref(detail))
+        return self._check(rc, stage, detail, "fft64_device")
 
     def batch_diagnostics(self) -> PrometheusSgemmBatchDiagnostics:
         d = PrometheusSgemmBatchDiagnostics()

@@ -73,6 +73,10 @@ def lib() -> ctypes.CDLL:
             "oct_reduction_cpu_reference": (c_int32, [P, P, c_uint32, c_uint32, c_uint32]),
             "oct_reduction_compare": (c_int32, [c_uint32, c_uint32, c_uint32, P, P, POINTER(OctReductionMismatch)]),
             "oct_rmsnorm_cpu_reference": (c_int32, [P, P, P, P, c_uint32, c_uint32, c_uint32, c_float]),
+            "oct_fft64_roots": (None, [P, c_uint32]),
+            "oct_fft64_with_roots": (None, [P, P, P, c_uint32]),
+            "oct_fft64": (c_int32, [P, P, P, c_uint32]),
+            "oct_fft64_agrees": (c_int32, [P, P, c_uint32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -227,3 +231,31 @@ def rmsnorm_reference(z: np.ndarray, w: np.ndarray, eps: float, width=None):
     inv = np.zeros(tokens, dtype=np.float32)
     rc = lib().oct_rmsnorm_cpu_reference(_p(z), _p(w), _p(y), _p(inv), tokens, width, stride, eps)
     return rc, y, inv
+
+
+# ---- FFT (internal/fft/fft.go) --------------------------------------------------
+def fft64_roots(n: int) -> np.ndarray:
+    """fft.go:218-226: the n/2 twiddles cos(a) + i sin(a), a = -2*pi/n * j."""
+    tw = np.zeros(max(1, n // 2), dtype=np.complex128)
+    lib().oct_fft64_roots(_p(tw), n)
+    return tw[: n // 2]
+
+
+def fft64(x) -> np.ndarray:
+    """fft.go:206-258 restated in C: forward, unnormalised, binary64."""
+    x = np.ascontiguousarray(x, dtype=np.complex128)
+    n = x.size
+    out = np.zeros(n, dtype=np.complex128)
+    scratch = np.zeros(max(1, n), dtype=np.float64)
+    if lib().oct_fft64(_p(x), _p(out), _p(scratch), n) != 0:
+        raise ValueError("FFT requires a non-empty power-of-two length")
+    return out
+
+
+def fft64_agrees(reference, actual) -> bool:
+    """fft.go:176-192: |actual - reference| <= 1e-12 * max|reference| per component."""
+    r = np.ascontiguousarray(reference, dtype=np.complex128)
+    a = np.ascontiguousarray(actual, dtype=np.complex128)
+    if r.size != a.size:
+        return False
+    return bool(lib().oct_fft64_agrees(_p(r), _p(a), r.size))

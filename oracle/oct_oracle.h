@@ -107,6 +107,17 @@ int32_t oct_rmsnorm_cpu_reference(const float* z, const float* weight, float* y,
                                   uint32_t tokens, uint32_t width, uint32_t z_row_stride,
                                   float epsilon);
 
+/* internal/fft/fft.go:218-226 (roots): n/2 interleaved (cos, sin) pairs. */
+void oct_fft64_roots(double* twiddles, uint32_t n);
+/* internal/fft/fft.go:228-258 (cpuWithRoots): interleaved complex binary64,
+   forward, unnormalised; input and output may not overlap. */
+void oct_fft64_with_roots(const double* input, double* output, const double* twiddles, uint32_t n);
+/* roots + transform; scratch_twiddles holds n doubles.  Returns 1 on an
+   invalid request (NULL, zero or non-power-of-two n). */
+int32_t oct_fft64(const double* input, double* output, double* scratch_twiddles, uint32_t n);
+/* internal/fft/fft.go:176-192 (agrees). */
+int32_t oct_fft64_agrees(const double* reference, const double* actual, uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

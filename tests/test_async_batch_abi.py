@@ -83,3 +83,24 @@ def test_batch_handle_validation(rt):
     assert rt.lib.prometheus_reactor_runtime_sgemm_batch_diagnostics(None, None) == p.PROM_ERROR
     diag = p.PrometheusSgemmBatchDiagnostics()
     assert rt.lib.prometheus_reactor_runtime_sgemm_batch_diagnostics(None, ctypes.byref(diag)) == p.PROM_INVALID_HANDLE
+
+
+# ------------------------------------------------------------------ FFT64
+def test_fft64_validation_without_device(rt):
+    # reactor_concept_fft.cpp:97-104, then :36-46 (no device -> INIT / VULKAN_UNAVAILABLE)
+    for n in (0, 3, 12, (1 << 20) + 1):
+        rc, cs, _ = rt.fft64(np.zeros(n, np.complex128))
+        assert (rc, cs.stage, cs.detail) == (p.PROM_ERROR, p.STAGE_INIT, p.DETAIL_FFT_INVALID_REQUEST)
+    big = np.zeros(1 << 21, np.complex128)
+    rc, cs, _ = rt.fft64(big)
+    assert (rc, cs.detail) == (p.PROM_ERROR, p.DETAIL_FFT_INVALID_REQUEST)
+    rc, cs, _ = rt.fft64(np.zeros(4, np.complex128))
+    assert (rc, cs.stage, cs.detail) == (p.PROM_ERROR, p.STAGE_INIT, p.DETAIL_FFT_VULKAN_UNAVAILABLE)
+    st, d = ctypes.c_uint32(), ctypes.c_int()
+    x = np.zeros(4, np.complex128)
+    assert rt.lib.prometheus_reactor_runtime_fft64(None, x.ctypes.data, x.ctypes.data, 4, ctypes.byref(st),
+                                                   ctypes.byref(d)) == p.PROM_INVALID_HANDLE
+    assert (st.value, d.value) == (p.STAGE_INIT, p.PROM_INVALID_HANDLE)
+    assert rt.lib.prometheus_reactor_runtime_fft64(rt.handle, None, x.ctypes.data, 4, ctypes.byref(st),
+                                                   ctypes.byref(d)) == p.PROM_ERROR
+    assert d.value == p.DETAIL_FFT_INVALID_REQUEST
