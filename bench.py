@@ -130,9 +130,19 @@ def cpu_baseline_secondary(seconds: float):
     blocks.decoder_layer_f32(xx, wl, Hq, hd)
     out["gemma2b_layer_f64_t512_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
     out["gemma2b_layer_cores"] = _blas_threads()
+    xf = oracle.normal(31, (2 << 20,)).astype(np.float64).view(np.complex128)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.fft64(xf)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min(2.0, seconds / 4) or reps >= 20:
+            break
+    out["fft64_2p20_us"] = round(dt / reps * 1e6, 1)
     out["kind"] = "port"
     out["sample"] = ("reductions: one full [8192,4096] pass per repetition (C oracle, fp32 data, binary64 sums); "
-                     "layer: one full T=512 Gemma-2B-shaped layer in binary64 numpy")
+                     "layer: one full T=512 Gemma-2B-shaped layer in binary64 numpy; "
+                     "fft64: internal/fft/fft.go's radix-2 restated in C, one thread, 2^20 points (twiddles included)")
     return out
 
 
@@ -217,6 +227,17 @@ def main() -> int:
     line["parity_rows_normwise_max"] = float(max(errs))
     for d in (da, db, dc):
         rt.free(d)
+    if not args.no_secondary:
+        # the reference's synchronous host-pointer contract: copies in and out over PCIe included
+        for _ in range(2):
+            rt.sgemm(n, n, n, a, b)
+        t0 = time.perf_counter()
+        for _ in range(3):
+            rt.sgemm(n, n, n, a, b)
+        e2e = (time.perf_counter() - t0) / 3
+        line["host_pointer_e2e"] = {"ms": round(e2e * 1e3, 3), "tflops": round(flops / e2e / 1e12, 2),
+                                    "note": "prometheus_reactor_runtime_sgemm with host A, B, C (H2D 128 MiB, "
+                                            "D2H 64 MiB included); not the headline value"}
 
     if not args.no_secondary:
         sec = {}
@@ -313,6 +334,17 @@ def main() -> int:
         sec["dit_block_bf16_t4224_ms"] = round(ev, 4)
         sec["dit_block_bf16_t4224_tflops"] = round(1.769e12 / (ev * 1e-3) / 1e12, 2)
         for d in dptr.values():
+            rt.free(d)
+        # binary64 FFT, 2^20 points (device entry: two four-step passes)
+        nf = 1 << 20
+        xf = (oracle.normal(31, (2 * nf,)).astype(np.float64)).view(np.complex128)
+        dfi, dfo = rt.upload_new(xf.view(np.float64)), rt.alloc(xf.nbytes)
+        _, ev = _timed_launches(rt, lambda: rt.fft64_device(dfi, dfo, nf), 100, 10)
+        sec["fft64_2p20_us"] = round(ev * 1e3, 2)
+        gbs = 2 * xf.nbytes / (ev * 1e-3) / 1e9
+        sec["fft64_2p20_gbs"] = round(gbs, 1)
+        sec["fft64_2p20_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+        for d in (dfi, dfo):
             rt.free(d)
         line["secondary"] = sec
 
