@@ -396,8 +396,11 @@ enum {
   PROM_M46_DETAIL_INVALID_REQUEST = -7401,
   PROM_M46_DETAIL_SHAPE = -7403,
   PROM_M46_DETAIL_STRIDE = -7404,
+  PROM_M46_DETAIL_STALE_WEIGHT_GENERATION = -7406,
   PROM_M46_DETAIL_EPSILON = -7407,
   PROM_M46_DETAIL_SIZE_OVERFLOW = -7409,
+  PROM_M46_DETAIL_RESOURCE = -7411,
+  PROM_M46_DETAIL_READBACK = -7416,
   PROM_M46_DETAIL_NONFINITE_INPUT = -7418,
 };
 #define PROM_M42_MAX_TOKENS 1024u
@@ -461,7 +464,14 @@ PROM_REACTOR_API int prometheus_reactor_runtime_reduction(void* handle, const Pr
 PROM_REACTOR_API int prometheus_reactor_runtime_row_wise_softmax(void* handle,
                                                                  const PrometheusRowWiseSoftmaxRequest* request,
                                                                  PrometheusRowWiseSoftmaxResult* out_result);
-/* reactor_api.h:2686-2689; reactor_api.c:250-359 */
+/* reactor_api.h:2686-2689; reactor_api.c:250-359.  Gemma-4-E2B M1 family
+   (this and the five entries below) follows the reference's call chain:
+   request validation (INIT / -7401) -> weight commit, which requires a
+   weight_generation strictly greater than the runtime's last committed one
+   (PrometheusRmsNorm.concept:199-213; stale -> TRANSFER_IN / -7406) -> shape,
+   epsilon and finiteness checks (-7401 / -7418) -> execution.  Success reports
+   stage 0 and detail 0, as reactor_concept_rmsnorm.cpp:110-146 leaves them.
+   RMSNorm: y = x * inv * w, inv = 1/sqrt(sum(x^2)/W + eps) (sum in binary64). */
 PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm(
     void* handle, const PrometheusGemma4E2BM1InputRmsNormRequest* request,
     PrometheusGemma4E2BM1InputRmsNormResult* out_result);
@@ -1018,6 +1028,193 @@ PROM_REACTOR_API int prometheus_reactor_runtime_fft64(void* handle, const double
    (success -> SUBMIT / 0; synchronise before reading output). */
 PROM_REACTOR_API int prometheus_reactor_runtime_fft64_device(void* handle, const double* input, double* output,
                                                              uint32_t count, uint32_t* stage, int* detail);
+
+/* ------------------------------------------------------------------------ */
+/* Gemma-4-E2B M1 positional and score entries (reactor_api.h:1826-1985)     */
+/* ------------------------------------------------------------------------ */
+
+typedef PrometheusGemma4E2BM1InputRmsNormRequest PrometheusGemma4E2BM1HeadRmsNormRequest;
+typedef PrometheusGemma4E2BM1InputRmsNormResult PrometheusGemma4E2BM1HeadRmsNormResult;
+
+/* reactor_api.h:1837-1852 */
+typedef struct PrometheusGemma4E2BM1RopeRequest {
+  uint32_t struct_size;
+  const float* source;
+  const float* cosine;
+  const float* sine;
+  float* output;
+  uint64_t source_element_count;
+  uint64_t cosine_element_count;
+  uint64_t sine_element_count;
+  uint64_t output_element_count;
+  uint32_t tokens;
+  uint32_t heads;
+  uint32_t head_width;
+  uint32_t reserved0;
+  uint64_t source_generation;
+  uint64_t table_generation;
+} PrometheusGemma4E2BM1RopeRequest;
+
+/* reactor_api.h:1854-1869 */
+typedef struct PrometheusGemma4E2BM1RopeResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint32_t output_written;
+  uint32_t dispatch_count;
+  uint64_t source_hash;
+  uint64_t cosine_hash;
+  uint64_t sine_hash;
+  uint64_t output_hash;
+  uint64_t buffer_allocation_count;
+  uint64_t buffer_reuse_count;
+  uint64_t descriptor_update_count;
+  uint64_t pipeline_create_count;
+  uint64_t command_buffer_reuse_count;
+} PrometheusGemma4E2BM1RopeResult;
+
+/* reactor_api.h:1875-1897 */
+typedef struct PrometheusGemma4E2BM1HeadRmsNormRopeRequest {
+  uint32_t struct_size;
+  const float* input;
+  const float* weight;
+  const float* cosine;
+  const float* sine;
+  float* output;
+  uint64_t input_element_count;
+  uint64_t weight_element_count;
+  uint64_t cosine_element_count;
+  uint64_t sine_element_count;
+  uint64_t output_element_count;
+  uint32_t tokens;
+  uint32_t heads;
+  uint32_t head_width;
+  uint32_t reserved0;
+  float epsilon;
+  uint64_t input_generation;
+  uint64_t weight_generation;
+  uint64_t table_generation;
+  uint64_t exact_source_hash;
+} PrometheusGemma4E2BM1HeadRmsNormRopeRequest;
+
+/* reactor_api.h:1899-1921 */
+typedef struct PrometheusGemma4E2BM1HeadRmsNormRopeResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint32_t output_written;
+  uint32_t dispatch_count;
+  uint32_t resident_source_bound;
+  uint32_t normalized_readback_count;
+  uint64_t source_byte_offset;
+  uint64_t source_byte_range;
+  uint64_t destination_byte_offset;
+  uint64_t destination_byte_range;
+  uint64_t input_hash;
+  uint64_t weight_hash;
+  uint64_t output_hash;
+  uint64_t buffer_allocation_count;
+  uint64_t buffer_reuse_count;
+  uint64_t descriptor_update_count;
+  uint64_t pipeline_create_count;
+  uint64_t command_buffer_reuse_count;
+  uint64_t observed_weight_generation;
+  uint64_t requested_weight_generation;
+} PrometheusGemma4E2BM1HeadRmsNormRopeResult;
+
+/* reactor_api.h:1926-1959 */
+typedef struct PrometheusGemma4E2BM1AttentionScoresRequest {
+  uint32_t struct_size;
+  const float* query_input;
+  const float* key_input;
+  const float* query_weight;
+  const float* key_weight;
+  const float* cosine;
+  const float* sine;
+  float* scores;
+  uint64_t query_input_element_count;
+  uint64_t key_input_element_count;
+  uint64_t query_weight_element_count;
+  uint64_t key_weight_element_count;
+  uint64_t cosine_element_count;
+  uint64_t sine_element_count;
+  uint64_t score_element_count;
+  uint32_t tokens;
+  uint32_t query_heads;
+  uint32_t key_heads;
+  uint32_t head_width;
+  float epsilon;
+  float scale;
+  uint32_t preparation_order; /* 0: query then key; 1: key then query */
+  uint64_t query_input_generation;
+  uint64_t key_input_generation;
+  uint64_t query_weight_generation;
+  uint64_t key_weight_generation;
+  uint64_t table_generation;
+  uint64_t query_exact_source_hash;
+  uint64_t key_exact_source_hash;
+} PrometheusGemma4E2BM1AttentionScoresRequest;
+
+/* reactor_api.h:1961-1985 */
+typedef struct PrometheusGemma4E2BM1AttentionScoresResult {
+  uint32_t struct_size;
+  uint32_t stage;
+  int32_t detail_code;
+  uint32_t score_written;
+  uint32_t positional_dispatch_count;
+  uint32_t score_dispatch_count;
+  uint32_t score_readback_count;
+  uint32_t host_detour_count;
+  uint32_t query_slot_id;
+  uint32_t query_slot_generation;
+  uint32_t key_slot_id;
+  uint32_t key_slot_generation;
+  uint32_t score_slot_id;
+  uint32_t score_slot_generation;
+  uint64_t query_byte_range;
+  uint64_t key_byte_range;
+  uint64_t score_byte_range;
+  uint64_t score_hash;
+  uint64_t buffer_allocation_count;
+  uint64_t buffer_reuse_count;
+  uint64_t descriptor_update_count;
+  uint64_t pipeline_create_count;
+  uint64_t observed_weight_generation;
+  uint64_t requested_weight_generation;
+} PrometheusGemma4E2BM1AttentionScoresResult;
+
+/* reactor_api.h:2690-2695; reactor_api.c:362-368 -- the input RMSNorm with the
+   output rounded to BF16 (round to nearest even) and re-expanded: the storage
+   boundary of the Q/K/V projection inputs. */
+PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_projection_activation_rmsnorm(
+    void* handle, const PrometheusGemma4E2BM1InputRmsNormRequest* request,
+    PrometheusGemma4E2BM1InputRmsNormResult* out_result);
+/* reactor_api.h:2696-2699; reactor_api.c:370-395 -- per-head RMSNorm of
+   [token, head] rows of 256 channels (tokens field = rows <= 120, stride 256,
+   epsilon exactly 1e-6), input and output BF16-rounded. */
+PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_head_rmsnorm(
+    void* handle, const PrometheusGemma4E2BM1HeadRmsNormRequest* request,
+    PrometheusGemma4E2BM1HeadRmsNormResult* out_result);
+/* reactor_api.h:2700-2703; reactor_concept_rmsnorm.cpp:157-189 and
+   gemma4e2b/rope_half_split.sdslv -- half-split RoPE of [15, heads (1 or 8),
+   256] with [15, 256] cosine/sine tables: each product, then the
+   difference (first half) or sum (second half), rounded to BF16. */
+PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_rope(void* handle,
+                                                                  const PrometheusGemma4E2BM1RopeRequest* request,
+                                                                  PrometheusGemma4E2BM1RopeResult* out_result);
+/* reactor_api.h:2704-2707; reactor_api.c:404-505 -- head RMSNorm (BF16 in and
+   out) followed by the RoPE above in one submission; output may be NULL with
+   output_element_count 0. */
+PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_head_rmsnorm_rope(
+    void* handle, const PrometheusGemma4E2BM1HeadRmsNormRopeRequest* request,
+    PrometheusGemma4E2BM1HeadRmsNormRopeResult* out_result);
+/* reactor_api.h:2708-2711; reactor_api.c:507-587 and
+   gemma4e2b/attention_scores.sdslv -- both positional preparations (query
+   weight and key weight committed in preparation_order), then raw pre-mask
+   scores[h][i][j] = (sum_c Q[i,h,c] * K[j,0,c]) * 0.0625 in fp32 (1800 scores). */
+PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_attention_scores(
+    void* handle, const PrometheusGemma4E2BM1AttentionScoresRequest* request,
+    PrometheusGemma4E2BM1AttentionScoresResult* out_result);
 
 #ifdef __cplusplus
 }

@@ -672,61 +672,6 @@ PROM_REACTOR_API int prometheus_reactor_runtime_row_wise_softmax(void* handle,
   return PROM_OK;
 }
 
-// reactor_api.c:250-359 (validation order and codes), executed by the fused kernel.
-PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm(
-    void* handle, const PrometheusGemma4E2BM1InputRmsNormRequest* request,
-    PrometheusGemma4E2BM1InputRmsNormResult* out_result) {
-  if (out_result == nullptr) return PROM_ERROR;
-  memset(out_result, 0, sizeof(*out_result));
-  out_result->struct_size = sizeof(*out_result);
-  const uint64_t t0 = wall_ns();
-  Runtime* rt = lookup(handle);
-  if (rt == nullptr) {
-    out_result->stage = PROM_STAGE_INIT;
-    out_result->detail_code = PROM_M46_DETAIL_INVALID_REQUEST;
-    return PROM_INVALID_HANDLE;
-  }
-  const PrometheusGemma4E2BM1InputRmsNormRequest* r = request;
-  if (r == nullptr || r->struct_size < sizeof(*r) || r->input == nullptr || r->weight == nullptr ||
-      r->output == nullptr || r->inv_rms_output == nullptr || r->tokens == 0u || r->model_width == 0u ||
-      r->input_row_stride < r->model_width || r->input_generation == 0u || r->weight_generation == 0u ||
-      r->exact_source_hash == 0u) {
-    out_result->stage = PROM_STAGE_INIT;
-    out_result->detail_code = PROM_M46_DETAIL_INVALID_REQUEST;
-    return PROM_ERROR;
-  }
-  if (r->tokens > PROM_M42_MAX_TOKENS || r->model_width > PROM_M42_MAX_MODEL_WIDTH ||
-      r->weight_element_count != r->model_width ||
-      r->input_element_count < (uint64_t)(r->tokens - 1u) * r->input_row_stride + r->model_width ||
-      r->output_element_count < (uint64_t)r->tokens * r->model_width ||
-      r->inv_rms_output_element_count < r->tokens) {
-    out_result->stage = PROM_STAGE_INIT;
-    out_result->detail_code = PROM_M46_DETAIL_SHAPE;
-    return PROM_ERROR;
-  }
-  if (!isfinite(r->epsilon) || r->epsilon <= 0.0f) {
-    out_result->stage = PROM_STAGE_INIT;
-    out_result->detail_code = PROM_M46_DETAIL_EPSILON;
-    return PROM_ERROR;
-  }
-  RmsArgs a{r->input, r->weight, r->output, r->inv_rms_output, r->tokens, r->model_width, r->input_row_stride,
-            r->epsilon};
-  uint32_t stage = PROM_STAGE_NONE;
-  int32_t detail = 0;
-  uint64_t gpu_ns = 0;
-  const int status = rmsnorm_host(rt, a, &stage, &detail, &gpu_ns);
-  out_result->stage = stage;
-  out_result->detail_code = detail;
-  out_result->end_to_end_ns = wall_ns() - t0;
-  if (status != PROM_OK) return status;
-  out_result->output_written = 1u;
-  out_result->matched_input = 1u;
-  out_result->submit_count = 1u;
-  out_result->final_readback_count = 1u;
-  out_result->apply_gpu_ns = gpu_ns;
-  return PROM_OK;
-}
-
 PROM_REACTOR_API int prometheus_reactor_runtime_rmsnorm(void* handle, const PrometheusRmsNormRequest* request,
                                                         PrometheusRmsNormResult* out_result) {
   if (out_result == nullptr) return PROM_ERROR;

@@ -34,6 +34,10 @@ struct Runtime {
   uint64_t successes;
   uint32_t batch_ring_depth;  // 1..4 (config batch_ring_depth; 0 selects 2)
   AsyncState* async;          // created on first async or batch call
+  // Gemma-4-E2B M1 committed RMSNorm weight (generation 0: none committed yet).
+  uint64_t m1_weight_generation;
+  uint64_t m1_weight_hash;
+  uint32_t m1_weight_width;
 };
 
 struct DeviceContext {

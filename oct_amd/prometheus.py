@@ -75,6 +75,11 @@ BATCH_EXECUTION_SINGLE_WORKER = 1
 # FFT (reactor_api.h:361-379)
 DETAIL_FFT_INVALID_REQUEST = -6702
 DETAIL_FFT_VULKAN_UNAVAILABLE = -6712
+# Gemma-4-E2B M1 (reactor_vulkan.h:1869-1888)
+DETAIL_M46_INVALID_REQUEST = -7401
+DETAIL_M46_STALE_WEIGHT_GENERATION = -7406
+DETAIL_M46_RESOURCE = -7411
+DETAIL_M46_NONFINITE_INPUT = -7418
 
 
 # ---- ABI structs -----------------------------------------------------------
@@ -454,6 +459,71 @@ class PrometheusSgemmAsyncDiagnostics(Structure):
                 ("runtime_unsafe_to_reuse", c_uint32), ("tasks", PrometheusSgemmAsyncTaskDiagnostics * 4)]
 
 
+def _fields(spec: str):
+    """'u32 a, u64 b, f32 c, p d, i32 e' -> ctypes field list."""
+    kinds = {"u32": c_uint32, "u64": c_uint64, "f32": c_float, "p": c_void_p, "i32": ctypes.c_int32}
+    out = []
+    for item in spec.split(","):
+        kind, name = item.split()
+        out.append((name, kinds[kind]))
+    return out
+
+
+class PrometheusGemma4E2BM1RopeRequest(Structure):
+    """reactor_api.h:1837-1852"""
+    _fields_ = _fields("u32 struct_size, p source, p cosine, p sine, p output, u64 source_element_count, "
+                       "u64 cosine_element_count, u64 sine_element_count, u64 output_element_count, u32 tokens, "
+                       "u32 heads, u32 head_width, u32 reserved0, u64 source_generation, u64 table_generation")
+
+
+class PrometheusGemma4E2BM1RopeResult(Structure):
+    _fields_ = _fields("u32 struct_size, u32 stage, i32 detail_code, u32 output_written, u32 dispatch_count, "
+                       "u64 source_hash, u64 cosine_hash, u64 sine_hash, u64 output_hash, "
+                       "u64 buffer_allocation_count, u64 buffer_reuse_count, u64 descriptor_update_count, "
+                       "u64 pipeline_create_count, u64 command_buffer_reuse_count")
+
+
+class PrometheusGemma4E2BM1HeadRmsNormRopeRequest(Structure):
+    """reactor_api.h:1875-1897"""
+    _fields_ = _fields("u32 struct_size, p input, p weight, p cosine, p sine, p output, u64 input_element_count, "
+                       "u64 weight_element_count, u64 cosine_element_count, u64 sine_element_count, "
+                       "u64 output_element_count, u32 tokens, u32 heads, u32 head_width, u32 reserved0, "
+                       "f32 epsilon, u64 input_generation, u64 weight_generation, u64 table_generation, "
+                       "u64 exact_source_hash")
+
+
+class PrometheusGemma4E2BM1HeadRmsNormRopeResult(Structure):
+    _fields_ = _fields("u32 struct_size, u32 stage, i32 detail_code, u32 output_written, u32 dispatch_count, "
+                       "u32 resident_source_bound, u32 normalized_readback_count, u64 source_byte_offset, "
+                       "u64 source_byte_range, u64 destination_byte_offset, u64 destination_byte_range, "
+                       "u64 input_hash, u64 weight_hash, u64 output_hash, u64 buffer_allocation_count, "
+                       "u64 buffer_reuse_count, u64 descriptor_update_count, u64 pipeline_create_count, "
+                       "u64 command_buffer_reuse_count, u64 observed_weight_generation, "
+                       "u64 requested_weight_generation")
+
+
+class PrometheusGemma4E2BM1AttentionScoresRequest(Structure):
+    """reactor_api.h:1926-1959"""
+    _fields_ = _fields("u32 struct_size, p query_input, p key_input, p query_weight, p key_weight, p cosine, "
+                       "p sine, p scores, u64 query_input_element_count, u64 key_input_element_count, "
+                       "u64 query_weight_element_count, u64 key_weight_element_count, u64 cosine_element_count, "
+                       "u64 sine_element_count, u64 score_element_count, u32 tokens, u32 query_heads, "
+                       "u32 key_heads, u32 head_width, f32 epsilon, f32 scale, u32 preparation_order, "
+                       "u64 query_input_generation, u64 key_input_generation, u64 query_weight_generation, "
+                       "u64 key_weight_generation, u64 table_generation, u64 query_exact_source_hash, "
+                       "u64 key_exact_source_hash")
+
+
+class PrometheusGemma4E2BM1AttentionScoresResult(Structure):
+    _fields_ = _fields("u32 struct_size, u32 stage, i32 detail_code, u32 score_written, "
+                       "u32 positional_dispatch_count, u32 score_dispatch_count, u32 score_readback_count, "
+                       "u32 host_detour_count, u32 query_slot_id, u32 query_slot_generation, u32 key_slot_id, "
+                       "u32 key_slot_generation, u32 score_slot_id, u32 score_slot_generation, "
+                       "u64 query_byte_range, u64 key_byte_range, u64 score_byte_range, u64 score_hash, "
+                       "u64 buffer_allocation_count, u64 buffer_reuse_count, u64 descriptor_update_count, "
+                       "u64 pipeline_create_count, u64 observed_weight_generation, u64 requested_weight_generation")
+
+
 # ---- errors and status (status.go, bridge.go) ------------------------------
 class ReactorIssue(RuntimeError):
     """Structured reactor failure (reference ``ReactorIssue``, bridge.go:33-66)."""
@@ -559,6 +629,20 @@ _SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_fft64_device": (
         c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_gemma4e2b_m1_projection_activation_rmsnorm": (
+        c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1InputRmsNormRequest),
+                POINTER(PrometheusGemma4E2BM1InputRmsNormResult)]),
+    "prometheus_reactor_runtime_gemma4e2b_m1_head_rmsnorm": (
+        c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1InputRmsNormRequest),
+                POINTER(PrometheusGemma4E2BM1InputRmsNormResult)]),
+    "prometheus_reactor_runtime_gemma4e2b_m1_rope": (
+        c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1RopeRequest), POINTER(PrometheusGemma4E2BM1RopeResult)]),
+    "prometheus_reactor_runtime_gemma4e2b_m1_head_rmsnorm_rope": (
+        c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1HeadRmsNormRopeRequest),
+                POINTER(PrometheusGemma4E2BM1HeadRmsNormRopeResult)]),
+    "prometheus_reactor_runtime_gemma4e2b_m1_attention_scores": (
+        c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1AttentionScoresRequest),
+                POINTER(PrometheusGemma4E2BM1AttentionScoresResult)]),
 }
 
 MANDATORY_SYMBOLS = (

@@ -77,6 +77,10 @@ def lib() -> ctypes.CDLL:
             "oct_fft64_with_roots": (None, [P, P, P, c_uint32]),
             "oct_fft64": (c_int32, [P, P, P, c_uint32]),
             "oct_fft64_agrees": (c_int32, [P, P, c_uint32]),
+            "oct_m1_rmsnorm": (None, [P, c_uint32, P, P, P, c_uint32, c_uint32, c_float, c_int32, c_int32]),
+            "oct_m1_head_rmsnorm_go": (None, [P, P, P, c_uint32, c_uint32, c_float]),
+            "oct_m1_rope": (None, [P, P, P, P, c_uint32, c_uint32, c_uint32]),
+            "oct_m1_raw_scores": (None, [P, P, P, c_uint32, c_uint32, c_uint32, c_float]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -259,3 +263,48 @@ def fft64_agrees(reference, actual) -> bool:
     if r.size != a.size:
         return False
     return bool(lib().oct_fft64_agrees(_p(r), _p(a), r.size))
+
+
+# ---- Gemma-4-E2B M1 stages (oct_oracle_m1.c) -----------------------------------------
+def m1_rmsnorm(x, w, eps: float = 1e-6, round_in: bool = False, round_out: bool = False, width=None):
+    """Double-sum RMSNorm of rows of x (row pitch = x.shape[1]); returns (y, inv_rms)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, stride = x.shape
+    width = width or w.size
+    y = np.zeros((rows, width), np.float32)
+    inv = np.zeros(rows, np.float32)
+    lib().oct_m1_rmsnorm(_p(x), stride, _p(w), _p(y), _p(inv), rows, width, eps, int(round_in), int(round_out))
+    return y, inv
+
+
+def m1_head_rmsnorm_go(x, w, eps: float = 1e-6):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, width = x.shape
+    y = np.zeros_like(x)
+    lib().oct_m1_head_rmsnorm_go(_p(x), _p(w), _p(y), rows, width, eps)
+    return y
+
+
+def m1_rope(source, cosine, sine, tokens: int = 15, heads: int = 8, width: int = 256):
+    s = np.ascontiguousarray(source, dtype=np.float32).reshape(-1)
+    c = np.ascontiguousarray(cosine, dtype=np.float32).reshape(-1)
+    n = np.ascontiguousarray(sine, dtype=np.float32).reshape(-1)
+    out = np.zeros_like(s)
+    lib().oct_m1_rope(_p(s), _p(c), _p(n), _p(out), tokens, heads, width)
+    return out
+
+
+def m1_raw_scores(query, key, tokens: int = 15, query_heads: int = 8, width: int = 256, scale: float = 0.0625):
+    q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
+    k = np.ascontiguousarray(key, dtype=np.float32).reshape(-1)
+    out = np.zeros(query_heads * tokens * tokens, np.float32)
+    lib().oct_m1_raw_scores(_p(q), _p(k), _p(out), tokens, query_heads, width, scale)
+    return out
+
+
+def m1_positional(x, w, cosine, sine, heads: int):
+    """Head RMSNorm (BF16 in and out) then RoPE: the head_rmsnorm_rope chain."""
+    y, _ = m1_rmsnorm(np.asarray(x, np.float32).reshape(15 * heads, 256), w, 1e-6, True, True)
+    return m1_rope(y, cosine, sine, 15, heads, 256)

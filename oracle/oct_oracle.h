@@ -118,6 +118,16 @@ int32_t oct_fft64(const double* input, double* output, double* scratch_twiddles,
 /* internal/fft/fft.go:176-192 (agrees). */
 int32_t oct_fft64_agrees(const double* reference, const double* actual, uint32_t n);
 
+/* Gemma-4-E2B M1 stages (oct_oracle_m1.c). */
+void oct_m1_rmsnorm(const float* input, uint32_t stride, const float* weight, float* output, float* inv_rms,
+                    uint32_t rows, uint32_t width, float epsilon, int32_t round_in, int32_t round_out);
+void oct_m1_head_rmsnorm_go(const float* input, const float* weight, float* output, uint32_t rows, uint32_t width,
+                            float epsilon);
+void oct_m1_rope(const float* source, const float* cosine, const float* sine, float* output, uint32_t tokens,
+                 uint32_t heads, uint32_t width);
+void oct_m1_raw_scores(const float* query, const float* key, float* scores, uint32_t tokens, uint32_t query_heads,
+                       uint32_t width, float scale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,6 +69,12 @@ STRUCTS = {
     "PrometheusSgemmBatchDiagnostics": p.PrometheusSgemmBatchDiagnostics,
     "PrometheusSgemmAsyncTaskDiagnostics": p.PrometheusSgemmAsyncTaskDiagnostics,
     "PrometheusSgemmAsyncDiagnostics": p.PrometheusSgemmAsyncDiagnostics,
+    "PrometheusGemma4E2BM1RopeRequest": p.PrometheusGemma4E2BM1RopeRequest,
+    "PrometheusGemma4E2BM1RopeResult": p.PrometheusGemma4E2BM1RopeResult,
+    "PrometheusGemma4E2BM1HeadRmsNormRopeRequest": p.PrometheusGemma4E2BM1HeadRmsNormRopeRequest,
+    "PrometheusGemma4E2BM1HeadRmsNormRopeResult": p.PrometheusGemma4E2BM1HeadRmsNormRopeResult,
+    "PrometheusGemma4E2BM1AttentionScoresRequest": p.PrometheusGemma4E2BM1AttentionScoresRequest,
+    "PrometheusGemma4E2BM1AttentionScoresResult": p.PrometheusGemma4E2BM1AttentionScoresResult,
 }
 
 # Structs whose layout the reference header fixes (a drop-in caller compiled
@@ -79,6 +85,9 @@ REFERENCE_STRUCTS = (
     "PrometheusRowWiseSoftmaxRequest", "PrometheusRowWiseSoftmaxResult", "PrometheusGemma4E2BM1InputRmsNormRequest",
     "PrometheusGemma4E2BM1InputRmsNormResult", "PrometheusAsyncStatus", "PrometheusSgemmBatchEntry",
     "PrometheusSgemmBatchDiagnostics", "PrometheusSgemmAsyncTaskDiagnostics", "PrometheusSgemmAsyncDiagnostics",
+    "PrometheusGemma4E2BM1RopeRequest", "PrometheusGemma4E2BM1RopeResult", "PrometheusGemma4E2BM1HeadRmsNormRopeRequest",
+    "PrometheusGemma4E2BM1HeadRmsNormRopeResult", "PrometheusGemma4E2BM1AttentionScoresRequest",
+    "PrometheusGemma4E2BM1AttentionScoresResult",
 )
 REFERENCE_HEADER = Path("/root/reference/internal/prometheus/native/reactor_api.h")
 
@@ -141,6 +150,11 @@ def test_reference_struct_sizes_unchanged():
     assert ctypes.sizeof(p.PrometheusAsyncStatus) == 28
     assert ctypes.sizeof(p.PrometheusSgemmAsyncTaskDiagnostics) == 88
     assert ctypes.sizeof(p.PrometheusSgemmAsyncDiagnostics) == 488
+    # reactor_api.h:1837-1985
+    assert ctypes.sizeof(p.PrometheusGemma4E2BM1RopeRequest) == 104
+    assert ctypes.sizeof(p.PrometheusGemma4E2BM1HeadRmsNormRopeRequest) == 144
+    assert ctypes.sizeof(p.PrometheusGemma4E2BM1AttentionScoresRequest) == 208
+    assert ctypes.sizeof(p.PrometheusGemma4E2BM1AttentionScoresResult) == 136
 
 
 @pytest.fixture
@@ -319,6 +333,8 @@ def test_row_wise_softmax_validation(lib):
 
 
 def test_gemma_rmsnorm_validation(lib):
+    # reactor_api.c:250-275 then reactor_concept_rmsnorm.cpp:85-95: malformed requests and a
+    # runtime without a device both end at INIT / -7401 with PROM_ERROR
     with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
         x = np.ones((2, 8), np.float32)
         w = np.ones(8, np.float32)
@@ -327,20 +343,102 @@ def test_gemma_rmsnorm_validation(lib):
         req = p.PrometheusGemma4E2BM1InputRmsNormRequest()
         req.struct_size = ctypes.sizeof(req)
         res = p.PrometheusGemma4E2BM1InputRmsNormResult()
-        call = lambda: lib.prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm(rt.handle, ctypes.byref(req),
-                                                                                   ctypes.byref(res))
-        assert call() == 1 and res.detail_code == -7401
-        req.input, req.weight, req.output, req.inv_rms_output = (x.ctypes.data, w.ctypes.data, y.ctypes.data,
-                                                                 inv.ctypes.data)
-        req.input_element_count, req.weight_element_count, req.output_element_count = 16, 8, 16
-        req.inv_rms_output_element_count = 2
-        req.tokens, req.model_width, req.input_row_stride, req.epsilon = 2, 8, 8, 1e-6
-        req.input_generation = req.weight_generation = req.exact_source_hash = 1
-        assert call() == 1 and res.stage == p.STAGE_INIT and res.detail_code == p.DETAIL_HIP_UNAVAILABLE
-        req.epsilon = 0.0
-        assert call() == 1 and res.detail_code == -7407
-        req.epsilon, req.tokens = 1e-6, 1025
-        assert call() == 1 and res.detail_code == -7403
+        for fn in (lib.prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm,
+                   lib.prometheus_reactor_runtime_gemma4e2b_m1_projection_activation_rmsnorm):
+            call = lambda: fn(rt.handle, ctypes.byref(req), ctypes.byref(res))
+            assert call() == 1 and (res.stage, res.detail_code) == (p.STAGE_INIT, -7401)
+            req.input, req.weight, req.output, req.inv_rms_output = (x.ctypes.data, w.ctypes.data, y.ctypes.data,
+                                                                     inv.ctypes.data)
+            req.input_element_count, req.weight_element_count, req.output_element_count = 16, 8, 16
+            req.inv_rms_output_element_count = 2
+            req.tokens, req.model_width, req.input_row_stride, req.epsilon = 2, 8, 8, 1e-6
+            req.input_generation = req.weight_generation = req.exact_source_hash = 1
+            assert call() == 1 and (res.stage, res.detail_code) == (p.STAGE_INIT, -7401)
+            assert res.weight_hash != 0  # the weight was hashed before the device check
+            w[3] = np.nan
+            assert call() == 1 and (res.stage, res.detail_code) == (p.STAGE_INIT, p.DETAIL_M46_NONFINITE_INPUT)
+            w[3] = 1.0
+            req.input_generation = 0
+            assert call() == 1 and res.detail_code == -7401
+            req.input_generation = 1
+        # an invalid handle is reported through the weight step: PROM_ERROR, INIT / -7401
+        assert lib.prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm(None, ctypes.byref(req), ctypes.byref(res)) == 1
+        assert (res.stage, res.detail_code) == (p.STAGE_INIT, -7401)
+
+
+def _head_request(x, w, y, inv, rows):
+    r = p.PrometheusGemma4E2BM1InputRmsNormRequest()
+    r.struct_size = ctypes.sizeof(r)
+    r.input, r.weight, r.output, r.inv_rms_output = x.ctypes.data, w.ctypes.data, y.ctypes.data, inv.ctypes.data
+    r.input_element_count = r.output_element_count = rows * 256
+    r.weight_element_count, r.inv_rms_output_element_count = 256, rows
+    r.tokens, r.model_width, r.input_row_stride, r.epsilon = rows, 256, 256, 1e-6
+    r.input_generation = r.weight_generation = r.exact_source_hash = 1
+    return r
+
+
+def test_gemma_head_rmsnorm_shape_lock(lib):
+    # reactor_api.c:373-392: rows <= 120, width and stride 256, exact counts, epsilon exactly 1e-6
+    with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        x, w = np.ones((121, 256), np.float32), np.ones(256, np.float32)
+        y, inv = np.zeros_like(x), np.zeros(121, np.float32)
+        res = p.PrometheusGemma4E2BM1InputRmsNormResult()
+        fn = lib.prometheus_reactor_runtime_gemma4e2b_m1_head_rmsnorm
+        for mutate in (lambda r: setattr(r, "tokens", 121), lambda r: setattr(r, "epsilon", 1e-5),
+                       lambda r: setattr(r, "input_row_stride", 257), lambda r: setattr(r, "model_width", 128),
+                       lambda r: setattr(r, "output_element_count", 120 * 256 + 1)):
+            req = _head_request(x, w, y, inv, 120)
+            mutate(req)
+            assert fn(rt.handle, ctypes.byref(req), ctypes.byref(res)) == 1
+            assert (res.stage, res.detail_code) == (p.STAGE_INIT, -7401)
+
+
+def test_gemma_rope_and_scores_validation(lib):
+    with p.NativeRuntime(lib=lib, test_flags=p.TESTCFG_SKIP_VULKAN_INIT) as rt:
+        src, out = np.ones(15 * 8 * 256, np.float32), np.zeros(15 * 8 * 256, np.float32)
+        cos, sin = np.ones(3840, np.float32), np.zeros(3840, np.float32)
+        r = p.PrometheusGemma4E2BM1RopeRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.source, r.cosine, r.sine, r.output = src.ctypes.data, cos.ctypes.data, sin.ctypes.data, out.ctypes.data
+        r.source_element_count = r.output_element_count = src.size
+        r.cosine_element_count = r.sine_element_count = 3840
+        r.tokens, r.heads, r.head_width = 15, 8, 256
+        r.source_generation = r.table_generation = 1
+        res = p.PrometheusGemma4E2BM1RopeResult()
+        rope = lambda h: lib.prometheus_reactor_runtime_gemma4e2b_m1_rope(h, ctypes.byref(r), ctypes.byref(res))
+        # reactor_concept_rmsnorm.cpp:157-172: handle first, then the request
+        assert rope(None) == p.PROM_INVALID_HANDLE
+        # no device: the request is valid, inputs hashed, then RESOURCE at INIT
+        assert rope(rt.handle) == 1 and (res.stage, res.detail_code) == (p.STAGE_INIT, p.DETAIL_M46_RESOURCE)
+        assert res.source_hash != 0 and res.cosine_hash != res.sine_hash
+        r.output = src.ctypes.data  # in place is refused
+        assert rope(rt.handle) == 1 and res.detail_code == -7401
+        r.output, r.heads = out.ctypes.data, 2
+        assert rope(rt.handle) == 1 and res.detail_code == -7401
+        r.heads = 8
+        src[5] = np.inf
+        assert rope(rt.handle) == 1 and res.detail_code == p.DETAIL_M46_NONFINITE_INPUT
+        # attention scores: the closed 15 x 8 x 1 x 256 geometry and scale 0.0625
+        a = p.PrometheusGemma4E2BM1AttentionScoresRequest()
+        a.struct_size = ctypes.sizeof(a)
+        scores = np.full(1800, -99, np.float32)
+        a.query_input = a.key_input = a.query_weight = a.key_weight = src.ctypes.data
+        a.cosine, a.sine, a.scores = cos.ctypes.data, sin.ctypes.data, scores.ctypes.data
+        a.query_input_element_count, a.key_input_element_count = 15 * 8 * 256, 15 * 256
+        a.query_weight_element_count = a.key_weight_element_count = 256
+        a.cosine_element_count = a.sine_element_count = 3840
+        a.score_element_count = 1800
+        a.tokens, a.query_heads, a.key_heads, a.head_width, a.epsilon, a.scale = 15, 8, 1, 256, 1e-6, 0.125
+        for f in ("query_input_generation", "key_input_generation", "query_weight_generation",
+                  "key_weight_generation", "table_generation", "query_exact_source_hash", "key_exact_source_hash"):
+            setattr(a, f, 1)
+        ares = p.PrometheusGemma4E2BM1AttentionScoresResult()
+        call = lambda: lib.prometheus_reactor_runtime_gemma4e2b_m1_attention_scores(rt.handle, ctypes.byref(a),
+                                                                                    ctypes.byref(ares))
+        assert call() == 1 and (ares.stage, ares.detail_code) == (p.STAGE_INIT, -7401)
+        a.scale, a.preparation_order = 0.0625, 2
+        assert call() == 1 and ares.detail_code == -7401
+        assert np.all(scores == -99)
 
 
 def test_strict_path_raises_without_device(monkeypatch):

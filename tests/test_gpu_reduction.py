@@ -199,6 +199,7 @@ def test_gemma_input_rmsnorm_entry(gpu_runtime):
     res = p.PrometheusGemma4E2BM1InputRmsNormResult()
     rc = gpu_runtime.lib.prometheus_reactor_runtime_gemma4e2b_m1_input_rmsnorm(gpu_runtime.handle, ctypes.byref(req),
                                                                                ctypes.byref(res))
-    assert rc == 0 and res.output_written == 1 and res.stage == p.STAGE_TRANSFER_OUT
+    # success leaves stage 0 (reactor_concept_rmsnorm.cpp:110-146 never sets it)
+    assert rc == 0 and res.output_written == 1 and res.stage == 0 and res.detail_code == 0
     rc2, y_ref, inv_ref = oracle.rmsnorm_reference(z, wt, 1e-6)
     assert oracle.normwise_rel_err(y, y_ref) <= NORMWISE
