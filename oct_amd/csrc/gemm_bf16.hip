@@ -228,6 +228,7 @@ __device__ __forceinline__ void map_tile2(int tiles_m, int tiles_n, int* tm, int
   *tn = in_group / group_m;
 }
 
+template <bool kBuf, int kStoreAt>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16_t* __restrict__ A,
                                                                    const uint16_t* __restrict__ B, float* C, int M,
                                                                    int N, int K, int tiles_m, int tiles_n, int lda,
@@ -247,6 +248,13 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16
   const int wn = wave & 3;   // 0..3
 
   u32x4 ra[4], rb[4];
+  // Branch-free path (kBuf): buffer loads return zero past the end of A or B, which
+  // covers rows >= M and k >= K (K is a multiple of the K tile there); columns >= N
+  // read the next row of B but only feed output columns that are never stored.
+  const __amdgpu_buffer_rsrc_t rsa =
+      __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, kBuf ? (int)((size_t)M * lda * 2) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, kBuf ? (int)((size_t)K * ldb * 2) : 0, 0x00020000);
   auto load_tile = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -254,9 +262,13 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16
       const int r = c >> 3;
       const int kc = (c & 7) * 8;
       const int gr = row0 + r, gk = k0 + kc;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (gr < M && gk < K) v = *reinterpret_cast<const u32x4*>(A + (size_t)gr * lda + gk);
-      ra[u] = v;
+      if constexpr (kBuf) {
+        ra[u] = __builtin_amdgcn_raw_buffer_load_b128(rsa, (uint32_t)((gr * lda + gk) * 2), 0, 0);
+      } else {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (gr < M && gk < K) v = *reinterpret_cast<const u32x4*>(A + (size_t)gr * lda + gk);
+        ra[u] = v;
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -264,9 +276,13 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16
       const int kr = c >> 5;
       const int nc = (c & 31) * 8;
       const int gk = k0 + kr, gn = col0 + nc;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (gk < K && gn < N) v = *reinterpret_cast<const u32x4*>(B + (size_t)gk * ldb + gn);
-      rb[u] = v;
+      if constexpr (kBuf) {
+        rb[u] = __builtin_amdgcn_raw_buffer_load_b128(rsb, (uint32_t)((gk * ldb + gn) * 2), 0, 0);
+      } else {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (gk < K && gn < N) v = *reinterpret_cast<const u32x4*>(B + (size_t)gk * ldb + gn);
+        rb[u] = v;
+      }
     }
   };
   auto store_tile = [&](int buf) {
@@ -326,8 +342,10 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16
         for (int ni = 0; ni < 2; ++ni)
           acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
       }
+      // The other buffer was last read before the previous barrier, so the next
+      // tile may be written into it at any point of this iteration.
+      if (s == kStoreAt && more) store_tile(cur ^ 1);
     }
-    if (more) store_tile(cur ^ 1);
     __syncthreads();
   }
 
@@ -365,8 +383,14 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
   const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
   const int tiles_n2 = (int)((n + kBN2 - 1) / kBN2);
   if (vec && tiles_m2 * tiles_n2 >= 128) {
-    hipLaunchKernelGGL(gemm_bf16_mfma_256_kernel, dim3((unsigned)(tiles_m2 * tiles_n2)), dim3(512), 0, stream, a, b, c,
-                       (int)m, (int)n, (int)k, tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
+    const dim3 grid2((unsigned)(tiles_m2 * tiles_n2));
+    const bool buf = (k % kBK2 == 0) && (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * ldb * 2 < (1ull << 31);
+    if (buf)
+      hipLaunchKernelGGL((gemm_bf16_mfma_256_kernel<true, 1>), grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n,
+                         (int)k, tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
+    else
+      hipLaunchKernelGGL((gemm_bf16_mfma_256_kernel<false, 1>), grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n,
+                         (int)k, tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
     if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_BF16;
     return hipGetLastError();
   }

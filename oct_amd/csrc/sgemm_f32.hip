@@ -55,7 +55,7 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int*
 // Strides are leading dimensions in elements.  R (may be null) is added in the
 // epilogue: C = A @ B + R; R may alias C (each element is read, then written,
 // by the same lane).
-template <bool kVec>
+template <bool kVec, bool kBuf>
 __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __restrict__ A,
                                                                 const float* __restrict__ B, float* C, int M,
                                                                 int N, int K, int tiles_m, int tiles_n, int lda,
@@ -93,11 +93,40 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 
   float ra[8];
   float rb[16];
+  // Branch-free loads (kBuf: K of this slice is a multiple of the K tile): buffer
+  // loads return zero for rows of A at or past M and past the end of B; columns of
+  // B at or past N only feed output columns that are never stored.
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)A, (short)0, kBuf ? (int)(((size_t)M * lda - (gridDim.y > 1 ? (size_t)blockIdx.y * k_len : 0)) * 4) : 0,
+      0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, kBuf ? (int)((size_t)K * ldb * 4) : 0, 0x00020000);
 
   auto load_tile = [&](int k0) {
     const int gr = row0 + a_row;
     const int gn = col0 + b_n;
-    if constexpr (kVec) {
+    if constexpr (kBuf) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int gk = k0 + a_k + 4 * h;
+        const floatx4 v =
+            __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (uint32_t)((gr * lda + gk) * 4), 0, 0));
+        ra[4 * h + 0] = v.x;
+        ra[4 * h + 1] = v.y;
+        ra[4 * h + 2] = v.z;
+        ra[4 * h + 3] = v.w;
+      }
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int gk = k0 + b_k + 4 * h;
+        const floatx4 v =
+            __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (uint32_t)((gk * ldb + gn) * 4), 0, 0));
+        rb[4 * h + 0] = v.x;
+        rb[4 * h + 1] = v.y;
+        rb[4 * h + 2] = v.z;
+        rb[4 * h + 3] = v.w;
+      }
+    } else if constexpr (kVec) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int gk = k0 + a_k + 4 * h;
@@ -302,12 +331,19 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
   float* out = splits > 1 ? partial : c;
   const int ldo = splits > 1 ? (int)n : ldc;
   const float* res = splits > 1 ? nullptr : residual;
-  if (vec)
-    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<true>, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
+  // Buffer-load path: every slice length a multiple of the K tile and every
+  // 32-bit byte offset (rows up to M + kBM, all of B plus a tile row) in range.
+  const bool buf = vec && (k % kBK == 0) && (k_len % kBK == 0) &&
+                   (size_t)(m + kBM) * lda * 4 < (1ull << 31) && ((size_t)k * ldb + n + kBN) * 4 < (1ull << 31);
+  if (buf)
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, true>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
+  else if (vec)
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, false>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
   else
-    hipLaunchKernelGGL(sgemm_f32_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
-                       tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<false, false>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
   if (splits > 1) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
