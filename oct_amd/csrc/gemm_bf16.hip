@@ -372,6 +372,158 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16
   }
 }
 
+// Direct-to-LDS variant of the 8-wave large tile.  Tiles travel HBM -> LDS
+// with buffer_load_dwordx4 ... lds (no staging registers, no ds_write), so
+// tile kt+1 streams into the other stage during all of tile kt's MFMAs.  Each
+// wave instruction fills 1 KiB of LDS, lane i at +16*i, which fixes an
+// unpadded layout; the global address each lane fetches applies an XOR
+// swizzle on 16-byte chunks so that the MFMA operand reads are bank-conflict
+// free: A (256 x 64, 128-byte rows) chunk c of row R sits at c ^ ((R&7) ^ ((R>>3)&1)),
+// B (64 x 256, 512-byte rows) chunk c of row k at c ^ {0,4,10,14}[k&3].
+// The two stages are separate LDS arrays and the K loop is unrolled by two so
+// that reads of one stage are visibly independent of the DMA into the other.
+__device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_b(int k) { return (0xEA40 >> (4 * (k & 3))) & 15; }  // {0,4,10,14}
+
+__global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_t* __restrict__ A,
+                                                                  const uint16_t* __restrict__ B, float* C, int M,
+                                                                  int N, int K, int tiles_m, int tiles_n, int lda,
+                                                                  int ldb, int ldc, const float* R, int ldr,
+                                                                  uint16_t* Cb) {
+  __shared__ __attribute__((aligned(1024))) uint16_t S0[2 * kBM2 * kBK2];
+  __shared__ __attribute__((aligned(1024))) uint16_t S1[2 * kBM2 * kBK2];
+
+  int tm, tn;
+  map_tile2(tiles_m, tiles_n, &tm, &tn);
+  const int row0 = tm * kBM2;
+  const int col0 = tn * kBN2;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2;
+  const int wn = wave & 3;
+
+  const __amdgpu_buffer_rsrc_t rsa =
+      __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)((size_t)M * lda * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)((size_t)K * ldb * 2), 0x00020000);
+
+  // Per-lane source offsets (bytes) of this wave's 4 A and 4 B instructions at
+  // k0 = 0; the k offset of a tile travels in the scalar soffset.
+  uint32_t a_off[4], b_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = wave * 4 + i;
+    const int r = 8 * q + (lane >> 3);
+    const int c = (lane & 7) ^ swz_a(r);
+    a_off[i] = (uint32_t)(((row0 + r) * lda + 8 * c) * 2);
+    const int kr = 2 * q + (lane >> 5);
+    const int cb = (lane & 31) ^ swz_b(kr);
+    b_off[i] = (uint32_t)((kr * ldb + col0 + 8 * cb) * 2);
+  }
+  typedef __attribute__((address_space(3))) void lds_void;
+  auto issue = [&](uint16_t* stage, int k0) {
+    const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
+    const int sb = __builtin_amdgcn_readfirstlane(k0 * ldb * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = wave * 4 + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)((char*)stage + q * 1024), 16, a_off[i], sa, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_void*)((char*)stage + 32768 + q * 1024), 16, b_off[i], sb,
+                                               0, 0);
+    }
+  };
+
+  // Operand addresses.  A row R = wm*128 + mi*32 + lrow has swizzle swz_a(lrow)
+  // for every mi, and chunk 2s + hk = 2s ^ hk, so the byte address of step s is
+  // a_base ^ (32 s) plus the immediate mi*4096.  B rows 16s + tr_row (+4) share
+  // swizzle swz_b(tr_row); chunk (wn*8 + 4ni + x) ^ sw = ((wn*8 + x) ^ sw) ^ 4ni,
+  // so its address is b_base ^ (64 ni) plus the immediates 8192 s (+2048).
+  const int lrow = lane & 31;
+  const int hk = lane >> 5;
+  const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_e = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const uint32_t a_base = (uint32_t)((wm * 128 + lrow) * 128 + ((hk ^ swz_a(lrow)) << 4));
+  const uint32_t b_base =
+      (uint32_t)(32768 + tr_row * 512 + (((wn * 8 + (tr_e >> 3)) ^ swz_b(tr_row)) << 4) + (tr_e & 7) * 2);
+  struct Frags {
+    bf16x8 a[4], b[2];
+  };
+  auto read_frags = [&](const uint16_t* stage, int s) {
+    Frags f;
+    const char* st = (const char*)stage;
+    const uint32_t as = a_base ^ (uint32_t)(32 * s);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) f.a[mi] = *reinterpret_cast<const bf16x8*>(st + as + mi * 4096);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const uint32_t bs = (b_base ^ (uint32_t)(64 * ni)) + 8192 * s;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + bs));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + bs + 2048));
+      f.b[ni] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    return f;
+  };
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[i][0] = floatx16{};
+    acc[i][1] = floatx16{};
+  }
+  auto compute = [&](const uint16_t* stage) {
+#pragma unroll
+    for (int s = 0; s < kBK2 / 16; ++s) {
+      const Frags fc = read_frags(stage, s);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fc.a[mi], fc.b[ni], acc[mi][ni], 0, 0, 0);
+    }
+  };
+
+  const int k_tiles = K / kBK2;
+  issue(S0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    // stage kt&1 holds tile kt; the other stage was last read before the previous barrier
+    uint16_t* cur = (kt & 1) ? S1 : S0;
+    uint16_t* nxt = (kt & 1) ? S0 : S1;
+    if (kt + 1 < k_tiles) issue(nxt, (kt + 1) * kBK2);
+    compute(cur);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  const int lgrp = (lane >> 5) * 4;
+  auto store_block = [&](const floatx16& v16, int mi, int ni) {
+    const int col = col0 + wn * 64 + ni * 32 + lrow;
+    if (col >= N) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + wm * 128 + mi * 32 + 8 * (r >> 2) + lgrp + (r & 3);
+      if (row < M) {
+        float v = v16[r];
+        if (R != nullptr) v += R[(size_t)row * ldr + col];
+        if (Cb != nullptr)
+          Cb[(size_t)row * ldc + col] = f32_to_bf16_rne(v);
+        else
+          C[(size_t)row * ldc + col] = v;
+      }
+    }
+  };
+  store_block(acc[0][0], 0, 0);
+  store_block(acc[0][1], 0, 1);
+  store_block(acc[1][0], 1, 0);
+  store_block(acc[1][1], 1, 1);
+  store_block(acc[2][0], 2, 0);
+  store_block(acc[2][1], 2, 1);
+  store_block(acc[3][0], 3, 0);
+  store_block(acc[3][1], 3, 1);
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -386,8 +538,8 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
     const dim3 grid2((unsigned)(tiles_m2 * tiles_n2));
     const bool buf = (k % kBK2 == 0) && (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * ldb * 2 < (1ull << 31);
     if (buf)
-      hipLaunchKernelGGL((gemm_bf16_mfma_256_kernel<true, 1>), grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n,
-                         (int)k, tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
+      hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel, grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n, (int)k,
+                         tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
     else
       hipLaunchKernelGGL((gemm_bf16_mfma_256_kernel<false, 1>), grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n,
                          (int)k, tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
