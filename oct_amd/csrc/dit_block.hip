@@ -18,7 +18,8 @@
 //   qk_norm_rope   per (token, head): RMSNorm(q), RMSNorm(k), RoPE, V copy -> bf16
 //   resid_norm_mod r = x + gateA * RMSNorm(proj; n2)             -> fp32
 //                  f = RMSNorm(r; n3) * scaleM                   -> bf16
-//   swiglu         h = silu(g) * u                                -> bf16
+//   swiglu         h = silu(g) * u -> bf16, fused into the W1|W3 GEMM epilogue
+//                  (gemm_bf16.hip) when F % 128 == 0 and D % 64 == 0
 //   final_resid    out = r + gateM * RMSNorm(w2; n4)              -> fp32
 #include <math.h>
 #include <string.h>
@@ -384,12 +385,17 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   hipLaunchKernelGGL(resid_norm_mod_kernel, rows, blk, 0, st, r->input, proj, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
                      R, Fb, T, D, eps);
   PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_gemm_bf16_ex(Fb, D, r->w_13, 2 * F, G, nullptr, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
-  {
+  // FFN up-projection with SwiGLU fused into the GEMM epilogue when the shape
+  // allows (F a multiple of 128, D of 64); otherwise GEMM to fp32, then SwiGLU.
+  const hipError_t fused = launch_gemm_bf16_swiglu(Fb, D, r->w_13, Hb, F, T, F, D, st);
+  if (fused == hipErrorNotSupported) {
+    PROM_STEP(launch_gemm_bf16_ex(Fb, D, r->w_13, 2 * F, G, nullptr, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
     const size_t total = (size_t)T * (F / 4);
     hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)std::min((size_t)65536, (total + 255) / 256)), blk, 0, st, G, Hb,
                        T, F);
     PROM_STEP(hipGetLastError());
+  } else {
+    PROM_STEP(fused);
   }
   PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, W2, nullptr, D, T, D, F, nullptr, 0, st, nullptr));
   hipLaunchKernelGGL(final_resid_kernel, rows, blk, 0, st, R, W2, r->ffn_norm2, gateM, r->output, T, D, eps);

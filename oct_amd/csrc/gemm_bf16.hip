@@ -385,6 +385,13 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_256_kernel(const uint16
 __device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_b(int k) { return (0xEA40 >> (4 * (k & 3))) & 15; }  // {0,4,10,14}
 
+//
+// kSwiGLU: B is [K, 2F] = [W1 | W3] and the output is h = silu(x W1) * (x W3)
+// in bf16 [M, F].  A tile then covers 128 output columns: in each wave's 64
+// B columns the first 32 are gate (W1) columns and the last 32 the matching
+// up (W3) columns, so accumulator blocks ni = 0 and 1 hold g and u of the same
+// outputs and the product is formed in registers (N is F here).
+template <bool kSwiGLU>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_t* __restrict__ A,
                                                                   const uint16_t* __restrict__ B, float* C, int M,
                                                                   int N, int K, int tiles_m, int tiles_n, int lda,
@@ -396,7 +403,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_
   int tm, tn;
   map_tile2(tiles_m, tiles_n, &tm, &tn);
   const int row0 = tm * kBM2;
-  const int col0 = tn * kBN2;
+  const int col0 = kSwiGLU ? tn * (kBN2 / 2) : tn * kBN2;
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -419,7 +426,12 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_
     a_off[i] = (uint32_t)(((row0 + r) * lda + 8 * c) * 2);
     const int kr = 2 * q + (lane >> 5);
     const int cb = (lane & 31) ^ swz_b(kr);
-    b_off[i] = (uint32_t)((kr * ldb + col0 + 8 * cb) * 2);
+    int gcol = col0 + 8 * cb;
+    if constexpr (kSwiGLU) {
+      const int e = 8 * cb;  // tile column: wave block e / 64, gate half if e % 64 < 32
+      gcol = col0 + (e >> 6) * 32 + (e & 31) + ((e & 32) ? N : 0);
+    }
+    b_off[i] = (uint32_t)((kr * ldb + gcol) * 2);
   }
   typedef __attribute__((address_space(3))) void lds_void;
   auto issue = [&](uint16_t* stage, int k0) {
@@ -498,6 +510,23 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_
   }
 
   const int lgrp = (lane >> 5) * 4;
+  if constexpr (kSwiGLU) {
+    const int col = col0 + wn * 32 + lrow;
+    if (col < N) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row0 + wm * 128 + mi * 32 + 8 * (r >> 2) + lgrp + (r & 3);
+          if (row < M) {
+            const float g = acc[mi][0][r], u = acc[mi][1][r];
+            Cb[(size_t)row * ldc + col] = f32_to_bf16_rne(g / (1.0f + expf(-g)) * u);
+          }
+        }
+      }
+    }
+    return;
+  }
   auto store_block = [&](const floatx16& v16, int mi, int ni) {
     const int col = col0 + wn * 64 + ni * 32 + lrow;
     if (col >= N) return;
@@ -538,7 +567,7 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
     const dim3 grid2((unsigned)(tiles_m2 * tiles_n2));
     const bool buf = (k % kBK2 == 0) && (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * ldb * 2 < (1ull << 31);
     if (buf)
-      hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel, grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n, (int)k,
+      hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<false>, grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n, (int)k,
                          tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
     else
       hipLaunchKernelGGL((gemm_bf16_mfma_256_kernel<false, 1>), grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n,
@@ -556,6 +585,21 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
     hipLaunchKernelGGL(gemm_bf16_mfma_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n, (int)k,
                        tiles_m, tiles_n, lda, ldb, ldc, residual, ldr, cb);
   if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_BF16;
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w13, uint16_t* h, int ldh, uint32_t m,
+                                   uint32_t f, uint32_t k, hipStream_t stream) {
+  // Fused path conditions: whole 128-column output tiles, K a multiple of the K
+  // tile, 16-byte aligned rows, byte offsets below 2^31; otherwise the caller
+  // runs the GEMM and the elementwise SwiGLU separately.
+  const bool ok = f % 128 == 0 && k % kBK2 == 0 && lda % 8 == 0 && aligned16(a) && aligned16(w13) &&
+                  (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * 2 * f * 2 < (1ull << 31);
+  if (!ok) return hipErrorNotSupported;
+  const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
+  const int tiles_n2 = (int)(f / 128);
+  hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<true>, dim3((unsigned)(tiles_m2 * tiles_n2)), dim3(512), 0, stream, a,
+                     w13, nullptr, (int)m, (int)f, (int)k, tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, nullptr, 0, h);
   return hipGetLastError();
 }
 

@@ -89,6 +89,10 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
                                hipStream_t stream, int* path_detail);
 hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
                             hipStream_t stream, int* path_detail);
+// h[m, f] (bf16) = silu(a @ w13[:, :f]) * (a @ w13[:, f:]) in one GEMM; returns
+// hipErrorNotSupported, launching nothing, when the shape is outside the fused path.
+hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w13, uint16_t* h, int ldh, uint32_t m,
+                                   uint32_t f, uint32_t k, hipStream_t stream);
 // Binary64 FFT of n = 2^k <= 2^20 points (interleaved complex); temp holds n
 // points and is used when n > 4096.  roots comes from fft64_roots(n).
 hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,

@@ -67,8 +67,11 @@ def test_decoder_layer_rejects_gqa(gpu_runtime):
 BF16_BLOCK = 2e-2
 
 
+# F % 128 == 0 takes the W1|W3 GEMM with SwiGLU fused into its epilogue; F = 200
+# and F = 72 take the separate GEMM + SwiGLU kernel.
 @pytest.mark.parametrize("grid,text,heads,F,C", [((3, 5), 7, 2, 256, 32), ((8, 16), 40, 4, 1024, 64),
-                                                 ((10, 13), 0, 1, 384, 16)])
+                                                 ((10, 13), 0, 1, 384, 16), ((6, 7), 5, 2, 200, 32),
+                                                 ((4, 4), 3, 1, 72, 16)])
 def test_dit_block_small_shapes(gpu_runtime, grid, text, heads, F, C):
     T = grid[0] * grid[1] + text
     D = heads * 128
