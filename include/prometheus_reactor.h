@@ -1216,6 +1216,475 @@ PROM_REACTOR_API int prometheus_reactor_runtime_gemma4e2b_m1_attention_scores(
     void* handle, const PrometheusGemma4E2BM1AttentionScoresRequest* request,
     PrometheusGemma4E2BM1AttentionScoresResult* out_result);
 
+/* ------------------------------------------------------------------------ */
+/* Resident model blocks and the compiled Z-Image session                   */
+/* (reactor_api.h:25-45, 666-1249, 2713-2821)                               */
+/* ------------------------------------------------------------------------ */
+
+/* reactor_api.h:198-202: one-shot faults taken from the runtime config's
+   reduction_test_flags; the resident model block consumes them in phase order. */
+enum {
+  PROM_REDUCTION_TESTCFG_FAIL_COMMAND_RECORD = 1u << 0,
+  PROM_REDUCTION_TESTCFG_FAIL_QUEUE_SUBMIT = 1u << 1,
+  PROM_REDUCTION_TESTCFG_FAIL_COMPLETION_OBSERVATION = 1u << 2,
+};
+
+enum {
+  PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY = 1u,
+  PROM_MODEL_EXECUTION_PROFILE_PREFETCH = 2u,
+};
+enum {
+  PROM_MAIN_ATTENTION_ROUTE_AUTO = 1u,
+  PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL = 2u,
+  PROM_MAIN_ATTENTION_ROUTE_SUBGROUP_OWNED32 = 3u,
+};
+
+#define PROM_MODEL_BLOCK_MAX_WEIGHTS 13u
+#define PROM_MODEL_BLOCK_MAX_STEPS 7u
+#define PROM_MODEL_BLOCK_MAX_AUDIT_POINTS 1u
+#define PROM_MODEL_BLOCK_M1B_PIPELINE_COUNT 6u
+#define PROM_MODEL_BLOCK_MAIN_STAGE_COUNT 13u
+
+enum {
+  PROM_MODEL_BLOCK_STEP_BIND_PIPELINE = 1u,
+  PROM_MODEL_BLOCK_STEP_BIND_RESOURCES = 2u,
+  PROM_MODEL_BLOCK_STEP_PUSH_CONSTANTS = 3u,
+  PROM_MODEL_BLOCK_STEP_DISPATCH = 4u,
+  PROM_MODEL_BLOCK_STEP_BARRIER = 5u,
+  PROM_MODEL_BLOCK_STEP_AUDIT_COPY = 6u,
+  PROM_MODEL_BLOCK_STEP_OUTPUT_COPY = 7u,
+};
+
+enum {
+  PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST = -6901,
+  PROM_MODEL_BLOCK_DETAIL_NOT_FOUND = -6902,
+  PROM_MODEL_BLOCK_DETAIL_ALREADY_CREATED = -6903,
+  PROM_MODEL_BLOCK_DETAIL_WEIGHT_MISMATCH = -6904,
+  PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED = -6905,
+  PROM_MODEL_BLOCK_DETAIL_PIPELINE_CREATE_FAILED = -6906,
+  PROM_MODEL_BLOCK_DETAIL_UPLOAD_FAILED = -6907,
+  PROM_MODEL_BLOCK_DETAIL_COMMAND_RECORD_FAILED = -6908,
+  PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED = -6909,
+  PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN = -6910,
+  PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED = -6911,
+  PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT = -6912,
+  PROM_MODEL_BLOCK_DETAIL_INGRESS_PIPELINE_CREATE_FAILED = -6913,
+  PROM_MODEL_BLOCK_DETAIL_INGRESS_DISPATCH_FAILED = -6914,
+  PROM_MODEL_BLOCK_DETAIL_INGRESS_AUDIT_MISMATCH = -6915,
+  PROM_MODEL_BLOCK_DETAIL_INGRESS_INPUT_SIZE_MISMATCH = -6916,
+  PROM_MODEL_BLOCK_DETAIL_INGRESS_TIMESTEP_SIZE_MISMATCH = -6917,
+  PROM_MODEL_BLOCK_DETAIL_M1C_SOFTMAX_INVALID = -6918,
+  PROM_MODEL_BLOCK_DETAIL_M1D_NONFINITE = -6919,
+  PROM_MODEL_BLOCK_DETAIL_PARAMETER_SET_MISMATCH = -6920,
+  PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED = -6921,
+  PROM_MODEL_BLOCK_DETAIL_DESCRIPTOR_UPDATE_FAILED = -6922,
+  PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST = -6923,
+  PROM_MODEL_SESSION_DETAIL_STALE_STREAM = -6924,
+  PROM_MODEL_SESSION_DETAIL_STREAM_MISMATCH = -6925,
+  PROM_MODEL_SESSION_DETAIL_COMPLETION_UNCERTAIN = -6926,
+  PROM_MODEL_SESSION_DETAIL_MAIN_ATTENTION_ROUTE_REJECTED = -6927,
+};
+
+enum {
+  PROM_ZIMAGE_STREAM_PREPARED_IMAGE = 1u,
+  PROM_ZIMAGE_STREAM_PREPARED_CONTEXT = 2u,
+  PROM_ZIMAGE_STREAM_JOINT_WORKING = 3u,
+  PROM_ZIMAGE_STREAM_MAIN_IMAGE_OUTPUT = 4u,
+  PROM_ZIMAGE_STREAM_MAIN_CONTEXT_OUTPUT = 5u,
+  PROM_ZIMAGE_STREAM_SLOT_COUNT = 5u,
+};
+
+enum {
+  PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO = 1u,
+  PROM_NOISE_REFINER_PARAMETER_SET_0 = 1u,
+  PROM_NOISE_REFINER_PARAMETER_SET_1 = 2u,
+  PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO = 2u,
+  PROM_CONTEXT_REFINER_PARAMETER_SET_0 = 1u,
+  PROM_CONTEXT_REFINER_PARAMETER_SET_1 = 2u,
+  PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO = 3u,
+  PROM_MAIN_TRANSFORMER_PARAMETER_SET_0 = 1u,
+};
+
+enum {
+  PROM_NOISE_REFINER_BINDING_BOUND = 1u,
+  PROM_NOISE_REFINER_BINDING_VALIDATING = 2u,
+  PROM_NOISE_REFINER_BINDING_UPLOADING = 3u,
+  PROM_NOISE_REFINER_BINDING_UPDATING_DESCRIPTORS = 4u,
+  PROM_NOISE_REFINER_BINDING_READY_TO_COMMIT = 5u,
+  PROM_NOISE_REFINER_BINDING_COMMITTED = 6u,
+  PROM_NOISE_REFINER_BINDING_FAILED_BEFORE_COMMIT = 7u,
+  PROM_NOISE_REFINER_BINDING_COMPLETION_UNCERTAIN = 8u,
+  PROM_NOISE_REFINER_BINDING_QUARANTINED = 9u,
+};
+
+enum {
+  PROM_MODEL_WEIGHT_WINDOW_EMPTY = 0u,
+  PROM_MODEL_WEIGHT_WINDOW_HOST_PREPARED = 1u,
+  PROM_MODEL_WEIGHT_WINDOW_UPLOAD_SUBMITTED = 2u,
+  PROM_MODEL_WEIGHT_WINDOW_DEVICE_READY = 3u,
+  PROM_MODEL_WEIGHT_WINDOW_ACTIVE = 4u,
+  PROM_MODEL_WEIGHT_WINDOW_UNCERTAIN = 5u,
+  PROM_MODEL_WEIGHT_WINDOW_QUARANTINED = 6u,
+};
+
+enum {
+  PROM_NOISE_REFINER_AUDIT_NONE = 0u,
+  PROM_NOISE_REFINER_AUDIT_M1B = 1u,
+  PROM_NOISE_REFINER_AUDIT_M1C = 2u,
+  PROM_NOISE_REFINER_AUDIT_M1D = 3u,
+};
+
+/* The model lock of the Z-Image Turbo compiled model (the reference's
+   generated models/zimage-turbo/resolved_descriptor.h). */
+#define PROM_ZIMAGE_TURBO_LOCK_ID 0x71ef202b4e34b562ull
+#define PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES 47186176u
+
+typedef struct PrometheusModelBlockWeightDeclaration {
+  uint64_t content_identity;
+  uint64_t layout_identity;
+  uint64_t byte_count;
+} PrometheusModelBlockWeightDeclaration;
+
+typedef struct PrometheusModelBlockCreateRequest {
+  uint32_t struct_size;
+  uint32_t assembly_family;
+  uint32_t parameter_set;
+  uint64_t parameter_set_aggregate_identity;
+  uint64_t model_contract_identity;
+  uint64_t weight_identity;
+  uint64_t shader_portfolio_identity;
+  uint64_t precision_policy_identity;
+  uint64_t capability_route_identity;
+  uint64_t memory_ceiling_bytes;
+  uint64_t external_input_bytes;
+  uint64_t external_output_bytes;
+  uint64_t audit_bytes;
+  uint32_t shader_id;
+  uint32_t weight_count;
+  PrometheusModelBlockWeightDeclaration weights[PROM_MODEL_BLOCK_MAX_WEIGHTS];
+  uint32_t step_count;
+  uint32_t steps[PROM_MODEL_BLOCK_MAX_STEPS];
+} PrometheusModelBlockCreateRequest;
+
+typedef struct PrometheusModelBlockWeightUpload {
+  uint32_t binding_index;
+  const void* bytes;
+  uint64_t byte_count;
+  uint64_t content_identity;
+  uint64_t layout_identity;
+} PrometheusModelBlockWeightUpload;
+
+typedef struct PrometheusNoiseRefinerRebindRequest {
+  uint32_t struct_size;
+  uint32_t model_local_block_id;
+  uint64_t lock_identity;
+  uint32_t upload_count;
+  const PrometheusModelBlockWeightUpload* uploads;
+} PrometheusNoiseRefinerRebindRequest;
+
+typedef struct PrometheusContextRefinerCreateRequest {
+  uint32_t struct_size;
+  uint32_t model_local_block_id;
+  uint64_t lock_identity;
+  uint32_t upload_count;
+  const PrometheusModelBlockWeightUpload* uploads;
+} PrometheusContextRefinerCreateRequest;
+
+typedef PrometheusContextRefinerCreateRequest PrometheusContextRefinerRebindRequest;
+typedef PrometheusContextRefinerCreateRequest PrometheusMainTransformerCreateRequest;
+typedef PrometheusContextRefinerCreateRequest PrometheusMainTransformerRebindRequest;
+
+typedef struct PrometheusMainTransformerExecuteRequest {
+  uint32_t struct_size;
+  uint64_t session_identity;
+  uint64_t lock_identity;
+  uint32_t model_local_block_id;
+  uint32_t audit_enabled;
+  uint32_t resident_chain_mode;
+  uint32_t reserved0;
+  uint64_t required_image_generation;
+  uint64_t required_context_generation;
+  uint64_t required_joint_generation;
+  const void* timestep_bf16;
+  uint64_t timestep_bytes;
+  uint64_t timestep_identity;
+  uint64_t output_identity;
+} PrometheusMainTransformerExecuteRequest;
+
+typedef struct PrometheusModelBlockExecuteRequest {
+  uint32_t struct_size;
+  const float* input;
+  float* output;
+  uint64_t element_count;
+  uint64_t input_identity;
+  uint32_t audit_enabled;
+  float* audit_output;
+  uint64_t audit_element_capacity;
+} PrometheusModelBlockExecuteRequest;
+
+typedef struct PrometheusNoiseRefiner0ExecuteRequest {
+  uint32_t struct_size;
+  const void* model_input_bf16;
+  const void* timestep_bf16;
+  uint64_t model_input_bytes;
+  uint64_t timestep_bytes;
+  uint64_t input_identity;
+  uint64_t timestep_identity;
+  uint64_t output_identity;
+  uint32_t audit_enabled;
+} PrometheusNoiseRefiner0ExecuteRequest;
+
+typedef PrometheusNoiseRefiner0ExecuteRequest PrometheusNoiseRefiner1ExecuteRequest;
+
+typedef struct PrometheusNoiseRefinerResidentExecuteRequest {
+  uint32_t struct_size;
+  uint64_t input_generation;
+  uint64_t output_identity;
+  uint32_t audit_enabled;
+  uint32_t audit_family;
+  uint32_t audit_stage;
+  float* audit_output;
+  uint64_t audit_element_capacity;
+} PrometheusNoiseRefinerResidentExecuteRequest;
+
+typedef struct PrometheusContextRefiner0ExecuteRequest {
+  uint32_t struct_size;
+  const float* context_input;
+  uint64_t context_input_bytes;
+  uint64_t input_identity;
+  uint64_t output_identity;
+  uint32_t audit_enabled;
+} PrometheusContextRefiner0ExecuteRequest;
+
+typedef struct PrometheusContextRefinerResidentExecuteRequest {
+  uint32_t struct_size;
+  uint64_t input_generation;
+  uint64_t output_identity;
+  uint32_t audit_enabled;
+} PrometheusContextRefinerResidentExecuteRequest;
+
+typedef struct PrometheusNoiseRefinerFinalAuditRequest {
+  uint32_t struct_size;
+  uint64_t required_output_generation;
+  uint64_t output_identity;
+  float* output;
+  uint64_t output_element_capacity;
+} PrometheusNoiseRefinerFinalAuditRequest;
+
+typedef PrometheusNoiseRefinerFinalAuditRequest PrometheusContextRefinerFinalAuditRequest;
+typedef PrometheusNoiseRefinerFinalAuditRequest PrometheusMainTransformerFinalAuditRequest;
+
+typedef struct PrometheusModelBlockEvidence {
+  uint32_t struct_size;
+  int32_t detail_code;
+  uint32_t created;
+  uint32_t weights_uploaded;
+  uint32_t quarantined;
+  uint32_t output_valid;
+  uint32_t audit_valid;
+  uint32_t fixed_step_count;
+  uint32_t weight_count;
+  uint64_t persistent_bytes;
+  uint64_t reusable_bytes;
+  uint64_t audit_bytes;
+  uint64_t external_bytes;
+  uint64_t total_committed_bytes;
+  uint64_t peak_plan_bytes;
+  uint64_t cold_buffer_allocation_count;
+  uint64_t warm_buffer_allocation_count;
+  uint64_t pipeline_create_count;
+  uint64_t descriptor_set_count;
+  uint64_t weight_upload_count;
+  uint64_t execution_count;
+  uint64_t last_execution_ns;
+  uint64_t execution_plan_identity;
+  uint64_t replay_identity;
+  uint32_t assembly_family;
+  uint32_t parameter_set;
+  uint32_t binding_state;
+  uint32_t active_weight_window;
+  uint64_t parameter_set_aggregate_identity;
+  uint64_t binding_generation;
+  uint64_t output_generation;
+  uint64_t descriptor_generation;
+  uint64_t m1b_boundary_gpu_ns[PROM_MODEL_BLOCK_M1B_PIPELINE_COUNT];
+  uint64_t gpu_total_begin_tick;
+  uint64_t gpu_total_end_tick;
+  uint64_t gpu_total_ns;
+  uint64_t gpu_compute_begin_tick;
+  uint64_t gpu_compute_end_tick;
+  uint64_t gpu_compute_ns;
+  uint64_t gpu_ingress_transfer_ns;
+  uint64_t gpu_joint_copy_ns;
+  uint64_t gpu_readback_ns;
+  uint64_t main_stage_gpu_begin_tick[PROM_MODEL_BLOCK_MAIN_STAGE_COUNT];
+  uint64_t main_stage_gpu_end_tick[PROM_MODEL_BLOCK_MAIN_STAGE_COUNT];
+  uint64_t main_stage_gpu_ns[PROM_MODEL_BLOCK_MAIN_STAGE_COUNT];
+  uint64_t last_active_target_validation_ns;
+  uint64_t last_command_reset_ns;
+  uint64_t last_command_begin_ns;
+  uint64_t last_command_record_ns;
+  uint64_t last_command_end_ns;
+  uint64_t last_queue_submit_ns;
+  uint64_t last_fence_wait_ns;
+  uint64_t last_descriptor_update_ns;
+  uint64_t last_staging_memcpy_ns;
+  uint64_t last_output_readback_ns;
+  /* The reference's Vulkan object counters; this library creates no Vulkan
+     objects and reports them as 0. */
+  uint64_t vk_create_buffer_count;
+  uint64_t vk_destroy_buffer_count;
+  uint64_t vk_allocate_memory_count;
+  uint64_t vk_free_memory_count;
+  uint64_t vk_create_shader_module_count;
+  uint64_t vk_destroy_shader_module_count;
+  uint64_t vk_create_compute_pipelines_count;
+  uint64_t vk_allocate_descriptor_sets_count;
+  uint64_t vk_update_descriptor_sets_count;
+  uint64_t vk_create_command_pool_count;
+  uint64_t vk_allocate_command_buffers_count;
+  uint64_t vk_reset_command_buffer_count;
+  uint64_t vk_queue_submit_count;
+  uint64_t vk_fence_wait_count;
+  uint64_t vk_timeline_wait_count;
+  uint64_t vk_map_memory_count;
+  uint64_t vk_unmap_memory_count;
+  uint64_t vk_flush_count;
+  uint64_t vk_invalidate_count;
+  uint64_t m6a_activation_pack_gpu_ns;
+  uint64_t m6a_cooperative_execute_gpu_ns;
+  uint64_t m6a_w3_segment_repack_gpu_ns;
+} PrometheusModelBlockEvidence;
+
+typedef struct PrometheusCompiledModelSessionCreateRequest {
+  uint32_t struct_size;
+  uint64_t lock_identity;
+  uint32_t execution_profile;
+  uint32_t main_attention_route_policy;
+} PrometheusCompiledModelSessionCreateRequest;
+
+typedef struct PrometheusCompiledModelSessionCaptureRequest {
+  uint32_t struct_size;
+  uint64_t source_output_generation;
+} PrometheusCompiledModelSessionCaptureRequest;
+
+typedef struct PrometheusCompiledModelSessionComposeRequest {
+  uint32_t struct_size;
+  uint64_t required_image_generation;
+  uint64_t required_context_generation;
+} PrometheusCompiledModelSessionComposeRequest;
+
+typedef struct PrometheusCompiledModelSessionEvidence {
+  uint32_t struct_size;
+  int32_t detail_code;
+  uint32_t created;
+  uint32_t quarantined;
+  uint64_t session_identity;
+  uint64_t lock_identity;
+  uint64_t active_block_id;
+  uint64_t binding_generation;
+  uint64_t replay_identity;
+  uint64_t prepared_image_generation;
+  uint64_t prepared_context_generation;
+  uint64_t joint_generation;
+  uint64_t joint_image_generation;
+  uint64_t joint_context_generation;
+  uint64_t prepared_image_bytes;
+  uint64_t prepared_context_bytes;
+  uint64_t joint_bytes;
+  uint64_t cold_buffer_allocation_count;
+  uint64_t warm_buffer_allocation_count;
+  uint64_t composition_count;
+  uint32_t requested_execution_profile;
+  uint32_t selected_execution_profile;
+  uint32_t profile_fallback_reason;
+  uint32_t requested_main_attention_route;
+  uint32_t selected_main_attention_route;
+  uint32_t main_attention_fallback_reason;
+  uint32_t main_attention_shader_id;
+} PrometheusCompiledModelSessionEvidence;
+
+/* reactor_api.h:2713-2733: the closed resident program.  One model block per
+   runtime; ids are never reused.  Family 0 (shader 23, the seven fixed steps)
+   is the resident proof: output = input, audit = the first audit_bytes/4
+   input floats.  Family 1 (shader 24) is the NoiseRefiner. */
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_create(void* handle,
+                                                                   const PrometheusModelBlockCreateRequest* request,
+                                                                   uint64_t* out_block_id,
+                                                                   PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_upload_weights(
+    void* handle, uint64_t block_id, const PrometheusModelBlockWeightUpload* uploads, uint32_t upload_count,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute(void* handle, uint64_t block_id,
+                                                                    const PrometheusModelBlockExecuteRequest* request,
+                                                                    PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2734-2758: NoiseRefiner (1024 image tokens, width 3840):
+   BF16 model input and timestep widened on the device, the fp32 block on the
+   resident weights, output kept resident (output_generation advances). */
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner0_execute(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefiner0ExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner1_execute(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefiner1ExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_rebind(void* handle, uint64_t block_id,
+                                                                     const PrometheusNoiseRefinerRebindRequest* request,
+                                                                     PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_execute_resident(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefinerResidentExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_audit_final(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefinerFinalAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2759-2776: ContextRefiner (32 context tokens, no adaLN). */
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_create(
+    void* handle, const PrometheusContextRefinerCreateRequest* request, uint64_t* out_block_id,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_rebind(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerRebindRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner0_execute(
+    void* handle, uint64_t block_id, const PrometheusContextRefiner0ExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_execute_resident(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerResidentExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_audit_final(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerFinalAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2777-2791: MainTransformer layer i of 30 over the session's
+   1056-token JointWorking stream (image then context). */
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_create(
+    void* handle, const PrometheusMainTransformerCreateRequest* request, uint64_t* out_block_id,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_rebind(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerRebindRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_audit_final(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerFinalAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2792-2794 */
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_get_evidence(void* handle, uint64_t block_id,
+                                                                         PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_destroy(void* handle, uint64_t block_id);
+/* reactor_api.h:2795-2808: the session owns the PreparedImage (1024 x 3840),
+   PreparedContext (32 x 3840) and JointWorking (1056 x 3840) fp32 streams. */
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_create(
+    void* handle, const PrometheusCompiledModelSessionCreateRequest* request, uint64_t* out_session_id,
+    PrometheusCompiledModelSessionEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_capture_completed(
+    void* handle, uint64_t session_id, uint64_t completed_block_id,
+    const PrometheusCompiledModelSessionCaptureRequest* request, PrometheusCompiledModelSessionEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_compose_joint(
+    void* handle, uint64_t session_id, const PrometheusCompiledModelSessionComposeRequest* request,
+    PrometheusCompiledModelSessionEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_get_evidence(
+    void* handle, uint64_t session_id, PrometheusCompiledModelSessionEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_destroy(void* handle, uint64_t session_id);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,7 @@
 #include <math.h>
 #include <string.h>
 
+#include "block_rows.h"
 #include "reactor_internal.h"
 
 namespace prom {
@@ -33,30 +34,11 @@ hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k,
 
 namespace {
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-constexpr int kRowChunks = 16;  // rows up to 16 * 64 * 4 = 4096 floats stay in registers
-
-__device__ __forceinline__ uint16_t f2bf(float v) {
-  const uint32_t bits = __float_as_uint(v);
-  return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
-}
+using rows::f2bf;
+using rows::floatx4;
+using rows::wave_sum;
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-__device__ __forceinline__ void store_bf16x4(uint16_t* dst, floatx4 v) {
-  u32x2 w;
-  w.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
-  w.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
-  *reinterpret_cast<u32x2*>(dst) = w;
-}
 
 // mod[j] = b[j] + sum_k c[k] * W[k][j]; chunk 0 and 2 -> 1 + m, chunk 1 and 3 -> tanh(m)
 // (canonical_reference.go:373-383).  A workgroup owns 64 columns; its 4 waves
@@ -103,44 +85,6 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict
   tab[idx] = make_float2((float)cos(angle), (float)sin(angle));
 }
 
-// a = RMSNorm(x; w) * scale  -> bf16.  One wave per row, D % 4 == 0, D <= 4096.
-__global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                       const float* __restrict__ scale, uint16_t* __restrict__ out,
-                                                       int T, int D, float eps) {
-  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = (int)blockIdx.x * 4 + wave;
-  if (t >= T) return;
-  const int d4 = D >> 2;
-  const floatx4* row = reinterpret_cast<const floatx4*>(x + (size_t)t * D);
-  floatx4 v[kRowChunks];
-  float ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      v[c] = row[i];
-      ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
-    }
-  }
-  ss = wave_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const floatx4* w4 = reinterpret_cast<const floatx4*>(w);
-  const floatx4* s4 = reinterpret_cast<const floatx4*>(scale);
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 g = w4[i], sc = s4[i];
-      floatx4 o;
-      o.x = v[c].x * inv * g.x * sc.x;
-      o.y = v[c].y * inv * g.y * sc.y;
-      o.z = v[c].z * inv * g.z * sc.z;
-      o.w = v[c].w * inv * g.w * sc.w;
-      store_bf16x4(out + (size_t)t * D + 4 * i, o);
-    }
-  }
-}
-
 // Per (token, head): q and k RMSNorm over 128 channels, then RoPE on the
 // interleaved pairs (2p, 2p+1) with the token's (cos, sin) table entry for
 // pair p (zimage/canonical_contract.go:66-87, zimage_main_transformer_canonical.py:124-140).
@@ -181,106 +125,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restri
   }
 }
 
-// r = x + gateA * RMSNorm(proj; n2)  (fp32 out), f = RMSNorm(r; n3) * scaleM (bf16 out)
-__global__ __launch_bounds__(256) void resid_norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ proj,
-                                                             const float* __restrict__ n2, const float* __restrict__ gate,
-                                                             const float* __restrict__ n3, const float* __restrict__ scale,
-                                                             float* __restrict__ r_out, uint16_t* __restrict__ f_out,
-                                                             int T, int D, float eps) {
-  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = (int)blockIdx.x * 4 + wave;
-  if (t >= T) return;
-  const int d4 = D >> 2;
-  const floatx4* p4 = reinterpret_cast<const floatx4*>(proj + (size_t)t * D);
-  const floatx4* x4 = reinterpret_cast<const floatx4*>(x + (size_t)t * D);
-  floatx4 v[kRowChunks];
-  float ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      v[c] = p4[i];
-      ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
-    }
-  }
-  ss = wave_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const floatx4* g4 = reinterpret_cast<const floatx4*>(gate);
-  const floatx4* w4 = reinterpret_cast<const floatx4*>(n2);
-  float ss2 = 0.0f;
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 xv = x4[i], g = g4[i], w = w4[i];
-      floatx4 r;
-      r.x = xv.x + g.x * (v[c].x * inv * w.x);
-      r.y = xv.y + g.y * (v[c].y * inv * w.y);
-      r.z = xv.z + g.z * (v[c].z * inv * w.z);
-      r.w = xv.w + g.w * (v[c].w * inv * w.w);
-      v[c] = r;
-      reinterpret_cast<floatx4*>(r_out + (size_t)t * D)[i] = r;
-      ss2 += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
-    }
-  }
-  ss2 = wave_sum(ss2);
-  const float inv2 = 1.0f / sqrtf(ss2 / (float)D + eps);
-  const floatx4* w3 = reinterpret_cast<const floatx4*>(n3);
-  const floatx4* s4 = reinterpret_cast<const floatx4*>(scale);
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 w = w3[i], sc = s4[i];
-      floatx4 o;
-      o.x = v[c].x * inv2 * w.x * sc.x;
-      o.y = v[c].y * inv2 * w.y * sc.y;
-      o.z = v[c].z * inv2 * w.z * sc.z;
-      o.w = v[c].w * inv2 * w.w * sc.w;
-      store_bf16x4(f_out + (size_t)t * D + 4 * i, o);
-    }
-  }
-}
-
-// out = r + gateM * RMSNorm(w2; n4)
-__global__ __launch_bounds__(256) void final_resid_kernel(const float* __restrict__ r, const float* __restrict__ w2,
-                                                          const float* __restrict__ n4, const float* __restrict__ gate,
-                                                          float* __restrict__ out, int T, int D, float eps) {
-  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = (int)blockIdx.x * 4 + wave;
-  if (t >= T) return;
-  const int d4 = D >> 2;
-  const floatx4* y4 = reinterpret_cast<const floatx4*>(w2 + (size_t)t * D);
-  floatx4 v[kRowChunks];
-  float ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      v[c] = y4[i];
-      ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
-    }
-  }
-  ss = wave_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const floatx4* r4 = reinterpret_cast<const floatx4*>(r + (size_t)t * D);
-  const floatx4* w4 = reinterpret_cast<const floatx4*>(n4);
-  const floatx4* g4 = reinterpret_cast<const floatx4*>(gate);
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 rv = r4[i], w = w4[i], g = g4[i];
-      floatx4 o;
-      o.x = rv.x + g.x * (v[c].x * inv * w.x);
-      o.y = rv.y + g.y * (v[c].y * inv * w.y);
-      o.z = rv.z + g.z * (v[c].z * inv * w.z);
-      o.w = rv.w + g.w * (v[c].w * inv * w.w);
-      reinterpret_cast<floatx4*>(out + (size_t)t * D)[i] = o;
-    }
-  }
-}
-
 // G [T, 2F] (w1 | w3) -> h [T, F] bf16: silu(g) * u (canonical_reference.go:457-460)
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ G, uint16_t* __restrict__ Hb, int T,
                                                      int F) {
@@ -296,7 +140,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ G
     o.y = g.y / (1.0f + expf(-g.y)) * u.y;
     o.z = g.z / (1.0f + expf(-g.z)) * u.z;
     o.w = g.w / (1.0f + expf(-g.w)) * u.w;
-    store_bf16x4(Hb + t * F + 4 * i, o);
+    rows::store4(Hb + t * F + 4 * i, o);
   }
 }
 
@@ -368,13 +212,13 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     if (e != hipSuccess) return e; \
     ++n;                           \
   } while (0)
-  const dim3 rows((T + 3) / 4), blk(256);
+  const dim3 row_grid((T + 3) / 4), blk(256);
   hipLaunchKernelGGL(adaln_kernel, dim3((4 * D + 63) / 64), blk, 0, st, r->condition, r->w_adaln, r->b_adaln, mod, C, D);
   PROM_STEP(hipGetLastError());
   hipLaunchKernelGGL(rope_table_kernel, dim3((T * 64 + 255) / 256), blk, 0, st, r->coordinates, rope, T, r->rope_theta,
                      (int)r->rope_axes[0], (int)r->rope_axes[1]);
   PROM_STEP(hipGetLastError());
-  hipLaunchKernelGGL(norm_mod_kernel, rows, blk, 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
+  hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, row_grid, blk, 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, qkv, nullptr, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, Q, K, V,
@@ -382,7 +226,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_flash_attn_bf16(Q, D, K, D, V, D, O, D, T, H, 1.0f / sqrtf(128.0f), st));
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, proj, nullptr, D, T, D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(resid_norm_mod_kernel, rows, blk, 0, st, r->input, proj, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
+  hipLaunchKernelGGL(rows::resid_norm_mod_kernel<uint16_t>, row_grid, blk, 0, st, r->input, proj, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
                      R, Fb, T, D, eps);
   PROM_STEP(hipGetLastError());
   // FFN up-projection with SwiGLU fused into the GEMM epilogue when the shape
@@ -398,7 +242,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     PROM_STEP(fused);
   }
   PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, W2, nullptr, D, T, D, F, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(final_resid_kernel, rows, blk, 0, st, R, W2, r->ffn_norm2, gateM, r->output, T, D, eps);
+  hipLaunchKernelGGL(rows::final_resid_kernel, row_grid, blk, 0, st, R, W2, r->ffn_norm2, gateM, r->output, T, D, eps);
   PROM_STEP(hipGetLastError());
 #undef PROM_STEP
   if (launches) *launches = n;

@@ -1,0 +1,1819 @@
+// Resident model blocks and the compiled Z-Image session
+// (internal/prometheus/native/reactor_api.h:666-1249, 2713-2821;
+//  reactor_vulkan_model_block.c; reactors/PrometheusModelBlock.concept).
+//
+// The reference's contract, kept here:
+//   * one model block and one session per runtime; ids are never reused;
+//   * a create request is a closed program: the seven fixed steps, declared
+//     weights (content/layout identity, byte count) and, for the Z-Image
+//     families, the model lock's parameter-set aggregates and weight sizes
+//     (reactor_vulkan_model_block.c:393-493);
+//   * weights bind in one transaction: an initial upload invalidates the set
+//     until every weight has landed; a rebind (replacement) uploads into a
+//     second set and swaps at commit, so the old set stays valid on failure
+//     (PrometheusModelBlock.concept:1140-1268); the binding generation
+//     advances only at commit;
+//   * block outputs stay resident and are versioned by output_generation; a
+//     resident execution names the generation it consumes; audits copy a
+//     completed output (or one stage) to the host;
+//   * the session owns the PreparedImage, PreparedContext and JointWorking
+//     streams; capture, compose and the MainTransformer's joint read/write are
+//     generation-checked (PrometheusModelBlock.concept:860-1098);
+//   * faults: the config's test_flags (FAIL_UPLOAD, FAIL_DOWNLOAD) and the
+//     one-shot reduction_test_flags (command record, queue submit, completion
+//     observation), consumed in execution order; an unobserved completion
+//     quarantines the block until the next call reaps it.
+//
+// The MI355X design: Vulkan buffers, descriptor sets and command buffers
+// become plain device allocations made once at create (nothing is allocated
+// by an execution), work is queued on the runtime's HIP stream and completion
+// is a stream synchronisation.  FP16 weights are widened to fp32 once, at
+// upload, into the layouts the fp32 Z-Image block (zimage_f32.hip) reads; the
+// W1 and W3 tensors land side by side in one [3840, 20480] matrix so the FFN
+// up-projection is a single GEMM.
+#include <string.h>
+
+#include <new>
+
+#include "reactor_internal.h"
+
+namespace prom {
+
+namespace {
+
+constexpr uint32_t kShaderResident = 23u;  // the resident proof program (identity)
+constexpr uint32_t kShaderNoise = 24u;     // NoiseRefiner (M1B ingress + block)
+constexpr uint32_t kShaderContext = 25u;   // ContextRefiner
+constexpr uint32_t kShaderMain = 40u;      // MainTransformer
+
+constexpr int kWidth = 3840, kHeads = 30, kFfn = 10240;
+constexpr int kImageTokens = 1024, kContextTokens = 32, kJointTokens = 1056;
+constexpr float kEps = 1e-5f;
+constexpr uint32_t kTransientAuditFloats = 64u;  // PROM_MODEL_BLOCK_M1C_TRANSIENT_AUDIT_FLOATS
+
+const uint32_t kSteps[PROM_MODEL_BLOCK_MAX_STEPS] = {1u, 2u, 3u, 4u, 5u, 6u, 7u};
+
+// Cache-manifest lexical order of one NoiseRefiner / MainTransformer layer
+// (reactor_vulkan_model_block.c:158-161) and of the unmodulated ContextRefiner
+// (:198-200), whose tensor i is semantic slot i + 2.
+const uint64_t kNoiseWeightBytes[13] = {30720ull,    7864320ull,  256ull,      29491200ull, 256ull,
+                                        88473600ull, 7680ull,     7680ull,     78643200ull, 78643200ull,
+                                        78643200ull, 7680ull,     7680ull};
+const uint64_t kContextWeightBytes[11] = {256ull,       29491200ull, 256ull,       88473600ull,
+                                          7680ull,      7680ull,     78643200ull,  78643200ull,
+                                          78643200ull, 7680ull,     7680ull};
+
+// Parameter-set aggregates and descriptor identities of the Z-Image Turbo lock
+// (the reference's generated models/zimage-turbo/resolved_descriptor.h).
+const uint64_t kNoiseAggregate[2] = {0xa1ba526898a2a752ull, 0x80c0cd75f44cc434ull};
+const uint64_t kContextAggregate[2] = {0xc08b908a921a80e1ull, 0x30268c3b0d7a6fafull};
+const uint64_t kContextMemoryPlan = 536870912ull;
+const uint64_t kContextExecutionPlan = 0xa30b2ac6ff947b21ull;
+const uint64_t kContextCanonical[2] = {0xd2b8167de614da25ull, 0x08377e8a46b65cffull};
+const uint64_t kMainAggregate[30] = {
+    0x48e987811885741aull, 0x7ec04d7363bb1ac0ull, 0x41b9b7985035fd20ull, 0x3ba944c7dd3bc787ull,
+    0xc83fa21d17408859ull, 0xa643f7836a056d34ull, 0x6ee8d2ce1947fb66ull, 0xc00357c21617e910ull,
+    0xfc1f557f75895368ull, 0xf3d59ef2a2f18d24ull, 0x7e79e59c29ee081bull, 0x3fef07f8f482453eull,
+    0xa2067c05a569f2d5ull, 0xd4bcc84602cd9e77ull, 0xebc24a91474ac4d5ull, 0xa42866e4b7a055f8ull,
+    0xdb0272f70aa50aa9ull, 0xf6aa44dcc9f59945ull, 0xf921c7aa36817102ull, 0x96a9d4e83e046880ull,
+    0xc161dd253cfe99d7ull, 0x9638d4a676d163acull, 0x0e4070f7fda57719ull, 0x76813a3cc2486108ull,
+    0xd64f21d7e6b80100ull, 0xe616bea34a39ed99ull, 0xf177c2e5179c53c4ull, 0x75700608176f4340ull,
+    0x7750f6f142eeb066ull, 0xdb7de286ef1f507aull};
+const uint64_t kStreamBytes[3] = {15728640ull, 491520ull, 16220160ull};  // image, context, joint
+
+// fp32 destination of semantic weight slot s: [rows, cols] written with
+// leading dimension ld at column offset col0 of the buffer of slot `owner`.
+struct SlotShape {
+  uint32_t rows, cols, ld, col0, owner;
+};
+const SlotShape kSlots[13] = {
+    {1, 4 * kWidth, 4 * kWidth, 0, 0},           // adaLN bias
+    {256, 4 * kWidth, 4 * kWidth, 0, 1},         // adaLN weight [256, 15360]
+    {1, 128, 128, 0, 2},                         // k_norm
+    {kWidth, kWidth, kWidth, 0, 3},              // attention.out [3840, 3840]
+    {1, 128, 128, 0, 4},                         // q_norm
+    {kWidth, 3 * kWidth, 3 * kWidth, 0, 5},      // attention.qkv [3840, 11520]
+    {1, kWidth, kWidth, 0, 6},                   // attention_norm1
+    {1, kWidth, kWidth, 0, 7},                   // attention_norm2
+    {kWidth, kFfn, 2 * kFfn, 0, 8},              // w1 -> columns [0, F) of W13
+    {kFfn, kWidth, kWidth, 0, 9},                // w2 [10240, 3840]
+    {kWidth, kFfn, 2 * kFfn, kFfn, 8},           // w3 -> columns [F, 2F) of W13
+    {1, kWidth, kWidth, 0, 11},                  // ffn_norm1
+    {1, kWidth, kWidth, 0, 12}};                 // ffn_norm2
+
+enum Program { kProgProof, kProgNoise, kProgContext, kProgMain };
+
+uint64_t hash_u64(uint64_t h, uint64_t v) {  // FNV-1a over the 8 little-endian bytes
+  for (int i = 0; i < 8; ++i) {
+    h ^= (v >> (8 * i)) & 0xffu;
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+struct WeightSet {
+  void* buf[13] = {};  // device buffers per slot (slot 10 aliases slot 8's W13)
+  uint64_t bytes = 0;
+  uint32_t allocations = 0;
+};
+
+struct ModelBlock {
+  bool created = false;
+  uint64_t id = 0;
+  Program program = kProgProof;
+  int tokens = 0;
+  // declared program
+  uint32_t family = 0, parameter_set = 0, shader_id = 0, weight_count = 0, step_count = 0;
+  uint32_t steps[PROM_MODEL_BLOCK_MAX_STEPS] = {};
+  uint64_t aggregate = 0, model_contract = 0, weight_identity = 0, shader_portfolio = 0, precision = 0,
+           capability = 0, memory_ceiling = 0, ext_in = 0, ext_out = 0, declared_audit = 0;
+  PrometheusModelBlockWeightDeclaration decl[PROM_MODEL_BLOCK_MAX_WEIGHTS] = {};
+  // binding
+  WeightSet active, candidate;
+  bool binding_valid = false;
+  uint32_t binding_phase = 0;  // 0 empty, 3 uploading, 7 failed (binding_state when not valid)
+  uint64_t binding_generation = 0, descriptor_generation = 0;
+  // device buffers, allocated at create
+  void* staging = nullptr;  // raw upload bytes (largest declared weight)
+  uint64_t staging_bytes = 0;
+  float* x = nullptr;       // block input [T, D] (external ingress or resident boundary)
+  float* out = nullptr;     // resident output [T, D]
+  uint16_t* x_bf16 = nullptr;
+  uint16_t* cond_bf16 = nullptr;
+  float* cond = nullptr;    // [256]
+  float* coords = nullptr;  // [T, 3]
+  char* ws = nullptr;
+  size_t ws_off[kZCount] = {};
+  float* proof_in = nullptr;  // resident proof: input, output, audit
+  float* proof_out = nullptr;
+  float* proof_audit = nullptr;
+  uint64_t reusable_bytes = 0, audit_alloc_bytes = 0;
+  hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+  // execution state
+  bool quarantined = false, output_valid = false, audit_valid = false;
+  uint64_t output_generation = 0, resident_input_generation = 0;
+  uint64_t plan_identity = 0, replay_identity = 0, prefix_replay = 0;
+  uint64_t cold_allocations = 0, pipelines = 0, uploads = 0, executions = 0;
+  uint64_t last_execution_ns = 0, gpu_total_ns = 0, gpu_compute_ns = 0, last_memcpy_ns = 0, last_readback_ns = 0;
+  int32_t last_detail = 0;
+};
+
+struct Stream {
+  uint64_t generation = 0, producer = 0, output = 0;
+  bool valid = false;
+};
+
+struct ModelSession {
+  bool created = false;
+  uint64_t id = 0, lock = 0;
+  uint32_t requested_profile = 0, requested_route = 0;
+  float* buf[3] = {};  // image [1024, D], context [32, D], joint [1056, D]
+  Stream streams[3];
+  bool joint_writing = false;
+  uint64_t joint_image_generation = 0, joint_context_generation = 0, compositions = 0;
+  uint64_t active_block_id = 0, binding_generation = 0, replay = 0, cold_allocations = 0;
+  int32_t last_detail = 0;
+};
+
+}  // namespace
+
+struct ModelState {
+  ModelBlock block;
+  ModelSession session;
+  uint64_t next_block_id = 1, next_session_id = 1;
+};
+
+namespace {
+
+// ---------------------------------------------------------------- helpers
+
+__global__ __launch_bounds__(256) void proof_kernel(const float* __restrict__ in, float* __restrict__ out, uint64_t n,
+                                                    float* __restrict__ audit, uint64_t audit_n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const float v = in[i];
+    out[i] = v;
+    if (i < audit_n) audit[i] = v;
+  }
+}
+
+// coords [T, 3] of the image grid (frame 33 = 15 text tokens + 17 padding + 1,
+// row t/32, column t%32: zimage/canonical_contract.go:36-64) followed by the
+// context tokens (frame 1 + i, 0, 0: context_refiner_reference.go:156-158).
+__global__ void coords_kernel(float* __restrict__ c, int image, int context) {
+  const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (t >= image + context) return;
+  if (t < image) {
+    c[3 * t] = 33.0f;
+    c[3 * t + 1] = (float)(t / 32);
+    c[3 * t + 2] = (float)(t % 32);
+  } else {
+    c[3 * t] = (float)(t - image + 1);
+    c[3 * t + 1] = 0.0f;
+    c[3 * t + 2] = 0.0f;
+  }
+}
+
+ModelState* state_of(Runtime* rt) {
+  if (rt->model == nullptr) rt->model = new (std::nothrow) ModelState();
+  return rt->model;
+}
+
+bool alloc_dev(ModelBlock* b, void** p, uint64_t bytes) {
+  *p = nullptr;
+  if (bytes == 0) return true;
+  if (hipMalloc(p, (size_t)bytes) != hipSuccess) {
+    *p = nullptr;
+    return false;
+  }
+  ++b->cold_allocations;
+  return true;
+}
+
+void free_dev(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+void free_set(WeightSet* s) {
+  for (int i = 0; i < 13; ++i)
+    if (i != 10) free_dev(s->buf[i]);  // slot 10 aliases slot 8 for the Z-Image programs
+  *s = WeightSet{};
+}
+
+void free_set_proof(WeightSet* s) {
+  for (int i = 0; i < 13; ++i) free_dev(s->buf[i]);
+  *s = WeightSet{};
+}
+
+void release_block(ModelBlock* b) {
+  if (ctx().available) (void)hipStreamSynchronize(ctx().stream);
+  if (b->program == kProgProof) {
+    free_set_proof(&b->active);
+    free_set_proof(&b->candidate);
+  } else {
+    free_set(&b->active);
+    free_set(&b->candidate);
+  }
+  void* ptrs[] = {b->staging, b->x, b->out, b->x_bf16, b->cond_bf16, b->cond, b->coords, b->ws,
+                  b->proof_in, b->proof_out, b->proof_audit};
+  for (void* p : ptrs) free_dev(p);
+  if (b->ev_begin) (void)hipEventDestroy(b->ev_begin);
+  if (b->ev_end) (void)hipEventDestroy(b->ev_end);
+  *b = ModelBlock{};
+}
+
+void release_session(ModelSession* s) {
+  if (!s->created) return;
+  if (ctx().available) (void)hipStreamSynchronize(ctx().stream);
+  for (float* p : s->buf) free_dev(p);
+  *s = ModelSession{};
+}
+
+// Drains work whose completion was not observed (reactor_vulkan_model_block.c:1045-1063).
+bool reap(ModelBlock* b) {
+  if (!b->quarantined) return true;
+  if (hipStreamSynchronize(ctx().stream) != hipSuccess) return false;
+  b->quarantined = false;
+  b->output_valid = false;
+  b->audit_valid = false;
+  return true;
+}
+
+void mark_failure(ModelBlock* b, int32_t detail) {
+  b->output_valid = false;
+  b->audit_valid = false;
+  b->last_detail = detail;
+}
+
+uint32_t binding_state(const ModelBlock* b) {
+  if (b->quarantined) return PROM_NOISE_REFINER_BINDING_QUARANTINED;
+  if (b->binding_valid) return PROM_NOISE_REFINER_BINDING_BOUND;
+  return b->binding_phase;
+}
+
+void fill_evidence(const ModelBlock* b, int32_t detail, PrometheusModelBlockEvidence* ev) {
+  if (ev == nullptr) return;
+  memset(ev, 0, sizeof(*ev));
+  ev->struct_size = (uint32_t)sizeof(*ev);
+  ev->detail_code = detail;
+  if (b == nullptr || !b->created) return;
+  const uint64_t persistent = b->active.bytes + b->candidate.bytes;
+  const uint64_t audit = b->audit_alloc_bytes;
+  ev->created = 1u;
+  ev->weights_uploaded = b->binding_valid ? 1u : 0u;
+  ev->quarantined = b->quarantined ? 1u : 0u;
+  ev->output_valid = b->output_valid ? 1u : 0u;
+  ev->audit_valid = b->audit_valid ? 1u : 0u;
+  ev->fixed_step_count = b->step_count;
+  ev->weight_count = b->weight_count;
+  ev->persistent_bytes = persistent;
+  ev->reusable_bytes = b->reusable_bytes;
+  ev->audit_bytes = audit;
+  ev->external_bytes = b->ext_in + b->ext_out;
+  ev->total_committed_bytes = persistent + b->reusable_bytes + audit;
+  ev->peak_plan_bytes = ev->total_committed_bytes;
+  ev->cold_buffer_allocation_count = b->cold_allocations;
+  ev->warm_buffer_allocation_count = 0;  // executions never allocate
+  ev->pipeline_create_count = b->pipelines;
+  ev->weight_upload_count = b->uploads;
+  ev->execution_count = b->executions;
+  ev->last_execution_ns = b->last_execution_ns;
+  ev->execution_plan_identity = b->plan_identity;
+  ev->replay_identity = b->replay_identity;
+  ev->assembly_family = b->family;
+  ev->parameter_set = b->parameter_set;
+  ev->binding_state = binding_state(b);
+  ev->parameter_set_aggregate_identity = b->aggregate;
+  ev->binding_generation = b->binding_generation;
+  ev->output_generation = b->output_generation;
+  ev->descriptor_generation = b->descriptor_generation;
+  ev->gpu_total_ns = b->gpu_total_ns;
+  ev->gpu_compute_ns = b->gpu_compute_ns;
+  ev->last_staging_memcpy_ns = b->last_memcpy_ns;
+  ev->last_output_readback_ns = b->last_readback_ns;
+}
+
+void fill_session_evidence(const ModelSession* s, PrometheusCompiledModelSessionEvidence* ev, int32_t detail_if_null) {
+  if (ev == nullptr) return;
+  memset(ev, 0, sizeof(*ev));
+  ev->struct_size = (uint32_t)sizeof(*ev);
+  if (s == nullptr || !s->created) {
+    ev->detail_code = detail_if_null;
+    return;
+  }
+  ev->detail_code = s->last_detail;
+  ev->created = 1u;
+  ev->session_identity = s->id;
+  ev->lock_identity = s->lock;
+  ev->active_block_id = s->active_block_id;
+  ev->binding_generation = s->binding_generation;
+  ev->replay_identity = s->replay;
+  ev->prepared_image_generation = s->streams[0].generation;
+  ev->prepared_context_generation = s->streams[1].generation;
+  ev->joint_generation = s->streams[2].generation;
+  ev->joint_image_generation = s->joint_image_generation;
+  ev->joint_context_generation = s->joint_context_generation;
+  ev->prepared_image_bytes = kStreamBytes[0];
+  ev->prepared_context_bytes = kStreamBytes[1];
+  ev->joint_bytes = kStreamBytes[2];
+  ev->cold_buffer_allocation_count = s->cold_allocations;
+  ev->composition_count = s->compositions;
+  ev->requested_execution_profile = s->requested_profile;
+  ev->selected_execution_profile = PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY;
+  ev->requested_main_attention_route = s->requested_route;
+  ev->selected_main_attention_route = PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL;
+}
+
+bool add_bytes(uint64_t* total, uint64_t v) {
+  if (v > UINT64_MAX - *total) return false;
+  *total += v;
+  return true;
+}
+
+bool steps_exact(const PrometheusModelBlockCreateRequest* r) {
+  if (r->step_count != PROM_MODEL_BLOCK_MAX_STEPS) return false;
+  for (uint32_t i = 0; i < PROM_MODEL_BLOCK_MAX_STEPS; ++i)
+    if (r->steps[i] != kSteps[i]) return false;
+  return true;
+}
+
+// reactor_vulkan_model_block.c:393-493
+bool validate_create(const PrometheusModelBlockCreateRequest* r) {
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->model_contract_identity == 0 || r->weight_identity == 0 ||
+      r->shader_portfolio_identity == 0 || r->precision_policy_identity == 0 || r->capability_route_identity == 0 ||
+      r->memory_ceiling_bytes == 0 ||
+      (r->shader_id != kShaderResident && r->shader_id != kShaderNoise && r->shader_id != kShaderContext &&
+       r->shader_id != kShaderMain) ||
+      r->weight_count == 0 || r->weight_count > PROM_MODEL_BLOCK_MAX_WEIGHTS || r->audit_bytes == 0 ||
+      (r->external_input_bytes % 4) != 0 || (r->external_output_bytes % 4) != 0 || (r->audit_bytes % 4) != 0 ||
+      !steps_exact(r))
+    return false;
+  if (r->shader_id != kShaderMain && r->external_input_bytes == 0) return false;
+  if (r->shader_id == kShaderResident && r->external_output_bytes == 0) return false;
+  const uint32_t f = r->assembly_family, p = r->parameter_set;
+  if (f == PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO &&
+      ((p != 1u && p != 2u) || r->parameter_set_aggregate_identity != kNoiseAggregate[p == 2u ? 1 : 0] ||
+       r->shader_id != kShaderNoise))
+    return false;
+  if (f == PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO &&
+      ((p != 1u && p != 2u) || r->parameter_set_aggregate_identity != kContextAggregate[p == 2u ? 1 : 0] ||
+       r->shader_id != kShaderContext))
+    return false;
+  if (f == PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO &&
+      (p == 0u || p > 30u || r->parameter_set_aggregate_identity != kMainAggregate[p - 1] || r->shader_id != kShaderMain))
+    return false;
+  if (f > PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO) return false;
+  if (f == 0u && (p != 0u || r->parameter_set_aggregate_identity != 0u)) return false;
+  if (r->shader_id == kShaderNoise &&
+      (r->weight_count != 13u || r->external_input_bytes != (uint64_t)kImageTokens * kWidth * 2 ||
+       r->external_output_bytes != 0 || r->audit_bytes > PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES))
+    return false;
+  if (f == PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO &&
+      (r->weight_count != 11u || r->external_input_bytes != (uint64_t)kContextTokens * kWidth * 4 ||
+       r->external_output_bytes != 0 || r->audit_bytes > PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES))
+    return false;
+  if (f == PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO &&
+      (r->weight_count != 13u || r->external_input_bytes != 0 || r->external_output_bytes != 0 ||
+       r->audit_bytes > PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES))
+    return false;
+  uint64_t weights = 0, total = 0;
+  for (uint32_t i = 0; i < r->weight_count; ++i) {
+    const PrometheusModelBlockWeightDeclaration& w = r->weights[i];
+    if (w.content_identity == 0 || w.layout_identity == 0 || w.byte_count == 0 || !add_bytes(&weights, w.byte_count))
+      return false;
+    if ((r->shader_id == kShaderNoise || f == PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO) &&
+        w.byte_count != kNoiseWeightBytes[i])
+      return false;
+    if (f == PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO && w.byte_count != kContextWeightBytes[i]) return false;
+  }
+  uint64_t reserve = 0;
+  if (r->shader_id == kShaderNoise) reserve = 128ull << 20;
+  else if (f == PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO) reserve = 16ull << 20;
+  else if (f == PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO) reserve = 192ull << 20;
+  if (r->shader_id == kShaderNoise || f >= PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO) {
+    total = weights;
+    return add_bytes(&total, reserve) && total <= r->memory_ceiling_bytes;
+  }
+  return add_bytes(&total, weights) && add_bytes(&total, r->external_input_bytes) &&
+         add_bytes(&total, r->external_input_bytes) && add_bytes(&total, r->external_output_bytes) &&
+         add_bytes(&total, r->external_output_bytes) && add_bytes(&total, r->audit_bytes) &&
+         add_bytes(&total, r->audit_bytes) && add_bytes(&total, weights) && total <= r->memory_ceiling_bytes;
+}
+
+// Program identity: the reference's field order (reactor_vulkan_model_block.c:495-522)
+// followed, for the Z-Image programs, by this library's fixed kernel chain.
+uint64_t plan_identity(const ModelBlock* b) {
+  uint64_t h = 1469598103934665603ull;
+  const uint64_t fields[] = {b->model_contract, b->family,       b->parameter_set, b->aggregate,
+                             b->weight_identity, b->shader_portfolio, b->precision, b->capability,
+                             b->shader_id,      b->ext_in,       b->ext_out,       b->declared_audit,
+                             kTransientAuditFloats * 4ull, 3ull};
+  for (uint64_t v : fields) h = hash_u64(h, v);
+  for (uint32_t i = 0; i < b->weight_count; ++i) {
+    h = hash_u64(h, b->decl[i].content_identity);
+    h = hash_u64(h, b->decl[i].layout_identity);
+    h = hash_u64(h, b->decl[i].byte_count);
+  }
+  for (uint32_t i = 0; i < b->step_count; ++i) h = hash_u64(h, b->steps[i]);
+  if (b->program != kProgProof) {
+    // adaln, norm_mod, qkv sgemm, qkv_split, scores, softmax, pv, out sgemm,
+    // resid_norm_mod, w13 sgemm, swiglu, w2 sgemm, final_resid
+    for (uint64_t k = 1; k <= 13; ++k) h = hash_u64(h, 0x4d49333535000000ull | k);
+    h = hash_u64(h, (uint64_t)b->tokens);
+  }
+  return h;
+}
+
+int slot_of(const ModelBlock* b, uint32_t index) { return b->program == kProgContext ? (int)index + 2 : (int)index; }
+
+// Allocates the device buffers of one weight set (the Z-Image layout or the
+// declared raw bytes of the resident proof).
+bool alloc_set(ModelBlock* b, WeightSet* s) {
+  *s = WeightSet{};
+  if (b->program == kProgProof) {
+    for (uint32_t i = 0; i < b->weight_count; ++i) {
+      if (!alloc_dev(b, &s->buf[i], b->decl[i].byte_count)) return false;
+      ++s->allocations;
+      s->bytes += b->decl[i].byte_count;
+    }
+    return true;
+  }
+  for (uint32_t i = 0; i < b->weight_count; ++i) {
+    const int slot = slot_of(b, i);
+    if (slot == 10) continue;  // lands in W13 with slot 8
+    const SlotShape& sh = kSlots[slot];
+    const uint64_t bytes = (uint64_t)sh.rows * sh.ld * 4;
+    if (!alloc_dev(b, &s->buf[slot], bytes)) return false;
+    ++s->allocations;
+    s->bytes += bytes;
+  }
+  if (s->buf[8]) s->buf[10] = s->buf[8];
+  return true;
+}
+
+// Uploads weight i of `u` into set `s`: raw bytes, or FP16 widened to fp32.
+hipError_t upload_one(ModelBlock* b, WeightSet* s, uint32_t i, const PrometheusModelBlockWeightUpload& u) {
+  hipStream_t st = ctx().stream;
+  if (b->program == kProgProof)
+    return hipMemcpyAsync(s->buf[i], u.bytes, (size_t)u.byte_count, hipMemcpyHostToDevice, st);
+  const int slot = slot_of(b, i);
+  const SlotShape& sh = kSlots[slot];
+  hipError_t e = hipMemcpyAsync(b->staging, u.bytes, (size_t)u.byte_count, hipMemcpyHostToDevice, st);
+  if (e != hipSuccess) return e;
+  float* dst = static_cast<float*>(s->buf[sh.owner]) + sh.col0;
+  e = launch_widen_f16(static_cast<const uint16_t*>(b->staging), dst, sh.rows, sh.cols, sh.ld, st);
+  if (e != hipSuccess) return e;
+  return hipStreamSynchronize(st);  // the staging buffer is reused by the next weight
+}
+
+bool upload_matches(const ModelBlock* b, const PrometheusModelBlockWeightUpload* uploads, uint32_t count,
+                    const uint64_t* sizes) {
+  for (uint32_t i = 0; i < count; ++i) {
+    const PrometheusModelBlockWeightUpload& u = uploads[i];
+    if (u.binding_index != i || u.bytes == nullptr || u.byte_count > b->staging_bytes) return false;
+    if (sizes != nullptr) {
+      if (u.content_identity == 0 || u.layout_identity == 0 || u.byte_count != sizes[i]) return false;
+    } else if (u.byte_count != b->decl[i].byte_count || u.content_identity != b->decl[i].content_identity ||
+               u.layout_identity != b->decl[i].layout_identity) {
+      return false;
+    }
+  }
+  return true;
+}
+
+// The binding transaction (PrometheusModelBlock.concept:1140-1268 and
+// reactor_vulkan_model_block.c:1065-1123).  replacement: upload into a second
+// set and swap at commit; otherwise overwrite the active set in place.
+bool change_weights(Runtime* rt, ModelBlock* b, const PrometheusModelBlockWeightUpload* uploads, uint32_t count,
+                    bool replacement) {
+  if (!reap(b)) {
+    b->last_detail = PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
+    return false;
+  }
+  WeightSet* target = &b->active;
+  if (replacement) {
+    if (!alloc_set(b, &b->candidate)) {
+      free_set(&b->candidate);
+      b->last_detail = PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED;
+      return false;
+    }
+    target = &b->candidate;
+  } else {
+    b->binding_valid = false;
+    b->binding_phase = PROM_NOISE_REFINER_BINDING_UPLOADING;
+  }
+  const uint64_t t0 = wall_ns();
+  for (uint32_t i = 0; i < count; ++i) {
+    if ((rt->test_flags & PROM_TESTCFG_FAIL_UPLOAD) != 0u || upload_one(b, target, i, uploads[i]) != hipSuccess) {
+      (void)hipStreamSynchronize(ctx().stream);
+      if (replacement) {
+        free_set(&b->candidate);
+      } else {
+        b->binding_phase = PROM_NOISE_REFINER_BINDING_FAILED_BEFORE_COMMIT;
+      }
+      b->last_detail = PROM_MODEL_BLOCK_DETAIL_UPLOAD_FAILED;
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_UPLOAD_FAILED);
+      return false;
+    }
+    ++b->uploads;
+  }
+  if (hipStreamSynchronize(ctx().stream) != hipSuccess) {
+    b->last_detail = PROM_MODEL_BLOCK_DETAIL_UPLOAD_FAILED;
+    return false;
+  }
+  b->last_memcpy_ns = wall_ns() - t0;
+  if (replacement) {
+    free_set(&b->active);
+    b->active = b->candidate;
+    b->candidate = WeightSet{};
+  }
+  b->binding_valid = true;
+  b->binding_phase = PROM_NOISE_REFINER_BINDING_BOUND;
+  b->binding_generation += 1;
+  b->descriptor_generation += 1;
+  b->output_valid = false;
+  b->audit_valid = false;
+  b->resident_input_generation = 0;
+  b->replay_identity = 0;
+  b->prefix_replay = 0;
+  b->last_detail = 0;
+  return true;
+}
+
+ZImageBlockWeights weights_of(const ModelBlock* b) {
+  const WeightSet& s = b->active;
+  auto f = [&](int slot) { return static_cast<const float*>(s.buf[slot]); };
+  ZImageBlockWeights w{};
+  w.adaln_b = f(0);
+  w.adaln_w = b->program == kProgContext ? nullptr : f(1);
+  w.k_norm = f(2);
+  w.w_out = f(3);
+  w.q_norm = f(4);
+  w.w_qkv = f(5);
+  w.attn_norm1 = f(6);
+  w.attn_norm2 = f(7);
+  w.w_13 = f(8);
+  w.w_2 = f(9);
+  w.ffn_norm1 = f(11);
+  w.ffn_norm2 = f(12);
+  return w;
+}
+
+// One-shot faults of the runtime config, taken in execution order
+// (reactor_concept_model_block_abi.c:184-202).  Returns the failing detail, or 0.
+int32_t take_phase_fault(Runtime* rt, bool* unobserved) {
+  *unobserved = false;
+  if (rt->reduction_test_flags & PROM_REDUCTION_TESTCFG_FAIL_COMMAND_RECORD) {
+    rt->reduction_test_flags &= ~(uint32_t)PROM_REDUCTION_TESTCFG_FAIL_COMMAND_RECORD;
+    return PROM_MODEL_BLOCK_DETAIL_COMMAND_RECORD_FAILED;
+  }
+  if (rt->reduction_test_flags & PROM_REDUCTION_TESTCFG_FAIL_QUEUE_SUBMIT) {
+    rt->reduction_test_flags &= ~(uint32_t)PROM_REDUCTION_TESTCFG_FAIL_QUEUE_SUBMIT;
+    return PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
+  }
+  if (rt->reduction_test_flags & PROM_REDUCTION_TESTCFG_FAIL_COMPLETION_OBSERVATION) {
+    rt->reduction_test_flags &= ~(uint32_t)PROM_REDUCTION_TESTCFG_FAIL_COMPLETION_OBSERVATION;
+    *unobserved = true;
+  }
+  return 0;
+}
+
+// Runs the Z-Image block of b on x -> out (or stops at an audit point), timing
+// it with events.  Returns 0 or a model-block detail; an injected unobserved
+// completion leaves the work queued and quarantines the block.
+int32_t run_block(Runtime* rt, ModelBlock* b, const float* x, float* out, int stop_after) {
+  bool unobserved = false;
+  const int32_t fault = take_phase_fault(rt, &unobserved);
+  if (fault != 0) return fault;
+  hipStream_t st = ctx().stream;
+  const ZImageBlockWeights w = weights_of(b);
+  (void)hipEventRecord(b->ev_begin, st);
+  uint32_t launches = 0;
+  if (enqueue_zimage_block_f32(w, x, b->cond, out, b->ws, b->ws_off, b->tokens, kWidth, kFfn, kEps, st, &launches,
+                               stop_after) != hipSuccess) {
+    (void)hipStreamSynchronize(st);
+    return PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
+  }
+  (void)hipEventRecord(b->ev_end, st);
+  if (unobserved) {
+    b->quarantined = true;
+    return PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
+  }
+  if (hipStreamSynchronize(st) != hipSuccess) return PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, b->ev_begin, b->ev_end) == hipSuccess) b->gpu_compute_ns = (uint64_t)(ms * 1.0e6);
+  b->gpu_total_ns = b->gpu_compute_ns;
+  return 0;
+}
+
+// Allocates everything a block executes with (create time; executions never allocate).
+bool alloc_block_buffers(ModelBlock* b) {
+  uint64_t max_weight = 0;
+  for (uint32_t i = 0; i < b->weight_count; ++i) max_weight = std::max(max_weight, b->decl[i].byte_count);
+  b->staging_bytes = max_weight;
+  if (hipEventCreate(&b->ev_begin) != hipSuccess || hipEventCreate(&b->ev_end) != hipSuccess) return false;
+  if (b->program == kProgProof) {
+    const bool ok = alloc_dev(b, reinterpret_cast<void**>(&b->proof_in), b->ext_in) &&
+                    alloc_dev(b, reinterpret_cast<void**>(&b->proof_out), b->ext_out) &&
+                    alloc_dev(b, reinterpret_cast<void**>(&b->proof_audit), b->declared_audit) &&
+                    alloc_dev(b, &b->staging, max_weight);
+    b->reusable_bytes = b->ext_in + b->ext_out + max_weight;
+    b->audit_alloc_bytes = b->declared_audit;
+    b->pipelines = 1;
+    return ok && alloc_set(b, &b->active);
+  }
+  const int T = b->tokens;
+  const size_t act = (size_t)T * kWidth * 4;
+  const size_t ws_bytes = zimage_workspace_layout(T, kWidth, kHeads, kFfn, b->ws_off);
+  const bool ok = alloc_dev(b, &b->staging, max_weight) && alloc_dev(b, reinterpret_cast<void**>(&b->x), act) &&
+                  alloc_dev(b, reinterpret_cast<void**>(&b->out), act) &&
+                  alloc_dev(b, reinterpret_cast<void**>(&b->x_bf16), (size_t)T * kWidth * 2) &&
+                  alloc_dev(b, reinterpret_cast<void**>(&b->cond_bf16), kZImageConditionWidth * 2) &&
+                  alloc_dev(b, reinterpret_cast<void**>(&b->cond), kZImageConditionWidth * 4) &&
+                  alloc_dev(b, reinterpret_cast<void**>(&b->coords), (size_t)T * 3 * 4) &&
+                  alloc_dev(b, reinterpret_cast<void**>(&b->ws), ws_bytes);
+  b->reusable_bytes = max_weight + 2 * act + (uint64_t)T * kWidth * 2 + kZImageConditionWidth * 6 +
+                      (uint64_t)T * 12 + ws_bytes;
+  b->audit_alloc_bytes = 0;  // audits copy workspace stages directly
+  b->pipelines = 13;         // the fixed kernel chain of the block
+  if (!ok || !alloc_set(b, &b->active)) return false;
+  // Coordinates and the RoPE table are fixed per program: build them once.
+  hipStream_t st = ctx().stream;
+  const int image = b->program == kProgContext ? 0 : kImageTokens;
+  const int context = b->program == kProgNoise ? 0 : kContextTokens;
+  hipLaunchKernelGGL(coords_kernel, dim3((T + 255) / 256), dim3(256), 0, st, b->coords, image, context);
+  if (hipGetLastError() != hipSuccess) return false;
+  if (launch_zimage_rope_table(b->coords, reinterpret_cast<float2*>(b->ws + b->ws_off[kZRope]), T, st) != hipSuccess)
+    return false;
+  return hipStreamSynchronize(st) == hipSuccess;
+}
+
+// ---------------------------------------------------------------- create
+
+int create_block(Runtime* rt, const PrometheusModelBlockCreateRequest* r, uint64_t* out_id,
+                 PrometheusModelBlockEvidence* ev) {
+  if (out_id) *out_id = 0;
+  if (!validate_create(r) || out_id == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelState* ms = rt->available ? state_of(rt) : nullptr;
+  if (ms == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = &ms->block;
+  if (b->created) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_ALREADY_CREATED, ev);
+    return PROM_ERROR;
+  }
+  *b = ModelBlock{};
+  if (r->assembly_family == PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO) {
+    b->program = kProgContext;
+    b->tokens = kContextTokens;
+  } else if (r->assembly_family == PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO) {
+    b->program = kProgMain;
+    b->tokens = kJointTokens;
+  } else if (r->shader_id == kShaderNoise) {
+    b->program = kProgNoise;
+    b->tokens = kImageTokens;
+  } else {
+    b->program = kProgProof;
+  }
+  b->family = r->assembly_family;
+  b->parameter_set = r->parameter_set;
+  b->aggregate = r->parameter_set_aggregate_identity;
+  b->model_contract = r->model_contract_identity;
+  b->weight_identity = r->weight_identity;
+  b->shader_portfolio = r->shader_portfolio_identity;
+  b->precision = r->precision_policy_identity;
+  b->capability = r->capability_route_identity;
+  b->memory_ceiling = r->memory_ceiling_bytes;
+  b->ext_in = r->external_input_bytes;
+  b->ext_out = r->external_output_bytes;
+  b->declared_audit = r->audit_bytes;
+  b->shader_id = r->shader_id;
+  b->weight_count = r->weight_count;
+  b->step_count = r->step_count;
+  memcpy(b->steps, r->steps, sizeof(b->steps));
+  memcpy(b->decl, r->weights, sizeof(b->decl));
+  if ((rt->test_flags & PROM_TESTCFG_FAIL_BUFFER_ALLOC) != 0u || !alloc_block_buffers(b)) {
+    release_block(b);
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED, ev);
+    return PROM_ERROR;
+  }
+  b->created = true;
+  b->id = ms->next_block_id++;
+  b->plan_identity = plan_identity(b);
+  *out_id = b->id;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+ModelBlock* find_block(Runtime* rt, uint64_t id) {
+  if (rt->model == nullptr || !rt->model->block.created || rt->model->block.id != id) return nullptr;
+  return &rt->model->block;
+}
+
+int upload_weights(Runtime* rt, uint64_t id, const PrometheusModelBlockWeightUpload* uploads, uint32_t count,
+                   PrometheusModelBlockEvidence* ev) {
+  if (uploads == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  if (!reap(b)) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN, ev);
+    return PROM_ERROR;
+  }
+  if (b->binding_valid || count != b->weight_count) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_WEIGHT_MISMATCH);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  if ((rt->test_flags & PROM_TESTCFG_FAIL_UPLOAD) != 0u) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_UPLOAD_FAILED);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  if (!upload_matches(b, uploads, count, nullptr)) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_WEIGHT_MISMATCH);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  if (!change_weights(rt, b, uploads, count, false)) {
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// Facade create of the lock-selected ContextRefiner / MainTransformer: the
+// closed create request is derived from the lock, then the initial payload
+// binds atomically (reactor_vulkan_model_block.c:2305-2462).
+int facade_create(Runtime* rt, const PrometheusContextRefinerCreateRequest* r, uint64_t* out_id,
+                  PrometheusModelBlockEvidence* ev, bool main) {
+  PrometheusModelBlockCreateRequest c;
+  memset(&c, 0, sizeof(c));
+  c.struct_size = sizeof(c);
+  const uint32_t count = main ? 13u : 11u;
+  for (uint32_t i = 0; i < count; ++i) {
+    c.weights[i].content_identity = r->uploads[i].content_identity;
+    c.weights[i].layout_identity = r->uploads[i].layout_identity;
+    c.weights[i].byte_count = r->uploads[i].byte_count;
+  }
+  c.weight_count = count;
+  c.step_count = PROM_MODEL_BLOCK_MAX_STEPS;
+  memcpy(c.steps, kSteps, sizeof(c.steps));
+  c.audit_bytes = PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES;
+  if (main) {
+    c.assembly_family = PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO;
+    c.parameter_set = r->model_local_block_id + 1u;
+    c.parameter_set_aggregate_identity = kMainAggregate[r->model_local_block_id];
+    c.model_contract_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.weight_identity = c.parameter_set_aggregate_identity;
+    c.shader_portfolio_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.precision_policy_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.capability_route_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.memory_ceiling_bytes = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.shader_id = kShaderMain;
+  } else {
+    c.assembly_family = PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO;
+    c.parameter_set = PROM_CONTEXT_REFINER_PARAMETER_SET_0;
+    c.parameter_set_aggregate_identity = kContextAggregate[0];
+    c.model_contract_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.weight_identity = kContextAggregate[0];
+    c.shader_portfolio_identity = kContextExecutionPlan;
+    c.precision_policy_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.capability_route_identity = kContextCanonical[0];
+    c.memory_ceiling_bytes = kContextMemoryPlan;
+    c.external_input_bytes = (uint64_t)kContextTokens * kWidth * 4;
+    c.shader_id = kShaderContext;
+  }
+  if (create_block(rt, &c, out_id, ev) != PROM_OK) return PROM_ERROR;
+  if (upload_weights(rt, *out_id, r->uploads, r->upload_count, ev) != PROM_OK) {
+    release_block(&rt->model->block);
+    *out_id = 0;
+    return PROM_ERROR;
+  }
+  return PROM_OK;
+}
+
+// Rebind to the next parameter set of the same family (replacement binding).
+int rebind(Runtime* rt, uint64_t id, ModelBlock* b, const PrometheusModelBlockWeightUpload* uploads, uint32_t count,
+           const uint64_t* sizes, uint32_t new_set, uint64_t new_aggregate, PrometheusModelBlockEvidence* ev) {
+  (void)id;
+  if (!upload_matches(b, uploads, count, sizes)) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_WEIGHT_MISMATCH, ev);
+    return PROM_ERROR;
+  }
+  if (!change_weights(rt, b, uploads, count, true)) {
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  b->parameter_set = new_set;
+  b->aggregate = new_aggregate;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// Copies stage `count` floats (rows x cols with source pitch) of the last
+// execution to the host.
+bool copy_out(float* dst, const float* src, size_t rows, size_t cols, size_t src_ld) {
+  hipStream_t st = ctx().stream;
+  hipError_t e;
+  if (cols == src_ld)
+    e = hipMemcpyAsync(dst, src, rows * cols * 4, hipMemcpyDeviceToHost, st);
+  else
+    e = hipMemcpy2DAsync(dst, cols * 4, src, src_ld * 4, cols * 4, rows, hipMemcpyDeviceToHost, st);
+  return e == hipSuccess && hipStreamSynchronize(st) == hipSuccess;
+}
+
+uint64_t audit_elements(uint32_t family, uint32_t stage, int T) {
+  const uint64_t model = (uint64_t)T * kWidth;
+  if (family == PROM_NOISE_REFINER_AUDIT_M1B) {
+    if (stage == 3) return 4ull * kWidth;
+    if (stage == 14) return (uint64_t)T * 3 * kWidth;
+    if (stage == 2) return kZImageConditionWidth;
+    if (stage >= 4 && stage <= 11) return kWidth;
+    return model;
+  }
+  if (family == PROM_NOISE_REFINER_AUDIT_M1D && (stage == 3 || stage == 4 || stage == 5)) return (uint64_t)T * kFfn;
+  return model;
+}
+
+// Copies one stage of the completed (or stopped) chain to the host
+// (stage numbering: reactor_api.h:776-797, 988-992, 1085-1093).
+bool copy_stage(ModelBlock* b, uint32_t family, uint32_t stage, float* dst) {
+  const int T = b->tokens, H = kHeads, D = kWidth;
+  hipStream_t st = ctx().stream;
+  char* ws = b->ws;
+  auto W = [&](int k) { return reinterpret_cast<float*>(ws + b->ws_off[k]); };
+  const ZImageBlockWeights w = weights_of(b);
+  const float2* tab = reinterpret_cast<const float2*>(ws + b->ws_off[kZRope]);
+  float* scratch = W(kZO);  // free before attention (M1B) and reused only for audits
+  if (family == PROM_NOISE_REFINER_AUDIT_M1B) {
+    switch (stage) {
+      case 1: return copy_out(dst, b->x, T, D, D);
+      case 2: return copy_out(dst, b->cond, 1, kZImageConditionWidth, kZImageConditionWidth);
+      case 3: return copy_out(dst, W(kZModRaw), 1, 4 * D, 4 * D);
+      case 4: case 6: case 8: case 10: return copy_out(dst, W(kZModRaw) + (stage - 4) / 2 * D, 1, D, D);
+      case 5: case 7: case 9: case 11: return copy_out(dst, W(kZMod) + (stage - 5) / 2 * D, 1, D, D);
+      case 12:
+        return launch_zimage_norm(b->x, w.attn_norm1, scratch, T, D, kEps, st) == hipSuccess &&
+               copy_out(dst, scratch, T, D, D);
+      case 13: return copy_out(dst, W(kZA), T, D, D);
+      case 14: return copy_out(dst, W(kZQkv), T, 3 * D, 3 * D);
+      case 15: case 16: case 17: return copy_out(dst, W(kZQkv) + (stage - 15) * D, T, D, 3 * D);
+      case 18: case 19: case 20: case 21: {
+        const int which = (stage == 18 || stage == 20) ? 0 : 1;
+        const bool rope = stage >= 20;
+        return launch_zimage_qk_audit(W(kZQkv), tab, which ? w.k_norm : w.q_norm, scratch, T, H, kEps, which, rope,
+                                      st) == hipSuccess &&
+               copy_out(dst, scratch, T, D, D);
+      }
+      default: return false;
+    }
+  }
+  if (family == PROM_NOISE_REFINER_AUDIT_M1C) {
+    if (stage == 1) return copy_out(dst, W(kZO), T, D, D);
+    if (stage == 2) return copy_out(dst, W(kZProj), T, D, D);
+    if (stage == 3) return copy_out(dst, W(kZR), T, D, D);
+    return false;
+  }
+  switch (stage) {  // M1D
+    case 1:
+      return launch_zimage_norm(W(kZR), w.ffn_norm1, W(kZA), T, D, kEps, st) == hipSuccess &&
+             copy_out(dst, W(kZA), T, D, D);
+    case 2: return copy_out(dst, W(kZF), T, D, D);
+    case 3: return copy_out(dst, W(kZG), T, kFfn, 2 * kFfn);
+    case 4: return copy_out(dst, W(kZG) + kFfn, T, kFfn, 2 * kFfn);
+    case 5: return copy_out(dst, W(kZH), T, kFfn, kFfn);
+    case 6: return copy_out(dst, W(kZW2), T, D, D);
+    case 7: return copy_out(dst, b->out, T, D, D);
+    default: return false;
+  }
+}
+
+// ---------------------------------------------------------------- NoiseRefiner
+
+// External BF16 ingress of parameter set `required_set`
+// (reactor_vulkan_model_block.c:2204-2289).
+int noise_external(Runtime* rt, uint64_t id, const PrometheusNoiseRefiner0ExecuteRequest* r, uint32_t required_set,
+                   PrometheusModelBlockEvidence* ev) {
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->model_input_bf16 == nullptr || r->timestep_bf16 == nullptr ||
+      r->model_input_bytes != (uint64_t)kImageTokens * kWidth * 2 || r->timestep_bytes != kZImageConditionWidth * 2 ||
+      r->input_identity == 0 || r->timestep_identity == 0 || r->output_identity == 0 || r->audit_enabled != 0) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr || b->family != PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO || b->parameter_set != required_set ||
+      binding_state(b) != PROM_NOISE_REFINER_BINDING_BOUND) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_PARAMETER_SET_MISMATCH, ev);
+    return PROM_ERROR;
+  }
+  if (!reap(b)) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  b->resident_input_generation = 0;  // an external ingress starts a new chain
+  b->output_valid = false;
+  b->audit_valid = false;
+  const uint64_t t0 = wall_ns();
+  hipStream_t st = ctx().stream;
+  if (hipMemcpyAsync(b->x_bf16, r->model_input_bf16, (size_t)r->model_input_bytes, hipMemcpyHostToDevice, st) !=
+          hipSuccess ||
+      hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st) !=
+          hipSuccess ||
+      launch_widen_bf16(b->x_bf16, b->x, (size_t)kImageTokens * kWidth, st) != hipSuccess ||
+      launch_widen_bf16(b->cond_bf16, b->cond, kZImageConditionWidth, st) != hipSuccess) {
+    (void)hipStreamSynchronize(st);
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_INGRESS_DISPATCH_FAILED);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  const int32_t d = run_block(rt, b, b->x, b->out, 0);
+  if (d != 0) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  }
+  b->prefix_replay = hash_u64(hash_u64(hash_u64(hash_u64(b->family, b->parameter_set), b->binding_generation),
+                                       r->input_identity),
+                              r->timestep_identity);
+  b->replay_identity = hash_u64(hash_u64(b->prefix_replay, r->output_identity), 3u);
+  b->replay_identity = hash_u64(hash_u64(b->replay_identity, r->output_identity), 7u);
+  b->output_valid = true;
+  b->output_generation += 1;
+  b->executions += 3;
+  b->last_execution_ns = wall_ns() - t0;
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// Resident chain execution of parameter set 1 (reactor_vulkan_model_block.c:3274-3400).
+int noise_resident(Runtime* rt, uint64_t id, const PrometheusNoiseRefinerResidentExecuteRequest* r,
+                   PrometheusModelBlockEvidence* ev) {
+  const bool bad_shape =
+      r == nullptr || r->struct_size != sizeof(*r) || r->input_generation == 0 || r->output_identity == 0 ||
+      r->audit_enabled > 1u ||
+      (r->audit_enabled == 0 && (r->audit_family != PROM_NOISE_REFINER_AUDIT_NONE || r->audit_stage != 0 ||
+                                 r->audit_output != nullptr || r->audit_element_capacity != 0)) ||
+      (r->audit_enabled != 0 && (r->audit_family < PROM_NOISE_REFINER_AUDIT_M1B ||
+                                 r->audit_family > PROM_NOISE_REFINER_AUDIT_M1D || r->audit_output == nullptr));
+  if (bad_shape) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  const uint32_t fam = r->audit_enabled ? r->audit_family : 0u;
+  const uint32_t stage = r->audit_stage;
+  if ((fam == PROM_NOISE_REFINER_AUDIT_M1B && (stage < 1 || stage > 21)) ||
+      (fam == PROM_NOISE_REFINER_AUDIT_M1C && (stage < 1 || stage > 3)) ||
+      (fam == PROM_NOISE_REFINER_AUDIT_M1D && (stage < 1 || stage > 7)) ||
+      (fam != 0 && r->audit_element_capacity < audit_elements(fam, stage, kImageTokens))) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  const bool first = b->resident_input_generation == 0;
+  if (b->family != PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO || b->parameter_set != PROM_NOISE_REFINER_PARAMETER_SET_1 ||
+      binding_state(b) != PROM_NOISE_REFINER_BINDING_BOUND ||
+      (first ? r->input_generation != b->output_generation : r->input_generation != b->resident_input_generation) ||
+      !reap(b)) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  b->output_valid = false;
+  b->audit_valid = false;
+  b->prefix_replay =
+      hash_u64(hash_u64(hash_u64(b->family, b->parameter_set), b->binding_generation), r->input_generation);
+  const uint64_t t0 = wall_ns();
+  hipStream_t st = ctx().stream;
+  // The first resident execution takes the predecessor's resident output as
+  // its boundary input; later ones re-run that same boundary.
+  if (first && hipMemcpyAsync(b->x, b->out, (size_t)kImageTokens * kWidth * 4, hipMemcpyDeviceToDevice, st) !=
+                   hipSuccess) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  const int stop = fam == PROM_NOISE_REFINER_AUDIT_M1B ? 1 : (fam == PROM_NOISE_REFINER_AUDIT_M1C ? 2 : 0);
+  const int32_t d = run_block(rt, b, b->x, b->out, stop);
+  if (d != 0) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  }
+  if (fam != 0) {
+    if (!copy_stage(b, fam, stage, r->audit_output)) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+      fill_evidence(b, b->last_detail, ev);
+      return PROM_ERROR;
+    }
+    b->audit_valid = true;
+  }
+  if (stop != 0) {  // a stage audit ends the chain early and publishes no output
+    b->executions += stop;
+    b->last_execution_ns = wall_ns() - t0;
+    b->replay_identity = hash_u64(b->prefix_replay, stage);
+    b->last_detail = 0;
+    fill_evidence(b, 0, ev);
+    return PROM_OK;
+  }
+  if (first) b->resident_input_generation = r->input_generation;
+  b->output_valid = true;
+  b->output_generation += 1;
+  b->executions += 3;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(hash_u64(b->prefix_replay, r->output_identity), b->aggregate);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// Final audit egress of a completed resident output (reactor_vulkan_model_block.c:3402-3460).
+int audit_final(Runtime* rt, uint64_t id, const PrometheusNoiseRefinerFinalAuditRequest* r, Program program,
+                PrometheusModelBlockEvidence* ev) {
+  const int T = program == kProgNoise ? kImageTokens : (program == kProgContext ? kContextTokens : kJointTokens);
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->output == nullptr || r->output_identity == 0 ||
+      r->required_output_generation == 0 || r->output_element_capacity < (uint64_t)T * kWidth) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  if (b->program != program || !b->output_valid || b->output_generation != r->required_output_generation ||
+      !reap(b)) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  const uint64_t t0 = wall_ns();
+  if ((rt->test_flags & PROM_TESTCFG_FAIL_DOWNLOAD) != 0u || !copy_out(r->output, b->out, T, kWidth, kWidth)) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  b->last_readback_ns = wall_ns() - t0;
+  b->audit_valid = true;
+  b->replay_identity = hash_u64(b->replay_identity, r->output_identity);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// ---------------------------------------------------------------- ContextRefiner
+
+// reactor_vulkan_model_block.c:2510-2583
+int context_execute(Runtime* rt, uint64_t id, uint32_t required_set, const float* input, uint64_t input_bytes,
+                    uint64_t input_generation, uint64_t input_identity, uint64_t output_identity,
+                    uint32_t audit_enabled, bool resident, PrometheusModelBlockEvidence* ev) {
+  if (output_identity == 0 || audit_enabled != 0 ||
+      (!resident && (input == nullptr || input_identity == 0 ||
+                     input_bytes != (uint64_t)kContextTokens * kWidth * 4))) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  if (!reap(b)) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN, ev);
+    return PROM_ERROR;
+  }
+  const bool first = resident && b->resident_input_generation == 0;
+  if (b->program != kProgContext || b->parameter_set != required_set ||
+      binding_state(b) != PROM_NOISE_REFINER_BINDING_BOUND ||
+      (resident && (input_generation == 0 || (first ? input_generation != b->output_generation
+                                                    : input_generation != b->resident_input_generation)))) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  if ((uint32_t)(b->output_generation + 1u) == 0u) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  b->output_valid = false;
+  b->audit_valid = false;
+  const uint64_t t0 = wall_ns();
+  hipStream_t st = ctx().stream;
+  const size_t bytes = (size_t)kContextTokens * kWidth * 4;
+  hipError_t e = hipSuccess;
+  if (!resident) e = hipMemcpyAsync(b->x, input, bytes, hipMemcpyHostToDevice, st);
+  else if (first) e = hipMemcpyAsync(b->x, b->out, bytes, hipMemcpyDeviceToDevice, st);
+  if (e != hipSuccess) {
+    mark_failure(b, PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED);
+    fill_evidence(b, b->last_detail, ev);
+    return PROM_ERROR;
+  }
+  const int32_t d = run_block(rt, b, b->x, b->out, 0);
+  if (d != 0) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  }
+  b->output_valid = true;
+  b->output_generation += 1;
+  if (first) b->resident_input_generation = input_generation;
+  b->executions += 1;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(b->plan_identity, resident ? input_generation : input_identity);
+  b->replay_identity = hash_u64(b->replay_identity, output_identity);
+  b->replay_identity = hash_u64(b->replay_identity, b->aggregate);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// ---------------------------------------------------------------- session
+
+bool joint_valid(const ModelSession* s) {
+  return s->streams[2].valid && !s->joint_writing && s->streams[0].valid && s->streams[1].valid &&
+         s->joint_image_generation == s->streams[0].generation &&
+         s->joint_context_generation == s->streams[1].generation;
+}
+
+ModelSession* find_session(Runtime* rt, uint64_t id) {
+  if (rt->model == nullptr || !rt->model->session.created || rt->model->session.id != id) return nullptr;
+  return &rt->model->session;
+}
+
+}  // namespace
+
+void model_release(Runtime* rt) {
+  if (rt == nullptr || rt->model == nullptr) return;
+  std::lock_guard<std::mutex> lock(ctx().mu);
+  release_block(&rt->model->block);
+  release_session(&rt->model->session);
+  delete rt->model;
+  rt->model = nullptr;
+}
+
+}  // namespace prom
+
+using namespace prom;
+
+namespace {
+
+// Runs `body` with the device context locked and the handle resolved; an
+// unknown handle reports the invalid-request evidence.
+template <typename F>
+int with_runtime(void* handle, PrometheusModelBlockEvidence* ev, F body) {
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  std::lock_guard<std::mutex> lock(ctx().mu);
+  return body(rt);
+}
+
+template <typename F>
+int with_session_runtime(void* handle, PrometheusCompiledModelSessionEvidence* ev, F body) {
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) {
+    fill_session_evidence(nullptr, ev, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+    return PROM_ERROR;
+  }
+  std::lock_guard<std::mutex> lock(ctx().mu);
+  return body(rt);
+}
+
+}  // namespace
+
+extern "C" {
+
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_create(void* handle,
+                                                                   const PrometheusModelBlockCreateRequest* request,
+                                                                   uint64_t* out_block_id,
+                                                                   PrometheusModelBlockEvidence* out_evidence) {
+  if (out_block_id) *out_block_id = 0;
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return create_block(rt, request, out_block_id, out_evidence); });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_upload_weights(
+    void* handle, uint64_t block_id, const PrometheusModelBlockWeightUpload* uploads, uint32_t upload_count,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    return upload_weights(rt, block_id, uploads, upload_count, out_evidence);
+  });
+}
+
+// reactor_vulkan_model_block.c:1884-1953: the resident proof program.
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute(void* handle, uint64_t block_id,
+                                                                    const PrometheusModelBlockExecuteRequest* request,
+                                                                    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusModelBlockExecuteRequest* r = request;
+    if (r == nullptr || r->struct_size != sizeof(*r) || r->input == nullptr || r->output == nullptr ||
+        r->input_identity == 0 || r->audit_enabled > 1u || r->element_count == 0 ||
+        r->element_count > UINT64_MAX / 4) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelBlock* b = find_block(rt, block_id);
+    if (b == nullptr) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, out_evidence);
+      return PROM_ERROR;
+    }
+    const uint64_t bytes = r->element_count * 4;
+    if (b->program != kProgProof || !b->binding_valid || bytes != b->ext_in || bytes != b->ext_out ||
+        r->element_count > 4194304u) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    if (!reap(b)) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    const uint64_t audit_n = b->declared_audit / 4;
+    if (r->audit_enabled && (r->audit_output == nullptr || r->audit_element_capacity * 4 < b->declared_audit)) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    b->output_valid = false;
+    b->audit_valid = false;
+    const uint64_t t0 = wall_ns();
+    bool unobserved = false;
+    const int32_t fault = take_phase_fault(rt, &unobserved);
+    if (fault != 0) {
+      mark_failure(b, fault);
+      fill_evidence(b, fault, out_evidence);
+      return PROM_ERROR;
+    }
+    hipStream_t st = ctx().stream;
+    (void)hipEventRecord(b->ev_begin, st);
+    hipError_t e = hipMemcpyAsync(b->proof_in, r->input, (size_t)bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) {
+      const unsigned blocks = (unsigned)std::min<uint64_t>(4096, (r->element_count + 255) / 256);
+      hipLaunchKernelGGL(proof_kernel, dim3(blocks), dim3(256), 0, st, b->proof_in, b->proof_out, r->element_count,
+                         b->proof_audit, r->audit_enabled ? std::min(audit_n, r->element_count) : 0ull);
+      e = hipGetLastError();
+    }
+    (void)hipEventRecord(b->ev_end, st);
+    if (e != hipSuccess) {
+      (void)hipStreamSynchronize(st);
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    if (unobserved) {
+      b->quarantined = true;
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    if ((rt->test_flags & PROM_TESTCFG_FAIL_DOWNLOAD) != 0u) {
+      (void)hipStreamSynchronize(st);
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    e = hipMemcpyAsync(r->output, b->proof_out, (size_t)b->ext_out, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess && r->audit_enabled)
+      e = hipMemcpyAsync(r->audit_output, b->proof_audit, (size_t)b->declared_audit, hipMemcpyDeviceToHost, st);
+    if (e != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, b->ev_begin, b->ev_end) == hipSuccess) b->gpu_compute_ns = (uint64_t)(ms * 1.0e6);
+    b->gpu_total_ns = b->gpu_compute_ns;
+    b->output_valid = true;
+    b->audit_valid = r->audit_enabled != 0;
+    b->executions += 1;
+    b->last_execution_ns = wall_ns() - t0;
+    b->replay_identity = hash_u64(hash_u64(b->plan_identity, r->input_identity), r->audit_enabled);
+    b->last_detail = 0;
+    fill_evidence(b, 0, out_evidence);
+    return PROM_OK;
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner0_execute(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefiner0ExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    return noise_external(rt, block_id, request, PROM_NOISE_REFINER_PARAMETER_SET_0, out_evidence);
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner1_execute(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefiner1ExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    return noise_external(rt, block_id, request, PROM_NOISE_REFINER_PARAMETER_SET_1, out_evidence);
+  });
+}
+
+// reactor_vulkan_model_block.c:1831-1882
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_rebind(void* handle, uint64_t block_id,
+                                                                     const PrometheusNoiseRefinerRebindRequest* request,
+                                                                     PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusNoiseRefinerRebindRequest* r = request;
+    if (r == nullptr || r->struct_size != sizeof(*r) || r->uploads == nullptr || r->upload_count != 13u ||
+        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID || r->model_local_block_id != 1u) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelBlock* b = find_block(rt, block_id);
+    if (b == nullptr) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, out_evidence);
+      return PROM_ERROR;
+    }
+    if (b->family != PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO || b->parameter_set != PROM_NOISE_REFINER_PARAMETER_SET_0 ||
+        !b->binding_valid) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    return rebind(rt, block_id, b, r->uploads, 13u, kNoiseWeightBytes, PROM_NOISE_REFINER_PARAMETER_SET_1,
+                  kNoiseAggregate[1], out_evidence);
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_execute_resident(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefinerResidentExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return noise_resident(rt, block_id, request, out_evidence); });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_audit_final(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefinerFinalAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return audit_final(rt, block_id, request, kProgNoise, out_evidence); });
+}
+
+// reactor_vulkan_model_block.c:2305-2367
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_create(
+    void* handle, const PrometheusContextRefinerCreateRequest* request, uint64_t* out_block_id,
+    PrometheusModelBlockEvidence* out_evidence) {
+  if (out_block_id) *out_block_id = 0;
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusContextRefinerCreateRequest* r = request;
+    if (r == nullptr || out_block_id == nullptr || r->struct_size != sizeof(*r) || r->uploads == nullptr ||
+        r->upload_count != 11u || r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID || r->model_local_block_id != 0u) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    return facade_create(rt, r, out_block_id, out_evidence, false);
+  });
+}
+
+// reactor_vulkan_model_block.c:2464-2508
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_rebind(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerRebindRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusContextRefinerRebindRequest* r = request;
+    if (r == nullptr || r->uploads == nullptr || r->struct_size != sizeof(*r) || r->upload_count != 11u ||
+        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID || r->model_local_block_id != 1u) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelBlock* b = find_block(rt, block_id);
+    if (b == nullptr) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, out_evidence);
+      return PROM_ERROR;
+    }
+    if (b->program != kProgContext || b->parameter_set != PROM_CONTEXT_REFINER_PARAMETER_SET_0 || !b->binding_valid) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    return rebind(rt, block_id, b, r->uploads, 11u, kContextWeightBytes, PROM_CONTEXT_REFINER_PARAMETER_SET_1,
+                  kContextAggregate[1], out_evidence);
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner0_execute(
+    void* handle, uint64_t block_id, const PrometheusContextRefiner0ExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    if (request == nullptr || request->struct_size != sizeof(*request)) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    return context_execute(rt, block_id, PROM_CONTEXT_REFINER_PARAMETER_SET_0, request->context_input,
+                           request->context_input_bytes, 0, request->input_identity, request->output_identity,
+                           request->audit_enabled, false, out_evidence);
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_execute_resident(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerResidentExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    if (request == nullptr || request->struct_size != sizeof(*request)) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    return context_execute(rt, block_id, PROM_CONTEXT_REFINER_PARAMETER_SET_1, nullptr, 0, request->input_generation,
+                           0, request->output_identity, request->audit_enabled, true, out_evidence);
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_audit_final(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerFinalAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return audit_final(rt, block_id, request, kProgContext, out_evidence); });
+}
+
+// reactor_vulkan_model_block.c:2369-2462: needs a session of the same lock.
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_create(
+    void* handle, const PrometheusMainTransformerCreateRequest* request, uint64_t* out_block_id,
+    PrometheusModelBlockEvidence* out_evidence) {
+  if (out_block_id) *out_block_id = 0;
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusMainTransformerCreateRequest* r = request;
+    if (r == nullptr || out_block_id == nullptr || r->struct_size != sizeof(*r) || r->uploads == nullptr ||
+        r->upload_count != 13u || r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID || r->model_local_block_id >= 30u) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    if (rt->model == nullptr || !rt->model->session.created || rt->model->session.lock != r->lock_identity) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    return facade_create(rt, r, out_block_id, out_evidence, true);
+  });
+}
+
+// reactor_vulkan_model_block.c:3833-3881: only the lock's immediate successor layer.
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_rebind(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerRebindRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusMainTransformerRebindRequest* r = request;
+    if (r == nullptr || r->uploads == nullptr || r->struct_size != sizeof(*r) || r->upload_count != 13u ||
+        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID || r->model_local_block_id >= 30u) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelBlock* b = find_block(rt, block_id);
+    if (b == nullptr) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, out_evidence);
+      return PROM_ERROR;
+    }
+    const uint32_t set = r->model_local_block_id + 1u;
+    if (b->program != kProgMain || set != b->parameter_set + 1u || !b->binding_valid) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    return rebind(rt, block_id, b, r->uploads, 13u, kNoiseWeightBytes, set, kMainAggregate[set - 1], out_evidence);
+  });
+}
+
+// reactor_vulkan_model_block.c:3883-4024
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusMainTransformerExecuteRequest* r = request;
+    if (r == nullptr || r->struct_size != sizeof(*r) || r->audit_enabled != 0 || r->resident_chain_mode > 1u ||
+        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID || r->timestep_bf16 == nullptr ||
+        r->timestep_bytes != kZImageConditionWidth * 2 || r->timestep_identity == 0 || r->output_identity == 0 ||
+        r->required_image_generation == 0 || r->required_context_generation == 0 ||
+        r->required_joint_generation == 0 || r->model_local_block_id >= 30u) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelBlock* b = find_block(rt, block_id);
+    if (b == nullptr) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, out_evidence);
+      return PROM_ERROR;
+    }
+    if (!reap(b)) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelSession* s = &rt->model->session;
+    const uint32_t set = r->model_local_block_id + 1u;
+    if (b->program != kProgMain || b->parameter_set != set || b->aggregate != kMainAggregate[set - 1] ||
+        binding_state(b) != PROM_NOISE_REFINER_BINDING_BOUND || !s->created || s->id != r->session_identity ||
+        s->lock != r->lock_identity || !s->streams[0].valid || !s->streams[1].valid || !joint_valid(s) ||
+        s->streams[0].generation != r->required_image_generation ||
+        s->streams[1].generation != r->required_context_generation ||
+        s->streams[2].generation != r->required_joint_generation) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    if (b->output_generation == UINT32_MAX || s->streams[2].generation == UINT64_MAX) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT, out_evidence);
+      return PROM_ERROR;
+    }
+    const bool chain = r->resident_chain_mode != 0;
+    if (chain) {  // PromSessionBeginJoint: the joint is being rewritten
+      s->streams[2].valid = false;
+      s->joint_writing = true;
+    }
+    b->output_valid = false;
+    b->audit_valid = false;
+    const uint64_t t0 = wall_ns();
+    hipStream_t st = ctx().stream;
+    hipError_t e = hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = launch_widen_bf16(b->cond_bf16, b->cond, kZImageConditionWidth, st);
+    b->last_memcpy_ns = wall_ns() - t0;
+    int32_t d = e == hipSuccess ? run_block(rt, b, s->buf[2], b->out, 0) : PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
+    if (d == 0 && chain &&
+        (hipMemcpyAsync(s->buf[2], b->out, (size_t)kStreamBytes[2], hipMemcpyDeviceToDevice, st) != hipSuccess ||
+         hipStreamSynchronize(st) != hipSuccess))
+      d = PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
+    if (d != 0) {
+      if (chain) {  // PromSessionEndJoint(commit = false)
+        s->joint_writing = false;
+        s->streams[2].valid = d != PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
+      }
+      mark_failure(b, d);
+      fill_evidence(b, d, out_evidence);
+      return PROM_ERROR;
+    }
+    if (chain) {  // PromSessionEndJoint(commit = true)
+      s->joint_writing = false;
+      s->streams[2] = Stream{s->streams[2].generation + 1, block_id, b->output_generation + 1, true};
+    }
+    b->output_valid = true;
+    b->output_generation += 1;
+    b->executions += 1;
+    b->last_execution_ns = wall_ns() - t0;
+    uint64_t h = hash_u64(r->lock_identity, r->session_identity);
+    h = hash_u64(h, r->required_image_generation);
+    h = hash_u64(h, r->required_context_generation);
+    h = hash_u64(h, r->required_joint_generation);
+    h = hash_u64(h, b->aggregate);
+    h = hash_u64(h, r->timestep_identity);
+    b->replay_identity = hash_u64(h, r->output_identity);
+    s->active_block_id = block_id;
+    s->binding_generation = b->binding_generation;
+    s->replay = hash_u64(s->replay, b->replay_identity);
+    b->last_detail = 0;
+    fill_evidence(b, 0, out_evidence);
+    return PROM_OK;
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_audit_final(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerFinalAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return audit_final(rt, block_id, request, kProgMain, out_evidence); });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_get_evidence(void* handle, uint64_t block_id,
+                                                                         PrometheusModelBlockEvidence* out_evidence) {
+  if (out_evidence == nullptr) return PROM_ERROR;
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    ModelBlock* b = find_block(rt, block_id);
+    if (b == nullptr) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, out_evidence);
+      return PROM_ERROR;
+    }
+    fill_evidence(b, b->last_detail, out_evidence);
+    return PROM_OK;
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_destroy(void* handle, uint64_t block_id) {
+  return with_runtime(handle, nullptr, [&](Runtime* rt) -> int {
+    ModelBlock* b = find_block(rt, block_id);
+    if (b == nullptr) return PROM_ERROR;
+    release_block(b);
+    return PROM_OK;
+  });
+}
+
+// reactor_vulkan_model_block.c:3654-3731
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_create(
+    void* handle, const PrometheusCompiledModelSessionCreateRequest* request, uint64_t* out_session_id,
+    PrometheusCompiledModelSessionEvidence* out_evidence) {
+  if (out_session_id) *out_session_id = 0;
+  return with_session_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusCompiledModelSessionCreateRequest* r = request;
+    if (r == nullptr || out_session_id == nullptr || r->struct_size != sizeof(*r) ||
+        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID ||
+        (r->execution_profile != PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY &&
+         r->execution_profile != PROM_MODEL_EXECUTION_PROFILE_PREFETCH) ||
+        (r->main_attention_route_policy < PROM_MAIN_ATTENTION_ROUTE_AUTO ||
+         r->main_attention_route_policy > PROM_MAIN_ATTENTION_ROUTE_SUBGROUP_OWNED32)) {
+      fill_session_evidence(nullptr, out_evidence, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    ModelState* ms = rt->available ? state_of(rt) : nullptr;
+    if (ms == nullptr || ms->session.created) {
+      fill_session_evidence(ms ? &ms->session : nullptr, out_evidence, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    ModelSession* s = &ms->session;
+    *s = ModelSession{};
+    for (int i = 0; i < 3; ++i) {
+      if ((rt->test_flags & PROM_TESTCFG_FAIL_BUFFER_ALLOC) != 0u ||
+          hipMalloc(reinterpret_cast<void**>(&s->buf[i]), (size_t)kStreamBytes[i]) != hipSuccess) {
+        s->buf[i] = nullptr;
+        for (float* p : s->buf) free_dev(p);
+        *s = ModelSession{};
+        fill_session_evidence(nullptr, out_evidence, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED);
+        return PROM_ERROR;
+      }
+    }
+    s->cold_allocations = 3;
+    s->lock = r->lock_identity;
+    s->requested_profile = r->execution_profile;
+    s->requested_route = r->main_attention_route_policy;
+    s->id = ms->next_session_id++;
+    s->created = true;
+    *out_session_id = s->id;
+    fill_session_evidence(s, out_evidence, 0);
+    return PROM_OK;
+  });
+}
+
+// reactor_vulkan_model_block.c:3733-3792: NoiseRefiner set 1 -> PreparedImage,
+// ContextRefiner set 1 -> PreparedContext (PrometheusModelBlock.concept:920-1000).
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_capture_completed(
+    void* handle, uint64_t session_id, uint64_t completed_block_id,
+    const PrometheusCompiledModelSessionCaptureRequest* request, PrometheusCompiledModelSessionEvidence* out_evidence) {
+  return with_session_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    if (request == nullptr || request->struct_size != sizeof(*request) || rt->model == nullptr) {
+      fill_session_evidence(nullptr, out_evidence, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    ModelSession* s = &rt->model->session;
+    ModelBlock* b = &rt->model->block;
+    if (!s->created || s->id != session_id || !b->created || b->id != completed_block_id || !b->output_valid ||
+        b->output_generation != request->source_output_generation || !reap(b)) {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_STALE_STREAM;
+      fill_session_evidence(s->created && s->id == session_id ? s : nullptr, out_evidence,
+                            PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    int role;
+    if (b->family == PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO && b->parameter_set == PROM_NOISE_REFINER_PARAMETER_SET_1)
+      role = 0;
+    else if (b->program == kProgContext && b->parameter_set == PROM_CONTEXT_REFINER_PARAMETER_SET_1)
+      role = 1;
+    else {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_STREAM_MISMATCH;
+      fill_session_evidence(s, out_evidence, 0);
+      return PROM_ERROR;
+    }
+    if (s->joint_writing || s->streams[role].generation == UINT64_MAX) {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_STALE_STREAM;
+      fill_session_evidence(s, out_evidence, 0);
+      return PROM_ERROR;
+    }
+    hipStream_t st = ctx().stream;
+    s->streams[role].valid = false;
+    if (hipMemcpyAsync(s->buf[role], b->out, (size_t)kStreamBytes[role], hipMemcpyDeviceToDevice, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_COMPLETION_UNCERTAIN;
+      fill_session_evidence(s, out_evidence, 0);
+      return PROM_ERROR;
+    }
+    s->streams[role] = Stream{s->streams[role].generation + 1, completed_block_id, b->output_generation, true};
+    s->active_block_id = completed_block_id;
+    s->binding_generation = b->binding_generation;
+    s->replay = hash_u64(s->replay == 0 ? s->lock : s->replay, completed_block_id);
+    s->replay = hash_u64(s->replay, s->streams[role].generation);
+    s->last_detail = 0;
+    fill_session_evidence(s, out_evidence, 0);
+    return PROM_OK;
+  });
+}
+
+// reactor_vulkan_model_block.c:3794-3831: JointWorking = PreparedImage | PreparedContext.
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_compose_joint(
+    void* handle, uint64_t session_id, const PrometheusCompiledModelSessionComposeRequest* request,
+    PrometheusCompiledModelSessionEvidence* out_evidence) {
+  return with_session_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    ModelSession* s = find_session(rt, session_id);
+    if (request == nullptr || request->struct_size != sizeof(*request) || s == nullptr) {
+      fill_session_evidence(nullptr, out_evidence, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    if (!reap(&rt->model->block)) {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_COMPLETION_UNCERTAIN;
+      fill_session_evidence(s, out_evidence, 0);
+      return PROM_ERROR;
+    }
+    const uint64_t ig = request->required_image_generation, cg = request->required_context_generation;
+    if (s->joint_writing || !s->streams[0].valid || !s->streams[1].valid || ig == 0 || cg == 0 ||
+        ig != s->streams[0].generation || cg != s->streams[1].generation || s->streams[2].generation == UINT64_MAX) {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_STALE_STREAM;
+      fill_session_evidence(s, out_evidence, 0);
+      return PROM_ERROR;
+    }
+    hipStream_t st = ctx().stream;
+    s->streams[2].valid = false;
+    char* joint = reinterpret_cast<char*>(s->buf[2]);
+    if (hipMemcpyAsync(joint, s->buf[0], (size_t)kStreamBytes[0], hipMemcpyDeviceToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(joint + kStreamBytes[0], s->buf[1], (size_t)kStreamBytes[1], hipMemcpyDeviceToDevice, st) !=
+            hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_COMPLETION_UNCERTAIN;
+      fill_session_evidence(s, out_evidence, 0);
+      return PROM_ERROR;
+    }
+    s->streams[2] = Stream{s->streams[2].generation + 1, 0, 0, true};
+    s->joint_image_generation = ig;
+    s->joint_context_generation = cg;
+    s->compositions += 1;
+    s->replay = hash_u64(s->replay, s->joint_image_generation);
+    s->replay = hash_u64(s->replay, s->joint_context_generation);
+    s->replay = hash_u64(s->replay, s->streams[2].generation);
+    s->last_detail = 0;
+    fill_session_evidence(s, out_evidence, 0);
+    return PROM_OK;
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_get_evidence(
+    void* handle, uint64_t session_id, PrometheusCompiledModelSessionEvidence* out_evidence) {
+  if (out_evidence == nullptr) return PROM_ERROR;
+  return with_session_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    ModelSession* s = find_session(rt, session_id);
+    if (s == nullptr) {
+      fill_session_evidence(nullptr, out_evidence, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    fill_session_evidence(s, out_evidence, 0);
+    return PROM_OK;
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_destroy(void* handle, uint64_t session_id) {
+  return with_session_runtime(handle, nullptr, [&](Runtime* rt) -> int {
+    ModelSession* s = find_session(rt, session_id);
+    if (s == nullptr || !reap(&rt->model->block)) return PROM_ERROR;
+    release_session(s);
+    return PROM_OK;
+  });
+}
+
+}  // extern "C"

@@ -23,6 +23,7 @@ constexpr uint32_t kEventSlots = 64;
 constexpr uint32_t kStagingSlots = 8;
 
 struct AsyncState;  // async task table, submission slots and batch arenas (sgemm_async.hip)
+struct ModelState;  // resident model block and compiled session (model_block.hip)
 
 struct Runtime {
   uint64_t magic;
@@ -38,6 +39,7 @@ struct Runtime {
   uint64_t m1_weight_generation;
   uint64_t m1_weight_hash;
   uint32_t m1_weight_width;
+  ModelState* model;  // created by the first model-block or session call
 };
 
 struct DeviceContext {
@@ -68,6 +70,8 @@ void* staging(uint32_t slot, size_t bytes);
 uint32_t async_outstanding(Runtime* rt);
 // Waits for the runtime's queued work and frees its async/batch resources.
 void async_release(Runtime* rt);
+// Frees the runtime's resident model block, session and their device memory.
+void model_release(Runtime* rt);
 
 inline void set_status(uint32_t* stage, int* detail, uint32_t s, int d) {
   if (stage) *stage = s;
@@ -84,6 +88,10 @@ hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m
 hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
                                uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
                                int* path_detail);
+// C_z = A_z @ B_z for z < batch, A_z = a + z*sa etc. (elements); no residual, no split-K.
+hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
+                                    float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
+                                    uint32_t batch, hipStream_t stream);
 hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, int ldb, float* c, uint16_t* cb,
                                int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
                                hipStream_t stream, int* path_detail);
@@ -103,5 +111,64 @@ hipError_t launch_row_reduction(const float* in, float* out, uint32_t rows, uint
                                 hipStream_t stream);
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, float* inv_rms, uint32_t tokens,
                           uint32_t width, uint32_t stride, float eps, hipStream_t stream);
+
+// ---- fp32 Z-Image transformer block on resident weights (zimage_f32.hip)
+constexpr int kZImageConditionWidth = 256;  // timestep embedding width (adaLN input)
+
+// Workspace buffers of one block execution (byte offsets from zimage_workspace_layout).
+enum ZImageWorkspace {
+  kZModRaw,  // [4D] adaLN projection before adjustment
+  kZMod,     // [4D] scaleA+1 | tanh gateA | scaleM+1 | tanh gateM
+  kZA,       // [T, D] RMSNorm(x; n1) * scaleA
+  kZQkv,     // [T, 3D]
+  kZQ,       // [H, T, 128] normalized, rotated, scaled by 1/sqrt(128)
+  kZKt,      // [H, 128, T] normalized, rotated, transposed
+  kZV,       // [H, T, 128]
+  kZS,       // [H, T, T] scores, then probabilities
+  kZO,       // [T, D] attention aggregation
+  kZProj,    // [T, D] attention projection
+  kZR,       // [T, D] attention residual
+  kZF,       // [T, D] RMSNorm(r; n3) * scaleM
+  kZG,       // [T, 2F] w1 | w3
+  kZH,       // [T, F] gated hidden
+  kZW2,      // [T, D]
+  kZRope,    // [T, 64] (cos, sin), filled by launch_zimage_rope_table
+  kZCount
+};
+
+struct ZImageBlockWeights {
+  const float* adaln_w;  // [256, 4D]; null for the unmodulated ContextRefiner
+  const float* adaln_b;  // [4D]
+  const float* attn_norm1;
+  const float* attn_norm2;
+  const float* ffn_norm1;
+  const float* ffn_norm2;  // [D] each
+  const float* q_norm;
+  const float* k_norm;  // [128] each
+  const float* w_qkv;   // [D, 3D]
+  const float* w_out;   // [D, D]
+  const float* w_13;    // [D, 2F]: w1 in columns [0, F), w3 in [F, 2F)
+  const float* w_2;     // [F, D]
+};
+
+size_t zimage_workspace_layout(int T, int D, int H, int F, size_t off[kZCount]);
+// dst[r * dst_ld + c] = (float) fp16 src[r * cols + c]
+hipError_t launch_widen_f16(const uint16_t* src, float* dst, size_t rows, size_t cols, size_t dst_ld,
+                            hipStream_t stream);
+hipError_t launch_widen_bf16(const uint16_t* src, float* dst, size_t n, hipStream_t stream);
+// coords [T, 3] (frame, row, column) -> workspace rope table
+hipError_t launch_zimage_rope_table(const float* coords, float2* tab, int T, hipStream_t stream);
+// One block: out = block(x); cond [256] is read only when w.adaln_w is set;
+// the workspace rope table must already hold this sequence's coordinates.
+// stop_after 1 ends after the Q/K/V split (pre-attention), 2 after the
+// attention residual and FFN input; 0 runs the whole block.
+hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x, const float* cond, float* out,
+                                    char* ws, const size_t off[kZCount], int T, int D, int F, float eps,
+                                    hipStream_t st, uint32_t* launches, int stop_after);
+// Audit recomputations: out = RMSNorm(x; w) (no modulation), and q or k
+// (which 0 / 1) after the head RMSNorm and optionally RoPE, [T, H*128].
+hipError_t launch_zimage_norm(const float* x, const float* w, float* out, int T, int D, float eps, hipStream_t stream);
+hipError_t launch_zimage_qk_audit(const float* qkv, const float2* tab, const float* norm_w, float* out, int T, int H,
+                                  float eps, int which, bool rope, hipStream_t stream);
 
 }  // namespace prom

@@ -154,6 +154,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_destroy(void* handle) {
     (void)hipStreamSynchronize(c.stream);
   }
   async_release(rt);
+  model_release(rt);
   rt->magic = 0;
   delete rt;
   return PROM_OK;

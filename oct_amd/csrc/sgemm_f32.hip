@@ -60,10 +60,17 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
                                                                 const float* __restrict__ B, float* C, int M,
                                                                 int N, int K, int tiles_m, int tiles_n, int lda,
                                                                 int ldb, int ldc, const float* R, int ldr,
-                                                                int k_len) {
+                                                                int k_len, long long sa, long long sb, long long sc) {
   __shared__ float As[2][kBK][kLdsA];
   __shared__ float Bs[2][kBK][kLdsB];
 
+  // Batched launches (gridDim.z > 1, never split-K): matrix z of A, B and C
+  // starts sa, sb and sc elements after the previous one.
+  if (gridDim.z > 1) {
+    A += (size_t)blockIdx.z * sa;
+    B += (size_t)blockIdx.z * sb;
+    C += (size_t)blockIdx.z * sc;
+  }
   int tm, tn;
   map_tile(tiles_m, tiles_n, &tm, &tn);
   const int row0 = tm * kBM;
@@ -337,13 +344,13 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
                    (size_t)(m + kBM) * lda * 4 < (1ull << 31) && ((size_t)k * ldb + n + kBN) * 4 < (1ull << 31);
   if (buf)
     hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, true>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len, 0ll, 0ll, 0ll);
   else if (vec)
     hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, false>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len, 0ll, 0ll, 0ll);
   else
     hipLaunchKernelGGL((sgemm_f32_mfma_kernel<false, false>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len);
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len, 0ll, 0ll, 0ll);
   if (splits > 1) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -353,6 +360,31 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
                        splits, residual, ldr);
   }
   if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_F32;
+  return hipGetLastError();
+}
+
+hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
+                                    float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
+                                    uint32_t batch, hipStream_t stream) {
+  if (batch == 0 || m == 0 || n == 0) return hipSuccess;
+  if (batch == 1) return launch_sgemm_f32_ex(a, lda, b, ldb, c, ldc, m, n, k, nullptr, 0, stream, nullptr);
+  const int tiles_m = (int)((m + kBM - 1) / kBM);
+  const int tiles_n = (int)((n + kBN - 1) / kBN);
+  const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
+                   (sb % 4 == 0) && aligned16(a) && aligned16(b);
+  // Per-matrix extents bound every buffer offset, as in the single launch.
+  const bool buf = vec && (k % kBK == 0) && (size_t)(m + kBM) * lda * 4 < (1ull << 31) &&
+                   ((size_t)k * ldb + n + kBN) * 4 < (1ull << 31);
+  const dim3 grid((unsigned)(tiles_m * tiles_n), 1u, batch);
+  if (buf)
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, true>), grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n,
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldc, (const float*)nullptr, 0, (int)k, sa, sb, sc);
+  else if (vec)
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, false>), grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n,
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldc, (const float*)nullptr, 0, (int)k, sa, sb, sc);
+  else
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<false, false>), grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n,
+                       (int)k, tiles_m, tiles_n, lda, ldb, ldc, (const float*)nullptr, 0, (int)k, sa, sb, sc);
   return hipGetLastError();
 }
 

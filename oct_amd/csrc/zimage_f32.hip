@@ -1,0 +1,323 @@
+// fp32 Z-Image transformer block on resident weights: the compute behind the
+// resident model-block ABI's NoiseRefiner, ContextRefiner and MainTransformer
+// families (model_block.hip).
+//
+// Stage definitions are the reference's canonical blocks:
+//   NoiseRefiner   internal/prometheus/zimage/canonical_reference.go:315-480
+//   ContextRefiner internal/prometheus/zimage/context_refiner_reference.go:230-311
+//                  (no adaLN: every scale and gate is 1)
+//   MainTransformer tools/python/zimage/zimage_main_transformer_canonical.py:178-277
+//                  (joint sequence, image tokens then context tokens)
+// with weights cached row-major [input, output] (canonical_reference.go:153-175)
+// and fp32 arithmetic throughout (FP16 weights are widened exactly once, at
+// upload).
+//
+// MI355X design: the matrix work is the fp32 MFMA SGEMM (sgemm_f32.hip);
+// attention is two batched SGEMMs over the heads (S_h = Q_h K_h^T with the
+// 1/sqrt(128) scale folded into Q, then O_h = softmax(S_h) V_h) around the
+// one-pass row softmax (reduction.hip).  Between them:
+//   adaln         m = c @ Wada + b; raw and adjusted (1 + scale, tanh gate)
+//   rope_table    (cos, sin) per token and pair, the reference's float32 angle
+//   norm_mod      a = RMSNorm(x; n1) * scaleA                    (block_rows.h)
+//   qkv_split     per (64 tokens, head): RMSNorm(q), RMSNorm(k), RoPE; writes
+//                 Q [H, T, 128], K^T [H, 128, T] (transposed through LDS so the
+//                 stores stay coalesced) and V [H, T, 128]
+//   resid_norm_mod r = x + gateA * RMSNorm(proj; n2), f = RMSNorm(r; n3) * scaleM
+//   swiglu        h = silu(w1) * w3
+//   final_resid   out = r + gateM * RMSNorm(w2; n4)
+// Every intermediate stays in its own workspace buffer, so any stage can be
+// copied out for an audit after the chain completes.
+#include <math.h>
+
+#include "block_rows.h"
+#include "reactor_internal.h"
+
+namespace prom {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHead = 128;
+constexpr int kSplitTokens = 64;  // tokens per qkv_split workgroup
+
+__global__ __launch_bounds__(256) void widen_f16_kernel(const uint16_t* __restrict__ src, float* __restrict__ dst,
+                                                        size_t rows, size_t cols, size_t dst_ld) {
+  const size_t total = rows * cols;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / cols, c = i - r * cols;
+    dst[r * dst_ld + c] = (float)__builtin_bit_cast(_Float16, src[i]);
+  }
+}
+
+__global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ src, float* __restrict__ dst,
+                                                         size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = __uint_as_float((uint32_t)src[i] << 16);
+}
+
+// raw[j] = b[j] + sum_k c[k] * W[k][j]; adjusted: chunks 0 and 2 -> 1 + raw,
+// chunks 1 and 3 -> tanh(raw) (canonical_reference.go:360-383).  A workgroup
+// owns 64 columns; its 4 waves take every 4th k and combine through LDS.
+__global__ __launch_bounds__(256) void adaln_f32_kernel(const float* __restrict__ cond, const float* __restrict__ W,
+                                                        const float* __restrict__ b, float* __restrict__ raw,
+                                                        float* __restrict__ mod, int C, int D) {
+  __shared__ float part[4][64];
+  const int lane = (int)(threadIdx.x & 63);
+  const int kg = (int)(threadIdx.x >> 6);
+  const int j = (int)blockIdx.x * 64 + lane;
+  float acc = 0.0f;
+  if (j < 4 * D) {
+    for (int k = kg; k < C; k += 4) acc += cond[k] * W[(size_t)k * 4 * D + j];
+  }
+  part[kg][lane] = acc;
+  __syncthreads();
+  if (kg == 0 && j < 4 * D) {
+    const float m = b[j] + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+    const int chunk = j / D;
+    raw[j] = m;
+    mod[j] = (chunk == 0 || chunk == 2) ? 1.0f + m : (float)tanh((double)m);
+  }
+}
+
+// tab[t][p] = (cos, sin) of angle = coord(float32) * freq(float32), with
+// freq = float32(1 / 256^(2*pair/width)) and cos/sin evaluated in binary64 on
+// the float32 angle: CanonicalRopeFrequency/CanonicalRopeRotate
+// (zimage/canonical_contract.go:66-87), axes [32, 48, 48].
+__global__ __launch_bounds__(256) void rope_table_f32_kernel(const float* __restrict__ coords, float2* __restrict__ tab,
+                                                             int T) {
+  const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (idx >= T * 64) return;
+  const int t = idx >> 6;
+  const int p = idx & 63;
+  int axis, width, pair;
+  if (p < 16) {
+    axis = 0; width = 32; pair = p;
+  } else if (p < 40) {
+    axis = 1; width = 48; pair = p - 16;
+  } else {
+    axis = 2; width = 48; pair = p - 40;
+  }
+  const float freq = (float)(1.0 / pow(256.0, (double)(2 * pair) / (double)width));
+  const float angle = coords[(size_t)t * 3 + axis] * freq;
+  tab[idx] = make_float2((float)cos((double)angle), (float)sin((double)angle));
+}
+
+// Workgroup (token tile of 64, head h).  Wave w handles tokens t0 + w + 4i;
+// lane l owns the rotary pair (2l, 2l+1) of the 128-wide head.  q and k are
+// RMSNormed over the head (eps), rotated with the token's table entry; q is
+// scaled by q_scale.  K is staged in LDS and written transposed.
+__global__ __launch_bounds__(256) void qkv_split_kernel(const float* __restrict__ qkv, const float2* __restrict__ tab,
+                                                        const float* __restrict__ qn, const float* __restrict__ kn,
+                                                        float* __restrict__ Q, float* __restrict__ Kt,
+                                                        float* __restrict__ V, int T, int H, float eps, float q_scale) {
+  __shared__ float ks[kHead][kSplitTokens + 1];
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int t0 = (int)blockIdx.x * kSplitTokens;
+  const int h = (int)blockIdx.y;
+  const int D = H * kHead;
+  const float qw0 = qn[2 * lane], qw1 = qn[2 * lane + 1];
+  const float kw0 = kn[2 * lane], kw1 = kn[2 * lane + 1];
+  for (int j = wave; j < kSplitTokens; j += 4) {
+    const int t = t0 + j;
+    if (t >= T) break;
+    const float* row = qkv + (size_t)t * 3 * D + h * kHead + 2 * lane;
+    const float2 cs = tab[(size_t)t * 64 + lane];
+    {
+      const float e = row[0], o = row[1];
+      const float inv = 1.0f / sqrtf(rows::wave_sum(e * e + o * o) / (float)kHead + eps);
+      const float ne = e * inv * qw0, no = o * inv * qw1;
+      float2 out;
+      out.x = (ne * cs.x - no * cs.y) * q_scale;
+      out.y = (ne * cs.y + no * cs.x) * q_scale;
+      *reinterpret_cast<float2*>(Q + ((size_t)h * T + t) * kHead + 2 * lane) = out;
+    }
+    {
+      const float e = row[D], o = row[D + 1];
+      const float inv = 1.0f / sqrtf(rows::wave_sum(e * e + o * o) / (float)kHead + eps);
+      const float ne = e * inv * kw0, no = o * inv * kw1;
+      ks[2 * lane][j] = ne * cs.x - no * cs.y;
+      ks[2 * lane + 1][j] = ne * cs.y + no * cs.x;
+    }
+    *reinterpret_cast<float2*>(V + ((size_t)h * T + t) * kHead + 2 * lane) =
+        *reinterpret_cast<const float2*>(row + 2 * D);
+  }
+  __syncthreads();
+  const int n = min(kSplitTokens, T - t0);
+  for (int i = (int)threadIdx.x; i < kHead * kSplitTokens; i += 256) {
+    const int c = i / kSplitTokens, j = i - c * kSplitTokens;
+    if (j < n) Kt[((size_t)h * kHead + c) * T + t0 + j] = ks[c][j];
+  }
+}
+
+// Audit recomputation of q or k (which = 0 / 1) after the head RMSNorm and,
+// when rope is set, the rotation, in the canonical [T, H*128] layout without
+// the attention scale (the "q_norm" / "q_rope" stages of canonical_reference.go:412-426).
+__global__ __launch_bounds__(256) void qk_audit_kernel(const float* __restrict__ qkv, const float2* __restrict__ tab,
+                                                       const float* __restrict__ nw, float* __restrict__ out, int T,
+                                                       int H, float eps, int which, int rope) {
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int unit = (int)blockIdx.x * 4 + wave;
+  if (unit >= T * H) return;
+  const int t = unit / H, h = unit - t * H;
+  const int D = H * kHead;
+  const float* row = qkv + (size_t)t * 3 * D + (size_t)which * D + h * kHead + 2 * lane;
+  const float e = row[0], o = row[1];
+  const float inv = 1.0f / sqrtf(rows::wave_sum(e * e + o * o) / (float)kHead + eps);
+  float ne = e * inv * nw[2 * lane], no = o * inv * nw[2 * lane + 1];
+  if (rope) {
+    const float2 cs = tab[(size_t)t * 64 + lane];
+    const float re = ne * cs.x - no * cs.y, ro = ne * cs.y + no * cs.x;
+    ne = re;
+    no = ro;
+  }
+  *reinterpret_cast<float2*>(out + (size_t)t * D + h * kHead + 2 * lane) = make_float2(ne, no);
+}
+
+// G [T, 2F] (w1 | w3) -> h [T, F] = silu(w1) * w3 (canonical_reference.go:457-460).
+__global__ __launch_bounds__(256) void swiglu_f32_kernel(const float* __restrict__ G, float* __restrict__ Hd, int T,
+                                                         int F) {
+  const size_t total = (size_t)T * F;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = idx / F, i = idx - t * F;
+    const float g = G[t * 2 * F + i], u = G[t * 2 * F + F + i];
+    Hd[idx] = g / (1.0f + expf(-g)) * u;
+  }
+}
+
+inline unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>(65536, (n + 255) / 256); }
+
+}  // namespace
+
+size_t zimage_workspace_layout(int T, int D, int H, int F, size_t off[kZCount]) {
+  const size_t t = (size_t)T, d = (size_t)D, f = (size_t)F;
+  size_t sizes[kZCount] = {};
+  sizes[kZModRaw] = 4 * d * 4;
+  sizes[kZMod] = 4 * d * 4;
+  sizes[kZA] = t * d * 4;
+  sizes[kZQkv] = t * 3 * d * 4;
+  sizes[kZQ] = t * d * 4;
+  sizes[kZKt] = t * d * 4;
+  sizes[kZV] = t * d * 4;
+  sizes[kZS] = (size_t)H * t * t * 4;
+  sizes[kZO] = t * d * 4;
+  sizes[kZProj] = t * d * 4;
+  sizes[kZR] = t * d * 4;
+  sizes[kZF] = t * d * 4;
+  sizes[kZG] = t * 2 * f * 4;
+  sizes[kZH] = t * f * 4;
+  sizes[kZW2] = t * d * 4;
+  sizes[kZRope] = t * 64 * 8;
+  size_t o = 0;
+  for (int i = 0; i < kZCount; ++i) {
+    off[i] = o;
+    o += (sizes[i] + 255) & ~(size_t)255;
+  }
+  return o;
+}
+
+hipError_t launch_widen_f16(const uint16_t* src, float* dst, size_t rows_n, size_t cols, size_t dst_ld,
+                            hipStream_t stream) {
+  if (rows_n * cols == 0) return hipSuccess;
+  hipLaunchKernelGGL(widen_f16_kernel, dim3(grid_for(rows_n * cols)), dim3(256), 0, stream, src, dst, rows_n, cols,
+                     dst_ld);
+  return hipGetLastError();
+}
+
+hipError_t launch_widen_bf16(const uint16_t* src, float* dst, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(widen_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, stream, src, dst, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_zimage_rope_table(const float* coords, float2* tab, int T, hipStream_t stream) {
+  hipLaunchKernelGGL(rope_table_f32_kernel, dim3((T * 64 + 255) / 256), dim3(256), 0, stream, coords, tab, T);
+  return hipGetLastError();
+}
+
+hipError_t launch_zimage_norm(const float* x, const float* w, float* out, int T, int D, float eps, hipStream_t stream) {
+  hipLaunchKernelGGL(rows::norm_mod_kernel<float>, dim3((T + 3) / 4), dim3(256), 0, stream, x, w, (const float*)nullptr,
+                     out, T, D, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_zimage_qk_audit(const float* qkv, const float2* tab, const float* norm_w, float* out, int T, int H,
+                                  float eps, int which, bool rope, hipStream_t stream) {
+  hipLaunchKernelGGL(qk_audit_kernel, dim3((T * H + 3) / 4), dim3(256), 0, stream, qkv, tab, norm_w, out, T, H, eps,
+                     which, rope ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x, const float* cond, float* out,
+                                    char* ws, const size_t off[kZCount], int T, int D, int F, float eps,
+                                    hipStream_t st, uint32_t* launches, int stop_after) {
+  const int H = D / kHead;
+  float* raw = reinterpret_cast<float*>(ws + off[kZModRaw]);
+  float* mod = reinterpret_cast<float*>(ws + off[kZMod]);
+  float* A = reinterpret_cast<float*>(ws + off[kZA]);
+  float* qkv = reinterpret_cast<float*>(ws + off[kZQkv]);
+  float* Q = reinterpret_cast<float*>(ws + off[kZQ]);
+  float* Kt = reinterpret_cast<float*>(ws + off[kZKt]);
+  float* V = reinterpret_cast<float*>(ws + off[kZV]);
+  float* S = reinterpret_cast<float*>(ws + off[kZS]);
+  float* O = reinterpret_cast<float*>(ws + off[kZO]);
+  float* proj = reinterpret_cast<float*>(ws + off[kZProj]);
+  float* R = reinterpret_cast<float*>(ws + off[kZR]);
+  float* Fm = reinterpret_cast<float*>(ws + off[kZF]);
+  float* G = reinterpret_cast<float*>(ws + off[kZG]);
+  float* Hd = reinterpret_cast<float*>(ws + off[kZH]);
+  float* W2 = reinterpret_cast<float*>(ws + off[kZW2]);
+  const float2* rope = reinterpret_cast<const float2*>(ws + off[kZRope]);
+  const bool modulated = w.adaln_w != nullptr;
+  const float* scaleA = modulated ? mod : nullptr;
+  const float* gateA = modulated ? mod + D : nullptr;
+  const float* scaleM = modulated ? mod + 2 * D : nullptr;
+  const float* gateM = modulated ? mod + 3 * D : nullptr;
+  hipError_t e;
+  uint32_t n = 0;
+#define PROM_STEP(call)            \
+  do {                             \
+    e = (call);                    \
+    if (e != hipSuccess) return e; \
+    ++n;                           \
+  } while (0)
+  const dim3 row_grid((T + 3) / 4), blk(256);
+  if (modulated) {
+    hipLaunchKernelGGL(adaln_f32_kernel, dim3((4 * D + 63) / 64), blk, 0, st, cond, w.adaln_w, w.adaln_b, raw, mod,
+                       kZImageConditionWidth, D);
+    PROM_STEP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(rows::norm_mod_kernel<float>, row_grid, blk, 0, st, x, w.attn_norm1, scaleA, A, T, D, eps);
+  PROM_STEP(hipGetLastError());
+  PROM_STEP(launch_sgemm_f32_ex(A, D, w.w_qkv, 3 * D, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(qkv_split_kernel, dim3((T + kSplitTokens - 1) / kSplitTokens, H), blk, 0, st, qkv, rope, w.q_norm,
+                     w.k_norm, Q, Kt, V, T, H, eps, 1.0f / sqrtf((float)kHead));
+  PROM_STEP(hipGetLastError());
+  if (stop_after == 1) {
+    if (launches) *launches = n;
+    return hipSuccess;
+  }
+  PROM_STEP(launch_sgemm_f32_batched(Q, kHead, (long long)T * kHead, Kt, T, (long long)kHead * T, S, T,
+                                     (long long)T * T, T, T, kHead, H, st));
+  PROM_STEP(launch_row_reduction(S, S, (uint32_t)(H * T), (uint32_t)T, 3u, st));
+  PROM_STEP(launch_sgemm_f32_batched(S, T, (long long)T * T, V, kHead, (long long)T * kHead, O, D, kHead, T, kHead, T,
+                                     H, st));
+  PROM_STEP(launch_sgemm_f32_ex(O, D, w.w_out, D, proj, D, T, D, D, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(rows::resid_norm_mod_kernel<float>, row_grid, blk, 0, st, x, proj, w.attn_norm2, gateA,
+                     w.ffn_norm1, scaleM, R, Fm, T, D, eps);
+  PROM_STEP(hipGetLastError());
+  if (stop_after == 2) {
+    if (launches) *launches = n;
+    return hipSuccess;
+  }
+  PROM_STEP(launch_sgemm_f32_ex(Fm, D, w.w_13, 2 * F, G, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(swiglu_f32_kernel, dim3(grid_for((size_t)T * F)), blk, 0, st, G, Hd, T, F);
+  PROM_STEP(hipGetLastError());
+  PROM_STEP(launch_sgemm_f32_ex(Hd, F, w.w_2, D, W2, D, T, D, F, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(rows::final_resid_kernel, row_grid, blk, 0, st, R, W2, w.ffn_norm2, gateM, out, T, D, eps);
+  PROM_STEP(hipGetLastError());
+#undef PROM_STEP
+  if (launches) *launches = n;
+  return hipSuccess;
+}
+
+}  // namespace prom

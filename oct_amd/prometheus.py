@@ -524,6 +524,149 @@ class PrometheusGemma4E2BM1AttentionScoresResult(Structure):
                        "u64 pipeline_create_count, u64 observed_weight_generation, u64 requested_weight_generation")
 
 
+# ---- resident model blocks and the compiled session (reactor_api.h:666-1249)
+PROM_MODEL_BLOCK_MAX_WEIGHTS = 13
+PROM_MODEL_BLOCK_MAX_STEPS = 7
+PROM_ZIMAGE_TURBO_LOCK_ID = 0x71EF202B4E34B562
+PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES = 47186176
+PROM_NOISE_REFINER_FAMILY = 1
+PROM_CONTEXT_REFINER_FAMILY = 2
+PROM_MAIN_TRANSFORMER_FAMILY = 3
+PROM_MODEL_BLOCK_SHADER_RESIDENT = 23
+PROM_MODEL_BLOCK_SHADER_NOISE = 24
+NOISE_REFINER_AGGREGATES = (0xA1BA526898A2A752, 0x80C0CD75F44CC434)
+PROM_MODEL_BLOCK_DETAIL = {
+    "INVALID_REQUEST": -6901, "NOT_FOUND": -6902, "ALREADY_CREATED": -6903, "WEIGHT_MISMATCH": -6904,
+    "RESOURCE_CREATE_FAILED": -6905, "PIPELINE_CREATE_FAILED": -6906, "UPLOAD_FAILED": -6907,
+    "COMMAND_RECORD_FAILED": -6908, "QUEUE_SUBMIT_FAILED": -6909, "COMPLETION_UNCERTAIN": -6910,
+    "AUDIT_FAILED": -6911, "STALE_OUTPUT": -6912, "PARAMETER_SET_MISMATCH": -6920, "REBIND_FAILED": -6921,
+    "SESSION_INVALID_REQUEST": -6923, "SESSION_STALE_STREAM": -6924, "SESSION_STREAM_MISMATCH": -6925,
+    "SESSION_COMPLETION_UNCERTAIN": -6926,
+}
+PROM_REDUCTION_TESTCFG_FAIL_COMMAND_RECORD = 1 << 0
+PROM_REDUCTION_TESTCFG_FAIL_QUEUE_SUBMIT = 1 << 1
+PROM_REDUCTION_TESTCFG_FAIL_COMPLETION_OBSERVATION = 1 << 2
+
+
+class PrometheusModelBlockWeightDeclaration(Structure):
+    _fields_ = _fields("u64 content_identity, u64 layout_identity, u64 byte_count")
+
+
+class PrometheusModelBlockCreateRequest(Structure):
+    """reactor_api.h:806-826"""
+    _fields_ = _fields("u32 struct_size, u32 assembly_family, u32 parameter_set, "
+                       "u64 parameter_set_aggregate_identity, u64 model_contract_identity, u64 weight_identity, "
+                       "u64 shader_portfolio_identity, u64 precision_policy_identity, u64 capability_route_identity, "
+                       "u64 memory_ceiling_bytes, u64 external_input_bytes, u64 external_output_bytes, "
+                       "u64 audit_bytes, u32 shader_id, u32 weight_count") + [
+        ("weights", PrometheusModelBlockWeightDeclaration * PROM_MODEL_BLOCK_MAX_WEIGHTS),
+        ("step_count", c_uint32), ("steps", c_uint32 * PROM_MODEL_BLOCK_MAX_STEPS)]
+
+
+class PrometheusModelBlockWeightUpload(Structure):
+    _fields_ = _fields("u32 binding_index, p bytes, u64 byte_count, u64 content_identity, u64 layout_identity")
+
+
+class PrometheusNoiseRefinerRebindRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u32 model_local_block_id, u64 lock_identity, u32 upload_count, p uploads")
+
+
+# ContextRefiner create/rebind and MainTransformer create/rebind share this layout.
+PrometheusContextRefinerCreateRequest = PrometheusNoiseRefinerRebindRequest
+
+
+class PrometheusMainTransformerExecuteRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u64 session_identity, u64 lock_identity, u32 model_local_block_id, "
+                       "u32 audit_enabled, u32 resident_chain_mode, u32 reserved0, u64 required_image_generation, "
+                       "u64 required_context_generation, u64 required_joint_generation, p timestep_bf16, "
+                       "u64 timestep_bytes, u64 timestep_identity, u64 output_identity")
+
+
+class PrometheusModelBlockExecuteRequest(Structure):
+    _fields_ = _fields("u32 struct_size, p input, p output, u64 element_count, u64 input_identity, "
+                       "u32 audit_enabled, p audit_output, u64 audit_element_capacity")
+
+
+class PrometheusNoiseRefiner0ExecuteRequest(Structure):
+    _fields_ = _fields("u32 struct_size, p model_input_bf16, p timestep_bf16, u64 model_input_bytes, "
+                       "u64 timestep_bytes, u64 input_identity, u64 timestep_identity, u64 output_identity, "
+                       "u32 audit_enabled")
+
+
+class PrometheusNoiseRefinerResidentExecuteRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u64 input_generation, u64 output_identity, u32 audit_enabled, "
+                       "u32 audit_family, u32 audit_stage, p audit_output, u64 audit_element_capacity")
+
+
+class PrometheusContextRefiner0ExecuteRequest(Structure):
+    _fields_ = _fields("u32 struct_size, p context_input, u64 context_input_bytes, u64 input_identity, "
+                       "u64 output_identity, u32 audit_enabled")
+
+
+class PrometheusContextRefinerResidentExecuteRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u64 input_generation, u64 output_identity, u32 audit_enabled")
+
+
+class PrometheusNoiseRefinerFinalAuditRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u64 required_output_generation, u64 output_identity, p output, "
+                       "u64 output_element_capacity")
+
+
+class PrometheusModelBlockEvidence(Structure):
+    """reactor_api.h:1103-1186"""
+    _fields_ = _fields(
+        "u32 struct_size, i32 detail_code, u32 created, u32 weights_uploaded, u32 quarantined, u32 output_valid, "
+        "u32 audit_valid, u32 fixed_step_count, u32 weight_count, u64 persistent_bytes, u64 reusable_bytes, "
+        "u64 audit_bytes, u64 external_bytes, u64 total_committed_bytes, u64 peak_plan_bytes, "
+        "u64 cold_buffer_allocation_count, u64 warm_buffer_allocation_count, u64 pipeline_create_count, "
+        "u64 descriptor_set_count, u64 weight_upload_count, u64 execution_count, u64 last_execution_ns, "
+        "u64 execution_plan_identity, u64 replay_identity, u32 assembly_family, u32 parameter_set, "
+        "u32 binding_state, u32 active_weight_window, u64 parameter_set_aggregate_identity, "
+        "u64 binding_generation, u64 output_generation, u64 descriptor_generation") + [
+        ("m1b_boundary_gpu_ns", c_uint64 * 6)] + _fields(
+        "u64 gpu_total_begin_tick, u64 gpu_total_end_tick, u64 gpu_total_ns, u64 gpu_compute_begin_tick, "
+        "u64 gpu_compute_end_tick, u64 gpu_compute_ns, u64 gpu_ingress_transfer_ns, u64 gpu_joint_copy_ns, "
+        "u64 gpu_readback_ns") + [
+        ("main_stage_gpu_begin_tick", c_uint64 * 13), ("main_stage_gpu_end_tick", c_uint64 * 13),
+        ("main_stage_gpu_ns", c_uint64 * 13)] + _fields(
+        "u64 last_active_target_validation_ns, u64 last_command_reset_ns, u64 last_command_begin_ns, "
+        "u64 last_command_record_ns, u64 last_command_end_ns, u64 last_queue_submit_ns, u64 last_fence_wait_ns, "
+        "u64 last_descriptor_update_ns, u64 last_staging_memcpy_ns, u64 last_output_readback_ns, "
+        "u64 vk_create_buffer_count, u64 vk_destroy_buffer_count, u64 vk_allocate_memory_count, "
+        "u64 vk_free_memory_count, u64 vk_create_shader_module_count, u64 vk_destroy_shader_module_count, "
+        "u64 vk_create_compute_pipelines_count, u64 vk_allocate_descriptor_sets_count, "
+        "u64 vk_update_descriptor_sets_count, u64 vk_create_command_pool_count, "
+        "u64 vk_allocate_command_buffers_count, u64 vk_reset_command_buffer_count, u64 vk_queue_submit_count, "
+        "u64 vk_fence_wait_count, u64 vk_timeline_wait_count, u64 vk_map_memory_count, u64 vk_unmap_memory_count, "
+        "u64 vk_flush_count, u64 vk_invalidate_count, u64 m6a_activation_pack_gpu_ns, "
+        "u64 m6a_cooperative_execute_gpu_ns, u64 m6a_w3_segment_repack_gpu_ns")
+
+
+class PrometheusCompiledModelSessionCreateRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u64 lock_identity, u32 execution_profile, u32 main_attention_route_policy")
+
+
+class PrometheusCompiledModelSessionCaptureRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u64 source_output_generation")
+
+
+class PrometheusCompiledModelSessionComposeRequest(Structure):
+    _fields_ = _fields("u32 struct_size, u64 required_image_generation, u64 required_context_generation")
+
+
+class PrometheusCompiledModelSessionEvidence(Structure):
+    """reactor_api.h:1208-1236"""
+    _fields_ = _fields(
+        "u32 struct_size, i32 detail_code, u32 created, u32 quarantined, u64 session_identity, u64 lock_identity, "
+        "u64 active_block_id, u64 binding_generation, u64 replay_identity, u64 prepared_image_generation, "
+        "u64 prepared_context_generation, u64 joint_generation, u64 joint_image_generation, "
+        "u64 joint_context_generation, u64 prepared_image_bytes, u64 prepared_context_bytes, u64 joint_bytes, "
+        "u64 cold_buffer_allocation_count, u64 warm_buffer_allocation_count, u64 composition_count, "
+        "u32 requested_execution_profile, u32 selected_execution_profile, u32 profile_fallback_reason, "
+        "u32 requested_main_attention_route, u32 selected_main_attention_route, "
+        "u32 main_attention_fallback_reason, u32 main_attention_shader_id")
+
+
 # ---- errors and status (status.go, bridge.go) ------------------------------
 class ReactorIssue(RuntimeError):
     """Structured reactor failure (reference ``ReactorIssue``, bridge.go:33-66)."""
@@ -643,6 +786,73 @@ _SIGNATURES = {
     "prometheus_reactor_runtime_gemma4e2b_m1_attention_scores": (
         c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1AttentionScoresRequest),
                 POINTER(PrometheusGemma4E2BM1AttentionScoresResult)]),
+    # resident model blocks and the compiled session (reactor_api.h:2713-2808)
+    "prometheus_reactor_runtime_model_block_create": (
+        c_int, [c_void_p, POINTER(PrometheusModelBlockCreateRequest), POINTER(c_uint64),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_model_block_upload_weights": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockWeightUpload), c_uint32,
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_model_block_execute": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_noise_refiner0_execute": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefiner0ExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_noise_refiner1_execute": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefiner0ExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_noise_refiner_rebind": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefinerRebindRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_noise_refiner_execute_resident": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefinerResidentExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_noise_refiner_audit_final": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefinerFinalAuditRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_context_refiner_create": (
+        c_int, [c_void_p, POINTER(PrometheusContextRefinerCreateRequest), POINTER(c_uint64),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_context_refiner_rebind": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusContextRefinerCreateRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_context_refiner0_execute": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusContextRefiner0ExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_context_refiner_execute_resident": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusContextRefinerResidentExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_context_refiner_audit_final": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefinerFinalAuditRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_main_transformer_create": (
+        c_int, [c_void_p, POINTER(PrometheusContextRefinerCreateRequest), POINTER(c_uint64),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_main_transformer_rebind": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusContextRefinerCreateRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_main_transformer_execute": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusMainTransformerExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_main_transformer_audit_final": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefinerFinalAuditRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_model_block_get_evidence": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_model_block_destroy": (c_int, [c_void_p, c_uint64]),
+    "prometheus_reactor_runtime_compiled_model_session_create": (
+        c_int, [c_void_p, POINTER(PrometheusCompiledModelSessionCreateRequest), POINTER(c_uint64),
+                POINTER(PrometheusCompiledModelSessionEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_session_capture_completed": (
+        c_int, [c_void_p, c_uint64, c_uint64, POINTER(PrometheusCompiledModelSessionCaptureRequest),
+                POINTER(PrometheusCompiledModelSessionEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_session_compose_joint": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusCompiledModelSessionComposeRequest),
+                POINTER(PrometheusCompiledModelSessionEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_session_get_evidence": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusCompiledModelSessionEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_session_destroy": (c_int, [c_void_p, c_uint64]),
 }
 
 MANDATORY_SYMBOLS = (

@@ -227,3 +227,134 @@ def make_dit_block(seed: int, tokens: int, hidden: int, ffn: int, cond_dim: int 
         w_2=oracle.to_bf16(oracle.normal(seed + 13, (F, D), 0.0, 0.02)),
     )
     return x, cond, w
+
+
+# ------------------------------------------------- resident Z-Image blocks (fp32 path)
+# Lexical cache-manifest order of one NoiseRefiner / MainTransformer layer
+# (reactor_vulkan_model_block.c:158-161); the ContextRefiner omits the two
+# adaLN tensors (:198-200).  Every tensor is FP16, linear weights [in, out].
+ZIMAGE_TENSORS = ("adaln_b", "adaln_w", "k_norm", "w_out", "q_norm", "w_qkv", "attn_norm1", "attn_norm2",
+                  "w1", "w2", "w3", "ffn_norm1", "ffn_norm2")
+CONTEXT_TENSORS = ZIMAGE_TENSORS[2:]
+
+
+def zimage_weight_shapes(width: int = 3840, ffn: int = 10240, cond: int = 256, head: int = 128) -> dict:
+    return {"adaln_b": (4 * width,), "adaln_w": (cond, 4 * width), "k_norm": (head,), "w_out": (width, width),
+            "q_norm": (head,), "w_qkv": (width, 3 * width), "attn_norm1": (width,), "attn_norm2": (width,),
+            "w1": (width, ffn), "w2": (ffn, width), "w3": (width, ffn), "ffn_norm1": (width,),
+            "ffn_norm2": (width,)}
+
+
+def make_zimage_weights(seed: int, modulated: bool = True, width: int = 3840, ffn: int = 10240) -> dict:
+    """Random FP16 weights of one layer: linear weights ~ N(0, 1/in), norm
+    weights ~ 1 + N(0, 0.1^2), adaLN bias ~ N(0, 0.1^2)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in zimage_weight_shapes(width, ffn).items():
+        if not modulated and name.startswith("adaln"):
+            continue
+        if len(shape) == 2:
+            v = rng.standard_normal(shape, dtype=np.float32) * np.float32(1.0 / np.sqrt(shape[0]))
+        elif name == "adaln_b":
+            v = rng.standard_normal(shape, dtype=np.float32) * np.float32(0.1)
+        else:
+            v = 1.0 + rng.standard_normal(shape, dtype=np.float32) * np.float32(0.1)
+        out[name] = v.astype(np.float16)
+    return out
+
+
+def image_coordinates(tokens: int = 1024) -> np.ndarray:
+    """NoiseRefiner token t: (frame 33, t // 32, t % 32) -- CanonicalImageTokenCoordinate(15, t),
+    canonical_contract.go:36-64 (15 text tokens, 17 padding, +1)."""
+    t = np.arange(tokens)
+    return np.stack((np.full(tokens, 15 + text_padding(15) + 1), t // 32, t % 32), axis=1).astype(np.float32)
+
+
+def context_coordinates(tokens: int = 32) -> np.ndarray:
+    """ContextRefiner token t: (t + 1, 0, 0) -- context_refiner_reference.go:156-158."""
+    t = np.arange(1, tokens + 1)
+    return np.stack((t, np.zeros(tokens), np.zeros(tokens)), axis=1).astype(np.float32)
+
+
+def rope_canonical_f32(x: np.ndarray, coords: np.ndarray, axes=(32, 48, 48), theta: float = 256.0) -> np.ndarray:
+    """CanonicalRopeRotate (canonical_contract.go:66-87): frequency and angle are
+    float32 values (freq = float32(1 / theta^(2p/w)), angle = float32(coord * freq)),
+    cos/sin evaluated in binary64 on that angle; the rotation itself in binary64."""
+    out = np.array(x, dtype=np.float64, copy=True)
+    start = 0
+    for axis, width in enumerate(axes):
+        pairs = np.arange(width // 2, dtype=np.float64)
+        freq = (1.0 / np.power(float(theta), 2.0 * pairs / width)).astype(np.float32)
+        ang = (coords[:, axis:axis + 1].astype(np.float32) * freq[None, :]).astype(np.float64)
+        c = np.cos(ang)[:, None, :]
+        s = np.sin(ang)[:, None, :]
+        even = out[:, :, start:start + width:2].copy()
+        odd = out[:, :, start + 1:start + width:2].copy()
+        out[:, :, start:start + width:2] = even * c - odd * s
+        out[:, :, start + 1:start + width:2] = even * s + odd * c
+        start += width
+    return out
+
+
+def zimage_block_f64(x, coords, w: dict, cond=None, heads: int = 30, eps: float = 1e-5, rows=None,
+                     stages: dict | None = None) -> np.ndarray:
+    """One Z-Image block in binary64 on FP16 weights widened exactly: the
+    NoiseRefiner / MainTransformer (canonical_reference.go:358-480, with adaLN
+    from ``cond``) or, with ``cond`` None, the unmodulated ContextRefiner
+    (context_refiner_reference.go:230-311).  ``rows`` restricts the evaluated
+    output tokens (K and V still use every token); ``stages`` (a dict) receives
+    the canonical intermediate stages for those rows."""
+    f = lambda name: np.asarray(w[name], dtype=np.float64)
+    x = np.asarray(x, np.float64)
+    T, D = x.shape
+    hd = D // heads
+    F = w["w2"].shape[0]
+    sel = np.arange(T) if rows is None else np.asarray(rows)
+    keep = stages if stages is not None else {}
+    if cond is not None:
+        raw = np.asarray(cond, np.float64) @ f("adaln_w") + f("adaln_b")
+        keep["adaln_projection"] = raw
+        scale_a, gate_a = 1.0 + raw[:D], np.tanh(raw[D:2 * D])
+        scale_m, gate_m = 1.0 + raw[2 * D:3 * D], np.tanh(raw[3 * D:])
+    else:
+        scale_a = gate_a = scale_m = gate_m = np.ones(D)
+    a = rmsnorm(x, f("attn_norm1"), eps) * scale_a
+    keep["attention_modulated"] = a[sel]
+    w_qkv = f("w_qkv")
+    qkv = a @ w_qkv
+    keep["qkv"] = qkv[sel]
+    q = qkv[sel, :D].reshape(len(sel), heads, hd)
+    k = qkv[:, D:2 * D].reshape(T, heads, hd)
+    v = qkv[:, 2 * D:].reshape(T, heads, hd)
+    q = rmsnorm(q, f("q_norm"), eps)
+    k = rmsnorm(k, f("k_norm"), eps)
+    keep["q_norm"] = q.reshape(len(sel), D)
+    keep["k_norm"] = k[sel].reshape(len(sel), D)
+    q = rope_canonical_f32(q, coords[sel])
+    k = rope_canonical_f32(k, coords)
+    keep["q_rope"] = q.reshape(len(sel), D)
+    keep["k_rope"] = k[sel].reshape(len(sel), D)
+    o = np.empty((len(sel), heads, hd))
+    for h in range(heads):
+        s = (q[:, h, :] @ k[:, h, :].T) / np.sqrt(hd)
+        o[:, h, :] = softmax_rows(s) @ v[:, h, :]
+    o = o.reshape(len(sel), D)
+    keep["attention_aggregation"] = o
+    proj = o @ f("w_out")
+    keep["attention_projection"] = proj
+    r = x[sel] + gate_a * rmsnorm(proj, f("attn_norm2"), eps)
+    keep["attention_residual"] = r
+    fn = rmsnorm(r, f("ffn_norm1"), eps)
+    keep["ffn_norm"] = fn
+    fm = fn * scale_m
+    keep["ffn_modulated"] = fm
+    w1 = fm @ f("w1")
+    w3 = fm @ f("w3")
+    keep["w1"], keep["w3"] = w1, w3
+    hdn = silu(w1) * w3
+    keep["ffn_gated_hidden"] = hdn
+    w2 = hdn @ f("w2")
+    keep["w2"] = w2
+    out = r + gate_m * rmsnorm(w2, f("ffn_norm2"), eps)
+    keep["final_output"] = out
+    return out

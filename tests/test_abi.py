@@ -75,7 +75,28 @@ STRUCTS = {
     "PrometheusGemma4E2BM1HeadRmsNormRopeResult": p.PrometheusGemma4E2BM1HeadRmsNormRopeResult,
     "PrometheusGemma4E2BM1AttentionScoresRequest": p.PrometheusGemma4E2BM1AttentionScoresRequest,
     "PrometheusGemma4E2BM1AttentionScoresResult": p.PrometheusGemma4E2BM1AttentionScoresResult,
+    "PrometheusModelBlockWeightDeclaration": p.PrometheusModelBlockWeightDeclaration,
+    "PrometheusModelBlockCreateRequest": p.PrometheusModelBlockCreateRequest,
+    "PrometheusModelBlockWeightUpload": p.PrometheusModelBlockWeightUpload,
+    "PrometheusNoiseRefinerRebindRequest": p.PrometheusNoiseRefinerRebindRequest,
+    "PrometheusContextRefinerCreateRequest": p.PrometheusContextRefinerCreateRequest,
+    "PrometheusMainTransformerCreateRequest": p.PrometheusContextRefinerCreateRequest,
+    "PrometheusMainTransformerExecuteRequest": p.PrometheusMainTransformerExecuteRequest,
+    "PrometheusModelBlockExecuteRequest": p.PrometheusModelBlockExecuteRequest,
+    "PrometheusNoiseRefiner0ExecuteRequest": p.PrometheusNoiseRefiner0ExecuteRequest,
+    "PrometheusNoiseRefiner1ExecuteRequest": p.PrometheusNoiseRefiner0ExecuteRequest,
+    "PrometheusNoiseRefinerResidentExecuteRequest": p.PrometheusNoiseRefinerResidentExecuteRequest,
+    "PrometheusContextRefiner0ExecuteRequest": p.PrometheusContextRefiner0ExecuteRequest,
+    "PrometheusContextRefinerResidentExecuteRequest": p.PrometheusContextRefinerResidentExecuteRequest,
+    "PrometheusNoiseRefinerFinalAuditRequest": p.PrometheusNoiseRefinerFinalAuditRequest,
+    "PrometheusModelBlockEvidence": p.PrometheusModelBlockEvidence,
+    "PrometheusCompiledModelSessionCreateRequest": p.PrometheusCompiledModelSessionCreateRequest,
+    "PrometheusCompiledModelSessionCaptureRequest": p.PrometheusCompiledModelSessionCaptureRequest,
+    "PrometheusCompiledModelSessionComposeRequest": p.PrometheusCompiledModelSessionComposeRequest,
+    "PrometheusCompiledModelSessionEvidence": p.PrometheusCompiledModelSessionEvidence,
 }
+MODEL_BLOCK_STRUCTS = tuple(n for n in STRUCTS if "ModelBlock" in n or "Refiner" in n or "MainTransformer" in n
+                            or "CompiledModel" in n)
 
 # Structs whose layout the reference header fixes (a drop-in caller compiled
 # against it must read the same bytes).
@@ -88,7 +109,7 @@ REFERENCE_STRUCTS = (
     "PrometheusGemma4E2BM1RopeRequest", "PrometheusGemma4E2BM1RopeResult", "PrometheusGemma4E2BM1HeadRmsNormRopeRequest",
     "PrometheusGemma4E2BM1HeadRmsNormRopeResult", "PrometheusGemma4E2BM1AttentionScoresRequest",
     "PrometheusGemma4E2BM1AttentionScoresResult",
-)
+) + MODEL_BLOCK_STRUCTS
 REFERENCE_HEADER = Path("/root/reference/internal/prometheus/native/reactor_api.h")
 
 
