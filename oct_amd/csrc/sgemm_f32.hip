@@ -293,14 +293,31 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Number of K slices for an under-filled launch: aim for >= 2 workgroups per
-// CU (512 on 256 CUs) while keeping every slice >= 128 deep.
-int choose_splits(int tiles, uint32_t k) {
-  if (tiles >= 512 || k < 512) return 1;
-  int s = (512 + tiles - 1) / tiles;
-  s = std::min(s, (int)(k / 128));
-  s = std::min(s, 16);
-  return std::max(s, 1);
+// Number of K slices.  2 workgroups per CU make 512 concurrent slots; a grid
+// of w workgroups runs in ceil(w / 512) rounds, each as long as one slice's
+// K tiles (~4 us per 128x256x16 tile step at full rate, plus ~2 us of
+// prologue and epilogue).  Slicing adds the reduce launch (~8 us) and
+// (2s + 1) M N floats of partial-sum traffic (~3 TB/s effective).  The count
+// minimising this estimate is chosen, with slices at least 128 deep and at
+// most 16 of them.
+int choose_splits(int tiles, uint32_t m, uint32_t n, uint32_t k) {
+  const int k_tiles = (int)((k + kBK - 1) / kBK);
+  auto cost = [&](int s) {
+    const int per = (k_tiles + s - 1) / s;
+    const double rounds = (double)(((size_t)tiles * s + 511) / 512);
+    const double reduce = s == 1 ? 0.0 : 8.0 + (double)(2 * s + 1) * m * n * 4.0 / 3.0e6;
+    return rounds * (per * 4.0 + 2.0) + reduce;
+  };
+  int best = 1;
+  double best_cost = cost(1);
+  for (int s = 2; s <= 16 && k / (uint32_t)s >= 128; ++s) {
+    const double c = cost(s);
+    if (c < best_cost) {
+      best_cost = c;
+      best = s;
+    }
+  }
+  return best;
 }
 
 }  // namespace
@@ -321,7 +338,7 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && aligned16(a) && aligned16(b);
-  int splits = choose_splits(tiles_m * tiles_n, k);
+  int splits = choose_splits(tiles_m * tiles_n, m, n, k);
   int k_len = (int)k;
   float* partial = nullptr;
   if (splits > 1) {
