@@ -27,6 +27,9 @@ sys.path.insert(0, str(REPO))
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_BF16_MFMA_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# One NoiseRefiner layer: 2*T*D*(3D + D + 3F) projection flops + 4*T^2*D attention flops,
+# T = 1024, D = 3840, F = 10240.
+NOISE_REFINER_FLOP = 2.0 * 1024 * 3840 * (3 * 3840 + 3840 + 3 * 10240) + 4.0 * 1024 * 1024 * 3840
 
 
 def _timed_launches(rt, launch, steps: int, warmup: int):
@@ -55,12 +58,16 @@ def _traffic_from_profiles(name: str):
         return None
 
 
-def cpu_baseline_sgemm(n: int, seconds: float):
-    """Oct's compiled CPU `@` (__octMatMulMM restatement, binary64 ijk, one thread) on a row sample."""
+def cpu_baseline_sgemm(a32: np.ndarray, b32: np.ndarray, gpu_rows: dict, seconds: float):
+    """Oct's compiled CPU `@` (__octMatMulMM restatement, binary64 ijk, one thread) on a row sample
+    of the benchmark's own operands; also checks the GPU's output rows against the oracle."""
     import oracle
 
-    a = oracle.uniform(11, (n, n)).astype(np.float64)
-    b = oracle.uniform(12, (n, n)).astype(np.float64)
+    n = a32.shape[0]
+    parity = max(oracle.normwise_rel_err(row, oracle.matmul_f64(a32, b32, rows=(r, r + 1))[r])
+                 for r, row in gpu_rows.items())
+    a = a32.astype(np.float64)
+    b = b32.astype(np.float64)
     rows = 0
     t0 = time.perf_counter()
     while rows < n:
@@ -70,7 +77,7 @@ def cpu_baseline_sgemm(n: int, seconds: float):
             break
     dt = time.perf_counter() - t0
     flops = 2.0 * rows * n * n
-    return {
+    return parity, {
         "value": round(flops / dt / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": 1,
@@ -165,7 +172,7 @@ def main() -> int:
         return 2
 
     from oct_amd import prometheus as p
-    import oracle
+    from oct_amd import synthetic as syn
 
     if args.copy_calibration_mib:
         import torch
@@ -183,8 +190,8 @@ def main() -> int:
 
     # ---- headline: fp32 SGEMM 4096^3 ------------------------------------------
     n = 4096
-    a = oracle.uniform(11, (n, n))
-    b = oracle.uniform(12, (n, n))
+    a = syn.uniform(11, (n, n))
+    b = syn.uniform(12, (n, n))
     da, db, dc = rt.alloc(a.nbytes), rt.alloc(b.nbytes), rt.alloc(a.nbytes)
     rt.upload(da, a)
     rt.upload(db, b)
@@ -204,7 +211,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: A,B ~ U[-1,1] (SplitMix64/xoshiro256** seeds 11,12), fp32 row-major, resident in HBM",
+        "data": "synthetic: A,B ~ U[-1,1] (numpy PCG64 seeds 11,12), fp32 row-major, resident in HBM",
         "config": {"workload": "sgemm_f32 C=A@B M=N=K=4096 row-major (BASELINE configs[1])", "m": n, "n": n, "k": n,
                    "kernel": "sgemm_f32_mfma_kernel (v_mfma_f32_32x32x2_f32, 128x256x16 tiles, 64x128 per wave)"},
         "roofline": {
@@ -220,11 +227,10 @@ def main() -> int:
         "device": {"name": diag.device_name.decode(), "arch": diag.gcn_arch_name.decode(),
                    "cus": diag.compute_units, "clock_mhz": diag.clock_khz // 1000},
     }
-    # verify the measured output once (outside the timed region)
-    out_rows = rt.download(np.empty((n, n), np.float32), dc)
-    chk_rows = [0, 1777, n - 1]
-    errs = [oracle.normwise_rel_err(out_rows[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r]) for r in chk_rows]
-    line["parity_rows_normwise_max"] = float(max(errs))
+    # rows of the measured output, checked against the oracle in the CPU-baseline leg
+    out_all = rt.download(np.empty((n, n), np.float32), dc)
+    gpu_rows = {r: out_all[r].copy() for r in (0, 1777, n - 1)}
+    del out_all
     for d in (da, db, dc):
         rt.free(d)
     if not args.no_secondary:
@@ -243,7 +249,7 @@ def main() -> int:
         sec = {}
         # fp32 1024^3
         m1 = 1024
-        a1, b1 = oracle.uniform(1, (m1, m1)), oracle.uniform(2, (m1, m1))
+        a1, b1 = syn.uniform(1, (m1, m1)), syn.uniform(2, (m1, m1))
         d1 = [rt.alloc(a1.nbytes) for _ in range(3)]
         rt.upload(d1[0], a1)
         rt.upload(d1[1], b1)
@@ -254,7 +260,7 @@ def main() -> int:
         # ragged and GEMV
         for (m, nn, k, key) in ((1000, 1000, 1000, "sgemm_f32_1000_tflops"),
                                 (4097, 3001, 513, "sgemm_f32_4097x3001x513_tflops")):
-            aa, bb = oracle.uniform(3, (m, k)), oracle.uniform(4, (k, nn))
+            aa, bb = syn.uniform(3, (m, k)), syn.uniform(4, (k, nn))
             dd = [rt.alloc(aa.nbytes), rt.alloc(bb.nbytes), rt.alloc(m * nn * 4)]
             rt.upload(dd[0], aa)
             rt.upload(dd[1], bb)
@@ -263,7 +269,7 @@ def main() -> int:
             for d in dd:
                 rt.free(d)
         m, k = 8192, 4096
-        aa, xx = oracle.uniform(7, (m, k)), oracle.uniform(8, (k, 1))
+        aa, xx = syn.uniform(7, (m, k)), syn.uniform(8, (k, 1))
         dd = [rt.alloc(aa.nbytes), rt.alloc(xx.nbytes), rt.alloc(m * 4)]
         rt.upload(dd[0], aa)
         rt.upload(dd[1], xx)
@@ -272,7 +278,7 @@ def main() -> int:
         for d in dd:
             rt.free(d)
         # bf16 4096^3
-        ab, bbf = oracle.to_bf16(oracle.uniform(41, (n, n))), oracle.to_bf16(oracle.uniform(42, (n, n)))
+        ab, bbf = syn.to_bf16(syn.uniform(41, (n, n))), syn.to_bf16(syn.uniform(42, (n, n)))
         dd = [rt.alloc(ab.nbytes), rt.alloc(bbf.nbytes), rt.alloc(n * n * 4)]
         rt.upload(dd[0], ab)
         rt.upload(dd[1], bbf)
@@ -284,7 +290,7 @@ def main() -> int:
             rt.free(d)
         # reductions on [8192, 4096]
         rows, width = 8192, 4096
-        x = oracle.normal(77, (rows, width))
+        x = syn.normal(77, (rows, width))
         dx, dy = rt.alloc(x.nbytes), rt.alloc(x.nbytes)
         rt.upload(dx, x)
         for op, name, nbytes in ((p.OP_SOFTMAX, "softmax", 2 * x.nbytes), (p.OP_SUM, "row_sum", x.nbytes + rows * 4),
@@ -293,7 +299,7 @@ def main() -> int:
             gbs = nbytes / (ev * 1e-3) / 1e9
             sec[f"{name}_8192x4096_gbs"] = round(gbs, 1)
             sec[f"{name}_8192x4096_frac"] = round(gbs / PEAK_HBM_GBS, 4)
-        w = (1.0 + oracle.normal(89, (width,), 0.0, 0.02)).astype(np.float32)
+        w = syn.normal(89, (width,), 1.0, 0.02)
         dw, dinv = rt.alloc(w.nbytes), rt.alloc(rows * 4)
         rt.upload(dw, w)
         _, ev = _timed_launches(rt, lambda: rt.rmsnorm_device(dx, dw, dy, dinv, rows, width, width, 1e-6), 100, 10)
@@ -303,12 +309,8 @@ def main() -> int:
         for d in (dx, dy, dw, dinv):
             rt.free(d)
         # transformer layers, weights resident
-        from oracle import blocks
-
         T, D, Hq, hd, F = 512, 2048, 8, 256, 16384
-        x, w = blocks.make_decoder_layer(4, T, D, Hq, hd, F)
-        ptrs = {"input": x, "attn_norm_weight": w.attn_norm, "w_qkv": w.w_qkv, "w_o": w.w_o,
-                "ffn_norm_weight": w.ffn_norm, "w_gate_up": w.w_gate_up, "w_down": w.w_down}
+        ptrs = syn.decoder_layer(4, T, D, Hq, hd, F)
         dptr = {k: rt.upload_new(np.ascontiguousarray(v, np.float32)) for k, v in ptrs.items()}
         dptr["output"] = rt.alloc(T * D * 4)
         req = rt.decoder_layer_request(T, D, Hq, hd, F, dptr)
@@ -317,16 +319,11 @@ def main() -> int:
         sec["gemma2b_layer_f32_t512_tflops"] = round(1.149e11 / (ev * 1e-3) / 1e12, 2)
         for d in dptr.values():
             rt.free(d)
-        del x, w
+        del ptrs
         grid, text, heads, F5, C = (64, 64), 128, 30, 10240, 256
         T5 = grid[0] * grid[1] + text
         D5 = heads * 128
-        x, cond, w = blocks.make_dit_block(5, T5, D5, F5, C)
-        coords = blocks.joint_coordinates(grid[0], grid[1], text)
-        arrs = {"input": x, "coordinates": coords, "condition": cond, "w_adaln": w.w_adaln, "b_adaln": w.b_adaln,
-                "attn_norm1": w.attn_norm1, "attn_norm2": w.attn_norm2, "ffn_norm1": w.ffn_norm1,
-                "ffn_norm2": w.ffn_norm2, "q_norm": w.q_norm, "k_norm": w.k_norm, "w_qkv": w.w_qkv,
-                "w_out": w.w_out, "w_13": w.w_13, "w_2": w.w_2}
+        arrs = syn.dit_block(5, T5, D5, F5, C, syn.joint_coordinates(grid[0], grid[1], text))
         dptr = {k: rt.upload_new(v) for k, v in arrs.items()}
         dptr["output"] = rt.alloc(T5 * D5 * 4)
         req = rt.dit_block_request(T5, D5, heads, F5, C, dptr)
@@ -337,7 +334,7 @@ def main() -> int:
             rt.free(d)
         # binary64 FFT, 2^20 points (device entry: two four-step passes)
         nf = 1 << 20
-        xf = (oracle.normal(31, (2 * nf,)).astype(np.float64)).view(np.complex128)
+        xf = syn.normal(31, (2 * nf,)).astype(np.float64).view(np.complex128)
         dfi, dfo = rt.upload_new(xf.view(np.float64)), rt.alloc(xf.nbytes)
         _, ev = _timed_launches(rt, lambda: rt.fft64_device(dfi, dfo, nf), 100, 10)
         sec["fft64_2p20_us"] = round(ev * 1e3, 2)
@@ -346,10 +343,37 @@ def main() -> int:
         sec["fft64_2p20_frac"] = round(gbs / PEAK_HBM_GBS, 4)
         for d in (dfi, dfo):
             rt.free(d)
+        # resident model block: one Z-Image NoiseRefiner layer (1024 tokens, fp32 on
+        # resident FP16-widened weights), chained on its own resident output
+        from oct_amd import model_block as mb
+
+        mrt = p.NativeRuntime()
+        model = mb.ResidentModel(mrt)
+        wz = syn.zimage_weights(1)
+        rc, bid, _ = model.noise_refiner_create(wz)
+        x_bits = syn.to_bf16(syn.normal(2, (1024, 3840)))
+        t_bits = syn.to_bf16(syn.normal(3, (256,)))
+        ok = (rc == p.PROM_OK and model.noise_refiner_execute(bid, x_bits, t_bits)[0] == p.PROM_OK
+              and model.noise_refiner_rebind(bid, wz)[0] == p.PROM_OK)
+        if ok:
+            times = []
+            for _ in range(13):
+                rc, ev = model.noise_refiner_resident(bid, 1)
+                times.append(ev.gpu_compute_ns / 1e6)
+            ms = float(np.median(times[3:]))
+            sec["zimage_noise_refiner_f32_ms"] = round(ms, 4)
+            sec["zimage_noise_refiner_f32_tflops"] = round(NOISE_REFINER_FLOP / (ms * 1e-3) / 1e12, 2)
+            sec["zimage_noise_refiner_f32_frac"] = round(NOISE_REFINER_FLOP / (ms * 1e-3) / 1e12 /
+                                                         PEAK_FP32_MFMA_TFLOPS, 4)
+        mrt.close()
+        del wz
         line["secondary"] = sec
 
     rt.close()
-    line["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline_sgemm(n, args.cpu_seconds)
+    line["cpu_baseline"] = None
+    if not args.no_cpu_baseline:
+        parity, line["cpu_baseline"] = cpu_baseline_sgemm(a, b, gpu_rows, args.cpu_seconds)
+        line["parity_rows_normwise_max"] = float(parity)
     if not args.no_cpu_baseline and not args.no_secondary:
         line["secondary_cpu_baseline"] = cpu_baseline_secondary(args.cpu_seconds)
     print(json.dumps(line), flush=True)
