@@ -1604,6 +1604,18 @@ typedef struct PrometheusCompiledModelSessionEvidence {
   uint32_t main_attention_shader_id;
 } PrometheusCompiledModelSessionEvidence;
 
+/* reactor_api.h:1237-1249 */
+typedef struct PrometheusCompiledModelRetargetRequest {
+  uint32_t struct_size;
+  uint64_t session_identity;
+  uint64_t lock_identity;
+  uint32_t model_local_block_id;
+  uint32_t upload_count;
+  const PrometheusModelBlockWeightUpload* uploads;
+} PrometheusCompiledModelRetargetRequest;
+
+typedef PrometheusCompiledModelRetargetRequest PrometheusCompiledModelPrefetchRequest;
+
 /* reactor_api.h:2713-2733: the closed resident program.  One model block per
    runtime; ids are never reused.  Family 0 (shader 23, the seven fixed steps)
    is the resident proof: output = input, audit = the first audit_bytes/4
@@ -1684,6 +1696,25 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_compose_j
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_get_evidence(
     void* handle, uint64_t session_id, PrometheusCompiledModelSessionEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_destroy(void* handle, uint64_t session_id);
+/* reactor_api.h:2809-2821: the compiled-model owner the Z-Image bridge drives
+   (tools/prometheus_zimage_bridge/reactor_windows.go:86-115): one block,
+   created bound to NoiseRefiner 0 for an existing session, retargeted in
+   place through NoiseRefiner 1, ContextRefiner 0/1 and MainTransformer 0..29
+   (the session's position names the next block), reset for a new evaluation.
+   The PREFETCH profile is not selected here (profile_fallback_reason 1), so
+   prefetch and activate_prefetch report REBIND_FAILED as the reference does
+   without a separate transfer queue. */
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_owner_create(
+    void* handle, const PrometheusNoiseRefinerRebindRequest* request, uint64_t* out_block_id,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_retarget(
+    void* handle, const PrometheusCompiledModelRetargetRequest* request, PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_prefetch(
+    void* handle, const PrometheusCompiledModelPrefetchRequest* request, PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_activate_prefetch(
+    void* handle, uint64_t session_id, PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_evaluation_reset(
+    void* handle, uint64_t session_id, PrometheusCompiledModelSessionEvidence* out_evidence);
 
 #ifdef __cplusplus
 }

@@ -67,6 +67,8 @@ const uint64_t kContextWeightBytes[11] = {256ull,       29491200ull, 256ull,    
 // (the reference's generated models/zimage-turbo/resolved_descriptor.h).
 const uint64_t kNoiseAggregate[2] = {0xa1ba526898a2a752ull, 0x80c0cd75f44cc434ull};
 const uint64_t kContextAggregate[2] = {0xc08b908a921a80e1ull, 0x30268c3b0d7a6fafull};
+const uint64_t kNoiseMemoryPlan = 654891776ull;
+const uint64_t kNoiseExecutionPlan = 6517444848718386192ull;
 const uint64_t kContextMemoryPlan = 536870912ull;
 const uint64_t kContextExecutionPlan = 0xa30b2ac6ff947b21ull;
 const uint64_t kContextCanonical[2] = {0xd2b8167de614da25ull, 0x08377e8a46b65cffull};
@@ -119,9 +121,11 @@ struct WeightSet {
 
 struct ModelBlock {
   bool created = false;
+  bool shared = false;  // the compiled-model owner: retargeted through every family
   uint64_t id = 0;
   Program program = kProgProof;
   int tokens = 0;
+  int alloc_tokens = 0;  // buffers are sized for this many tokens (the owner: the joint 1056)
   // declared program
   uint32_t family = 0, parameter_set = 0, shader_id = 0, weight_count = 0, step_count = 0;
   uint32_t steps[PROM_MODEL_BLOCK_MAX_STEPS] = {};
@@ -172,6 +176,11 @@ struct ModelSession {
   bool joint_writing = false;
   uint64_t joint_image_generation = 0, joint_context_generation = 0, compositions = 0;
   uint64_t active_block_id = 0, binding_generation = 0, replay = 0, cold_allocations = 0;
+  // owner position: 0 NoiseRefiner 0, 1 NoiseRefiner 1, 2 ContextRefiner 0,
+  // 3 ContextRefiner 1, 4 + i MainTransformer layer i
+  uint32_t retarget_position = 0;
+  uint64_t evaluation_generation = 0;
+  uint32_t profile_fallback = 0;
   int32_t last_detail = 0;
 };
 
@@ -359,6 +368,7 @@ void fill_session_evidence(const ModelSession* s, PrometheusCompiledModelSession
   ev->composition_count = s->compositions;
   ev->requested_execution_profile = s->requested_profile;
   ev->selected_execution_profile = PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY;
+  ev->profile_fallback_reason = s->profile_fallback;
   ev->requested_main_attention_route = s->requested_route;
   ev->selected_main_attention_route = PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL;
 }
@@ -661,7 +671,7 @@ bool alloc_block_buffers(ModelBlock* b) {
     b->pipelines = 1;
     return ok && alloc_set(b, &b->active);
   }
-  const int T = b->tokens;
+  const int T = b->alloc_tokens;
   const size_t act = (size_t)T * kWidth * 4;
   const size_t ws_bytes = zimage_workspace_layout(T, kWidth, kHeads, kFfn, b->ws_off);
   const bool ok = alloc_dev(b, &b->staging, max_weight) && alloc_dev(b, reinterpret_cast<void**>(&b->x), act) &&
@@ -675,14 +685,22 @@ bool alloc_block_buffers(ModelBlock* b) {
                       (uint64_t)T * 12 + ws_bytes;
   b->audit_alloc_bytes = 0;  // audits copy workspace stages directly
   b->pipelines = 13;         // the fixed kernel chain of the block
-  if (!ok || !alloc_set(b, &b->active)) return false;
-  // Coordinates and the RoPE table are fixed per program: build them once.
+  return ok && alloc_set(b, &b->active);
+}
+
+// Selects the Z-Image program (sequence length, workspace offsets inside the
+// allocation, coordinates and RoPE table); the owner calls it on every retarget.
+bool set_program(ModelBlock* b, Program program) {
+  b->program = program;
+  b->tokens = program == kProgNoise ? kImageTokens : (program == kProgContext ? kContextTokens : kJointTokens);
+  (void)zimage_workspace_layout(b->tokens, kWidth, kHeads, kFfn, b->ws_off);
   hipStream_t st = ctx().stream;
-  const int image = b->program == kProgContext ? 0 : kImageTokens;
-  const int context = b->program == kProgNoise ? 0 : kContextTokens;
-  hipLaunchKernelGGL(coords_kernel, dim3((T + 255) / 256), dim3(256), 0, st, b->coords, image, context);
+  const int image = program == kProgContext ? 0 : kImageTokens;
+  const int context = program == kProgNoise ? 0 : kContextTokens;
+  hipLaunchKernelGGL(coords_kernel, dim3((b->tokens + 255) / 256), dim3(256), 0, st, b->coords, image, context);
   if (hipGetLastError() != hipSuccess) return false;
-  if (launch_zimage_rope_table(b->coords, reinterpret_cast<float2*>(b->ws + b->ws_off[kZRope]), T, st) != hipSuccess)
+  if (launch_zimage_rope_table(b->coords, reinterpret_cast<float2*>(b->ws + b->ws_off[kZRope]), b->tokens, st) !=
+      hipSuccess)
     return false;
   return hipStreamSynchronize(st) == hipSuccess;
 }
@@ -690,7 +708,7 @@ bool alloc_block_buffers(ModelBlock* b) {
 // ---------------------------------------------------------------- create
 
 int create_block(Runtime* rt, const PrometheusModelBlockCreateRequest* r, uint64_t* out_id,
-                 PrometheusModelBlockEvidence* ev) {
+                 PrometheusModelBlockEvidence* ev, bool shared = false) {
   if (out_id) *out_id = 0;
   if (!validate_create(r) || out_id == nullptr) {
     fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
@@ -736,7 +754,10 @@ int create_block(Runtime* rt, const PrometheusModelBlockCreateRequest* r, uint64
   b->step_count = r->step_count;
   memcpy(b->steps, r->steps, sizeof(b->steps));
   memcpy(b->decl, r->weights, sizeof(b->decl));
-  if ((rt->test_flags & PROM_TESTCFG_FAIL_BUFFER_ALLOC) != 0u || !alloc_block_buffers(b)) {
+  b->shared = shared;
+  b->alloc_tokens = shared ? kJointTokens : b->tokens;
+  if ((rt->test_flags & PROM_TESTCFG_FAIL_BUFFER_ALLOC) != 0u || !alloc_block_buffers(b) ||
+      (b->program != kProgProof && !set_program(b, b->program))) {
     release_block(b);
     fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED, ev);
     return PROM_ERROR;
@@ -1194,6 +1215,46 @@ bool joint_valid(const ModelSession* s) {
 ModelSession* find_session(Runtime* rt, uint64_t id) {
   if (rt->model == nullptr || !rt->model->session.created || rt->model->session.id != id) return nullptr;
   return &rt->model->session;
+}
+
+// ---------------------------------------------------------------- compiled-model owner
+
+struct Target {
+  Program program;
+  uint32_t family, parameter_set, count, local;
+  uint64_t aggregate;
+  const uint64_t* bytes;
+};
+
+// The block the owner binds at `position` (reactor_vulkan_model_block.c:4474-4503).
+bool target_at(uint32_t position, Target* t) {
+  if (position <= 1) {
+    *t = Target{kProgNoise, PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO, position + 1, 13u, position,
+                kNoiseAggregate[position], kNoiseWeightBytes};
+    return true;
+  }
+  if (position <= 3) {
+    *t = Target{kProgContext, PROM_CONTEXT_REFINER_FAMILY_Z_IMAGE_TURBO, position - 1, 11u, position - 2,
+                kContextAggregate[position - 2], kContextWeightBytes};
+    return true;
+  }
+  if (position < 34) {
+    const uint32_t layer = position - 4;
+    *t = Target{kProgMain, PROM_MAIN_TRANSFORMER_FAMILY_Z_IMAGE_TURBO, layer + 1, 13u, layer, kMainAggregate[layer],
+                kNoiseWeightBytes};
+    return true;
+  }
+  return false;
+}
+
+bool retarget_uploads_match(const ModelBlock* b, const PrometheusModelBlockWeightUpload* uploads, const Target& t) {
+  for (uint32_t i = 0; i < t.count; ++i) {
+    const PrometheusModelBlockWeightUpload& u = uploads[i];
+    if (u.binding_index != i || u.bytes == nullptr || u.content_identity == 0 || u.layout_identity == 0 ||
+        u.byte_count != t.bytes[i] || u.byte_count > b->staging_bytes)
+      return false;
+  }
+  return true;
 }
 
 }  // namespace
@@ -1812,6 +1873,166 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_destroy(v
     ModelSession* s = find_session(rt, session_id);
     if (s == nullptr || !reap(&rt->model->block)) return PROM_ERROR;
     release_session(s);
+    return PROM_OK;
+  });
+}
+
+// reactor_vulkan_model_block.c:4348-4450: the shared owner, bound to NoiseRefiner 0.
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_owner_create(
+    void* handle, const PrometheusNoiseRefinerRebindRequest* request, uint64_t* out_block_id,
+    PrometheusModelBlockEvidence* out_evidence) {
+  if (out_block_id) *out_block_id = 0;
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusNoiseRefinerRebindRequest* r = request;
+    if (r == nullptr || out_block_id == nullptr || r->struct_size != sizeof(*r) || r->model_local_block_id != 0u ||
+        r->uploads == nullptr || r->upload_count != 13u || r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID ||
+        rt->model == nullptr || rt->model->block.created || !rt->model->session.created ||
+        rt->model->session.lock != r->lock_identity) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelSession* s = &rt->model->session;
+    // A weight prefetch needs a transfer queue of its own; this library runs
+    // every copy on the runtime stream, so PREFETCH falls back (reason 1).
+    s->profile_fallback = s->requested_profile == PROM_MODEL_EXECUTION_PROFILE_PREFETCH ? 1u : 0u;
+    PrometheusModelBlockCreateRequest c;
+    memset(&c, 0, sizeof(c));
+    c.struct_size = sizeof(c);
+    c.assembly_family = PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO;
+    c.parameter_set = PROM_NOISE_REFINER_PARAMETER_SET_0;
+    c.parameter_set_aggregate_identity = kNoiseAggregate[0];
+    c.model_contract_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.weight_identity = kNoiseAggregate[0];
+    c.shader_portfolio_identity = kNoiseExecutionPlan;
+    c.precision_policy_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.capability_route_identity = PROM_ZIMAGE_TURBO_LOCK_ID;
+    c.memory_ceiling_bytes = kNoiseMemoryPlan + (uint64_t)kImageTokens * kWidth * 4 + (uint64_t)kContextTokens * kFfn * 4;
+    c.external_input_bytes = (uint64_t)kImageTokens * kWidth * 2;
+    c.audit_bytes = PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES;
+    c.shader_id = kShaderNoise;
+    c.weight_count = 13u;
+    c.step_count = PROM_MODEL_BLOCK_MAX_STEPS;
+    memcpy(c.steps, kSteps, sizeof(c.steps));
+    for (uint32_t i = 0; i < 13u; ++i) {
+      c.weights[i].content_identity = r->uploads[i].content_identity;
+      c.weights[i].layout_identity = r->uploads[i].layout_identity;
+      c.weights[i].byte_count = r->uploads[i].byte_count;
+    }
+    if (create_block(rt, &c, out_block_id, out_evidence, true) != PROM_OK) return PROM_ERROR;
+    if (upload_weights(rt, *out_block_id, r->uploads, 13u, out_evidence) != PROM_OK) {
+      release_block(&rt->model->block);
+      *out_block_id = 0;
+      return PROM_ERROR;
+    }
+    s->evaluation_generation = 1;
+    s->retarget_position = 1;
+    s->active_block_id = *out_block_id;
+    s->binding_generation = rt->model->block.binding_generation;
+    return PROM_OK;
+  });
+}
+
+// reactor_vulkan_model_block.c:4452-4543: the owner moves to the block its
+// position names; the weights are overwritten in place.
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_retarget(
+    void* handle, const PrometheusCompiledModelRetargetRequest* request, PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    const PrometheusCompiledModelRetargetRequest* r = request;
+    if (r == nullptr || r->struct_size != sizeof(*r) || r->uploads == nullptr ||
+        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID || rt->model == nullptr) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    ModelBlock* b = &rt->model->block;
+    ModelSession* s = &rt->model->session;
+    if (!b->created || !b->shared || !s->created || s->id != r->session_identity || s->lock != r->lock_identity ||
+        !reap(b)) {
+      if (b->created) {
+        mark_failure(b, b->quarantined ? PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN
+                                       : PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED);
+        fill_evidence(b, b->last_detail, out_evidence);
+      } else {
+        fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, out_evidence);
+      }
+      return PROM_ERROR;
+    }
+    Target t;
+    if (!target_at(s->retarget_position, &t) || r->model_local_block_id != t.local || r->upload_count != t.count ||
+        !retarget_uploads_match(b, r->uploads, t)) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    if (b->program != t.program && !set_program(b, t.program)) {
+      mark_failure(b, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED);
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    b->family = t.family;
+    b->weight_count = t.count;
+    if (!change_weights(rt, b, r->uploads, t.count, false)) {
+      fill_evidence(b, b->last_detail, out_evidence);
+      return PROM_ERROR;
+    }
+    b->parameter_set = t.parameter_set;
+    b->aggregate = t.aggregate;
+    s->retarget_position += 1;
+    s->active_block_id = b->id;
+    s->binding_generation = b->binding_generation;
+    fill_evidence(b, 0, out_evidence);
+    return PROM_OK;
+  });
+}
+
+// reactor_vulkan_model_block.c:4545-4715: only under the PREFETCH profile,
+// which this library does not select (see owner_create).
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_prefetch(
+    void* handle, const PrometheusCompiledModelPrefetchRequest* request, PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime*) -> int {
+    const PrometheusCompiledModelPrefetchRequest* r = request;
+    if (r == nullptr || r->struct_size != sizeof(*r) || r->uploads == nullptr ||
+        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID) {
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+      return PROM_ERROR;
+    }
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+    return PROM_ERROR;
+  });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_activate_prefetch(
+    void* handle, uint64_t session_id, PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    ModelBlock* b = rt->model && rt->model->block.created ? &rt->model->block : nullptr;
+    (void)session_id;
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+    return PROM_ERROR;
+  });
+}
+
+// reactor_vulkan_model_block.c:4717-4752 and PromSessionReset
+// (PrometheusModelBlock.concept:1080-1088): a new evaluation starts at NoiseRefiner 0.
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_evaluation_reset(
+    void* handle, uint64_t session_id, PrometheusCompiledModelSessionEvidence* out_evidence) {
+  return with_session_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    ModelSession* s = find_session(rt, session_id);
+    ModelBlock* b = rt->model ? &rt->model->block : nullptr;
+    if (s == nullptr || b == nullptr || !b->created || !b->shared || s->joint_writing || !reap(b)) {
+      fill_session_evidence(nullptr, out_evidence, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    for (Stream& st : s->streams) st = Stream{st.generation, 0, 0, false};
+    s->joint_image_generation = 0;
+    s->joint_context_generation = 0;
+    s->evaluation_generation += 1;
+    s->retarget_position = 0;
+    s->active_block_id = 0;
+    s->binding_generation = 0;
+    s->replay = 0;
+    b->output_valid = false;
+    b->audit_valid = false;
+    b->replay_identity = 0;
+    s->last_detail = 0;
+    fill_session_evidence(s, out_evidence, 0);
     return PROM_OK;
   });
 }

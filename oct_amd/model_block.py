@@ -321,3 +321,46 @@ class ResidentModel:
 
     def session_destroy(self, session_id: int) -> int:
         return self.lib.prometheus_reactor_runtime_compiled_model_session_destroy(self.h, session_id)
+
+    # -- the compiled-model owner (tools/prometheus_zimage_bridge/reactor_windows.go:190-238)
+    def owner_create(self, weights: dict, content_base: int = 0x5E00):
+        uploads = zimage_uploads(weights, content_base)
+        r = self._lock_request(uploads, 0, p.PROM_ZIMAGE_TURBO_LOCK_ID)
+        ev = p.PrometheusModelBlockEvidence()
+        bid = c_uint64(0)
+        rc = self.lib.prometheus_reactor_runtime_compiled_model_owner_create(self.h, byref(r), byref(bid), byref(ev))
+        return rc, bid.value, ev
+
+    def _retarget_request(self, session_id: int, local: int, uploads: Uploads):
+        r = p.PrometheusCompiledModelRetargetRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.session_identity = session_id
+        r.lock_identity = p.PROM_ZIMAGE_TURBO_LOCK_ID
+        r.model_local_block_id = local
+        r.upload_count = len(uploads)
+        r.uploads = ctypes.cast(uploads.items, ctypes.c_void_p)
+        return r
+
+    def retarget(self, session_id: int, local: int, weights: dict, names=ZIMAGE_TENSORS, content_base: int = 0x5F00):
+        uploads = zimage_uploads(weights, content_base, names)
+        r = self._retarget_request(session_id, local, uploads)
+        ev = p.PrometheusModelBlockEvidence()
+        rc = self.lib.prometheus_reactor_runtime_compiled_model_retarget(self.h, byref(r), byref(ev))
+        return rc, ev
+
+    def prefetch(self, session_id: int, local: int, weights: dict, names=ZIMAGE_TENSORS):
+        uploads = zimage_uploads(weights, 0x6F00, names)
+        r = self._retarget_request(session_id, local, uploads)
+        ev = p.PrometheusModelBlockEvidence()
+        rc = self.lib.prometheus_reactor_runtime_compiled_model_prefetch(self.h, byref(r), byref(ev))
+        return rc, ev
+
+    def activate_prefetch(self, session_id: int):
+        ev = p.PrometheusModelBlockEvidence()
+        rc = self.lib.prometheus_reactor_runtime_compiled_model_activate_prefetch(self.h, session_id, byref(ev))
+        return rc, ev
+
+    def evaluation_reset(self, session_id: int):
+        ev = p.PrometheusCompiledModelSessionEvidence()
+        rc = self.lib.prometheus_reactor_runtime_compiled_model_evaluation_reset(self.h, session_id, byref(ev))
+        return rc, ev

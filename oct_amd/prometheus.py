@@ -642,6 +642,12 @@ class PrometheusModelBlockEvidence(Structure):
         "u64 m6a_cooperative_execute_gpu_ns, u64 m6a_w3_segment_repack_gpu_ns")
 
 
+class PrometheusCompiledModelRetargetRequest(Structure):
+    """reactor_api.h:1237-1249 (also the prefetch request)"""
+    _fields_ = _fields("u32 struct_size, u64 session_identity, u64 lock_identity, u32 model_local_block_id, "
+                       "u32 upload_count, p uploads")
+
+
 class PrometheusCompiledModelSessionCreateRequest(Structure):
     _fields_ = _fields("u32 struct_size, u64 lock_identity, u32 execution_profile, u32 main_attention_route_policy")
 
@@ -853,6 +859,17 @@ _SIGNATURES = {
     "prometheus_reactor_runtime_compiled_model_session_get_evidence": (
         c_int, [c_void_p, c_uint64, POINTER(PrometheusCompiledModelSessionEvidence)]),
     "prometheus_reactor_runtime_compiled_model_session_destroy": (c_int, [c_void_p, c_uint64]),
+    "prometheus_reactor_runtime_compiled_model_owner_create": (
+        c_int, [c_void_p, POINTER(PrometheusNoiseRefinerRebindRequest), POINTER(c_uint64),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_retarget": (
+        c_int, [c_void_p, POINTER(PrometheusCompiledModelRetargetRequest), POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_prefetch": (
+        c_int, [c_void_p, POINTER(PrometheusCompiledModelRetargetRequest), POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_activate_prefetch": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_evaluation_reset": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusCompiledModelSessionEvidence)]),
 }
 
 MANDATORY_SYMBOLS = (

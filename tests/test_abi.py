@@ -94,6 +94,8 @@ STRUCTS = {
     "PrometheusCompiledModelSessionCaptureRequest": p.PrometheusCompiledModelSessionCaptureRequest,
     "PrometheusCompiledModelSessionComposeRequest": p.PrometheusCompiledModelSessionComposeRequest,
     "PrometheusCompiledModelSessionEvidence": p.PrometheusCompiledModelSessionEvidence,
+    "PrometheusCompiledModelRetargetRequest": p.PrometheusCompiledModelRetargetRequest,
+    "PrometheusCompiledModelPrefetchRequest": p.PrometheusCompiledModelRetargetRequest,
 }
 MODEL_BLOCK_STRUCTS = tuple(n for n in STRUCTS if "ModelBlock" in n or "Refiner" in n or "MainTransformer" in n
                             or "CompiledModel" in n)

@@ -363,3 +363,85 @@ def test_session_main_transformer_chain(model, weights, inputs):
     assert model.destroy(mid) == p.PROM_OK
     assert model.session_destroy(sid) == p.PROM_OK
     assert model.session_destroy(sid) == p.PROM_ERROR
+
+
+# ------------------------------------------------------------ compiled-model owner
+def test_compiled_owner_drives_the_bridge_sequence(model, weights, inputs):
+    """The call sequence of tools/prometheus_zimage_bridge/reactor_windows.go:805-1000
+    (MINIMUM_MEMORY profile): one owner retargeted through NoiseRefiner 0/1,
+    ContextRefiner 0/1 and MainTransformer layers, then a reset evaluation."""
+    x_bits, t_bits, ctx = inputs
+    cond = oracle.from_bf16(t_bits).astype(np.float64)
+    rc, sid, sev = model.session_create(profile=2)  # PREFETCH requested
+    assert rc == p.PROM_OK
+    rc, oid, ev = model.owner_create(weights["nr0"])
+    assert rc == p.PROM_OK and oid != 0, ev.detail_code
+    sev = model.session_evidence(sid)[1]
+    assert sev.selected_execution_profile == 1 and sev.profile_fallback_reason == 1
+    assert model.prefetch(sid, 1, weights["nr1"])[1].detail_code == D["REBIND_FAILED"]
+    rc, ev = model.noise_refiner_execute(oid, x_bits, t_bits)
+    assert rc == p.PROM_OK
+    first_nr0 = np.zeros(T_IMG * W, np.float32)
+    assert model.audit_final("noise", oid, ev.output_generation, first_nr0)[0] == p.PROM_OK
+    # the position names the next block: ContextRefiner weights are refused here
+    rc, ev = model.retarget(sid, 0, weights["cr0"], mb.CONTEXT_TENSORS)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"]
+    rc, ev = model.retarget(sid, 1, weights["nr1"])
+    assert rc == p.PROM_OK and ev.parameter_set == 2
+    gen = ev.output_generation
+    rc, ev = model.noise_refiner_resident(oid, gen)
+    assert rc == p.PROM_OK
+    rc, sev = model.session_capture(sid, oid, ev.output_generation)
+    assert rc == p.PROM_OK and sev.prepared_image_generation == 1
+    image = np.zeros(T_IMG * W, np.float32)
+    assert model.audit_final("noise", oid, ev.output_generation, image)[0] == p.PROM_OK
+    # ContextRefiner 0 -> 1 on the same owner
+    rc, ev = model.retarget(sid, 0, weights["cr0"], mb.CONTEXT_TENSORS)
+    assert rc == p.PROM_OK and ev.assembly_family == p.PROM_CONTEXT_REFINER_FAMILY and ev.weight_count == 11
+    rc, ev = model.context_refiner0_execute(oid, ctx)
+    assert rc == p.PROM_OK
+    rc, ev = model.retarget(sid, 1, weights["cr1"], mb.CONTEXT_TENSORS)
+    assert rc == p.PROM_OK
+    rc, ev = model.context_refiner_resident(oid, ev.output_generation)
+    assert rc == p.PROM_OK
+    rc, sev = model.session_capture(sid, oid, ev.output_generation)
+    assert rc == p.PROM_OK and sev.prepared_context_generation == 1
+    context = np.zeros(T_CTX * W, np.float32)
+    assert model.audit_final("context", oid, ev.output_generation, context)[0] == p.PROM_OK
+    np.testing.assert_allclose(context.reshape(T_CTX, W)[:2],
+                               blocks.zimage_block_f64(
+                                   blocks.zimage_block_f64(ctx, blocks.context_coordinates(), weights["cr0"], None),
+                                   blocks.context_coordinates(), weights["cr1"], None)[:2], rtol=0, atol=1e-3)
+    rc, sev = model.session_compose(sid, 1, 1)
+    assert rc == p.PROM_OK
+    joint_gen = sev.joint_generation
+    # MainTransformer layers 0 and 1 in chain mode
+    for layer, name in ((0, "main0"), (1, "nr1")):
+        rc, ev = model.retarget(sid, layer, weights[name])
+        assert rc == p.PROM_OK and ev.parameter_set == layer + 1, (layer, ev.detail_code)
+        rc, ev = model.main_transformer_execute(oid, sid, layer, t_bits, 1, 1, joint_gen, chain=True)
+        assert rc == p.PROM_OK, (layer, ev.detail_code)
+        joint_gen += 1
+    out = np.zeros(T_JOINT * W, np.float32)
+    assert model.audit_final("main", oid, ev.output_generation, out)[0] == p.PROM_OK
+    joint = np.concatenate((image.reshape(T_IMG, W), context.reshape(T_CTX, W)), axis=0)
+    coords = blocks.joint_coordinates(32, 32, 32)
+    mid = blocks.zimage_block_f64(joint, coords, weights["main0"], cond)
+    ref = blocks.zimage_block_f64(mid, coords, weights["nr1"], cond, rows=ROWS_JOINT)
+    err = rel_l2(out.reshape(T_JOINT, W)[ROWS_JOINT], ref)
+    print(f"owner chain: main layers 0..1 rel L2 {err:.3e}", flush=True)
+    assert err <= BAR
+    # a new evaluation starts again at NoiseRefiner 0 and reproduces it exactly
+    rc, sev = model.evaluation_reset(sid)
+    assert rc == p.PROM_OK and sev.joint_generation == joint_gen
+    rc, ev = model.retarget(sid, 1, weights["nr1"])
+    assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"]
+    rc, ev = model.retarget(sid, 0, weights["nr0"])
+    assert rc == p.PROM_OK and ev.parameter_set == 1
+    rc, ev = model.noise_refiner_execute(oid, x_bits, t_bits)
+    assert rc == p.PROM_OK
+    again = np.zeros(T_IMG * W, np.float32)
+    assert model.audit_final("noise", oid, ev.output_generation, again)[0] == p.PROM_OK
+    np.testing.assert_array_equal(again, first_nr0)
+    assert model.destroy(oid) == p.PROM_OK
+    assert model.session_destroy(sid) == p.PROM_OK

@@ -238,3 +238,36 @@ def test_reference_struct_sizes():
     assert ctypes.sizeof(p.PrometheusCompiledModelSessionEvidence) == 176
     assert ctypes.sizeof(p.PrometheusModelBlockWeightUpload) == 40
     assert ctypes.sizeof(p.PrometheusMainTransformerExecuteRequest) == 96
+
+
+def test_owner_entries_validate_before_any_work(model):
+    import numpy as np
+
+    ups = FakeUploads(NOISE_BYTES)
+    r = model._lock_request(ups, 0, p.PROM_ZIMAGE_TURBO_LOCK_ID)
+    ev = p.PrometheusModelBlockEvidence()
+    bid = ctypes.c_uint64(5)
+    # no session: the owner needs one of the same lock
+    rc = model.lib.prometheus_reactor_runtime_compiled_model_owner_create(model.h, ctypes.byref(r), ctypes.byref(bid),
+                                                                          ctypes.byref(ev))
+    assert rc == p.PROM_ERROR and bid.value == 0 and ev.detail_code == D["INVALID_REQUEST"]
+    for local, count in ((1, 13), (0, 12)):
+        r = model._lock_request(ups, local, p.PROM_ZIMAGE_TURBO_LOCK_ID)
+        r.upload_count = count
+        rc = model.lib.prometheus_reactor_runtime_compiled_model_owner_create(model.h, ctypes.byref(r),
+                                                                              ctypes.byref(bid), ctypes.byref(ev))
+        assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"]
+    rr = model._retarget_request(1, 0, ups)
+    rr.lock_identity = 0x77
+    rc = model.lib.prometheus_reactor_runtime_compiled_model_retarget(model.h, ctypes.byref(rr), ctypes.byref(ev))
+    assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"]
+    rr = model._retarget_request(1, 0, ups)
+    rc = model.lib.prometheus_reactor_runtime_compiled_model_retarget(model.h, ctypes.byref(rr), ctypes.byref(ev))
+    assert rc == p.PROM_ERROR  # no owner
+    rc = model.lib.prometheus_reactor_runtime_compiled_model_prefetch(model.h, ctypes.byref(rr), ctypes.byref(ev))
+    assert rc == p.PROM_ERROR and ev.detail_code == D["REBIND_FAILED"]
+    rc, ev = model.activate_prefetch(1)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["REBIND_FAILED"]
+    rc, sev = model.evaluation_reset(1)
+    assert rc == p.PROM_ERROR and sev.detail_code == D["SESSION_INVALID_REQUEST"]
+    assert ctypes.sizeof(p.PrometheusCompiledModelRetargetRequest) == 40
