@@ -35,6 +35,7 @@ namespace {
 constexpr uint32_t kFftThreads = 256;
 constexpr uint32_t kFftMaxLds = 4096;  // double2 elements per workgroup (64 KiB)
 constexpr uint32_t kFftMaxLog2 = 20;
+constexpr uint32_t kFftPerThread = kFftMaxLds / kFftThreads;  // elements each thread loads and stores
 
 // Go's complex product (xu - yv) + (xv + yu)i with every operation rounded.
 __device__ __forceinline__ double2 cmul(double2 w, double2 v) {
@@ -51,72 +52,124 @@ __device__ __forceinline__ double2 cmul(double2 w, double2 v) {
 // seq_fast_in / seq_fast_out pick the thread order of the global accesses
 // (adjacent threads on adjacent sequences when the sequences are adjacent in
 // memory).  post multiplies output k of sequence q by W_N^(q*k).
+//
+// The sub-transform's twiddles W_L^j = roots[j * N / L] (j < L/2) are copied
+// to LDS once.  Butterfly stages run two at a time: a thread loads the four
+// elements p, p+h, p+2h, p+3h of a stage pair (h = 2^(lg-1)), performs the two
+// stage-lg butterflies and then the two stage-(lg+1) butterflies in
+// registers, and stores them back -- the same operations on the same values as
+// one stage per barrier, with half the barriers and LDS round trips.
 __global__ __launch_bounds__(256) void fft_lds_kernel(const double2* __restrict__ in, double2* __restrict__ out,
                                                       const double2* __restrict__ roots, uint32_t n_total,
                                                       uint32_t log2l, uint32_t log2seqs, uint64_t in_seq,
                                                       uint64_t in_elem, uint64_t out_seq, uint64_t out_elem,
                                                       int post, int seq_fast_in, int seq_fast_out) {
 #pragma clang fp contract(off)
-  extern __shared__ double2 buf[];
+  extern __shared__ double2 smem[];
   const uint32_t L = 1u << log2l;
   const uint32_t seqs = 1u << log2seqs;
   const uint32_t total = L << log2seqs;
-  const uint64_t q0 = (uint64_t)blockIdx.x << log2seqs;
-  for (uint32_t e = threadIdx.x; e < total; e += blockDim.x) {
-    uint32_t s, i;
-    if (seq_fast_in) {
-      s = e & (seqs - 1);
-      i = e >> log2seqs;
-    } else {
-      s = e >> log2l;
-      i = e & (L - 1);
+  double2* buf = smem;
+  double2* tw = smem + total;
+  const uint32_t tstride = n_total >> log2l;
+  for (uint32_t j = threadIdx.x; j < (L >> 1); j += blockDim.x) tw[j] = roots[(size_t)j * tstride];
+  // Hardware deals workgroups to the 8 XCDs round-robin; remap so that each
+  // XCD takes a contiguous range of sequences and the 128-byte lines shared
+  // by neighbouring sequences (strided passes) are filled in one L2.
+  uint32_t blk = blockIdx.x;
+  if ((gridDim.x & 7u) == 0u) blk = (blk & 7u) * (gridDim.x >> 3) + (blk >> 3);
+  const uint64_t q0 = (uint64_t)blk << log2seqs;
+  // Every global load of the thread is issued before the first LDS store, so
+  // the strided reads overlap instead of waiting one at a time.
+  double2 v[kFftPerThread];
+#pragma unroll
+  for (uint32_t u = 0; u < kFftPerThread; ++u) {
+    const uint32_t e = threadIdx.x + u * kFftThreads;
+    if (e < total) {
+      const uint32_t s = seq_fast_in ? (e & (seqs - 1)) : (e >> log2l);
+      const uint32_t i = seq_fast_in ? (e >> log2seqs) : (e & (L - 1));
+      v[u] = in[(q0 + s) * in_seq + (uint64_t)i * in_elem];
     }
-    const double2 v = in[(q0 + s) * in_seq + (uint64_t)i * in_elem];
-    const uint32_t r = log2l == 0 ? 0u : (__brev(i) >> (32u - log2l));
-    buf[(s << log2l) + r] = v;
+  }
+#pragma unroll
+  for (uint32_t u = 0; u < kFftPerThread; ++u) {
+    const uint32_t e = threadIdx.x + u * kFftThreads;
+    if (e < total) {
+      const uint32_t s = seq_fast_in ? (e & (seqs - 1)) : (e >> log2l);
+      const uint32_t i = seq_fast_in ? (e >> log2seqs) : (e & (L - 1));
+      const uint32_t r = log2l == 0 ? 0u : (__brev(i) >> (32u - log2l));
+      buf[(s << log2l) + r] = v[u];
+    }
   }
   __syncthreads();
-  const uint32_t butterflies = total >> 1;
-  for (uint32_t lg = 1; lg <= log2l; ++lg) {
-    const uint32_t half = 1u << (lg - 1);
-    const uint32_t stride = n_total >> lg;  // N / span
-    for (uint32_t b = threadIdx.x; b < butterflies; b += blockDim.x) {
+  uint32_t lg = 1;
+  for (; lg + 1 <= log2l; lg += 2) {
+    const uint32_t h = 1u << (lg - 1);
+    const uint32_t groups = total >> 2;
+    for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
+      const uint32_t s = g >> (log2l - 2);
+      const uint32_t gg = g & ((L >> 2) - 1);
+      const uint32_t j = gg & (h - 1);
+      const uint32_t p = (s << log2l) + ((gg >> (lg - 1)) << (lg + 1)) + j;
+      const double2 a0 = buf[p], a1 = buf[p + h], a2 = buf[p + 2 * h], a3 = buf[p + 3 * h];
+      const double2 w1 = tw[j << (log2l - lg)];
+      double2 t = cmul(w1, a1);
+      const double2 b0 = make_double2(a0.x + t.x, a0.y + t.y);
+      const double2 b1 = make_double2(a0.x - t.x, a0.y - t.y);
+      t = cmul(w1, a3);
+      const double2 b2 = make_double2(a2.x + t.x, a2.y + t.y);
+      const double2 b3 = make_double2(a2.x - t.x, a2.y - t.y);
+      t = cmul(tw[j << (log2l - lg - 1)], b2);
+      buf[p] = make_double2(b0.x + t.x, b0.y + t.y);
+      buf[p + 2 * h] = make_double2(b0.x - t.x, b0.y - t.y);
+      t = cmul(tw[(j + h) << (log2l - lg - 1)], b3);
+      buf[p + h] = make_double2(b1.x + t.x, b1.y + t.y);
+      buf[p + 3 * h] = make_double2(b1.x - t.x, b1.y - t.y);
+    }
+    __syncthreads();
+  }
+  if (lg == log2l) {  // an odd stage count leaves the last stage (span L) alone
+    const uint32_t half = L >> 1;
+    for (uint32_t b = threadIdx.x; b < (total >> 1); b += blockDim.x) {
       const uint32_t s = b >> (log2l - 1);
-      const uint32_t bb = b & ((L >> 1) - 1);
-      const uint32_t j = bb & (half - 1);
-      const uint32_t base = (bb >> (lg - 1)) << lg;
-      const uint32_t p = (s << log2l) + base + j;
-      const uint32_t q = p + half;
-      const double2 t = cmul(roots[(size_t)j * stride], buf[q]);
+      const uint32_t j = b & (half - 1);
+      const uint32_t p = (s << log2l) + j;
+      const double2 t = cmul(tw[j], buf[p + half]);
       const double2 a = buf[p];
       buf[p] = make_double2(a.x + t.x, a.y + t.y);
-      buf[q] = make_double2(a.x - t.x, a.y - t.y);
+      buf[p + half] = make_double2(a.x - t.x, a.y - t.y);
     }
     __syncthreads();
   }
   const uint32_t half_n = n_total >> 1;
-  for (uint32_t e = threadIdx.x; e < total; e += blockDim.x) {
-    uint32_t s, k;
-    if (seq_fast_out) {
-      s = e & (seqs - 1);
-      k = e >> log2seqs;
-    } else {
-      s = e >> log2l;
-      k = e & (L - 1);
-    }
-    double2 v = buf[(s << log2l) + k];
-    if (post) {
-      const uint64_t p = (q0 + s) * (uint64_t)k;  // < N
-      double2 w;
-      if (p < half_n) {
-        w = roots[p];
-      } else {
-        const double2 r = roots[p - half_n];
-        w = make_double2(-r.x, -r.y);
+  double2 w[kFftPerThread];
+#pragma unroll
+  for (uint32_t u = 0; u < kFftPerThread; ++u) {
+    const uint32_t e = threadIdx.x + u * kFftThreads;
+    if (e < total) {
+      const uint32_t s = seq_fast_out ? (e & (seqs - 1)) : (e >> log2l);
+      const uint32_t k = seq_fast_out ? (e >> log2seqs) : (e & (L - 1));
+      v[u] = buf[(s << log2l) + k];
+      if (post) {
+        const uint64_t p = (q0 + s) * (uint64_t)k;  // < N
+        w[u] = roots[p < half_n ? p : p - half_n];
       }
-      v = cmul(w, v);
     }
-    out[(q0 + s) * out_seq + (uint64_t)k * out_elem] = v;
+  }
+#pragma unroll
+  for (uint32_t u = 0; u < kFftPerThread; ++u) {
+    const uint32_t e = threadIdx.x + u * kFftThreads;
+    if (e < total) {
+      const uint32_t s = seq_fast_out ? (e & (seqs - 1)) : (e >> log2l);
+      const uint32_t k = seq_fast_out ? (e >> log2seqs) : (e & (L - 1));
+      double2 r = v[u];
+      if (post) {
+        const uint64_t p = (q0 + s) * (uint64_t)k;
+        const double2 wt = p < half_n ? w[u] : make_double2(-w[u].x, -w[u].y);
+        r = cmul(wt, r);
+      }
+      out[(q0 + s) * out_seq + (uint64_t)k * out_elem] = r;
+    }
   }
 }
 
@@ -141,7 +194,16 @@ hipError_t launch_pass(const double2* in, double2* out, const double2* roots, ui
                        int post, int fast_in, int fast_out, hipStream_t stream) {
   const uint32_t log2seqs = pick_log2seqs(log2l, log2count);
   const uint32_t blocks = 1u << (log2count - log2seqs);
-  const size_t lds = ((size_t)1 << (log2l + log2seqs)) * sizeof(double2);
+  // the sequences plus the L/2 twiddles of the sub-transform (at most 64 + 32 KiB)
+  const size_t lds = (((size_t)1 << (log2l + log2seqs)) + ((size_t)1 << log2l) / 2) * sizeof(double2);
+  static bool lds_raised = false;
+  if (!lds_raised) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_lds_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)((kFftMaxLds + kFftMaxLds / 2) * sizeof(double2)));
+    if (e != hipSuccess) return e;
+    lds_raised = true;
+  }
   hipLaunchKernelGGL(fft_lds_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l, log2seqs,
                      in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
   return hipGetLastError();
