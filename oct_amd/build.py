@@ -64,7 +64,9 @@ def build_reactor(verbose: bool = False) -> Path:
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(_compile, sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    # -z defs: an unresolved symbol (e.g. a kernel stub clang failed to emit)
+    # fails the build instead of the first call.
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")

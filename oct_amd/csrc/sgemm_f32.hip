@@ -23,6 +23,7 @@
 //     chunks of a grouped (GROUP_M) tile order, keeping each XCD's L2 on a
 //     compact block of A rows and B columns.
 #include <algorithm>
+#include <cmath>
 
 #include "reactor_internal.h"
 
@@ -32,11 +33,7 @@ namespace {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;
-constexpr int kBN = 256;
 constexpr int kBK = 16;
-constexpr int kLdsA = kBM + 2;  // k-major A rows; +2 keeps the transposing stores conflict-free
-constexpr int kLdsB = kBN + 4;  // k-major B rows; multiple of 4 for 128-bit stores
 constexpr int kGroupM = 8;
 
 __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int* tn) {
@@ -52,17 +49,33 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int*
   *tn = in_group / group_m;
 }
 
+// Macro tile kBM x kBN (kBM in {64, 128}, kBN in {128, 256}); the four waves
+// form a 2x2 grid, each owning (kBM/2) x (kBN/2) = kMI x kNI MFMA 32x32 blocks.
+// Occupancy: 2 workgroups per CU for 128x256 (198 VGPRs), more for the
+// smaller tiles.
+template <int kBM, int kBN>
+struct TileCfg {
+  static constexpr int kMI = kBM / 64;
+  static constexpr int kNI = kBN / 64;
+  static constexpr int kLdsA = kBM + 2;  // k-major A rows; +2 keeps the transposing stores conflict-free
+  static constexpr int kLdsB = kBN + 4;  // k-major B rows; multiple of 4 for 128-bit stores
+  static constexpr int kAPer = kBM / 16;            // A floats per thread per K tile (one row, consecutive k)
+  static constexpr int kAThreadsPerRow = 16 / kAPer;
+  static constexpr int kBVec = kBN / 64;            // B float4s per thread per K tile
+  static constexpr int kBRowStep = 1024 / kBN;      // K rows between a thread's float4s
+};
+
 // Strides are leading dimensions in elements.  R (may be null) is added in the
 // epilogue: C = A @ B + R; R may alias C (each element is read, then written,
 // by the same lane).
-template <bool kVec, bool kBuf>
-__global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __restrict__ A,
-                                                                const float* __restrict__ B, float* C, int M,
-                                                                int N, int K, int tiles_m, int tiles_n, int lda,
-                                                                int ldb, int ldc, const float* R, int ldr,
-                                                                int k_len, long long sa, long long sb, long long sc) {
-  __shared__ float As[2][kBK][kLdsA];
-  __shared__ float Bs[2][kBK][kLdsB];
+template <bool kVec, bool kBuf, int kBM, int kBN>
+__global__ __launch_bounds__(256, (kBM * kBN >= 128 * 256 ? 2 : 3)) void sgemm_f32_mfma_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* C, int M, int N, int K, int tiles_m,
+    int tiles_n, int lda, int ldb, int ldc, const float* R, int ldr, int k_len, long long sa, long long sb,
+    long long sc) {
+  using T = TileCfg<kBM, kBN>;
+  __shared__ float As[2][kBK][T::kLdsA];
+  __shared__ float Bs[2][kBK][T::kLdsB];
 
   // Batched launches (gridDim.z > 1, never split-K): matrix z of A, B and C
   // starts sa, sb and sc elements after the previous one.
@@ -91,15 +104,15 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
   const int wm = wave >> 1;
   const int wn = wave & 1;
 
-  // Global->register assignment: A: one row, 8 consecutive k;
-  // B: k rows tid/64 + {0,4,8,12}, 4 consecutive n at (tid%64)*4.
-  const int a_row = tid >> 1;
-  const int a_k = (tid & 1) * 8;
-  const int b_k = tid >> 6;
-  const int b_n = (tid & 63) * 4;
+  // Global->register assignment: A: one row, kAPer consecutive k;
+  // B: k rows b_k + kBRowStep*h, 4 consecutive n at b_n.
+  const int a_row = tid / T::kAThreadsPerRow;
+  const int a_k = (tid % T::kAThreadsPerRow) * T::kAPer;
+  const int b_k = tid / (kBN / 4);
+  const int b_n = (tid % (kBN / 4)) * 4;
 
-  float ra[8];
-  float rb[16];
+  float ra[T::kAPer];
+  float rb[4 * T::kBVec];
   // Branch-free loads (kBuf: K of this slice is a multiple of the K tile): buffer
   // loads return zero for rows of A at or past M and past the end of B; columns of
   // B at or past N only feed output columns that are never stored.
@@ -114,7 +127,7 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
     const int gn = col0 + b_n;
     if constexpr (kBuf) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < T::kAPer / 4; ++h) {
         const int gk = k0 + a_k + 4 * h;
         const floatx4 v =
             __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (uint32_t)((gr * lda + gk) * 4), 0, 0));
@@ -124,8 +137,8 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
         ra[4 * h + 3] = v.w;
       }
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const int gk = k0 + b_k + 4 * h;
+      for (int h = 0; h < T::kBVec; ++h) {
+        const int gk = k0 + b_k + T::kBRowStep * h;
         const floatx4 v =
             __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (uint32_t)((gk * ldb + gn) * 4), 0, 0));
         rb[4 * h + 0] = v.x;
@@ -135,7 +148,7 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
       }
     } else if constexpr (kVec) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < T::kAPer / 4; ++h) {
         const int gk = k0 + a_k + 4 * h;
         floatx4 v = {0.f, 0.f, 0.f, 0.f};
         if (gr < M && gk < K) v = *reinterpret_cast<const floatx4*>(A + (size_t)gr * lda + gk);
@@ -145,8 +158,8 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
         ra[4 * h + 3] = v.w;
       }
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const int gk = k0 + b_k + 4 * h;
+      for (int h = 0; h < T::kBVec; ++h) {
+        const int gk = k0 + b_k + T::kBRowStep * h;
         floatx4 v = {0.f, 0.f, 0.f, 0.f};
         if (gk < K && gn < N) v = *reinterpret_cast<const floatx4*>(B + (size_t)gk * ldb + gn);
         rb[4 * h + 0] = v.x;
@@ -156,13 +169,13 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < T::kAPer; ++j) {
         const int gk = k0 + a_k + j;
         ra[j] = (gr < M && gk < K) ? A[(size_t)gr * lda + gk] : 0.f;
       }
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const int gk = k0 + b_k + 4 * h;
+      for (int h = 0; h < T::kBVec; ++h) {
+        const int gk = k0 + b_k + T::kBRowStep * h;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           rb[4 * h + j] = (gk < K && gn + j < N) ? B[(size_t)gk * ldb + gn + j] : 0.f;
@@ -173,19 +186,19 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) As[buf][a_k + j][a_row] = ra[j];
+    for (int j = 0; j < T::kAPer; ++j) As[buf][a_k + j][a_row] = ra[j];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
+    for (int h = 0; h < T::kBVec; ++h) {
       floatx4 v = {rb[4 * h + 0], rb[4 * h + 1], rb[4 * h + 2], rb[4 * h + 3]};
-      *reinterpret_cast<floatx4*>(&Bs[buf][b_k + 4 * h][b_n]) = v;
+      *reinterpret_cast<floatx4*>(&Bs[buf][b_k + T::kBRowStep * h][b_n]) = v;
     }
   };
 
-  floatx16 acc[2][4];
+  floatx16 acc[T::kMI][T::kNI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < T::kMI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
+    for (int j = 0; j < T::kNI; ++j) acc[i][j] = floatx16{};
 
   const int k_tiles = (K + kBK - 1) / kBK;
   load_tile(0);
@@ -194,25 +207,33 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 
   const int lrow = lane & 31;
   const int lk = lane >> 5;
-  const int am = wm * 64 + lrow;
-  const int bn = wn * 128 + lrow;
+  const int am = wm * (kBM / 2) + lrow;
+  const int bn = wn * (kBN / 2) + lrow;
+
+  // MFMA operands of one k step (k = 2s + lane/32): register double buffering
+  // reads step s+1 from LDS while step s's MFMAs run.
+  float a_op[2][T::kMI], b_op[2][T::kNI];
+  auto read_step = [&](int buf, int s, int slot) {
+    const int kr = 2 * s + lk;
+#pragma unroll
+    for (int i = 0; i < T::kMI; ++i) a_op[slot][i] = As[buf][kr][am + 32 * i];
+#pragma unroll
+    for (int j = 0; j < T::kNI; ++j) b_op[slot][j] = Bs[buf][kr][bn + 32 * j];
+  };
 
   for (int kt = 0; kt < k_tiles; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < k_tiles;
     if (more) load_tile((kt + 1) * kBK);
+    read_step(cur, 0, 0);
 #pragma unroll
     for (int s = 0; s < kBK / 2; ++s) {
-      const int kr = 2 * s + lk;
-      float a[2], b[4];
+      if (s + 1 < kBK / 2) read_step(cur, s + 1, (s + 1) & 1);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = As[cur][kr][am + 32 * i];
+      for (int i = 0; i < T::kMI; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[cur][kr][bn + 32 * j];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < T::kNI; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a_op[s & 1][i], b_op[s & 1][j], acc[i][j], 0, 0, 0);
     }
     if (more) store_tile(cur ^ 1);
     __syncthreads();
@@ -221,7 +242,197 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
   // Accumulator layout of a 32x32 MFMA block: lane l, register r holds
   // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
   auto store_block = [&](const floatx16& acc, int mi, int ni) {
-    const int col = col0 + wn * 128 + ni * 32 + lrow;
+    const int col = col0 + wn * (kBN / 2) + ni * 32 + lrow;
+    if (col >= N) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + wm * (kBM / 2) + mi * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+      if (row < M) {
+        float v = acc[r];
+        if (R != nullptr) v += R[(size_t)row * ldr + col];
+        C[(size_t)row * ldc + col] = v;
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < T::kMI; ++i)
+#pragma unroll
+    for (int j = 0; j < T::kNI; ++j) store_block(acc[i][j], i, j);
+}
+
+// Direct-to-LDS variant for the branch-free shapes (k, n, lda, ldb multiples
+// of 4, every slice a multiple of the K tile): A and B tiles go from HBM to LDS
+// with buffer_load ... lds (16 bytes per lane, no register staging), which
+// frees the staging registers for a third workgroup per CU (128x256) and
+// removes the transposing LDS stores.
+//
+// LDS stage (kBM = 128, K tile 16): A is row-major, 8 blocks of 16 rows x 64 B,
+// and chunk kc (4 floats) of block row r sits at position kc ^ ((r >> 2) & 3);
+// B is k-major: 256-wide rows at a 1056-byte pitch, or 128-wide rows at 512
+// bytes with chunk c of row k at c ^ (8 * ((k >> 2) & 1)).  Both choices make
+// the MFMA operand reads bank-conflict free.
+//
+// K order: an MFMA 32x32x2 takes k index 0 from lanes 0-31 and k index 1 from
+// lanes 32-63.  Lane half h reads the 4-float chunk 2p + h of its A row with
+// one 128-bit read, so step (p, j) pairs k = 8p + j (lanes 0-31) with
+// k = 8p + 4 + j (lanes 32-63); the B operand reads the same two k rows.
+// Every k of the tile enters each accumulator exactly once.
+template <int kBN>
+struct DlCfg {
+  static constexpr int kNI = kBN / 64;
+  static constexpr int kABytes = 128 * kBK * 4;
+  static constexpr int kBPitch = kBN == 256 ? 1056 : 512;
+  static constexpr int kStage = kABytes + kBK * kBPitch;
+};
+
+template <int kBN>
+__device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, const float* __restrict__ B, float* C,
+                                                  int M, int N, int K, int tiles_m, int tiles_n, int lda, int ldb,
+                                                  int ldc, const float* R, int ldr, int k_len, long long sa,
+                                                  long long sb, long long sc, char* S0, char* S1) {
+  using D = DlCfg<kBN>;
+  constexpr int kNI = D::kNI;
+  typedef __attribute__((address_space(3))) void lds_void;
+
+  if (gridDim.z > 1) {
+    A += (size_t)blockIdx.z * sa;
+    B += (size_t)blockIdx.z * sb;
+    C += (size_t)blockIdx.z * sc;
+  }
+  int tm, tn;
+  map_tile(tiles_m, tiles_n, &tm, &tn);
+  const int row0 = tm * 128;
+  const int col0 = tn * kBN;
+  size_t a_extent = (size_t)M * lda;
+  if (gridDim.y > 1) {
+    const int kb = (int)blockIdx.y * k_len;
+    A += kb;
+    a_extent -= (size_t)kb;
+    B += (size_t)kb * ldb;
+    C += (size_t)blockIdx.y * M * ldc;
+    K = min(k_len, K - kb);
+  }
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+
+  const __amdgpu_buffer_rsrc_t rsa =
+      __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)(a_extent * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)((size_t)K * ldb * 4), 0x00020000);
+
+  // Per-lane source offsets (bytes, k0 = 0) of this wave's 2 A and kBN/64 B
+  // instructions; the tile's k offset travels in the scalar soffset.
+  uint32_t a_off[2], b_off[kBN / 64];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = 2 * wave + i;  // A block: rows 16q..16q+15
+    const int r = lane >> 2;
+    const int kc = (lane & 3) ^ ((r >> 2) & 3);
+    a_off[i] = (uint32_t)(((row0 + 16 * q + r) * lda + 4 * kc) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < kBN / 64; ++i) {
+    if constexpr (kBN == 256) {
+      const int kr = 4 * wave + i;  // one 256-wide row per instruction
+      b_off[i] = (uint32_t)((kr * ldb + col0 + 4 * lane) * 4);
+    } else {
+      const int q = 2 * wave + i;  // rows 2q, 2q+1
+      const int kr = 2 * q + (lane >> 5);
+      const int c = (lane & 31) ^ (((kr >> 2) & 1) << 3);
+      b_off[i] = (uint32_t)((kr * ldb + col0 + 4 * c) * 4);
+    }
+  }
+  auto issue = [&](char* stage, int k0) {
+    const int sa_k = __builtin_amdgcn_readfirstlane(k0 * 4);
+    const int sb_k = __builtin_amdgcn_readfirstlane(k0 * ldb * 4);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(stage + (2 * wave + i) * 1024), 16, a_off[i], sa_k, 0,
+                                               0);
+#pragma unroll
+    for (int i = 0; i < kBN / 64; ++i) {
+      char* dst = kBN == 256 ? stage + D::kABytes + (4 * wave + i) * D::kBPitch
+                             : stage + D::kABytes + (2 * wave + i) * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_void*)dst, 16, b_off[i], sb_k, 0, 0);
+    }
+  };
+
+  // Operand addresses (bytes within a stage).
+  const int lrow = lane & 31;
+  const int h = lane >> 5;
+  const int am = wm * 64 + lrow;  // + 32 mi: two blocks further, same swizzle
+  const int ar = am & 15;
+  const uint32_t a_base = (uint32_t)((am >> 4) * 1024 + ar * 64 + ((h ^ ((ar >> 2) & 3)) << 4));
+  uint32_t b_base[kBN == 256 ? 1 : 2];
+  if constexpr (kBN == 256) {
+    b_base[0] = (uint32_t)(D::kABytes + 4 * h * D::kBPitch + (wn * 128 + lrow) * 4);
+  } else {
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+      b_base[ni] = (uint32_t)(D::kABytes + 4 * h * D::kBPitch + (wn * 16 + ((ni ^ h) << 3) + (lrow >> 2)) * 16 +
+                              (lrow & 3) * 4);
+  }
+
+  floatx16 acc[2][kNI];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < kNI; ++j) acc[i][j] = floatx16{};
+
+  auto compute = [&](const char* st) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      floatx4 a[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+        a[mi] = *reinterpret_cast<const floatx4*>(st + ((a_base ^ (uint32_t)(32 * p)) + mi * 2048));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float b[kNI];
+        const int row_off = (8 * p + j) * D::kBPitch;
+#pragma unroll
+        for (int ni = 0; ni < kNI; ++ni) {
+          if constexpr (kBN == 256)
+            b[ni] = *reinterpret_cast<const float*>(st + b_base[0] + row_off + ni * 128);
+          else
+            b[ni] = *reinterpret_cast<const float*>(st + b_base[ni] + row_off);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < kNI; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mi][j], b[ni], acc[mi][ni], 0, 0, 0);
+      }
+      // Keep each half's operand reads within the half: bounds register pressure.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  const int k_tiles = K / kBK;
+  issue(S0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  // Unrolled by two so that the reads of one stage are visibly independent of
+  // the transfers into the other (separate arrays).
+  int kt = 0;
+  for (; kt + 1 < k_tiles; kt += 2) {
+    issue(S1, (kt + 1) * kBK);
+    compute(S0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (kt + 2 < k_tiles) issue(S0, (kt + 2) * kBK);
+    compute(S1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  if (kt < k_tiles) compute(S0);  // odd count: the last tile was issued into S0
+
+  const int lk = h;
+  auto store_block = [&](const floatx16& acc, int mi, int ni) {
+    const int col = col0 + wn * (kBN / 2) + ni * 32 + lrow;
     if (col >= N) return;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -236,7 +447,28 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32_mfma_kernel(const float* __r
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) store_block(acc[i][j], i, j);
+    for (int j = 0; j < kNI; ++j) store_block(acc[i][j], i, j);
+}
+
+// Two stages of LDS; the kernels differ in tile width and occupancy target.
+__global__ __launch_bounds__(256, 3) void sgemm_f32_dl256_kernel(const float* __restrict__ A,
+                                                                 const float* __restrict__ B, float* C, int M, int N,
+                                                                 int K, int tiles_m, int tiles_n, int lda, int ldb,
+                                                                 int ldc, const float* R, int ldr, int k_len,
+                                                                 long long sa, long long sb, long long sc) {
+  __shared__ __attribute__((aligned(1024))) char S0[DlCfg<256>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S1[DlCfg<256>::kStage];
+  sgemm_f32_dl_body<256>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+}
+
+__global__ __launch_bounds__(256, 4) void sgemm_f32_dl128_kernel(const float* __restrict__ A,
+                                                                 const float* __restrict__ B, float* C, int M, int N,
+                                                                 int K, int tiles_m, int tiles_n, int lda, int ldb,
+                                                                 int ldc, const float* R, int ldr, int k_len,
+                                                                 long long sa, long long sb, long long sc) {
+  __shared__ __attribute__((aligned(1024))) char S0[DlCfg<128>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S1[DlCfg<128>::kStage];
+  sgemm_f32_dl_body<128>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
 }
 
 // y[m] = A[m,:] . x : one wave per row, 4 rows per workgroup.  HBM-bound:
@@ -293,31 +525,160 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Number of K slices.  2 workgroups per CU make 512 concurrent slots; a grid
-// of w workgroups runs in ceil(w / 512) rounds, each as long as one slice's
-// K tiles (~4 us per 128x256x16 tile step at full rate, plus ~2 us of
-// prologue and epilogue).  Slicing adds the reduce launch (~8 us) and
-// (2s + 1) M N floats of partial-sum traffic (~3 TB/s effective).  The count
-// minimising this estimate is chosen, with slices at least 128 deep and at
-// most 16 of them.
-int choose_splits(int tiles, uint32_t m, uint32_t n, uint32_t k) {
-  const int k_tiles = (int)((k + kBK - 1) / kBK);
-  auto cost = [&](int s) {
-    const int per = (k_tiles + s - 1) / s;
-    const double rounds = (double)(((size_t)tiles * s + 511) / 512);
-    const double reduce = s == 1 ? 0.0 : 8.0 + (double)(2 * s + 1) * m * n * 4.0 / 3.0e6;
-    return rounds * (per * 4.0 + 2.0) + reduce;
-  };
-  int best = 1;
-  double best_cost = cost(1);
-  for (int s = 2; s <= 16 && k / (uint32_t)s >= 128; ++s) {
-    const double c = cost(s);
-    if (c < best_cost) {
-      best_cost = c;
-      best = s;
+// Tile shapes: 0 = 128x256, 1 = 128x128, 2 = 64x128 (register-staged loads);
+// 3 = 128x256, 4 = 128x128 (direct-to-LDS, branch-free shapes only).
+constexpr int kTileShapes = 5;
+constexpr int kTileM[kTileShapes] = {128, 128, 64, 128, 128};
+constexpr int kTileN[kTileShapes] = {256, 128, 128, 256, 128};
+
+struct SgemmPlan {
+  int tile;    // index into kTileM / kTileN
+  int splits;  // K slices (1: no split)
+  int k_len;   // K elements per slice (a multiple of the K tile when split)
+};
+
+// Rounds a requested slice count to whole K tiles per slice.
+SgemmPlan make_plan(int tile, int splits, uint32_t k) {
+  SgemmPlan p{tile, 1, (int)k};
+  if (splits > 1) {
+    p.k_len = (int)((((k + splits - 1) / splits) + kBK - 1) / kBK * kBK);
+    p.splits = (int)((k + p.k_len - 1) / p.k_len);
+    if (p.splits <= 1) {
+      p.splits = 1;
+      p.k_len = (int)k;
+    }
+  }
+  return p;
+}
+
+// True when the buffer-load kernels apply: 128-bit aligned operands, every
+// slice length a multiple of the K tile and every 32-bit byte offset (rows up
+// to M + 128, all of B plus a tile row) in range.
+bool buffer_path(const float* a, int lda, long long sa, const float* b, int ldb, long long sb, uint32_t m,
+                 uint32_t n, uint32_t k, int k_len) {
+  const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
+                   (sb % 4 == 0) && aligned16(a) && aligned16(b);
+  return vec && (k % kBK == 0) && (k_len % kBK == 0) && (size_t)(m + 128) * lda * 4 < (1ull << 31) &&
+         ((size_t)k * ldb + n + 256) * 4 < (1ull << 31);
+}
+
+// Plan choice: the (tile shape, K slices) pair with the least estimated time.
+// A grid of W workgroups fills the CUs in rounds of occ*256 (occ = resident
+// workgroups per CU for the tile); a CU holding w workgroups runs them at
+// efficiency eff(w) of its MFMA rate (256 flop/clk at 2.38 GHz), so a K tile
+// of a BMxBN workgroup costs w * BM*BN*32/609280 us / eff(w).  Each round adds
+// ~2 us of prologue/epilogue, a launch ~3 us, and a split adds the reduce
+// (~3 us + (s+1) M N floats at ~2 TB/s).  The constants are fitted to timings of
+// all tile shapes and slice counts at the benchmark and transformer-block
+// shapes on MI355X.
+constexpr int kTileOcc[kTileShapes] = {2, 3, 4, 3, 4};
+constexpr double kTileEff[kTileShapes] = {0.92, 1.03, 0.835, 1.0, 1.05};
+constexpr double kOccEff[4] = {0.70, 0.846, 0.93, 0.932};
+
+double plan_cost(const SgemmPlan& p, uint32_t m, uint32_t n, uint32_t batch) {
+  const int t = p.tile;
+  const double w_total = (double)((m + kTileM[t] - 1) / kTileM[t]) * ((n + kTileN[t] - 1) / kTileN[t]) * p.splits *
+                         batch;
+  const double k_tiles = (double)((p.k_len + kBK - 1) / kBK);
+  const double t16 = (double)kTileM[t] * kTileN[t] * 32.0 / 609280.0;
+  const double slots = 256.0 * kTileOcc[t];
+  const double full = std::floor(w_total / slots);
+  const double rest = w_total - full * slots;
+  auto eff = [&](int w) { return kOccEff[std::min(w, 4) - 1] * kTileEff[t]; };
+  double us = full * kTileOcc[t] * k_tiles * t16 / eff(kTileOcc[t]);
+  if (rest > 0) {
+    const int w = (int)std::ceil(rest / 256.0);
+    us += w * k_tiles * t16 / eff(w);
+  }
+  us += 3.0 + 2.0 * (full + (rest > 0 ? 1.0 : 0.0));
+  if (p.splits > 1) us += 3.0 + (double)(p.splits + 1) * m * n * 4.0 / 2.0e6;
+  return us;
+}
+
+SgemmPlan plan_sgemm(const float* a, int lda, long long sa, const float* b, int ldb, long long sb, uint32_t m,
+                     uint32_t n, uint32_t k, uint32_t batch) {
+  static const int kSplitChoices[] = {1, 2, 3, 4, 6, 8, 12, 16};
+  SgemmPlan best = make_plan(0, 1, k);
+  double best_cost = 1e300;
+  for (int t = 0; t < kTileShapes; ++t) {
+    for (int s : kSplitChoices) {
+      if (s > 1 && (batch > 1 || k / (uint32_t)s < 64)) break;
+      const SgemmPlan p = make_plan(t, s, k);
+      if (p.splits != s) continue;
+      if (t >= 3 && !buffer_path(a, lda, sa, b, ldb, sb, m, n, k, p.k_len)) continue;
+      const double c = plan_cost(p, m, n, batch);
+      if (c < best_cost) {
+        best_cost = c;
+        best = p;
+      }
     }
   }
   return best;
+}
+
+template <int kBM, int kBN>
+void launch_tile(bool buf, bool vec, dim3 grid, hipStream_t stream, const float* a, const float* b, float* c, int m,
+                 int n, int k, int tiles_m, int tiles_n, int lda, int ldb, int ldc, const float* r, int ldr, int k_len,
+                 long long sa, long long sb, long long sc) {
+  if (buf)
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, true, kBM, kBN>), grid, dim3(256), 0, stream, a, b, c, m, n, k,
+                       tiles_m, tiles_n, lda, ldb, ldc, r, ldr, k_len, sa, sb, sc);
+  else if (vec)
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, false, kBM, kBN>), grid, dim3(256), 0, stream, a, b, c, m, n, k,
+                       tiles_m, tiles_n, lda, ldb, ldc, r, ldr, k_len, sa, sb, sc);
+  else
+    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<false, false, kBM, kBN>), grid, dim3(256), 0, stream, a, b, c, m, n, k,
+                       tiles_m, tiles_n, lda, ldb, ldc, r, ldr, k_len, sa, sb, sc);
+}
+
+// Launches the MFMA kernel of plan p over `batch` matrices (batch > 1 only
+// without split) and, when split, the reduce into c (partial: splits*m*n floats).
+hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long sa, const float* b, int ldb,
+                          long long sb, float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
+                          uint32_t batch, const float* residual, int ldr, float* partial, hipStream_t stream) {
+  const bool split = p.splits > 1;
+  const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
+                   (sb % 4 == 0) && aligned16(a) && aligned16(b);
+  const bool buf = buffer_path(a, lda, sa, b, ldb, sb, m, n, k, p.k_len);
+  const int tile = (p.tile >= 3 && !buf) ? p.tile - 3 : p.tile;
+  const int bm = kTileM[tile], bn = kTileN[tile];
+  const int tiles_m = (int)((m + bm - 1) / bm);
+  const int tiles_n = (int)((n + bn - 1) / bn);
+  const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)p.splits, batch);
+  float* out = split ? partial : c;
+  const int ldo = split ? (int)n : ldc;
+  const float* res = split ? nullptr : residual;
+  switch (tile) {
+    case 3:
+      hipLaunchKernelGGL(sgemm_f32_dl256_kernel, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+                         tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      break;
+    case 4:
+      hipLaunchKernelGGL(sgemm_f32_dl128_kernel, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+                         tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      break;
+    case 0:
+      launch_tile<128, 256>(buf, vec, grid, stream, a, b, out, (int)m, (int)n, (int)k, tiles_m, tiles_n, lda, ldb,
+                            ldo, res, ldr, p.k_len, sa, sb, sc);
+      break;
+    case 1:
+      launch_tile<128, 128>(buf, vec, grid, stream, a, b, out, (int)m, (int)n, (int)k, tiles_m, tiles_n, lda, ldb,
+                            ldo, res, ldr, p.k_len, sa, sb, sc);
+      break;
+    default:
+      launch_tile<64, 128>(buf, vec, grid, stream, a, b, out, (int)m, (int)n, (int)k, tiles_m, tiles_n, lda, ldb,
+                           ldo, res, ldr, p.k_len, sa, sb, sc);
+      break;
+  }
+  if (split) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t total = (size_t)m * n;
+    const unsigned blocks = (unsigned)std::min((size_t)8192, (total + 255) / 256);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, c, (int)m, (int)n, ldc,
+                       p.splits, residual, ldr);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -335,49 +696,14 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
     if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_GEMV_F32;
     return hipGetLastError();
   }
-  const int tiles_m = (int)((m + kBM - 1) / kBM);
-  const int tiles_n = (int)((n + kBN - 1) / kBN);
-  const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && aligned16(a) && aligned16(b);
-  int splits = choose_splits(tiles_m * tiles_n, m, n, k);
-  int k_len = (int)k;
+  SgemmPlan p = plan_sgemm(a, lda, 0, b, ldb, 0, m, n, k, 1);
   float* partial = nullptr;
-  if (splits > 1) {
-    // slices are whole K tiles (multiples of 16 keep 128-bit loads aligned)
-    k_len = (int)((((k + splits - 1) / splits) + kBK - 1) / kBK * kBK);
-    splits = (int)((k + k_len - 1) / k_len);
-    partial = splits > 1 ? static_cast<float*>(staging(6, (size_t)splits * m * n * sizeof(float))) : nullptr;
-    if (partial == nullptr) {
-      splits = 1;
-      k_len = (int)k;
-    }
-  }
-  const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits);
-  float* out = splits > 1 ? partial : c;
-  const int ldo = splits > 1 ? (int)n : ldc;
-  const float* res = splits > 1 ? nullptr : residual;
-  // Buffer-load path: every slice length a multiple of the K tile and every
-  // 32-bit byte offset (rows up to M + kBM, all of B plus a tile row) in range.
-  const bool buf = vec && (k % kBK == 0) && (k_len % kBK == 0) &&
-                   (size_t)(m + kBM) * lda * 4 < (1ull << 31) && ((size_t)k * ldb + n + kBN) * 4 < (1ull << 31);
-  if (buf)
-    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, true>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len, 0ll, 0ll, 0ll);
-  else if (vec)
-    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, false>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len, 0ll, 0ll, 0ll);
-  else
-    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<false, false>), grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, k_len, 0ll, 0ll, 0ll);
-  if (splits > 1) {
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const size_t total = (size_t)m * n;
-    const unsigned blocks = (unsigned)std::min((size_t)8192, (total + 255) / 256);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, c, (int)m, (int)n, ldc,
-                       splits, residual, ldr);
+  if (p.splits > 1) {
+    partial = static_cast<float*>(staging(6, (size_t)p.splits * m * n * sizeof(float)));
+    if (partial == nullptr) p = make_plan(p.tile, 1, k);
   }
   if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_F32;
-  return hipGetLastError();
+  return run_sgemm_plan(p, a, lda, 0, b, ldb, 0, c, ldc, 0, m, n, k, 1, residual, ldr, partial, stream);
 }
 
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
@@ -385,24 +711,8 @@ hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const
                                     uint32_t batch, hipStream_t stream) {
   if (batch == 0 || m == 0 || n == 0) return hipSuccess;
   if (batch == 1) return launch_sgemm_f32_ex(a, lda, b, ldb, c, ldc, m, n, k, nullptr, 0, stream, nullptr);
-  const int tiles_m = (int)((m + kBM - 1) / kBM);
-  const int tiles_n = (int)((n + kBN - 1) / kBN);
-  const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
-                   (sb % 4 == 0) && aligned16(a) && aligned16(b);
-  // Per-matrix extents bound every buffer offset, as in the single launch.
-  const bool buf = vec && (k % kBK == 0) && (size_t)(m + kBM) * lda * 4 < (1ull << 31) &&
-                   ((size_t)k * ldb + n + kBN) * 4 < (1ull << 31);
-  const dim3 grid((unsigned)(tiles_m * tiles_n), 1u, batch);
-  if (buf)
-    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, true>), grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldc, (const float*)nullptr, 0, (int)k, sa, sb, sc);
-  else if (vec)
-    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<true, false>), grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldc, (const float*)nullptr, 0, (int)k, sa, sb, sc);
-  else
-    hipLaunchKernelGGL((sgemm_f32_mfma_kernel<false, false>), grid, dim3(256), 0, stream, a, b, c, (int)m, (int)n,
-                       (int)k, tiles_m, tiles_n, lda, ldb, ldc, (const float*)nullptr, 0, (int)k, sa, sb, sc);
-  return hipGetLastError();
+  return run_sgemm_plan(plan_sgemm(a, lda, sa, b, ldb, sb, m, n, k, batch), a, lda, sa, b, ldb, sb, c, ldc, sc, m, n, k,
+                        batch, nullptr, 0, nullptr, stream);
 }
 
 hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
