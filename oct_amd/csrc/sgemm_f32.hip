@@ -244,13 +244,16 @@ __global__ __launch_bounds__(256, (kBM * kBN >= 128 * 256 ? 2 : 3)) void sgemm_f
   auto store_block = [&](const floatx16& acc, int mi, int ni) {
     const int col = col0 + wn * (kBN / 2) + ni * 32 + lrow;
     if (col >= N) return;
+    const int rb = row0 + wm * (kBM / 2) + mi * 32 + 4 * lk;
+    float* cp = C + (size_t)rb * ldc + col;
+    const float* rp = R != nullptr ? R + (size_t)rb * ldr + col : nullptr;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = row0 + wm * (kBM / 2) + mi * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-      if (row < M) {
+      const int dr = 8 * (r >> 2) + (r & 3);
+      if (rb + dr < M) {
         float v = acc[r];
-        if (R != nullptr) v += R[(size_t)row * ldr + col];
-        C[(size_t)row * ldc + col] = v;
+        if (rp != nullptr) v += rp[(size_t)dr * ldr];
+        cp[(size_t)dr * ldc] = v;
       }
     }
   };
@@ -430,17 +433,21 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
   }
   if (kt < k_tiles) compute(S0);  // odd count: the last tile was issued into S0
 
-  const int lk = h;
+  // Row offsets from the block's first row are wave-uniform (scalar), so only
+  // one 64-bit address per block lives in vector registers.
   auto store_block = [&](const floatx16& acc, int mi, int ni) {
     const int col = col0 + wn * (kBN / 2) + ni * 32 + lrow;
     if (col >= N) return;
+    const int rb = row0 + wm * 64 + mi * 32 + 4 * h;
+    float* cp = C + (size_t)rb * ldc + col;
+    const float* rp = R != nullptr ? R + (size_t)rb * ldr + col : nullptr;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = row0 + wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-      if (row < M) {
+      const int dr = 8 * (r >> 2) + (r & 3);
+      if (rb + dr < M) {
         float v = acc[r];
-        if (R != nullptr) v += R[(size_t)row * ldr + col];
-        C[(size_t)row * ldc + col] = v;
+        if (rp != nullptr) v += rp[(size_t)dr * ldr];
+        cp[(size_t)dr * ldc] = v;
       }
     }
   };
