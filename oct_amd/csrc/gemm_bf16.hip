@@ -553,7 +553,250 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_
   store_block(acc[3][1], 3, 1);
 }
 
+// Four-stage variant of the direct-to-LDS kernel: K tile 32, four 32 KB LDS
+// stages, so each tile's transfers are issued three tiles ahead of its MFMAs
+// (one 32-k step of the whole tile takes ~1000 cycles per SIMD, the HBM and
+// Infinity Cache latency is longer).  A rows are 64 bytes here: chunk c of row
+// R sits at c ^ ((R >> 2) & 3); B keeps the 512-byte rows and swizzle above.
+// Waits count this wave's outstanding transfers (4 per tile) and a bare
+// s_barrier publishes a tile: transfers of the next tiles stay in flight
+// across it.  Faster than the two-stage kernel on long K and on grids of more
+// than one workgroup per CU (C5's QKV, W1|W3 and W2 products, 8192^3: 6-16 %),
+// slower on single-round grids with K <= 4096 (4096^3: -9 %).
+constexpr int kBK4 = 32;
+constexpr int kStage4 = kBM2 * kBK4 * 2 + kBK4 * kBN2 * 2;  // 16 KB A + 16 KB B
+
+// s_waitcnt vmcnt(n) with the LDS and export counters left free (gfx9 encoding).
+#define PROM_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <bool kSwiGLU>
+__device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                                   float* C, int M, int N, int K, int tiles_m, int tiles_n, int lda,
+                                                   int ldb, int ldc, const float* R, int ldr, uint16_t* Cb, char* S0,
+                                                   char* S1, char* S2, char* S3) {
+  int tm, tn;
+  map_tile2(tiles_m, tiles_n, &tm, &tn);
+  const int row0 = tm * kBM2;
+  const int col0 = kSwiGLU ? tn * (kBN2 / 2) : tn * kBN2;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2;
+  const int wn = wave & 3;
+
+  // This wave's 2 A instructions (rows 16q..16q+15, 4 lanes per row) and 2 B
+  // instructions (k rows 2q, 2q+1, 32 lanes per row), q = 2 wave + i.
+  uint32_t a_off[2], b_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = wave * 2 + i;
+    const int r = 16 * q + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    a_off[i] = (uint32_t)(((row0 + r) * lda + 8 * c) * 2);
+    const int kr = 2 * q + (lane >> 5);
+    const int cb = (lane & 31) ^ swz_b(kr);
+    int gcol = col0 + 8 * cb;
+    if constexpr (kSwiGLU) {
+      const int e = 8 * cb;
+      gcol = col0 + (e >> 6) * 32 + (e & 31) + ((e & 32) ? N : 0);
+    }
+    b_off[i] = (uint32_t)((kr * ldb + gcol) * 2);
+  }
+  // The transfers are written as inline assembly (M0 = LDS destination of
+  // the wave's 1 KB, 16 bytes per lane; buffer descriptors built here, raw,
+  // range-checked: out-of-range rows read zero).  The compiler then does not
+  // track them as LDS stores, so it adds no conservative vmcnt(0) before the
+  // LDS reads of the other stages; the explicit vmcnt waits and barriers of the
+  // K loop order every transfer before the reads of its tile.  Nothing else in
+  // this kernel uses M0.
+  typedef int int4v __attribute__((ext_vector_type(4)));
+  auto desc = [](const void* p, uint32_t bytes) {
+    const unsigned long long a = (unsigned long long)p;
+    int4v d;
+    d.x = __builtin_amdgcn_readfirstlane((int)(a & 0xffffffffu));
+    d.y = __builtin_amdgcn_readfirstlane((int)(a >> 32));
+    d.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    d.w = 0x00020000;
+    return d;
+  };
+  const int4v da = desc(A, (uint32_t)((size_t)M * lda * 2));
+  const int4v db = desc(B, (uint32_t)((size_t)K * ldb * 2));
+  auto issue = [&](char* stage, int k0) {
+    const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
+    const int sb = __builtin_amdgcn_readfirstlane(k0 * ldb * 2);
+    const uint32_t base = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)stage;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = wave * 2 + i;
+      const uint32_t la = __builtin_amdgcn_readfirstlane(base + q * 1024);
+      const uint32_t lb = __builtin_amdgcn_readfirstlane(base + 16384 + q * 1024);
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(la), "v"(a_off[i]), "s"(da),
+                   "s"(sa)
+                   : "memory");
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lb), "v"(b_off[i]), "s"(db),
+                   "s"(sb)
+                   : "memory");
+    }
+  };
+
+  const int lrow = lane & 31;
+  const int hk = lane >> 5;
+  const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_e = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const uint32_t a_base = (uint32_t)((wm * 128 + lrow) * 64 + ((hk ^ ((lrow >> 2) & 3)) << 4));
+  const uint32_t b_base =
+      (uint32_t)(16384 + tr_row * 512 + (((wn * 8 + (tr_e >> 3)) ^ swz_b(tr_row)) << 4) + (tr_e & 7) * 2);
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[i][0] = floatx16{};
+    acc[i][1] = floatx16{};
+  }
+  struct Frags {
+    bf16x8 a[4], b[2];
+  };
+  auto read = [&](const char* st, int s) {
+    Frags f;
+    const uint32_t as = a_base ^ (uint32_t)(32 * s);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) f.a[mi] = *reinterpret_cast<const bf16x8*>(st + as + mi * 2048);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const uint32_t bs = (b_base ^ (uint32_t)(64 * ni)) + 8192 * s;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + bs));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + bs + 2048));
+      f.b[ni] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    return f;
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
+  };
+
+  const int k_tiles = K / kBK4;
+  // Step t: wait until this wave's transfers of tile t+1 have landed (tile t+2
+  // may stay in flight), barrier (tile t+1 complete for all waves, tile t-1's
+  // stage free), issue tile t+3 into that stage, run tile t, and read the first
+  // fragments of tile t+1 before the next barrier.
+  Frags f0;
+  auto step = [&](const char* cur, const char* next, char* nxt, int t) {
+    if (t + 2 < k_tiles)
+      PROM_WAIT_VMCNT(4);
+    else
+      PROM_WAIT_VMCNT(0);
+    stage_barrier();
+    if (t + 3 < k_tiles) issue(nxt, (t + 3) * kBK4);
+    const Frags f1 = read(cur, 1);
+    mma(f0);
+    mma(f1);
+    if (t + 1 < k_tiles) f0 = read(next, 0);
+  };
+  issue(S0, 0);
+  if (k_tiles > 1) issue(S1, kBK4);
+  if (k_tiles > 2) issue(S2, 2 * kBK4);
+  // tile 0 complete before its first reads
+  if (k_tiles > 2)
+    PROM_WAIT_VMCNT(8);
+  else if (k_tiles > 1)
+    PROM_WAIT_VMCNT(4);
+  else
+    PROM_WAIT_VMCNT(0);
+  stage_barrier();
+  f0 = read(S0, 0);
+  int t = 0;
+  for (; t + 4 <= k_tiles; t += 4) {
+    step(S0, S1, S3, t);
+    step(S1, S2, S0, t + 1);
+    step(S2, S3, S1, t + 2);
+    step(S3, S0, S2, t + 3);
+  }
+  if (t < k_tiles) step(S0, S1, S3, t);
+  if (t + 1 < k_tiles) step(S1, S2, S0, t + 1);
+  if (t + 2 < k_tiles) step(S2, S3, S1, t + 2);
+
+  const int lgrp = hk * 4;
+  if constexpr (kSwiGLU) {
+    const int col = col0 + wn * 32 + lrow;
+    if (col < N) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const int rb = row0 + wm * 128 + mi * 32 + lgrp;
+        uint16_t* hp = Cb + (size_t)rb * ldc + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = 8 * (r >> 2) + (r & 3);
+          if (rb + dr < M) {
+            const float g = acc[mi][0][r], u = acc[mi][1][r];
+            hp[(size_t)dr * ldc] = f32_to_bf16_rne(g / (1.0f + expf(-g)) * u);
+          }
+        }
+      }
+    }
+    return;
+  }
+  auto store_block = [&](const floatx16& v16, int mi, int ni) {
+    const int col = col0 + wn * 64 + ni * 32 + lrow;
+    if (col >= N) return;
+    const int rb = row0 + wm * 128 + mi * 32 + lgrp;
+    const float* rp = R != nullptr ? R + (size_t)rb * ldr + col : nullptr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int dr = 8 * (r >> 2) + (r & 3);
+      if (rb + dr < M) {
+        float v = v16[r];
+        if (rp != nullptr) v += rp[(size_t)dr * ldr];
+        if (Cb != nullptr)
+          Cb[(size_t)(rb + dr) * ldc + col] = f32_to_bf16_rne(v);
+        else
+          C[(size_t)(rb + dr) * ldc + col] = v;
+      }
+    }
+  };
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    store_block(acc[mi][0], mi, 0);
+    store_block(acc[mi][1], mi, 1);
+  }
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_kernel(const uint16_t* __restrict__ A,
+                                                              const uint16_t* __restrict__ B, float* C, int M, int N,
+                                                              int K, int tiles_m, int tiles_n, int lda, int ldb,
+                                                              int ldc, const float* R, int ldr, uint16_t* Cb) {
+  __shared__ __attribute__((aligned(1024))) char S0[kStage4];
+  __shared__ __attribute__((aligned(1024))) char S1[kStage4];
+  __shared__ __attribute__((aligned(1024))) char S2[kStage4];
+  __shared__ __attribute__((aligned(1024))) char S3[kStage4];
+  gemm_bf16_dl4_body<false>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, Cb, S0, S1, S2, S3);
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_swiglu_kernel(const uint16_t* __restrict__ A,
+                                                                     const uint16_t* __restrict__ B, int M, int N,
+                                                                     int K, int tiles_m, int tiles_n, int lda, int ldb,
+                                                                     int ldh, uint16_t* H) {
+  __shared__ __attribute__((aligned(1024))) char S0[kStage4];
+  __shared__ __attribute__((aligned(1024))) char S1[kStage4];
+  __shared__ __attribute__((aligned(1024))) char S2[kStage4];
+  __shared__ __attribute__((aligned(1024))) char S3[kStage4];
+  gemm_bf16_dl4_body<true>(A, B, nullptr, M, N, K, tiles_m, tiles_n, lda, ldb, ldh, nullptr, 0, H, S0, S1, S2, S3);
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The four-stage kernel wins once a CU runs more than one tile in turn or the
+// K loop is long (measured on MI355X; see its comment).
+inline bool use_four_stage(int tiles, uint32_t k) { return tiles > 256 || k >= 8192; }
 
 }  // namespace
 
@@ -565,8 +808,11 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
   const int tiles_n2 = (int)((n + kBN2 - 1) / kBN2);
   if (vec && tiles_m2 * tiles_n2 >= 128) {
     const dim3 grid2((unsigned)(tiles_m2 * tiles_n2));
-    const bool buf = (k % kBK2 == 0) && (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * ldb * 2 < (1ull << 31);
-    if (buf)
+    const bool range = (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * ldb * 2 < (1ull << 31);
+    if (range && k % kBK4 == 0 && use_four_stage(tiles_m2 * tiles_n2, k))
+      hipLaunchKernelGGL(gemm_bf16_dl4_kernel, grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n, (int)k, tiles_m2,
+                         tiles_n2, lda, ldb, ldc, residual, ldr, cb);
+    else if (range && k % kBK2 == 0)
       hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<false>, grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n, (int)k,
                          tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
     else
@@ -593,13 +839,20 @@ hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w
   // Fused path conditions: whole 128-column output tiles, K a multiple of the K
   // tile, 16-byte aligned rows, byte offsets below 2^31; otherwise the caller
   // runs the GEMM and the elementwise SwiGLU separately.
-  const bool ok = f % 128 == 0 && k % kBK2 == 0 && lda % 8 == 0 && aligned16(a) && aligned16(w13) &&
+  const bool ok = f % 128 == 0 && k % kBK4 == 0 && lda % 8 == 0 && aligned16(a) && aligned16(w13) &&
                   (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * 2 * f * 2 < (1ull << 31);
   if (!ok) return hipErrorNotSupported;
   const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
   const int tiles_n2 = (int)(f / 128);
-  hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<true>, dim3((unsigned)(tiles_m2 * tiles_n2)), dim3(512), 0, stream, a,
-                     w13, nullptr, (int)m, (int)f, (int)k, tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, nullptr, 0, h);
+  const dim3 grid((unsigned)(tiles_m2 * tiles_n2));
+  if (use_four_stage(tiles_m2 * tiles_n2, k))
+    hipLaunchKernelGGL(gemm_bf16_dl4_swiglu_kernel, grid, dim3(512), 0, stream, a, w13, (int)m, (int)f, (int)k,
+                       tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, h);
+  else if (k % kBK2 == 0)
+    hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<true>, grid, dim3(512), 0, stream, a, w13, nullptr, (int)m, (int)f,
+                       (int)k, tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, nullptr, 0, h);
+  else
+    return hipErrorNotSupported;
   return hipGetLastError();
 }
 

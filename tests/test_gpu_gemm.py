@@ -202,9 +202,12 @@ def test_bf16_4096_cubed(gpu_runtime):
         assert oracle.normwise_rel_err(out[r], ref) <= 1e-5
 
 
-@pytest.mark.parametrize("m,n,k", [(4224, 2056, 72), (600, 8200, 136), (1024, 4096, 8)])
+@pytest.mark.parametrize("m,n,k", [(4224, 2056, 72), (600, 8200, 136), (1024, 4096, 8),
+                                   (1100, 16400, 96), (2560, 3584, 8224)])
 def test_bf16_large_tile_kernel_ragged(gpu_runtime, m, n, k):
-    """Shapes with >= 128 256x256 tiles take the large-tile kernel; ragged m/n/k tails."""
+    """Shapes with >= 128 256x256 tiles take the large-tile kernels; ragged m/n/k tails.
+    (1100, 16400, 96) and (2560, 3584, 8224) take the four-stage kernel (more
+    than 256 tiles, or K >= 8192; K a multiple of 32 but not of 64)."""
     a = oracle.to_bf16(oracle.uniform(50 + m, (m, k)))
     b = oracle.to_bf16(oracle.uniform(60 + n, (k, n)))
     out = gpu_runtime.gemm_bf16(m, n, k, a, b).reshape(m, n)
@@ -212,4 +215,6 @@ def test_bf16_large_tile_kernel_ragged(gpu_runtime, m, n, k):
     assert oracle.normwise_rel_err(out, ref) <= 1e-5
     rows = [0, m // 2, m - 1]
     for r in rows:
-        np.testing.assert_allclose(out[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r], rtol=1e-4, atol=1e-5)
+        ref_r = oracle.matmul_f64(a, b, rows=(r, r + 1))[r]
+        # fp32 accumulation over k terms: absolute slack relative to the row's scale
+        np.testing.assert_allclose(out[r], ref_r, rtol=1e-4, atol=2e-6 * np.abs(ref_r).max())
