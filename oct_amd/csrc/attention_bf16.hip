@@ -18,7 +18,11 @@
 //     stays in registers: the key order inside each 16-key MFMA step is the
 //     permutation the S^T accumulator layout hands out, and the V^T operand is
 //     built in the same key order by two ds_read_b64_tr_b16 transpose reads;
-//   * softmax runs in the log2 domain (exp2), running max/sum in fp32;
+//   * softmax runs in the log2 domain: max on raw scores, one FMA and one
+//     v_exp_f32 per score, running max/sum in fp32; O is rescaled only when
+//     some query's maximum grew; masking only on the last, partial tile;
+//     P and O go to bf16 with the hardware round-to-nearest-even pair
+//     conversion (VALU work per tile is the bound of this kernel, not MFMA);
 //   * the output tile is staged through LDS for 128-bit coalesced stores.
 #include "reactor_internal.h"
 
@@ -38,15 +42,6 @@ constexpr int kKB = 64;     // keys per tile
 constexpr int kKP = kD + 8;   // K row pitch (bf16): 68 words, 16 rows on distinct 16-byte bank groups
 constexpr int kVP = kD + 16;  // V row pitch (bf16): 72 words, 4 consecutive rows on distinct banks
 constexpr float kNegBig = -1.0e30f;
-
-__device__ __forceinline__ uint16_t f2bf(float v) {
-  const uint32_t bits = __float_as_uint(v);
-  return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
-}
-
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-}
 
 __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t* __restrict__ Q,
                                                                  const uint16_t* __restrict__ K,
@@ -125,73 +120,77 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
     const bool more = kt + 1 < n_tiles;
     if (more) load_tile(k0 + kKB);
 
-    // S^T for two 32-key blocks.
+    // S^T for two 32-key blocks (raw scores).
+    const uint16_t* kb_base = &Ks[cur][lq][8 * hi];
     floatx16 s0 = {}, s1 = {};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[cur][lq][16 * s + 8 * hi]);
-      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[cur][32 + lq][16 * s + 8 * hi]);
+      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kb_base + 16 * s);
+      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(kb_base + 32 * kKP + 16 * s);
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[s], s1, 0, 0, 0);
     }
-    // scale to the log2 domain, mask keys past T, tile max
+    // Keys past T (last tile only) get a huge negative raw score.
+    if (k0 + kKB > T) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 8 * (r >> 2) + 4 * hi + (r & 3);
+        if (k0 + kr >= T) s0[r] = kNegBig;
+        if (k0 + 32 + kr >= T) s1[r] = kNegBig;
+      }
+    }
+    // Tile max on raw scores (scale > 0 commutes with max), then the log2
+    // domain: p = 2^(s * scale_log2 - m) with one FMA per score.
     float mt = kNegBig;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kr = 8 * (r >> 2) + 4 * hi + (r & 3);
-      float a = s0[r] * scale_log2;
-      float b = s1[r] * scale_log2;
-      if (k0 + kr >= T) a = kNegBig;
-      if (k0 + 32 + kr >= T) b = kNegBig;
-      s0[r] = a;
-      s1[r] = b;
-      mt = fmaxf(mt, fmaxf(a, b));
-    }
+    for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = exp2f(m_run - m_new);
+    const float m_new = fmaxf(m_run, mt * scale_log2);
     float lt = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      s0[r] = exp2f(s0[r] - m_new);
-      s1[r] = exp2f(s1[r] - m_new);
+      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, -m_new));
+      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, -m_new));
       lt += s0[r] + s1[r];
     }
     lt += __shfl_xor(lt, 32, 64);
-    l_run = l_run * alpha + lt;
-    m_run = m_new;
+    // Rescale the running sum and O only when some query's maximum grew
+    // (alpha = 1 exactly for the others); after the first tiles this is rare.
+    if (__builtin_amdgcn_read_exec() & __ballot(m_new > m_run)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < 4; ++db) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      }
     }
+    l_run += lt;
+    m_run = m_new;
     // P^T operands: chunk c covers keys 16c..16c+15 of the tile in the
     // accumulator's order: lane half hi holds keys 16c + 4*hi + 0..3 (regs
     // 8*(c%2)+0..3 of block c/2) and 16c + 8 + 4*hi + 0..3 (regs +4..7).
+    // Hardware round-to-nearest-even fp32 -> bf16 pairs.
     bf16x8 pc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const floatx16& sb = (c < 2) ? s0 : s1;
       const int base = 8 * (c & 1);
-      u32x4 w;
-      w.x = pack2(sb[base + 0], sb[base + 1]);
-      w.y = pack2(sb[base + 2], sb[base + 3]);
-      w.z = pack2(sb[base + 4], sb[base + 5]);
-      w.w = pack2(sb[base + 6], sb[base + 7]);
-      pc[c] = __builtin_bit_cast(bf16x8, w);
+      pc[c] = bf16x8{(__bf16)sb[base + 0], (__bf16)sb[base + 1], (__bf16)sb[base + 2], (__bf16)sb[base + 3],
+                     (__bf16)sb[base + 4], (__bf16)sb[base + 5], (__bf16)sb[base + 6], (__bf16)sb[base + 7]};
     }
     // O^T += V^T P^T.  The V^T operand for chunk c needs, for d = 32*db + lq,
     // the same 8 keys in the same order: two transpose reads of 4 keys each.
+    const uint16_t* vb_base = &Vs[cur][tr_row][tr_col];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(&Vs[cur][16 * c + tr_row][32 * db + tr_col]));
-        const s16x4 hv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(&Vs[cur][16 * c + 8 + tr_row][32 * db + tr_col]));
-        const short w8[8] = {lo[0], lo[1], lo[2], lo[3], hv[0], hv[1], hv[2], hv[3]};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w8), pc[c], o[db], 0, 0, 0);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb_base + (16 * c) * kVP + 32 * db));
+        const s16x4 hv =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb_base + (16 * c + 8) * kVP + 32 * db));
+        const bf16x8 vt = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hv, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt, pc[c], o[db], 0, 0, 0);
       }
     }
     if (more) store_tile(cur ^ 1);
@@ -207,7 +206,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int d = 32 * db + 8 * (r >> 2) + 4 * hi + (r & 3);
-      stage[lq * kKP + d] = f2bf(o[db][r] * inv_l);
+      stage[lq * kKP + d] = __builtin_bit_cast(uint16_t, (__bf16)(o[db][r] * inv_l));
     }
   }
   __syncthreads();
