@@ -11,7 +11,8 @@
 // 16 * 64 * 4 = 4096 floats (D % 4 == 0) stay in registers, so every input
 // row is read from HBM once and every output written once with 128-bit
 // accesses.  OutT selects the store format: float, or uint16_t for bf16
-// (round to nearest even).
+// (round to nearest even).  Callers guarantee D % 4 == 0, D <= 4096 and
+// 16-byte aligned rows.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -23,12 +24,21 @@ namespace rows {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kRowChunks = 16;
 
-__device__ __forceinline__ uint16_t f2bf(float v) {
-  const uint32_t bits = __float_as_uint(v);
-  return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+// Every access goes through a buffer resource spanning exactly one row (or
+// one D-vector): chunks past D read zero and their stores are dropped by the
+// hardware range check, so the 16 loads of a row are issued back to back with
+// no per-chunk branch (and no wait between them).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ floatx4 ld4(__amdgpu_buffer_rsrc_t r, int i) {
+  return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(16 * i), 0, 0));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -37,32 +47,48 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// fp32 -> bf16 bits, hardware round-to-nearest-even (finite inputs).
+__device__ __forceinline__ uint16_t f2bf(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+
+// 4 values to dst with one 128-bit (fp32) or 64-bit (bf16) store.
 __device__ __forceinline__ void store4(float* dst, floatx4 v) { *reinterpret_cast<floatx4*>(dst) = v; }
 
 __device__ __forceinline__ void store4(uint16_t* dst, floatx4 v) {
-  u32x2 w;
-  w.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
-  w.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
-  *reinterpret_cast<u32x2*>(dst) = w;
+  const bf16x4 h = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+  *reinterpret_cast<u32x2*>(dst) = __builtin_bit_cast(u32x2, h);
 }
 
-__device__ __forceinline__ floatx4 load_or_one(const float* p, int i) {
-  return p ? reinterpret_cast<const floatx4*>(p)[i] : floatx4{1.f, 1.f, 1.f, 1.f};
+// Chunk i (4 values) of a row: fp32, or bf16 with the hardware
+// round-to-nearest-even conversion.
+__device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, int i, floatx4 v, float*) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (uint32_t)(16 * i), 0, 0);
 }
 
-// Loads row t of src into v and returns the wave-wide sum of squares.
-__device__ __forceinline__ float load_row(const float* __restrict__ src, int d4, int lane, floatx4 (&v)[kRowChunks]) {
-  const floatx4* row = reinterpret_cast<const floatx4*>(src);
+__device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, int i, floatx4 v, uint16_t*) {
+  const bf16x4 h = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, h), r, (uint32_t)(8 * i), 0, 0);
+}
+
+// Issues the 16 chunk loads of a row (zero past D) into v.
+__device__ __forceinline__ void load_row(const float* __restrict__ src, int D, int lane, floatx4 (&v)[kRowChunks]) {
+  const __amdgpu_buffer_rsrc_t r = row_rsrc(src, 4 * D);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) v[c] = ld4(r, c * 64 + lane);
+}
+
+__device__ __forceinline__ float sum_sq(const floatx4 (&v)[kRowChunks]) {
   float ss = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int i = c * 64 + lane;
-    if (i < d4) {
-      v[c] = row[i];
-      ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
-    }
-  }
+  for (int c = 0; c < kRowChunks; ++c) ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
   return wave_sum(ss);
+}
+
+// The D-vectors (norm weights, adaLN scale and gate) are staged once per
+// workgroup in LDS (absent vectors as ones) while the row loads are in
+// flight; the per-chunk reads are then LDS reads, not dependent global loads.
+__device__ __forceinline__ void stage_vec(floatx4* dst, const float* src, int d4) {
+  for (int i = (int)threadIdx.x; i < d4; i += (int)blockDim.x)
+    dst[i] = src ? reinterpret_cast<const floatx4*>(src)[i] : floatx4{1.f, 1.f, 1.f, 1.f};
 }
 
 // out = RMSNorm(x; w) * scale.
@@ -70,26 +96,28 @@ template <typename OutT>
 __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                        const float* __restrict__ scale, OutT* __restrict__ out, int T,
                                                        int D, float eps) {
+  __shared__ floatx4 sw[1024], ssc[1024];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = (int)blockIdx.x * 4 + wave;
-  if (t >= T) return;
+  const int t = min((int)blockIdx.x * 4 + wave, T - 1);
   const int d4 = D >> 2;
   floatx4 v[kRowChunks];
-  const float ss = load_row(x + (size_t)t * D, d4, lane, v);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const floatx4* w4 = reinterpret_cast<const floatx4*>(w);
+  load_row(x + (size_t)t * D, D, lane, v);
+  stage_vec(sw, w, d4);
+  stage_vec(ssc, scale, d4);
+  __syncthreads();
+  if ((int)blockIdx.x * 4 + wave >= T) return;
+  const float inv = 1.0f / sqrtf(sum_sq(v) / (float)D + eps);
+  const __amdgpu_buffer_rsrc_t ro = row_rsrc(out + (size_t)t * D, (int)sizeof(OutT) * D);
 #pragma unroll
   for (int c = 0; c < kRowChunks; ++c) {
     const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 g = w4[i], sc = load_or_one(scale, i);
-      floatx4 o;
-      o.x = v[c].x * inv * g.x * sc.x;
-      o.y = v[c].y * inv * g.y * sc.y;
-      o.z = v[c].z * inv * g.z * sc.z;
-      o.w = v[c].w * inv * g.w * sc.w;
-      store4(out + (size_t)t * D + 4 * i, o);
-    }
+    const floatx4 g = sw[i], sc = ssc[i];
+    floatx4 o;
+    o.x = v[c].x * inv * g.x * sc.x;
+    o.y = v[c].y * inv * g.y * sc.y;
+    o.z = v[c].z * inv * g.z * sc.z;
+    o.w = v[c].w * inv * g.w * sc.w;
+    st4(ro, i, o, out);
   }
 }
 
@@ -100,46 +128,50 @@ __global__ __launch_bounds__(256) void resid_norm_mod_kernel(const float* __rest
                                                              const float* __restrict__ n3, const float* __restrict__ scale,
                                                              float* __restrict__ r_out, OutT* __restrict__ f_out, int T,
                                                              int D, float eps) {
+  __shared__ floatx4 s2[1024], sg[1024], s3[1024], ssc[1024];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = (int)blockIdx.x * 4 + wave;
-  if (t >= T) return;
+  const int t = min((int)blockIdx.x * 4 + wave, T - 1);
   const int d4 = D >> 2;
-  floatx4 v[kRowChunks];
-  const float ss = load_row(proj + (size_t)t * D, d4, lane, v);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const floatx4* x4 = reinterpret_cast<const floatx4*>(x + (size_t)t * D);
-  const floatx4* w4 = reinterpret_cast<const floatx4*>(n2);
+  floatx4 v[kRowChunks], xv[kRowChunks];
+  load_row(proj + (size_t)t * D, D, lane, v);
+  load_row(x + (size_t)t * D, D, lane, xv);
+  stage_vec(s2, n2, d4);
+  stage_vec(sg, gate, d4);
+  stage_vec(s3, n3, d4);
+  stage_vec(ssc, scale, d4);
+  __syncthreads();
+  if ((int)blockIdx.x * 4 + wave >= T) return;
+  const float inv = 1.0f / sqrtf(sum_sq(v) / (float)D + eps);
+  const __amdgpu_buffer_rsrc_t rr = row_rsrc(r_out + (size_t)t * D, 4 * D);
   float ss2 = 0.0f;
 #pragma unroll
   for (int c = 0; c < kRowChunks; ++c) {
     const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 xv = x4[i], g = load_or_one(gate, i), w = w4[i];
-      floatx4 r;
-      r.x = xv.x + g.x * (v[c].x * inv * w.x);
-      r.y = xv.y + g.y * (v[c].y * inv * w.y);
-      r.z = xv.z + g.z * (v[c].z * inv * w.z);
-      r.w = xv.w + g.w * (v[c].w * inv * w.w);
-      v[c] = r;
-      reinterpret_cast<floatx4*>(r_out + (size_t)t * D)[i] = r;
-      ss2 += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
-    }
+    const floatx4 g = sg[i], w = s2[i];
+    floatx4 r;
+    r.x = xv[c].x + g.x * (v[c].x * inv * w.x);
+    r.y = xv[c].y + g.y * (v[c].y * inv * w.y);
+    r.z = xv[c].z + g.z * (v[c].z * inv * w.z);
+    r.w = xv[c].w + g.w * (v[c].w * inv * w.w);
+    // chunks past D hold garbage vector values: keep them out of the sum
+    if (i >= d4) r = floatx4{0.f, 0.f, 0.f, 0.f};
+    v[c] = r;
+    st4(rr, i, r, r_out);
+    ss2 += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
   }
   ss2 = wave_sum(ss2);
   const float inv2 = 1.0f / sqrtf(ss2 / (float)D + eps);
-  const floatx4* w3 = reinterpret_cast<const floatx4*>(n3);
+  const __amdgpu_buffer_rsrc_t rf = row_rsrc(f_out + (size_t)t * D, (int)sizeof(OutT) * D);
 #pragma unroll
   for (int c = 0; c < kRowChunks; ++c) {
     const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 w = w3[i], sc = load_or_one(scale, i);
-      floatx4 o;
-      o.x = v[c].x * inv2 * w.x * sc.x;
-      o.y = v[c].y * inv2 * w.y * sc.y;
-      o.z = v[c].z * inv2 * w.z * sc.z;
-      o.w = v[c].w * inv2 * w.w * sc.w;
-      store4(f_out + (size_t)t * D + 4 * i, o);
-    }
+    const floatx4 w = s3[i], sc = ssc[i];
+    floatx4 o;
+    o.x = v[c].x * inv2 * w.x * sc.x;
+    o.y = v[c].y * inv2 * w.y * sc.y;
+    o.z = v[c].z * inv2 * w.z * sc.z;
+    o.w = v[c].w * inv2 * w.w * sc.w;
+    st4(rf, i, o, f_out);
   }
 }
 
@@ -147,27 +179,29 @@ __global__ __launch_bounds__(256) void resid_norm_mod_kernel(const float* __rest
 __global__ __launch_bounds__(256) void final_resid_kernel(const float* __restrict__ r, const float* __restrict__ w2,
                                                           const float* __restrict__ n4, const float* __restrict__ gate,
                                                           float* __restrict__ out, int T, int D, float eps) {
+  __shared__ floatx4 s4[1024], sg[1024];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = (int)blockIdx.x * 4 + wave;
-  if (t >= T) return;
+  const int t = min((int)blockIdx.x * 4 + wave, T - 1);
   const int d4 = D >> 2;
-  floatx4 v[kRowChunks];
-  const float ss = load_row(w2 + (size_t)t * D, d4, lane, v);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const floatx4* r4 = reinterpret_cast<const floatx4*>(r + (size_t)t * D);
-  const floatx4* w4 = reinterpret_cast<const floatx4*>(n4);
+  floatx4 v[kRowChunks], rv[kRowChunks];
+  load_row(w2 + (size_t)t * D, D, lane, v);
+  load_row(r + (size_t)t * D, D, lane, rv);
+  stage_vec(s4, n4, d4);
+  stage_vec(sg, gate, d4);
+  __syncthreads();
+  if ((int)blockIdx.x * 4 + wave >= T) return;
+  const float inv = 1.0f / sqrtf(sum_sq(v) / (float)D + eps);
+  const __amdgpu_buffer_rsrc_t ro = row_rsrc(out + (size_t)t * D, 4 * D);
 #pragma unroll
   for (int c = 0; c < kRowChunks; ++c) {
     const int i = c * 64 + lane;
-    if (i < d4) {
-      const floatx4 rv = r4[i], w = w4[i], g = load_or_one(gate, i);
-      floatx4 o;
-      o.x = rv.x + g.x * (v[c].x * inv * w.x);
-      o.y = rv.y + g.y * (v[c].y * inv * w.y);
-      o.z = rv.z + g.z * (v[c].z * inv * w.z);
-      o.w = rv.w + g.w * (v[c].w * inv * w.w);
-      reinterpret_cast<floatx4*>(out + (size_t)t * D)[i] = o;
-    }
+    const floatx4 w = s4[i], g = sg[i];
+    floatx4 o;
+    o.x = rv[c].x + g.x * (v[c].x * inv * w.x);
+    o.y = rv[c].y + g.y * (v[c].y * inv * w.y);
+    o.z = rv[c].z + g.z * (v[c].z * inv * w.z);
+    o.w = rv[c].w + g.w * (v[c].w * inv * w.w);
+    st4(ro, i, o, out);
   }
 }
 
