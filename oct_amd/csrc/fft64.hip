@@ -173,6 +173,146 @@ __global__ __launch_bounds__(256) void fft_lds_kernel(const double2* __restrict_
   }
 }
 
+// LDS index with one unused slot after every 16 elements: 16-element groups
+// written by neighbouring lanes land on distinct bank groups.
+__device__ __forceinline__ uint32_t pad16(uint32_t i) { return i + (i >> 4); }
+
+// Lengths L >= 16.  Each of the first total/16 threads owns 16 consecutive
+// bit-reversed positions 16b..16b+15 of one sequence: position 16b + k holds
+// x[rev(16b + k)] = x[rev'(b) + rev4(k) * L/16] (rev' over log2(L)-4 bits),
+// so the thread loads those 16 inputs directly (stride L/16, the bit-reversal
+// done by register placement), runs butterfly stages 1-4 in registers -- the
+// same operations, operands and twiddles as one stage per barrier -- and
+// writes its 16 results contiguously to LDS (padded).  The remaining stages
+// (span >= 32) run two per barrier as in fft_lds_kernel, on padded indices.
+// Against fft_lds_kernel this removes the bank-conflicted bit-reversed
+// scatter and two LDS round trips with their barriers.
+__global__ __launch_bounds__(256) void fft_reg16_kernel(const double2* __restrict__ in, double2* __restrict__ out,
+                                                        const double2* __restrict__ roots, uint32_t n_total,
+                                                        uint32_t log2l, uint32_t log2seqs, uint64_t in_seq,
+                                                        uint64_t in_elem, uint64_t out_seq, uint64_t out_elem,
+                                                        int post, int seq_fast_in, int seq_fast_out) {
+#pragma clang fp contract(off)
+  extern __shared__ double2 smem[];
+  const uint32_t L = 1u << log2l;
+  const uint32_t seqs = 1u << log2seqs;
+  const uint32_t total = L << log2seqs;
+  double2* buf = smem;
+  double2* tw = smem + pad16(total);
+  const uint32_t tstride = n_total >> log2l;
+  for (uint32_t j = threadIdx.x; j < (L >> 1); j += blockDim.x) tw[j] = roots[(size_t)j * tstride];
+  uint32_t blk = blockIdx.x;
+  if ((gridDim.x & 7u) == 0u) blk = (blk & 7u) * (gridDim.x >> 3) + (blk >> 3);
+  const uint64_t q0 = (uint64_t)blk << log2seqs;
+
+  const uint32_t lgq = log2l - 4;        // log2 of 16-element groups per sequence
+  const uint32_t groups = total >> 4;    // <= 256
+  const uint32_t g = threadIdx.x;
+  double2 a[16];
+  uint32_t s = 0, b = 0;
+  if (g < groups) {
+    s = seq_fast_in ? (g & (seqs - 1)) : (g >> lgq);
+    b = seq_fast_in ? (g >> log2seqs) : (g & ((1u << lgq) - 1));
+    const uint32_t base = lgq == 0 ? 0u : (__brev(b) >> (32u - lgq));
+    const double2* src = in + (q0 + s) * in_seq;
+#pragma unroll
+    for (uint32_t m = 0; m < 16; ++m) {
+      const uint32_t k = ((m & 1u) << 3) | ((m & 2u) << 1) | ((m & 4u) >> 1) | ((m & 8u) >> 3);  // rev4(m)
+      a[k] = src[(uint64_t)(base + (m << lgq)) * in_elem];
+    }
+  }
+  __syncthreads();  // twiddles in LDS
+  if (g < groups) {
+#pragma unroll
+    for (uint32_t lg = 1; lg <= 4; ++lg) {
+      const uint32_t half = 1u << (lg - 1);
+#pragma unroll
+      for (uint32_t p = 0; p < 16; ++p) {
+        if (p & half) continue;
+        const double2 t = cmul(tw[(p & (half - 1)) << (log2l - lg)], a[p + half]);
+        const double2 x = a[p];
+        a[p] = make_double2(x.x + t.x, x.y + t.y);
+        a[p + half] = make_double2(x.x - t.x, x.y - t.y);
+      }
+    }
+    double2* dst = buf + 17u * ((s << lgq) + b);  // pad16((s << log2l) + 16 b)
+#pragma unroll
+    for (uint32_t k = 0; k < 16; ++k) dst[k] = a[k];
+  }
+  __syncthreads();
+  uint32_t lg = 5;
+  for (; lg + 1 <= log2l; lg += 2) {
+    const uint32_t h = 1u << (lg - 1);
+    const uint32_t quads = total >> 2;
+    for (uint32_t q = threadIdx.x; q < quads; q += blockDim.x) {
+      const uint32_t sq = q >> (log2l - 2);
+      const uint32_t gg = q & ((L >> 2) - 1);
+      const uint32_t j = gg & (h - 1);
+      const uint32_t p = (sq << log2l) + ((gg >> (lg - 1)) << (lg + 1)) + j;
+      const uint32_t i0 = pad16(p), i1 = pad16(p + h), i2 = pad16(p + 2 * h), i3 = pad16(p + 3 * h);
+      const double2 a0 = buf[i0], a1 = buf[i1], a2 = buf[i2], a3 = buf[i3];
+      const double2 w1 = tw[j << (log2l - lg)];
+      double2 t = cmul(w1, a1);
+      const double2 b0 = make_double2(a0.x + t.x, a0.y + t.y);
+      const double2 b1 = make_double2(a0.x - t.x, a0.y - t.y);
+      t = cmul(w1, a3);
+      const double2 b2 = make_double2(a2.x + t.x, a2.y + t.y);
+      const double2 b3 = make_double2(a2.x - t.x, a2.y - t.y);
+      t = cmul(tw[j << (log2l - lg - 1)], b2);
+      buf[i0] = make_double2(b0.x + t.x, b0.y + t.y);
+      buf[i2] = make_double2(b0.x - t.x, b0.y - t.y);
+      t = cmul(tw[(j + h) << (log2l - lg - 1)], b3);
+      buf[i1] = make_double2(b1.x + t.x, b1.y + t.y);
+      buf[i3] = make_double2(b1.x - t.x, b1.y - t.y);
+    }
+    __syncthreads();
+  }
+  if (lg == log2l) {  // an odd count of LDS stages leaves the last stage (span L) alone
+    const uint32_t half = L >> 1;
+    for (uint32_t bb = threadIdx.x; bb < (total >> 1); bb += blockDim.x) {
+      const uint32_t sq = bb >> (log2l - 1);
+      const uint32_t j = bb & (half - 1);
+      const uint32_t p = (sq << log2l) + j;
+      const uint32_t i0 = pad16(p), i1 = pad16(p + half);
+      const double2 t = cmul(tw[j], buf[i1]);
+      const double2 x = buf[i0];
+      buf[i0] = make_double2(x.x + t.x, x.y + t.y);
+      buf[i1] = make_double2(x.x - t.x, x.y - t.y);
+    }
+    __syncthreads();
+  }
+  const uint32_t half_n = n_total >> 1;
+  double2 v[kFftPerThread], w[kFftPerThread];
+#pragma unroll
+  for (uint32_t u = 0; u < kFftPerThread; ++u) {
+    const uint32_t e = threadIdx.x + u * kFftThreads;
+    if (e < total) {
+      const uint32_t so = seq_fast_out ? (e & (seqs - 1)) : (e >> log2l);
+      const uint32_t k = seq_fast_out ? (e >> log2seqs) : (e & (L - 1));
+      v[u] = buf[pad16((so << log2l) + k)];
+      if (post) {
+        const uint64_t pp = (q0 + so) * (uint64_t)k;  // < N
+        w[u] = roots[pp < half_n ? pp : pp - half_n];
+      }
+    }
+  }
+#pragma unroll
+  for (uint32_t u = 0; u < kFftPerThread; ++u) {
+    const uint32_t e = threadIdx.x + u * kFftThreads;
+    if (e < total) {
+      const uint32_t so = seq_fast_out ? (e & (seqs - 1)) : (e >> log2l);
+      const uint32_t k = seq_fast_out ? (e >> log2seqs) : (e & (L - 1));
+      double2 r = v[u];
+      if (post) {
+        const uint64_t pp = (q0 + so) * (uint64_t)k;
+        const double2 wt = pp < half_n ? w[u] : make_double2(-w[u].x, -w[u].y);
+        r = cmul(wt, r);
+      }
+      out[(q0 + so) * out_seq + (uint64_t)k * out_elem] = r;
+    }
+  }
+}
+
 uint32_t ilog2(uint32_t v) {
   uint32_t r = 0;
   while ((1u << r) < v) ++r;
@@ -195,17 +335,28 @@ hipError_t launch_pass(const double2* in, double2* out, const double2* roots, ui
   const uint32_t log2seqs = pick_log2seqs(log2l, log2count);
   const uint32_t blocks = 1u << (log2count - log2seqs);
   // the sequences plus the L/2 twiddles of the sub-transform (at most 64 + 32 KiB)
-  const size_t lds = (((size_t)1 << (log2l + log2seqs)) + ((size_t)1 << log2l) / 2) * sizeof(double2);
+  const size_t elems = (size_t)1 << (log2l + log2seqs);
   static bool lds_raised = false;
   if (!lds_raised) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_lds_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)((kFftMaxLds + kFftMaxLds / 2) * sizeof(double2)));
+    // the sequences (padded for the 16-element kernel) plus the L/2 twiddles
+    const int max_lds = (int)((kFftMaxLds + kFftMaxLds / 16 + kFftMaxLds / 2) * sizeof(double2));
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_lds_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_reg16_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
     if (e != hipSuccess) return e;
     lds_raised = true;
   }
-  hipLaunchKernelGGL(fft_lds_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l, log2seqs,
-                     in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
+  if (log2l >= 4) {
+    const size_t lds = (elems + elems / 16 + ((size_t)1 << log2l) / 2) * sizeof(double2);
+    hipLaunchKernelGGL(fft_reg16_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l,
+                       log2seqs, in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
+  } else {
+    const size_t lds = (elems + ((size_t)1 << log2l) / 2) * sizeof(double2);
+    hipLaunchKernelGGL(fft_lds_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l,
+                       log2seqs, in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
+  }
   return hipGetLastError();
 }
 
