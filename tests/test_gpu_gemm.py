@@ -67,6 +67,22 @@ def test_exact_tail_shapes(gpu_runtime, m, n, k):
     assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
 
 
+# One shape per kernel variant the plan model chooses (tile shape, direct-to-LDS
+# or register-staged loads, split-K or not), ragged in m and n:
+#   64x128 staged (1,2,1) and 4 K slices (1,2,256); 128x128 staged (513,4100,1)
+#   and 12 slices (100,2050,4096); 128x128 direct (513,4100,16) and 6 slices
+#   (100,4100,1024); 128x256 staged (3000,4100,1); 128x256 direct (4097,4100,16).
+@pytest.mark.parametrize("m,n,k", [(1, 2, 1), (1, 2, 256), (513, 4100, 1), (100, 2050, 4096), (513, 4100, 16),
+                                   (100, 4100, 1024), (3000, 4100, 1), (4097, 4100, 16)])
+def test_plan_variants(gpu_runtime, m, n, k):
+    a = oracle.uniform(300 + m, (m, k))
+    b = oracle.uniform(400 + n, (k, n))
+    out = _sgemm(gpu_runtime, a, b)
+    rows = (0, m // 2, m - 1)
+    for r in rows:
+        assert oracle.normwise_rel_err(out[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r]) <= FP32_NORMWISE
+
+
 def test_c1_1024_full(gpu_runtime):
     # M=N=K=1024, U[-1,1] seeded
     a = oracle.uniform(1, (1024, 1024))
