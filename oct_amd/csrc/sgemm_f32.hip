@@ -288,13 +288,17 @@ struct DlCfg {
   static constexpr int kStage = kABytes + kBK * kBPitch;
 };
 
-template <int kBN>
+template <int kBN, int kWaves>
 __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, const float* __restrict__ B, float* C,
                                                   int M, int N, int K, int tiles_m, int tiles_n, int lda, int ldb,
                                                   int ldc, const float* R, int ldr, int k_len, long long sa,
                                                   long long sb, long long sc, char* S0, char* S1) {
   using D = DlCfg<kBN>;
   constexpr int kNI = D::kNI;
+  constexpr int kRW = 256 / kWaves;                  // rows per wave (waves: kWaves/2 along M, 2 along N)
+  constexpr int kMI = kRW / 32;
+  constexpr int kAI = 8 / kWaves;                    // A transfers (16-row blocks) per wave
+  constexpr int kBI = (kBN == 256 ? 16 : 8) / kWaves;  // B transfers per wave
   typedef __attribute__((address_space(3))) void lds_void;
 
   if (gridDim.z > 1) {
@@ -326,23 +330,23 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
   const __amdgpu_buffer_rsrc_t rsb =
       __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)((size_t)K * ldb * 4), 0x00020000);
 
-  // Per-lane source offsets (bytes, k0 = 0) of this wave's 2 A and kBN/64 B
+  // Per-lane source offsets (bytes, k0 = 0) of this wave's kAI A and kBI B
   // instructions; the tile's k offset travels in the scalar soffset.
-  uint32_t a_off[2], b_off[kBN / 64];
+  uint32_t a_off[kAI], b_off[kBI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = 2 * wave + i;  // A block: rows 16q..16q+15
+  for (int i = 0; i < kAI; ++i) {
+    const int q = kAI * wave + i;  // A block: rows 16q..16q+15
     const int r = lane >> 2;
     const int kc = (lane & 3) ^ ((r >> 2) & 3);
     a_off[i] = (uint32_t)(((row0 + 16 * q + r) * lda + 4 * kc) * 4);
   }
 #pragma unroll
-  for (int i = 0; i < kBN / 64; ++i) {
+  for (int i = 0; i < kBI; ++i) {
     if constexpr (kBN == 256) {
-      const int kr = 4 * wave + i;  // one 256-wide row per instruction
+      const int kr = kBI * wave + i;  // one 256-wide row per instruction
       b_off[i] = (uint32_t)((kr * ldb + col0 + 4 * lane) * 4);
     } else {
-      const int q = 2 * wave + i;  // rows 2q, 2q+1
+      const int q = kBI * wave + i;  // rows 2q, 2q+1
       const int kr = 2 * q + (lane >> 5);
       const int c = (lane & 31) ^ (((kr >> 2) & 1) << 3);
       b_off[i] = (uint32_t)((kr * ldb + col0 + 4 * c) * 4);
@@ -352,13 +356,13 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
     const int sa_k = __builtin_amdgcn_readfirstlane(k0 * 4);
     const int sb_k = __builtin_amdgcn_readfirstlane(k0 * ldb * 4);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(stage + (2 * wave + i) * 1024), 16, a_off[i], sa_k, 0,
-                                               0);
+    for (int i = 0; i < kAI; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(stage + (kAI * wave + i) * 1024), 16, a_off[i], sa_k,
+                                               0, 0);
 #pragma unroll
-    for (int i = 0; i < kBN / 64; ++i) {
-      char* dst = kBN == 256 ? stage + D::kABytes + (4 * wave + i) * D::kBPitch
-                             : stage + D::kABytes + (2 * wave + i) * 1024;
+    for (int i = 0; i < kBI; ++i) {
+      char* dst = kBN == 256 ? stage + D::kABytes + (kBI * wave + i) * D::kBPitch
+                             : stage + D::kABytes + (kBI * wave + i) * 1024;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_void*)dst, 16, b_off[i], sb_k, 0, 0);
     }
   };
@@ -366,7 +370,7 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
   // Operand addresses (bytes within a stage).
   const int lrow = lane & 31;
   const int h = lane >> 5;
-  const int am = wm * 64 + lrow;  // + 32 mi: two blocks further, same swizzle
+  const int am = wm * kRW + lrow;  // + 32 mi: two blocks further, same swizzle
   const int ar = am & 15;
   const uint32_t a_base = (uint32_t)((am >> 4) * 1024 + ar * 64 + ((h ^ ((ar >> 2) & 3)) << 4));
   uint32_t b_base[kBN == 256 ? 1 : 2];
@@ -379,18 +383,18 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
                               (lrow & 3) * 4);
   }
 
-  floatx16 acc[2][kNI];
+  floatx16 acc[kMI][kNI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kMI; ++i)
 #pragma unroll
     for (int j = 0; j < kNI; ++j) acc[i][j] = floatx16{};
 
   auto compute = [&](const char* st) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      floatx4 a[2];
+      floatx4 a[kMI];
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int mi = 0; mi < kMI; ++mi)
         a[mi] = *reinterpret_cast<const floatx4*>(st + ((a_base ^ (uint32_t)(32 * p)) + mi * 2048));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -404,7 +408,7 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
             b[ni] = *reinterpret_cast<const float*>(st + b_base[ni] + row_off);
         }
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < kMI; ++mi)
 #pragma unroll
           for (int ni = 0; ni < kNI; ++ni)
             acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mi][j], b[ni], acc[mi][ni], 0, 0, 0);
@@ -438,7 +442,7 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
   auto store_block = [&](const floatx16& acc, int mi, int ni) {
     const int col = col0 + wn * (kBN / 2) + ni * 32 + lrow;
     if (col >= N) return;
-    const int rb = row0 + wm * 64 + mi * 32 + 4 * h;
+    const int rb = row0 + wm * kRW + mi * 32 + 4 * h;
     float* cp = C + (size_t)rb * ldc + col;
     const float* rp = R != nullptr ? R + (size_t)rb * ldr + col : nullptr;
 #pragma unroll
@@ -452,7 +456,7 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
     }
   };
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kMI; ++i)
 #pragma unroll
     for (int j = 0; j < kNI; ++j) store_block(acc[i][j], i, j);
 }
@@ -465,17 +469,21 @@ __global__ __launch_bounds__(256, 3) void sgemm_f32_dl256_kernel(const float* __
                                                                  long long sa, long long sb, long long sc) {
   __shared__ __attribute__((aligned(1024))) char S0[DlCfg<256>::kStage];
   __shared__ __attribute__((aligned(1024))) char S1[DlCfg<256>::kStage];
-  sgemm_f32_dl_body<256>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+  sgemm_f32_dl_body<256, 4>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
 }
 
-__global__ __launch_bounds__(256, 4) void sgemm_f32_dl128_kernel(const float* __restrict__ A,
-                                                                 const float* __restrict__ B, float* C, int M, int N,
-                                                                 int K, int tiles_m, int tiles_n, int lda, int ldb,
-                                                                 int ldc, const float* R, int ldr, int k_len,
-                                                                 long long sa, long long sb, long long sc) {
+// 128x128 with eight waves (each 32x64, 50 VGPRs): two waves per SIMD even
+// when the grid gives one workgroup per CU (small and split-K products), and
+// five workgroups per CU (LDS-bound) on large grids.
+__global__ __launch_bounds__(512, 1) void sgemm_f32_dl128w8_kernel(const float* __restrict__ A,
+                                                                   const float* __restrict__ B, float* C, int M,
+                                                                   int N, int K, int tiles_m, int tiles_n, int lda,
+                                                                   int ldb, int ldc, const float* R, int ldr,
+                                                                   int k_len, long long sa, long long sb,
+                                                                   long long sc) {
   __shared__ __attribute__((aligned(1024))) char S0[DlCfg<128>::kStage];
   __shared__ __attribute__((aligned(1024))) char S1[DlCfg<128>::kStage];
-  sgemm_f32_dl_body<128>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+  sgemm_f32_dl_body<128, 8>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
 }
 
 // y[m] = A[m,:] . x : one wave per row, 4 rows per workgroup.  HBM-bound:
@@ -530,13 +538,52 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+// Same sum, 4 columns per thread (N, ldc, ldr multiples of 4, 16-byte aligned
+// C and R): one workgroup row-slice per (blockIdx.x, row), no per-element
+// 64-bit division; the slabs are read with 128-bit loads, all issued before
+// the adds (same order of additions as the scalar kernel).
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(const float* __restrict__ P, float* C, int M, int N,
+                                                             int ldc, int splits, const float* R, int ldr) {
+  const int n4 = N >> 2;
+  const int c4 = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (c4 >= n4) return;
+  const size_t slab4 = (size_t)M * n4;
+  const floatx4* P4 = reinterpret_cast<const floatx4*>(P);
+  for (int row = (int)blockIdx.y; row < M; row += (int)gridDim.y) {
+    const size_t i = (size_t)row * n4 + c4;
+    floatx4 part[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      if (s < splits) part[s] = P4[(size_t)s * slab4 + i];
+    floatx4 v = part[0];
+#pragma unroll
+    for (int s = 1; s < 16; ++s)
+      if (s < splits) {
+        v.x += part[s].x;
+        v.y += part[s].y;
+        v.z += part[s].z;
+        v.w += part[s].w;
+      }
+    if (R != nullptr) {
+      const floatx4 r = reinterpret_cast<const floatx4*>(R + (size_t)row * ldr)[c4];
+      v.x += r.x;
+      v.y += r.y;
+      v.z += r.z;
+      v.w += r.w;
+    }
+    reinterpret_cast<floatx4*>(C + (size_t)row * ldc)[c4] = v;
+  }
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Tile shapes: 0 = 128x256, 1 = 128x128, 2 = 64x128 (register-staged loads);
-// 3 = 128x256, 4 = 128x128 (direct-to-LDS, branch-free shapes only).
+// 3 = 128x256 (four waves), 4 = 128x128 (eight waves) direct-to-LDS, for
+// branch-free shapes only (otherwise the staged shape of the same size runs).
 constexpr int kTileShapes = 5;
 constexpr int kTileM[kTileShapes] = {128, 128, 64, 128, 128};
 constexpr int kTileN[kTileShapes] = {256, 128, 128, 256, 128};
+constexpr int kStagedFallback[kTileShapes] = {0, 1, 2, 0, 1};
 
 struct SgemmPlan {
   int tile;    // index into kTileM / kTileN
@@ -578,8 +625,8 @@ bool buffer_path(const float* a, int lda, long long sa, const float* b, int ldb,
 // (~3 us + (s+1) M N floats at ~2 TB/s).  The constants are fitted to timings of
 // all tile shapes and slice counts at the benchmark and transformer-block
 // shapes on MI355X.
-constexpr int kTileOcc[kTileShapes] = {2, 3, 4, 3, 4};
-constexpr double kTileEff[kTileShapes] = {0.92, 1.03, 0.835, 1.0, 1.05};
+constexpr int kTileOcc[kTileShapes] = {2, 3, 4, 3, 5};
+constexpr double kTileEff[kTileShapes] = {0.92, 0.95, 0.835, 1.0, 1.05};
 constexpr double kOccEff[4] = {0.70, 0.846, 0.93, 0.932};
 
 double plan_cost(const SgemmPlan& p, uint32_t m, uint32_t n, uint32_t batch) {
@@ -647,7 +694,7 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
   const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
                    (sb % 4 == 0) && aligned16(a) && aligned16(b);
   const bool buf = buffer_path(a, lda, sa, b, ldb, sb, m, n, k, p.k_len);
-  const int tile = (p.tile >= 3 && !buf) ? p.tile - 3 : p.tile;
+  const int tile = (p.tile >= 3 && !buf) ? kStagedFallback[p.tile] : p.tile;
   const int bm = kTileM[tile], bn = kTileN[tile];
   const int tiles_m = (int)((m + bm - 1) / bm);
   const int tiles_n = (int)((n + bn - 1) / bn);
@@ -661,7 +708,7 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
                          tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
       break;
     case 4:
-      hipLaunchKernelGGL(sgemm_f32_dl128_kernel, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+      hipLaunchKernelGGL(sgemm_f32_dl128w8_kernel, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n, (int)k,
                          tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
       break;
     case 0:
@@ -680,10 +727,18 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
   if (split) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const size_t total = (size_t)m * n;
-    const unsigned blocks = (unsigned)std::min((size_t)8192, (total + 255) / 256);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, c, (int)m, (int)n, ldc,
-                       p.splits, residual, ldr);
+    const bool vec4 = n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && (residual == nullptr || (ldr % 4 == 0 && aligned16(residual)));
+    if (vec4 && p.splits <= 16) {
+      const unsigned bx = (unsigned)((n / 4 + 255) / 256);
+      const unsigned by = (unsigned)std::min<uint32_t>(m, std::max(1u, 8192u / bx));
+      hipLaunchKernelGGL(splitk_reduce4_kernel, dim3(bx, by), dim3(256), 0, stream, partial, c, (int)m, (int)n, ldc,
+                         p.splits, residual, ldr);
+    } else {
+      const size_t total = (size_t)m * n;
+      const unsigned blocks = (unsigned)std::min((size_t)8192, (total + 255) / 256);
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, c, (int)m, (int)n, ldc,
+                         p.splits, residual, ldr);
+    }
   }
   return hipGetLastError();
 }

@@ -68,12 +68,13 @@ def test_exact_tail_shapes(gpu_runtime, m, n, k):
 
 
 # One shape per kernel variant the plan model chooses (tile shape, direct-to-LDS
-# or register-staged loads, split-K or not), ragged in m and n:
-#   64x128 staged (1,2,1) and 4 K slices (1,2,256); 128x128 staged (513,4100,1)
-#   and 12 slices (100,2050,4096); 128x128 direct (513,4100,16) and 6 slices
-#   (100,4100,1024); 128x256 staged (3000,4100,1); 128x256 direct (4097,4100,16).
-@pytest.mark.parametrize("m,n,k", [(1, 2, 1), (1, 2, 256), (513, 4100, 1), (100, 2050, 4096), (513, 4100, 16),
-                                   (100, 4100, 1024), (3000, 4100, 1), (4097, 4100, 16)])
+# or register-staged loads, split-K or not), ragged in m and/or n:
+#   64x128 staged (1,2,1) and 4 K slices (1,2,256); 128x128 staged (255,32768,1)
+#   and 12 slices (100,4100,8200); 128x128 direct, eight waves (100,32768,16)
+#   and 6 slices (100,4100,1024); 128x256 staged (1000,16384,1); 128x256 direct
+#   (700,32768,16).
+@pytest.mark.parametrize("m,n,k", [(1, 2, 1), (1, 2, 256), (255, 32768, 1), (100, 4100, 8200), (100, 32768, 16),
+                                   (100, 4100, 1024), (1000, 16384, 1), (700, 32768, 16)])
 def test_plan_variants(gpu_runtime, m, n, k):
     a = oracle.uniform(300 + m, (m, k))
     b = oracle.uniform(400 + n, (k, n))
