@@ -1238,6 +1238,18 @@ enum {
   PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL = 2u,
   PROM_MAIN_ATTENTION_ROUTE_SUBGROUP_OWNED32 = 3u,
 };
+/* reactor_api.h:43-53 */
+enum {
+  PROM_MAIN_ATTENTION_FALLBACK_NONE = 0u,
+  PROM_MAIN_ATTENTION_FALLBACK_RUNTIME_CONTRACT = 1u,
+  PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_COMPUTE = 2u,
+  PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SIZE = 3u,
+  PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_ARITHMETIC = 4u,
+  PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_BASIC = 5u,
+  PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SHUFFLE = 6u,
+  PROM_MAIN_ATTENTION_FALLBACK_TOPOLOGY_PROOF = 7u,
+  PROM_MAIN_ATTENTION_FALLBACK_SHAPE = 8u,
+};
 
 #define PROM_MODEL_BLOCK_MAX_WEIGHTS 13u
 #define PROM_MODEL_BLOCK_MAX_STEPS 7u
@@ -1338,6 +1350,64 @@ enum {
    generated models/zimage-turbo/resolved_descriptor.h). */
 #define PROM_ZIMAGE_TURBO_LOCK_ID 0x71ef202b4e34b562ull
 #define PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES 47186176u
+/* The lock's static-audit arenas (generated
+   models/zimage-turbo/resolved_audit_schedule.h:5-10, 67-70): the
+   NoiseRefiner arena holds nine full adaLN vectors (bytes 0..184319), twenty
+   256-byte summary records (184320..189439) and the 64-float attention
+   witness (189440); the ContextRefiner arena sixteen records and the witness
+   at 4096.  Bytes past the required ones are zero. */
+#define PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID PROM_ZIMAGE_TURBO_LOCK_ID
+#define PROM_ZIMAGE_TURBO_AUDIT_REQUIRED_BYTES 189696u
+#define PROM_ZIMAGE_TURBO_AUDIT_TRANSIENT_ATTENTION_OFFSET 189440u
+#define PROM_ZIMAGE_TURBO_AUDIT_STAGE_COUNT 29u
+#define PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_ARENA_BYTES 1048576u
+#define PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_REQUIRED_BYTES 4352u
+#define PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_TRANSIENT_ATTENTION_OFFSET 4096u
+#define PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_STAGE_COUNT 16u
+#define PROM_ZIMAGE_TURBO_AUDIT_TRANSIENT_ATTENTION_BYTES 256u
+
+/* reactor_api.h:775-798: the NoiseRefiner pre-attention (M1B) audit stages. */
+enum {
+  PROM_MODEL_BLOCK_M1B_AUDIT_NONE = 0u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_INGRESS_INPUT = 1u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_INGRESS_TIMESTEP = 2u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_ADALN_PROJECTION = 3u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_ATTENTION_SCALE_RAW = 4u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_ATTENTION_SCALE_ADJUSTED = 5u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_ATTENTION_GATE_RAW = 6u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_ATTENTION_GATE_TANH = 7u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_MLP_SCALE_RAW = 8u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_MLP_SCALE_ADJUSTED = 9u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_MLP_GATE_RAW = 10u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_MLP_GATE_TANH = 11u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_ATTENTION_NORM = 12u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_ATTENTION_MODULATED = 13u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_FUSED_QKV = 14u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_Q = 15u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_K = 16u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_V = 17u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_Q_NORM = 18u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_K_NORM = 19u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_POSITIONED_Q = 20u,
+  PROM_MODEL_BLOCK_M1B_AUDIT_POSITIONED_K = 21u,
+};
+
+/* reactor_api.h:989-995, 1095-1103: attention (M1C) and FFN (M1D) stages. */
+enum {
+  PROM_MODEL_BLOCK_M1C_AUDIT_ATTENTION = 1u,
+  PROM_MODEL_BLOCK_M1C_AUDIT_PROJECTION = 2u,
+  PROM_MODEL_BLOCK_M1C_AUDIT_RESIDUAL = 3u,
+};
+#define PROM_MODEL_BLOCK_M1C_TRANSIENT_AUDIT_FLOATS 64u
+enum {
+  PROM_MODEL_BLOCK_M1D_AUDIT_FFN_NORM = 1u,
+  PROM_MODEL_BLOCK_M1D_AUDIT_FFN_MODULATED = 2u,
+  PROM_MODEL_BLOCK_M1D_AUDIT_W1 = 3u,
+  PROM_MODEL_BLOCK_M1D_AUDIT_W3 = 4u,
+  PROM_MODEL_BLOCK_M1D_AUDIT_GATED_HIDDEN = 5u,
+  PROM_MODEL_BLOCK_M1D_AUDIT_W2 = 6u,
+  PROM_MODEL_BLOCK_M1D_AUDIT_FINAL_OUTPUT = 7u,
+};
 
 typedef struct PrometheusModelBlockWeightDeclaration {
   uint64_t content_identity;
@@ -1473,6 +1543,70 @@ typedef struct PrometheusNoiseRefinerFinalAuditRequest {
 
 typedef PrometheusNoiseRefinerFinalAuditRequest PrometheusContextRefinerFinalAuditRequest;
 typedef PrometheusNoiseRefinerFinalAuditRequest PrometheusMainTransformerFinalAuditRequest;
+
+/* reactor_api.h:957-1007: the stage-split NoiseRefiner.  M1B takes the BF16
+   model input and timestep and runs adaLN through the Q/K/V split (audit
+   stage optional); M1C runs the attention, projection and gated residual of
+   the matching M1B prefix and returns one of its stages plus the 64-float
+   witness; M1D runs the FFN of the matching M1C and returns one stage. */
+typedef struct PrometheusModelBlockM1BExecuteRequest {
+  uint32_t struct_size;
+  const void* model_input_bf16;
+  const void* timestep_bf16;
+  uint64_t model_input_bytes;
+  uint64_t timestep_bytes;
+  uint64_t input_identity;
+  uint64_t timestep_identity;
+  uint32_t audit_enabled;
+  uint32_t audit_stage;
+  float* audit_output;
+  uint64_t audit_element_capacity;
+} PrometheusModelBlockM1BExecuteRequest;
+
+typedef struct PrometheusModelBlockM1CExecuteRequest {
+  uint32_t struct_size;
+  uint64_t m1b_prefix_replay_identity;
+  uint64_t output_identity;
+  float* output;
+  uint64_t output_element_capacity;
+  uint32_t audit_stage;
+  float* transient_audit;
+  uint64_t transient_audit_element_capacity;
+} PrometheusModelBlockM1CExecuteRequest;
+
+typedef struct PrometheusModelBlockM1DExecuteRequest {
+  uint32_t struct_size;
+  uint64_t m1c_prefix_replay_identity;
+  uint64_t output_identity;
+  float* output;
+  uint64_t output_element_capacity;
+  uint32_t audit_stage;
+} PrometheusModelBlockM1DExecuteRequest;
+
+/* reactor_api.h:1070-1093: one audited execution into the caller's arena. */
+typedef struct PrometheusNoiseRefinerStaticAuditRequest {
+  uint32_t struct_size;
+  uint64_t lock_identity;
+  uint64_t input_generation;
+  uint64_t output_identity;
+  void* audit_arena;
+  uint64_t audit_arena_capacity_bytes;
+} PrometheusNoiseRefinerStaticAuditRequest;
+
+typedef PrometheusNoiseRefinerStaticAuditRequest PrometheusContextRefinerStaticAuditRequest;
+
+typedef struct PrometheusMainTransformerStaticAuditRequest {
+  uint32_t struct_size;
+  uint64_t session_identity;
+  uint64_t lock_identity;
+  uint32_t model_local_block_id;
+  uint64_t required_image_generation;
+  uint64_t required_context_generation;
+  uint64_t required_joint_generation;
+  uint64_t output_identity;
+  void* audit_arena;
+  uint64_t audit_arena_capacity_bytes;
+} PrometheusMainTransformerStaticAuditRequest;
 
 typedef struct PrometheusModelBlockEvidence {
   uint32_t struct_size;
@@ -1630,6 +1764,18 @@ PROM_REACTOR_API int prometheus_reactor_runtime_model_block_upload_weights(
 PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute(void* handle, uint64_t block_id,
                                                                     const PrometheusModelBlockExecuteRequest* request,
                                                                     PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2722-2730: the stage-split NoiseRefiner on a shader-24
+   block (NoiseRefiner family, bound weights); M1C and M1D need a declared
+   audit size of at least the stage they return. */
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute_m1b(
+    void* handle, uint64_t block_id, const PrometheusModelBlockM1BExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute_m1c(
+    void* handle, uint64_t block_id, const PrometheusModelBlockM1CExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute_m1d(
+    void* handle, uint64_t block_id, const PrometheusModelBlockM1DExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
 /* reactor_api.h:2734-2758: NoiseRefiner (1024 image tokens, width 3840):
    BF16 model input and timestep widened on the device, the fp32 block on the
    resident weights, output kept resident (output_generation advances). */
@@ -1644,6 +1790,11 @@ PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_rebind(void* handl
                                                                      PrometheusModelBlockEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_execute_resident(
     void* handle, uint64_t block_id, const PrometheusNoiseRefinerResidentExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2743-2745: one resident NoiseRefiner 1 execution that also
+   fills the lock's audit arena (output_generation advances). */
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_execute_static_audit(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefinerStaticAuditRequest* request,
     PrometheusModelBlockEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_audit_final(
     void* handle, uint64_t block_id, const PrometheusNoiseRefinerFinalAuditRequest* request,
@@ -1661,6 +1812,11 @@ PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner0_execute(
 PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_execute_resident(
     void* handle, uint64_t block_id, const PrometheusContextRefinerResidentExecuteRequest* request,
     PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2761-2763: parameter set 0 re-runs its external input,
+   set 1 its resident boundary, filling the ContextRefiner audit arena. */
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_execute_static_audit(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerStaticAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_audit_final(
     void* handle, uint64_t block_id, const PrometheusContextRefinerFinalAuditRequest* request,
     PrometheusModelBlockEvidence* out_evidence);
@@ -1674,6 +1830,11 @@ PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_rebind(
     PrometheusModelBlockEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute(
     void* handle, uint64_t block_id, const PrometheusMainTransformerExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence);
+/* reactor_api.h:2776-2778: layer 0 re-run on the session's JointWorking
+   stream (the session is not advanced); the arena receives its output. */
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute_static_audit(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerStaticAuditRequest* request,
     PrometheusModelBlockEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_audit_final(
     void* handle, uint64_t block_id, const PrometheusMainTransformerFinalAuditRequest* request,
@@ -1695,6 +1856,14 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_compose_j
     PrometheusCompiledModelSessionEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_get_evidence(
     void* handle, uint64_t session_id, PrometheusCompiledModelSessionEvidence* out_evidence);
+/* reactor_api.h:2798-2802: records the route the next MainTransformer
+   create decides; rejected while a model block exists.  The subgroup-owned
+   route needs 32-lane subgroups: on 64-lane wavefronts AUTO selects the
+   serial-canonical route (fallback SUBGROUP_SIZE) and an explicit
+   SUBGROUP_OWNED32 makes that create fail. */
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_set_main_attention_route(
+    void* handle, uint64_t session_id, uint32_t main_attention_route_policy,
+    PrometheusCompiledModelSessionEvidence* out_evidence);
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_destroy(void* handle, uint64_t session_id);
 /* reactor_api.h:2809-2821: the compiled-model owner the Z-Image bridge drives
    (tools/prometheus_zimage_bridge/reactor_windows.go:86-115): one block,

@@ -32,7 +32,7 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     "-Wall",
     "-Wno-unused-function",
-    # Packed-fp32 instructions are excluded on these boxes.
+    # Packed-fp32 instructions are excluded: some of their forms have given wrong results on these boxes.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{REPO_DIR / 'include'}",
 ]

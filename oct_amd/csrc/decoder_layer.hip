@@ -1,6 +1,6 @@
-// Gemma-style fp32 decoder layer on one HIP stream.
+// Gemma-style fp32 decoder layer (T=512, width 2048, FFN 16384) on one HIP stream.
 //
-// The reference has no Gemma-2B layer (SURVEY F4); its Gemma-4-E2B pieces fix
+// The reference has no Gemma-2B layer; its Gemma-4-E2B pieces fix
 // the conventions used here: RMSNorm y = x*inv*w with no mean subtraction
 // (reactor_vulkan_gemma4e2b.c:286-319), half-split RoPE pairing
 // (gemma4e2b_m1_rtx.go:834-861), multi-query scores with every query head on

@@ -51,6 +51,17 @@ constexpr int kImageTokens = 1024, kContextTokens = 32, kJointTokens = 1056;
 constexpr float kEps = 1e-5f;
 constexpr uint32_t kTransientAuditFloats = 64u;  // PROM_MODEL_BLOCK_M1C_TRANSIENT_AUDIT_FLOATS
 
+// Device audit area of a Z-Image block, allocated at create: the audit-arena
+// records (both lock arenas need fewer bytes), the summary job table, the
+// M1C witness and a [T, D] scratch for the stages the chain does not keep.
+constexpr size_t kAuditRecordBytes = 196608;
+constexpr uint32_t kAuditMaxJobs = 32;
+constexpr size_t kAuditJobOffset = kAuditRecordBytes;
+constexpr size_t kAuditWitnessOffset = kAuditJobOffset + 4096;
+constexpr size_t kAuditScratchOffset = kAuditWitnessOffset + 256;
+static_assert(PROM_ZIMAGE_TURBO_AUDIT_REQUIRED_BYTES <= kAuditRecordBytes, "NoiseRefiner arena records");
+static_assert(kAuditMaxJobs * sizeof(ZImageAuditJob) <= 4096, "audit job table");
+
 const uint32_t kSteps[PROM_MODEL_BLOCK_MAX_STEPS] = {1u, 2u, 3u, 4u, 5u, 6u, 7u};
 
 // Cache-manifest lexical order of one NoiseRefiner / MainTransformer layer
@@ -148,6 +159,7 @@ struct ModelBlock {
   float* coords = nullptr;  // [T, 3]
   char* ws = nullptr;
   size_t ws_off[kZCount] = {};
+  char* audit_dev = nullptr;  // Z-Image programs: audit records, job table, witness, scratch
   float* proof_in = nullptr;  // resident proof: input, output, audit
   float* proof_out = nullptr;
   float* proof_audit = nullptr;
@@ -157,6 +169,7 @@ struct ModelBlock {
   bool quarantined = false, output_valid = false, audit_valid = false;
   uint64_t output_generation = 0, resident_input_generation = 0;
   uint64_t plan_identity = 0, replay_identity = 0, prefix_replay = 0;
+  uint64_t m1b_prefix = 0;  // replay identity of the M1B whose pre-attention state the workspace holds
   uint64_t cold_allocations = 0, pipelines = 0, uploads = 0, executions = 0;
   uint64_t last_execution_ns = 0, gpu_total_ns = 0, gpu_compute_ns = 0, last_memcpy_ns = 0, last_readback_ns = 0;
   int32_t last_detail = 0;
@@ -171,6 +184,7 @@ struct ModelSession {
   bool created = false;
   uint64_t id = 0, lock = 0;
   uint32_t requested_profile = 0, requested_route = 0;
+  uint32_t selected_route = 0, route_fallback = 0, route_shader = 0;
   float* buf[3] = {};  // image [1024, D], context [32, D], joint [1056, D]
   Stream streams[3];
   bool joint_writing = false;
@@ -262,8 +276,8 @@ void release_block(ModelBlock* b) {
     free_set(&b->active);
     free_set(&b->candidate);
   }
-  void* ptrs[] = {b->staging, b->x, b->out, b->x_bf16, b->cond_bf16, b->cond, b->coords, b->ws,
-                  b->proof_in, b->proof_out, b->proof_audit};
+  void* ptrs[] = {b->staging, b->x,       b->out,      b->x_bf16,   b->cond_bf16,  b->cond,
+                  b->coords,  b->ws,      b->audit_dev, b->proof_in, b->proof_out, b->proof_audit};
   for (void* p : ptrs) free_dev(p);
   if (b->ev_begin) (void)hipEventDestroy(b->ev_begin);
   if (b->ev_end) (void)hipEventDestroy(b->ev_end);
@@ -370,7 +384,9 @@ void fill_session_evidence(const ModelSession* s, PrometheusCompiledModelSession
   ev->selected_execution_profile = PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY;
   ev->profile_fallback_reason = s->profile_fallback;
   ev->requested_main_attention_route = s->requested_route;
-  ev->selected_main_attention_route = PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL;
+  ev->selected_main_attention_route = s->selected_route;
+  ev->main_attention_fallback_reason = s->route_fallback;
+  ev->main_attention_shader_id = s->route_shader;
 }
 
 bool add_bytes(uint64_t* total, uint64_t v) {
@@ -627,19 +643,22 @@ int32_t take_phase_fault(Runtime* rt, bool* unobserved) {
   return 0;
 }
 
-// Runs the Z-Image block of b on x -> out (or stops at an audit point), timing
-// it with events.  Returns 0 or a model-block detail; an injected unobserved
-// completion leaves the work queued and quarantines the block.
-int32_t run_block(Runtime* rt, ModelBlock* b, const float* x, float* out, int stop_after) {
+// Runs phases first..last of the Z-Image block of b on x -> out (1 through the
+// Q/K/V split, 2 through the attention residual, 3 the FFN), timing them with
+// events.  A run from phase 1 replaces the pre-attention state an M1B left.
+// Returns 0 or a model-block detail; an injected unobserved completion leaves
+// the work queued and quarantines the block.
+int32_t run_block(Runtime* rt, ModelBlock* b, const float* x, float* out, int first_phase = 1, int last_phase = 3) {
   bool unobserved = false;
   const int32_t fault = take_phase_fault(rt, &unobserved);
   if (fault != 0) return fault;
   hipStream_t st = ctx().stream;
   const ZImageBlockWeights w = weights_of(b);
+  if (first_phase == 1) b->m1b_prefix = 0;
   (void)hipEventRecord(b->ev_begin, st);
   uint32_t launches = 0;
   if (enqueue_zimage_block_f32(w, x, b->cond, out, b->ws, b->ws_off, b->tokens, kWidth, kFfn, kEps, st, &launches,
-                               stop_after) != hipSuccess) {
+                               first_phase, last_phase) != hipSuccess) {
     (void)hipStreamSynchronize(st);
     return PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
   }
@@ -680,10 +699,12 @@ bool alloc_block_buffers(ModelBlock* b) {
                   alloc_dev(b, reinterpret_cast<void**>(&b->cond_bf16), kZImageConditionWidth * 2) &&
                   alloc_dev(b, reinterpret_cast<void**>(&b->cond), kZImageConditionWidth * 4) &&
                   alloc_dev(b, reinterpret_cast<void**>(&b->coords), (size_t)T * 3 * 4) &&
-                  alloc_dev(b, reinterpret_cast<void**>(&b->ws), ws_bytes);
+                  alloc_dev(b, reinterpret_cast<void**>(&b->ws), ws_bytes) &&
+                  alloc_dev(b, reinterpret_cast<void**>(&b->audit_dev), kAuditScratchOffset + act) &&
+                  hipMemset(b->cond, 0, kZImageConditionWidth * 4) == hipSuccess;
   b->reusable_bytes = max_weight + 2 * act + (uint64_t)T * kWidth * 2 + kZImageConditionWidth * 6 +
                       (uint64_t)T * 12 + ws_bytes;
-  b->audit_alloc_bytes = 0;  // audits copy workspace stages directly
+  b->audit_alloc_bytes = kAuditScratchOffset + act;  // stage audits copy workspace buffers directly
   b->pipelines = 13;         // the fixed kernel chain of the block
   return ok && alloc_set(b, &b->active);
 }
@@ -999,7 +1020,7 @@ int noise_external(Runtime* rt, uint64_t id, const PrometheusNoiseRefiner0Execut
     fill_evidence(b, b->last_detail, ev);
     return PROM_ERROR;
   }
-  const int32_t d = run_block(rt, b, b->x, b->out, 0);
+  const int32_t d = run_block(rt, b, b->x, b->out);
   if (d != 0) {
     mark_failure(b, d);
     fill_evidence(b, d, ev);
@@ -1071,7 +1092,7 @@ int noise_resident(Runtime* rt, uint64_t id, const PrometheusNoiseRefinerResiden
     return PROM_ERROR;
   }
   const int stop = fam == PROM_NOISE_REFINER_AUDIT_M1B ? 1 : (fam == PROM_NOISE_REFINER_AUDIT_M1C ? 2 : 0);
-  const int32_t d = run_block(rt, b, b->x, b->out, stop);
+  const int32_t d = run_block(rt, b, b->x, b->out, 1, stop == 0 ? 3 : stop);
   if (d != 0) {
     mark_failure(b, d);
     fill_evidence(b, d, ev);
@@ -1185,7 +1206,7 @@ int context_execute(Runtime* rt, uint64_t id, uint32_t required_set, const float
     fill_evidence(b, b->last_detail, ev);
     return PROM_ERROR;
   }
-  const int32_t d = run_block(rt, b, b->x, b->out, 0);
+  const int32_t d = run_block(rt, b, b->x, b->out);
   if (d != 0) {
     mark_failure(b, d);
     fill_evidence(b, d, ev);
@@ -1255,6 +1276,593 @@ bool retarget_uploads_match(const ModelBlock* b, const PrometheusModelBlockWeigh
       return false;
   }
   return true;
+}
+
+
+// ---------------------------------------------------------------- main attention route
+
+// The MainTransformer attention route (reactor_sgemm.cpp:1479-1516).  The
+// subgroup-owned route is defined on 32-lane subgroups; a CDNA wavefront has
+// 64 lanes, so this library admits the serial-canonical route (its shader 41)
+// only: AUTO falls back to it with reason SUBGROUP_SIZE and an explicit
+// SUBGROUP_OWNED32 request is not admitted.
+struct RouteDecision {
+  bool admitted;
+  uint32_t selected, fallback, shader;
+};
+constexpr uint32_t kShaderMainAttentionSerial = 41u;
+
+RouteDecision decide_main_route(uint32_t requested) {
+  if (requested == PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL)
+    return {true, PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL, PROM_MAIN_ATTENTION_FALLBACK_NONE,
+            kShaderMainAttentionSerial};
+  if (requested == PROM_MAIN_ATTENTION_ROUTE_SUBGROUP_OWNED32)
+    return {false, 0u, PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SIZE, 0u};
+  return {true, PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL, PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SIZE,
+          kShaderMainAttentionSerial};
+}
+
+void reset_main_route(ModelSession* s) {
+  s->selected_route = PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL;
+  s->route_fallback = PROM_MAIN_ATTENTION_FALLBACK_NONE;
+  s->route_shader = kShaderMainAttentionSerial;
+}
+
+// ---------------------------------------------------------------- stage-split NoiseRefiner
+
+bool stage_split_block(const ModelBlock* b) {
+  return b->shader_id == kShaderNoise && b->program == kProgNoise && b->binding_valid;
+}
+
+// The 64-float attention witness of the workspace's last phase 2 into device
+// memory `dst` (stream-ordered).
+hipError_t enqueue_witness(ModelBlock* b, bool image_format, float* dst) {
+  auto W = [&](int k) { return reinterpret_cast<const float*>(b->ws + b->ws_off[k]); };
+  return launch_zimage_attention_witness(W(kZQ), W(kZKt), W(kZV), W(kZO), b->tokens, kHeads,
+                                         1.0f / sqrtf((float)(kWidth / kHeads)), image_format, dst, ctx().stream);
+}
+
+// reactor_vulkan_model_block.c:1955-2057: BF16 ingress and the pre-attention
+// phase; the workspace keeps Q, K, V, the gates and the residual input for M1C.
+int m1b_execute(Runtime* rt, uint64_t id, const PrometheusModelBlockM1BExecuteRequest* r,
+                PrometheusModelBlockEvidence* ev) {
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->model_input_bf16 == nullptr || r->timestep_bf16 == nullptr ||
+      r->input_identity == 0 || r->timestep_identity == 0 || r->audit_enabled > 1u ||
+      (r->audit_enabled == 0 && r->audit_stage != PROM_MODEL_BLOCK_M1B_AUDIT_NONE) ||
+      (r->audit_enabled != 0 && (r->audit_stage < PROM_MODEL_BLOCK_M1B_AUDIT_INGRESS_INPUT ||
+                                 r->audit_stage > PROM_MODEL_BLOCK_M1B_AUDIT_POSITIONED_K))) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  auto fail = [&](int32_t d) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  };
+  if (r->model_input_bytes != (uint64_t)kImageTokens * kWidth * 2)
+    return fail(PROM_MODEL_BLOCK_DETAIL_INGRESS_INPUT_SIZE_MISMATCH);
+  if (r->timestep_bytes != kZImageConditionWidth * 2) return fail(PROM_MODEL_BLOCK_DETAIL_INGRESS_TIMESTEP_SIZE_MISMATCH);
+  if (!stage_split_block(b)) return fail(PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+  if (!reap(b)) return fail(PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN);
+  const uint64_t audit_n =
+      r->audit_enabled ? audit_elements(PROM_NOISE_REFINER_AUDIT_M1B, r->audit_stage, kImageTokens) : 0;
+  if (r->audit_enabled != 0 &&
+      (r->audit_output == nullptr || r->audit_element_capacity < audit_n || audit_n * 4 > b->declared_audit))
+    return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  b->output_valid = false;
+  b->audit_valid = false;
+  b->resident_input_generation = 0;  // the ingress buffer is also the resident boundary
+  const uint64_t t0 = wall_ns();
+  hipStream_t st = ctx().stream;
+  if (hipMemcpyAsync(b->x_bf16, r->model_input_bf16, (size_t)r->model_input_bytes, hipMemcpyHostToDevice, st) !=
+          hipSuccess ||
+      hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st) !=
+          hipSuccess ||
+      launch_widen_bf16(b->x_bf16, b->x, (size_t)kImageTokens * kWidth, st) != hipSuccess ||
+      launch_widen_bf16(b->cond_bf16, b->cond, kZImageConditionWidth, st) != hipSuccess) {
+    (void)hipStreamSynchronize(st);
+    return fail(PROM_MODEL_BLOCK_DETAIL_INGRESS_DISPATCH_FAILED);
+  }
+  const int32_t d = run_block(rt, b, b->x, b->out, 1, 1);
+  if (d != 0) return fail(d);
+  if ((rt->test_flags & PROM_TESTCFG_FAIL_DOWNLOAD) != 0u) return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  if (r->audit_enabled != 0) {
+    if (!copy_stage(b, PROM_NOISE_REFINER_AUDIT_M1B, r->audit_stage, r->audit_output))
+      return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+    b->audit_valid = true;
+  }
+  b->output_valid = true;
+  b->executions += 1;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(hash_u64(hash_u64(hash_u64(b->plan_identity, r->input_identity), r->timestep_identity),
+                                         r->audit_enabled),
+                                r->audit_stage);
+  b->m1b_prefix = b->replay_identity;
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// reactor_vulkan_model_block.c:2059-2130: attention, projection and gated
+// residual of the matching M1B prefix; one stage to the host with the witness.
+int m1c_execute(Runtime* rt, uint64_t id, const PrometheusModelBlockM1CExecuteRequest* r,
+                PrometheusModelBlockEvidence* ev) {
+  const uint64_t model_n = (uint64_t)kImageTokens * kWidth;
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->output == nullptr || r->output_identity == 0 ||
+      r->m1b_prefix_replay_identity == 0 || r->output_element_capacity < model_n ||
+      r->audit_stage < PROM_MODEL_BLOCK_M1C_AUDIT_ATTENTION || r->audit_stage > PROM_MODEL_BLOCK_M1C_AUDIT_RESIDUAL) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  auto fail = [&](int32_t d) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  };
+  if (!stage_split_block(b) || b->m1b_prefix != r->m1b_prefix_replay_identity || b->declared_audit < model_n * 4)
+    return fail(PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+  if (!reap(b)) return fail(PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN);
+  b->output_valid = false;
+  b->audit_valid = false;
+  b->resident_input_generation = 0;
+  const uint64_t t0 = wall_ns();
+  const int32_t d = run_block(rt, b, b->x, b->out, 2, 2);
+  if (d != 0) return fail(d);
+  if ((rt->test_flags & PROM_TESTCFG_FAIL_DOWNLOAD) != 0u) return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  float witness[kTransientAuditFloats];
+  float* dev_witness = reinterpret_cast<float*>(b->audit_dev + kAuditWitnessOffset);
+  if (enqueue_witness(b, true, dev_witness) != hipSuccess ||
+      !copy_out(witness, dev_witness, 1, kTransientAuditFloats, kTransientAuditFloats))
+    return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  // both selected softmax denominators must be finite and positive
+  if (witness[30] != 1.0f || witness[62] != 1.0f) return fail(PROM_MODEL_BLOCK_DETAIL_M1C_SOFTMAX_INVALID);
+  if (r->transient_audit != nullptr && r->transient_audit_element_capacity >= kTransientAuditFloats)
+    memcpy(r->transient_audit, witness, sizeof(witness));
+  if (!copy_stage(b, PROM_NOISE_REFINER_AUDIT_M1C, r->audit_stage, r->output))
+    return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  b->output_valid = true;
+  b->executions += 1;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(hash_u64(b->m1b_prefix, r->output_identity), r->audit_stage);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// reactor_vulkan_model_block.c:2132-2199: the FFN and final residual of the
+// matching M1C; one stage to the host (the final output stays resident).
+int m1d_execute(Runtime* rt, uint64_t id, const PrometheusModelBlockM1DExecuteRequest* r,
+                PrometheusModelBlockEvidence* ev) {
+  const bool hidden = r != nullptr && (r->audit_stage == PROM_MODEL_BLOCK_M1D_AUDIT_W1 ||
+                                       r->audit_stage == PROM_MODEL_BLOCK_M1D_AUDIT_W3 ||
+                                       r->audit_stage == PROM_MODEL_BLOCK_M1D_AUDIT_GATED_HIDDEN);
+  const uint64_t required = (uint64_t)kImageTokens * (hidden ? kFfn : kWidth);
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->output == nullptr || r->output_identity == 0 ||
+      r->m1c_prefix_replay_identity == 0 || r->output_element_capacity < required ||
+      r->audit_stage < PROM_MODEL_BLOCK_M1D_AUDIT_FFN_NORM || r->audit_stage > PROM_MODEL_BLOCK_M1D_AUDIT_FINAL_OUTPUT) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  auto fail = [&](int32_t d) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  };
+  if (!stage_split_block(b) || b->replay_identity != r->m1c_prefix_replay_identity ||
+      b->declared_audit < required * 4)
+    return fail(PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+  if (!reap(b)) return fail(PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN);
+  b->output_valid = false;
+  b->audit_valid = false;
+  const uint64_t t0 = wall_ns();
+  const int32_t d = run_block(rt, b, b->x, b->out, 3, 3);
+  if (d != 0) return fail(d);
+  if ((rt->test_flags & PROM_TESTCFG_FAIL_DOWNLOAD) != 0u ||
+      !copy_stage(b, PROM_NOISE_REFINER_AUDIT_M1D, r->audit_stage, r->output))
+    return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  b->output_valid = true;
+  b->audit_valid = true;
+  b->executions += 1;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(hash_u64(r->m1c_prefix_replay_identity, r->output_identity), r->audit_stage);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// ---------------------------------------------------------------- static audits
+
+// Sources of the lock's audit schedules in this library's workspace.  The
+// first six recomputed ones are stages the chain does not keep: the norms
+// before modulation and the head norms with and without RoPE.
+enum AuditSource : uint8_t {
+  kAsAttnNorm, kAsQNorm, kAsKNorm, kAsQRope, kAsKRope, kAsFfnNorm,
+  kAsInput, kAsModRaw, kAsMod, kAsA, kAsQkv, kAsQ, kAsK, kAsV, kAsO, kAsProj, kAsR, kAsF, kAsW1, kAsW3, kAsGated,
+  kAsW2, kAsOut
+};
+bool recomputed(uint8_t s) { return s <= kAsFfnNorm; }
+
+// Projection keys of a stage, by the shape of its view (N = T * 3840, NH =
+// T * 10240): a row view takes {0, N-1, N/2, 3839}, a head view {0, N-1, N/2,
+// 127, 128}, a rotated head view adds the pair boundary {63, 64}, the fused
+// QKV {0, 3N-1, 3N/2, N-1, N, 2N}, the FFN hidden {0, NH-1, NH/2, 10239}; the
+// NoiseRefiner schedule adds the first element of the last row (and 2N-1 to
+// the fused QKV).  These are the projection keys of the lock's generated
+// schedule (resolved_audit_schedule.h:14-30, 71-81).
+enum AuditKeys : uint8_t { kKeysNone, kKeysRow, kKeysHead, kKeysRope, kKeysFused, kKeysHidden };
+
+uint32_t audit_keys(uint8_t kind, uint32_t T, bool tail, uint32_t* k) {
+  const uint32_t D = kWidth, N = T * kWidth, NH = T * kFfn;
+  uint32_t n = 0;
+  switch (kind) {
+    case kKeysRow:
+      for (uint32_t v : {0u, N - 1, N / 2, D - 1}) k[n++] = v;
+      if (tail) k[n++] = N - D;
+      break;
+    case kKeysHead:
+    case kKeysRope:
+      for (uint32_t v : {0u, N - 1, N / 2}) k[n++] = v;
+      if (kind == kKeysRope) k[n++] = 63u, k[n++] = 64u;
+      k[n++] = 127u;
+      k[n++] = 128u;
+      if (tail) k[n++] = N - D;
+      break;
+    case kKeysFused:
+      for (uint32_t v : {0u, 3 * N - 1, 3 * N / 2, N - 1, N}) k[n++] = v;
+      if (tail) k[n++] = 2 * N - 1;
+      k[n++] = 2 * N;
+      break;
+    case kKeysHidden:
+      for (uint32_t v : {0u, NH - 1, NH / 2, (uint32_t)kFfn - 1}) k[n++] = v;
+      if (tail) k[n++] = NH - kFfn;
+      break;
+    default:
+      break;
+  }
+  return n;
+}
+
+// One stage of a schedule: a full copy of `count` elements of the source from
+// `base`, or a 256-byte summary record, at byte `dest` of the arena.
+struct AuditStage {
+  uint8_t stage, source, keys;
+  uint32_t dest;
+  bool full;
+  uint32_t base, count;
+};
+
+// resolved_audit_schedule.h:20-50 (NoiseRefiner, witness at 189440; the
+// schedule's resource of each stage in the comment).
+const AuditStage kNoiseAudit[29] = {
+    {1, kAsModRaw, kKeysNone, 0, true, 0, 4 * kWidth},            // ADALN: timestep_linear
+    {2, kAsModRaw, kKeysNone, 61440, true, 0, kWidth},            // ADALN: attention_scale_raw
+    {3, kAsMod, kKeysNone, 76800, true, 0, kWidth},               // ATTENTION_SCALE
+    {4, kAsModRaw, kKeysNone, 92160, true, kWidth, kWidth},       // ADALN: attention_gate_raw
+    {5, kAsMod, kKeysNone, 107520, true, kWidth, kWidth},         // ATTENTION_GATE (tanh)
+    {6, kAsModRaw, kKeysNone, 122880, true, 2 * kWidth, kWidth},  // ADALN: mlp_scale_raw
+    {7, kAsMod, kKeysNone, 138240, true, 2 * kWidth, kWidth},     // MLP_SCALE
+    {8, kAsModRaw, kKeysNone, 153600, true, 3 * kWidth, kWidth},  // ADALN: mlp_gate_raw
+    {9, kAsMod, kKeysNone, 168960, true, 3 * kWidth, kWidth},     // MLP_GATE (tanh)
+    {10, kAsAttnNorm, kKeysRow, 184320, false, 0, 0},             // NORM: attention_norm
+    {11, kAsA, kKeysRow, 184576, false, 0, 0},                    // MODULATED
+    {12, kAsQkv, kKeysFused, 184832, false, 0, 0},                // QKV
+    {13, kAsQ, kKeysHead, 185088, false, 0, 0},                   // QKV: q
+    {14, kAsK, kKeysHead, 185344, false, 0, 0},                   // QKV: k
+    {15, kAsV, kKeysHead, 185600, false, 0, 0},                   // QKV: v
+    {16, kAsQNorm, kKeysHead, 185856, false, 0, 0},               // NORM: q_norm
+    {17, kAsKNorm, kKeysHead, 186112, false, 0, 0},               // NORM: k_norm
+    {18, kAsQRope, kKeysRope, 186368, false, 0, 0},               // QKV: q_rope
+    {19, kAsKRope, kKeysRope, 186624, false, 0, 0},               // QKV: k_rope
+    {20, kAsO, kKeysHead, 186880, false, 0, 0},                   // ATTENTION: aggregation
+    {21, kAsProj, kKeysRow, 187136, false, 0, 0},                 // ATTENTION_PROJECTION
+    {22, kAsR, kKeysRow, 187392, false, 0, 0},                    // ATTENTION_RESIDUAL
+    {23, kAsFfnNorm, kKeysRow, 187648, false, 0, 0},              // NORM: ffn_norm
+    {24, kAsF, kKeysRow, 187904, false, 0, 0},                    // MODULATED: ffn_modulated
+    {25, kAsW1, kKeysHidden, 188160, false, 0, 0},                // w1
+    {26, kAsW3, kKeysHidden, 188416, false, 0, 0},                // w3
+    {27, kAsGated, kKeysHidden, 188672, false, 0, 0},             // ffn_gated_hidden
+    {28, kAsW2, kKeysRow, 188928, false, 0, 0},                   // w2
+    {29, kAsOut, kKeysRow, 189184, false, 0, 0}};                 // final_output
+
+// resolved_audit_schedule.h:84-101 (ContextRefiner, witness at 4096; with no
+// adaLN its ffn_norm stage is the FFN input).
+const AuditStage kContextAudit[16] = {
+    {1, kAsInput, kKeysRow, 0, false, 0, 0},        {2, kAsAttnNorm, kKeysRow, 256, false, 0, 0},
+    {3, kAsQkv, kKeysFused, 512, false, 0, 0},      {4, kAsQNorm, kKeysHead, 768, false, 0, 0},
+    {5, kAsKNorm, kKeysHead, 1024, false, 0, 0},    {6, kAsQRope, kKeysRope, 1280, false, 0, 0},
+    {7, kAsKRope, kKeysRope, 1536, false, 0, 0},    {8, kAsO, kKeysHead, 1792, false, 0, 0},
+    {9, kAsProj, kKeysRow, 2048, false, 0, 0},      {10, kAsR, kKeysRow, 2304, false, 0, 0},
+    {11, kAsF, kKeysRow, 2560, false, 0, 0},        {12, kAsW1, kKeysHidden, 2816, false, 0, 0},
+    {13, kAsW3, kKeysHidden, 3072, false, 0, 0},    {14, kAsGated, kKeysHidden, 3328, false, 0, 0},
+    {15, kAsW2, kKeysRow, 3584, false, 0, 0},       {16, kAsOut, kKeysRow, 3840, false, 0, 0}};
+
+struct AuditView {
+  const float* src;
+  uint32_t count, cols, ld;  // v[e] = src[(e / cols) * ld + e % cols]
+};
+
+AuditView view_of(const ModelBlock* b, uint8_t source, const float* scratch) {
+  const uint32_t T = (uint32_t)b->tokens, D = kWidth, F = kFfn;
+  auto W = [&](int k) { return reinterpret_cast<const float*>(b->ws + b->ws_off[k]); };
+  switch (source) {
+    case kAsInput: return {b->x, T * D, D, D};
+    case kAsModRaw: return {W(kZModRaw), 4 * D, 4 * D, 4 * D};
+    case kAsMod: return {W(kZMod), 4 * D, 4 * D, 4 * D};
+    case kAsA: return {W(kZA), T * D, D, D};
+    case kAsQkv: return {W(kZQkv), 3 * T * D, 3 * D, 3 * D};
+    case kAsQ: case kAsK: case kAsV: return {W(kZQkv) + (source - kAsQ) * D, T * D, D, 3 * D};
+    case kAsO: return {W(kZO), T * D, D, D};
+    case kAsProj: return {W(kZProj), T * D, D, D};
+    case kAsR: return {W(kZR), T * D, D, D};
+    case kAsF: return {W(kZF), T * D, D, D};
+    case kAsW1: return {W(kZG), T * F, F, 2 * F};
+    case kAsW3: return {W(kZG) + F, T * F, F, 2 * F};
+    case kAsGated: return {W(kZH), T * F, F, F};
+    case kAsW2: return {W(kZW2), T * D, D, D};
+    case kAsOut: return {b->out, T * D, D, D};
+    default: return {scratch, T * D, D, D};  // recomputed into the scratch
+  }
+}
+
+hipError_t recompute(ModelBlock* b, uint8_t source, float* scratch) {
+  hipStream_t st = ctx().stream;
+  const ZImageBlockWeights w = weights_of(b);
+  const float* qkv = reinterpret_cast<const float*>(b->ws + b->ws_off[kZQkv]);
+  const float* R = reinterpret_cast<const float*>(b->ws + b->ws_off[kZR]);
+  const float2* tab = reinterpret_cast<const float2*>(b->ws + b->ws_off[kZRope]);
+  const int T = b->tokens;
+  switch (source) {
+    case kAsAttnNorm: return launch_zimage_norm(b->x, w.attn_norm1, scratch, T, kWidth, kEps, st);
+    case kAsFfnNorm: return launch_zimage_norm(R, w.ffn_norm1, scratch, T, kWidth, kEps, st);
+    case kAsQNorm: return launch_zimage_qk_audit(qkv, tab, w.q_norm, scratch, T, kHeads, kEps, 0, false, st);
+    case kAsKNorm: return launch_zimage_qk_audit(qkv, tab, w.k_norm, scratch, T, kHeads, kEps, 1, false, st);
+    case kAsQRope: return launch_zimage_qk_audit(qkv, tab, w.q_norm, scratch, T, kHeads, kEps, 0, true, st);
+    case kAsKRope: return launch_zimage_qk_audit(qkv, tab, w.k_norm, scratch, T, kHeads, kEps, 1, true, st);
+    default: return hipSuccess;
+  }
+}
+
+// Fills the device records of one schedule from the completed chain: the full
+// copies, one summary launch over the stages the workspace keeps, then each
+// recomputed stage (recompute into the scratch, summarise), and the attention
+// witness at byte `witness_offset`.  Stream-ordered.
+bool record_schedule(ModelBlock* b, const AuditStage* sched, uint32_t n, bool tail, uint32_t generation,
+                     uint32_t witness_offset, bool image_format) {
+  hipStream_t st = ctx().stream;
+  char* dev = b->audit_dev;
+  float* scratch = reinterpret_cast<float*>(dev + kAuditScratchOffset);
+  ZImageAuditJob* djobs = reinterpret_cast<ZImageAuditJob*>(dev + kAuditJobOffset);
+  ZImageAuditJob jobs[kAuditMaxJobs];
+  uint8_t later_source[kAuditMaxJobs];
+  memset(jobs, 0, sizeof(jobs));
+  uint32_t live = 0, later = 0;  // live jobs fill the table from the front, recomputed ones from the back
+  if (hipMemsetAsync(dev, 0, kAuditRecordBytes, st) != hipSuccess) return false;
+  for (uint32_t i = 0; i < n; ++i) {
+    const AuditStage& a = sched[i];
+    const AuditView v = view_of(b, a.source, scratch);
+    if (a.full) {
+      if (a.base + a.count > v.count ||
+          hipMemcpyAsync(dev + a.dest, v.src + a.base, (size_t)a.count * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return false;
+      continue;
+    }
+    if (live + later >= kAuditMaxJobs || a.dest + 256u > kAuditRecordBytes) return false;
+    const uint32_t slot = recomputed(a.source) ? kAuditMaxJobs - 1 - later : live;
+    ZImageAuditJob& j = jobs[slot];
+    j.src = v.src;
+    j.count = v.count;
+    j.cols = v.cols;
+    j.ld = v.ld;
+    j.stage_id = a.stage;
+    j.generation = generation;
+    j.dest_word = a.dest / 4;
+    j.key_count = audit_keys(a.keys, (uint32_t)b->tokens, tail, j.keys);
+    if (recomputed(a.source)) later_source[later++] = a.source;
+    else ++live;
+  }
+  // the table is read by the launches below; the copy completes before the host array goes away
+  if (hipMemcpyAsync(djobs, jobs, sizeof(jobs), hipMemcpyHostToDevice, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess ||
+      launch_zimage_audit_summary(djobs, live, reinterpret_cast<uint32_t*>(dev), st) != hipSuccess)
+    return false;
+  for (uint32_t r = 0; r < later; ++r) {
+    if (recompute(b, later_source[r], scratch) != hipSuccess ||
+        launch_zimage_audit_summary(djobs + (kAuditMaxJobs - 1 - r), 1, reinterpret_cast<uint32_t*>(dev), st) !=
+            hipSuccess)
+      return false;
+  }
+  return enqueue_witness(b, image_format, reinterpret_cast<float*>(dev + witness_offset)) == hipSuccess;
+}
+
+// Copies `bytes` of device memory into the caller's arena after zeroing its
+// bytes [bytes, clear_to).
+bool arena_out(void* arena, uint64_t clear_to, const void* src, uint64_t bytes) {
+  if (clear_to > bytes) memset(static_cast<char*>(arena) + bytes, 0, (size_t)(clear_to - bytes));
+  return hipMemcpyAsync(arena, src, (size_t)bytes, hipMemcpyDeviceToHost, ctx().stream) == hipSuccess &&
+         hipStreamSynchronize(ctx().stream) == hipSuccess;
+}
+
+// reactor_vulkan_model_block.c:3212-3272: one resident NoiseRefiner 1
+// execution (first-resident rules as execute_resident) with the arena.
+int noise_static_audit(Runtime* rt, uint64_t id, const PrometheusNoiseRefinerStaticAuditRequest* r,
+                       PrometheusModelBlockEvidence* ev) {
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->lock_identity != PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID ||
+      r->input_generation == 0 || r->output_identity == 0 || r->audit_arena == nullptr ||
+      r->audit_arena_capacity_bytes < PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  auto fail = [&](int32_t d) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  };
+  const bool first = b->resident_input_generation == 0;
+  if (b->program != kProgNoise || b->family != PROM_NOISE_REFINER_FAMILY_Z_IMAGE_TURBO ||
+      b->parameter_set != PROM_NOISE_REFINER_PARAMETER_SET_1 || binding_state(b) != PROM_NOISE_REFINER_BINDING_BOUND ||
+      (first ? r->input_generation != b->output_generation : r->input_generation != b->resident_input_generation) ||
+      !reap(b) || b->declared_audit != PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES)
+    return fail(PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+  const uint32_t generation = (uint32_t)(b->output_generation + 1u);
+  if (generation == 0u) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  b->output_valid = false;
+  b->audit_valid = false;
+  const uint64_t t0 = wall_ns();
+  hipStream_t st = ctx().stream;
+  if (first && hipMemcpyAsync(b->x, b->out, (size_t)kImageTokens * kWidth * 4, hipMemcpyDeviceToDevice, st) !=
+                   hipSuccess)
+    return fail(PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED);
+  const int32_t d = run_block(rt, b, b->x, b->out);
+  if (d != 0) return fail(d);
+  if (!record_schedule(b, kNoiseAudit, 29, true, generation, PROM_ZIMAGE_TURBO_AUDIT_TRANSIENT_ATTENTION_OFFSET,
+                       true) ||
+      !arena_out(r->audit_arena, PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES, b->audit_dev,
+                 PROM_ZIMAGE_TURBO_AUDIT_REQUIRED_BYTES))
+    return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  if (first) b->resident_input_generation = r->input_generation;
+  b->output_valid = true;
+  b->audit_valid = true;
+  b->output_generation = generation;
+  b->executions += 1;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(hash_u64(PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID, r->output_identity), generation);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// reactor_vulkan_model_block.c:2671-2735: parameter set 0 re-runs the
+// external input, set 1 the resident boundary, with the ContextRefiner arena.
+int context_static_audit(Runtime* rt, uint64_t id, const PrometheusContextRefinerStaticAuditRequest* r,
+                         PrometheusModelBlockEvidence* ev) {
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->lock_identity != PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID ||
+      r->input_generation == 0 || r->output_identity == 0 || r->audit_arena == nullptr ||
+      r->audit_arena_capacity_bytes < PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_ARENA_BYTES) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  auto fail = [&](int32_t d) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  };
+  const bool set1 = b->parameter_set == PROM_CONTEXT_REFINER_PARAMETER_SET_1;
+  const bool first = set1 && b->resident_input_generation == 0;
+  if (b->program != kProgContext || binding_state(b) != PROM_NOISE_REFINER_BINDING_BOUND ||
+      (!set1 && r->input_generation != b->output_generation) ||
+      (set1 && (first ? r->input_generation != b->output_generation
+                      : r->input_generation != b->resident_input_generation)) ||
+      !reap(b))
+    return fail(PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+  const uint32_t generation = (uint32_t)(b->output_generation + 1u);
+  if (generation == 0u) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  b->output_valid = false;
+  b->audit_valid = false;
+  const uint64_t t0 = wall_ns();
+  hipStream_t st = ctx().stream;
+  if (first && hipMemcpyAsync(b->x, b->out, (size_t)kContextTokens * kWidth * 4, hipMemcpyDeviceToDevice, st) !=
+                   hipSuccess)
+    return fail(PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED);
+  const int32_t d = run_block(rt, b, b->x, b->out);
+  if (d != 0) return fail(d);
+  if (!record_schedule(b, kContextAudit, 16, false, generation,
+                       PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_TRANSIENT_ATTENTION_OFFSET, false) ||
+      !arena_out(r->audit_arena, r->audit_arena_capacity_bytes, b->audit_dev,
+                 PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_REQUIRED_BYTES))
+    return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  b->output_valid = true;
+  b->audit_valid = true;
+  if (first) b->resident_input_generation = r->input_generation;
+  b->output_generation = generation;
+  b->executions += 1;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(b->replay_identity, r->output_identity);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
+}
+
+// reactor_vulkan_model_block.c:4020-4131: MainTransformer layer 0 re-run on
+// the session's JointWorking stream with the timestep it last took; the
+// session is not advanced and the arena receives the [1056, 3840] output.
+int main_static_audit(Runtime* rt, uint64_t id, const PrometheusMainTransformerStaticAuditRequest* r,
+                      PrometheusModelBlockEvidence* ev) {
+  const uint64_t out_bytes = (uint64_t)kJointTokens * kWidth * 4;
+  if (r == nullptr || r->struct_size != sizeof(*r) || r->lock_identity != PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID ||
+      r->model_local_block_id != 0u || r->session_identity == 0 || r->required_image_generation == 0 ||
+      r->required_context_generation == 0 || r->required_joint_generation == 0 || r->output_identity == 0 ||
+      r->audit_arena == nullptr || r->audit_arena_capacity_bytes < out_bytes) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, ev);
+    return PROM_ERROR;
+  }
+  ModelBlock* b = find_block(rt, id);
+  if (b == nullptr) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_NOT_FOUND, ev);
+    return PROM_ERROR;
+  }
+  if (!reap(b)) {
+    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN, ev);
+    return PROM_ERROR;
+  }
+  auto fail = [&](int32_t d) {
+    mark_failure(b, d);
+    fill_evidence(b, d, ev);
+    return PROM_ERROR;
+  };
+  const ModelSession* s = &rt->model->session;
+  if (b->program != kProgMain || b->parameter_set != 1u || b->aggregate != kMainAggregate[0] ||
+      binding_state(b) != PROM_NOISE_REFINER_BINDING_BOUND || !s->created || s->id != r->session_identity ||
+      s->lock != r->lock_identity || !joint_valid(s) || s->streams[0].generation != r->required_image_generation ||
+      s->streams[1].generation != r->required_context_generation ||
+      s->streams[2].generation != r->required_joint_generation)
+    return fail(PROM_MODEL_BLOCK_DETAIL_STALE_OUTPUT);
+  b->output_valid = false;
+  b->audit_valid = false;
+  const uint64_t t0 = wall_ns();
+  const int32_t d = run_block(rt, b, s->buf[2], b->out);
+  if (d != 0) return fail(d);
+  if (!arena_out(r->audit_arena, r->audit_arena_capacity_bytes, b->out, out_bytes))
+    return fail(PROM_MODEL_BLOCK_DETAIL_AUDIT_FAILED);
+  b->output_valid = true;
+  b->audit_valid = true;
+  b->output_generation += 1;
+  b->executions += 1;
+  b->last_execution_ns = wall_ns() - t0;
+  b->replay_identity = hash_u64(b->replay_identity, r->output_identity);
+  b->last_detail = 0;
+  fill_evidence(b, 0, ev);
+  return PROM_OK;
 }
 
 }  // namespace
@@ -1414,6 +2022,27 @@ PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute(void* handle
   });
 }
 
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute_m1b(
+    void* handle, uint64_t block_id, const PrometheusModelBlockM1BExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return m1b_execute(rt, block_id, request, out_evidence); });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute_m1c(
+    void* handle, uint64_t block_id, const PrometheusModelBlockM1CExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return m1c_execute(rt, block_id, request, out_evidence); });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute_m1d(
+    void* handle, uint64_t block_id, const PrometheusModelBlockM1DExecuteRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return m1d_execute(rt, block_id, request, out_evidence); });
+}
+
 PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner0_execute(
     void* handle, uint64_t block_id, const PrometheusNoiseRefiner0ExecuteRequest* request,
     PrometheusModelBlockEvidence* out_evidence) {
@@ -1461,6 +2090,13 @@ PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_execute_resident(
     PrometheusModelBlockEvidence* out_evidence) {
   return with_runtime(handle, out_evidence,
                       [&](Runtime* rt) -> int { return noise_resident(rt, block_id, request, out_evidence); });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_execute_static_audit(
+    void* handle, uint64_t block_id, const PrometheusNoiseRefinerStaticAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return noise_static_audit(rt, block_id, request, out_evidence); });
 }
 
 PROM_REACTOR_API int prometheus_reactor_runtime_noise_refiner_audit_final(
@@ -1538,6 +2174,13 @@ PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_execute_resident
   });
 }
 
+PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_execute_static_audit(
+    void* handle, uint64_t block_id, const PrometheusContextRefinerStaticAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return context_static_audit(rt, block_id, request, out_evidence); });
+}
+
 PROM_REACTOR_API int prometheus_reactor_runtime_context_refiner_audit_final(
     void* handle, uint64_t block_id, const PrometheusContextRefinerFinalAuditRequest* request,
     PrometheusModelBlockEvidence* out_evidence) {
@@ -1561,6 +2204,15 @@ PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_create(
       fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED, out_evidence);
       return PROM_ERROR;
     }
+    ModelSession* s = &rt->model->session;
+    const RouteDecision route = decide_main_route(s->requested_route);
+    if (!route.admitted) {  // reactor_vulkan_model_block.c:2419-2430
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    s->selected_route = route.selected;
+    s->route_fallback = route.fallback;
+    s->route_shader = route.shader;
     return facade_create(rt, r, out_block_id, out_evidence, true);
   });
 }
@@ -1642,7 +2294,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute(
     hipError_t e = hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) e = launch_widen_bf16(b->cond_bf16, b->cond, kZImageConditionWidth, st);
     b->last_memcpy_ns = wall_ns() - t0;
-    int32_t d = e == hipSuccess ? run_block(rt, b, s->buf[2], b->out, 0) : PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
+    int32_t d = e == hipSuccess ? run_block(rt, b, s->buf[2], b->out) : PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
     if (d == 0 && chain &&
         (hipMemcpyAsync(s->buf[2], b->out, (size_t)kStreamBytes[2], hipMemcpyDeviceToDevice, st) != hipSuccess ||
          hipStreamSynchronize(st) != hipSuccess))
@@ -1678,6 +2330,13 @@ PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute(
     fill_evidence(b, 0, out_evidence);
     return PROM_OK;
   });
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute_static_audit(
+    void* handle, uint64_t block_id, const PrometheusMainTransformerStaticAuditRequest* request,
+    PrometheusModelBlockEvidence* out_evidence) {
+  return with_runtime(handle, out_evidence,
+                      [&](Runtime* rt) -> int { return main_static_audit(rt, block_id, request, out_evidence); });
 }
 
 PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_audit_final(
@@ -1747,6 +2406,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_create(
     s->lock = r->lock_identity;
     s->requested_profile = r->execution_profile;
     s->requested_route = r->main_attention_route_policy;
+    reset_main_route(s);  // the MainTransformer create decides the route
     s->id = ms->next_session_id++;
     s->created = true;
     *out_session_id = s->id;
@@ -1868,6 +2528,27 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_get_evide
   });
 }
 
+// reactor_vulkan_model_block.c:4229-4251
+PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_set_main_attention_route(
+    void* handle, uint64_t session_id, uint32_t main_attention_route_policy,
+    PrometheusCompiledModelSessionEvidence* out_evidence) {
+  if (out_evidence == nullptr || main_attention_route_policy < PROM_MAIN_ATTENTION_ROUTE_AUTO ||
+      main_attention_route_policy > PROM_MAIN_ATTENTION_ROUTE_SUBGROUP_OWNED32 || lookup(handle) == nullptr)
+    return PROM_ERROR;
+  return with_session_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
+    ModelSession* s = find_session(rt, session_id);
+    if (s == nullptr || rt->model->block.created) {  // the route is fixed once a block exists
+      fill_session_evidence(rt->model ? &rt->model->session : nullptr, out_evidence,
+                            PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
+      return PROM_ERROR;
+    }
+    s->requested_route = main_attention_route_policy;
+    reset_main_route(s);
+    fill_session_evidence(s, out_evidence, 0);
+    return PROM_OK;
+  });
+}
+
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_destroy(void* handle, uint64_t session_id) {
   return with_session_runtime(handle, nullptr, [&](Runtime* rt) -> int {
     ModelSession* s = find_session(rt, session_id);
@@ -1895,6 +2576,15 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_owner_create(
     // A weight prefetch needs a transfer queue of its own; this library runs
     // every copy on the runtime stream, so PREFETCH falls back (reason 1).
     s->profile_fallback = s->requested_profile == PROM_MODEL_EXECUTION_PROFILE_PREFETCH ? 1u : 0u;
+    const RouteDecision route = decide_main_route(s->requested_route);  // reactor_vulkan_model_block.c:4381-4408
+    s->selected_route = route.selected;
+    s->route_fallback = route.fallback;
+    s->route_shader = route.shader;
+    if (!route.admitted) {
+      s->last_detail = PROM_MODEL_SESSION_DETAIL_MAIN_ATTENTION_ROUTE_REJECTED;
+      fill_evidence(nullptr, PROM_MODEL_SESSION_DETAIL_MAIN_ATTENTION_ROUTE_REJECTED, out_evidence);
+      return PROM_ERROR;
+    }
     PrometheusModelBlockCreateRequest c;
     memset(&c, 0, sizeof(c));
     c.struct_size = sizeof(c);

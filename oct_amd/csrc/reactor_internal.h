@@ -160,15 +160,44 @@ hipError_t launch_widen_bf16(const uint16_t* src, float* dst, size_t n, hipStrea
 hipError_t launch_zimage_rope_table(const float* coords, float2* tab, int T, hipStream_t stream);
 // One block: out = block(x); cond [256] is read only when w.adaln_w is set;
 // the workspace rope table must already hold this sequence's coordinates.
-// stop_after 1 ends after the Q/K/V split (pre-attention), 2 after the
-// attention residual and FFN input; 0 runs the whole block.
+// The block runs in three phases, first_phase..last_phase of: 1 adaLN to the
+// Q/K/V split (pre-attention), 2 attention to the gated residual and FFN
+// input, 3 the FFN and final residual.  A later phase reads the workspace the
+// earlier ones left, so 2..2 re-runs the attention of the last phase 1.
 hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x, const float* cond, float* out,
                                     char* ws, const size_t off[kZCount], int T, int D, int F, float eps,
-                                    hipStream_t st, uint32_t* launches, int stop_after);
+                                    hipStream_t st, uint32_t* launches, int first_phase, int last_phase);
 // Audit recomputations: out = RMSNorm(x; w) (no modulation), and q or k
 // (which 0 / 1) after the head RMSNorm and optionally RoPE, [T, H*128].
 hipError_t launch_zimage_norm(const float* x, const float* w, float* out, int T, int D, float eps, hipStream_t stream);
 hipError_t launch_zimage_qk_audit(const float* qkv, const float2* tab, const float* norm_w, float* out, int T, int H,
                                   float eps, int which, bool rope, hipStream_t stream);
+
+// One 256-byte (64-word) audit summary record of the fp32 view
+// v[e] = src[(e / cols) * ld + e % cols], 0 <= e < count: words 0 stage,
+// 1 generation, 2 count, 3 all-finite flag, 4 NaN count, 5 infinity count,
+// 6 finite count, 7 key count, 8 min, 9 max, 10 sum of squares, 11 RMS (finite
+// values; quiet NaN when none), 12 completion (1), 13 status (1 if a key is out
+// of range), 16 + 2i / 17 + 2i (key i, v[key i]); other words zero
+// (shaders/sdslv/production/zimage/nr0_persistent_audit_summary.sdslv:56-217).
+struct ZImageAuditJob {
+  const float* src;
+  uint32_t count, cols, ld, stage_id;
+  uint32_t generation, dest_word, key_count, reserved;
+  uint32_t keys[16];
+};
+constexpr uint32_t kZImageAuditMaxKeys = 15u;
+// One workgroup per job; jobs and arena are device memory.
+hipError_t launch_zimage_audit_summary(const ZImageAuditJob* jobs, uint32_t job_count, uint32_t* arena,
+                                       hipStream_t stream);
+// The 64-float streaming-attention witness of (token 0, head 0) at out[0..31]
+// and (token T-1, head H-1) at out[32..63] from the split Q (scaled by
+// q_scale) [H, T, 128], K^T [H, 128, T], V [H, T, 128] and the attention
+// output O [T, H*128].  image_format selects the NoiseRefiner record
+// (nr0_attention_streaming.sdslv:24-116) over the ContextRefiner one
+// (context_refiner_attention_streaming.sdslv:44-73).  T <= kZImageWitnessMaxTokens.
+constexpr int kZImageWitnessMaxTokens = 1056;
+hipError_t launch_zimage_attention_witness(const float* Q, const float* Kt, const float* V, const float* O, int T,
+                                           int H, float q_scale, bool image_format, float* out, hipStream_t stream);
 
 }  // namespace prom

@@ -184,6 +184,149 @@ __global__ __launch_bounds__(256) void swiglu_f32_kernel(const float* __restrict
   }
 }
 
+// One audit summary record per workgroup.  Lane l reduces the elements
+// l, l + 256, ... in increasing order; the lanes then combine in a fixed
+// binary tree (strides 128 .. 1), the reference's order.
+__global__ __launch_bounds__(256) void audit_summary_kernel(const ZImageAuditJob* __restrict__ jobs,
+                                                            uint32_t* __restrict__ arena) {
+  __shared__ float ss[256], lo[256], hi[256];
+  __shared__ uint32_t nfin[256], nnan[256], ninf[256];
+  const ZImageAuditJob& j = jobs[blockIdx.x];
+  const uint32_t lane = threadIdx.x;
+  const float* src = j.src;
+  const uint32_t count = j.count, cols = j.cols, ld = j.ld;
+  float sum = 0.0f, mn = __uint_as_float(0x7f800000u), mx = __uint_as_float(0xff800000u);
+  uint32_t nf = 0, nn = 0, ni = 0;
+#pragma unroll 4
+  for (uint32_t e = lane; e < count; e += 256u) {
+    const uint32_t r = e / cols;
+    const float v = src[(size_t)r * ld + (e - r * cols)];
+    if (v != v) {
+      ++nn;
+    } else if (v - v != 0.0f) {
+      ++ni;
+    } else {
+      ++nf;
+      sum += v * v;
+      mn = v < mn ? v : mn;
+      mx = v > mx ? v : mx;
+    }
+  }
+  ss[lane] = sum;
+  lo[lane] = mn;
+  hi[lane] = mx;
+  nfin[lane] = nf;
+  nnan[lane] = nn;
+  ninf[lane] = ni;
+  __syncthreads();
+  for (uint32_t stride = 128u; stride > 0u; stride >>= 1) {
+    if (lane < stride) {
+      const uint32_t o = lane + stride;
+      ss[lane] = ss[lane] + ss[o];
+      nfin[lane] += nfin[o];
+      nnan[lane] += nnan[o];
+      ninf[lane] += ninf[o];
+      if (lo[o] < lo[lane]) lo[lane] = lo[o];
+      if (hi[o] > hi[lane]) hi[lane] = hi[o];
+    }
+    __syncthreads();
+  }
+  if (lane != 0) return;
+  const uint32_t qnan = 0x7fc00000u;
+  uint32_t* rec = arena + j.dest_word;
+  for (int i = 0; i < 64; ++i) rec[i] = 0u;
+  const uint32_t finite = nfin[0];
+  rec[0] = j.stage_id;
+  rec[1] = j.generation;
+  rec[2] = count;
+  rec[3] = finite == count ? 1u : 0u;
+  rec[4] = nnan[0];
+  rec[5] = ninf[0];
+  rec[6] = finite;
+  rec[7] = j.key_count;
+  rec[8] = finite ? __float_as_uint(lo[0]) : qnan;
+  rec[9] = finite ? __float_as_uint(hi[0]) : qnan;
+  rec[10] = __float_as_uint(ss[0]);
+  rec[11] = finite ? __float_as_uint(sqrtf(ss[0] / (float)finite)) : qnan;
+  rec[12] = 1u;
+  for (uint32_t k = 0; k < j.key_count && k < kZImageAuditMaxKeys; ++k) {
+    const uint32_t e = j.keys[k];
+    rec[16 + 2 * k] = e;
+    if (e < count) {
+      const uint32_t r = e / cols;
+      rec[17 + 2 * k] = __float_as_uint(src[(size_t)r * ld + (e - r * cols)]);
+    } else {
+      rec[17 + 2 * k] = qnan;
+      rec[13] = 1u;
+    }
+  }
+}
+
+// The streaming-attention witness: workgroup 0 takes (token 0, head 0),
+// workgroup 1 (token T-1, head H-1).  The scores come from the split Q and
+// K^T (Q carries the 1/sqrt(128) scale, so s is the scaled score); lane 0
+// then makes the reference's serial passes over the keys: the maximum, the
+// exponentials and their sum, the normalisation and the row sum.
+__global__ __launch_bounds__(256) void attention_witness_kernel(const float* __restrict__ Q,
+                                                                const float* __restrict__ Kt,
+                                                                const float* __restrict__ V,
+                                                                const float* __restrict__ O, int T, int H,
+                                                                float q_scale, int image_format,
+                                                                float* __restrict__ out) {
+  __shared__ float s[kZImageWitnessMaxTokens], p[kZImageWitnessMaxTokens];
+  const int row = (int)blockIdx.x;
+  const int t = row ? T - 1 : 0, h = row ? H - 1 : 0;
+  const float* q = Q + ((size_t)h * T + t) * kHead;
+  const float* kt = Kt + (size_t)h * kHead * T;
+  for (int k = (int)threadIdx.x; k < T; k += 256) {
+    float d = 0.0f;
+    for (int c = 0; c < kHead; ++c) d += q[c] * kt[(size_t)c * T + k];
+    s[k] = d;
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  float w[32] = {};
+  float mx = s[0];
+  for (int k = 1; k < T; ++k) mx = s[k] > mx ? s[k] : mx;
+  float sum = 0.0f;
+  for (int k = 0; k < T; ++k) {
+    p[k] = expf(s[k] - mx);
+    sum += p[k];
+  }
+  const bool valid = sum == sum && sum > 0.0f && sum - sum == 0.0f;
+  const int keys[4] = {0, 1, T / 2, T - 1};
+  if (image_format) {
+    for (int i = 0; i < 4; ++i) {
+      const int k = keys[i];
+      w[5 * i] = s[k] / q_scale;
+      w[5 * i + 1] = s[k];
+      w[5 * i + 2] = s[k] - mx;
+      w[5 * i + 3] = p[k];
+    }
+    w[20] = mx;
+    w[21] = sum;
+  }
+  float row_sum = 0.0f;
+  for (int k = 0; k < T; ++k) {
+    p[k] = valid ? p[k] / sum : 0.0f;
+    row_sum += p[k];
+  }
+  if (image_format) {
+    for (int i = 0; i < 4; ++i) w[5 * i + 4] = p[keys[i]];
+    w[22] = row_sum;
+    w[23] = p[0] * V[(size_t)h * T * kHead];
+    w[24] = O[(size_t)t * H * kHead + (size_t)h * kHead];
+  } else {
+    w[0] = s[0] / q_scale;
+    w[1] = s[0];
+    w[2] = s[0] - mx;
+    w[3] = p[0];
+    w[4] = row_sum;
+  }
+  w[30] = valid ? 1.0f : 0.0f;
+  for (int i = 0; i < 32; ++i) out[32 * row + i] = w[i];
+}
+
 inline unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>(65536, (n + 255) / 256); }
 
 }  // namespace
@@ -247,9 +390,24 @@ hipError_t launch_zimage_qk_audit(const float* qkv, const float2* tab, const flo
   return hipGetLastError();
 }
 
+hipError_t launch_zimage_audit_summary(const ZImageAuditJob* jobs, uint32_t job_count, uint32_t* arena,
+                                       hipStream_t stream) {
+  if (job_count == 0) return hipSuccess;
+  hipLaunchKernelGGL(audit_summary_kernel, dim3(job_count), dim3(256), 0, stream, jobs, arena);
+  return hipGetLastError();
+}
+
+hipError_t launch_zimage_attention_witness(const float* Q, const float* Kt, const float* V, const float* O, int T,
+                                           int H, float q_scale, bool image_format, float* out, hipStream_t stream) {
+  if (T < 1 || T > kZImageWitnessMaxTokens || H < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attention_witness_kernel, dim3(2), dim3(256), 0, stream, Q, Kt, V, O, T, H, q_scale,
+                     image_format ? 1 : 0, out);
+  return hipGetLastError();
+}
+
 hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x, const float* cond, float* out,
                                     char* ws, const size_t off[kZCount], int T, int D, int F, float eps,
-                                    hipStream_t st, uint32_t* launches, int stop_after) {
+                                    hipStream_t st, uint32_t* launches, int first_phase, int last_phase) {
   const int H = D / kHead;
   float* raw = reinterpret_cast<float*>(ws + off[kZModRaw]);
   float* mod = reinterpret_cast<float*>(ws + off[kZMod]);
@@ -281,40 +439,40 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
     ++n;                           \
   } while (0)
   const dim3 row_grid((T + 3) / 4), blk(256);
-  if (modulated) {
-    hipLaunchKernelGGL(adaln_f32_kernel, dim3((4 * D + 63) / 64), blk, 0, st, cond, w.adaln_w, w.adaln_b, raw, mod,
-                       kZImageConditionWidth, D);
+  if (first_phase > last_phase || first_phase < 1 || last_phase > 3) return hipErrorInvalidValue;
+  if (launches) *launches = 0;
+  if (first_phase == 1) {  // adaLN, attention norm, QKV, head norms and RoPE
+    if (modulated) {
+      hipLaunchKernelGGL(adaln_f32_kernel, dim3((4 * D + 63) / 64), blk, 0, st, cond, w.adaln_w, w.adaln_b, raw, mod,
+                         kZImageConditionWidth, D);
+      PROM_STEP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(rows::norm_mod_kernel<float>, row_grid, blk, 0, st, x, w.attn_norm1, scaleA, A, T, D, eps);
+    PROM_STEP(hipGetLastError());
+    PROM_STEP(launch_sgemm_f32_ex(A, D, w.w_qkv, 3 * D, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
+    hipLaunchKernelGGL(qkv_split_kernel, dim3((T + kSplitTokens - 1) / kSplitTokens, H), blk, 0, st, qkv, rope,
+                       w.q_norm, w.k_norm, Q, Kt, V, T, H, eps, 1.0f / sqrtf((float)kHead));
     PROM_STEP(hipGetLastError());
   }
-  hipLaunchKernelGGL(rows::norm_mod_kernel<float>, row_grid, blk, 0, st, x, w.attn_norm1, scaleA, A, T, D, eps);
-  PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_sgemm_f32_ex(A, D, w.w_qkv, 3 * D, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(qkv_split_kernel, dim3((T + kSplitTokens - 1) / kSplitTokens, H), blk, 0, st, qkv, rope, w.q_norm,
-                     w.k_norm, Q, Kt, V, T, H, eps, 1.0f / sqrtf((float)kHead));
-  PROM_STEP(hipGetLastError());
-  if (stop_after == 1) {
-    if (launches) *launches = n;
-    return hipSuccess;
+  if (first_phase <= 2 && last_phase >= 2) {  // attention, projection, gated residual, FFN norm
+    PROM_STEP(launch_sgemm_f32_batched(Q, kHead, (long long)T * kHead, Kt, T, (long long)kHead * T, S, T,
+                                       (long long)T * T, T, T, kHead, H, st));
+    PROM_STEP(launch_row_reduction(S, S, (uint32_t)(H * T), (uint32_t)T, 3u, st));
+    PROM_STEP(launch_sgemm_f32_batched(S, T, (long long)T * T, V, kHead, (long long)T * kHead, O, D, kHead, T, kHead,
+                                       T, H, st));
+    PROM_STEP(launch_sgemm_f32_ex(O, D, w.w_out, D, proj, D, T, D, D, nullptr, 0, st, nullptr));
+    hipLaunchKernelGGL(rows::resid_norm_mod_kernel<float>, row_grid, blk, 0, st, x, proj, w.attn_norm2, gateA,
+                       w.ffn_norm1, scaleM, R, Fm, T, D, eps);
+    PROM_STEP(hipGetLastError());
   }
-  PROM_STEP(launch_sgemm_f32_batched(Q, kHead, (long long)T * kHead, Kt, T, (long long)kHead * T, S, T,
-                                     (long long)T * T, T, T, kHead, H, st));
-  PROM_STEP(launch_row_reduction(S, S, (uint32_t)(H * T), (uint32_t)T, 3u, st));
-  PROM_STEP(launch_sgemm_f32_batched(S, T, (long long)T * T, V, kHead, (long long)T * kHead, O, D, kHead, T, kHead, T,
-                                     H, st));
-  PROM_STEP(launch_sgemm_f32_ex(O, D, w.w_out, D, proj, D, T, D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(rows::resid_norm_mod_kernel<float>, row_grid, blk, 0, st, x, proj, w.attn_norm2, gateA,
-                     w.ffn_norm1, scaleM, R, Fm, T, D, eps);
-  PROM_STEP(hipGetLastError());
-  if (stop_after == 2) {
-    if (launches) *launches = n;
-    return hipSuccess;
+  if (last_phase == 3) {  // W1/W3, SwiGLU, W2, gated final residual
+    PROM_STEP(launch_sgemm_f32_ex(Fm, D, w.w_13, 2 * F, G, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
+    hipLaunchKernelGGL(swiglu_f32_kernel, dim3(grid_for((size_t)T * F)), blk, 0, st, G, Hd, T, F);
+    PROM_STEP(hipGetLastError());
+    PROM_STEP(launch_sgemm_f32_ex(Hd, F, w.w_2, D, W2, D, T, D, F, nullptr, 0, st, nullptr));
+    hipLaunchKernelGGL(rows::final_resid_kernel, row_grid, blk, 0, st, R, W2, w.ffn_norm2, gateM, out, T, D, eps);
+    PROM_STEP(hipGetLastError());
   }
-  PROM_STEP(launch_sgemm_f32_ex(Fm, D, w.w_13, 2 * F, G, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(swiglu_f32_kernel, dim3(grid_for((size_t)T * F)), blk, 0, st, G, Hd, T, F);
-  PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_sgemm_f32_ex(Hd, F, w.w_2, D, W2, D, T, D, F, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(rows::final_resid_kernel, row_grid, blk, 0, st, R, W2, w.ffn_norm2, gateM, out, T, D, eps);
-  PROM_STEP(hipGetLastError());
 #undef PROM_STEP
   if (launches) *launches = n;
   return hipSuccess;

@@ -127,11 +127,12 @@ class ResidentModel:
         return self.lib.prometheus_reactor_runtime_model_block_destroy(self.h, block_id)
 
     # -- NoiseRefiner ----------------------------------------------------------
-    def noise_refiner_create(self, weights: dict, parameter_set: int = 1, content_base: int = 0x5A00):
+    def noise_refiner_create(self, weights: dict, parameter_set: int = 1, content_base: int = 0x5A00,
+                             audit_bytes: int = 65536 * 4):
         uploads = zimage_uploads(weights, content_base)
         req = create_request(uploads, shader_id=p.PROM_MODEL_BLOCK_SHADER_NOISE, family=p.PROM_NOISE_REFINER_FAMILY,
                              parameter_set=parameter_set, aggregate=p.NOISE_REFINER_AGGREGATES[parameter_set - 1],
-                             external_input_bytes=IMAGE_TOKENS * WIDTH * 2, audit_bytes=65536 * 4,
+                             external_input_bytes=IMAGE_TOKENS * WIDTH * 2, audit_bytes=audit_bytes,
                              memory_ceiling=512 << 20)
         rc, bid, ev = self.create(req)
         if rc != p.PROM_OK:
@@ -185,6 +186,97 @@ class ResidentModel:
             r.audit_element_capacity = audit.size
         ev = p.PrometheusModelBlockEvidence()
         rc = self.lib.prometheus_reactor_runtime_noise_refiner_execute_resident(self.h, block_id, byref(r), byref(ev))
+        return rc, ev
+
+    # -- stage-split NoiseRefiner (reactor_api.h:957-1007, 2722-2730) -----------
+    def execute_m1b(self, block_id: int, model_input_bf16: np.ndarray, timestep_bf16: np.ndarray,
+                    audit_stage: int = 0, audit: Optional[np.ndarray] = None, input_identity: int = 0x51,
+                    timestep_identity: int = 0x52, request_patch=None):
+        r = p.PrometheusModelBlockM1BExecuteRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.model_input_bf16 = model_input_bf16.ctypes.data
+        r.timestep_bf16 = timestep_bf16.ctypes.data
+        r.model_input_bytes = model_input_bf16.nbytes
+        r.timestep_bytes = timestep_bf16.nbytes
+        r.input_identity = input_identity
+        r.timestep_identity = timestep_identity
+        if audit is not None:
+            r.audit_enabled = 1
+            r.audit_stage = audit_stage
+            r.audit_output = audit.ctypes.data
+            r.audit_element_capacity = audit.size
+        if request_patch:
+            request_patch(r)
+        ev = p.PrometheusModelBlockEvidence()
+        rc = self.lib.prometheus_reactor_runtime_model_block_execute_m1b(self.h, block_id, byref(r), byref(ev))
+        return rc, ev
+
+    def execute_m1c(self, block_id: int, prefix: int, out: np.ndarray, audit_stage: int = 3,
+                    transient: Optional[np.ndarray] = None, output_identity: int = 0x53, request_patch=None):
+        r = p.PrometheusModelBlockM1CExecuteRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.m1b_prefix_replay_identity = prefix
+        r.output_identity = output_identity
+        r.output = out.ctypes.data
+        r.output_element_capacity = out.size
+        r.audit_stage = audit_stage
+        if transient is not None:
+            r.transient_audit = transient.ctypes.data
+            r.transient_audit_element_capacity = transient.size
+        if request_patch:
+            request_patch(r)
+        ev = p.PrometheusModelBlockEvidence()
+        rc = self.lib.prometheus_reactor_runtime_model_block_execute_m1c(self.h, block_id, byref(r), byref(ev))
+        return rc, ev
+
+    def execute_m1d(self, block_id: int, prefix: int, out: np.ndarray, audit_stage: int = 7,
+                    output_identity: int = 0x54, request_patch=None):
+        r = p.PrometheusModelBlockM1DExecuteRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.m1c_prefix_replay_identity = prefix
+        r.output_identity = output_identity
+        r.output = out.ctypes.data
+        r.output_element_capacity = out.size
+        r.audit_stage = audit_stage
+        if request_patch:
+            request_patch(r)
+        ev = p.PrometheusModelBlockEvidence()
+        rc = self.lib.prometheus_reactor_runtime_model_block_execute_m1d(self.h, block_id, byref(r), byref(ev))
+        return rc, ev
+
+    # -- static audits (reactor_api.h:1070-1093, 2743-2778) ----------------------
+    def static_audit(self, kind: str, block_id: int, input_generation: int, arena: np.ndarray,
+                     output_identity: int = 0x57, lock: int = p.PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID):
+        """``kind`` "noise" or "context"; ``arena`` a uint8 array of the arena capacity."""
+        r = p.PrometheusNoiseRefinerStaticAuditRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.lock_identity = lock
+        r.input_generation = input_generation
+        r.output_identity = output_identity
+        r.audit_arena = arena.ctypes.data
+        r.audit_arena_capacity_bytes = arena.nbytes
+        ev = p.PrometheusModelBlockEvidence()
+        fn = {"noise": self.lib.prometheus_reactor_runtime_noise_refiner_execute_static_audit,
+              "context": self.lib.prometheus_reactor_runtime_context_refiner_execute_static_audit}[kind]
+        rc = fn(self.h, block_id, byref(r), byref(ev))
+        return rc, ev
+
+    def main_static_audit(self, block_id: int, session_id: int, image_gen: int, context_gen: int, joint_gen: int,
+                          arena: np.ndarray, output_identity: int = 0x58, layer: int = 0):
+        r = p.PrometheusMainTransformerStaticAuditRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.session_identity = session_id
+        r.lock_identity = p.PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID
+        r.model_local_block_id = layer
+        r.required_image_generation = image_gen
+        r.required_context_generation = context_gen
+        r.required_joint_generation = joint_gen
+        r.output_identity = output_identity
+        r.audit_arena = arena.ctypes.data
+        r.audit_arena_capacity_bytes = arena.nbytes
+        ev = p.PrometheusModelBlockEvidence()
+        rc = self.lib.prometheus_reactor_runtime_main_transformer_execute_static_audit(self.h, block_id, byref(r),
+                                                                                       byref(ev))
         return rc, ev
 
     def audit_final(self, kind: str, block_id: int, generation: int, out: np.ndarray, output_identity: int = 0xA0D1):
@@ -317,6 +409,12 @@ class ResidentModel:
     def session_evidence(self, session_id: int):
         ev = p.PrometheusCompiledModelSessionEvidence()
         rc = self.lib.prometheus_reactor_runtime_compiled_model_session_get_evidence(self.h, session_id, byref(ev))
+        return rc, ev
+
+    def set_main_attention_route(self, session_id: int, route: int, evidence: bool = True):
+        ev = p.PrometheusCompiledModelSessionEvidence()
+        rc = self.lib.prometheus_reactor_runtime_compiled_model_session_set_main_attention_route(
+            self.h, session_id, route, byref(ev) if evidence else None)
         return rc, ev
 
     def session_destroy(self, session_id: int) -> int:

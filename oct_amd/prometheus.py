@@ -6,7 +6,7 @@ check / create / probe (``bridge.go:276-394``), ``nativeRuntime.SGEMM``
 (``bridge.go:410-436``), status mapping (``status.go``, ``bridge.go:535-550``)
 and the strict ``@`` path that never substitutes the CPU
 (``strict.go:11-32``).  The Go toolchain is absent from this image, so the
-host side is Python; ``INTEGRATION.md`` shows the cgo binding a maintainer adds.
+host side is Python, over the same exported symbols a cgo binding resolves.
 
 Everything here calls the HIP library.  There is no CPU fallback: a missing
 library or device raises :class:`ReactorIssue`.
@@ -529,6 +529,17 @@ PROM_MODEL_BLOCK_MAX_WEIGHTS = 13
 PROM_MODEL_BLOCK_MAX_STEPS = 7
 PROM_ZIMAGE_TURBO_LOCK_ID = 0x71EF202B4E34B562
 PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES = 47186176
+# the lock's static-audit arenas (resolved_audit_schedule.h:5-11, 67-71)
+PROM_ZIMAGE_TURBO_AUDIT_LOCK_ID = PROM_ZIMAGE_TURBO_LOCK_ID
+PROM_ZIMAGE_TURBO_AUDIT_REQUIRED_BYTES = 189696
+PROM_ZIMAGE_TURBO_AUDIT_TRANSIENT_ATTENTION_OFFSET = 189440
+PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_ARENA_BYTES = 1048576
+PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_REQUIRED_BYTES = 4352
+PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_TRANSIENT_ATTENTION_OFFSET = 4096
+PROM_MODEL_BLOCK_M1C_TRANSIENT_AUDIT_FLOATS = 64
+# main attention routes and fallback reasons (reactor_api.h:37-53)
+PROM_MAIN_ATTENTION_ROUTE_AUTO, PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL, PROM_MAIN_ATTENTION_ROUTE_SUBGROUP_OWNED32 = 1, 2, 3
+PROM_MAIN_ATTENTION_FALLBACK_NONE, PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SIZE = 0, 3
 PROM_NOISE_REFINER_FAMILY = 1
 PROM_CONTEXT_REFINER_FAMILY = 2
 PROM_MAIN_TRANSFORMER_FAMILY = 3
@@ -541,7 +552,8 @@ PROM_MODEL_BLOCK_DETAIL = {
     "COMMAND_RECORD_FAILED": -6908, "QUEUE_SUBMIT_FAILED": -6909, "COMPLETION_UNCERTAIN": -6910,
     "AUDIT_FAILED": -6911, "STALE_OUTPUT": -6912, "PARAMETER_SET_MISMATCH": -6920, "REBIND_FAILED": -6921,
     "SESSION_INVALID_REQUEST": -6923, "SESSION_STALE_STREAM": -6924, "SESSION_STREAM_MISMATCH": -6925,
-    "SESSION_COMPLETION_UNCERTAIN": -6926,
+    "SESSION_COMPLETION_UNCERTAIN": -6926, "INGRESS_DISPATCH_FAILED": -6914, "INGRESS_INPUT_SIZE_MISMATCH": -6916,
+    "INGRESS_TIMESTEP_SIZE_MISMATCH": -6917, "M1C_SOFTMAX_INVALID": -6918, "MAIN_ATTENTION_ROUTE_REJECTED": -6927,
 }
 PROM_REDUCTION_TESTCFG_FAIL_COMMAND_RECORD = 1 << 0
 PROM_REDUCTION_TESTCFG_FAIL_QUEUE_SUBMIT = 1 << 1
@@ -610,6 +622,40 @@ class PrometheusContextRefinerResidentExecuteRequest(Structure):
 class PrometheusNoiseRefinerFinalAuditRequest(Structure):
     _fields_ = _fields("u32 struct_size, u64 required_output_generation, u64 output_identity, p output, "
                        "u64 output_element_capacity")
+
+
+class PrometheusModelBlockM1BExecuteRequest(Structure):
+    """reactor_api.h:961-973"""
+    _fields_ = _fields("u32 struct_size, p model_input_bf16, p timestep_bf16, u64 model_input_bytes, "
+                       "u64 timestep_bytes, u64 input_identity, u64 timestep_identity, u32 audit_enabled, "
+                       "u32 audit_stage, p audit_output, u64 audit_element_capacity")
+
+
+class PrometheusModelBlockM1CExecuteRequest(Structure):
+    """reactor_api.h:978-987"""
+    _fields_ = _fields("u32 struct_size, u64 m1b_prefix_replay_identity, u64 output_identity, p output, "
+                       "u64 output_element_capacity, u32 audit_stage, p transient_audit, "
+                       "u64 transient_audit_element_capacity")
+
+
+class PrometheusModelBlockM1DExecuteRequest(Structure):
+    """reactor_api.h:1000-1007"""
+    _fields_ = _fields("u32 struct_size, u64 m1c_prefix_replay_identity, u64 output_identity, p output, "
+                       "u64 output_element_capacity, u32 audit_stage")
+
+
+class PrometheusNoiseRefinerStaticAuditRequest(Structure):
+    """reactor_api.h:1070-1081 (also the ContextRefiner request)"""
+    _fields_ = _fields("u32 struct_size, u64 lock_identity, u64 input_generation, u64 output_identity, "
+                       "p audit_arena, u64 audit_arena_capacity_bytes")
+
+
+class PrometheusMainTransformerStaticAuditRequest(Structure):
+    """reactor_api.h:1082-1093"""
+    _fields_ = _fields("u32 struct_size, u64 session_identity, u64 lock_identity, u32 model_local_block_id, "
+                       "u64 required_image_generation, u64 required_context_generation, "
+                       "u64 required_joint_generation, u64 output_identity, p audit_arena, "
+                       "u64 audit_arena_capacity_bytes")
 
 
 class PrometheusModelBlockEvidence(Structure):
@@ -802,6 +848,26 @@ _SIGNATURES = {
     "prometheus_reactor_runtime_model_block_execute": (
         c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockExecuteRequest),
                 POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_model_block_execute_m1b": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockM1BExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_model_block_execute_m1c": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockM1CExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_model_block_execute_m1d": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusModelBlockM1DExecuteRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_noise_refiner_execute_static_audit": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefinerStaticAuditRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_context_refiner_execute_static_audit": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefinerStaticAuditRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_main_transformer_execute_static_audit": (
+        c_int, [c_void_p, c_uint64, POINTER(PrometheusMainTransformerStaticAuditRequest),
+                POINTER(PrometheusModelBlockEvidence)]),
+    "prometheus_reactor_runtime_compiled_model_session_set_main_attention_route": (
+        c_int, [c_void_p, c_uint64, c_uint32, POINTER(PrometheusCompiledModelSessionEvidence)]),
     "prometheus_reactor_runtime_noise_refiner0_execute": (
         c_int, [c_void_p, c_uint64, POINTER(PrometheusNoiseRefiner0ExecuteRequest),
                 POINTER(PrometheusModelBlockEvidence)]),

@@ -21,7 +21,7 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
 
 
 def gelu_tanh(x: np.ndarray) -> np.ndarray:
-    """Tanh-approximate GELU (Gemma's GeGLU activation; no reference implementation)."""
+    """Tanh-approximate GELU (Gemma's GeGLU activation; the reference has no implementation of it)."""
     return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
 
 
@@ -318,7 +318,9 @@ def zimage_block_f64(x, coords, w: dict, cond=None, heads: int = 30, eps: float 
         scale_m, gate_m = 1.0 + raw[2 * D:3 * D], np.tanh(raw[3 * D:])
     else:
         scale_a = gate_a = scale_m = gate_m = np.ones(D)
-    a = rmsnorm(x, f("attn_norm1"), eps) * scale_a
+    normed = rmsnorm(x, f("attn_norm1"), eps)
+    keep["attention_norm"] = normed[sel]
+    a = normed * scale_a
     keep["attention_modulated"] = a[sel]
     w_qkv = f("w_qkv")
     qkv = a @ w_qkv
@@ -334,6 +336,9 @@ def zimage_block_f64(x, coords, w: dict, cond=None, heads: int = 30, eps: float 
     k = rope_canonical_f32(k, coords)
     keep["q_rope"] = q.reshape(len(sel), D)
     keep["k_rope"] = k[sel].reshape(len(sel), D)
+    if stages is not None:  # every token's rotated key and value, for attention witnesses
+        keep["k_rope_all"] = k.reshape(T, D)
+        keep["v_all"] = v.reshape(T, D)
     o = np.empty((len(sel), heads, hd))
     for h in range(heads):
         s = (q[:, h, :] @ k[:, h, :].T) / np.sqrt(hd)

@@ -96,6 +96,12 @@ STRUCTS = {
     "PrometheusCompiledModelSessionEvidence": p.PrometheusCompiledModelSessionEvidence,
     "PrometheusCompiledModelRetargetRequest": p.PrometheusCompiledModelRetargetRequest,
     "PrometheusCompiledModelPrefetchRequest": p.PrometheusCompiledModelRetargetRequest,
+    "PrometheusModelBlockM1BExecuteRequest": p.PrometheusModelBlockM1BExecuteRequest,
+    "PrometheusModelBlockM1CExecuteRequest": p.PrometheusModelBlockM1CExecuteRequest,
+    "PrometheusModelBlockM1DExecuteRequest": p.PrometheusModelBlockM1DExecuteRequest,
+    "PrometheusNoiseRefinerStaticAuditRequest": p.PrometheusNoiseRefinerStaticAuditRequest,
+    "PrometheusContextRefinerStaticAuditRequest": p.PrometheusNoiseRefinerStaticAuditRequest,
+    "PrometheusMainTransformerStaticAuditRequest": p.PrometheusMainTransformerStaticAuditRequest,
 }
 MODEL_BLOCK_STRUCTS = tuple(n for n in STRUCTS if "ModelBlock" in n or "Refiner" in n or "MainTransformer" in n
                             or "CompiledModel" in n)

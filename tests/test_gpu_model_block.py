@@ -11,6 +11,9 @@ accepted FP32 bound for a block against its canonical stage, relative L2
 FP16 weights and BF16 inputs at the lock's shapes (1024 image, 32 context,
 1056 joint tokens; width 3840, 30 heads, FFN 10240).
 """
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -336,13 +339,31 @@ def test_session_main_transformer_chain(model, weights, inputs):
     err = rel_l2(out[ROWS_JOINT], ref)
     print(f"main transformer 0 rel L2 {err:.3e}", flush=True)
     assert err <= BAR
+    # the route the create decided: AUTO falls back to serial-canonical on 64-lane wavefronts
+    sev = model.session_evidence(sid)[1]
+    assert sev.requested_main_attention_route == p.PROM_MAIN_ATTENTION_ROUTE_AUTO
+    assert sev.selected_main_attention_route == p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL
+    assert sev.main_attention_fallback_reason == p.PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SIZE
+    assert sev.main_attention_shader_id == 41
+    assert model.set_main_attention_route(sid, p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL)[0] == p.PROM_ERROR
+    # the static audit re-runs layer 0 on the same JointWorking stream and the
+    # timestep it last took; the arena holds that output, the rest is zeroed
+    out_bytes = T_JOINT * W * 4
+    arena = np.full(out_bytes + 4096, 0xCD, np.uint8)
+    rc, ev = model.main_static_audit(mid, sid, 1, 1, 2, arena)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]
+    rc, ev = model.main_static_audit(mid, sid, 1, 1, 1, arena)
+    assert rc == p.PROM_OK and ev.output_generation == 2 and ev.audit_valid == 1 and ev.output_valid == 1
+    np.testing.assert_array_equal(arena[:out_bytes].view(np.float32).reshape(T_JOINT, W), out)
+    assert not arena[out_bytes:].any()
+    assert model.session_evidence(sid)[1].joint_generation == 1
     # chain mode writes the output back into JointWorking (generation 2)
     rc, ev = model.main_transformer_execute(mid, sid, 0, t_bits, 1, 1, 1, chain=True)
-    assert rc == p.PROM_OK and ev.output_generation == 2
+    assert rc == p.PROM_OK and ev.output_generation == 3
     sev = model.session_evidence(sid)[1]
     assert sev.joint_generation == 2 and sev.active_block_id == mid
     chained = np.zeros(T_JOINT * W, np.float32)
-    assert model.audit_final("main", mid, 2, chained)[0] == p.PROM_OK
+    assert model.audit_final("main", mid, 3, chained)[0] == p.PROM_OK
     np.testing.assert_array_equal(chained.reshape(T_JOINT, W), out)
     rc, ev = model.main_transformer_execute(mid, sid, 0, t_bits, 1, 1, 1, chain=True)
     assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]  # joint generation moved on
@@ -443,5 +464,285 @@ def test_compiled_owner_drives_the_bridge_sequence(model, weights, inputs):
     again = np.zeros(T_IMG * W, np.float32)
     assert model.audit_final("noise", oid, ev.output_generation, again)[0] == p.PROM_OK
     np.testing.assert_array_equal(again, first_nr0)
+    assert model.destroy(oid) == p.PROM_OK
+    assert model.session_destroy(sid) == p.PROM_OK
+
+
+# ------------------------------------------------------------ stage-split NoiseRefiner (M1B, M1C, M1D)
+ROWS_SPLIT = np.array([0, 1, 31, 32, 341, 512, 682, 1000, 1023])
+ARENA = p.PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES
+SCHEDULE = json.loads((Path(__file__).resolve().parent / "golden" / "zimage_audit_schedule.json").read_text())
+
+
+def close(got, ref, tol):
+    return abs(float(got) - float(ref)) <= tol * max(1.0, abs(float(ref)))
+
+
+def logits(q_rope, k_rope_all, t_index, h, hd=128):
+    """Scaled scores and probabilities of one (token, head) row in binary64."""
+    s = np.asarray(k_rope_all, np.float64)[:, h * hd:(h + 1) * hd] @ np.asarray(q_rope, np.float64)[
+        t_index, h * hd:(h + 1) * hd] / np.sqrt(hd)
+    e = np.exp(s - s.max())
+    return s, e / e.sum()
+
+
+def check_image_witness(w, q_rope, k_rope_all, v_all, aggregation, t_rows):
+    """The NoiseRefiner witness (nr0_attention_streaming.sdslv:24-116): per
+    selected row, keys 0, 1, 512, 1023 as (raw, scaled, shifted, exp,
+    probability), then max, sum, row sum, p0 * v0 and the head output."""
+    T = 1024
+    for base, (t, h) in ((0, (0, 0)), (32, (T - 1, 29))):
+        ti = int(np.where(t_rows == t)[0][0])
+        s, prob = logits(q_rope, k_rope_all, ti, h)
+        assert w[base + 30] == 1.0 and abs(w[base + 22] - 1.0) <= 2e-5, base
+        assert close(w[base + 20], s.max(), 1e-4)
+        for i, key in enumerate((0, 1, T // 2, T - 1)):
+            assert close(w[base + 5 * i + 1], s[key], 1e-4), (base, key)
+            assert close(w[base + 5 * i], s[key] * np.sqrt(128.0), 1e-4), (base, key)
+            assert close(w[base + 5 * i + 2], s[key] - s.max(), 1e-4), (base, key)
+            assert abs(w[base + 5 * i + 4] - prob[key]) <= 2e-6, (base, key)
+            assert close(w[base + 5 * i + 3], prob[key] * w[base + 21], 1e-4), (base, key)
+        assert close(w[base + 23], prob[0] * float(v_all[0, h * 128]), 1e-4)
+        assert close(w[base + 24], aggregation[ti, h * 128], 1e-4)
+
+
+def test_stage_split_noise_refiner(model, weights, inputs):
+    """M1B -> M1C -> M1D on the resident workspace (reactor_vulkan_model_block.c:
+    1955-2199) against the binary64 block, the witness against the same
+    oracle, and the split chain against the whole block bit for bit."""
+    x_bits, t_bits, _ = inputs
+    x = oracle.from_bf16(x_bits).astype(np.float64)
+    cond = oracle.from_bf16(t_bits).astype(np.float64)
+    stages = {}
+    blocks.zimage_block_f64(x, blocks.image_coordinates(T_IMG), weights["nr0"], cond, rows=ROWS_SPLIT, stages=stages)
+    out = np.zeros(T_IMG * W, np.float32)
+    # a block declaring a 256 KiB audit refuses large stage audits and M1C
+    rc, bid, ev = model.noise_refiner_create(weights["nr0"])
+    assert rc == p.PROM_OK
+    rc, ev = model.execute_m1b(bid, x_bits, t_bits, audit_stage=14, audit=np.zeros(T_IMG * 3 * W, np.float32))
+    assert rc == p.PROM_ERROR and ev.detail_code == D["AUDIT_FAILED"]
+    rc, ev = model.execute_m1b(bid, x_bits[:-1], t_bits)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["INGRESS_INPUT_SIZE_MISMATCH"]
+    rc, ev = model.execute_m1b(bid, x_bits, t_bits[:-1])
+    assert rc == p.PROM_ERROR and ev.detail_code == D["INGRESS_TIMESTEP_SIZE_MISMATCH"]
+    rc, ev = model.execute_m1b(bid, x_bits, t_bits)
+    assert rc == p.PROM_OK and ev.output_valid == 1 and ev.audit_valid == 0
+    rc, ev2 = model.execute_m1c(bid, ev.replay_identity, out)
+    assert rc == p.PROM_ERROR and ev2.detail_code == D["STALE_OUTPUT"]
+    assert model.destroy(bid) == p.PROM_OK
+
+    print("stage split: create with the lock's audit arena", flush=True)
+    rc, bid, ev = model.noise_refiner_create(weights["nr0"], audit_bytes=ARENA)
+    assert rc == p.PROM_OK
+    allocs = ev.cold_buffer_allocation_count
+    for stage, name, width in ((14, "qkv", 3 * W), (12, "attention_norm", W), (13, "attention_modulated", W),
+                               (20, "q_rope", W), (19, "k_norm", W), (3, "adaln_projection", None)):
+        buf = np.zeros(mb_audit_elements(1, stage), np.float32)
+        rc, ev = model.execute_m1b(bid, x_bits, t_bits, audit_stage=stage, audit=buf)
+        assert rc == p.PROM_OK and ev.audit_valid == 1 and ev.output_valid == 1, (stage, ev.detail_code)
+        got = buf if width is None else buf.reshape(T_IMG, width)[ROWS_SPLIT]
+        err = rel_l2(got, stages[name])
+        assert err <= BAR, (name, err)
+    rc, ev = model.execute_m1b(bid, x_bits, t_bits)
+    prefix = ev.replay_identity
+    rc, ev = model.execute_m1b(bid, x_bits, t_bits)
+    assert rc == p.PROM_OK and ev.replay_identity == prefix  # identical requests replay identically
+    rc, ev = model.execute_m1c(bid, prefix ^ 1, out)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]
+    transient = np.zeros(p.PROM_MODEL_BLOCK_M1C_TRANSIENT_AUDIT_FLOATS, np.float32)
+    for stage, name in ((1, "attention_aggregation"), (2, "attention_projection"), (3, "attention_residual")):
+        transient[:] = 0
+        rc, ev = model.execute_m1c(bid, prefix, out, audit_stage=stage, transient=transient)
+        assert rc == p.PROM_OK and ev.output_valid == 1, (stage, ev.detail_code)
+        err = rel_l2(out.reshape(T_IMG, W)[ROWS_SPLIT], stages[name])
+        print(f"M1C {name} rel L2 {err:.3e}", flush=True)
+        assert err <= BAR
+        check_image_witness(transient, stages["q_rope"], stages["k_rope_all"], stages["v_all"],
+                            stages["attention_aggregation"], ROWS_SPLIT)
+    m1c = ev.replay_identity
+    final = np.zeros(T_IMG * W, np.float32)
+    rc, ev = model.execute_m1d(bid, m1c, final, audit_stage=7)
+    assert rc == p.PROM_OK and ev.output_valid == 1 and ev.audit_valid == 1
+    err = rel_l2(final.reshape(T_IMG, W)[ROWS_SPLIT], stages["final_output"])
+    print(f"M1D final_output rel L2 {err:.3e}", flush=True)
+    assert err <= BAR
+    rc, ev = model.execute_m1d(bid, m1c, final, audit_stage=7)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]  # the chain moved on
+    rc, ev = model.execute_m1c(bid, prefix, out, audit_stage=3)
+    assert rc == p.PROM_OK and ev.replay_identity == m1c
+    hidden = np.zeros(T_IMG * 10240, np.float32)
+    rc, ev = model.execute_m1d(bid, m1c, hidden, audit_stage=5)
+    assert rc == p.PROM_OK
+    assert rel_l2(hidden.reshape(T_IMG, 10240)[ROWS_SPLIT], stages["ffn_gated_hidden"]) <= BAR
+    # the whole block on the same ingress reproduces the split chain bit for bit
+    rc, ev = model.noise_refiner_execute(bid, x_bits, t_bits)
+    assert rc == p.PROM_OK and ev.cold_buffer_allocation_count == allocs
+    whole = np.zeros(T_IMG * W, np.float32)
+    assert model.audit_final("noise", bid, ev.output_generation, whole)[0] == p.PROM_OK
+    np.testing.assert_array_equal(whole, final)
+    rc, ev = model.execute_m1c(bid, prefix, out)  # a full execution replaced the M1B state
+    assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]
+    assert model.destroy(bid) == p.PROM_OK
+
+
+# ------------------------------------------------------------ static audits
+def check_record(rec, entry, data, generation):
+    """One 256-byte summary record (nr0_persistent_audit_summary.sdslv:56-217)
+    against the fp32 stage it summarises: counts, keys and key values exact,
+    min and max exact, the sum of squares and RMS to fp32 summation accuracy."""
+    data = np.asarray(data, np.float32).ravel()
+    keys = entry["keys"]
+    fl = rec.view(np.float32)
+    assert rec[0] == entry["stage"] and rec[1] == generation and rec[2] == entry["count"] == data.size, entry["stage"]
+    assert rec[3] == 1 and rec[4] == 0 and rec[5] == 0 and rec[6] == data.size and rec[7] == len(keys)
+    assert fl[8] == data.min() and fl[9] == data.max(), entry["stage"]
+    ss = float(np.sum(np.square(data, dtype=np.float64)))
+    assert abs(fl[10] - ss) <= 2e-4 * ss, (entry["stage"], fl[10], ss)
+    assert abs(fl[11] - np.sqrt(ss / data.size)) <= 1e-4 * np.sqrt(ss / data.size)
+    assert rec[12] == 1 and rec[13] == 0 and rec[14] == 0 and rec[15] == 0
+    for i, k in enumerate(keys):
+        assert rec[16 + 2 * i] == k and fl[17 + 2 * i] == data[k], (entry["stage"], k)
+    assert not rec[16 + 2 * len(keys):].any()
+
+
+# NoiseRefiner schedule stage -> (audit family, stage) of the resident stage audits
+NOISE_AUDIT_SOURCE = {1: (1, 3), 2: (1, 4), 3: (1, 5), 4: (1, 6), 5: (1, 7), 6: (1, 8), 7: (1, 9), 8: (1, 10),
+                      9: (1, 11), 10: (1, 12), 11: (1, 13), 12: (1, 14), 13: (1, 15), 14: (1, 16), 15: (1, 17),
+                      16: (1, 18), 17: (1, 19), 18: (1, 20), 19: (1, 21), 20: (2, 1), 21: (2, 2), 22: (2, 3),
+                      23: (3, 1), 24: (3, 2), 25: (3, 3), 26: (3, 4), 27: (3, 5), 28: (3, 6), 29: (3, 7)}
+
+
+def test_noise_refiner_static_audit(model, weights, inputs):
+    """reactor_vulkan_model_block.c:3212-3272: one resident NoiseRefiner 1
+    execution fills the lock's arena; every record is checked against the
+    same stage fetched through the resident stage audits (a re-run of the
+    same boundary, bit-identical), the witness against those stages."""
+    x_bits, t_bits, _ = inputs
+    sched = SCHEDULE["noise"]
+    rc, bid, ev = model.noise_refiner_create(weights["nr0"], audit_bytes=ARENA)
+    assert rc == p.PROM_OK
+    assert model.noise_refiner_execute(bid, x_bits, t_bits)[0] == p.PROM_OK
+    arena = np.full(ARENA, 0xCD, np.uint8)
+    rc, ev = model.static_audit("noise", bid, 1, arena)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]  # parameter set 0
+    assert model.noise_refiner_rebind(bid, weights["nr1"])[0] == p.PROM_OK
+    rc, ev = model.static_audit("noise", bid, 2, arena)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]
+    print("noise refiner static audit", flush=True)
+    rc, ev = model.static_audit("noise", bid, 1, arena)
+    assert rc == p.PROM_OK and ev.output_generation == 2 and ev.audit_valid == 1 and ev.output_valid == 1
+    req = sched["required_bytes"]
+    assert not arena[req:].any()
+    words, floats = arena[:req].view(np.uint32), arena[:req].view(np.float32)
+    out = np.zeros(T_IMG * W, np.float32)  # the published output is the resident one of generation 2
+    assert model.audit_final("noise", bid, 2, out)[0] == p.PROM_OK
+    fetched = {}
+    for entry in sched["stages"]:
+        fam, stage = NOISE_AUDIT_SOURCE[entry["stage"]]
+        buf = np.zeros(mb_audit_elements(fam, stage), np.float32)
+        rc, ev = model.noise_refiner_resident(bid, 1, audit_family=fam, audit_stage=stage, audit=buf)
+        assert rc == p.PROM_OK, (entry["stage"], ev.detail_code)
+        d0 = entry["dest"] // 4
+        if entry["policy"] == 1:
+            np.testing.assert_array_equal(floats[d0:d0 + entry["count"]], buf[:entry["count"]])
+        else:
+            check_record(words[d0:d0 + 64], entry, buf, generation=2)
+        if entry["stage"] in (18, 19, 20):
+            fetched[entry["stage"]] = buf.reshape(T_IMG, W)
+        if entry["stage"] == 15:
+            fetched["v"] = buf.reshape(T_IMG, W)
+        if entry["stage"] == 29:
+            np.testing.assert_array_equal(buf, out)  # the same boundary re-run: bit-identical
+    w0 = sched["witness_offset"] // 4
+    check_image_witness(floats[w0:w0 + 64], fetched[18], fetched[19], fetched["v"], fetched[20], np.arange(T_IMG))
+    generation = model.evidence(bid)[1].output_generation
+    rc, ev = model.static_audit("noise", bid, 1, arena)  # the same boundary again
+    assert rc == p.PROM_OK and ev.output_generation == generation + 1
+    assert model.destroy(bid) == p.PROM_OK
+
+
+CONTEXT_STAGE_NAMES = {2: "attention_norm", 3: "qkv", 4: "q_norm", 5: "k_norm", 6: "q_rope", 7: "k_rope",
+                       8: "attention_aggregation", 9: "attention_projection", 10: "attention_residual",
+                       11: "ffn_modulated", 12: "w1", 13: "w3", 14: "ffn_gated_hidden", 15: "w2", 16: "final_output"}
+
+
+def test_context_refiner_static_audit(model, weights, inputs):
+    """reactor_vulkan_model_block.c:2671-2735 on parameter set 0: the arena's
+    records against the binary64 ContextRefiner (32 tokens, every row)."""
+    _, _, ctx = inputs
+    sched = SCHEDULE["context"]
+    stages = {}
+    ref = blocks.zimage_block_f64(ctx, blocks.context_coordinates(T_CTX), weights["cr0"], None, stages=stages)
+    stages["input"] = ctx
+    rc, bid, ev = model.context_refiner_create(weights["cr0"])
+    assert rc == p.PROM_OK
+    assert model.context_refiner0_execute(bid, ctx)[0] == p.PROM_OK
+    cap = p.PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_ARENA_BYTES + 512
+    arena = np.full(cap, 0xCD, np.uint8)
+    rc, ev = model.static_audit("context", bid, 2, arena)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["STALE_OUTPUT"]
+    rc, ev = model.static_audit("context", bid, 1, arena)
+    assert rc == p.PROM_OK and ev.output_generation == 2 and ev.audit_valid == 1
+    req = sched["required_bytes"]
+    assert not arena[req:].any()  # the whole capacity past the records is cleared
+    words, floats = arena[:req].view(np.uint32), arena[:req].view(np.float32)
+    for entry in sched["stages"]:
+        r = stages[CONTEXT_STAGE_NAMES.get(entry["stage"], "input")]
+        r = np.asarray(r, np.float64).ravel()
+        rec = words[entry["dest"] // 4:entry["dest"] // 4 + 64]
+        fl = rec.view(np.float32)
+        scale = np.abs(r).max()
+        assert rec[0] == entry["stage"] and rec[1] == 2 and rec[2] == entry["count"] == r.size
+        assert rec[3] == 1 and rec[6] == r.size and rec[7] == len(entry["keys"]) and rec[12] == 1 and rec[13] == 0
+        assert abs(fl[8] - r.min()) <= 1e-4 * scale and abs(fl[9] - r.max()) <= 1e-4 * scale, entry["stage"]
+        ss = float(np.sum(r * r))
+        assert abs(fl[10] - ss) <= 2e-4 * ss and abs(fl[11] - np.sqrt(ss / r.size)) <= 1e-4 * np.sqrt(ss / r.size)
+        for i, k in enumerate(entry["keys"]):
+            assert rec[16 + 2 * i] == k and abs(fl[17 + 2 * i] - r[k]) <= 1e-4 * scale, (entry["stage"], k)
+    # the witness (context_refiner_attention_streaming.sdslv:44-73): key 0 of
+    # (token 0, head 0) and (token 31, head 29)
+    w = floats[sched["witness_offset"] // 4:sched["witness_offset"] // 4 + 64]
+    for base, (t, h) in ((0, (0, 0)), (32, (T_CTX - 1, 29))):
+        s, prob = logits(stages["q_rope"], stages["k_rope_all"], t, h)
+        assert w[base + 30] == 1.0 and abs(w[base + 4] - 1.0) <= 2e-5
+        assert close(w[base + 1], s[0], 1e-4) and close(w[base], s[0] * np.sqrt(128.0), 1e-4)
+        assert close(w[base + 2], s[0] - s.max(), 1e-4) and abs(w[base + 3] - prob[0]) <= 2e-6
+    out = np.zeros(T_CTX * W, np.float32)
+    assert model.audit_final("context", bid, 2, out)[0] == p.PROM_OK
+    assert rel_l2(out.reshape(T_CTX, W), ref) <= BAR
+    assert model.destroy(bid) == p.PROM_OK
+
+
+# ------------------------------------------------------------ main attention route
+def test_main_attention_route(model, weights):
+    """reactor_sgemm.cpp:1479-1516 and reactor_vulkan_model_block.c:2419-2430,
+    4381-4408, 4229-4251 on 64-lane wavefronts."""
+    rc, sid, sev = model.session_create(route=p.PROM_MAIN_ATTENTION_ROUTE_SUBGROUP_OWNED32)
+    assert rc == p.PROM_OK
+    assert sev.selected_main_attention_route == p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL
+    assert sev.main_attention_shader_id == 41 and sev.main_attention_fallback_reason == 0
+    rc, mid, ev = model.main_transformer_create(0, weights["main0"])
+    assert rc == p.PROM_ERROR and ev.detail_code == D["RESOURCE_CREATE_FAILED"]
+    rc, oid, ev = model.owner_create(weights["nr0"])
+    assert rc == p.PROM_ERROR and ev.detail_code == D["MAIN_ATTENTION_ROUTE_REJECTED"]
+    sev = model.session_evidence(sid)[1]
+    assert sev.selected_main_attention_route == 0 and sev.main_attention_shader_id == 0
+    assert sev.main_attention_fallback_reason == p.PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SIZE
+    rc, sev = model.set_main_attention_route(sid, p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL)
+    assert rc == p.PROM_OK and sev.requested_main_attention_route == p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL
+    assert sev.selected_main_attention_route == p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL
+    rc, mid, ev = model.main_transformer_create(0, weights["main0"])
+    assert rc == p.PROM_OK, ev.detail_code
+    sev = model.session_evidence(sid)[1]
+    assert sev.main_attention_fallback_reason == 0 and sev.main_attention_shader_id == 41
+    assert model.set_main_attention_route(sid, p.PROM_MAIN_ATTENTION_ROUTE_AUTO)[0] == p.PROM_ERROR
+    assert model.destroy(mid) == p.PROM_OK
+    rc, sev = model.set_main_attention_route(sid, p.PROM_MAIN_ATTENTION_ROUTE_AUTO)
+    assert rc == p.PROM_OK
+    rc, oid, ev = model.owner_create(weights["nr0"])
+    assert rc == p.PROM_OK
+    sev = model.session_evidence(sid)[1]
+    assert sev.selected_main_attention_route == p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL
+    assert sev.main_attention_fallback_reason == p.PROM_MAIN_ATTENTION_FALLBACK_SUBGROUP_SIZE
     assert model.destroy(oid) == p.PROM_OK
     assert model.session_destroy(sid) == p.PROM_OK

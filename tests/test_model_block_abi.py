@@ -271,3 +271,91 @@ def test_owner_entries_validate_before_any_work(model):
     rc, sev = model.evaluation_reset(1)
     assert rc == p.PROM_ERROR and sev.detail_code == D["SESSION_INVALID_REQUEST"]
     assert ctypes.sizeof(p.PrometheusCompiledModelRetargetRequest) == 40
+
+
+def test_stage_split_request_checks(model):
+    """M1B/M1C/M1D argument validation (reactor_vulkan_model_block.c:1964-1980,
+    2068-2079, 2141-2158): malformed requests are INVALID_REQUEST before the
+    block lookup; well-formed ones for an unknown block are NOT_FOUND."""
+    import numpy as np
+
+    xb = np.zeros(1024 * 3840, np.uint16)
+    tb = np.zeros(256, np.uint16)
+    audit = np.zeros(4 * 3840, np.float32)
+    for stage, patch in ((0, lambda r: setattr(r, "struct_size", 8)), (0, lambda r: setattr(r, "input_identity", 0)),
+                         (0, lambda r: setattr(r, "timestep_identity", 0)),
+                         (0, lambda r: setattr(r, "model_input_bf16", None)),
+                         (0, lambda r: setattr(r, "audit_enabled", 2)),
+                         (0, lambda r: setattr(r, "audit_stage", 3)),   # a stage without auditing
+                         (22, None), (0, None)):                         # audited stage out of 1..21
+        audited = stage != 0 or patch is None
+        rc, ev = model.execute_m1b(1, xb, tb, audit_stage=stage, audit=audit if audited else None,
+                                   request_patch=patch)
+        assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"], (stage, patch)
+    rc, ev = model.execute_m1b(1, xb, tb, audit_stage=3, audit=audit)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["NOT_FOUND"]
+    # M1B sizes the ingress only after it has found the block
+    rc, ev = model.execute_m1b(1, xb[:-1], tb)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["NOT_FOUND"]
+
+    out = np.zeros(1024 * 3840, np.float32)
+    for patch in (lambda r: setattr(r, "struct_size", 8), lambda r: setattr(r, "output", None),
+                  lambda r: setattr(r, "output_identity", 0), lambda r: setattr(r, "m1b_prefix_replay_identity", 0),
+                  lambda r: setattr(r, "output_element_capacity", 1024 * 3840 - 1),
+                  lambda r: setattr(r, "audit_stage", 0), lambda r: setattr(r, "audit_stage", 4)):
+        rc, ev = model.execute_m1c(1, 0x77, out, request_patch=patch)
+        assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"]
+    rc, ev = model.execute_m1c(1, 0x77, out)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["NOT_FOUND"]
+
+    for stage, n in ((3, 1024 * 10240 - 1), (4, 1024 * 10240 - 1), (5, 1024 * 10240 - 1), (7, 1024 * 3840 - 1),
+                     (0, 1024 * 3840), (8, 1024 * 3840)):
+        rc, ev = model.execute_m1d(1, 0x78, np.zeros(n, np.float32), audit_stage=stage)
+        assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"], stage
+    for patch in (lambda r: setattr(r, "m1c_prefix_replay_identity", 0), lambda r: setattr(r, "output_identity", 0),
+                  lambda r: setattr(r, "struct_size", 8)):
+        rc, ev = model.execute_m1d(1, 0x78, out, request_patch=patch)
+        assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"]
+    rc, ev = model.execute_m1d(1, 0x78, out, audit_stage=6)
+    assert rc == p.PROM_ERROR and ev.detail_code == D["NOT_FOUND"]
+
+
+def test_static_audit_request_checks(model):
+    """Static-audit argument validation (reactor_vulkan_model_block.c:2681-2684,
+    3221-3227, 4041-4049): the lock, generations, identities and the arena
+    capacity come first; a well-formed request for an unknown block is NOT_FOUND."""
+    import numpy as np
+
+    arena = np.zeros(p.PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES, np.uint8)
+    for kind, cap in (("noise", p.PROM_ZIMAGE_TURBO_AUDIT_ARENA_BYTES),
+                      ("context", p.PROM_ZIMAGE_TURBO_CONTEXT_AUDIT_ARENA_BYTES)):
+        short = arena[:cap - 4]
+        for args in (dict(input_generation=0, arena=arena[:cap]), dict(input_generation=1, arena=short),
+                     dict(input_generation=1, arena=arena[:cap], output_identity=0),
+                     dict(input_generation=1, arena=arena[:cap], lock=0x1234)):
+            rc, ev = model.static_audit(kind, 1, **args)
+            assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"], (kind, args)
+        rc, ev = model.static_audit(kind, 1, 1, arena[:cap])
+        assert rc == p.PROM_ERROR and ev.detail_code == D["NOT_FOUND"]
+    out_bytes = 1056 * 3840 * 4
+    for args in (dict(layer=1), dict(session_id=0), dict(image_gen=0), dict(joint_gen=0),
+                 dict(arena=arena[:out_bytes - 4]), dict(output_identity=0)):
+        call = dict(block_id=1, session_id=1, image_gen=1, context_gen=1, joint_gen=1, arena=arena[:out_bytes])
+        call.update(args)
+        rc, ev = model.main_static_audit(**call)
+        assert rc == p.PROM_ERROR and ev.detail_code == D["INVALID_REQUEST"], args
+    rc, ev = model.main_static_audit(1, 1, 1, 1, 1, arena[:out_bytes])
+    assert rc == p.PROM_ERROR and ev.detail_code == D["NOT_FOUND"]
+
+
+def test_set_main_attention_route_argument_checks(model):
+    """reactor_vulkan_model_block.c:4229-4251: no evidence pointer or an unknown
+    route fails without touching anything; an unknown session fails with the
+    session evidence."""
+    for route in (0, 4):
+        rc, _ = model.set_main_attention_route(1, route)
+        assert rc == p.PROM_ERROR
+    rc, _ = model.set_main_attention_route(1, p.PROM_MAIN_ATTENTION_ROUTE_AUTO, evidence=False)
+    assert rc == p.PROM_ERROR
+    rc, ev = model.set_main_attention_route(7, p.PROM_MAIN_ATTENTION_ROUTE_SERIAL_CANONICAL)
+    assert rc == p.PROM_ERROR and ev.created == 0
