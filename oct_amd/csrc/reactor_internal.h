@@ -40,6 +40,7 @@ struct Runtime {
   uint64_t m1_weight_hash;
   uint32_t m1_weight_width;
   ModelState* model;  // created by the first model-block or session call
+  PrometheusFftDiagnostics fft_diag;  // the last fp32 FFT call (struct_size 0 before the first)
 };
 
 struct DeviceContext {

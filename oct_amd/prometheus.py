@@ -524,6 +524,46 @@ class PrometheusGemma4E2BM1AttentionScoresResult(Structure):
                        "u64 pipeline_create_count, u64 observed_weight_generation, u64 requested_weight_generation")
 
 
+# ---- batched complex-fp32 FFT (reactor_api.h:329-380, 1251-1305) ----------
+PROM_FFT_FLAG_FORWARD, PROM_FFT_FLAG_INVERSE, PROM_FFT_FLAG_INVERSE_NORMALIZE = 1, 2, 4
+PROM_FFT_FLAG_BENCHMARK_ALLOW_NON_PRODUCTION_PATH = 8
+PROM_FFT_PATH_NONE, PROM_FFT_PATH_UNAVAILABLE, PROM_FFT_PATH_VULKAN_RADIX2_RESERVED = 0, 1, 3
+PROM_FFT_BENCHMARK_VARIANT_RADIX2 = 2
+PROM_FFT_DETAIL = {
+    "UNAVAILABLE": -6701, "INVALID_REQUEST": -6702, "NULL_INPUT": -6703, "NULL_OUTPUT": -6704,
+    "ZERO_ELEMENT_COUNT": -6705, "NON_POWER_OF_TWO": -6706, "INVALID_DIRECTION_FLAGS": -6707,
+    "INVALID_STRIDE": -6708, "SIZE_OVERFLOW": -6709, "ZERO_BATCH_COUNT": -6710,
+    "INVERSE_NORMALIZE_REQUIRES_INVERSE": -6711, "VULKAN_UNAVAILABLE": -6712, "UNSUPPORTED_SIZE": -6713,
+    "ALLOCATION_FAILED": -6714, "UPLOAD_FAILED": -6715, "DISPATCH_FAILED": -6716, "READBACK_FAILED": -6717,
+    "PLAN_DISPATCH_DISAGREEMENT": -6719,
+}
+
+
+class PrometheusComplex32(Structure):
+    _fields_ = _fields("f32 real, f32 imag")
+
+
+class PrometheusFftRequest(Structure):
+    _fields_ = _fields("u32 struct_size, p input, p output, u32 element_count, u32 batch_count, "
+                       "u32 stride_elements, u32 flags")
+
+
+class PrometheusFftDiagnostics(Structure):
+    _fields_ = _fields(
+        "u32 struct_size, u32 api_declared, u32 capability_reported, u32 production_enabled, u32 benchmark_enabled, "
+        "u32 last_element_count, u32 last_batch_count, u32 last_stride_elements, u32 last_effective_stride_elements, "
+        "u32 last_flags, u32 last_direction, u32 last_validation_status, i32 last_failure_detail, "
+        "u32 requested_path_id, u32 executed_path_id, u32 requested_radix, u32 executed_radix, u32 fallback_reason, "
+        "u32 plan_pass_count, u32 ping_pong_swap_count, u32 final_output_role, u64 ping_arena_reuse_count, "
+        "u64 ping_arena_grow_count, u64 pong_arena_reuse_count, u64 pong_arena_grow_count, "
+        "u64 twiddle_arena_reuse_count, u64 twiddle_arena_grow_count, u32 selector_cache_valid, u32 plan_valid, "
+        "u32 plan_element_count, u32 plan_log2_element_count, u32 plan_first_span, u32 plan_last_span, "
+        "u32 plan_radix_mask, u32 plan_bit_reversal_required, u32 plan_first_source_role, "
+        "u32 plan_first_destination_role, u32 plan_direction, u32 plan_twiddle_mode, u64 selector_cache_reuse_count, "
+        "u64 selector_cache_recompute_count, u64 selector_cache_invalidation_count, "
+        "u64 selector_cache_last_dependency_mask")
+
+
 # ---- resident model blocks and the compiled session (reactor_api.h:666-1249)
 PROM_MODEL_BLOCK_MAX_WEIGHTS = 13
 PROM_MODEL_BLOCK_MAX_STEPS = 7
@@ -824,6 +864,13 @@ _SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_fft64_device": (
         c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_fft": (
+        c_int, [c_void_p, POINTER(PrometheusFftRequest), POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_fft_benchmark_variant": (
+        c_int, [c_void_p, POINTER(PrometheusFftRequest), c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_fft_diagnostics": (c_int, [c_void_p, POINTER(PrometheusFftDiagnostics)]),
+    "prometheus_reactor_runtime_fft_diagnostics_sized": (
+        c_int, [c_void_p, POINTER(PrometheusFftDiagnostics), c_uint32]),
     "prometheus_reactor_runtime_gemma4e2b_m1_projection_activation_rmsnorm": (
         c_int, [c_void_p, POINTER(PrometheusGemma4E2BM1InputRmsNormRequest),
                 POINTER(PrometheusGemma4E2BM1InputRmsNormResult)]),
@@ -1362,6 +1409,36 @@ class NativeRuntime:
                                                        _ptr(out) if out.size else None, x.size,
                                                        byref(stage), byref(detail))
         return rc, CallStatus(stage.value, detail.value), out
+
+    # -- batched complex-fp32 FFT (reactor_api.h:2656-2670) -------------------
+    def fft(self, values, count: int, batch: int = 1, stride: int = 0, flags: int = 0,
+            output: Optional[np.ndarray] = None, variant: Optional[int] = None, request_patch=None):
+        """complex64 ``values`` holding ``batch`` sequences of ``count`` points
+        ``stride`` apart (0: contiguous); returns (rc, status, output)."""
+        x = np.ascontiguousarray(values, dtype=np.complex64)
+        out = np.zeros_like(x) if output is None else output
+        r = PrometheusFftRequest()
+        r.struct_size = ctypes.sizeof(r)
+        r.input = _ptr(x) if x.size else None
+        r.output = _ptr(out) if out.size else None
+        r.element_count, r.batch_count, r.stride_elements, r.flags = count, batch, stride, flags
+        if request_patch:
+            request_patch(r)
+        stage, detail = c_uint32(0), c_int(0)
+        if variant is None:
+            rc = self.lib.prometheus_reactor_runtime_fft(self.handle, byref(r), byref(stage), byref(detail))
+        else:
+            rc = self.lib.prometheus_reactor_runtime_fft_benchmark_variant(self.handle, byref(r), variant,
+                                                                         byref(stage), byref(detail))
+        return rc, CallStatus(stage.value, detail.value), out
+
+    def fft_diagnostics(self, size: Optional[int] = None) -> PrometheusFftDiagnostics:
+        d = PrometheusFftDiagnostics()
+        rc = (self.lib.prometheus_reactor_runtime_fft_diagnostics(self.handle, byref(d)) if size is None else
+              self.lib.prometheus_reactor_runtime_fft_diagnostics_sized(self.handle, byref(d), size))
+        if rc != PROM_OK:
+            raise ReactorIssue("fft_diagnostics_failed", f"rc={rc}")
+        return d
 
     def fft64_device(self, din: int, dout: int, count: int) -> int:
         stage, detail = c_uint32(0), c_int(0)

@@ -77,6 +77,7 @@ def lib() -> ctypes.CDLL:
             "oct_fft64_with_roots": (None, [P, P, P, c_uint32]),
             "oct_fft64": (c_int32, [P, P, P, c_uint32]),
             "oct_fft64_agrees": (c_int32, [P, P, c_uint32]),
+            "oct_dft_c32": (None, [P, P, c_uint32, c_uint32, c_uint32, c_int32]),
             "oct_m1_rmsnorm": (None, [P, c_uint32, P, P, P, c_uint32, c_uint32, c_float, c_int32, c_int32]),
             "oct_m1_head_rmsnorm_go": (None, [P, P, P, c_uint32, c_uint32, c_float]),
             "oct_m1_rope": (None, [P, P, P, P, c_uint32, c_uint32, c_uint32]),
@@ -253,6 +254,20 @@ def fft64(x) -> np.ndarray:
     scratch = np.zeros(max(1, n), dtype=np.float64)
     if lib().oct_fft64(_p(x), _p(out), _p(scratch), n) != 0:
         raise ValueError("FFT requires a non-empty power-of-two length")
+    return out
+
+
+def dft_c32(x, n: int, batch: int = 1, stride: int = 0, inverse: bool = False) -> np.ndarray:
+    """reactor_fft_api_tests.cpp:525-553 restated in C: direct binary64 DFT of
+    ``batch`` complex64 sequences of ``n`` points ``stride`` apart (0:
+    contiguous), divided by n for the inverse, rounded to complex64; the
+    padding between batches is the input's."""
+    x = np.ascontiguousarray(x, dtype=np.complex64)
+    stride = stride or n
+    if n < 1 or batch < 1 or stride < n or x.size < (batch - 1) * stride + n:
+        raise ValueError("invalid batched DFT shape")
+    out = np.zeros_like(x)
+    lib().oct_dft_c32(_p(x), _p(out), n, batch, stride, 1 if inverse else 0)
     return out
 
 

@@ -117,6 +117,10 @@ void oct_fft64_with_roots(const double* input, double* output, const double* twi
 int32_t oct_fft64(const double* input, double* output, double* scratch_twiddles, uint32_t n);
 /* internal/fft/fft.go:176-192 (agrees). */
 int32_t oct_fft64_agrees(const double* reference, const double* actual, uint32_t n);
+/* reactor_fft_api_tests.cpp:525-553: the direct binary64 DFT of `batch`
+   complex-fp32 sequences of n points `stride` apart (inverse / n), rounded to
+   fp32; the padding is copied from the input. */
+void oct_dft_c32(const float* input, float* output, uint32_t n, uint32_t batch, uint32_t stride, int32_t inverse);
 
 /* Gemma-4-E2B M1 stages (oct_oracle_m1.c). */
 void oct_m1_rmsnorm(const float* input, uint32_t stride, const float* weight, float* output, float* inv_rms,

@@ -82,3 +82,36 @@ int32_t oct_fft64_agrees(const double* reference, const double* actual, uint32_t
   }
   return 1;
 }
+
+/*
+ * The batched complex-fp32 FFT's acceptance authority
+ * (internal/prometheus/native/Marionette/reactor_fft_api_tests.cpp:525-553):
+ * for each batch b (base b * stride) a direct binary64 DFT
+ * X[k] = sum_s x[s] * (cos a + i sin a), a = -+2*pi*(k*s)/n (k*s a 32-bit
+ * product, as there), divided by n for the inverse, rounded to fp32.  The
+ * padding between batches is copied from the input.  O(n^2) per batch.
+ */
+void oct_dft_c32(const float* input, float* output, uint32_t n, uint32_t batch, uint32_t stride, int32_t inverse) {
+  const double pi = 3.14159265358979323846264338327950288;
+  const uint64_t physical = (uint64_t)(batch - 1u) * stride + n;
+  for (uint64_t i = 0; i < 2 * physical; ++i) output[i] = input[i];
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint64_t base = (uint64_t)b * stride;
+    for (uint32_t k = 0; k < n; ++k) {
+      double re = 0.0, im = 0.0;
+      for (uint32_t s = 0; s < n; ++s) {
+        const double angle = (inverse ? 2.0 : -2.0) * pi * (double)(uint32_t)(k * s) / (double)n;
+        const double c = cos(angle), sn = sin(angle);
+        const double xr = input[2 * (base + s)], xi = input[2 * (base + s) + 1];
+        re += xr * c - xi * sn;
+        im += xr * sn + xi * c;
+      }
+      if (inverse) {
+        re /= (double)n;
+        im /= (double)n;
+      }
+      output[2 * (base + k)] = (float)re;
+      output[2 * (base + k) + 1] = (float)im;
+    }
+  }
+}

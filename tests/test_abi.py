@@ -102,6 +102,9 @@ STRUCTS = {
     "PrometheusNoiseRefinerStaticAuditRequest": p.PrometheusNoiseRefinerStaticAuditRequest,
     "PrometheusContextRefinerStaticAuditRequest": p.PrometheusNoiseRefinerStaticAuditRequest,
     "PrometheusMainTransformerStaticAuditRequest": p.PrometheusMainTransformerStaticAuditRequest,
+    "PrometheusComplex32": p.PrometheusComplex32,
+    "PrometheusFftRequest": p.PrometheusFftRequest,
+    "PrometheusFftDiagnostics": p.PrometheusFftDiagnostics,
 }
 MODEL_BLOCK_STRUCTS = tuple(n for n in STRUCTS if "ModelBlock" in n or "Refiner" in n or "MainTransformer" in n
                             or "CompiledModel" in n)
@@ -116,7 +119,8 @@ REFERENCE_STRUCTS = (
     "PrometheusSgemmBatchDiagnostics", "PrometheusSgemmAsyncTaskDiagnostics", "PrometheusSgemmAsyncDiagnostics",
     "PrometheusGemma4E2BM1RopeRequest", "PrometheusGemma4E2BM1RopeResult", "PrometheusGemma4E2BM1HeadRmsNormRopeRequest",
     "PrometheusGemma4E2BM1HeadRmsNormRopeResult", "PrometheusGemma4E2BM1AttentionScoresRequest",
-    "PrometheusGemma4E2BM1AttentionScoresResult",
+    "PrometheusGemma4E2BM1AttentionScoresResult", "PrometheusComplex32", "PrometheusFftRequest",
+    "PrometheusFftDiagnostics",
 ) + MODEL_BLOCK_STRUCTS
 REFERENCE_HEADER = Path("/root/reference/internal/prometheus/native/reactor_api.h")
 
