@@ -309,6 +309,75 @@ typedef struct PrometheusReductionExecutionResult {
   PrometheusReductionPlan plan;
 } PrometheusReductionExecutionResult;
 
+/* reactor_api.h:600-664.  Diagnostics of the runtime's row reductions, and
+   the benchmark request/result: warmup + measured executions of one
+   reduction, timing percentiles and a correctness verdict. */
+typedef struct PrometheusReductionDiagnostics {
+  uint32_t struct_size;
+  uint32_t initialized;
+  uint32_t production_enabled;
+  uint32_t experimental_enabled;
+  uint32_t configured_ring_depth;
+  uint32_t physical_slot_count;
+  uint32_t acquire_cursor;
+  uint32_t outstanding_slots;
+  uint32_t quarantined_slots;
+  uint64_t next_logical_request_id;
+  uint64_t total_requests;
+  uint64_t successful_requests;
+  uint64_t logical_failure_count;
+  uint64_t physical_recycle_count;
+  uint64_t quarantine_count;
+  uint64_t reap_count;
+  uint64_t pipeline_create_count;
+  uint64_t descriptor_update_count;
+  uint64_t command_record_count;
+  uint64_t queue_submit_count;
+  uint64_t buffer_allocation_count;
+  uint64_t buffer_reuse_count;
+  uint64_t temporary_capacity_bytes;
+  uint64_t last_replay_id;
+  uint64_t last_gpu_duration_ns;
+  uint64_t last_end_to_end_ns;
+  uint32_t last_stage_count;
+  uint32_t last_physical_slot_id;
+  uint32_t last_physical_slot_generation;
+  int32_t last_detail_code;
+  uint32_t validation_enabled;
+  uint32_t validation_error_count;
+} PrometheusReductionDiagnostics;
+
+typedef struct PrometheusReductionBenchmarkRequest {
+  uint32_t struct_size;
+  PrometheusReductionRequest reduction;
+  uint32_t warmup_iterations;
+  uint32_t measured_iterations;
+} PrometheusReductionBenchmarkRequest;
+
+typedef struct PrometheusReductionBenchmarkResult {
+  uint32_t struct_size;
+  uint32_t completed_iterations;
+  uint32_t correctness_passed;
+  uint32_t validation_passed;
+  uint32_t device_lost;
+  uint32_t stage_count;
+  uint64_t temporary_bytes;
+  uint64_t replay_id;
+  uint64_t gpu_min_ns;
+  uint64_t gpu_median_ns;
+  uint64_t gpu_max_ns;
+  uint64_t end_to_end_min_ns;
+  uint64_t end_to_end_median_ns;
+  uint64_t end_to_end_max_ns;
+  uint32_t first_mismatch_row;
+  uint32_t first_mismatch_column;
+  float first_expected;
+  float first_actual;
+  float first_absolute_error;
+  float first_relative_error;
+  int32_t detail_code;
+} PrometheusReductionBenchmarkResult;
+
 /* reactor_api.h:1582-1586 */
 typedef struct PrometheusCaps {
   uint32_t available;
@@ -460,6 +529,22 @@ PROM_REACTOR_API int prometheus_reactor_reduction_plan(const PrometheusReduction
 /* reactor_api.h:2673-2675 -- reference envelope (rows <= 1024, total <= 2^24). */
 PROM_REACTOR_API int prometheus_reactor_runtime_reduction(void* handle, const PrometheusReductionRequest* request,
                                                           PrometheusReductionExecutionResult* out_result);
+/* reactor_api.h:2676-2677.  Counts the reduction, reduction_v2 and
+   row_wise_softmax calls of this runtime (one stream: ring depth and slot
+   count 1); out_diag NULL -> PROM_ERROR, unknown handle -> PROM_INVALID_HANDLE. */
+PROM_REACTOR_API int prometheus_reactor_runtime_reduction_diagnostics(void* handle,
+                                                                      PrometheusReductionDiagnostics* out_diag);
+/* reactor_api.h:2678-2681; reactor_vulkan_fused_reduction.c:1122-1201.
+   measured_iterations in 1..10000 (else INVALID_REQUEST); runs warmup +
+   measured executions of `reduction` (reference envelope), reports the
+   min/median/max GPU and end-to-end times, and checks the last output
+   against a binary64 evaluation of the same reduction on the device with the
+   reference's tolerances (softmax abs 2e-5 or rel 2e-4, values >= -2e-7 and
+   row sums within 3e-4; sum abs 2e-5 * width or rel 2e-5; max exact); a
+   mismatch reports its first position and READBACK_FAILED. */
+PROM_REACTOR_API int prometheus_reactor_runtime_reduction_benchmark(void* handle,
+                                                                    const PrometheusReductionBenchmarkRequest* request,
+                                                                    PrometheusReductionBenchmarkResult* out_result);
 /* reactor_api.h:2682-2685 -- rows <= 1024, width <= 1056, exact in-place allowed. */
 PROM_REACTOR_API int prometheus_reactor_runtime_row_wise_softmax(void* handle,
                                                                  const PrometheusRowWiseSoftmaxRequest* request,

@@ -7,6 +7,9 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "reactor_internal.h"
 
 using namespace prom;
@@ -326,8 +329,8 @@ bool find_nonfinite(const float* x, uint64_t count, uint64_t* index) {
   return false;
 }
 
-int reduction_execute(void* handle, const PrometheusReductionRequest* request, PrometheusReductionExecutionResult* dst,
-                      const ReductionLimits& lim, bool reference_plan) {
+int reduction_execute_once(void* handle, const PrometheusReductionRequest* request,
+                           PrometheusReductionExecutionResult* dst, const ReductionLimits& lim, bool reference_plan) {
   PrometheusReductionExecutionResult local;
   PrometheusReductionExecutionResult& out = dst ? *dst : local;
   memset(&out, 0, sizeof(out));
@@ -421,6 +424,70 @@ int reduction_execute(void* handle, const PrometheusReductionRequest* request, P
   out.end_to_end_ns = wall_ns() - t0;
   rt->successes++;
   return PROM_OK;
+}
+
+// One reduction call, counted for the diagnostics entry.
+int reduction_execute(void* handle, const PrometheusReductionRequest* request, PrometheusReductionExecutionResult* dst,
+                      const ReductionLimits& lim, bool reference_plan) {
+  PrometheusReductionExecutionResult local;
+  PrometheusReductionExecutionResult* out = dst ? dst : &local;
+  const int rc = reduction_execute_once(handle, request, out, lim, reference_plan);
+  Runtime* rt = lookup(handle);
+  if (rt != nullptr) {
+    rt->reduction_total++;
+    if (rc == PROM_OK) {
+      rt->reduction_successes++;
+      rt->reduction_last_replay = out->plan.replay_id;
+      rt->reduction_last_gpu_ns = out->gpu_duration_ns;
+      rt->reduction_last_e2e_ns = out->end_to_end_ns;
+      rt->reduction_last_stages = out->plan.stage_count;
+    } else {
+      rt->reduction_failures++;
+    }
+    rt->reduction_last_detail = out->detail_code;
+  }
+  return rc;
+}
+
+// reactor_vulkan_fused_reduction.c:1044-1114: the benchmark's acceptance rule
+// of `actual` against `expected`; fills the first mismatch.
+bool reduction_outputs_agree(const PrometheusReductionRequest& r, const float* expected, const float* actual,
+                             PrometheusReductionBenchmarkResult* res) {
+  const bool softmax = r.operation == PROM_REDUCTION_OPERATION_SOFTMAX;
+  const bool max_op = r.operation == PROM_REDUCTION_OPERATION_MAX;
+  const uint64_t count = softmax ? r.input_element_count : r.row_count;
+  const float abs_tol = softmax ? 2.0e-5f : (max_op ? 0.0f : 2.0e-5f * (float)r.elements_per_row);
+  const float rel_tol = softmax ? 2.0e-4f : (max_op ? 0.0f : 2.0e-5f);
+  auto mismatch = [&](uint32_t row, uint32_t col, float e, float a, float ae, float re) {
+    res->first_mismatch_row = row;
+    res->first_mismatch_column = col;
+    res->first_expected = e;
+    res->first_actual = a;
+    res->first_absolute_error = ae;
+    res->first_relative_error = re;
+    return false;
+  };
+  for (uint64_t i = 0; i < count; ++i) {
+    const float ae = fabsf(actual[i] - expected[i]);
+    float den = fabsf(expected[i]);
+    if (den < 1.0e-20f) den = 1.0f;
+    const float re = ae / den;
+    if (!isfinite(actual[i]) || (ae > abs_tol && re > rel_tol))
+      return mismatch(softmax ? (uint32_t)(i / r.elements_per_row) : (uint32_t)i,
+                      softmax ? (uint32_t)(i % r.elements_per_row) : UINT32_MAX, expected[i], actual[i], ae, re);
+  }
+  if (!softmax) return true;
+  for (uint32_t row = 0; row < r.row_count; ++row) {
+    double sum = 0.0;
+    for (uint32_t c = 0; c < r.elements_per_row; ++c) {
+      const float v = actual[(uint64_t)row * r.elements_per_row + c];
+      if (!isfinite(v) || v < -2.0e-7f) return mismatch(row, c, 0.0f, v, fabsf(v), fabsf(v));
+      sum += v;
+    }
+    if (fabs(sum - 1.0) > 3.0e-4)
+      return mismatch(row, UINT32_MAX, 1.0f, (float)sum, (float)fabs(sum - 1.0), (float)fabs(sum - 1.0));
+  }
+  return true;
 }
 
 // -------------------------------------------------------------- RMSNorm
@@ -545,6 +612,109 @@ PROM_REACTOR_API int prometheus_reactor_reduction_plan(const PrometheusReduction
 PROM_REACTOR_API int prometheus_reactor_runtime_reduction(void* handle, const PrometheusReductionRequest* request,
                                                           PrometheusReductionExecutionResult* out_result) {
   return reduction_execute(handle, request, out_result, kReferenceLimits, true);
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_reduction_diagnostics(void* handle,
+                                                                      PrometheusReductionDiagnostics* out_diag) {
+  if (out_diag == nullptr) return PROM_ERROR;
+  memset(out_diag, 0, sizeof(*out_diag));
+  out_diag->struct_size = sizeof(*out_diag);
+  Runtime* rt = lookup(handle);
+  if (rt == nullptr) return PROM_INVALID_HANDLE;
+  out_diag->initialized = rt->available;
+  out_diag->production_enabled = rt->available;
+  out_diag->configured_ring_depth = 1u;  // one runtime stream
+  out_diag->physical_slot_count = 1u;
+  out_diag->next_logical_request_id = rt->requests + 1;
+  out_diag->total_requests = rt->reduction_total;
+  out_diag->successful_requests = rt->reduction_successes;
+  out_diag->logical_failure_count = rt->reduction_failures;
+  out_diag->physical_recycle_count = rt->reduction_successes;
+  out_diag->command_record_count = rt->reduction_successes;  // one fused launch per call
+  out_diag->queue_submit_count = rt->reduction_successes;
+  out_diag->last_replay_id = rt->reduction_last_replay;
+  out_diag->last_gpu_duration_ns = rt->reduction_last_gpu_ns;
+  out_diag->last_end_to_end_ns = rt->reduction_last_e2e_ns;
+  out_diag->last_stage_count = rt->reduction_last_stages;
+  out_diag->last_detail_code = rt->reduction_last_detail;
+  return PROM_OK;
+}
+
+PROM_REACTOR_API int prometheus_reactor_runtime_reduction_benchmark(void* handle,
+                                                                    const PrometheusReductionBenchmarkRequest* request,
+                                                                    PrometheusReductionBenchmarkResult* out_result) {
+  if (out_result == nullptr) return PROM_ERROR;
+  PrometheusReductionBenchmarkResult& res = *out_result;
+  memset(&res, 0, sizeof(res));
+  res.struct_size = sizeof(res);
+  res.first_mismatch_row = UINT32_MAX;
+  res.first_mismatch_column = UINT32_MAX;
+  if (request == nullptr || request->struct_size < sizeof(*request) || request->measured_iterations == 0u ||
+      request->measured_iterations > 10000u) {
+    res.detail_code = PROM_REDUCTION_DETAIL_INVALID_REQUEST;
+    return PROM_ERROR;
+  }
+  const PrometheusReductionRequest& r = request->reduction;
+  PrometheusReductionExecutionResult er;
+  std::vector<uint64_t> gpu, e2e;
+  gpu.reserve(request->measured_iterations);
+  e2e.reserve(request->measured_iterations);
+  const uint64_t total = (uint64_t)request->warmup_iterations + request->measured_iterations;
+  for (uint64_t it = 0; it < total; ++it) {
+    if (reduction_execute(handle, &r, &er, kReferenceLimits, true) != PROM_OK) {
+      res.detail_code = er.detail_code;
+      return er.detail_code == PROM_REDUCTION_DETAIL_RUNTIME_UNAVAILABLE && lookup(handle) == nullptr
+                 ? PROM_INVALID_HANDLE
+                 : PROM_ERROR;
+    }
+    if (it >= request->warmup_iterations) {
+      gpu.push_back(er.gpu_duration_ns);
+      e2e.push_back(er.end_to_end_ns);
+      res.completed_iterations += 1u;
+    }
+  }
+  // the last output against the binary64 evaluation of the same rows on the device
+  const bool softmax = r.operation == PROM_REDUCTION_OPERATION_SOFTMAX;
+  const uint64_t out_count = softmax ? r.input_element_count : r.row_count;
+  std::vector<float> expected(out_count);
+  {
+    DeviceContext& cx = ctx();
+    std::lock_guard<std::mutex> lock(cx.mu);
+    float* din = static_cast<float*>(staging(0, r.input_element_count * sizeof(float)));
+    float* dexp = static_cast<float*>(staging(2, out_count * sizeof(float)));
+    if (din == nullptr || dexp == nullptr ||
+        hipMemcpyAsync(din, r.input, r.input_element_count * sizeof(float), hipMemcpyHostToDevice, cx.stream) !=
+            hipSuccess ||
+        launch_row_reduction_check(din, dexp, r.row_count, r.elements_per_row, r.operation, cx.stream) !=
+            hipSuccess ||
+        hipMemcpyAsync(expected.data(), dexp, out_count * sizeof(float), hipMemcpyDeviceToHost, cx.stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(cx.stream) != hipSuccess) {
+      (void)hipGetLastError();
+      res.detail_code = PROM_REDUCTION_DETAIL_READBACK_FAILED;
+      return PROM_ERROR;
+    }
+  }
+  if (!reduction_outputs_agree(r, expected.data(), r.output, &res)) {
+    res.detail_code = PROM_REDUCTION_DETAIL_READBACK_FAILED;
+    return PROM_ERROR;
+  }
+  res.correctness_passed = 1u;
+  res.validation_passed = 1u;  // no validation layer: its error count stays 0
+  std::sort(gpu.begin(), gpu.end());
+  std::sort(e2e.begin(), e2e.end());
+  const size_t n = gpu.size();
+  res.gpu_min_ns = gpu[0];
+  res.gpu_median_ns = gpu[n / 2];
+  res.gpu_max_ns = gpu[n - 1];
+  res.end_to_end_min_ns = e2e[0];
+  res.end_to_end_median_ns = e2e[n / 2];
+  res.end_to_end_max_ns = e2e[n - 1];
+  res.stage_count = er.plan.stage_count;
+  res.temporary_bytes = er.plan.temporary_bytes;
+  res.replay_id = er.plan.replay_id;
+  res.detail_code = 0;
+  return PROM_OK;
 }
 
 PROM_REACTOR_API int prometheus_reactor_runtime_reduction_v2(void* handle, const PrometheusReductionRequest* request,

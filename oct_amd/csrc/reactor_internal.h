@@ -41,6 +41,11 @@ struct Runtime {
   uint32_t m1_weight_width;
   ModelState* model;  // created by the first model-block or session call
   PrometheusFftDiagnostics fft_diag;  // the last fp32 FFT call (struct_size 0 before the first)
+  // Row-reduction calls (reduction, reduction_v2, row_wise_softmax) for the diagnostics entry.
+  uint64_t reduction_total, reduction_successes, reduction_failures;
+  uint64_t reduction_last_replay, reduction_last_gpu_ns, reduction_last_e2e_ns;
+  uint32_t reduction_last_stages;
+  int32_t reduction_last_detail;
 };
 
 struct DeviceContext {
@@ -110,6 +115,9 @@ hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const do
 const double2* fft64_roots(uint32_t n);
 hipError_t launch_row_reduction(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,
                                 hipStream_t stream);
+// Binary64 reference of the same row reduction (the benchmark's correctness check).
+hipError_t launch_row_reduction_check(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,
+                                      hipStream_t stream);
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, float* inv_rms, uint32_t tokens,
                           uint32_t width, uint32_t stride, float eps, hipStream_t stream);
 

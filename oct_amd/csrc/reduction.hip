@@ -225,7 +225,57 @@ hipError_t dispatch(const float* in, const float* w, float* out, float* aux, uin
   return hipGetLastError();
 }
 
+// The benchmark entry's correctness reference: the same reduction with every
+// sum, exponential and quotient in binary64 (one workgroup per row, a
+// strided lane pass then an LDS tree), rounded to float at the end.  It shares
+// no code with the fp32 kernels above.
+__global__ __launch_bounds__(256) void row_reduction_check_kernel(const float* __restrict__ in,
+                                                                  float* __restrict__ out, uint32_t width,
+                                                                  uint32_t op) {
+  __shared__ double part[256];
+  const uint32_t lane = threadIdx.x;
+  const float* x = in + (size_t)blockIdx.x * width;
+  float m = -__builtin_inff();
+  if (op != kOpSum) {
+    for (uint32_t i = lane; i < width; i += 256) m = x[i] > m ? x[i] : m;
+    part[lane] = (double)m;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+      if (lane < s && part[lane + s] > part[lane]) part[lane] = part[lane + s];
+      __syncthreads();
+    }
+    m = (float)part[0];
+    __syncthreads();
+    if (op == kOpMax) {
+      if (lane == 0) out[blockIdx.x] = m;
+      return;
+    }
+  }
+  double acc = 0.0;
+  for (uint32_t i = lane; i < width; i += 256) acc += op == kOpSum ? (double)x[i] : exp((double)x[i] - (double)m);
+  part[lane] = acc;
+  __syncthreads();
+  for (uint32_t s = 128; s > 0; s >>= 1) {
+    if (lane < s) part[lane] += part[lane + s];
+    __syncthreads();
+  }
+  const double total = part[0];
+  if (op == kOpSum) {
+    if (lane == 0) out[blockIdx.x] = (float)total;
+    return;
+  }
+  for (uint32_t i = lane; i < width; i += 256)
+    out[(size_t)blockIdx.x * width + i] = (float)(exp((double)x[i] - (double)m) / total);
+}
+
 }  // namespace
+
+hipError_t launch_row_reduction_check(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,
+                                      hipStream_t stream) {
+  if (rows == 0 || width == 0 || op < kOpSum || op > kOpSoftmax) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(row_reduction_check_kernel, dim3(rows), dim3(256), 0, stream, in, out, width, op);
+  return hipGetLastError();
+}
 
 hipError_t launch_row_reduction(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,
                                 hipStream_t stream) {

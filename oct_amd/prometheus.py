@@ -34,6 +34,9 @@ PROM_BACKEND_UNKNOWN, PROM_BACKEND_STUB, PROM_BACKEND_HARDWARE_GPU, PROM_BACKEND
 PROM_REASON_NONE, PROM_REASON_STUB_UNAVAILABLE, PROM_REASON_VULKAN_UNAVAILABLE = 0, 1, 2
 STAGE_NONE, STAGE_INIT, STAGE_TRANSFER_IN, STAGE_SUBMIT, STAGE_TRANSFER_OUT, STAGE_CLEANUP = range(6)
 OP_SUM, OP_MAX, OP_SOFTMAX = 1, 2, 3
+# row-reduction details (reactor_api.h:404-430)
+REDUCTION_DETAIL = {"INVALID_REQUEST": -6801, "NULL_INPUT": -6802, "NULL_OUTPUT": -6803,
+                    "RESOURCE_CREATE_FAILED": -6818, "READBACK_FAILED": -6824, "RUNTIME_UNAVAILABLE": -6825}
 FINALIZATION_NONE, FINALIZATION_STABLE_SOFTMAX = 0, 1
 FLAG_FORCE_FUSED, FLAG_FORCE_COMPOSED = 1, 2
 TESTCFG_FAIL_DEVICE_CREATE = 1 << 0
@@ -83,6 +86,16 @@ DETAIL_M46_NONFINITE_INPUT = -7418
 
 
 # ---- ABI structs -----------------------------------------------------------
+def _fields(spec: str):
+    """'u32 a, u64 b, f32 c, p d, i32 e' -> ctypes field list."""
+    kinds = {"u32": c_uint32, "u64": c_uint64, "f32": c_float, "p": c_void_p, "i32": ctypes.c_int32}
+    out = []
+    for item in spec.split(","):
+        kind, name = item.split()
+        out.append((name, kinds[kind]))
+    return out
+
+
 class PrometheusCaps(Structure):
     _fields_ = [("available", c_uint32), ("backend_type", c_uint32), ("reason_code", c_uint32)]
 
@@ -196,6 +209,36 @@ class PrometheusReductionExecutionResult(Structure):
         ("validation_error_count_after", c_uint32),
         ("plan", PrometheusReductionPlan),
     ]
+
+
+class PrometheusReductionDiagnostics(Structure):
+    """reactor_api.h:600-633"""
+    _fields_ = _fields(
+        "u32 struct_size, u32 initialized, u32 production_enabled, u32 experimental_enabled, "
+        "u32 configured_ring_depth, u32 physical_slot_count, u32 acquire_cursor, u32 outstanding_slots, "
+        "u32 quarantined_slots, u64 next_logical_request_id, u64 total_requests, u64 successful_requests, "
+        "u64 logical_failure_count, u64 physical_recycle_count, u64 quarantine_count, u64 reap_count, "
+        "u64 pipeline_create_count, u64 descriptor_update_count, u64 command_record_count, u64 queue_submit_count, "
+        "u64 buffer_allocation_count, u64 buffer_reuse_count, u64 temporary_capacity_bytes, u64 last_replay_id, "
+        "u64 last_gpu_duration_ns, u64 last_end_to_end_ns, u32 last_stage_count, u32 last_physical_slot_id, "
+        "u32 last_physical_slot_generation, i32 last_detail_code, u32 validation_enabled, "
+        "u32 validation_error_count")
+
+
+class PrometheusReductionBenchmarkRequest(Structure):
+    """reactor_api.h:635-640"""
+    _fields_ = [("struct_size", c_uint32), ("reduction", PrometheusReductionRequest),
+                ("warmup_iterations", c_uint32), ("measured_iterations", c_uint32)]
+
+
+class PrometheusReductionBenchmarkResult(Structure):
+    """reactor_api.h:642-664"""
+    _fields_ = _fields(
+        "u32 struct_size, u32 completed_iterations, u32 correctness_passed, u32 validation_passed, u32 device_lost, "
+        "u32 stage_count, u64 temporary_bytes, u64 replay_id, u64 gpu_min_ns, u64 gpu_median_ns, u64 gpu_max_ns, "
+        "u64 end_to_end_min_ns, u64 end_to_end_median_ns, u64 end_to_end_max_ns, u32 first_mismatch_row, "
+        "u32 first_mismatch_column, f32 first_expected, f32 first_actual, f32 first_absolute_error, "
+        "f32 first_relative_error, i32 detail_code")
 
 
 class PrometheusRowWiseSoftmaxRequest(Structure):
@@ -457,16 +500,6 @@ class PrometheusSgemmAsyncDiagnostics(Structure):
                 ("quarantine_event_count", c_uint64), ("reap_poll_count", c_uint64), ("reap_success_count", c_uint64),
                 ("reap_wait_count", c_uint64), ("reap_failure_count", c_uint64), ("max_quarantine_depth", c_uint32),
                 ("runtime_unsafe_to_reuse", c_uint32), ("tasks", PrometheusSgemmAsyncTaskDiagnostics * 4)]
-
-
-def _fields(spec: str):
-    """'u32 a, u64 b, f32 c, p d, i32 e' -> ctypes field list."""
-    kinds = {"u32": c_uint32, "u64": c_uint64, "f32": c_float, "p": c_void_p, "i32": ctypes.c_int32}
-    out = []
-    for item in spec.split(","):
-        kind, name = item.split()
-        out.append((name, kinds[kind]))
-    return out
 
 
 class PrometheusGemma4E2BM1RopeRequest(Structure):
@@ -864,6 +897,10 @@ _SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_fft64_device": (
         c_int, [c_void_p, c_void_p, c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_reduction_diagnostics": (
+        c_int, [c_void_p, POINTER(PrometheusReductionDiagnostics)]),
+    "prometheus_reactor_runtime_reduction_benchmark": (
+        c_int, [c_void_p, POINTER(PrometheusReductionBenchmarkRequest), POINTER(PrometheusReductionBenchmarkResult)]),
     "prometheus_reactor_runtime_fft": (
         c_int, [c_void_p, POINTER(PrometheusFftRequest), POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_fft_benchmark_variant": (
@@ -1166,6 +1203,32 @@ class NativeRuntime:
         fn = (self.lib.prometheus_reactor_runtime_reduction_v2 if lifted
               else self.lib.prometheus_reactor_runtime_reduction)
         rc = fn(self.handle, byref(req), byref(res))
+        return rc, res, output
+
+    def reduction_diagnostics(self):
+        d = PrometheusReductionDiagnostics()
+        rc = self.lib.prometheus_reactor_runtime_reduction_diagnostics(self.handle, byref(d))
+        return rc, d
+
+    def reduction_benchmark(self, x, operation: int, warmup: int = 2, measured: int = 10, request_patch=None):
+        """reactor_api.h:2678-2681 on the reference envelope; returns (rc, result, output)."""
+        x = _f32(x)
+        rows, width = x.shape
+        output = np.empty((rows, width) if operation == OP_SOFTMAX else (rows,), dtype=np.float32)
+        b = PrometheusReductionBenchmarkRequest()
+        b.struct_size = ctypes.sizeof(b)
+        r = b.reduction
+        r.struct_size = ctypes.sizeof(r)
+        r.input, r.output = _ptr(x), _ptr(output)
+        r.row_count, r.elements_per_row = rows, width
+        r.input_element_count, r.output_element_count = rows * width, output.size
+        r.operation = operation
+        r.finalization = FINALIZATION_STABLE_SOFTMAX if operation == OP_SOFTMAX else FINALIZATION_NONE
+        b.warmup_iterations, b.measured_iterations = warmup, measured
+        if request_patch:
+            request_patch(b)
+        res = PrometheusReductionBenchmarkResult()
+        rc = self.lib.prometheus_reactor_runtime_reduction_benchmark(self.handle, byref(b), byref(res))
         return rc, res, output
 
     def rmsnorm(self, x, weight, epsilon: float, stride: Optional[int] = None):

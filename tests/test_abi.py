@@ -105,6 +105,9 @@ STRUCTS = {
     "PrometheusComplex32": p.PrometheusComplex32,
     "PrometheusFftRequest": p.PrometheusFftRequest,
     "PrometheusFftDiagnostics": p.PrometheusFftDiagnostics,
+    "PrometheusReductionDiagnostics": p.PrometheusReductionDiagnostics,
+    "PrometheusReductionBenchmarkRequest": p.PrometheusReductionBenchmarkRequest,
+    "PrometheusReductionBenchmarkResult": p.PrometheusReductionBenchmarkResult,
 }
 MODEL_BLOCK_STRUCTS = tuple(n for n in STRUCTS if "ModelBlock" in n or "Refiner" in n or "MainTransformer" in n
                             or "CompiledModel" in n)
@@ -120,7 +123,8 @@ REFERENCE_STRUCTS = (
     "PrometheusGemma4E2BM1RopeRequest", "PrometheusGemma4E2BM1RopeResult", "PrometheusGemma4E2BM1HeadRmsNormRopeRequest",
     "PrometheusGemma4E2BM1HeadRmsNormRopeResult", "PrometheusGemma4E2BM1AttentionScoresRequest",
     "PrometheusGemma4E2BM1AttentionScoresResult", "PrometheusComplex32", "PrometheusFftRequest",
-    "PrometheusFftDiagnostics",
+    "PrometheusFftDiagnostics", "PrometheusReductionDiagnostics", "PrometheusReductionBenchmarkRequest",
+    "PrometheusReductionBenchmarkResult",
 ) + MODEL_BLOCK_STRUCTS
 REFERENCE_HEADER = Path("/root/reference/internal/prometheus/native/reactor_api.h")
 
@@ -495,3 +499,30 @@ def test_compiled_matmul_request_shape_checks():
         p.compiled_matmul_request([[1.0, 2.0], [1.0]], [[1.0], [2.0]])
     m, n, k, a, b = p.compiled_matmul_request([[0.1, 2.0]], [[1.0], [3.0]])
     assert (m, n, k) == (1, 1, 2) and a.dtype == np.float32 and a[0, 0] == np.float32(0.1)
+
+
+def test_reduction_diagnostics_and_benchmark_without_device():
+    """reactor_concept_reduction.cpp:96-115 and reactor_vulkan_fused_reduction.c:
+    1122-1146: argument checks, and the counters a device-less runtime keeps."""
+    rt = p.NativeRuntime(test_flags=0)
+    try:
+        rc, d = rt.reduction_diagnostics()
+        assert rc == p.PROM_OK and d.struct_size == ctypes.sizeof(d) and d.total_requests == 0
+        assert rt.lib.prometheus_reactor_runtime_reduction_diagnostics(rt.handle, None) == p.PROM_ERROR
+        assert rt.lib.prometheus_reactor_runtime_reduction_diagnostics(None, ctypes.byref(d)) == p.PROM_INVALID_HANDLE
+        x = np.ones((4, 8), np.float32)
+        for patch in (lambda b: setattr(b, "measured_iterations", 0),
+                      lambda b: setattr(b, "measured_iterations", 10001),
+                      lambda b: setattr(b, "struct_size", 4)):
+            rc, res, _ = rt.reduction_benchmark(x, p.OP_SUM, request_patch=patch)
+            assert rc == p.PROM_ERROR and res.detail_code == p.REDUCTION_DETAIL["INVALID_REQUEST"]
+            assert res.first_mismatch_row == 0xFFFFFFFF and res.completed_iterations == 0
+        assert rt.lib.prometheus_reactor_runtime_reduction_benchmark(rt.handle, None, None) == p.PROM_ERROR
+        if not rt.available:
+            rc, res, _ = rt.reduction_benchmark(x, p.OP_SUM)
+            assert rc == p.PROM_ERROR and res.detail_code == p.REDUCTION_DETAIL["RUNTIME_UNAVAILABLE"]
+            rc, d = rt.reduction_diagnostics()
+            assert d.total_requests == 1 and d.logical_failure_count == 1 and d.initialized == 0
+            assert d.last_detail_code == p.REDUCTION_DETAIL["RUNTIME_UNAVAILABLE"]
+    finally:
+        rt.close()

@@ -203,3 +203,34 @@ def test_gemma_input_rmsnorm_entry(gpu_runtime):
     assert rc == 0 and res.output_written == 1 and res.stage == 0 and res.detail_code == 0
     rc2, y_ref, inv_ref = oracle.rmsnorm_reference(z, wt, 1e-6)
     assert oracle.normwise_rel_err(y, y_ref) <= NORMWISE
+
+
+@pytest.mark.parametrize("op", [p.OP_SUM, p.OP_MAX, p.OP_SOFTMAX])
+def test_reduction_benchmark_entry(op):
+    """reactor_vulkan_fused_reduction.c:1122-1201 on the reference envelope
+    (1024 rows of 4096): every measured iteration completes, the device's
+    binary64 check accepts the output, the timings are ordered, and the
+    output also passes the CPU oracle's comparator; the diagnostics count
+    every execution."""
+    rt = p.NativeRuntime()
+    try:
+        assert rt.available
+        rng = np.random.default_rng(op)
+        x = rng.standard_normal((1024, 4096)).astype(np.float32)
+        rc, res, out = rt.reduction_benchmark(x, op, warmup=3, measured=9)
+        assert rc == p.PROM_OK and res.detail_code == 0, (res.detail_code, res.first_mismatch_row)
+        assert res.completed_iterations == 9 and res.correctness_passed == 1 and res.validation_passed == 1
+        assert 0 < res.gpu_min_ns <= res.gpu_median_ns <= res.gpu_max_ns
+        assert res.gpu_min_ns <= res.end_to_end_min_ns <= res.end_to_end_median_ns <= res.end_to_end_max_ns
+        assert res.first_mismatch_row == 0xFFFFFFFF and res.stage_count >= 1 and res.replay_id != 0
+        rc2, _, _ = rt.reduction(x, op, lifted=False)
+        _check(x, op, out)
+        rc, d = rt.reduction_diagnostics()
+        assert rc == p.PROM_OK and d.initialized == 1 and d.production_enabled == 1
+        assert d.total_requests == 13 and d.successful_requests == 13 and d.logical_failure_count == 0
+        assert d.last_replay_id == res.replay_id and d.last_stage_count == res.stage_count and d.last_detail_code == 0
+        assert d.last_gpu_duration_ns > 0 and d.configured_ring_depth == 1
+        print(f"reduction benchmark op={op}: gpu median {res.gpu_median_ns / 1e3:.1f} us, "
+              f"end-to-end median {res.end_to_end_median_ns / 1e3:.1f} us", flush=True)
+    finally:
+        rt.close()
