@@ -186,13 +186,18 @@ __device__ __forceinline__ uint32_t pad16(uint32_t i) { return i + (i >> 4); }
 // writes its 16 results contiguously to LDS (padded).  The remaining stages
 // (span >= 32) run two per barrier as in fft_lds_kernel, on padded indices.
 // Against fft_lds_kernel this removes the bank-conflicted bit-reversed
-// scatter and two LDS round trips with their barriers.
-__global__ __launch_bounds__(256) void fft_reg16_kernel(const double2* __restrict__ in, double2* __restrict__ out,
-                                                        const double2* __restrict__ roots, uint32_t n_total,
-                                                        uint32_t log2l, uint32_t log2seqs, uint64_t in_seq,
-                                                        uint64_t in_elem, uint64_t out_seq, uint64_t out_elem,
-                                                        int post, int seq_fast_in, int seq_fast_out) {
+// scatter and two LDS round trips with their barriers.  kThreads is the
+// workgroup size: 256, or 1024 for a single sequence of up to 4096 points,
+// whose stages are latency-bound on one workgroup (the threads past the
+// register phase's total/16 take the LDS stages and the stores).
+template <uint32_t kThreads>
+__device__ __forceinline__ void fft_reg16_body(const double2* __restrict__ in, double2* __restrict__ out,
+                                               const double2* __restrict__ roots, uint32_t n_total, uint32_t log2l,
+                                               uint32_t log2seqs, uint64_t in_seq, uint64_t in_elem,
+                                               uint64_t out_seq, uint64_t out_elem, int post, int seq_fast_in,
+                                               int seq_fast_out) {
 #pragma clang fp contract(off)
+  constexpr uint32_t kPer = kFftMaxLds / kThreads;  // output elements per thread
   extern __shared__ double2 smem[];
   const uint32_t L = 1u << log2l;
   const uint32_t seqs = 1u << log2seqs;
@@ -282,10 +287,10 @@ __global__ __launch_bounds__(256) void fft_reg16_kernel(const double2* __restric
     __syncthreads();
   }
   const uint32_t half_n = n_total >> 1;
-  double2 v[kFftPerThread], w[kFftPerThread];
+  double2 v[kPer], w[kPer];
 #pragma unroll
-  for (uint32_t u = 0; u < kFftPerThread; ++u) {
-    const uint32_t e = threadIdx.x + u * kFftThreads;
+  for (uint32_t u = 0; u < kPer; ++u) {
+    const uint32_t e = threadIdx.x + u * kThreads;
     if (e < total) {
       const uint32_t so = seq_fast_out ? (e & (seqs - 1)) : (e >> log2l);
       const uint32_t k = seq_fast_out ? (e >> log2seqs) : (e & (L - 1));
@@ -297,8 +302,8 @@ __global__ __launch_bounds__(256) void fft_reg16_kernel(const double2* __restric
     }
   }
 #pragma unroll
-  for (uint32_t u = 0; u < kFftPerThread; ++u) {
-    const uint32_t e = threadIdx.x + u * kFftThreads;
+  for (uint32_t u = 0; u < kPer; ++u) {
+    const uint32_t e = threadIdx.x + u * kThreads;
     if (e < total) {
       const uint32_t so = seq_fast_out ? (e & (seqs - 1)) : (e >> log2l);
       const uint32_t k = seq_fast_out ? (e >> log2seqs) : (e & (L - 1));
@@ -311,6 +316,25 @@ __global__ __launch_bounds__(256) void fft_reg16_kernel(const double2* __restric
       out[(q0 + so) * out_seq + (uint64_t)k * out_elem] = r;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void fft_reg16_kernel(const double2* __restrict__ in, double2* __restrict__ out,
+                                                        const double2* __restrict__ roots, uint32_t n_total,
+                                                        uint32_t log2l, uint32_t log2seqs, uint64_t in_seq,
+                                                        uint64_t in_elem, uint64_t out_seq, uint64_t out_elem,
+                                                        int post, int seq_fast_in, int seq_fast_out) {
+  fft_reg16_body<256>(in, out, roots, n_total, log2l, log2seqs, in_seq, in_elem, out_seq, out_elem, post,
+                      seq_fast_in, seq_fast_out);
+}
+
+__global__ __launch_bounds__(1024) void fft_reg16_wide_kernel(const double2* __restrict__ in,
+                                                              double2* __restrict__ out,
+                                                              const double2* __restrict__ roots, uint32_t n_total,
+                                                              uint32_t log2l, uint32_t log2seqs, uint64_t in_seq,
+                                                              uint64_t in_elem, uint64_t out_seq, uint64_t out_elem,
+                                                              int post, int seq_fast_in, int seq_fast_out) {
+  fft_reg16_body<1024>(in, out, roots, n_total, log2l, log2seqs, in_seq, in_elem, out_seq, out_elem, post,
+                       seq_fast_in, seq_fast_out);
 }
 
 uint32_t ilog2(uint32_t v) {
@@ -345,13 +369,20 @@ hipError_t launch_pass(const double2* in, double2* out, const double2* roots, ui
     if (e == hipSuccess)
       e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_reg16_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_reg16_wide_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
     if (e != hipSuccess) return e;
     lds_raised = true;
   }
   if (log2l >= 4) {
     const size_t lds = (elems + elems / 16 + ((size_t)1 << log2l) / 2) * sizeof(double2);
-    hipLaunchKernelGGL(fft_reg16_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l,
-                       log2seqs, in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
+    if (blocks == 1 && log2l >= 10)  // one long sequence: a 1024-thread workgroup
+      hipLaunchKernelGGL(fft_reg16_wide_kernel, dim3(1), dim3(1024), lds, stream, in, out, roots, n, log2l, log2seqs,
+                         in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
+    else
+      hipLaunchKernelGGL(fft_reg16_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l,
+                         log2seqs, in_seq, in_elem, out_seq, out_elem, post, fast_in, fast_out);
   } else {
     const size_t lds = (elems + ((size_t)1 << log2l) / 2) * sizeof(double2);
     hipLaunchKernelGGL(fft_lds_kernel, dim3(blocks), dim3(kFftThreads), lds, stream, in, out, roots, n, log2l,
