@@ -264,6 +264,7 @@ void record_plan(PrometheusFftDiagnostics* d, uint32_t n, uint32_t direction) {
   d->plan_twiddle_mode = 2u;
 }
 
+// Caller holds ctx().mu (the diagnostics record and the staging buffers).
 int run_fft(Runtime* rt, const PrometheusFftRequest* r, uint32_t* stage, int* detail) {
   PrometheusFftDiagnostics* d = diag_of(rt);
   *d = default_diag();
@@ -307,7 +308,6 @@ int run_fft(Runtime* rt, const PrometheusFftRequest* r, uint32_t* stage, int* de
   const uint32_t stride = r->stride_elements == 0u ? n : r->stride_elements;
   const size_t bytes = (size_t)physical * sizeof(float2);
   DeviceContext& cx = ctx();
-  std::lock_guard<std::mutex> lock(cx.mu);
   float2* din = static_cast<float2*>(staging(0, bytes));
   float2* dout = static_cast<float2*>(staging(1, bytes));
   float2* dtmp = n > kMaxLds ? static_cast<float2*>(staging(3, (size_t)n * batch * sizeof(float2))) : nullptr;
@@ -349,6 +349,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_fft(void* handle, const Promethe
     set_status(out_stage, out_detail_code, PROM_STAGE_INIT, PROM_INVALID_HANDLE);
     return PROM_INVALID_HANDLE;
   }
+  std::lock_guard<std::mutex> lock(ctx().mu);
   return run_fft(rt, request, out_stage, out_detail_code);
 }
 
@@ -369,6 +370,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_fft_diagnostics_sized(void* hand
   Runtime* rt = lookup(handle);
   if (rt == nullptr) return PROM_INVALID_HANDLE;
   if (out_size > sizeof(*out_diag)) out_size = (uint32_t)sizeof(*out_diag);
+  std::lock_guard<std::mutex> lock(ctx().mu);
   memset(out_diag, 0, out_size);
   memcpy(out_diag, diag_of(rt), out_size);
   return PROM_OK;

@@ -434,6 +434,7 @@ int reduction_execute(void* handle, const PrometheusReductionRequest* request, P
   const int rc = reduction_execute_once(handle, request, out, lim, reference_plan);
   Runtime* rt = lookup(handle);
   if (rt != nullptr) {
+    std::lock_guard<std::mutex> lock(ctx().mu);
     rt->reduction_total++;
     if (rc == PROM_OK) {
       rt->reduction_successes++;
@@ -621,6 +622,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_reduction_diagnostics(void* hand
   out_diag->struct_size = sizeof(*out_diag);
   Runtime* rt = lookup(handle);
   if (rt == nullptr) return PROM_INVALID_HANDLE;
+  std::lock_guard<std::mutex> lock(ctx().mu);
   out_diag->initialized = rt->available;
   out_diag->production_enabled = rt->available;
   out_diag->configured_ring_depth = 1u;  // one runtime stream
