@@ -59,6 +59,10 @@ constexpr uint32_t kAuditMaxJobs = 32;
 constexpr size_t kAuditJobOffset = kAuditRecordBytes;
 constexpr size_t kAuditWitnessOffset = kAuditJobOffset + 4096;
 constexpr size_t kAuditScratchOffset = kAuditWitnessOffset + 256;
+constexpr size_t kAuditClockOffset = kAuditWitnessOffset - 64;  // device clock stamp of a timed execution
+static_assert(kAuditJobOffset + kAuditMaxJobs * sizeof(ZImageAuditJob) <= kAuditClockOffset,
+              "job table overlaps the clock stamp");
+constexpr int kStageEvents = 16;  // ingress begin, the 14 stage boundaries, joint copy end
 static_assert(PROM_ZIMAGE_TURBO_AUDIT_REQUIRED_BYTES <= kAuditRecordBytes, "NoiseRefiner arena records");
 static_assert(kAuditMaxJobs * sizeof(ZImageAuditJob) <= 4096, "audit job table");
 
@@ -165,6 +169,13 @@ struct ModelBlock {
   float* proof_audit = nullptr;
   uint64_t reusable_bytes = 0, audit_alloc_bytes = 0;
   hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+  hipEvent_t stage_ev[kStageEvents] = {};  // Z-Image programs
+  // per-stage timing of the last MainTransformer execution, in device wall-clock nanoseconds
+  uint64_t total_begin_tick = 0, total_end_tick = 0, compute_begin_tick = 0, compute_end_tick = 0;
+  uint64_t ingress_ns = 0, joint_copy_ns = 0;
+  uint64_t stage_begin_tick[PROM_MODEL_BLOCK_MAIN_STAGE_COUNT] = {};
+  uint64_t stage_end_tick[PROM_MODEL_BLOCK_MAIN_STAGE_COUNT] = {};
+  uint64_t stage_ns[PROM_MODEL_BLOCK_MAIN_STAGE_COUNT] = {};
   // execution state
   bool quarantined = false, output_valid = false, audit_valid = false;
   uint64_t output_generation = 0, resident_input_generation = 0;
@@ -209,6 +220,12 @@ struct ModelState {
 namespace {
 
 // ---------------------------------------------------------------- helpers
+
+// One lane writes the device's constant-rate wall clock (the time base of the
+// per-stage ticks in the evidence).
+__global__ __launch_bounds__(64) void device_clock_kernel(uint64_t* __restrict__ dst) {
+  if (threadIdx.x == 0) dst[0] = wall_clock64();
+}
 
 __global__ __launch_bounds__(256) void proof_kernel(const float* __restrict__ in, float* __restrict__ out, uint64_t n,
                                                     float* __restrict__ audit, uint64_t audit_n) {
@@ -281,6 +298,8 @@ void release_block(ModelBlock* b) {
   for (void* p : ptrs) free_dev(p);
   if (b->ev_begin) (void)hipEventDestroy(b->ev_begin);
   if (b->ev_end) (void)hipEventDestroy(b->ev_end);
+  for (hipEvent_t e : b->stage_ev)
+    if (e) (void)hipEventDestroy(e);
   *b = ModelBlock{};
 }
 
@@ -351,6 +370,17 @@ void fill_evidence(const ModelBlock* b, int32_t detail, PrometheusModelBlockEvid
   ev->descriptor_generation = b->descriptor_generation;
   ev->gpu_total_ns = b->gpu_total_ns;
   ev->gpu_compute_ns = b->gpu_compute_ns;
+  ev->gpu_total_begin_tick = b->total_begin_tick;
+  ev->gpu_total_end_tick = b->total_end_tick;
+  ev->gpu_compute_begin_tick = b->compute_begin_tick;
+  ev->gpu_compute_end_tick = b->compute_end_tick;
+  ev->gpu_ingress_transfer_ns = b->ingress_ns;
+  ev->gpu_joint_copy_ns = b->joint_copy_ns;
+  for (uint32_t i = 0; i < PROM_MODEL_BLOCK_MAIN_STAGE_COUNT; ++i) {
+    ev->main_stage_gpu_begin_tick[i] = b->stage_begin_tick[i];
+    ev->main_stage_gpu_end_tick[i] = b->stage_end_tick[i];
+    ev->main_stage_gpu_ns[i] = b->stage_ns[i];
+  }
   ev->last_staging_memcpy_ns = b->last_memcpy_ns;
   ev->last_output_readback_ns = b->last_readback_ns;
 }
@@ -645,10 +675,12 @@ int32_t take_phase_fault(Runtime* rt, bool* unobserved) {
 
 // Runs phases first..last of the Z-Image block of b on x -> out (1 through the
 // Q/K/V split, 2 through the attention residual, 3 the FFN), timing them with
-// events.  A run from phase 1 replaces the pre-attention state an M1B left.
+// events (stage_events: 14 more, at the boundaries of the 13 stages of a full
+// run).  A run from phase 1 replaces the pre-attention state an M1B left.
 // Returns 0 or a model-block detail; an injected unobserved completion leaves
 // the work queued and quarantines the block.
-int32_t run_block(Runtime* rt, ModelBlock* b, const float* x, float* out, int first_phase = 1, int last_phase = 3) {
+int32_t run_block(Runtime* rt, ModelBlock* b, const float* x, float* out, int first_phase = 1, int last_phase = 3,
+                  const hipEvent_t* stage_events = nullptr) {
   bool unobserved = false;
   const int32_t fault = take_phase_fault(rt, &unobserved);
   if (fault != 0) return fault;
@@ -658,7 +690,7 @@ int32_t run_block(Runtime* rt, ModelBlock* b, const float* x, float* out, int fi
   (void)hipEventRecord(b->ev_begin, st);
   uint32_t launches = 0;
   if (enqueue_zimage_block_f32(w, x, b->cond, out, b->ws, b->ws_off, b->tokens, kWidth, kFfn, kEps, st, &launches,
-                               first_phase, last_phase) != hipSuccess) {
+                               first_phase, last_phase, stage_events) != hipSuccess) {
     (void)hipStreamSynchronize(st);
     return PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
   }
@@ -674,12 +706,58 @@ int32_t run_block(Runtime* rt, ModelBlock* b, const float* x, float* out, int fi
   return 0;
 }
 
+// Opens a timed MainTransformer execution: stamps the device clock into the
+// audit area, then records the ingress-begin event.
+hipError_t begin_stage_timing(ModelBlock* b, hipStream_t st) {
+  hipLaunchKernelGGL(device_clock_kernel, dim3(1), dim3(64), 0, st,
+                     reinterpret_cast<uint64_t*>(b->audit_dev + kAuditClockOffset));
+  const hipError_t e = hipGetLastError();
+  return e != hipSuccess ? e : hipEventRecord(b->stage_ev[0], st);
+}
+
+// reactor_vulkan_model_block.c:3531-3565: resolves the 16 timestamps of a
+// completed timed execution (0 ingress begin, 1..14 the stage boundaries, 15
+// joint copy end) into the evidence's ticks and durations.  Ticks are
+// nanoseconds of the device wall clock: the stamp read just before event 0
+// plus each event's elapsed time from event 0, so every duration is the
+// difference of its two ticks.  Leaves the previous timing on any failure.
+void resolve_stage_timing(ModelBlock* b) {
+  uint64_t clock = 0;
+  int khz = 0;
+  if (hipMemcpy(&clock, b->audit_dev + kAuditClockOffset, sizeof(clock), hipMemcpyDeviceToHost) != hipSuccess ||
+      hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx().device) != hipSuccess || khz <= 0)
+    return;
+  uint64_t t[kStageEvents];
+  t[0] = (uint64_t)((double)clock * (1.0e6 / (double)khz) + 0.5);
+  for (int i = 1; i < kStageEvents; ++i) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, b->stage_ev[0], b->stage_ev[i]) != hipSuccess || ms < 0.f) return;
+    t[i] = std::max(t[i - 1], t[0] + (uint64_t)((double)ms * 1.0e6 + 0.5));
+  }
+  b->total_begin_tick = t[0];
+  b->total_end_tick = t[15];
+  b->compute_begin_tick = t[1];
+  b->compute_end_tick = t[14];
+  b->gpu_total_ns = t[15] - t[0];
+  b->gpu_compute_ns = t[14] - t[1];
+  b->ingress_ns = t[1] - t[0];
+  b->joint_copy_ns = t[15] - t[14];
+  for (uint32_t s = 0; s < PROM_MODEL_BLOCK_MAIN_STAGE_COUNT; ++s) {
+    b->stage_begin_tick[s] = t[s + 1];
+    b->stage_end_tick[s] = t[s + 2];
+    b->stage_ns[s] = t[s + 2] - t[s + 1];
+  }
+}
+
 // Allocates everything a block executes with (create time; executions never allocate).
 bool alloc_block_buffers(ModelBlock* b) {
   uint64_t max_weight = 0;
   for (uint32_t i = 0; i < b->weight_count; ++i) max_weight = std::max(max_weight, b->decl[i].byte_count);
   b->staging_bytes = max_weight;
   if (hipEventCreate(&b->ev_begin) != hipSuccess || hipEventCreate(&b->ev_end) != hipSuccess) return false;
+  if (b->program != kProgProof)
+    for (hipEvent_t& e : b->stage_ev)
+      if (hipEventCreate(&e) != hipSuccess) return false;
   if (b->program == kProgProof) {
     const bool ok = alloc_dev(b, reinterpret_cast<void**>(&b->proof_in), b->ext_in) &&
                     alloc_dev(b, reinterpret_cast<void**>(&b->proof_out), b->ext_out) &&
@@ -2291,14 +2369,18 @@ PROM_REACTOR_API int prometheus_reactor_runtime_main_transformer_execute(
     b->audit_valid = false;
     const uint64_t t0 = wall_ns();
     hipStream_t st = ctx().stream;
-    hipError_t e = hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st);
+    hipError_t e = begin_stage_timing(b, st);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) e = launch_widen_bf16(b->cond_bf16, b->cond, kZImageConditionWidth, st);
     b->last_memcpy_ns = wall_ns() - t0;
-    int32_t d = e == hipSuccess ? run_block(rt, b, s->buf[2], b->out) : PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
-    if (d == 0 && chain &&
-        (hipMemcpyAsync(s->buf[2], b->out, (size_t)kStreamBytes[2], hipMemcpyDeviceToDevice, st) != hipSuccess ||
-         hipStreamSynchronize(st) != hipSuccess))
+    int32_t d = e == hipSuccess ? run_block(rt, b, s->buf[2], b->out, 1, 3, b->stage_ev + 1)
+                                : PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
+    if (d == 0 && ((chain && hipMemcpyAsync(s->buf[2], b->out, (size_t)kStreamBytes[2], hipMemcpyDeviceToDevice,
+                                            st) != hipSuccess) ||
+                   hipEventRecord(b->stage_ev[15], st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess))
       d = PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
+    if (d == 0) resolve_stage_timing(b);
     if (d != 0) {
       if (chain) {  // PromSessionEndJoint(commit = false)
         s->joint_writing = false;

@@ -173,9 +173,14 @@ hipError_t launch_zimage_rope_table(const float* coords, float2* tab, int T, hip
 // Q/K/V split (pre-attention), 2 attention to the gated residual and FFN
 // input, 3 the FFN and final residual.  A later phase reads the workspace the
 // earlier ones left, so 2..2 re-runs the attention of the last phase 1.
+// stage_events (null: none; else 14 events) are recorded before the first of
+// the 13 stages (adaLN, norm, QKV, head norm + RoPE, scores, softmax, P.V,
+// projection, gated residual + FFN norm, W1|W3, SwiGLU, W2, final residual)
+// and after each one.
 hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x, const float* cond, float* out,
                                     char* ws, const size_t off[kZCount], int T, int D, int F, float eps,
-                                    hipStream_t st, uint32_t* launches, int first_phase, int last_phase);
+                                    hipStream_t st, uint32_t* launches, int first_phase, int last_phase,
+                                    const hipEvent_t* stage_events = nullptr);
 // Audit recomputations: out = RMSNorm(x; w) (no modulation), and q or k
 // (which 0 / 1) after the head RMSNorm and optionally RoPE, [T, H*128].
 hipError_t launch_zimage_norm(const float* x, const float* w, float* out, int T, int D, float eps, hipStream_t stream);

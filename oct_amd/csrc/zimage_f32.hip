@@ -407,7 +407,8 @@ hipError_t launch_zimage_attention_witness(const float* Q, const float* Kt, cons
 
 hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x, const float* cond, float* out,
                                     char* ws, const size_t off[kZCount], int T, int D, int F, float eps,
-                                    hipStream_t st, uint32_t* launches, int first_phase, int last_phase) {
+                                    hipStream_t st, uint32_t* launches, int first_phase, int last_phase,
+                                    const hipEvent_t* stage_events) {
   const int H = D / kHead;
   float* raw = reinterpret_cast<float*>(ws + off[kZModRaw]);
   float* mod = reinterpret_cast<float*>(ws + off[kZMod]);
@@ -438,40 +439,56 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
     if (e != hipSuccess) return e; \
     ++n;                           \
   } while (0)
+  // stage_events[0] before the first stage, stage_events[i] after stage i (1..13)
+  auto mark = [&](int i) { return stage_events ? hipEventRecord(stage_events[i], st) : hipSuccess; };
   const dim3 row_grid((T + 3) / 4), blk(256);
   if (first_phase > last_phase || first_phase < 1 || last_phase > 3) return hipErrorInvalidValue;
   if (launches) *launches = 0;
   if (first_phase == 1) {  // adaLN, attention norm, QKV, head norms and RoPE
+    if ((e = mark(0)) != hipSuccess) return e;
     if (modulated) {
       hipLaunchKernelGGL(adaln_f32_kernel, dim3((4 * D + 63) / 64), blk, 0, st, cond, w.adaln_w, w.adaln_b, raw, mod,
                          kZImageConditionWidth, D);
       PROM_STEP(hipGetLastError());
     }
+    if ((e = mark(1)) != hipSuccess) return e;
     hipLaunchKernelGGL(rows::norm_mod_kernel<float>, row_grid, blk, 0, st, x, w.attn_norm1, scaleA, A, T, D, eps);
     PROM_STEP(hipGetLastError());
+    if ((e = mark(2)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(A, D, w.w_qkv, 3 * D, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
+    if ((e = mark(3)) != hipSuccess) return e;
     hipLaunchKernelGGL(qkv_split_kernel, dim3((T + kSplitTokens - 1) / kSplitTokens, H), blk, 0, st, qkv, rope,
                        w.q_norm, w.k_norm, Q, Kt, V, T, H, eps, 1.0f / sqrtf((float)kHead));
     PROM_STEP(hipGetLastError());
+    if ((e = mark(4)) != hipSuccess) return e;
   }
   if (first_phase <= 2 && last_phase >= 2) {  // attention, projection, gated residual, FFN norm
     PROM_STEP(launch_sgemm_f32_batched(Q, kHead, (long long)T * kHead, Kt, T, (long long)kHead * T, S, T,
                                        (long long)T * T, T, T, kHead, H, st));
+    if ((e = mark(5)) != hipSuccess) return e;
     PROM_STEP(launch_row_reduction(S, S, (uint32_t)(H * T), (uint32_t)T, 3u, st));
+    if ((e = mark(6)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_batched(S, T, (long long)T * T, V, kHead, (long long)T * kHead, O, D, kHead, T, kHead,
                                        T, H, st));
+    if ((e = mark(7)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(O, D, w.w_out, D, proj, D, T, D, D, nullptr, 0, st, nullptr));
+    if ((e = mark(8)) != hipSuccess) return e;
     hipLaunchKernelGGL(rows::resid_norm_mod_kernel<float>, row_grid, blk, 0, st, x, proj, w.attn_norm2, gateA,
                        w.ffn_norm1, scaleM, R, Fm, T, D, eps);
     PROM_STEP(hipGetLastError());
+    if ((e = mark(9)) != hipSuccess) return e;
   }
   if (last_phase == 3) {  // W1/W3, SwiGLU, W2, gated final residual
     PROM_STEP(launch_sgemm_f32_ex(Fm, D, w.w_13, 2 * F, G, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
+    if ((e = mark(10)) != hipSuccess) return e;
     hipLaunchKernelGGL(swiglu_f32_kernel, dim3(grid_for((size_t)T * F)), blk, 0, st, G, Hd, T, F);
     PROM_STEP(hipGetLastError());
+    if ((e = mark(11)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(Hd, F, w.w_2, D, W2, D, T, D, F, nullptr, 0, st, nullptr));
+    if ((e = mark(12)) != hipSuccess) return e;
     hipLaunchKernelGGL(rows::final_resid_kernel, row_grid, blk, 0, st, R, W2, w.ffn_norm2, gateM, out, T, D, eps);
     PROM_STEP(hipGetLastError());
+    if ((e = mark(13)) != hipSuccess) return e;
   }
 #undef PROM_STEP
   if (launches) *launches = n;

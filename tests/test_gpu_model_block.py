@@ -280,6 +280,25 @@ def test_context_refiner_chain(model, weights, inputs):
 
 
 # ------------------------------------------------------------ session and MainTransformer
+def check_stage_timing(ev):
+    """The 13 per-stage GPU timings of a MainTransformer execution tile its
+    compute interval (reactor_vulkan_model_block.c:3545-3562): stage s runs
+    from boundary s+1 to s+2, ingress precedes the compute, the joint copy
+    follows it."""
+    ns = list(ev.main_stage_gpu_ns)
+    begin, end = list(ev.main_stage_gpu_begin_tick), list(ev.main_stage_gpu_end_tick)
+    assert all(n > 0 for n in ns), ns
+    assert [e - b for b, e in zip(begin, end)] == ns
+    assert begin[1:] == end[:-1]
+    assert begin[0] == ev.gpu_compute_begin_tick and end[-1] == ev.gpu_compute_end_tick
+    assert sum(ns) == ev.gpu_compute_ns
+    assert ev.gpu_total_begin_tick > 0
+    assert ev.gpu_total_begin_tick + ev.gpu_ingress_transfer_ns == ev.gpu_compute_begin_tick
+    assert ev.gpu_compute_end_tick + ev.gpu_joint_copy_ns == ev.gpu_total_end_tick
+    assert ev.gpu_total_ns == ev.gpu_total_end_tick - ev.gpu_total_begin_tick
+    print("main stages (us): " + " ".join(f"{n / 1e3:.1f}" for n in ns), flush=True)
+
+
 def test_session_main_transformer_chain(model, weights, inputs):
     x_bits, t_bits, ctx = inputs
     cond = oracle.from_bf16(t_bits).astype(np.float64)
@@ -331,6 +350,8 @@ def test_session_main_transformer_chain(model, weights, inputs):
     rc, ev = model.main_transformer_execute(mid, sid, 0, t_bits, 1, 1, 1, chain=False)
     assert rc == p.PROM_OK and ev.output_generation == 1
     print(f"main transformer layer 0: gpu {ev.gpu_compute_ns / 1e6:.3f} ms", flush=True)
+    check_stage_timing(ev)
+    first_end = ev.gpu_total_end_tick
     assert model.session_evidence(sid)[1].joint_generation == 1  # audit mode leaves the joint alone
     out = np.zeros(T_JOINT * W, np.float32)
     assert model.audit_final("main", mid, 1, out)[0] == p.PROM_OK
@@ -360,6 +381,8 @@ def test_session_main_transformer_chain(model, weights, inputs):
     # chain mode writes the output back into JointWorking (generation 2)
     rc, ev = model.main_transformer_execute(mid, sid, 0, t_bits, 1, 1, 1, chain=True)
     assert rc == p.PROM_OK and ev.output_generation == 3
+    check_stage_timing(ev)
+    assert ev.gpu_total_begin_tick > first_end and ev.gpu_joint_copy_ns > 0
     sev = model.session_evidence(sid)[1]
     assert sev.joint_generation == 2 and sev.active_block_id == mid
     chained = np.zeros(T_JOINT * W, np.float32)
