@@ -758,14 +758,33 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
     if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_GEMV_F32;
     return hipGetLastError();
   }
-  SgemmPlan p = plan_sgemm(a, lda, 0, b, ldb, 0, m, n, k, 1);
-  float* partial = nullptr;
-  if (p.splits > 1) {
-    partial = static_cast<float*>(staging(6, (size_t)p.splits * m * n * sizeof(float)));
-    if (partial == nullptr) p = make_plan(p.tile, 1, k);
-  }
   if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_F32;
-  return run_sgemm_plan(p, a, lda, 0, b, ldb, 0, c, ldc, 0, m, n, k, 1, residual, ldr, partial, stream);
+  auto run = [&](SgemmPlan p, const float* ap, float* cp, const float* rp, uint32_t rows) {
+    float* partial = nullptr;
+    if (p.splits > 1) {
+      partial = static_cast<float*>(staging(6, (size_t)p.splits * rows * n * sizeof(float)));
+      if (partial == nullptr) p = make_plan(p.tile, 1, k);
+    }
+    return run_sgemm_plan(p, ap, lda, 0, b, ldb, 0, cp, ldc, 0, rows, n, k, 1, rp, ldr, partial, stream);
+  };
+  const SgemmPlan p = plan_sgemm(a, lda, 0, b, ldb, 0, m, n, k, 1);
+  // A partial last row of 128-row tiles runs nearly empty for the whole K depth
+  // (M = 1056: a 32-row tail in 9 tile rows).  When the estimate favours it, the
+  // rows past the last full tile row run as a second product (usually K-split)
+  // after the rest, on the same stream.
+  const uint32_t tail = m % 128u;
+  if (tail != 0 && m > 128u) {
+    const uint32_t head = m - tail;
+    const float* at = a + (size_t)head * lda;
+    const SgemmPlan ph = plan_sgemm(a, lda, 0, b, ldb, 0, head, n, k, 1);
+    const SgemmPlan pt = plan_sgemm(at, lda, 0, b, ldb, 0, tail, n, k, 1);
+    if (plan_cost(ph, head, n, 1) + plan_cost(pt, tail, n, 1) < plan_cost(p, m, n, 1)) {
+      const hipError_t e = run(ph, a, c, residual, head);
+      if (e != hipSuccess) return e;
+      return run(pt, at, c + (size_t)head * ldc, residual ? residual + (size_t)head * ldr : nullptr, tail);
+    }
+  }
+  return run(p, a, c, residual, m);
 }
 
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
