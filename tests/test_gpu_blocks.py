@@ -43,6 +43,19 @@ def test_decoder_layer_c4_gemma2b(gpu_runtime):
     np.testing.assert_array_equal(out2[:T // 2], out[:T // 2])
 
 
+def test_decoder_layer_tail_rows(gpu_runtime):
+    """Gemma-2B widths at T = 1056: the output projection and the down
+    projection (both adding the residual) run their last 32 rows as a second,
+    K-split product."""
+    T, D, Hq, d, F = 1056, 2048, 8, 256, 16384
+    x, w = blocks.make_decoder_layer(77, T, D, Hq, d, F)
+    rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
+    assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)
+    ref = blocks.decoder_layer_f32(x, w, Hq, d)
+    assert oracle.normwise_rel_err(out, ref) <= F32_BLOCK
+    assert oracle.normwise_rel_err(out[1024:], ref[1024:]) <= F32_BLOCK
+
+
 def test_decoder_layer_position_offset(gpu_runtime):
     T, D, Hq, d, F = 16, 128, 2, 64, 256
     x, w = blocks.make_decoder_layer(8, T, D, Hq, d, F)

@@ -84,6 +84,19 @@ def test_plan_variants(gpu_runtime, m, n, k):
         assert oracle.normwise_rel_err(out[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r]) <= FP32_NORMWISE
 
 
+# M past a multiple of 128 where the plan model runs the last rows as a second,
+# K-split product after the full 128-row tiles: the rows either side of the
+# seam and the last row.
+@pytest.mark.parametrize("m,n,k", [(1056, 3840, 3840), (2049, 8192, 2048), (1056, 20480, 3840)])
+def test_tail_row_split(gpu_runtime, m, n, k):
+    a = oracle.uniform(500 + m, (m, k))
+    b = oracle.uniform(600 + n, (k, n))
+    out = _sgemm(gpu_runtime, a, b)
+    head = m - m % 128
+    for r in (0, head - 1, head, m - 1):
+        assert oracle.normwise_rel_err(out[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r]) <= FP32_NORMWISE, r
+
+
 def test_c1_1024_full(gpu_runtime):
     # M=N=K=1024, U[-1,1] seeded
     a = oracle.uniform(1, (1024, 1024))
