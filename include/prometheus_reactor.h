@@ -510,6 +510,12 @@ PROM_REACTOR_API int prometheus_reactor_runtime_destroy(void* handle);
 /* reactor_api.h:2560 -- available=1, backend 2 on a HIP device; else
    available=0, backend UNKNOWN, reason VULKAN_UNAVAILABLE (no device). */
 PROM_REACTOR_API int prometheus_reactor_runtime_probe(void* handle, PrometheusCaps* out_caps);
+/* reactor_api.h:2822-2825; reactor_api.c:801-812 -- backward-compatible
+   aliases of create / destroy / probe from the reference's earlier contract
+   drafts; each behaves exactly as the entry it names. */
+PROM_REACTOR_API int prometheus_runtime_create(void* config, void** out_handle);
+PROM_REACTOR_API int prometheus_runtime_destroy(void* handle);
+PROM_REACTOR_API int prometheus_runtime_probe(void* handle, PrometheusCaps* out_caps);
 /* reactor_api.h:2561-2562 */
 PROM_REACTOR_API int prometheus_reactor_runtime_vulkan_device_diagnostics(void* handle,
                                                                            PrometheusVulkanDeviceDiagnostics* out_diag);
@@ -615,6 +621,35 @@ PROM_REACTOR_API int prometheus_reactor_runtime_event_elapsed_ms(void* handle, u
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device(void* handle, const float* a, const float* b, float* c,
                                                              uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
                                                              int* out_detail_code);
+/* The SGEMM launch plan that ..._sgemm and ..._sgemm_device queue for a
+   contiguous row-major product with 16-byte-aligned operands.  It is a pure
+   function of the shape and needs neither a runtime nor a device.  The
+   reference reports its own choice (occupancy variant, geometry) through its
+   judgment engine, reactor_judgment_engine.c:895-948.
+   Admission is the device entries' rule: any dimension above 2^31 - 1, or
+   m*k, k*n or m*n at or above 2^32, returns PROM_ERROR with detail_code
+   PROM_DETAIL_SIZE_OVERFLOW; a zero dimension returns PROM_ERROR with detail
+   PROM_ERROR.  On success detail_code is the path detail the device entry
+   reports (PROM_DETAIL_PATH_HIP_MFMA_F32 or _GEMV_F32).  products is 0 for
+   the GEMV, else 1, or 2 when the rows past the last full 128-row tile row
+   (rows head_rows..m-1) run as a second product. */
+typedef struct PrometheusSgemmPlanInfo {
+  uint32_t struct_size;
+  int32_t detail_code;
+  uint32_t products;
+  uint32_t head_rows;
+  uint32_t tile_m[2];       /* macro tile of each product */
+  uint32_t tile_n[2];
+  uint32_t direct_to_lds[2]; /* 1: tiles go HBM -> LDS by buffer_load ... lds */
+  uint32_t k_slices[2];     /* split-K slices (1: no split) */
+  uint32_t k_slice_len[2];
+  uint32_t launches;        /* kernel launches queued (GEMM plus split-K reduce) */
+  uint32_t reserved;
+  uint64_t partial_bytes;   /* split-K partial buffer the plan writes */
+  double estimated_us;      /* the plan model's estimate */
+} PrometheusSgemmPlanInfo;
+PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32_t n, uint32_t k,
+                                                   PrometheusSgemmPlanInfo* out_plan);
 PROM_REACTOR_API int prometheus_reactor_runtime_gemm_bf16_device(void* handle, const uint16_t* a, const uint16_t* b,
                                                                  float* c, uint32_t m, uint32_t n, uint32_t k,
                                                                  uint32_t* out_stage, int* out_detail_code);

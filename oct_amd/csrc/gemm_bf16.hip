@@ -613,8 +613,8 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
   // range-checked: out-of-range rows read zero).  The compiler then does not
   // track them as LDS stores, so it adds no conservative vmcnt(0) before the
   // LDS reads of the other stages; the explicit vmcnt waits and barriers of the
-  // K loop order every transfer before the reads of its tile.  Nothing else in
-  // this kernel uses M0.
+  // K loop order every transfer before the reads of its tile.  M0 is declared
+  // clobbered, so the compiler keeps no live value in it across a transfer.
   typedef int int4v __attribute__((ext_vector_type(4)));
   auto desc = [](const void* p, uint32_t bytes) {
     const unsigned long long a = (unsigned long long)p;
@@ -638,10 +638,10 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
       const uint32_t lb = __builtin_amdgcn_readfirstlane(base + 16384 + q * 1024);
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(la), "v"(a_off[i]), "s"(da),
                    "s"(sa)
-                   : "memory");
+                   : "memory", "m0");
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lb), "v"(b_off[i]), "s"(db),
                    "s"(sb)
-                   : "memory");
+                   : "memory", "m0");
     }
   };
 

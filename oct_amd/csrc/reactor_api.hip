@@ -18,11 +18,6 @@ namespace {
 
 // ------------------------------------------------------------------ GEMM
 
-bool gemm_shape_fits(uint32_t m, uint32_t n, uint32_t k) {
-  const uint64_t lim = 1ull << 32;
-  return (uint64_t)m * k < lim && (uint64_t)k * n < lim && (uint64_t)m * n < lim;
-}
-
 // Common validation of reactor_sgemm.cpp:4152-4191; returns PROM_OK to proceed.
 int gemm_validate(Runtime* rt, const void* a, const void* b, const void* c, uint32_t m, uint32_t n, uint32_t k,
                   uint32_t* out_stage, int* out_detail) {

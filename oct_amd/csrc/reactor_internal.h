@@ -79,6 +79,17 @@ void async_release(Runtime* rt);
 // Frees the runtime's resident model block, session and their device memory.
 void model_release(Runtime* rt);
 
+// GEMM admission: every dimension fits the kernels' signed 32-bit index type
+// and each operand holds fewer than 2^32 elements.  The reference refuses
+// m*n*k >= 2^32 (reactor_sgemm.cpp:4186-4191), which excludes 4096^3; this
+// limit admits it and still rejects any shape whose leading dimension or
+// tile count would wrap an int.
+inline bool gemm_shape_fits(uint32_t m, uint32_t n, uint32_t k) {
+  const uint64_t lim = 1ull << 32;
+  if (m > 0x7fffffffu || n > 0x7fffffffu || k > 0x7fffffffu) return false;
+  return (uint64_t)m * k < lim && (uint64_t)k * n < lim && (uint64_t)m * n < lim;
+}
+
 inline void set_status(uint32_t* stage, int* detail, uint32_t s, int d) {
   if (stage) *stage = s;
   if (detail) *detail = d;

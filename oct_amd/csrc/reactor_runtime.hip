@@ -176,6 +176,17 @@ PROM_REACTOR_API int prometheus_reactor_runtime_probe(void* handle, PrometheusCa
   return PROM_OK;
 }
 
+// reactor_api.c:801-812: the earlier contract drafts' names forward unchanged.
+PROM_REACTOR_API int prometheus_runtime_create(void* config, void** out_handle) {
+  return prometheus_reactor_runtime_create(config, out_handle);
+}
+
+PROM_REACTOR_API int prometheus_runtime_destroy(void* handle) { return prometheus_reactor_runtime_destroy(handle); }
+
+PROM_REACTOR_API int prometheus_runtime_probe(void* handle, PrometheusCaps* out_caps) {
+  return prometheus_reactor_runtime_probe(handle, out_caps);
+}
+
 PROM_REACTOR_API int prometheus_reactor_runtime_vulkan_device_diagnostics(void* handle,
                                                                            PrometheusVulkanDeviceDiagnostics* out_diag) {
   Runtime* rt = lookup(handle);

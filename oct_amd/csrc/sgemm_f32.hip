@@ -24,6 +24,7 @@
 //     compact block of A rows and B columns.
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 
 #include "reactor_internal.h"
 
@@ -608,10 +609,11 @@ SgemmPlan make_plan(int tile, int splits, uint32_t k) {
 // True when the buffer-load kernels apply: 128-bit aligned operands, every
 // slice length a multiple of the K tile and every 32-bit byte offset (rows up
 // to M + 128, all of B plus a tile row) in range.
-bool buffer_path(const float* a, int lda, long long sa, const float* b, int ldb, long long sb, uint32_t m,
-                 uint32_t n, uint32_t k, int k_len) {
+// `aligned`: both operand base addresses are 16-byte aligned.
+bool buffer_path(bool aligned, int lda, long long sa, int ldb, long long sb, uint32_t m, uint32_t n, uint32_t k,
+                 int k_len) {
   const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
-                   (sb % 4 == 0) && aligned16(a) && aligned16(b);
+                   (sb % 4 == 0) && aligned;
   return vec && (k % kBK == 0) && (k_len % kBK == 0) && (size_t)(m + 128) * lda * 4 < (1ull << 31) &&
          ((size_t)k * ldb + n + 256) * 4 < (1ull << 31);
 }
@@ -649,8 +651,10 @@ double plan_cost(const SgemmPlan& p, uint32_t m, uint32_t n, uint32_t batch) {
   return us;
 }
 
-SgemmPlan plan_sgemm(const float* a, int lda, long long sa, const float* b, int ldb, long long sb, uint32_t m,
-                     uint32_t n, uint32_t k, uint32_t batch) {
+// max_partial_floats bounds the split-K partial buffer (splits * m * n floats)
+// a plan may use; a plan without a split needs none, so one always exists.
+SgemmPlan plan_sgemm(bool aligned, int lda, long long sa, int ldb, long long sb, uint32_t m, uint32_t n, uint32_t k,
+                     uint32_t batch, uint64_t max_partial_floats = ~0ull) {
   static const int kSplitChoices[] = {1, 2, 3, 4, 6, 8, 12, 16};
   SgemmPlan best = make_plan(0, 1, k);
   double best_cost = 1e300;
@@ -659,7 +663,8 @@ SgemmPlan plan_sgemm(const float* a, int lda, long long sa, const float* b, int 
       if (s > 1 && (batch > 1 || k / (uint32_t)s < 64)) break;
       const SgemmPlan p = make_plan(t, s, k);
       if (p.splits != s) continue;
-      if (t >= 3 && !buffer_path(a, lda, sa, b, ldb, sb, m, n, k, p.k_len)) continue;
+      if (p.splits > 1 && (uint64_t)p.splits * m * n > max_partial_floats) continue;
+      if (t >= 3 && !buffer_path(aligned, lda, sa, ldb, sb, m, n, k, p.k_len)) continue;
       const double c = plan_cost(p, m, n, batch);
       if (c < best_cost) {
         best_cost = c;
@@ -693,7 +698,7 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
   const bool split = p.splits > 1;
   const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
                    (sb % 4 == 0) && aligned16(a) && aligned16(b);
-  const bool buf = buffer_path(a, lda, sa, b, ldb, sb, m, n, k, p.k_len);
+  const bool buf = buffer_path(aligned16(a) && aligned16(b), lda, sa, ldb, sb, m, n, k, p.k_len);
   const int tile = (p.tile >= 3 && !buf) ? kStagedFallback[p.tile] : p.tile;
   const int bm = kTileM[tile], bn = kTileN[tile];
   const int tiles_m = (int)((m + bm - 1) / bm);
@@ -743,48 +748,98 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
   return hipGetLastError();
 }
 
-}  // namespace
+// What launch_sgemm_f32_ex queues for one product: the GEMV, or one or two
+// MFMA products (rows [0, head_rows) and, after a tail split, the rest).  A
+// pure function of the shape, strides and operand alignment.
+struct SgemmSchedule {
+  bool gemv;
+  bool tail_split;
+  uint32_t head_rows;  // rows of the first product (m without a tail split)
+  SgemmPlan plan[2];
+  double cost_us;      // plan-model estimate of the queued work
+};
 
-hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
-                               uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
-                               int* path_detail) {
-  if (n == 1 && residual == nullptr && ldb == 1 && lda == (int)k) {
+SgemmSchedule schedule_sgemm(bool aligned, int lda, int ldb, uint32_t m, uint32_t n, uint32_t k, bool has_residual,
+                             uint64_t max_partial_floats) {
+  SgemmSchedule s{};
+  s.head_rows = m;
+  if (n == 1 && !has_residual && ldb == 1 && lda == (int)k) {
+    s.gemv = true;
+    return s;
+  }
+  s.plan[0] = plan_sgemm(aligned, lda, 0, ldb, 0, m, n, k, 1, max_partial_floats);
+  s.cost_us = plan_cost(s.plan[0], m, n, 1);
+  // A partial last row of 128-row tiles runs nearly empty for the whole K depth
+  // (M = 1056: a 32-row tail in 9 tile rows).  When the estimate favours it, the
+  // rows past the last full tile row run as a second product (usually K-split)
+  // after the rest, on the same stream.  The tail starts 128 rows in, so its A
+  // keeps the alignment of a when lda is a multiple of 4.
+  const uint32_t tail = m % 128u;
+  if (tail != 0 && m > 128u) {
+    const uint32_t head = m - tail;
+    const bool tail_aligned = aligned && (lda % 4 == 0);
+    const SgemmPlan ph = plan_sgemm(aligned, lda, 0, ldb, 0, head, n, k, 1, max_partial_floats);
+    const SgemmPlan pt = plan_sgemm(tail_aligned, lda, 0, ldb, 0, tail, n, k, 1, max_partial_floats);
+    const double split_cost = plan_cost(ph, head, n, 1) + plan_cost(pt, tail, n, 1);
+    if (split_cost < s.cost_us) {
+      s.tail_split = true;
+      s.head_rows = head;
+      s.plan[0] = ph;
+      s.plan[1] = pt;
+      s.cost_us = split_cost;
+    }
+  }
+  return s;
+}
+
+// Queues schedule s; partial (null: runtime staging slot 6) receives the
+// split-K slices and must hold partial_floats.
+hipError_t run_sgemm_schedule(const SgemmSchedule& s, const float* a, int lda, const float* b, int ldb, float* c,
+                              int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
+                              float* partial, hipStream_t stream) {
+  if (s.gemv) {
     const bool vec = (k % 4 == 0) && aligned16(a) && aligned16(b);
     const dim3 grid((m + 3) / 4);
     if (vec)
       hipLaunchKernelGGL(gemv_f32_kernel<true>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)k);
     else
       hipLaunchKernelGGL(gemv_f32_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)k);
-    if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_GEMV_F32;
     return hipGetLastError();
   }
-  if (path_detail) *path_detail = PROM_DETAIL_PATH_HIP_MFMA_F32;
   auto run = [&](SgemmPlan p, const float* ap, float* cp, const float* rp, uint32_t rows) {
-    float* partial = nullptr;
+    float* part = nullptr;
     if (p.splits > 1) {
-      partial = static_cast<float*>(staging(6, (size_t)p.splits * rows * n * sizeof(float)));
-      if (partial == nullptr) p = make_plan(p.tile, 1, k);
+      part = partial != nullptr ? partial
+                                : static_cast<float*>(staging(6, (size_t)p.splits * rows * n * sizeof(float)));
+      if (part == nullptr) p = make_plan(p.tile, 1, k);
     }
-    return run_sgemm_plan(p, ap, lda, 0, b, ldb, 0, cp, ldc, 0, rows, n, k, 1, rp, ldr, partial, stream);
+    return run_sgemm_plan(p, ap, lda, 0, b, ldb, 0, cp, ldc, 0, rows, n, k, 1, rp, ldr, part, stream);
   };
-  const SgemmPlan p = plan_sgemm(a, lda, 0, b, ldb, 0, m, n, k, 1);
-  // A partial last row of 128-row tiles runs nearly empty for the whole K depth
-  // (M = 1056: a 32-row tail in 9 tile rows).  When the estimate favours it, the
-  // rows past the last full tile row run as a second product (usually K-split)
-  // after the rest, on the same stream.
-  const uint32_t tail = m % 128u;
-  if (tail != 0 && m > 128u) {
-    const uint32_t head = m - tail;
-    const float* at = a + (size_t)head * lda;
-    const SgemmPlan ph = plan_sgemm(a, lda, 0, b, ldb, 0, head, n, k, 1);
-    const SgemmPlan pt = plan_sgemm(at, lda, 0, b, ldb, 0, tail, n, k, 1);
-    if (plan_cost(ph, head, n, 1) + plan_cost(pt, tail, n, 1) < plan_cost(p, m, n, 1)) {
-      const hipError_t e = run(ph, a, c, residual, head);
-      if (e != hipSuccess) return e;
-      return run(pt, at, c + (size_t)head * ldc, residual ? residual + (size_t)head * ldr : nullptr, tail);
-    }
-  }
-  return run(p, a, c, residual, m);
+  if (!s.tail_split) return run(s.plan[0], a, c, residual, m);
+  const uint32_t head = s.head_rows;
+  const hipError_t e = run(s.plan[0], a, c, residual, head);
+  if (e != hipSuccess) return e;
+  return run(s.plan[1], a + (size_t)head * lda, c + (size_t)head * ldc,
+             residual ? residual + (size_t)head * ldr : nullptr, m - head);
+}
+
+uint64_t schedule_partial_floats(const SgemmSchedule& s, uint32_t m, uint32_t n) {
+  if (s.gemv) return 0;
+  uint64_t need = s.plan[0].splits > 1 ? (uint64_t)s.plan[0].splits * s.head_rows * n : 0;
+  if (s.tail_split && s.plan[1].splits > 1)
+    need = std::max<uint64_t>(need, (uint64_t)s.plan[1].splits * (m - s.head_rows) * n);
+  return need;
+}
+
+}  // namespace
+
+hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
+                               uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
+                               int* path_detail) {
+  const SgemmSchedule s =
+      schedule_sgemm(aligned16(a) && aligned16(b), lda, ldb, m, n, k, residual != nullptr, ~0ull);
+  if (path_detail) *path_detail = s.gemv ? PROM_DETAIL_PATH_HIP_GEMV_F32 : PROM_DETAIL_PATH_HIP_MFMA_F32;
+  return run_sgemm_schedule(s, a, lda, b, ldb, c, ldc, m, n, k, residual, ldr, nullptr, stream);
 }
 
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
@@ -792,8 +847,8 @@ hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const
                                     uint32_t batch, hipStream_t stream) {
   if (batch == 0 || m == 0 || n == 0) return hipSuccess;
   if (batch == 1) return launch_sgemm_f32_ex(a, lda, b, ldb, c, ldc, m, n, k, nullptr, 0, stream, nullptr);
-  return run_sgemm_plan(plan_sgemm(a, lda, sa, b, ldb, sb, m, n, k, batch), a, lda, sa, b, ldb, sb, c, ldc, sc, m, n, k,
-                        batch, nullptr, 0, nullptr, stream);
+  return run_sgemm_plan(plan_sgemm(aligned16(a) && aligned16(b), lda, sa, ldb, sb, m, n, k, batch), a, lda, sa, b, ldb,
+                        sb, c, ldc, sc, m, n, k, batch, nullptr, 0, nullptr, stream);
 }
 
 hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
@@ -802,3 +857,45 @@ hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m
 }
 
 }  // namespace prom
+
+using namespace prom;
+
+extern "C" PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32_t n, uint32_t k,
+                                                              PrometheusSgemmPlanInfo* out_plan) {
+  if (out_plan == nullptr || out_plan->struct_size < sizeof(PrometheusSgemmPlanInfo)) return PROM_ERROR;
+  const uint32_t size = out_plan->struct_size;
+  memset(out_plan, 0, sizeof(*out_plan));
+  out_plan->struct_size = size;
+  if (m == 0u || n == 0u || k == 0u) {
+    out_plan->detail_code = PROM_ERROR;
+    return PROM_ERROR;
+  }
+  if (!gemm_shape_fits(m, n, k)) {
+    out_plan->detail_code = PROM_DETAIL_SIZE_OVERFLOW;
+    return PROM_ERROR;
+  }
+  const SgemmSchedule s = schedule_sgemm(true, (int)k, (int)n, m, n, k, false, ~0ull);
+  out_plan->head_rows = s.head_rows;
+  if (s.gemv) {
+    out_plan->detail_code = PROM_DETAIL_PATH_HIP_GEMV_F32;
+    out_plan->launches = 1;
+    return PROM_OK;
+  }
+  out_plan->detail_code = PROM_DETAIL_PATH_HIP_MFMA_F32;
+  out_plan->products = s.tail_split ? 2u : 1u;
+  for (uint32_t i = 0; i < out_plan->products; ++i) {
+    const SgemmPlan& p = s.plan[i];
+    const uint32_t rows = i == 0 ? s.head_rows : m - s.head_rows;
+    const bool buf = buffer_path(true, (int)k, 0, (int)n, 0, rows, n, k, p.k_len);
+    const int tile = (p.tile >= 3 && !buf) ? kStagedFallback[p.tile] : p.tile;
+    out_plan->tile_m[i] = (uint32_t)kTileM[tile];
+    out_plan->tile_n[i] = (uint32_t)kTileN[tile];
+    out_plan->direct_to_lds[i] = tile >= 3 ? 1u : 0u;
+    out_plan->k_slices[i] = (uint32_t)p.splits;
+    out_plan->k_slice_len[i] = (uint32_t)p.k_len;
+    out_plan->launches += p.splits > 1 ? 2u : 1u;
+  }
+  out_plan->partial_bytes = schedule_partial_floats(s, m, n) * sizeof(float);
+  out_plan->estimated_us = s.cost_us;
+  return PROM_OK;
+}

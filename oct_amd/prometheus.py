@@ -127,6 +127,24 @@ class PrometheusVulkanDeviceDiagnostics(Structure):
     ]
 
 
+class PrometheusSgemmPlanInfo(Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("detail_code", ctypes.c_int32),
+        ("products", c_uint32),
+        ("head_rows", c_uint32),
+        ("tile_m", c_uint32 * 2),
+        ("tile_n", c_uint32 * 2),
+        ("direct_to_lds", c_uint32 * 2),
+        ("k_slices", c_uint32 * 2),
+        ("k_slice_len", c_uint32 * 2),
+        ("launches", c_uint32),
+        ("reserved", c_uint32),
+        ("partial_bytes", c_uint64),
+        ("estimated_us", ctypes.c_double),
+    ]
+
+
 class PrometheusHipDeviceDiagnostics(Structure):
     _fields_ = [
         ("struct_size", c_uint32),
@@ -835,6 +853,10 @@ _SIGNATURES = {
     "prometheus_reactor_runtime_create": (c_int, [c_void_p, POINTER(c_void_p)]),
     "prometheus_reactor_runtime_destroy": (c_int, [c_void_p]),
     "prometheus_reactor_runtime_probe": (c_int, [c_void_p, POINTER(PrometheusCaps)]),
+    "prometheus_runtime_create": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "prometheus_runtime_destroy": (c_int, [c_void_p]),
+    "prometheus_runtime_probe": (c_int, [c_void_p, POINTER(PrometheusCaps)]),
+    "prometheus_reactor_sgemm_plan": (c_int, [c_uint32, c_uint32, c_uint32, POINTER(PrometheusSgemmPlanInfo)]),
     "prometheus_reactor_runtime_vulkan_device_diagnostics": (c_int, [c_void_p, POINTER(PrometheusVulkanDeviceDiagnostics)]),
     "prometheus_reactor_runtime_hip_device_diagnostics": (c_int, [c_void_p, POINTER(PrometheusHipDeviceDiagnostics)]),
     "prometheus_reactor_runtime_sgemm": (
@@ -1045,12 +1067,11 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     last_err = None
     for cand in candidates:
         if not Path(cand).exists():
-            last_err = f"{cand} not found"
             continue
         try:
             lib = ctypes.CDLL(cand, mode=os.RTLD_NOW | os.RTLD_LOCAL)
         except OSError as exc:
-            last_err = str(exc)
+            last_err = ReactorIssue("reactor_load_failed", f"{cand}: {exc}")
             continue
         for name in MANDATORY_SYMBOLS:
             if not hasattr(lib, name):
@@ -1065,7 +1086,10 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
             raise ReactorIssue("abi_mismatch", f"expected ABI {REACTOR_EXPECTED_ABI_VERSION}, got {version}")
         lib._oct_path = cand  # type: ignore[attr-defined]
         return lib
-    raise ReactorIssue("library_unavailable", last_err or "no reactor candidates")
+    # bridge.go:262-267: a candidate that failed to load wins over "not found".
+    if last_err is not None:
+        raise last_err
+    raise ReactorIssue("reactor_not_found", "prometheus reactor not found")
 
 
 _SHARED_LIB: Optional[ctypes.CDLL] = None
@@ -1107,13 +1131,13 @@ class NativeRuntime:
         handle = c_void_p()
         rc = self.lib.prometheus_reactor_runtime_create(byref(cfg), byref(handle))
         if rc != PROM_OK or not handle.value:
-            raise ReactorIssue("create_failed", f"runtime_create returned {rc}")
+            raise ReactorIssue("runtime_create_failed", f"runtime_create returned {rc}")
         self.handle = handle
         caps = PrometheusCaps()
         rc = self.lib.prometheus_reactor_runtime_probe(self.handle, byref(caps))
         if rc != PROM_OK:
             self.close()
-            raise ReactorIssue("probe_failed", f"runtime_probe returned {rc}")
+            raise ReactorIssue("runtime_probe_unavailable", f"runtime_probe returned {rc}")
         self.caps = caps
 
     # -- lifecycle --------------------------------------------------------
@@ -1167,7 +1191,7 @@ class NativeRuntime:
         out, st, rc = self.sgemm_with_status(m, n, k, a, b)
         if rc != PROM_OK:
             status = RunStatus("error", stage_name(st.stage), st.detail)
-            raise ReactorIssue("sgemm_failed", f"native sgemm failed: {status}")
+            raise ReactorIssue("runtime_sgemm_failed", f"native sgemm failed: {status}")
         return out, RunStatus("ok")
 
     def gemm_bf16(self, m: int, n: int, k: int, a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
@@ -1515,6 +1539,15 @@ class NativeRuntime:
         if rc != PROM_OK:
             raise ReactorIssue("diagnostics_failed", f"batch_diagnostics returned {rc}")
         return d
+
+
+def sgemm_plan(m: int, n: int, k: int, lib: Optional[ctypes.CDLL] = None) -> Tuple[int, PrometheusSgemmPlanInfo]:
+    """The launch plan of a contiguous m x n x k SGEMM (no device needed): (rc, plan)."""
+    lib = lib or shared_library()
+    info = PrometheusSgemmPlanInfo()
+    info.struct_size = ctypes.sizeof(info)
+    rc = lib.prometheus_reactor_sgemm_plan(m, n, k, byref(info))
+    return rc, info
 
 
 # ---- the strict `@` path (strict.go:11-32, runtime.go:251-317) -------------

@@ -48,6 +48,9 @@ def test_decoder_layer_tail_rows(gpu_runtime):
     projection (both adding the residual) run their last 32 rows as a second,
     K-split product."""
     T, D, Hq, d, F = 1056, 2048, 8, 256, 16384
+    for m, n, k in ((T, D, Hq * d), (T, D, F)):
+        rc, plan = p.sgemm_plan(m, n, k)
+        assert rc == p.PROM_OK and plan.products == 2, "the tail split must be planned for this layer"
     x, w = blocks.make_decoder_layer(77, T, D, Hq, d, F)
     rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
     assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)

@@ -89,6 +89,8 @@ def test_plan_variants(gpu_runtime, m, n, k):
 # seam and the last row.
 @pytest.mark.parametrize("m,n,k", [(1056, 3840, 3840), (2049, 8192, 2048), (1056, 20480, 3840)])
 def test_tail_row_split(gpu_runtime, m, n, k):
+    rc, plan = p.sgemm_plan(m, n, k)
+    assert rc == p.PROM_OK and plan.products == 2 and plan.head_rows == m - m % 128, "the split must be planned"
     a = oracle.uniform(500 + m, (m, k))
     b = oracle.uniform(600 + n, (k, n))
     out = _sgemm(gpu_runtime, a, b)
@@ -248,3 +250,39 @@ def test_bf16_large_tile_kernel_ragged(gpu_runtime, m, n, k):
         ref_r = oracle.matmul_f64(a, b, rows=(r, r + 1))[r]
         # fp32 accumulation over k terms: absolute slack relative to the row's scale
         np.testing.assert_allclose(out[r], ref_r, rtol=1e-4, atol=2e-6 * np.abs(ref_r).max())
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 3_000_000_000), (1, 2**31, 1), (70000, 70000, 1)])
+def test_device_entry_rejects_oversized_shapes(gpu_runtime, m, n, k):
+    """Admission runs before any launch: no operand memory is touched."""
+    import ctypes
+
+    stage, detail = ctypes.c_uint32(0), ctypes.c_int(0)
+    dummy = gpu_runtime.alloc(256)
+    try:
+        rc = gpu_runtime.lib.prometheus_reactor_runtime_sgemm_device(gpu_runtime.handle, dummy, dummy, dummy, m, n, k,
+                                                                     ctypes.byref(stage), ctypes.byref(detail))
+    finally:
+        gpu_runtime.free(dummy)
+    assert rc == p.PROM_ERROR and stage.value == p.STAGE_TRANSFER_IN and detail.value == p.DETAIL_SIZE_OVERFLOW
+
+
+def test_nonstrict_path_runs_on_the_device_and_passes_its_gate():
+    """runtime.go:121-206 on the device: status ok, reactor backend, and the output
+    within the gate of Oct's fp32 CPU reference (checked here by the oracle)."""
+    from oct_amd import runtime as r
+
+    runs = r.run_starter_corpus(r.BACKEND_PROMETHEUS)
+    for run in runs:
+        assert str(run.status) == "ok" and run.used_backend == "prometheus", run
+        assert run.correctness.passed and run.detail_name in ("hip_mfma_f32", "hip_gemv_f32")
+    m, n, k = 257, 129, 300
+    a = oracle.uniform(71, (m, k))
+    b = oracle.uniform(72, (k, n))
+    out, res = r.run_sgemm_with_output(r.SGEMMRequest(r.BACKEND_PROMETHEUS, r.Shape(m, n, k), a, b))
+    assert str(res.status) == "ok" and res.used_backend == "prometheus" and res.vulkan_env == "hardware_gpu_hip"
+    gate = oracle.compare_against_oracle(oracle.cpu_sgemm_f32(a, b), out)
+    assert gate.pass_ == 1 and res.correctness.passed
+    assert oracle.normwise_rel_err(out.reshape(m, n), oracle.matmul_f64(a, b)) <= FP32_NORMWISE
+    rows, res2 = r.run_compiled_matmul_mm([[1.0, 2.0], [3.0, 4.0]], [[5.0, 6.0], [7.0, 8.0]])
+    assert rows == [[19.0, 22.0], [43.0, 50.0]] and str(res2.status) == "ok"
