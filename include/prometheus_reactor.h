@@ -93,6 +93,10 @@ enum {
   PROM_DETAIL_HIP_SYNC_FAILED = -6904,
   PROM_DETAIL_HIP_UNAVAILABLE = -6905,
   PROM_DETAIL_INVALID_ARGUMENT = -6906,
+  /* ..._sgemm_device_noalloc: the plan's split-K partials exceed the static
+     scratch array, or the array's device address could not be obtained. */
+  PROM_DETAIL_SCRATCH_LIMIT = -6930,
+  PROM_DETAIL_SCRATCH_UNAVAILABLE = -6931,
 };
 
 /* reactor_api.h:386-390 */
@@ -621,6 +625,24 @@ PROM_REACTOR_API int prometheus_reactor_runtime_event_elapsed_ms(void* handle, u
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device(void* handle, const float* a, const float* b, float* c,
                                                              uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
                                                              int* out_detail_code);
+/* No counterpart in the reference.  For callers that cannot allocate device
+   memory (code under HIP graph capture, tight serving loops, harnesses that
+   forbid hipMalloc): the product of ..._sgemm_device, with the same plan and
+   bit-identical results, that allocates nothing.  The split-K partial slices,
+   the only device memory the SGEMM needs beyond A, B and C, go to a static
+   device array of PROM_SGEMM_NOALLOC_SCRATCH_BYTES (64 MiB, one per GPU, held
+   until the process ends) instead of runtime-allocated staging.  A plan whose
+   partial buffer (PrometheusSgemmPlanInfo.partial_bytes) exceeds the array is
+   rejected: PROM_ERROR, stage TRANSFER_IN, PROM_DETAIL_SCRATCH_LIMIT.  Every
+   call on a GPU shares that GPU's array and leaves the last call's partials in
+   it (nothing in it needs to start at zero: each slice overwrites its part);
+   calls are ordered on the runtime's single stream, and work of two calls
+   that runs concurrently on one GPU (e.g. replayed from a captured graph on
+   another stream) races on the array. */
+#define PROM_SGEMM_NOALLOC_SCRATCH_BYTES (64ull << 20)
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_noalloc(void* handle, const float* a, const float* b,
+                                                                     float* c, uint32_t m, uint32_t n, uint32_t k,
+                                                                     uint32_t* out_stage, int* out_detail_code);
 /* The SGEMM launch plan that ..._sgemm and ..._sgemm_device queue for a
    contiguous row-major product with 16-byte-aligned operands.  It is a pure
    function of the shape and needs neither a runtime nor a device.  The

@@ -582,6 +582,34 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device(void* handle, const
   return gemm_device<float>(handle, a, b, c, m, n, k, out_stage, out_detail_code, launch_sgemm_f32);
 }
 
+// Allocation-free form of ..._sgemm_device (no reference counterpart): the
+// lookup, validation, lock and launch path allocate nothing.
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_noalloc(void* handle, const float* a, const float* b,
+                                                                     float* c, uint32_t m, uint32_t n, uint32_t k,
+                                                                     uint32_t* out_stage, int* out_detail_code) {
+  Runtime* rt = lookup(handle);
+  const int v = gemm_validate(rt, a, b, c, m, n, k, out_stage, out_detail_code);
+  if (v != PROM_OK) return v;
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  int path = 0;
+  const int r = launch_sgemm_f32_noalloc(a, b, c, m, n, k, cx.device, cx.stream, &path);
+  if (r == PROM_DETAIL_SCRATCH_LIMIT) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_TRANSFER_IN, PROM_DETAIL_SCRATCH_LIMIT);
+    return PROM_ERROR;
+  }
+  if (r == PROM_DETAIL_SCRATCH_UNAVAILABLE) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_INIT, PROM_DETAIL_SCRATCH_UNAVAILABLE);
+    return PROM_ERROR;
+  }
+  if (r != PROM_OK) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_SUBMIT, PROM_DETAIL_HIP_LAUNCH_FAILED);
+    return PROM_ERROR;
+  }
+  set_status(out_stage, out_detail_code, PROM_STAGE_SUBMIT, path);
+  return PROM_OK;
+}
+
 PROM_REACTOR_API int prometheus_reactor_runtime_gemm_bf16(void* handle, const uint16_t* a, const uint16_t* b, float* c,
                                                           uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
                                                           int* out_detail_code) {

@@ -106,6 +106,14 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
                                uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
                                int* path_detail);
 // C_z = A_z @ B_z for z < batch, A_z = a + z*sa etc. (elements); no residual, no split-K.
+// Allocation-free SGEMM: split-K partials in the library's static scratch
+// array.  init_sgemm_scratch(device) runs once per device at set-up (device
+// current).  launch_sgemm_f32_noalloc returns PROM_OK,
+// PROM_DETAIL_SCRATCH_LIMIT, PROM_DETAIL_SCRATCH_UNAVAILABLE or
+// PROM_DETAIL_HIP_LAUNCH_FAILED.
+hipError_t init_sgemm_scratch(int device);
+int launch_sgemm_f32_noalloc(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                             int device, hipStream_t stream, int* path_detail);
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
                                     float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
                                     uint32_t batch, hipStream_t stream);

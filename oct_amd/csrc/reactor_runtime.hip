@@ -60,6 +60,9 @@ bool ensure_device() {
   if (hipEventCreate(&c.op_begin) != hipSuccess || hipEventCreate(&c.op_end) != hipSuccess) return false;
   c.device = dev;
   c.available = true;
+  // Device address of the allocation-free SGEMM's scratch array; on failure
+  // only that entry reports PROM_DETAIL_SCRATCH_UNAVAILABLE.
+  (void)init_sgemm_scratch(dev);
   return true;
 }
 

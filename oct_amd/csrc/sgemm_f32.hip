@@ -842,6 +842,49 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
   return run_sgemm_schedule(s, a, lda, b, ldb, c, ldc, m, n, k, residual, ldr, nullptr, stream);
 }
 
+}  // namespace prom
+
+// Scratch of the allocation-free entry (prometheus_reactor_runtime_sgemm_device_noalloc):
+// the split-K partial slices go here instead of into runtime-allocated staging.
+// Host code never takes this array's name as an address; init_sgemm_scratch
+// obtains each device's copy with hipGetSymbolAddress once, at device set-up,
+// and the kernels receive that pointer.
+static __device__ __align__(256) float scratch[PROM_SGEMM_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace prom {
+namespace {
+constexpr int kScratchMaxDevices = 64;
+float* g_scratch_ptr[kScratchMaxDevices];  // device address of `scratch` per device ordinal
+}  // namespace
+
+hipError_t init_sgemm_scratch(int device) {
+  if (device < 0 || device >= kScratchMaxDevices) return hipErrorInvalidDevice;
+  if (g_scratch_ptr[device] != nullptr) return hipSuccess;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    return e != hipSuccess ? e : hipErrorInvalidSymbol;
+  }
+  g_scratch_ptr[device] = static_cast<float*>(ptr);
+  return hipSuccess;
+}
+
+int launch_sgemm_f32_noalloc(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                             int device, hipStream_t stream, int* path_detail) {
+  float* part = (device >= 0 && device < kScratchMaxDevices) ? g_scratch_ptr[device] : nullptr;
+  if (part == nullptr) return PROM_DETAIL_SCRATCH_UNAVAILABLE;
+  // The same plan as launch_sgemm_f32 (bit-identical results); a plan whose
+  // partials do not fit the array is refused rather than changed.
+  const SgemmSchedule s = schedule_sgemm(aligned16(a) && aligned16(b), (int)k, (int)n, m, n, k, false, ~0ull);
+  if (schedule_partial_floats(s, m, n) * sizeof(float) > PROM_SGEMM_NOALLOC_SCRATCH_BYTES)
+    return PROM_DETAIL_SCRATCH_LIMIT;
+  if (path_detail) *path_detail = s.gemv ? PROM_DETAIL_PATH_HIP_GEMV_F32 : PROM_DETAIL_PATH_HIP_MFMA_F32;
+  return run_sgemm_schedule(s, a, (int)k, b, (int)n, c, (int)n, m, n, k, nullptr, 0, part, stream) == hipSuccess
+             ? PROM_OK
+             : PROM_DETAIL_HIP_LAUNCH_FAILED;
+}
+
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
                                     float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
                                     uint32_t batch, hipStream_t stream) {

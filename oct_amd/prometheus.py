@@ -54,6 +54,9 @@ DETAIL_PATH_HIP_MFMA_F32 = 6120
 DETAIL_PATH_HIP_GEMV_F32 = 6121
 DETAIL_PATH_HIP_MFMA_BF16 = 6122
 DETAIL_HIP_UNAVAILABLE = -6905
+DETAIL_SCRATCH_LIMIT = -6930
+DETAIL_SCRATCH_UNAVAILABLE = -6931
+SGEMM_NOALLOC_SCRATCH_BYTES = 64 << 20
 # async and batch (reactor_api.h:84-114, 250-260, 282-295, 1448-1545)
 ASYNC_IDLE, ASYNC_SUBMITTED, ASYNC_READY, ASYNC_FAILED, ASYNC_CONSUMED = range(5)
 DETAIL_ASYNC_NOT_READY = -6108
@@ -863,6 +866,8 @@ _SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_sgemm_device": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_sgemm_device_noalloc": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_gemm_bf16": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_gemm_bf16_device": (
@@ -1398,6 +1403,14 @@ class NativeRuntime:
         rc = self.lib.prometheus_reactor_runtime_sgemm_device(self.handle, c_void_p(da), c_void_p(db), c_void_p(dc),
                                                               m, n, k, byref(stage), byref(detail))
         return self._check(rc, stage, detail, "sgemm_device")
+
+    def sgemm_device_noalloc(self, da: int, db: int, dc: int, m: int, n: int, k: int) -> Tuple[int, CallStatus]:
+        """The allocation-free SGEMM entry: (rc, stage/detail); does not raise."""
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_sgemm_device_noalloc(self.handle, c_void_p(da), c_void_p(db),
+                                                                       c_void_p(dc), m, n, k, byref(stage),
+                                                                       byref(detail))
+        return rc, CallStatus(stage.value, detail.value)
 
     def gemm_bf16_device(self, da: int, db: int, dc: int, m: int, n: int, k: int) -> int:
         stage, detail = c_uint32(0), c_int(0)

@@ -1,0 +1,73 @@
+"""The allocation-free SGEMM entry (prometheus_reactor_runtime_sgemm_device_noalloc)
+against the allocating device entry it mirrors: same plan, so the outputs must be
+bit-identical, and both within the fp32 parity bar of the binary64 oracle.  Two
+calls in a row, the second smaller, so a stale scratch array would show; a plan
+whose split-K partials exceed the array is refused without touching C."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from oct_amd import prometheus as p
+
+pytestmark = pytest.mark.gpu
+
+FP32_NORMWISE = 1e-5
+
+
+def _run_pair(rt, m, n, k, seed):
+    a = oracle.uniform(seed, (m, k))
+    b = oracle.uniform(seed + 1, (k, n))
+    da, db = rt.upload_new(a), rt.upload_new(b)
+    dc_ref, dc_new = rt.alloc(m * n * 4), rt.alloc(m * n * 4)
+    try:
+        rt.sgemm_device(da, db, dc_ref, m, n, k)
+        rc, st = rt.sgemm_device_noalloc(da, db, dc_new, m, n, k)
+        assert rc == p.PROM_OK and st.stage == p.STAGE_SUBMIT, st
+        assert st.detail in (p.DETAIL_PATH_HIP_MFMA_F32, p.DETAIL_PATH_HIP_GEMV_F32), st
+        rt.synchronize()
+        ref = rt.download(np.empty((m, n), np.float32), dc_ref)
+        new = rt.download(np.empty((m, n), np.float32), dc_new)
+    finally:
+        for d in (da, db, dc_ref, dc_new):
+            rt.free(d)
+    return a, b, ref, new
+
+
+@pytest.mark.parametrize("shapes", [((1056, 2048, 16384), (1000, 1000, 1000))])
+def test_noalloc_matches_the_device_entry_on_two_calls(gpu_runtime, shapes):
+    for i, (m, n, k) in enumerate(shapes):
+        rc, plan = p.sgemm_plan(m, n, k)
+        assert rc == p.PROM_OK and 0 < plan.partial_bytes <= p.SGEMM_NOALLOC_SCRATCH_BYTES, "scratch must be used"
+        print(f"noalloc call {i}: {m}x{n}x{k}, partials {plan.partial_bytes >> 20} MiB", flush=True)
+        a, b, ref, new = _run_pair(gpu_runtime, m, n, k, 900 + 10 * i)
+        assert np.array_equal(ref.view(np.uint32), new.view(np.uint32))
+        rows = sorted({0, m // 2, plan.head_rows - 1, min(plan.head_rows, m - 1), m - 1})
+        for r in rows:
+            got = oracle.normwise_rel_err(new[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r])
+            assert got <= FP32_NORMWISE, (m, n, k, r, got)
+
+
+def test_noalloc_refuses_a_plan_beyond_the_scratch(gpu_runtime):
+    m, n, k = 768, 1536, 8192
+    rc, plan = p.sgemm_plan(m, n, k)
+    assert rc == p.PROM_OK and plan.partial_bytes > p.SGEMM_NOALLOC_SCRATCH_BYTES
+    sentinel = np.full((m, n), 7.0, np.float32)
+    da, db, dc = gpu_runtime.alloc(m * k * 4), gpu_runtime.alloc(k * n * 4), gpu_runtime.upload_new(sentinel)
+    try:
+        rc, st = gpu_runtime.sgemm_device_noalloc(da, db, dc, m, n, k)
+        gpu_runtime.synchronize()
+        after = gpu_runtime.download(np.empty((m, n), np.float32), dc)
+    finally:
+        for d in (da, db, dc):
+            gpu_runtime.free(d)
+    assert rc == p.PROM_ERROR and st.stage == p.STAGE_TRANSFER_IN and st.detail == p.DETAIL_SCRATCH_LIMIT
+    assert np.array_equal(after, sentinel)
+
+
+def test_noalloc_without_split_and_gemv(gpu_runtime):
+    """Plans with no partials (the 4096-wide direct tile, the GEMV) run the same way."""
+    for (m, n, k) in ((512, 4096, 256), (8192, 1, 4096)):
+        a, b, ref, new = _run_pair(gpu_runtime, m, n, k, 950 + m)
+        assert np.array_equal(ref.view(np.uint32), new.view(np.uint32))
