@@ -74,9 +74,23 @@ def _traffic_from_profiles(name: str):
         return None
 
 
+class _OneCore:
+    """Pins this process to one of the cores it may use (Oct's CPU `@` is single-threaded)."""
+
+    def __enter__(self):
+        self.prev = os.sched_getaffinity(0)
+        self.core = min(self.prev)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.prev)
+
+
 def cpu_baseline_sgemm(a32: np.ndarray, b32: np.ndarray, gpu_rows: dict, seconds: float):
-    """Oct's compiled CPU `@` (__octMatMulMM restatement, binary64 ijk, one thread) on a row sample
-    of the benchmark's own operands; also checks the GPU's output rows against the oracle."""
+    """Oct's compiled CPU `@` (__octMatMulMM restatement, binary64 ijk, one thread pinned to
+    one core) on a row sample of the benchmark's own operands; also checks the GPU's output
+    rows against the oracle."""
     import oracle
 
     n = a32.shape[0]
@@ -85,13 +99,14 @@ def cpu_baseline_sgemm(a32: np.ndarray, b32: np.ndarray, gpu_rows: dict, seconds
     a = a32.astype(np.float64)
     b = b32.astype(np.float64)
     rows = 0
-    t0 = time.perf_counter()
-    while rows < n:
-        oracle.matmul_compiled_f64(a, b, rows=(rows, rows + 1))
-        rows += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
+    with _OneCore() as pin:
+        t0 = time.perf_counter()
+        while rows < n:
+            oracle.matmul_compiled_f64(a, b, rows=(rows, rows + 1))
+            rows += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = time.perf_counter() - t0
     flops = 2.0 * rows * n * n
     return parity, {
         "value": round(flops / dt / 1e12, 6),
@@ -99,8 +114,8 @@ def cpu_baseline_sgemm(a32: np.ndarray, b32: np.ndarray, gpu_rows: dict, seconds
         "cores": 1,
         "kind": "port",
         "sample": f"rows 0..{rows - 1} of the {n}^3 product ({rows}/{n} rows, {dt:.1f} s): "
-                  f"__octMatMulMM (emit_go_runtime.go:168-205) restated in C, binary64 ijk, 1 thread; "
-                  f"host has {os.cpu_count()} logical CPUs",
+                  f"__octMatMulMM (emit_go_runtime.go:168-205) restated in C, binary64 ijk, 1 thread pinned "
+                  f"to core {pin.core}; host has {len(pin.prev)} usable logical CPUs",
     }
 
 
@@ -124,6 +139,17 @@ def cpu_baseline_secondary(seconds: float):
     from oracle import blocks
 
     out = {}
+    # C1 in full: 1024^3 through the __octMatMulMM restatement on one pinned core
+    a1 = oracle.uniform(1, (1024, 1024)).astype(np.float64)
+    b1 = oracle.uniform(2, (1024, 1024)).astype(np.float64)
+    with _OneCore():
+        t0 = time.perf_counter()
+        oracle.matmul_compiled_f64(a1, b1)
+        dt = time.perf_counter() - t0
+    out["sgemm_1024_full_s"] = round(dt, 3)
+    out["sgemm_1024_full_tflops"] = round(2.0 * 1024 ** 3 / dt / 1e12, 6)
+    out["sgemm_1024_cores"] = 1
+    del a1, b1
     rows, width = 8192, 4096
     x = oracle.normal(77, (rows, width))
     for op, name, nbytes in ((3, "softmax", 2 * x.nbytes), (1, "row_sum", x.nbytes + rows * 4),
@@ -153,6 +179,17 @@ def cpu_baseline_secondary(seconds: float):
     blocks.decoder_layer_f32(xx, wl, Hq, hd)
     out["gemma2b_layer_f64_t512_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
     out["gemma2b_layer_cores"] = _blas_threads()
+    # C5: the binary64 block oracle on a row subset of the full 4224-token input
+    grid, text, heads, F5, C = (64, 64), 128, 30, 10240, 256
+    T5 = grid[0] * grid[1] + text
+    x5, cond5, w5 = blocks.make_dit_block(5, T5, heads * 128, F5, C)
+    coords5 = blocks.joint_coordinates(grid[0], grid[1], text)
+    sub = np.arange(0, T5, T5 // 64)[:64]
+    t0 = time.perf_counter()
+    blocks.dit_block_bf16(x5, coords5, cond5, w5, heads, rows=sub)
+    out["dit_block_bf16_t4224_rows64_f64_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+    out["dit_block_cores"] = _blas_threads()
+    del x5, w5
     xf = oracle.normal(31, (2 << 20,)).astype(np.float64).view(np.complex128)
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -163,8 +200,11 @@ def cpu_baseline_secondary(seconds: float):
             break
     out["fft64_2p20_us"] = round(dt / reps * 1e6, 1)
     out["kind"] = "port"
-    out["sample"] = ("reductions: one full [8192,4096] pass per repetition (C oracle, fp32 data, binary64 sums); "
+    out["sample"] = ("sgemm_1024: the full C1 product, __octMatMulMM restated in C, binary64, one pinned core; "
+                     "reductions: one full [8192,4096] pass per repetition (C oracle, fp32 data, binary64 sums); "
                      "layer: one full T=512 Gemma-2B-shaped layer in binary64 numpy; "
+                     "dit_block: the C5 block in binary64 numpy for 64 of the 4224 output tokens (Q, attention "
+                     "and FFN for those rows; K and V projected for all tokens), BLAS threads as dit_block_cores; "
                      "fft64: internal/fft/fft.go's radix-2 restated in C, one thread, 2^20 points (twiddles included)")
     return out
 

@@ -13,11 +13,11 @@
 //   2 QKV projection, fused         n1 @ Wqkv -> qkv [T, (Hq+2)d]
 //   3 RoPE + split                  qkv -> Q [T, Hq*d] (scaled by 1/sqrt d, exact
 //                                   power of two), K^T [d, T], V [T, d]
-//   4 scores, all heads in one GEMM Q viewed as [T*Hq, d] @ K^T -> S [T*Hq, T]
-//     (multi-query: all query heads share K, so rows (t, h) stack into one
-//     matrix; S is 8 MB at T=512 and stays in MALL)
-//   5 causal softmax rows           row (t, h) keeps keys 0..t
-//   6 P @ V                         [T*Hq, T] @ [T, d] -> O viewed as [T, Hq*d]
+//   4 causal flash attention        Q, K^T, V -> O [T, Hq*d] (attention_f32.hip:
+//     the query heads of a workgroup share each K/V tile; no score matrix;
+//     the key range is split over the grid at T = 512, then combined).  For
+//     head dims other than 64/128/256: scores as one GEMM [T*Hq, d] @ K^T ->
+//     S [T*Hq, T], a causal softmax over row (t, h)'s keys 0..t, and P @ V
 //   7 output projection + residual  x + O @ Wo -> h   (residual fused in the epilogue)
 //   8 RMSNorm                       h -> n2
 //   9 gate|up projection, fused     n2 @ Wgu -> G [T, 2F]
@@ -32,10 +32,11 @@ namespace prom {
 namespace {
 
 // qkv [T, ldq]: Q heads at column h*d, K at Hq*d, V at (Hq+1)*d.
+// K^T rows are ldkt (>= T) apart.
 __global__ __launch_bounds__(256) void gemma_rope_split_kernel(const float* __restrict__ qkv, int ldq, int T, int Hq,
                                                                int d, int pos0, float base, float q_scale,
                                                                float* __restrict__ Q, float* __restrict__ Kt,
-                                                               float* __restrict__ V) {
+                                                               int ldkt, float* __restrict__ V) {
   const int half = d >> 1;
   const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (idx < T * half) {
@@ -55,8 +56,8 @@ __global__ __launch_bounds__(256) void gemma_rope_split_kernel(const float* __re
     }
     const float k1 = row[Hq * d + i];
     const float k2 = row[Hq * d + i + half];
-    Kt[(size_t)i * T + t] = k1 * c - k2 * s;
-    Kt[(size_t)(i + half) * T + t] = k2 * c + k1 * s;
+    Kt[(size_t)i * ldkt + t] = k1 * c - k2 * s;
+    Kt[(size_t)(i + half) * ldkt + t] = k2 * c + k1 * s;
   }
   if (idx < T * d) {
     const int t = idx / d;
@@ -111,21 +112,27 @@ __global__ __launch_bounds__(256) void geglu_kernel(const float* __restrict__ G,
 
 struct LayerShape {
   int T, D, Hq, d, F, nqkv;
+  int ldkt() const { return (T + 3) & ~3; }  // K^T row stride: 16-byte rows for the attention's tile transfers
 };
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Workspace layout (floats): n1 [T,D] | qkv [T,nqkv] | Q [T,Hq*d] | Kt [d,T] | V [T,d]
-// | S [T*Hq,T] | O [T,Hq*d] | h [T,D] | n2 [T,D] | G [T,2F] | A [T,F]
+// Workspace layout: n1 [T,D] | qkv [T,nqkv] | Q [T,Hq*d] | Kt [d,ldkt] | V [T,d]
+// | attention partials (or S [T*Hq,T]) | O [T,Hq*d] | h [T,D] | n2 [T,D] | G [T,2F] | A [T,F]
 size_t layer_workspace_bytes(const LayerShape& s, size_t offsets[11]) {
-  const size_t sizes[11] = {(size_t)s.T * s.D,        (size_t)s.T * s.nqkv, (size_t)s.T * s.Hq * s.d,
-                            (size_t)s.d * s.T,        (size_t)s.T * s.d,    (size_t)s.T * s.Hq * s.T,
-                            (size_t)s.T * s.Hq * s.d, (size_t)s.T * s.D,    (size_t)s.T * s.D,
-                            (size_t)s.T * 2 * s.F,    (size_t)s.T * s.F};
+  // Slot 5: the key-split partials of the flash attention (often none), or
+  // the [T*Hq, T] score matrix of the unfused path for other head dims.
+  const size_t attn_bytes = flash_attn_f32_supported(s.d)
+                                ? flash_attn_f32_partial_bytes(s.T, s.Hq, s.Hq, s.d, 1)
+                                : (size_t)s.T * s.Hq * s.T * sizeof(float);
+  const size_t sizes[11] = {(size_t)s.T * s.D * 4,        (size_t)s.T * s.nqkv * 4, (size_t)s.T * s.Hq * s.d * 4,
+                            (size_t)s.d * s.ldkt() * 4,   (size_t)s.T * s.d * 4,    attn_bytes,
+                            (size_t)s.T * s.Hq * s.d * 4, (size_t)s.T * s.D * 4,    (size_t)s.T * s.D * 4,
+                            (size_t)s.T * 2 * s.F * 4,    (size_t)s.T * s.F * 4};
   size_t off = 0;
   for (int i = 0; i < 11; ++i) {
     offsets[i] = off;
-    off += align_up(sizes[i] * sizeof(float));
+    off += align_up(sizes[i]);
   }
   return off;
 }
@@ -178,13 +185,37 @@ hipError_t enqueue_layer(const PrometheusDecoderLayerF32Request* r, char* ws, co
     const int threads = s.T * s.d;  // covers T*d/2 rope pairs and T*d V elements
     const float q_scale = 1.0f / sqrtf((float)s.d);
     hipLaunchKernelGGL(gemma_rope_split_kernel, dim3((threads + 255) / 256), dim3(256), 0, st, qkv, s.nqkv, s.T, s.Hq,
-                       s.d, (int)r->position_offset, r->rope_base, q_scale, Q, Kt, V);
+                       s.d, (int)r->position_offset, r->rope_base, q_scale, Q, Kt, s.ldkt(), V);
     PROM_STEP(hipGetLastError());
   }
-  PROM_STEP(launch_sgemm_f32_ex(Q, s.d, Kt, s.T, S, s.T, s.T * s.Hq, s.T, s.d, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(causal_softmax_kernel, dim3((s.T * s.Hq + 3) / 4), dim3(256), 0, st, S, s.T * s.Hq, s.T, s.Hq);
-  PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_sgemm_f32_ex(S, s.T, V, s.d, O, s.d, s.T * s.Hq, s.d, s.T, nullptr, 0, st, nullptr));
+  if (flash_attn_f32_supported(s.d)) {
+    // Causal flash attention, every query head on the one K/V head; S holds
+    // only the key-split partials (no score matrix).
+    AttnF32Params ap{};
+    ap.q = Q;
+    ap.kt = Kt;
+    ap.v = V;
+    ap.o = O;
+    ap.q_hs = s.d;
+    ap.q_rs = s.Hq * s.d;
+    ap.kt_hs = 0;
+    ap.kt_rs = s.ldkt();
+    ap.v_hs = 0;
+    ap.v_rs = s.d;
+    ap.o_rs = s.Hq * s.d;
+    ap.T = s.T;
+    ap.q_heads = s.Hq;
+    ap.group = s.Hq;
+    ap.causal = 1;
+    flash_attn_f32_bind_partials(ap, s.d, S);
+    PROM_STEP(launch_flash_attn_f32(ap, s.d, 1.0f, st));
+  } else {
+    PROM_STEP(launch_sgemm_f32_ex(Q, s.d, Kt, s.ldkt(), S, s.T, s.T * s.Hq, s.T, s.d, nullptr, 0, st, nullptr));
+    hipLaunchKernelGGL(causal_softmax_kernel, dim3((s.T * s.Hq + 3) / 4), dim3(256), 0, st, S, s.T * s.Hq, s.T,
+                       s.Hq);
+    PROM_STEP(hipGetLastError());
+    PROM_STEP(launch_sgemm_f32_ex(S, s.T, V, s.d, O, s.d, s.T * s.Hq, s.d, s.T, nullptr, 0, st, nullptr));
+  }
   PROM_STEP(launch_sgemm_f32_ex(O, s.Hq * s.d, r->w_o, s.D, h, s.D, s.T, s.D, s.Hq * s.d, r->input, s.D, st, nullptr));
   PROM_STEP(launch_rmsnorm(h, r->ffn_norm_weight, n2, nullptr, s.T, s.D, s.D, r->rms_epsilon, st));
   PROM_STEP(launch_sgemm_f32_ex(n2, s.D, r->w_gate_up, 2 * s.F, G, 2 * s.F, s.T, 2 * s.F, s.D, nullptr, 0, st, nullptr));

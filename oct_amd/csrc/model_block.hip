@@ -511,9 +511,9 @@ uint64_t plan_identity(const ModelBlock* b) {
   }
   for (uint32_t i = 0; i < b->step_count; ++i) h = hash_u64(h, b->steps[i]);
   if (b->program != kProgProof) {
-    // adaln, norm_mod, qkv sgemm, qkv_split, scores, softmax, pv, out sgemm,
+    // adaln, norm_mod, qkv sgemm, qkv_split, flash attention, out sgemm,
     // resid_norm_mod, w13 sgemm, swiglu, w2 sgemm, final_resid
-    for (uint64_t k = 1; k <= 13; ++k) h = hash_u64(h, 0x4d49333535000000ull | k);
+    for (uint64_t k = 1; k <= 11; ++k) h = hash_u64(h, 0x4d49333535100000ull | k);
     h = hash_u64(h, (uint64_t)b->tokens);
   }
   return h;
@@ -783,7 +783,7 @@ bool alloc_block_buffers(ModelBlock* b) {
   b->reusable_bytes = max_weight + 2 * act + (uint64_t)T * kWidth * 2 + kZImageConditionWidth * 6 +
                       (uint64_t)T * 12 + ws_bytes;
   b->audit_alloc_bytes = kAuditScratchOffset + act;  // stage audits copy workspace buffers directly
-  b->pipelines = 13;         // the fixed kernel chain of the block
+  b->pipelines = 11;         // the fixed kernel chain of the block
   return ok && alloc_set(b, &b->active);
 }
 

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/prometheus_reactor.h"
@@ -140,6 +141,30 @@ hipError_t launch_row_reduction_check(const float* in, float* out, uint32_t rows
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, float* inv_rms, uint32_t tokens,
                           uint32_t width, uint32_t stride, float eps, hipStream_t stream);
 
+// ---- fp32 flash attention (attention_f32.hip)
+// O[t][hq*d + c] = sum_s softmax_s(scale * Q[hq][t] . K[hkv][s]) V[hkv][s][c] with
+// hkv = hq / group, keys s <= t when causal.  Element strides: Q[hq][t][c] at
+// q + hq*q_hs + t*q_rs + c; K^T[hkv][c][s] at kt + hkv*kt_hs + c*kt_rs + s;
+// V[hkv][s][c] at v + hkv*v_hs + s*v_rs + c; O[t][hq*d + c] at o + t*o_rs + hq*d + c.
+// part_o / part_ml hold key-split partials when flash_attn_f32_partial_bytes > 0.
+struct AttnF32Params {
+  const float* q;
+  const float* kt;
+  const float* v;
+  float* o;
+  float* part_o;
+  float* part_ml;
+  long long q_hs, kt_hs, v_hs;
+  int q_rs, kt_rs, v_rs, o_rs;
+  int T, q_heads, group, causal;
+};
+bool flash_attn_f32_supported(int head_dim);
+// Partial buffer bytes the launch needs (0: none); flash_attn_f32_bind_partials
+// points part_o and part_ml into such a buffer.
+size_t flash_attn_f32_partial_bytes(int T, int q_heads, int group, int head_dim, int causal);
+void flash_attn_f32_bind_partials(AttnF32Params& p, int head_dim, void* buffer);
+hipError_t launch_flash_attn_f32(const AttnF32Params& p, int head_dim, float scale, hipStream_t stream);
+
 // ---- fp32 Z-Image transformer block on resident weights (zimage_f32.hip)
 constexpr int kZImageConditionWidth = 256;  // timestep embedding width (adaLN input)
 
@@ -152,7 +177,7 @@ enum ZImageWorkspace {
   kZQ,       // [H, T, 128] normalized, rotated, scaled by 1/sqrt(128)
   kZKt,      // [H, 128, T] normalized, rotated, transposed
   kZV,       // [H, T, 128]
-  kZS,       // [H, T, T] scores, then probabilities
+  kZS,       // flash-attention key-split partials (no score matrix)
   kZO,       // [T, D] attention aggregation
   kZProj,    // [T, D] attention projection
   kZR,       // [T, D] attention residual

@@ -13,9 +13,9 @@
 // upload).
 //
 // MI355X design: the matrix work is the fp32 MFMA SGEMM (sgemm_f32.hip);
-// attention is two batched SGEMMs over the heads (S_h = Q_h K_h^T with the
-// 1/sqrt(128) scale folded into Q, then O_h = softmax(S_h) V_h) around the
-// one-pass row softmax (reduction.hip).  Between them:
+// attention is the fp32 flash kernel (attention_f32.hip: scores, online
+// softmax and P.V per 32-key tile in registers and LDS, the 1/sqrt(128) scale
+// folded into Q; no [H, T, T] score tensor).  Around them:
 //   adaln         m = c @ Wada + b; raw and adjusted (1 + scale, tanh gate)
 //   rope_table    (cos, sin) per token and pair, the reference's float32 angle
 //   norm_mod      a = RMSNorm(x; n1) * scaleA                    (block_rows.h)
@@ -341,7 +341,7 @@ size_t zimage_workspace_layout(int T, int D, int H, int F, size_t off[kZCount]) 
   sizes[kZQ] = t * d * 4;
   sizes[kZKt] = t * d * 4;
   sizes[kZV] = t * d * 4;
-  sizes[kZS] = (size_t)H * t * t * 4;
+  sizes[kZS] = flash_attn_f32_partial_bytes(T, H, 1, kHead, 0);  // attention key-split partials (usually none)
   sizes[kZO] = t * d * 4;
   sizes[kZProj] = t * d * 4;
   sizes[kZR] = t * d * 4;
@@ -463,13 +463,30 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
     if ((e = mark(4)) != hipSuccess) return e;
   }
   if (first_phase <= 2 && last_phase >= 2) {  // attention, projection, gated residual, FFN norm
-    PROM_STEP(launch_sgemm_f32_batched(Q, kHead, (long long)T * kHead, Kt, T, (long long)kHead * T, S, T,
-                                       (long long)T * T, T, T, kHead, H, st));
+    {
+      // Scores, softmax and P.V in one flash kernel (Q is already scaled by
+      // 1/sqrt(128)); stages 6 and 7 close immediately after stage 5.
+      AttnF32Params ap{};
+      ap.q = Q;
+      ap.kt = Kt;
+      ap.v = V;
+      ap.o = O;
+      ap.q_hs = (long long)T * kHead;
+      ap.q_rs = kHead;
+      ap.kt_hs = (long long)kHead * T;
+      ap.kt_rs = T;
+      ap.v_hs = (long long)T * kHead;
+      ap.v_rs = kHead;
+      ap.o_rs = D;
+      ap.T = T;
+      ap.q_heads = H;
+      ap.group = 1;
+      ap.causal = 0;
+      flash_attn_f32_bind_partials(ap, kHead, S);
+      PROM_STEP(launch_flash_attn_f32(ap, kHead, 1.0f, st));
+    }
     if ((e = mark(5)) != hipSuccess) return e;
-    PROM_STEP(launch_row_reduction(S, S, (uint32_t)(H * T), (uint32_t)T, 3u, st));
     if ((e = mark(6)) != hipSuccess) return e;
-    PROM_STEP(launch_sgemm_f32_batched(S, T, (long long)T * T, V, kHead, (long long)T * kHead, O, D, kHead, T, kHead,
-                                       T, H, st));
     if ((e = mark(7)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(O, D, w.w_out, D, proj, D, T, D, D, nullptr, 0, st, nullptr));
     if ((e = mark(8)) != hipSuccess) return e;

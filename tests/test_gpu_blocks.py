@@ -125,9 +125,26 @@ def test_dit_block_c5_full(gpu_runtime):
     coords = blocks.joint_coordinates(grid[0], grid[1], text)
     rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
     assert rc == p.PROM_OK, (res.stage, res.detail_code)
-    rows = sorted(set(np.linspace(0, T - 1, 48).astype(int).tolist()) | {0, 4095, 4096, T - 1})
-    ref = blocks.dit_block_bf16(x, coords, cond, w, heads, rows=rows)
-    err = oracle.normwise_rel_err(out[rows], ref)
-    print(f"C5 DiT block normwise rel err {err:.3e} on {len(rows)} rows, gpu {res.gpu_duration_ns / 1e6:.3f} ms")
+    print(f"C5 gpu {res.gpu_duration_ns / 1e6:.3f} ms; binary64 oracle over all {T} rows...", flush=True)
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads)
+    err = oracle.normwise_rel_err(out, ref)
+    row_err = np.linalg.norm(out - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    print(f"C5 DiT block normwise rel err {err:.3e} over all rows, worst row {row_err.max():.3e}", flush=True)
     assert err <= BF16_BLOCK
+    assert row_err.max() <= BF16_BLOCK
     assert np.all(np.isfinite(out))
+
+
+@pytest.mark.parametrize("q_heads,head_dim", [(8, 256), (3, 4)])
+def test_decoder_layer_attention_closed_form(gpu_runtime, q_heads, head_dim):
+    """T = 2 layer with a closed-form output (head h weights token 1 by
+    3^(h+1)/(3^(h+1)+1)): pins the kernel's 1/sqrt(d) scale, the shared K/V head
+    and the causal mask independently of the binary64 oracle."""
+    from tests.test_oracle_blocks import closed_form_attention_layer, closed_form_expected
+
+    x, w, qkv = closed_form_attention_layer(q_heads, head_dim)
+    rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=q_heads, head_dim=head_dim, eps=1e-6)
+    assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)
+    want = closed_form_expected(x, qkv, q_heads, head_dim, 1e-6)
+    assert oracle.normwise_rel_err(out, want) <= 1e-5
+    assert np.max(np.abs(out - want)) <= 1e-5

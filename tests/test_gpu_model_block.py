@@ -287,7 +287,10 @@ def check_stage_timing(ev):
     follows it."""
     ns = list(ev.main_stage_gpu_ns)
     begin, end = list(ev.main_stage_gpu_begin_tick), list(ev.main_stage_gpu_end_tick)
-    assert all(n > 0 for n in ns), ns
+    # Stage 5 (0-based 4) is the fused flash attention; the softmax and P.V
+    # stages that follow it close immediately, so only they may be empty.
+    assert all(n > 0 for i, n in enumerate(ns) if i not in (5, 6)), ns
+    assert all(n >= 0 for n in ns), ns
     assert [e - b for b, e in zip(begin, end)] == ns
     assert begin[1:] == end[:-1]
     assert begin[0] == ev.gpu_compute_begin_tick and end[-1] == ev.gpu_compute_end_tick

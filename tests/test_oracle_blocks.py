@@ -7,6 +7,7 @@ wrong sign, pairing or index would break.
 import math
 
 import numpy as np
+import pytest
 
 import oracle
 from oracle import blocks
@@ -257,3 +258,92 @@ def test_dit_block_permutation_equivariant():
     perm = np.array([3, 0, 5, 1, 4, 2])
     moved = blocks.dit_block_bf16(x[perm], coords[perm], cond, w, heads=2)
     np.testing.assert_allclose(moved, base[perm], rtol=1e-12, atol=1e-12)
+
+
+def closed_form_attention_layer(q_heads: int, head_dim: int, c0_over_sqrt_d: float = np.log(3.0)):
+    """A T = 2 layer whose output is known in closed form (conventions of
+    gemma4e2b_m1_rtx.go:863-883: scores scaled by 1/sqrt(d), every query head on
+    the single K/V head).  D = q_heads * head_dim; x0 = ones, x1 = alternating
+    signs (orthogonal, RMS 1), so with unit norm weights RMSNorm is the identity
+    up to 1/sqrt(1 + eps).  Token 0 has k = 0, so token 1's scores are 0 (key 0)
+    and c_h / sqrt(d) (key 1) with c_h = (h + 1) * c0: head h puts weight
+    3^(h+1) / (3^(h+1) + 1) on token 1 when c0 / sqrt(d) = ln 3.  W_o = I and a
+    zero gate|up make the layer output x + attention output."""
+    d, Hq = head_dim, q_heads
+    D = Hq * d
+    x = np.ones((2, D))
+    x[1, 1::2] = -1.0
+    a = 4.0
+    b = c0_over_sqrt_d * np.sqrt(d) / a
+    rng = np.random.default_rng(123)
+    v0, v1 = rng.uniform(-1, 1, d), rng.uniform(-1, 1, d)
+    cols = np.zeros((2, (Hq + 2) * d))  # per token: wanted q | k | v values
+    for h in range(Hq):
+        cols[1, h * d] = (h + 1) * a          # q head h at token 1 = (h+1) a e0; token 0's q = 0
+    cols[1, Hq * d] = b                        # k1 = b e0, k0 = 0
+    cols[0, (Hq + 1) * d:] = v0
+    cols[1, (Hq + 1) * d:] = v1
+    # column j = (val0 x0 + val1 x1) / D, then stored as float32
+    w_qkv = ((cols[0][None, :] * x[0][:, None] + cols[1][None, :] * x[1][:, None]) / D).astype(np.float32)
+    F = 4
+    w = blocks.DecoderLayerWeights(
+        attn_norm=np.ones(D, np.float32), w_qkv=w_qkv, w_o=np.eye(D, dtype=np.float32),
+        ffn_norm=np.ones(D, np.float32), w_gate_up=np.zeros((D, 2 * F), np.float32),
+        w_down=rng.uniform(-1, 1, (F, D)).astype(np.float32))
+    # what the float32 weights actually hold
+    qkv = x @ w_qkv.astype(np.float64)
+    return x.astype(np.float32), w, qkv
+
+
+def closed_form_expected(x, qkv, q_heads, head_dim, eps):
+    d, Hq = head_dim, q_heads
+    s2 = 1.0 / (1.0 + eps)          # both q and k carry the RMSNorm factor 1/sqrt(1+eps)
+    s1 = np.sqrt(s2)
+    v0 = qkv[0, (Hq + 1) * d:] * s1
+    v1 = qkv[1, (Hq + 1) * d:] * s1
+    k1 = qkv[1, Hq * d]
+    out = x.astype(np.float64).copy()
+    for h in range(Hq):
+        c = qkv[1, h * d] * k1 * s2 / np.sqrt(d)
+        p1 = 1.0 / (1.0 + np.exp(-c))  # two keys: softmax = sigmoid of the score difference
+        out[0, h * d:(h + 1) * d] += v0
+        out[1, h * d:(h + 1) * d] += p1 * v1 + (1.0 - p1) * v0
+    return out
+
+
+@pytest.mark.parametrize("q_heads,head_dim", [(8, 256), (3, 4)])
+def test_decoder_layer_attention_closed_form(q_heads, head_dim):
+    x, w, qkv = closed_form_attention_layer(q_heads, head_dim)
+    got = blocks.decoder_layer_f32(x, w, q_heads, head_dim, eps=0.0)
+    want = closed_form_expected(x, qkv, q_heads, head_dim, 0.0)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-12)
+    # the hand-computed weights: head h puts 3^(h+1)/(3^(h+1)+1) on token 1
+    d = head_dim
+    for h in range(q_heads):
+        c = qkv[1, h * d] * qkv[1, q_heads * d] / np.sqrt(d)
+        assert abs(1.0 / (1.0 + np.exp(-c)) - 3.0 ** (h + 1) / (3.0 ** (h + 1) + 1.0)) < 1e-6
+
+
+def test_closed_form_rejects_plausible_convention_mistakes():
+    """Each mistake the closed form is meant to catch moves the output well past its tolerance."""
+    Hq, d = 8, 256
+    x, w, qkv = closed_form_attention_layer(Hq, d)
+    want = closed_form_expected(x, qkv, Hq, d, 0.0)
+    # scale 1/d instead of 1/sqrt(d)
+    wrong_scale = closed_form_expected(x, qkv * np.where(np.arange(qkv.shape[1]) < Hq * d, 1.0 / np.sqrt(d), 1.0),
+                                       Hq, d, 0.0)
+    assert np.max(np.abs(wrong_scale - want)) > 1e-2
+    # per-head K (head h reading the columns after K, i.e. V, as its key) changes heads >= 1
+    x2, w2, _ = closed_form_attention_layer(Hq, d)
+    got = blocks.decoder_layer_f32(x2, w2, Hq, d, eps=0.0)
+    v_as_key = closed_form_expected(x, qkv, Hq, d, 0.0)
+    for h in range(1, Hq):
+        kv = qkv[1, (Hq + 1) * d]  # the first V component would be head 1's "key" component
+        c = qkv[1, h * d] * kv / np.sqrt(d)
+        p1 = 1.0 / (1.0 + np.exp(-c))
+        v0, v1 = qkv[0, (Hq + 1) * d:], qkv[1, (Hq + 1) * d:]
+        v_as_key[1, h * d:(h + 1) * d] = x[1, h * d:(h + 1) * d] + p1 * v1 + (1 - p1) * v0
+    assert np.max(np.abs(v_as_key - got)) > 1e-2
+    # a causal mask transposed (token 0 sees token 1) changes token 0
+    v0, v1 = qkv[0, (Hq + 1) * d:], qkv[1, (Hq + 1) * d:]
+    assert np.max(np.abs(0.5 * (v0 + v1) - (got[0, :d] - x[0, :d]))) > 1e-2
