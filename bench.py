@@ -48,8 +48,11 @@ def _settle(rt, launch, settle_ms: float) -> int:
     return launches
 
 
-def _timed_launches(rt, launch, steps: int, warmup: int):
-    """Returns (wall_ms_per_step, event_ms_per_step)."""
+def _timed_launches(rt, launch, steps: int, warmup: int, settle_ms: float = 0.0):
+    """Returns (wall_ms_per_step, event_ms_per_step).  ``settle_ms`` of untimed
+    launches come first (see ``_settle``): a secondary leg follows seconds of host
+    work (input generation, uploads) during which the clock falls back."""
+    _settle(rt, launch, settle_ms)
     for _ in range(warmup):
         launch()
     rt.synchronize()
@@ -216,7 +219,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--settle-ms", type=float, default=150.0,
-                    help="untimed headline launches before the warm-up, so the clock has ramped (reported)")
+                    help="untimed headline launches before the warm-up, so the clock has ramped (reported); "
+                         "each secondary leg settles for a third of it")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -309,13 +313,14 @@ def main() -> int:
 
     if not args.no_secondary:
         sec = {}
+        leg_settle = args.settle_ms / 3
         # fp32 1024^3
         m1 = 1024
         a1, b1 = syn.uniform(1, (m1, m1)), syn.uniform(2, (m1, m1))
         d1 = [rt.alloc(a1.nbytes) for _ in range(3)]
         rt.upload(d1[0], a1)
         rt.upload(d1[1], b1)
-        _, ev = _timed_launches(rt, lambda: rt.sgemm_device(d1[0], d1[1], d1[2], m1, m1, m1), 50, 5)
+        _, ev = _timed_launches(rt, lambda: rt.sgemm_device(d1[0], d1[1], d1[2], m1, m1, m1), 50, 5, leg_settle)
         sec["sgemm_f32_1024_tflops"] = round(2.0 * m1 ** 3 / (ev * 1e-3) / 1e12, 3)
         for d in d1:
             rt.free(d)
@@ -326,7 +331,7 @@ def main() -> int:
             dd = [rt.alloc(aa.nbytes), rt.alloc(bb.nbytes), rt.alloc(m * nn * 4)]
             rt.upload(dd[0], aa)
             rt.upload(dd[1], bb)
-            _, ev = _timed_launches(rt, lambda: rt.sgemm_device(dd[0], dd[1], dd[2], m, nn, k), 30, 5)
+            _, ev = _timed_launches(rt, lambda: rt.sgemm_device(dd[0], dd[1], dd[2], m, nn, k), 30, 5, leg_settle)
             sec[key] = round(2.0 * m * nn * k / (ev * 1e-3) / 1e12, 3)
             for d in dd:
                 rt.free(d)
@@ -335,7 +340,7 @@ def main() -> int:
         dd = [rt.alloc(aa.nbytes), rt.alloc(xx.nbytes), rt.alloc(m * 4)]
         rt.upload(dd[0], aa)
         rt.upload(dd[1], xx)
-        _, ev = _timed_launches(rt, lambda: rt.sgemm_device(dd[0], dd[1], dd[2], m, 1, k), 100, 10)
+        _, ev = _timed_launches(rt, lambda: rt.sgemm_device(dd[0], dd[1], dd[2], m, 1, k), 100, 10, leg_settle)
         sec["gemv_f32_8192x4096_gbs"] = round((m * k + k + m) * 4 / (ev * 1e-3) / 1e9, 1)
         for d in dd:
             rt.free(d)
@@ -344,7 +349,7 @@ def main() -> int:
         dd = [rt.alloc(ab.nbytes), rt.alloc(bbf.nbytes), rt.alloc(n * n * 4)]
         rt.upload(dd[0], ab)
         rt.upload(dd[1], bbf)
-        _, ev = _timed_launches(rt, lambda: rt.gemm_bf16_device(dd[0], dd[1], dd[2], n, n, n), 30, 5)
+        _, ev = _timed_launches(rt, lambda: rt.gemm_bf16_device(dd[0], dd[1], dd[2], n, n, n), 30, 5, leg_settle)
         tf = flops / (ev * 1e-3) / 1e12
         sec["gemm_bf16_4096_tflops"] = round(tf, 2)
         sec["gemm_bf16_4096_frac"] = round(tf / PEAK_BF16_MFMA_TFLOPS, 4)
@@ -357,14 +362,14 @@ def main() -> int:
         rt.upload(dx, x)
         for op, name, nbytes in ((p.OP_SOFTMAX, "softmax", 2 * x.nbytes), (p.OP_SUM, "row_sum", x.nbytes + rows * 4),
                                  (p.OP_MAX, "row_max", x.nbytes + rows * 4)):
-            _, ev = _timed_launches(rt, lambda: rt.reduction_device(dx, dy, rows, width, op), 100, 10)
+            _, ev = _timed_launches(rt, lambda: rt.reduction_device(dx, dy, rows, width, op), 100, 10, leg_settle)
             gbs = nbytes / (ev * 1e-3) / 1e9
             sec[f"{name}_8192x4096_gbs"] = round(gbs, 1)
             sec[f"{name}_8192x4096_frac"] = round(gbs / PEAK_HBM_GBS, 4)
         w = syn.normal(89, (width,), 1.0, 0.02)
         dw, dinv = rt.alloc(w.nbytes), rt.alloc(rows * 4)
         rt.upload(dw, w)
-        _, ev = _timed_launches(rt, lambda: rt.rmsnorm_device(dx, dw, dy, dinv, rows, width, width, 1e-6), 100, 10)
+        _, ev = _timed_launches(rt, lambda: rt.rmsnorm_device(dx, dw, dy, dinv, rows, width, width, 1e-6), 100, 10, leg_settle)
         gbs = (2 * x.nbytes + w.nbytes + rows * 4) / (ev * 1e-3) / 1e9
         sec["rmsnorm_8192x4096_gbs"] = round(gbs, 1)
         sec["rmsnorm_8192x4096_frac"] = round(gbs / PEAK_HBM_GBS, 4)
@@ -376,7 +381,7 @@ def main() -> int:
         dptr = {k: rt.upload_new(np.ascontiguousarray(v, np.float32)) for k, v in ptrs.items()}
         dptr["output"] = rt.alloc(T * D * 4)
         req = rt.decoder_layer_request(T, D, Hq, hd, F, dptr)
-        _, ev = _timed_launches(rt, lambda: rt.decoder_layer_f32_device(req), 10, 3)
+        _, ev = _timed_launches(rt, lambda: rt.decoder_layer_f32_device(req), 10, 3, leg_settle)
         sec["gemma2b_layer_f32_t512_ms"] = round(ev, 4)
         sec["gemma2b_layer_f32_t512_tflops"] = round(1.149e11 / (ev * 1e-3) / 1e12, 2)
         for d in dptr.values():
@@ -389,7 +394,7 @@ def main() -> int:
         dptr = {k: rt.upload_new(v) for k, v in arrs.items()}
         dptr["output"] = rt.alloc(T5 * D5 * 4)
         req = rt.dit_block_request(T5, D5, heads, F5, C, dptr)
-        _, ev = _timed_launches(rt, lambda: rt.dit_block_bf16_device(req), 10, 3)
+        _, ev = _timed_launches(rt, lambda: rt.dit_block_bf16_device(req), 10, 3, leg_settle)
         sec["dit_block_bf16_t4224_ms"] = round(ev, 4)
         sec["dit_block_bf16_t4224_tflops"] = round(1.769e12 / (ev * 1e-3) / 1e12, 2)
         for d in dptr.values():
@@ -398,7 +403,7 @@ def main() -> int:
         nf = 1 << 20
         xf = syn.normal(31, (2 * nf,)).astype(np.float64).view(np.complex128)
         dfi, dfo = rt.upload_new(xf.view(np.float64)), rt.alloc(xf.nbytes)
-        _, ev = _timed_launches(rt, lambda: rt.fft64_device(dfi, dfo, nf), 100, 10)
+        _, ev = _timed_launches(rt, lambda: rt.fft64_device(dfi, dfo, nf), 100, 10, leg_settle)
         sec["fft64_2p20_us"] = round(ev * 1e3, 2)
         gbs = 2 * xf.nbytes / (ev * 1e-3) / 1e9
         sec["fft64_2p20_gbs"] = round(gbs, 1)

@@ -643,6 +643,20 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device(void* handle, const
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_noalloc(void* handle, const float* a, const float* b,
                                                                      float* c, uint32_t m, uint32_t n, uint32_t k,
                                                                      uint32_t* out_stage, int* out_detail_code);
+/* No counterpart in the reference: ..._sgemm_device with a caller-chosen
+   kernel variant instead of the plan model's, for tuning and per-variant
+   tests.  tile: 0 = 128x256, 1 = 128x128, 2 = 64x128 (register-staged
+   loads), 3 = 128x256, 4 = 128x128 (HBM -> LDS loads, K tile 16: k and each
+   K slice multiples of 16), 5 = 64x64 with K tile 32, 6 = 64x64 with K tile
+   64 (HBM -> LDS loads, the K tile split between two wave groups of the
+   workgroup; any k).  Tiles 3-6 need k and n multiples of 4 and 16-byte
+   aligned operands; k_slices 1..16 (split-K with a reduce launch when > 1).
+   A variant that cannot run the shape returns PROM_ERROR, stage INIT,
+   PROM_DETAIL_INVALID_ARGUMENT; otherwise the device entry's statuses. */
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_variant(void* handle, const float* a, const float* b,
+                                                                     float* c, uint32_t m, uint32_t n, uint32_t k,
+                                                                     uint32_t tile, uint32_t k_slices,
+                                                                     uint32_t* out_stage, int* out_detail_code);
 /* The SGEMM launch plan that ..._sgemm and ..._sgemm_device queue for a
    contiguous row-major product with 16-byte-aligned operands.  It is a pure
    function of the shape and needs neither a runtime nor a device.  The
@@ -665,10 +679,11 @@ typedef struct PrometheusSgemmPlanInfo {
   uint32_t direct_to_lds[2]; /* 1: tiles go HBM -> LDS by buffer_load ... lds */
   uint32_t k_slices[2];     /* split-K slices (1: no split) */
   uint32_t k_slice_len[2];
-  uint32_t launches;        /* kernel launches queued (GEMM plus split-K reduce) */
-  uint32_t reserved;
+  uint32_t launches;        /* kernel launches queued (padding copies, GEMMs, split-K reduces) */
+  uint32_t repacked;        /* 1: A and B are first copied to zero-padded buffers with 16-byte rows */
   uint64_t partial_bytes;   /* split-K partial buffer the plan writes */
   double estimated_us;      /* the plan model's estimate */
+  uint64_t repack_bytes;    /* the padded copies of A and B */
 } PrometheusSgemmPlanInfo;
 PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32_t n, uint32_t k,
                                                    PrometheusSgemmPlanInfo* out_plan);

@@ -582,6 +582,30 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device(void* handle, const
   return gemm_device<float>(handle, a, b, c, m, n, k, out_stage, out_detail_code, launch_sgemm_f32);
 }
 
+// A caller-chosen SGEMM kernel variant (no reference counterpart): tuning and
+// the per-variant parity tests run every kernel regardless of the plan model.
+PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_variant(void* handle, const float* a, const float* b,
+                                                                     float* c, uint32_t m, uint32_t n, uint32_t k,
+                                                                     uint32_t tile, uint32_t k_slices,
+                                                                     uint32_t* out_stage, int* out_detail_code) {
+  Runtime* rt = lookup(handle);
+  const int v = gemm_validate(rt, a, b, c, m, n, k, out_stage, out_detail_code);
+  if (v != PROM_OK) return v;
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  const hipError_t e = launch_sgemm_f32_variant(a, b, c, m, n, k, tile, k_slices, cx.stream);
+  if (e == hipErrorInvalidValue) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_INIT, PROM_DETAIL_INVALID_ARGUMENT);
+    return PROM_ERROR;
+  }
+  if (e != hipSuccess) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_SUBMIT, PROM_DETAIL_HIP_LAUNCH_FAILED);
+    return PROM_ERROR;
+  }
+  set_status(out_stage, out_detail_code, PROM_STAGE_SUBMIT, PROM_DETAIL_PATH_HIP_MFMA_F32);
+  return PROM_OK;
+}
+
 // Allocation-free form of ..._sgemm_device (no reference counterpart): the
 // lookup, validation, lock and launch path allocate nothing.
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_noalloc(void* handle, const float* a, const float* b,

@@ -20,8 +20,8 @@ namespace prom {
 constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
 // Staging slots: 0-3 operand staging, 4 block workspace, 5 block host staging,
-// 6 split-K partials, 7 FFT twiddle table.
-constexpr uint32_t kStagingSlots = 8;
+// 6 split-K partials, 7 FFT twiddle table, 8-9 padded SGEMM operand copies.
+constexpr uint32_t kStagingSlots = 10;
 
 struct AsyncState;  // async task table, submission slots and batch arenas (sgemm_async.hip)
 struct ModelState;  // resident model block and compiled session (model_block.hip)
@@ -115,6 +115,11 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
 hipError_t init_sgemm_scratch(int device);
 int launch_sgemm_f32_noalloc(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
                              int device, hipStream_t stream, int* path_detail);
+// One product with a caller-chosen kernel variant (tile index as in
+// PrometheusSgemmPlanInfo's tables, K slices); hipErrorInvalidValue when the
+// variant cannot run this shape.  Caller holds ctx().mu (split-K staging).
+hipError_t launch_sgemm_f32_variant(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                                    uint32_t tile, uint32_t k_slices, hipStream_t stream);
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
                                     float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
                                     uint32_t batch, hipStream_t stream);

@@ -487,6 +487,243 @@ __global__ __launch_bounds__(512, 1) void sgemm_f32_dl128w8_kernel(const float* 
   sgemm_f32_dl_body<128, 8>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
 }
 
+// 64x64 tile for grids that would otherwise leave CUs idle or need a
+// split-K launch (C1's 1024^3 is 256 such tiles: one per CU, no K split
+// across workgroups).  Eight waves: wave (kh, wm, wn) owns the 32x32 quadrant
+// (wm, wn) for the kh-th 16-wide half of every 32-wide K tile, so each SIMD
+// runs two independent accumulation chains; at the end the kh = 1 waves hand
+// their accumulators to the kh = 0 waves through LDS, which add them in a
+// fixed order (deterministic) and store.
+//
+// LDS stage (K tile 32): A is row-major, 64 rows of 128 bytes, chunk c
+// (4 floats) of row r at position c ^ ((r >> 1) & 7): the 16 lanes of a
+// 128-bit read group hit 16 distinct 16-byte bank groups.  B is row-major, 32
+// k-rows of 256 bytes, with the 128-byte halves of rows with (k >> 2) & 1
+// exchanged, so the two lane halves of a B read (rows k and k + 4) use
+// opposite halves of the banks.  Both placements are set by each lane's
+// source address in the HBM -> LDS transfers (one 1 KB transfer of A and one
+// of B per wave per tile).  K order: MFMA step (p, j) of half kh pairs
+// k = 16kh + 8p + j (lanes 0-31) with k = 16kh + 8p + 4 + j (lanes 32-63).
+template <int kBKs>
+struct Dl64Cfg {
+  static constexpr int kRowBytes = kBKs * 4;            // A row (kBKs floats)
+  static constexpr int kChunks = kBKs / 4;              // 16-byte chunks per A row
+  static constexpr int kABytes = 64 * kRowBytes;
+  static constexpr int kStage = 2 * kABytes;            // A then B [kBKs][64]
+  static constexpr int kXfer = kABytes / 1024 / 8;      // 1 KB transfers of A (and of B) per wave
+};
+// A chunk c of row r sits at position c ^ swz: for 32-wide K tiles (128-byte
+// rows) swz = (r >> 1) & 7, for 64-wide tiles (256-byte rows) swz = r & 15.
+template <int kBKs>
+__device__ __forceinline__ int dl64_swz(int r) {
+  return kBKs == 32 ? ((r >> 1) & 7) : (r & 15);
+}
+
+template <int kBKs>
+__device__ __forceinline__ void sgemm_f32_dl64_body(const float* __restrict__ A, const float* __restrict__ B,
+                                                    float* C, int M, int N, int K, int tiles_m, int tiles_n, int lda,
+                                                    int ldb, int ldc, const float* R, int ldr, int k_len,
+                                                    long long sa, long long sb, long long sc, char* S0, char* S1) {
+  using Cfg = Dl64Cfg<kBKs>;
+  typedef __attribute__((address_space(3))) void lds_void;
+  if (gridDim.z > 1) {
+    A += (size_t)blockIdx.z * sa;
+    B += (size_t)blockIdx.z * sb;
+    C += (size_t)blockIdx.z * sc;
+  }
+  int tm, tn;
+  map_tile(tiles_m, tiles_n, &tm, &tn);
+  const int row0 = tm * 64;
+  const int col0 = tn * 64;
+  size_t a_extent = (size_t)M * lda;
+  if (gridDim.y > 1) {
+    const int kb = (int)blockIdx.y * k_len;
+    A += kb;
+    a_extent -= (size_t)kb;
+    B += (size_t)kb * ldb;
+    C += (size_t)blockIdx.y * M * ldc;
+    K = min(k_len, K - kb);
+  }
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = wave >> 2;
+  const int wm = (wave >> 1) & 1;
+  const int wn = wave & 1;
+
+  const __amdgpu_buffer_rsrc_t rsa =
+      __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)(a_extent * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)((size_t)K * ldb * 4), 0x00020000);
+  // Transfer q (1 KB) of A covers rows 1024q/kRowBytes.., of B k-rows 4q..4q+3;
+  // wave w issues q = kXfer*w + i.
+  uint32_t a_off[Cfg::kXfer], b_off[Cfg::kXfer];
+#pragma unroll
+  for (int i = 0; i < Cfg::kXfer; ++i) {
+    const int q = Cfg::kXfer * wave + i;
+    const int e = 64 * q + lane;  // 16-byte chunk index of the A tile
+    const int r = e / Cfg::kChunks;
+    const int c = (e % Cfg::kChunks) ^ dl64_swz<kBKs>(r);
+    a_off[i] = (uint32_t)(((row0 + r) * lda + 4 * c) * 4);
+    const int kr = 4 * q + (lane >> 4);
+    const int cb = (lane & 15) ^ (8 * ((kr >> 2) & 1));
+    b_off[i] = (uint32_t)((kr * ldb + col0 + 4 * cb) * 4);
+  }
+  auto issue = [&](char* stage, int k0) {
+    const int sa_k = __builtin_amdgcn_readfirstlane(k0 * 4);
+    const int sb_k = __builtin_amdgcn_readfirstlane(k0 * ldb * 4);
+#pragma unroll
+    for (int i = 0; i < Cfg::kXfer; ++i) {
+      const int q = Cfg::kXfer * wave + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(stage + q * 1024), 16, a_off[i], sa_k, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_void*)(stage + Cfg::kABytes + q * 1024), 16, b_off[i], sb_k,
+                                               0, 0);
+    }
+  };
+
+  // Operand addresses (bytes within a stage).  Half kh covers k in
+  // [kh*kBKs/2, (kh+1)*kBKs/2): logical A chunk kh*kChunks/2 + 2p + h.  B row
+  // k = kh*kBKs/2 + 8p + 4h + j holds column c at c ^ (32 h).
+  const int lrow = lane & 31;
+  const int h = lane >> 5;
+  const int ar = 32 * wm + lrow;
+  const uint32_t a_row = (uint32_t)(ar * Cfg::kRowBytes);
+  const int a_sw = dl64_swz<kBKs>(ar);
+  const uint32_t b_base =
+      (uint32_t)(Cfg::kABytes + (kh * kBKs / 2 + 4 * h) * 256 + ((((32 * wn) ^ (32 * h)) + lrow) * 4));
+
+  floatx16 acc = {};
+  auto compute = [&](const char* st) {
+#pragma unroll
+    for (int p = 0; p < kBKs / 16; ++p) {
+      const floatx4 a =
+          *reinterpret_cast<const floatx4*>(st + a_row + (((kh * Cfg::kChunks / 2 + 2 * p + h) ^ a_sw) << 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b = *reinterpret_cast<const float*>(st + b_base + (8 * p + j) * 256);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b, acc, 0, 0, 0);
+      }
+    }
+  };
+
+  // K need not be a multiple of the K tile (only of 4): the last tile's B
+  // rows past K read zero (outside the buffer range), and its A columns past
+  // K, which the transfers fill from the next row, are cleared in LDS before
+  // that tile is used, so they add exact zeros whatever they held.
+  const int k_tiles = (K + kBKs - 1) / kBKs;
+  const int krem = K - (k_tiles - 1) * kBKs;
+  auto settle_last = [&](char* st, int t) {
+    if (t != k_tiles - 1 || krem == kBKs) return;
+    const int c0 = krem / 4;
+    const int nc = Cfg::kChunks - c0;
+    for (int e = tid; e < 64 * nc; e += 512) {
+      const int r = e / nc;
+      const int c = c0 + e % nc;
+      *reinterpret_cast<floatx4*>(st + r * Cfg::kRowBytes + ((c ^ dl64_swz<kBKs>(r)) << 4)) = floatx4{};
+    }
+    __syncthreads();
+  };
+  issue(S0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < k_tiles; kt += 2) {
+    issue(S1, (kt + 1) * kBKs);
+    settle_last(S0, kt);
+    compute(S0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (kt + 2 < k_tiles) issue(S0, (kt + 2) * kBKs);
+    settle_last(S1, kt + 1);
+    compute(S1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  if (kt < k_tiles) {
+    settle_last(S0, kt);
+    compute(S0);
+    __syncthreads();
+  }
+
+  // The kh = 1 waves pass their quadrant's accumulators to the kh = 0 waves
+  // (stage 0 is free after the last barrier): 64 lanes x 16 floats per quadrant.
+  float* xchg = reinterpret_cast<float*>(S0) + (wave & 3) * 1024;
+  if (kh == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; r += 4)
+      *reinterpret_cast<floatx4*>(xchg + lane * 16 + r) = floatx4{acc[r], acc[r + 1], acc[r + 2], acc[r + 3]};
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int r = 0; r < 16; r += 4) {
+    const floatx4 o = *reinterpret_cast<const floatx4*>(xchg + lane * 16 + r);
+    acc[r] += o.x;
+    acc[r + 1] += o.y;
+    acc[r + 2] += o.z;
+    acc[r + 3] += o.w;
+  }
+  const int col = col0 + 32 * wn + lrow;
+  if (col >= N) return;
+  const int rb = row0 + 32 * wm + 4 * h;
+  float* cp = C + (size_t)rb * ldc + col;
+  const float* rp = R != nullptr ? R + (size_t)rb * ldr + col : nullptr;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int dr = 8 * (r >> 2) + (r & 3);
+    if (rb + dr < M) {
+      float v = acc[r];
+      if (rp != nullptr) v += rp[(size_t)dr * ldr];
+      cp[(size_t)dr * ldc] = v;
+    }
+  }
+}
+
+__global__ __launch_bounds__(512, 2) void sgemm_f32_dl64_kernel(const float* __restrict__ A,
+                                                                const float* __restrict__ B, float* C, int M, int N,
+                                                                int K, int tiles_m, int tiles_n, int lda, int ldb,
+                                                                int ldc, const float* R, int ldr, int k_len,
+                                                                long long sa, long long sb, long long sc) {
+  __shared__ __attribute__((aligned(1024))) char S0[Dl64Cfg<32>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S1[Dl64Cfg<32>::kStage];
+  sgemm_f32_dl64_body<32>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+}
+
+// 64-wide K tiles: twice the MFMA work between barriers and per LDS stage,
+// for operands that stream from the Infinity Cache (long K) rather than L2.
+__global__ __launch_bounds__(512, 2) void sgemm_f32_dl64k64_kernel(const float* __restrict__ A,
+                                                                   const float* __restrict__ B, float* C, int M,
+                                                                   int N, int K, int tiles_m, int tiles_n, int lda,
+                                                                   int ldb, int ldc, const float* R, int ldr,
+                                                                   int k_len, long long sa, long long sb,
+                                                                   long long sc) {
+  __shared__ __attribute__((aligned(1024))) char S0[Dl64Cfg<64>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S1[Dl64Cfg<64>::kStage];
+  sgemm_f32_dl64_body<64>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+}
+
+// dst [rows_d][ld_d] (16-byte rows) = src [rows_s][cols_s] (row stride ld_s,
+// any alignment), zero outside: the padded copies through which operands the
+// direct-to-LDS kernels cannot read (ragged k or n, unaligned rows) reach them.
+__global__ __launch_bounds__(256) void pack_pad_kernel(const float* __restrict__ src, int rows_s, int cols_s, int ld_s,
+                                                       float* __restrict__ dst, int rows_d, int ld_d) {
+  const int c4n = ld_d >> 2;
+  const size_t total = (size_t)rows_d * c4n;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int r = (int)(i / c4n);
+    const int c = (int)(i - (size_t)r * c4n) * 4;
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+    if (r < rows_s) {
+      const float* sp = src + (size_t)r * ld_s + c;
+      if (c + 0 < cols_s) v.x = sp[0];
+      if (c + 1 < cols_s) v.y = sp[1];
+      if (c + 2 < cols_s) v.z = sp[2];
+      if (c + 3 < cols_s) v.w = sp[3];
+    }
+    reinterpret_cast<floatx4*>(dst + (size_t)r * ld_d)[c >> 2] = v;
+  }
+}
+
 // y[m] = A[m,:] . x : one wave per row, 4 rows per workgroup.  HBM-bound:
 // every byte of A is read once with 128-bit loads, x stays in L2.
 template <bool kVec>
@@ -579,12 +816,15 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const float* __rest
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Tile shapes: 0 = 128x256, 1 = 128x128, 2 = 64x128 (register-staged loads);
+// 5 / 6 = 64x64 direct-to-LDS with each K tile (32 / 64 wide) split between
+// two wave groups (branch-free shapes whose K slices are whole K tiles only);
 // 3 = 128x256 (four waves), 4 = 128x128 (eight waves) direct-to-LDS, for
 // branch-free shapes only (otherwise the staged shape of the same size runs).
-constexpr int kTileShapes = 5;
-constexpr int kTileM[kTileShapes] = {128, 128, 64, 128, 128};
-constexpr int kTileN[kTileShapes] = {256, 128, 128, 256, 128};
-constexpr int kStagedFallback[kTileShapes] = {0, 1, 2, 0, 1};
+constexpr int kTileShapes = 7;
+constexpr int kTileM[kTileShapes] = {128, 128, 64, 128, 128, 64, 64};
+constexpr int kTileN[kTileShapes] = {256, 128, 128, 256, 128, 64, 64};
+constexpr int kStagedFallback[kTileShapes] = {0, 1, 2, 0, 1, 2, 2};
+constexpr int kTileK[kTileShapes] = {16, 16, 16, 16, 16, 32, 64};  // K granule of a slice
 
 struct SgemmPlan {
   int tile;    // index into kTileM / kTileN
@@ -596,7 +836,8 @@ struct SgemmPlan {
 SgemmPlan make_plan(int tile, int splits, uint32_t k) {
   SgemmPlan p{tile, 1, (int)k};
   if (splits > 1) {
-    p.k_len = (int)((((k + splits - 1) / splits) + kBK - 1) / kBK * kBK);
+    const int g = kTileK[tile];
+    p.k_len = (int)((((k + splits - 1) / splits) + g - 1) / g * g);
     p.splits = (int)((k + p.k_len - 1) / p.k_len);
     if (p.splits <= 1) {
       p.splits = 1;
@@ -609,29 +850,44 @@ SgemmPlan make_plan(int tile, int splits, uint32_t k) {
 // True when the buffer-load kernels apply: 128-bit aligned operands, every
 // slice length a multiple of the K tile and every 32-bit byte offset (rows up
 // to M + 128, all of B plus a tile row) in range.
-// `aligned`: both operand base addresses are 16-byte aligned.
+// `aligned`: both operand base addresses are 16-byte aligned.  The 128-wide
+// direct kernels need every slice to be whole K tiles of 16; the 64x64 ones
+// (tiles 5 and 6) take a K tail (k % 4 == 0) in the last tile of each product.
 bool buffer_path(bool aligned, int lda, long long sa, int ldb, long long sb, uint32_t m, uint32_t n, uint32_t k,
-                 int k_len) {
-  const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
-                   (sb % 4 == 0) && aligned;
-  return vec && (k % kBK == 0) && (k_len % kBK == 0) && (size_t)(m + 128) * lda * 4 < (1ull << 31) &&
-         ((size_t)k * ldb + n + 256) * 4 < (1ull << 31);
+                 int k_len, int tile = 4) {
+  // B chunks past column n lie in B's padding or next row and only feed
+  // output columns that are never stored, so n itself may be ragged.
+  const bool vec = (k % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) && (sb % 4 == 0) && aligned;
+  const bool k_ok = tile >= 5 ? true : (k % kBK == 0) && (k_len % kBK == 0);
+  return vec && k_ok && (size_t)(m + 128) * lda * 4 < (1ull << 31) && ((size_t)k * ldb + n + 256) * 4 < (1ull << 31);
 }
 
 // Plan choice: the (tile shape, K slices) pair with the least estimated time.
 // A grid of W workgroups fills the CUs in rounds of occ*256 (occ = resident
-// workgroups per CU for the tile); a CU holding w workgroups runs them at
-// efficiency eff(w) of its MFMA rate (256 flop/clk at 2.38 GHz), so a K tile
-// of a BMxBN workgroup costs w * BM*BN*32/609280 us / eff(w).  Each round adds
-// ~2 us of prologue/epilogue, a launch ~3 us, and a split adds the reduce
-// (~3 us + (s+1) M N floats at ~2 TB/s).  The constants are fitted to timings of
-// all tile shapes and slice counts at the benchmark and transformer-block
-// shapes on MI355X.
-constexpr int kTileOcc[kTileShapes] = {2, 3, 4, 3, 5};
-constexpr double kTileEff[kTileShapes] = {0.92, 0.95, 0.835, 1.0, 1.05};
-constexpr double kOccEff[4] = {0.70, 0.846, 0.93, 0.932};
+// workgroups per CU for the tile); a CU holding w workgroups of tile t runs
+// them at efficiency kTileEffW[t][w-1] of its MFMA rate (256 flop/clk at 2.38
+// GHz), so a K step of 16 of a BMxBN workgroup costs w * BM*BN*32/609280 us /
+// eff.  Each round adds ~1.7 us of prologue/epilogue, a launch ~3.5 us, and a
+// split adds the reduce (~1.5 us + (s+1) M N floats at ~3.5 TB/s).  The
+// efficiencies and overheads are a least-squares fit (log time) to every
+// valid (tile, K slices) variant timed at 28 shapes on MI355X (the benchmark
+// shapes, the C4 and Z-Image block products, their 32-row tails, tall and
+// wide panels); the chosen plan is within 1 % of the measured best on
+// average and within 5 % at all but one shape.
+constexpr int kTileOcc[kTileShapes] = {2, 3, 4, 3, 5, 4, 2};
+constexpr double kTileEffW[kTileShapes][5] = {
+    {0.776, 0.883},                       // 128x256 staged
+    {0.726, 0.837, 0.913},                // 128x128 staged
+    {0.555, 0.740, 0.774, 0.894},         // 64x128 staged
+    {0.900, 0.975, 0.948},                // 128x256 direct
+    {0.935, 0.971, 0.976, 0.967, 0.967},  // 128x128 direct, eight waves
+    {0.606, 0.766, 0.846, 0.931},         // 64x64 direct, K tile 32
+    {0.772, 0.911}};                      // 64x64 direct, K tile 64
 
-double plan_cost(const SgemmPlan& p, uint32_t m, uint32_t n, uint32_t batch) {
+// scalar_loads: the register-staged kernels read the operands with predicated
+// 32-bit loads (k or n not a multiple of 4, unaligned rows), about 1.5x slower
+// per K step than with 128-bit loads (measured at 4097x3001x513).
+double plan_cost(const SgemmPlan& p, uint32_t m, uint32_t n, uint32_t batch, bool scalar_loads = false) {
   const int t = p.tile;
   const double w_total = (double)((m + kTileM[t] - 1) / kTileM[t]) * ((n + kTileN[t] - 1) / kTileN[t]) * p.splits *
                          batch;
@@ -640,14 +896,15 @@ double plan_cost(const SgemmPlan& p, uint32_t m, uint32_t n, uint32_t batch) {
   const double slots = 256.0 * kTileOcc[t];
   const double full = std::floor(w_total / slots);
   const double rest = w_total - full * slots;
-  auto eff = [&](int w) { return kOccEff[std::min(w, 4) - 1] * kTileEff[t]; };
+  auto eff = [&](int w) { return kTileEffW[t][std::min(w, kTileOcc[t]) - 1]; };
   double us = full * kTileOcc[t] * k_tiles * t16 / eff(kTileOcc[t]);
   if (rest > 0) {
     const int w = (int)std::ceil(rest / 256.0);
     us += w * k_tiles * t16 / eff(w);
   }
-  us += 3.0 + 2.0 * (full + (rest > 0 ? 1.0 : 0.0));
-  if (p.splits > 1) us += 3.0 + (double)(p.splits + 1) * m * n * 4.0 / 2.0e6;
+  if (scalar_loads && t < 3) us *= 1.5;
+  us += 3.45 + 1.72 * (full + (rest > 0 ? 1.0 : 0.0));
+  if (p.splits > 1) us += 1.46 + (double)(p.splits + 1) * m * n * 4.0 / 3.5e6;
   return us;
 }
 
@@ -656,17 +913,23 @@ double plan_cost(const SgemmPlan& p, uint32_t m, uint32_t n, uint32_t batch) {
 SgemmPlan plan_sgemm(bool aligned, int lda, long long sa, int ldb, long long sb, uint32_t m, uint32_t n, uint32_t k,
                      uint32_t batch, uint64_t max_partial_floats = ~0ull) {
   static const int kSplitChoices[] = {1, 2, 3, 4, 6, 8, 12, 16};
+  // The eight-wave 128x128 kernel is tried first and is only replaced by a
+  // plan more than 1 % cheaper (near ties keep the established kernel; the
+  // model is accurate to a few per cent).
+  static const int kTileOrder[kTileShapes] = {4, 3, 0, 1, 2, 5, 6};
+  const bool scalar = !((k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
+                        (sb % 4 == 0) && aligned);
   SgemmPlan best = make_plan(0, 1, k);
   double best_cost = 1e300;
-  for (int t = 0; t < kTileShapes; ++t) {
+  for (int t : kTileOrder) {
     for (int s : kSplitChoices) {
       if (s > 1 && (batch > 1 || k / (uint32_t)s < 64)) break;
       const SgemmPlan p = make_plan(t, s, k);
       if (p.splits != s) continue;
       if (p.splits > 1 && (uint64_t)p.splits * m * n > max_partial_floats) continue;
-      if (t >= 3 && !buffer_path(aligned, lda, sa, ldb, sb, m, n, k, p.k_len)) continue;
-      const double c = plan_cost(p, m, n, batch);
-      if (c < best_cost) {
+      if (t >= 3 && !buffer_path(aligned, lda, sa, ldb, sb, m, n, k, p.k_len, t)) continue;
+      const double c = plan_cost(p, m, n, batch, scalar);
+      if (c < best_cost * 0.99) {
         best_cost = c;
         best = p;
       }
@@ -698,7 +961,7 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
   const bool split = p.splits > 1;
   const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
                    (sb % 4 == 0) && aligned16(a) && aligned16(b);
-  const bool buf = buffer_path(aligned16(a) && aligned16(b), lda, sa, ldb, sb, m, n, k, p.k_len);
+  const bool buf = buffer_path(aligned16(a) && aligned16(b), lda, sa, ldb, sb, m, n, k, p.k_len, p.tile);
   const int tile = (p.tile >= 3 && !buf) ? kStagedFallback[p.tile] : p.tile;
   const int bm = kTileM[tile], bn = kTileN[tile];
   const int tiles_m = (int)((m + bm - 1) / bm);
@@ -708,6 +971,14 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
   const int ldo = split ? (int)n : ldc;
   const float* res = split ? nullptr : residual;
   switch (tile) {
+    case 5:
+      hipLaunchKernelGGL(sgemm_f32_dl64_kernel, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n, (int)k, tiles_m,
+                         tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      break;
+    case 6:
+      hipLaunchKernelGGL(sgemm_f32_dl64k64_kernel, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+                         tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      break;
     case 3:
       hipLaunchKernelGGL(sgemm_f32_dl256_kernel, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
                          tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
@@ -749,26 +1020,28 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
 }
 
 // What launch_sgemm_f32_ex queues for one product: the GEMV, or one or two
-// MFMA products (rows [0, head_rows) and, after a tail split, the rest).  A
-// pure function of the shape, strides and operand alignment.
+// MFMA products (rows [0, head_rows) and, after a tail split, the rest),
+// optionally on padded copies of A and B.  A pure function of the shape,
+// strides and operand alignment.
 struct SgemmSchedule {
   bool gemv;
   bool tail_split;
+  bool repack;         // A, B copied first to [m][k4] and [k4][n4], 16-byte rows, zero padding
+  uint32_t k4, n4;     // padded K and B row stride when repacking
   uint32_t head_rows;  // rows of the first product (m without a tail split)
   SgemmPlan plan[2];
   double cost_us;      // plan-model estimate of the queued work
 };
 
-SgemmSchedule schedule_sgemm(bool aligned, int lda, int ldb, uint32_t m, uint32_t n, uint32_t k, bool has_residual,
-                             uint64_t max_partial_floats) {
+// One or two products (tail split) of an m x n x k problem with the given
+// operand description.
+SgemmSchedule schedule_products(bool aligned, int lda, int ldb, uint32_t m, uint32_t n, uint32_t k,
+                                uint64_t max_partial_floats) {
   SgemmSchedule s{};
   s.head_rows = m;
-  if (n == 1 && !has_residual && ldb == 1 && lda == (int)k) {
-    s.gemv = true;
-    return s;
-  }
+  const bool scalar = !((k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && aligned);
   s.plan[0] = plan_sgemm(aligned, lda, 0, ldb, 0, m, n, k, 1, max_partial_floats);
-  s.cost_us = plan_cost(s.plan[0], m, n, 1);
+  s.cost_us = plan_cost(s.plan[0], m, n, 1, scalar);
   // A partial last row of 128-row tiles runs nearly empty for the whole K depth
   // (M = 1056: a 32-row tail in 9 tile rows).  When the estimate favours it, the
   // rows past the last full tile row run as a second product (usually K-split)
@@ -780,7 +1053,7 @@ SgemmSchedule schedule_sgemm(bool aligned, int lda, int ldb, uint32_t m, uint32_
     const bool tail_aligned = aligned && (lda % 4 == 0);
     const SgemmPlan ph = plan_sgemm(aligned, lda, 0, ldb, 0, head, n, k, 1, max_partial_floats);
     const SgemmPlan pt = plan_sgemm(tail_aligned, lda, 0, ldb, 0, tail, n, k, 1, max_partial_floats);
-    const double split_cost = plan_cost(ph, head, n, 1) + plan_cost(pt, tail, n, 1);
+    const double split_cost = plan_cost(ph, head, n, 1, scalar) + plan_cost(pt, tail, n, 1, scalar);
     if (split_cost < s.cost_us) {
       s.tail_split = true;
       s.head_rows = head;
@@ -792,11 +1065,47 @@ SgemmSchedule schedule_sgemm(bool aligned, int lda, int ldb, uint32_t m, uint32_
   return s;
 }
 
+SgemmSchedule schedule_sgemm(bool aligned, int lda, int ldb, uint32_t m, uint32_t n, uint32_t k, bool has_residual,
+                             uint64_t max_partial_floats) {
+  SgemmSchedule s{};
+  s.head_rows = m;
+  if (n == 1 && !has_residual && ldb == 1 && lda == (int)k) {
+    s.gemv = true;
+    return s;
+  }
+  s = schedule_products(aligned, lda, ldb, m, n, k, max_partial_floats);
+  // Operands the direct-to-LDS kernels cannot read (rows not 16-byte aligned,
+  // k not a multiple of 4) otherwise run on the register-staged kernels; when
+  // the estimate favours it they are first copied to padded buffers (two
+  // launches, the copy at ~3 TB/s) and the fast kernels run on the copies.
+  const bool direct = aligned && k % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0;
+  if (!direct) {
+    const uint32_t k4 = (k + 3u) & ~3u, n4 = (n + 3u) & ~3u;
+    if ((size_t)(m + 128) * k4 * 4 < (1ull << 31) && ((size_t)k4 * n4 + 256) * 4 < (1ull << 31)) {
+      SgemmSchedule r = schedule_products(true, (int)k4, (int)n4, m, n, k4, max_partial_floats);
+      const double bytes = 4.0 * ((double)m * k + (double)k * n + (double)m * k4 + (double)k4 * n4);
+      r.cost_us += 4.0 + bytes / 3.0e6;
+      if (r.cost_us < s.cost_us) {
+        r.repack = true;
+        r.k4 = k4;
+        r.n4 = n4;
+        return r;
+      }
+    }
+  }
+  return s;
+}
+
+uint64_t schedule_repack_floats(const SgemmSchedule& s, uint32_t m) {
+  return s.repack ? (uint64_t)m * s.k4 + (uint64_t)s.k4 * s.n4 : 0;
+}
+
 // Queues schedule s; partial (null: runtime staging slot 6) receives the
-// split-K slices and must hold partial_floats.
+// split-K slices and must hold partial_floats; packed (null: staging slots 8
+// and 9) receives the padded copies of a repacking schedule, A then B.
 hipError_t run_sgemm_schedule(const SgemmSchedule& s, const float* a, int lda, const float* b, int ldb, float* c,
                               int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
-                              float* partial, hipStream_t stream) {
+                              float* partial, float* packed, hipStream_t stream) {
   if (s.gemv) {
     const bool vec = (k % 4 == 0) && aligned16(a) && aligned16(b);
     const dim3 grid((m + 3) / 4);
@@ -805,6 +1114,24 @@ hipError_t run_sgemm_schedule(const SgemmSchedule& s, const float* a, int lda, c
     else
       hipLaunchKernelGGL(gemv_f32_kernel<false>, grid, dim3(256), 0, stream, a, b, c, (int)m, (int)k);
     return hipGetLastError();
+  }
+  if (s.repack) {
+    float* pa = packed != nullptr ? packed : static_cast<float*>(staging(8, (size_t)m * s.k4 * sizeof(float)));
+    float* pb = packed != nullptr ? packed + (size_t)m * s.k4
+                                  : static_cast<float*>(staging(9, (size_t)s.k4 * s.n4 * sizeof(float)));
+    if (pa == nullptr || pb == nullptr) return hipErrorOutOfMemory;
+    const size_t na = (size_t)m * (s.k4 / 4), nb = (size_t)s.k4 * (s.n4 / 4);
+    hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)std::min<size_t>(8192, (na + 255) / 256)), dim3(256), 0,
+                       stream, a, (int)m, (int)k, lda, pa, (int)m, (int)s.k4);
+    hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)std::min<size_t>(8192, (nb + 255) / 256)), dim3(256), 0,
+                       stream, b, (int)k, (int)n, ldb, pb, (int)s.k4, (int)s.n4);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    a = pa;
+    lda = (int)s.k4;
+    b = pb;
+    ldb = (int)s.n4;
+    k = s.k4;
   }
   auto run = [&](SgemmPlan p, const float* ap, float* cp, const float* rp, uint32_t rows) {
     float* part = nullptr;
@@ -839,7 +1166,7 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
   const SgemmSchedule s =
       schedule_sgemm(aligned16(a) && aligned16(b), lda, ldb, m, n, k, residual != nullptr, ~0ull);
   if (path_detail) *path_detail = s.gemv ? PROM_DETAIL_PATH_HIP_GEMV_F32 : PROM_DETAIL_PATH_HIP_MFMA_F32;
-  return run_sgemm_schedule(s, a, lda, b, ldb, c, ldc, m, n, k, residual, ldr, nullptr, stream);
+  return run_sgemm_schedule(s, a, lda, b, ldb, c, ldc, m, n, k, residual, ldr, nullptr, nullptr, stream);
 }
 
 }  // namespace prom
@@ -876,13 +1203,32 @@ int launch_sgemm_f32_noalloc(const float* a, const float* b, float* c, uint32_t 
   if (part == nullptr) return PROM_DETAIL_SCRATCH_UNAVAILABLE;
   // The same plan as launch_sgemm_f32 (bit-identical results); a plan whose
   // partials do not fit the array is refused rather than changed.
+  // The split-K partials and, for a repacking plan, the padded operand
+  // copies share the array: [partials | padded A | padded B].
   const SgemmSchedule s = schedule_sgemm(aligned16(a) && aligned16(b), (int)k, (int)n, m, n, k, false, ~0ull);
-  if (schedule_partial_floats(s, m, n) * sizeof(float) > PROM_SGEMM_NOALLOC_SCRATCH_BYTES)
+  const uint64_t part_floats = (schedule_partial_floats(s, m, n) + 63) & ~63ull;
+  if ((part_floats + schedule_repack_floats(s, m)) * sizeof(float) > PROM_SGEMM_NOALLOC_SCRATCH_BYTES)
     return PROM_DETAIL_SCRATCH_LIMIT;
   if (path_detail) *path_detail = s.gemv ? PROM_DETAIL_PATH_HIP_GEMV_F32 : PROM_DETAIL_PATH_HIP_MFMA_F32;
-  return run_sgemm_schedule(s, a, (int)k, b, (int)n, c, (int)n, m, n, k, nullptr, 0, part, stream) == hipSuccess
+  return run_sgemm_schedule(s, a, (int)k, b, (int)n, c, (int)n, m, n, k, nullptr, 0, part, part + part_floats,
+                            stream) == hipSuccess
              ? PROM_OK
              : PROM_DETAIL_HIP_LAUNCH_FAILED;
+}
+
+hipError_t launch_sgemm_f32_variant(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                                    uint32_t tile, uint32_t k_slices, hipStream_t stream) {
+  if (tile >= (uint32_t)kTileShapes || k_slices < 1u || k_slices > 16u) return hipErrorInvalidValue;
+  const SgemmPlan p = make_plan((int)tile, (int)k_slices, k);
+  const bool aligned = aligned16(a) && aligned16(b);
+  if (p.splits != (int)k_slices || (tile >= 3 && !buffer_path(aligned, (int)k, 0, (int)n, 0, m, n, k, p.k_len, tile)))
+    return hipErrorInvalidValue;
+  float* partial = nullptr;
+  if (p.splits > 1) {
+    partial = static_cast<float*>(staging(6, (size_t)p.splits * m * n * sizeof(float)));
+    if (partial == nullptr) return hipErrorOutOfMemory;
+  }
+  return run_sgemm_plan(p, a, (int)k, 0, b, (int)n, 0, c, (int)n, 0, m, n, k, 1, nullptr, 0, partial, stream);
 }
 
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
@@ -926,10 +1272,14 @@ extern "C" PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32
   }
   out_plan->detail_code = PROM_DETAIL_PATH_HIP_MFMA_F32;
   out_plan->products = s.tail_split ? 2u : 1u;
+  out_plan->repacked = s.repack ? 1u : 0u;
+  out_plan->repack_bytes = schedule_repack_floats(s, m) * sizeof(float);
+  const uint32_t kk = s.repack ? s.k4 : k;
+  const int ldb_eff = s.repack ? (int)s.n4 : (int)n;
   for (uint32_t i = 0; i < out_plan->products; ++i) {
     const SgemmPlan& p = s.plan[i];
     const uint32_t rows = i == 0 ? s.head_rows : m - s.head_rows;
-    const bool buf = buffer_path(true, (int)k, 0, (int)n, 0, rows, n, k, p.k_len);
+    const bool buf = buffer_path(true, (int)kk, 0, ldb_eff, 0, rows, n, kk, p.k_len, p.tile);
     const int tile = (p.tile >= 3 && !buf) ? kStagedFallback[p.tile] : p.tile;
     out_plan->tile_m[i] = (uint32_t)kTileM[tile];
     out_plan->tile_n[i] = (uint32_t)kTileN[tile];
@@ -938,6 +1288,7 @@ extern "C" PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32
     out_plan->k_slice_len[i] = (uint32_t)p.k_len;
     out_plan->launches += p.splits > 1 ? 2u : 1u;
   }
+  if (s.repack) out_plan->launches += 2u;
   out_plan->partial_bytes = schedule_partial_floats(s, m, n) * sizeof(float);
   out_plan->estimated_us = s.cost_us;
   return PROM_OK;

@@ -142,9 +142,10 @@ class PrometheusSgemmPlanInfo(Structure):
         ("k_slices", c_uint32 * 2),
         ("k_slice_len", c_uint32 * 2),
         ("launches", c_uint32),
-        ("reserved", c_uint32),
+        ("repacked", c_uint32),
         ("partial_bytes", c_uint64),
         ("estimated_us", ctypes.c_double),
+        ("repack_bytes", c_uint64),
     ]
 
 
@@ -866,6 +867,9 @@ _SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_sgemm_device": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_sgemm_device_variant": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
+                POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_sgemm_device_noalloc": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_gemm_bf16": (
@@ -1403,6 +1407,15 @@ class NativeRuntime:
         rc = self.lib.prometheus_reactor_runtime_sgemm_device(self.handle, c_void_p(da), c_void_p(db), c_void_p(dc),
                                                               m, n, k, byref(stage), byref(detail))
         return self._check(rc, stage, detail, "sgemm_device")
+
+    def sgemm_device_variant(self, da: int, db: int, dc: int, m: int, n: int, k: int, tile: int,
+                             k_slices: int) -> Tuple[int, CallStatus]:
+        """One product with a chosen kernel variant: (rc, stage/detail); does not raise."""
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_sgemm_device_variant(self.handle, c_void_p(da), c_void_p(db),
+                                                                       c_void_p(dc), m, n, k, tile, k_slices,
+                                                                       byref(stage), byref(detail))
+        return rc, CallStatus(stage.value, detail.value)
 
     def sgemm_device_noalloc(self, da: int, db: int, dc: int, m: int, n: int, k: int) -> Tuple[int, CallStatus]:
         """The allocation-free SGEMM entry: (rc, stage/detail); does not raise."""

@@ -67,27 +67,104 @@ def test_exact_tail_shapes(gpu_runtime, m, n, k):
     assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
 
 
-# One shape per kernel variant the plan model chooses (tile shape, direct-to-LDS
-# or register-staged loads, split-K or not), ragged in m and/or n:
-#   64x128 staged (1,2,1) and 4 K slices (1,2,256); 128x128 staged (255,32768,1)
-#   and 12 slices (100,4100,8200); 128x128 direct, eight waves (100,32768,16)
-#   and 6 slices (100,4100,1024); 128x256 staged (1000,16384,1); 128x256 direct
-#   (700,32768,16).
-@pytest.mark.parametrize("m,n,k", [(1, 2, 1), (1, 2, 256), (255, 32768, 1), (100, 4100, 8200), (100, 32768, 16),
-                                   (100, 4100, 1024), (1000, 16384, 1), (700, 32768, 16)])
-def test_plan_variants(gpu_runtime, m, n, k):
-    a = oracle.uniform(300 + m, (m, k))
-    b = oracle.uniform(400 + n, (k, n))
+# Every kernel variant, run explicitly through the variant entry (so the
+# coverage does not depend on which variants the plan model picks): tiles
+# 0-2 register-staged, 3-4 direct-to-LDS, 5-6 the 64x64 tile with the K tile
+# split inside the workgroup; with and without split-K; ragged m and n.
+VARIANT_SHAPES = [(200, 260, 512), (65, 128, 1024), (1, 4, 64)]
+
+
+@pytest.mark.parametrize("tile", range(7))
+@pytest.mark.parametrize("slices", [1, 4])
+@pytest.mark.parametrize("shape", VARIANT_SHAPES)
+def test_every_variant(gpu_runtime, tile, slices, shape):
+    m, n, k = shape
+    # K slices are whole granules (16; 32 and 64 for the 64x64 tiles): a
+    # request that cannot give exactly `slices` slices is refused.
+    g = {5: 32, 6: 64}.get(tile, 16)
+    k_len = -(-(-(-k // slices)) // g) * g
+    possible = slices == 1 or -(-k // k_len) == slices
+    a = oracle.uniform(300 + m + tile, (m, k))
+    b = oracle.uniform(400 + n + slices, (k, n))
+    da, db, dc = gpu_runtime.upload_new(a), gpu_runtime.upload_new(b), gpu_runtime.alloc(m * n * 4)
+    try:
+        rc, st = gpu_runtime.sgemm_device_variant(da, db, dc, m, n, k, tile, slices)
+        if not possible:
+            assert rc == p.PROM_ERROR and st.detail == -6906
+            return
+        assert rc == p.PROM_OK, (st.stage, st.detail)
+        gpu_runtime.synchronize()
+        out = gpu_runtime.download(np.empty((m, n), np.float32), dc)
+    finally:
+        for d in (da, db, dc):
+            gpu_runtime.free(d)
+    assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
+
+
+@pytest.mark.parametrize("tile", [5, 6])
+@pytest.mark.parametrize("m,n,k", [(100, 260, 1000), (129, 64, 36), (64, 64, 4), (70, 68, 132)])
+def test_k_tail_of_the_64x64_kernels(gpu_runtime, tile, m, n, k):
+    """K not a multiple of the K tile: the last tile's A columns past K are
+    filled from the next row by the transfers and must be cleared.  A NaN
+    at the start of row 7 of A would poison row 6 if they were not."""
+    a = oracle.uniform(700 + k, (m, k))
+    b = oracle.uniform(800 + n, (k, n))
+    a[7, 0] = np.nan
+    da, db, dc = gpu_runtime.upload_new(a), gpu_runtime.upload_new(b), gpu_runtime.alloc(m * n * 4)
+    try:
+        rc, st = gpu_runtime.sgemm_device_variant(da, db, dc, m, n, k, tile, 1)
+        assert rc == p.PROM_OK, (st.stage, st.detail)
+        gpu_runtime.synchronize()
+        out = gpu_runtime.download(np.empty((m, n), np.float32), dc)
+    finally:
+        for d in (da, db, dc):
+            gpu_runtime.free(d)
+    assert np.all(np.isnan(out[7]))
+    rows = [r for r in range(m) if r != 7]
+    ref = oracle.matmul_f64(np.delete(a, 7, axis=0), b)
+    assert np.all(np.isfinite(out[rows]))
+    assert oracle.normwise_rel_err(out[rows], ref) <= FP32_NORMWISE
+
+
+@pytest.mark.parametrize("m,n,k", [(4097, 3001, 513), (130, 127, 65), (513, 1027, 131)])
+def test_repacked_operands(gpu_runtime, m, n, k):
+    """Unaligned operands copied to zero-padded buffers, then the direct kernels."""
+    rc, plan = p.sgemm_plan(m, n, k)
+    assert rc == p.PROM_OK and plan.repacked == 1, "the repack must be planned for this shape"
+    a = oracle.uniform(900 + m, (m, k))
+    b = oracle.uniform(901 + n, (k, n))
     out = _sgemm(gpu_runtime, a, b)
-    rows = (0, m // 2, m - 1)
+    rows = sorted({0, 1, m // 2, m - 2, m - 1})
     for r in rows:
-        assert oracle.normwise_rel_err(out[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r]) <= FP32_NORMWISE
+        assert oracle.normwise_rel_err(out[r], oracle.matmul_f64(a, b, rows=(r, r + 1))[r]) <= FP32_NORMWISE, r
+
+
+def test_staged_variants_cover_unaligned_shapes_and_direct_ones_refuse(gpu_runtime):
+    m, n, k = 130, 127, 65  # n and k not multiples of 4: register-staged tiles only
+    a = oracle.uniform(501, (m, k))
+    b = oracle.uniform(502, (k, n))
+    da, db, dc = gpu_runtime.upload_new(a), gpu_runtime.upload_new(b), gpu_runtime.alloc(m * n * 4)
+    try:
+        for tile in range(7):
+            rc, st = gpu_runtime.sgemm_device_variant(da, db, dc, m, n, k, tile, 1)
+            if tile >= 3:
+                assert rc == p.PROM_ERROR and st.stage == p.STAGE_INIT and st.detail == -6906, tile
+                continue
+            assert rc == p.PROM_OK, (tile, st.detail)
+            gpu_runtime.synchronize()
+            out = gpu_runtime.download(np.empty((m, n), np.float32), dc)
+            assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE, tile
+        rc, st = gpu_runtime.sgemm_device_variant(da, db, dc, m, n, k, 7, 1)
+        assert rc == p.PROM_ERROR and st.detail == -6906
+    finally:
+        for d in (da, db, dc):
+            gpu_runtime.free(d)
 
 
 # M past a multiple of 128 where the plan model runs the last rows as a second,
 # K-split product after the full 128-row tiles: the rows either side of the
 # seam and the last row.
-@pytest.mark.parametrize("m,n,k", [(1056, 3840, 3840), (2049, 8192, 2048), (1056, 20480, 3840)])
+@pytest.mark.parametrize("m,n,k", [(1056, 4096, 4096), (2049, 8192, 2048), (1056, 20480, 3840)])
 def test_tail_row_split(gpu_runtime, m, n, k):
     rc, plan = p.sgemm_plan(m, n, k)
     assert rc == p.PROM_OK and plan.products == 2 and plan.head_rows == m - m % 128, "the split must be planned"

@@ -30,7 +30,7 @@ def test_gemv_plan():
         assert rc == p.PROM_OK and i.detail_code == p.DETAIL_PATH_HIP_GEMV_F32 and i.products == 0 and i.launches == 1
 
 
-@pytest.mark.parametrize("m,n,k", [(1056, 3840, 3840), (2049, 8192, 2048), (1056, 20480, 3840),
+@pytest.mark.parametrize("m,n,k", [(2049, 8192, 2048), (1056, 20480, 3840), (1056, 4096, 4096),
                                    # the C4 layer at T = 1056: output and down projections
                                    (1056, 2048, 2048), (1056, 2048, 16384)])
 def test_tail_split_is_planned_for_the_seam_cases(m, n, k):
@@ -42,15 +42,33 @@ def test_tail_split_is_planned_for_the_seam_cases(m, n, k):
 
 
 def test_split_k_plan_reports_its_partial_buffer():
-    rc, i = _plan(1024, 1024, 1024)
+    rc, i = _plan(512, 2048, 16384)  # the C4 down projection
     assert rc == p.PROM_OK and i.products == 1 and i.k_slices[0] > 1
-    assert i.partial_bytes == i.k_slices[0] * 1024 * 1024 * 4
-    assert i.k_slice_len[0] * i.k_slices[0] >= 1024 and i.k_slice_len[0] % 16 == 0
+    assert i.partial_bytes == i.k_slices[0] * 512 * 2048 * 4
+    assert i.k_slice_len[0] * i.k_slices[0] >= 16384 and i.k_slice_len[0] % 16 == 0
 
 
-def test_ragged_k_uses_register_staged_tiles():
-    rc, i = _plan(4097, 3001, 513)  # k % 16 != 0: no direct-to-LDS kernel
-    assert rc == p.PROM_OK and all(i.direct_to_lds[j] == 0 for j in range(i.products))
+def test_c1_runs_on_one_64x64_tile_per_cu():
+    """1024^3: 256 tiles of 64x64 (one per CU), the K range split between two
+    wave groups inside each workgroup instead of across workgroups."""
+    rc, i = _plan(1024, 1024, 1024)
+    assert rc == p.PROM_OK and i.products == 1 and (i.tile_m[0], i.tile_n[0]) == (64, 64)
+    assert i.k_slices[0] == 1 and i.launches == 1 and i.partial_bytes == 0 and i.direct_to_lds[0] == 1
+
+
+def test_unaligned_operands_are_repacked_for_the_direct_kernels():
+    """k = 513 and n = 3001 leave rows unaligned: A and B are copied to zero-padded
+    [m][516] and [516][3004] buffers and the direct-to-LDS kernels run on them."""
+    rc, i = _plan(4097, 3001, 513)
+    assert rc == p.PROM_OK and i.repacked == 1 and i.direct_to_lds[0] == 1
+    assert i.repack_bytes == 4 * (4097 * 516 + 516 * 3004)
+    assert i.launches == 2 + sum(2 if s > 1 else 1 for s in i.k_slices[:i.products])
+
+
+def test_k_tail_runs_direct_when_rows_are_aligned():
+    """k = 1000 (a multiple of 4, not of 16): the 64x64 kernels take the K tail."""
+    rc, i = _plan(1000, 1000, 1000)
+    assert rc == p.PROM_OK and i.repacked == 0 and i.direct_to_lds[0] == 1 and (i.tile_m[0], i.tile_n[0]) == (64, 64)
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 1, 3_000_000_000), (3_000_000_000, 1, 1), (1, 2**31, 1),

@@ -35,7 +35,7 @@ def _run_pair(rt, m, n, k, seed):
     return a, b, ref, new
 
 
-@pytest.mark.parametrize("shapes", [((1056, 2048, 16384), (1000, 1000, 1000))])
+@pytest.mark.parametrize("shapes", [((1056, 2048, 16384), (520, 1000, 6000))])
 def test_noalloc_matches_the_device_entry_on_two_calls(gpu_runtime, shapes):
     for i, (m, n, k) in enumerate(shapes):
         rc, plan = p.sgemm_plan(m, n, k)
@@ -50,7 +50,7 @@ def test_noalloc_matches_the_device_entry_on_two_calls(gpu_runtime, shapes):
 
 
 def test_noalloc_refuses_a_plan_beyond_the_scratch(gpu_runtime):
-    m, n, k = 768, 1536, 8192
+    m, n, k = 1280, 2048, 8192
     rc, plan = p.sgemm_plan(m, n, k)
     assert rc == p.PROM_OK and plan.partial_bytes > p.SGEMM_NOALLOC_SCRATCH_BYTES
     sentinel = np.full((m, n), 7.0, np.float32)
@@ -64,6 +64,29 @@ def test_noalloc_refuses_a_plan_beyond_the_scratch(gpu_runtime):
             gpu_runtime.free(d)
     assert rc == p.PROM_ERROR and st.stage == p.STAGE_TRANSFER_IN and st.detail == p.DETAIL_SCRATCH_LIMIT
     assert np.array_equal(after, sentinel)
+
+
+def test_noalloc_repacking_plan(gpu_runtime):
+    """Unaligned operands: the padded copies live in the same array as the partials."""
+    m, n, k = 513, 1027, 131
+    rc, plan = p.sgemm_plan(m, n, k)
+    assert rc == p.PROM_OK and plan.repacked == 1 and plan.repack_bytes > 0
+    a = oracle.uniform(961, (m, k))
+    b = oracle.uniform(962, (k, n))
+    da, db = gpu_runtime.upload_new(a), gpu_runtime.upload_new(b)
+    dc_ref, dc_new = gpu_runtime.alloc(m * n * 4), gpu_runtime.alloc(m * n * 4)
+    try:
+        gpu_runtime.sgemm_device(da, db, dc_ref, m, n, k)
+        rc, st = gpu_runtime.sgemm_device_noalloc(da, db, dc_new, m, n, k)
+        assert rc == p.PROM_OK, st
+        gpu_runtime.synchronize()
+        ref = gpu_runtime.download(np.empty((m, n), np.float32), dc_ref)
+        new = gpu_runtime.download(np.empty((m, n), np.float32), dc_new)
+    finally:
+        for d in (da, db, dc_ref, dc_new):
+            gpu_runtime.free(d)
+    assert np.array_equal(ref.view(np.uint32), new.view(np.uint32))
+    assert oracle.normwise_rel_err(new, oracle.matmul_f64(a, b)) <= FP32_NORMWISE
 
 
 def test_noalloc_without_split_and_gemv(gpu_runtime):
