@@ -14,13 +14,16 @@
 // factorisation N = N1 * N2 (N1, N2 <= 1024 for N <= 2^20), with n = N2*n1 + n2
 // and k = k1 + N1*k2:
 //   pass 1: for every column n2, an N1-point transform over x[N2*n1 + n2],
-//           multiplied by W_N^(n2*k1) on the way out and stored as T[k1*N2 + n2];
-//   pass 2: for every row k1, an N2-point transform over T[k1*N2 + n2], stored
+//           multiplied by W_N^(n2*k1) on the way out and stored as T(k1, n2);
+//   pass 2: for every row k1, an N2-point transform over T(k1, n2), stored
 //           to X[k1 + N1*k2].
-// Each workgroup takes several adjacent columns (rows) so that its strided
-// loads and stores touch contiguous runs; the whole 16 MiB working set of a
-// 2^20-point transform stays resident in the MI355X's 256 MiB Infinity Cache
-// between the passes.
+// T holds its rows in tiles of G = 4096/N2 (T(k1, n2) at
+// (k1/G)*N2*G + n2*G + k1%G), so that pass 2 reads whole tiles.
+// Both passes run fft_wave_pass_kernel: a wave holds 1024 points in
+// registers, a workgroup four adjacent columns (rows), so that strided loads
+// and stores touch 64-byte runs; the whole 16 MiB working set of a 2^20-point
+// transform stays resident in the MI355X's 256 MiB Infinity Cache between the
+// passes.
 #include <math.h>
 #include <string.h>
 
@@ -337,6 +340,252 @@ __global__ __launch_bounds__(1024) void fft_reg16_wide_kernel(const double2* __r
                        seq_fast_in, seq_fast_out);
 }
 
+// ---------------------------------------------------------------------------
+// Four-step passes of the long transforms (N > 4096, sub-transform lengths
+// L in [64, 1024]).  One wave holds 1024 elements in registers, 16 per lane:
+// 1024/L whole sequences.  Element e of a wave (e = s*L + pos, position pos of
+// its sequence s in bit-reversed order) moves through three register phases,
+// each running the butterfly stages of four bits of pos:
+//   phase 1: lane = e bits 4-9,        element j = e bits 0-3 (stages 1-4);
+//   phase 2: lane = e bits 0-3, 8-9,   j = e bits 4-7         (stages 5-8);
+//   phase 3: lane = e bits 0-3, 6-7,   j = e bits 4-5, 8-9    (stages 9-10).
+// Between phases the wave exchanges its elements through its own 16 KiB of
+// LDS (16-byte slot e ^ ((e >> 4) & 15): the 16 lanes of each access touch 16
+// distinct bank groups); LDS operations of one wave complete in order, so the
+// exchange needs no workgroup barrier and the four waves of a workgroup run
+// their stages independently.  Each butterfly is the reference's (same
+// operands, twiddle W_L^((p mod half) * L/2^t), no contraction); only the
+// order in which independent butterflies run differs from fft_reg16_kernel.
+// Global loads and stores run in memory order through a workgroup tile
+// (fft_wave_pass_body); each thread issues all 16 of its loads at once (64 KiB
+// per workgroup in flight).
+//
+// Twiddles come from a compact per-length table built on the host from the
+// same roots: the stage twiddles of each pass (L/2 entries), lo[j] = W_N^j
+// (j < 1024) and hi[h] = W_N^(1024 h) (h < N/1024), staged in LDS once per
+// workgroup.  The four-step twiddle W_N^p, p = n2 * k1, is hi[p >> 10] *
+// lo[p & 1023] (one extra rounded product; well inside fft.go:176-192's
+// 1e-12 agreement bound), which replaces a scattered read of the N/2-entry
+// roots table per output element.
+constexpr uint32_t kPassWaves = 4;
+constexpr uint32_t kWaveElems = 1024;
+
+__device__ __forceinline__ uint32_t xslot(uint32_t e) { return e ^ ((e >> 4) & 15u); }
+
+__device__ __forceinline__ void butterfly(double2& x, double2& y, double2 w) {
+#pragma clang fp contract(off)
+  const double2 t = cmul(w, y);
+  const double2 u = x;
+  x = make_double2(u.x + t.x, u.y + t.y);
+  y = make_double2(u.x - t.x, u.y - t.y);
+}
+
+// A workgroup takes R = 4096/L adjacent sequences q = blk*R + r.  Pass 1
+// (kColumns) reads column q of x (element i at x[i*N2 + q]) and writes the
+// twiddled outputs to T in tiles of G = 4096/N2 rows, T[(k/G)*N2*G + q*G + k%G];
+// pass 2 reads row q of T (element i at T[(q/G)*N2*G + i*G + q%G], R = G, so one
+// workgroup's rows are one contiguous 64 KiB tile) and writes X[q + k*N1].  The
+// global loads and stores go in memory order through a 64 KiB LDS tile (the
+// 16-byte slot of tile index f at sslot(f)): inputs f = i*R + r, outputs
+// f = ((k/G)*R + r)*G + k%G in pass 1 and f = k*R + r in pass 2, so
+// consecutive lanes move consecutive addresses -- runs of 64 bytes (the
+// column reads and the final transposed writes at L = 1024), 256 bytes (the
+// tiled T writes) or whole tiles (the T reads).  The tile and the waves'
+// exchange buffers share the same LDS, ordered by workgroup barriers.
+__device__ __forceinline__ uint32_t sslot(uint32_t f) { return f ^ ((f >> 4) & 15u) ^ ((f >> 8) & 15u); }
+// Pass 1's output tile: bits 4-7 enter rotated by two, which keeps the tiled
+// (k/G, r, k%G) order conflict-free at N >= 2^19 (at most two-way below).
+__device__ __forceinline__ uint32_t oslot1(uint32_t f) {
+  const uint32_t x = (f >> 4) & 15u;
+  return f ^ (((x << 2) | (x >> 2)) & 15u) ^ ((f >> 8) & 15u);
+}
+
+template <bool kColumns>
+__device__ __forceinline__ void fft_wave_pass_body(const double2* __restrict__ in, double2* __restrict__ out,
+                                                   const double2* __restrict__ tables, uint32_t log2l,
+                                                   uint32_t tw_off, uint32_t lo_off, uint32_t hi_count,
+                                                   uint32_t log2n1, uint32_t log2n2) {
+#pragma clang fp contract(off)
+  extern __shared__ double2 smem[];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = tid >> 6;
+  const uint32_t L = 1u << log2l;
+  const uint32_t lgr = 12u - log2l;  // log2 of sequences per workgroup
+  const uint32_t lgg = 12u - log2n2;  // log2 of the T tile height G
+  const uint32_t lgs = 10u - log2l;  // log2 of sequences per wave
+  double2* xb = smem + wave * kWaveElems;
+  double2* tw = smem + kPassWaves * kWaveElems;
+  double2* lo = tw + (L >> 1);
+  double2* hi = lo + 1024;
+  uint32_t blk = blockIdx.x;
+  if ((gridDim.x & 7u) == 0u) blk = (blk & 7u) * (gridDim.x >> 3) + (blk >> 3);
+  const uint64_t qwg = (uint64_t)blk << lgr;
+  const uint64_t q0 = qwg + ((uint64_t)wave << lgs);
+
+  // Table entries of this thread (tw: L/2 <= 512, lo: 1024, hi: N/1024 <= 1024
+  // entries over 256 threads) and the 16 tile elements: every load is issued
+  // before the first LDS store (a loop of load-then-store waits one memory
+  // round trip per iteration).  Table indices past the end are clamped, so
+  // the surplus threads load and store the last entry again (same value,
+  // same slot).
+  constexpr uint32_t kT = kPassWaves * 64;
+  const uint32_t tw_last = (L >> 1) - 1u, hi_last = hi_count - 1u;
+  double2 rt[2], rl[4], rh[4];
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) rt[u] = tables[tw_off + min(tid + u * kT, tw_last)];
+  if constexpr (kColumns) {
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+      rl[u] = tables[lo_off + tid + u * kT];
+      rh[u] = tables[lo_off + 1024u + min(tid + u * kT, hi_last)];
+    }
+  }
+  {
+    double2 v[16];
+#pragma unroll
+    for (uint32_t m = 0; m < 16; ++m) {
+      const uint32_t f = tid + m * kT;
+      const uint32_t r = f & ((1u << lgr) - 1u);
+      const uint64_t i = f >> lgr;
+      v[m] = kColumns ? in[qwg + r + (i << log2n2)] : in[(qwg << log2n2) + (i << lgg) + r];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) tw[min(tid + u * kT, tw_last)] = rt[u];
+    if constexpr (kColumns) {
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u) {
+        lo[tid + u * kT] = rl[u];
+        hi[min(tid + u * kT, hi_last)] = rh[u];
+      }
+    }
+#pragma unroll
+    for (uint32_t m = 0; m < 16; ++m) smem[sslot(tid + m * kT)] = v[m];
+  }
+  __syncthreads();
+
+  // phase-1 reads: lane holds positions 16 b .. 16 b + 15 of its sequence s1,
+  // i.e. inputs rev(b) + m * L/16 (see fft_reg16_body)
+  const uint32_t lgq = log2l - 4u;
+  const uint32_t s1 = lane >> lgq;
+  const uint32_t b1 = lane & ((1u << lgq) - 1u);
+  const uint32_t base = __brev(b1) >> (32u - lgq);
+  const uint32_t r1 = (wave << lgs) | s1;
+  double2 a[16];
+#pragma unroll
+  for (uint32_t m = 0; m < 16; ++m) {
+    const uint32_t k = ((m & 1u) << 3) | ((m & 2u) << 1) | ((m & 4u) >> 1) | ((m & 8u) >> 3);  // rev4(m)
+    const uint32_t i = base + (m << lgq);
+    a[k] = smem[sslot((i << lgr) | r1)];
+  }
+  __syncthreads();  // the tile is consumed; the exchange buffers overlay it
+
+  // phase 1: stages 1-4 on the lane's 16 consecutive positions
+#pragma unroll
+  for (uint32_t t = 1; t <= 4; ++t) {
+    const uint32_t half = 1u << (t - 1);
+#pragma unroll
+    for (uint32_t p = 0; p < 16; ++p) {
+      if (p & half) continue;
+      butterfly(a[p], a[p + half], tw[(p & (half - 1)) << (log2l - t)]);
+    }
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < 16; ++j) xb[xslot(16u * lane + j)] = a[j];
+  __builtin_amdgcn_wave_barrier();
+
+  // phase 2: stages 5-8 (those below log2l)
+  const uint32_t e2 = (lane & 15u) | ((lane >> 4) << 8);
+#pragma unroll
+  for (uint32_t j = 0; j < 16; ++j) a[j] = xb[xslot(e2 | (j << 4))];
+#pragma unroll
+  for (uint32_t t = 5; t <= 8; ++t) {
+    if (t > log2l) break;
+    const uint32_t hj = 1u << (t - 5);
+    const uint32_t pmask = (1u << (t - 1)) - 1u;
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j) {
+      if (j & hj) continue;
+      const uint32_t pos = (e2 | (j << 4)) & (L - 1u);
+      butterfly(a[j], a[j + hj], tw[(pos & pmask) << (log2l - t)]);
+    }
+  }
+  uint32_t e_lane = e2, e_j[16];
+#pragma unroll
+  for (uint32_t j = 0; j < 16; ++j) e_j[j] = j << 4;
+  if (log2l >= 9) {
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j) xb[xslot(e2 | (j << 4))] = a[j];
+    __builtin_amdgcn_wave_barrier();
+    // phase 3: stages 9-10
+    const uint32_t e3 = (lane & 15u) | (((lane >> 4) & 3u) << 6);
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j) e_j[j] = ((j & 3u) << 4) | ((j >> 2) << 8);
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j) a[j] = xb[xslot(e3 | e_j[j])];
+#pragma unroll
+    for (uint32_t t = 9; t <= 10; ++t) {
+      if (t > log2l) break;
+      const uint32_t hj = 4u << (t - 9);
+      const uint32_t pmask = (1u << (t - 1)) - 1u;
+#pragma unroll
+      for (uint32_t j = 0; j < 16; ++j) {
+        if (j & hj) continue;
+        const uint32_t pos = (e3 | e_j[j]) & (L - 1u);
+        butterfly(a[j], a[j + hj], tw[(pos & pmask) << (log2l - t)]);
+      }
+    }
+    e_lane = e3;
+  }
+
+  // outputs: element j of the lane is position k of sequence s, staged
+  // through the tile in output memory order
+  __syncthreads();  // every wave is done with its exchange buffer
+#pragma unroll
+  for (uint32_t j = 0; j < 16; ++j) {
+    const uint32_t e = e_lane | e_j[j];
+    const uint32_t s = e >> log2l;
+    const uint32_t k = e & (L - 1u);
+    double2 r = a[j];
+    if constexpr (kColumns) {
+      const uint64_t p = (q0 + s) * (uint64_t)k;  // < N
+      r = cmul(cmul(hi[p >> 10], lo[p & 1023u]), r);
+    }
+    const uint32_t rq = (wave << lgs) | s;
+    const uint32_t f = kColumns ? (((((k >> lgg) << lgr) | rq) << lgg) | (k & ((1u << lgg) - 1u))) : ((k << lgr) | rq);
+    smem[kColumns ? oslot1(f) : sslot(f)] = r;
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t m = 0; m < 16; ++m) {
+    const uint32_t f = tid + m * kT;
+    if constexpr (kColumns) {
+      const uint64_t kk = f & ((1u << lgg) - 1u);
+      const uint64_t r = (f >> lgg) & ((1u << lgr) - 1u);
+      const uint64_t kg = f >> (lgg + lgr);
+      out[(kg << (log2n2 + lgg)) + ((qwg + r) << lgg) + kk] = smem[oslot1(f)];
+    } else {
+      const uint32_t r = f & ((1u << lgr) - 1u);
+      const uint64_t k = f >> lgr;
+      out[qwg + r + (k << log2n1)] = smem[sslot(f)];
+    }
+  }
+}
+
+// Pass 1 (twiddled outputs) and pass 2.  At most two workgroups fit a CU's
+// LDS (104 or 72 KiB each), so the kernels may use 256 VGPRs.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void fft_wave_pass1_kernel(
+    const double2* __restrict__ in, double2* __restrict__ out, const double2* __restrict__ tables, uint32_t log2l,
+    uint32_t tw_off, uint32_t lo_off, uint32_t hi_count, uint32_t log2n1, uint32_t log2n2) {
+  fft_wave_pass_body<true>(in, out, tables, log2l, tw_off, lo_off, hi_count, log2n1, log2n2);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void fft_wave_pass2_kernel(
+    const double2* __restrict__ in, double2* __restrict__ out, const double2* __restrict__ tables, uint32_t log2l,
+    uint32_t tw_off, uint32_t lo_off, uint32_t hi_count, uint32_t log2n1, uint32_t log2n2) {
+  fft_wave_pass_body<false>(in, out, tables, log2l, tw_off, lo_off, hi_count, log2n1, log2n2);
+}
+
 uint32_t ilog2(uint32_t v) {
   uint32_t r = 0;
   while ((1u << r) < v) ++r;
@@ -391,10 +640,45 @@ hipError_t launch_pass(const double2* in, double2* out, const double2* roots, ui
   return hipGetLastError();
 }
 
+// One four-step pass of an n = 2^(log2n1 + log2n2) point transform
+// (n in (4096, 2^20], N1 = 2^log2n1 >= N2): n/4096 workgroups of four waves,
+// 1024 elements per wave; post selects pass 1 (columns of x to tiled T).
+hipError_t launch_wave_pass(const double2* in, double2* out, const double2* tables, uint32_t log2n1,
+                            uint32_t log2n2, uint32_t tw_off, uint32_t lo_off, int post, hipStream_t stream) {
+  const uint32_t log2l = post ? log2n1 : log2n2;
+  const uint32_t n = 1u << (log2n1 + log2n2);
+  if (log2n2 < 6 || log2n1 > 10 || log2n1 < log2n2) return hipErrorInvalidValue;
+  static bool lds_raised = false;
+  const uint32_t max_elems = kPassWaves * kWaveElems + 512 + 1024 + 1024;
+  if (!lds_raised) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_wave_pass1_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)(max_elems * sizeof(double2)));
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_wave_pass2_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)(max_elems * sizeof(double2)));
+    if (e != hipSuccess) return e;
+    lds_raised = true;
+  }
+  const uint32_t hi_count = n / 1024;
+  const size_t lds = (kPassWaves * kWaveElems + (1u << log2l) / 2 + (post ? 1024 + hi_count : 0)) * sizeof(double2);
+  const dim3 grid(n / (kPassWaves * kWaveElems)), block(64 * kPassWaves);
+  if (post)
+    hipLaunchKernelGGL(fft_wave_pass1_kernel, grid, block, lds, stream, in, out, tables, log2l, tw_off, lo_off,
+                       hi_count, log2n1, log2n2);
+  else
+    hipLaunchKernelGGL(fft_wave_pass2_kernel, grid, block, lds, stream, in, out, tables, log2l, tw_off, lo_off,
+                       hi_count, log2n1, log2n2);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 // Twiddles for length n (reactor_concept_fft.cpp:50-57 computes the same
-// table on the host and caches it per length).  Caller holds ctx().mu.
+// table on the host and caches it per length).  For n > 4096 the compact
+// tables of the four-step passes follow the n/2 roots (fft_wave_pass_kernel):
+// pass-1 stage twiddles (N1/2), pass-2 stage twiddles (N2/2), lo (1024), hi
+// (n/1024), each entry copied from the roots (hi[h] = W_n^(1024 h), negated
+// from roots[1024 h - n/2] past the half).  Caller holds ctx().mu.
 const double2* fft64_roots(uint32_t n) {
   DeviceContext& c = ctx();
   if (c.fft_roots_n == n && c.fft_roots != nullptr) return static_cast<const double2*>(c.fft_roots);
@@ -406,6 +690,19 @@ const double2* fft64_roots(uint32_t n) {
     const double angle = -2.0 * pi / (double)n * (double)j;
     host[2 * j] = cos(angle);
     host[2 * j + 1] = sin(angle);
+  }
+  if (n > kFftMaxLds) {
+    const uint32_t log2n = ilog2(n), n1 = 1u << ((log2n + 1) / 2), n2 = n / n1;
+    auto push = [&](uint64_t idx) {  // W_n^idx, idx < n
+      const bool neg = idx >= n / 2;
+      const uint64_t r = neg ? idx - n / 2 : idx;
+      host.push_back(neg ? -host[2 * r] : host[2 * r]);
+      host.push_back(neg ? -host[2 * r + 1] : host[2 * r + 1]);
+    };
+    for (uint32_t j = 0; j < n1 / 2; ++j) push((uint64_t)j * n2);
+    for (uint32_t j = 0; j < n2 / 2; ++j) push((uint64_t)j * n1);
+    for (uint32_t j = 0; j < 1024; ++j) push(j);
+    for (uint32_t h = 0; h < n / 1024; ++h) push((uint64_t)h * 1024);
   }
   void* dev = staging(7, host.size() * sizeof(double));
   if (dev == nullptr) return nullptr;
@@ -427,11 +724,13 @@ hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const do
   if (n <= kFftMaxLds) return launch_pass(in, out, roots, n, log2n, 0, 0, 1, 0, 1, 0, 0, 0, stream);
   const uint32_t log2n1 = (log2n + 1) / 2, log2n2 = log2n - log2n1;
   const uint64_t n1 = 1ull << log2n1, n2 = 1ull << log2n2;
-  // pass 1: N2 columns of length N1 (stride N2), twiddled, to T[k1*N2 + n2]
-  hipError_t e = launch_pass(in, temp, roots, n, log2n1, log2n2, 1, n2, 1, n2, 1, 1, 1, stream);
+  const double2* tables = roots + n / 2;
+  const uint32_t tw2_off = (uint32_t)(n1 / 2), lo_off = (uint32_t)(n1 / 2 + n2 / 2);
+  // pass 1: N2 columns of length N1 (stride N2), twiddled, to T (tiled rows k1)
+  hipError_t e = launch_wave_pass(in, temp, tables, log2n1, log2n2, 0, lo_off, 1, stream);
   if (e != hipSuccess) return e;
-  // pass 2: N1 rows of length N2 (contiguous), to X[k1 + N1*k2]
-  return launch_pass(temp, out, roots, n, log2n2, log2n1, n2, 1, 1, n1, 0, 0, 1, stream);
+  // pass 2: N1 rows of length N2, to X[k1 + N1*k2]
+  return launch_wave_pass(temp, out, tables, log2n1, log2n2, tw2_off, lo_off, 0, stream);
 }
 
 }  // namespace prom

@@ -136,7 +136,8 @@ hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w
 // points and is used when n > 4096.  roots comes from fft64_roots(n).
 hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,
                         hipStream_t stream);
-// Device twiddle table for length n (cached; caller holds ctx().mu).
+// Device twiddle table for length n (cached; caller holds ctx().mu): the n/2
+// roots, followed for n > 4096 by the four-step passes' compact tables.
 const double2* fft64_roots(uint32_t n);
 hipError_t launch_row_reduction(const float* in, float* out, uint32_t rows, uint32_t width, uint32_t op,
                                 hipStream_t stream);
