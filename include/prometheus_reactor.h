@@ -657,6 +657,20 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_variant(void* handl
                                                                      float* c, uint32_t m, uint32_t n, uint32_t k,
                                                                      uint32_t tile, uint32_t k_slices,
                                                                      uint32_t* out_stage, int* out_detail_code);
+/* No counterpart in the reference (its attention exists only inside the
+   Z-Image block shaders, main_transformer_joint_attention_streaming.sdslv):
+   the bf16 flash attention of the DiT block on device pointers, for its own
+   parity tests and tuning.  O = softmax(Q K^T / sqrt(128)) V per head, full
+   attention; q, k, v, o are bf16 [tokens, ld] with head h at column 128 h,
+   16-byte aligned, ld a multiple of 8 and >= 128 * heads, tokens * ld * 2 <
+   2^31.  variant 0 = the block's kernel (DMA-fed), 1 = the register-staged
+   kernel.  Invalid arguments: PROM_ERROR, stage INIT,
+   PROM_DETAIL_INVALID_ARGUMENT.  Queued on the runtime's stream. */
+PROM_REACTOR_API int prometheus_reactor_runtime_attention_bf16_device(void* handle, const uint16_t* q,
+                                                                      const uint16_t* k, const uint16_t* v,
+                                                                      uint16_t* o, uint32_t tokens, uint32_t heads,
+                                                                      uint32_t ld, uint32_t variant,
+                                                                      uint32_t* out_stage, int* out_detail_code);
 /* The SGEMM launch plan that ..._sgemm and ..._sgemm_device queue for a
    contiguous row-major product with 16-byte-aligned operands.  It is a pure
    function of the shape and needs neither a runtime nor a device.  The

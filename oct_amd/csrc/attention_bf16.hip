@@ -24,6 +24,13 @@
 //     P and O go to bf16 with the hardware round-to-nearest-even pair
 //     conversion (VALU work per tile is the bound of this kernel, not MFMA);
 //   * the output tile is staged through LDS for 128-bit coalesced stores.
+//
+// Two kernels share that design: flash_attn_bf16_dma_kernel (the DiT block's,
+// tiles moved HBM -> LDS by DMA, less VALU work per tile; see its comment)
+// and flash_attn_bf16_kernel (tiles staged through registers), kept as the
+// cross-check of the parity tests.
+#include <type_traits>
+
 #include "reactor_internal.h"
 
 namespace prom {
@@ -223,14 +230,253 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
   }
 }
 
+// ---------------------------------------------------------------------------
+// Default kernel: the same work mapping, operand layouts and arithmetic as
+// flash_attn_bf16_kernel, with the per-tile VALU work cut down -- this kernel
+// is bound by VALU issue (its MFMAs are 32 per tile per wave, its softmax
+// about as many cycles), and the register-staged tile loads spent a third of
+// that VALU work on 64-bit address arithmetic:
+//   * K and V tiles go HBM -> LDS by buffer_load ... lds (16 bytes per lane,
+//     offsets precomputed once) into unpadded 256-byte rows, two stages each
+//     (64 KiB, two workgroups per CU): no global-load addresses, no staging
+//     registers, no LDS stores.  K row r keeps 16-byte chunk c at slot
+//     c ^ (r & 15), so each 16-lane group of the S^T operand reads (16 rows,
+//     one chunk) hits 16 distinct bank groups; V row r keeps chunk c at
+//     c ^ 4(r & 3), so the transpose reads (4 rows x 16 d per 16-lane group,
+//     two groups side by side) are conflict-free over 32 lanes;
+//   * the tile maximum is a chain of three-input maxima;
+//   * the running sum adds the bf16 P values themselves, two per
+//     v_dot2_f32_bf16 against (1, 1): the normaliser is the sum of exactly the
+//     weights the P V MFMAs use, and half the additions;
+//   * the running sum stays a per-lane partial; its two lane halves are added
+//     once at the end.
+// The transfers are inline assembly (M0 = the wave's 1 KiB LDS destination,
+// M0 declared clobbered) and the waits before each barrier too: the compiler
+// would otherwise wait for every transfer before the next LDS read (it cannot
+// tell the stages apart), or drop a builtin wait it considers satisfied.
+constexpr int kTileB = kKB * kD * 2;  // one K or V tile, 16 KiB
+constexpr int kDmaLds = 4 * kTileB;   // K and V, two stages each
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+struct Bf16Pairs {
+  bf16x2 v[4];
+};
+
+__global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint16_t* __restrict__ Q,
+                                                                     const uint16_t* __restrict__ K,
+                                                                     const uint16_t* __restrict__ V,
+                                                                     uint16_t* __restrict__ O, int T, int ldq,
+                                                                     int ldk, int ldv, int ldo, float scale_log2) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int head = (int)blockIdx.y;
+  const int q0 = (int)blockIdx.x * (4 * kQW) + wave * kQW;
+  const int lq = lane & 31;
+  const int hi = lane >> 5;
+  const int qi = q0 + lq;
+  const int n_tiles = (T + kKB - 1) / kKB;
+
+  // HBM -> LDS transfers; the buffer range ends with the head's last row
+  // (row T-1, 128 columns), so the rows of the last tile past T read zero.
+  typedef int int4v __attribute__((ext_vector_type(4)));
+  auto desc = [](const void* ptr, uint32_t bytes) {
+    const unsigned long long a = (unsigned long long)ptr;
+    int4v d;
+    d.x = __builtin_amdgcn_readfirstlane((int)(a & 0xffffffffu));
+    d.y = __builtin_amdgcn_readfirstlane((int)(a >> 32));
+    d.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    d.w = 0x00020000;
+    return d;
+  };
+  const int4v rs_k = desc(K + head * kD, (uint32_t)(((size_t)(T - 1) * ldk + kD) * 2));
+  const int4v rs_v = desc(V + head * kD, (uint32_t)(((size_t)(T - 1) * ldv + kD) * 2));
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // 1 KiB block 4*wave + i of a tile: rows 16*wave + 4i .. +3, lane -> (row, slot)
+    const int row = 16 * wave + 4 * i + (lane >> 4);
+    const int slot = lane & 15;
+    koff[i] = (uint32_t)((row * ldk + 8 * (slot ^ (row & 15))) * 2);
+    voff[i] = (uint32_t)((row * ldv + 8 * (slot ^ (4 * (row & 3)))) * 2);
+  }
+  auto issue = [&](const int4v& rs, const uint32_t* off, char* st, uint32_t add) {
+    const uint32_t base = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)st;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t la = __builtin_amdgcn_readfirstlane(base + (4 * wave + i) * 1024);
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(off[i] + add),
+                   "s"(rs)
+                   : "memory", "m0");
+    }
+  };
+  auto issue_tile = [&](int j) {
+    issue(rs_k, koff, lds + (j & 1) * kTileB, (uint32_t)(j * kKB * ldk * 2));
+    issue(rs_v, voff, lds + (2 + (j & 1)) * kTileB, (uint32_t)(j * kKB * ldv * 2));
+  };
+
+  bf16x8 qf[8];
+  {
+    const uint16_t* qrow = Q + (size_t)qi * ldq + head * kD;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (qi < T) v = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * hi);
+      qf[s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  // operand addresses within a stage (bytes)
+  const int k_lane = lq * 256;
+  const int k_swz = lq & 15;
+  const int tr_row = 4 * hi + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int v_swz = 4 * (tr_row & 3);
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+
+  floatx16 o[4] = {};
+  float m_run = kNegBig;
+  float l_part = 0.0f;  // this lane half's share of the running sum
+
+  // One tile; kStage (0 or 1) is a compile-time constant so that the stage
+  // offsets fold into the LDS instructions' offset fields.
+  auto tile = [&](int t, auto stage_c) {
+    constexpr int kStage = decltype(stage_c)::value;
+    const int k0 = t * kKB;
+    // tile t has landed (this wave's transfers; the barrier covers the
+    // others'), and every wave is past tile t-1, whose stages take tile t+1
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + 1 < n_tiles) issue_tile(t + 1);
+    const char* kst = lds + kStage * kTileB;
+    const char* vst = lds + (2 + kStage) * kTileB;
+
+    // S^T for two 32-key blocks (raw scores)
+    floatx16 s0 = {}, s1 = {};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int off = ((2 * s + hi) ^ k_swz) << 4;
+      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kst + k_lane + off);
+      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(kst + k_lane + 32 * 256 + off);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[s], s1, 0, 0, 0);
+    }
+    if (k0 + kKB > T) {  // the last, partial tile: keys past T get a huge negative score
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 8 * (r >> 2) + 4 * hi + (r & 3);
+        if (k0 + kr >= T) s0[r] = kNegBig;
+        if (k0 + 32 + kr >= T) s1[r] = kNegBig;
+      }
+    }
+    float mt = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int r = 1; r < 16; ++r) asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mt) : "v"(mt), "v"(s0[r]), "v"(s1[r]));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt * scale_log2);
+    if (__builtin_amdgcn_read_exec() & __ballot(m_new > m_run)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    }
+    m_run = m_new;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, -m_new));
+      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, -m_new));
+    }
+    // P^T operands (keys of chunk c in the accumulator's order, see
+    // flash_attn_bf16_kernel), and their sum two at a time
+    bf16x8 pc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const floatx16& sb = (c < 2) ? s0 : s1;
+      const int base = 8 * (c & 1);
+      pc[c] = bf16x8{(__bf16)sb[base + 0], (__bf16)sb[base + 1], (__bf16)sb[base + 2], (__bf16)sb[base + 3],
+                     (__bf16)sb[base + 4], (__bf16)sb[base + 5], (__bf16)sb[base + 6], (__bf16)sb[base + 7]};
+      const Bf16Pairs pairs = __builtin_bit_cast(Bf16Pairs, pc[c]);
+#pragma unroll
+      for (int pr = 0; pr < 4; ++pr) l_part = __builtin_amdgcn_fdot2_f32_bf16(pairs.v[pr], ones, l_part, false);
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int col = tr_col + 32 * db;
+        const int coff = (((col >> 3) ^ v_swz) << 4) + ((col & 7) << 1);
+        const char* r0 = vst + (16 * c + tr_row) * 256 + coff;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)r0);
+        const s16x4 hv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r0 + 8 * 256));
+        const bf16x8 vt = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hv, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt, pc[c], o[db], 0, 0, 0);
+      }
+    }
+  };
+  issue_tile(0);
+  const std::integral_constant<int, 0> st0{};
+  const std::integral_constant<int, 1> st1{};
+  int t = 0;
+  for (; t + 1 < n_tiles; t += 2) {
+    tile(t, st0);
+    tile(t + 1, st1);
+  }
+  if (t < n_tiles) tile(t, st0);
+
+  // Normalise and stage the wave's [32 q][128 d] output through LDS (34 KiB
+  // from offset 0); the barrier ends every wave's reads of the stages.
+  __syncthreads();
+  const float l_run = l_part + __shfl_xor(l_part, 32, 64);
+  uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + wave * (kQW * kKP);
+  const float inv_l = 1.0f / l_run;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * db + 8 * (r >> 2) + 4 * hi + (r & 3);
+      stage[lq * kKP + d] = __builtin_bit_cast(uint16_t, (__bf16)(o[db][r] * inv_l));
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int c = lane + 64 * u;
+    const int row = c >> 4;
+    const int dc = (c & 15) * 8;
+    const int q = q0 + row;
+    if (q < T)
+      *reinterpret_cast<u32x4*>(O + (size_t)q * ldo + head * kD + dc) =
+          *reinterpret_cast<const u32x4*>(&stage[row * kKP + dc]);
+  }
+}
+
 }  // namespace
 
-// Q/K/V/O bf16 [T, ld*] with `heads` heads of 128 columns each.
+// Q/K/V/O bf16 [T, ld*] with `heads` heads of 128 columns each.  variant 0
+// is the DMA-fed kernel, 1 the register-staged one (kept as a cross-check).
 hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v, int ldv,
-                                  uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream) {
+                                  uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream,
+                                  int variant) {
   const dim3 grid((unsigned)((T + 4 * kQW - 1) / (4 * kQW)), (unsigned)heads);
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(flash_attn_bf16_kernel, grid, dim3(256), 0, stream, q, k, v, o, T, ldq, ldk, ldv, ldo,
+  if (variant == 1) {
+    hipLaunchKernelGGL(flash_attn_bf16_kernel, grid, dim3(256), 0, stream, q, k, v, o, T, ldq, ldk, ldv, ldo,
+                       scale_log2);
+    return hipGetLastError();
+  }
+  if (variant != 0) return hipErrorInvalidValue;
+  static bool lds_raised = false;
+  if (!lds_raised) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(flash_attn_bf16_dma_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kDmaLds);
+    if (e != hipSuccess) return e;
+    lds_raised = true;
+  }
+  hipLaunchKernelGGL(flash_attn_bf16_dma_kernel, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk, ldv, ldo,
                      scale_log2);
   return hipGetLastError();
 }

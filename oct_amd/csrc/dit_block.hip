@@ -29,9 +29,6 @@
 
 namespace prom {
 
-hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v, int ldv,
-                                  uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream);
-
 namespace {
 
 using rows::f2bf;
@@ -224,7 +221,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, Q, K, V,
                      T, H, eps);
   PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_flash_attn_bf16(Q, D, K, D, V, D, O, D, T, H, 1.0f / sqrtf(128.0f), st));
+  PROM_STEP(launch_flash_attn_bf16(Q, D, K, D, V, D, O, D, T, H, 1.0f / sqrtf(128.0f), st, 0));
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, proj, nullptr, D, T, D, D, nullptr, 0, st, nullptr));
   hipLaunchKernelGGL(rows::resid_norm_mod_kernel<uint16_t>, row_grid, blk, 0, st, r->input, proj, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
                      R, Fb, T, D, eps);

@@ -566,8 +566,10 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_
 constexpr int kBK4 = 32;
 constexpr int kStage4 = kBM2 * kBK4 * 2 + kBK4 * kBN2 * 2;  // 16 KB A + 16 KB B
 
-// s_waitcnt vmcnt(n) with the LDS and export counters left free (gfx9 encoding).
-#define PROM_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+// s_waitcnt vmcnt(n), as inline assembly: the compiler does not see the
+// transfers (inline assembly), and could drop a builtin wait it considers
+// already satisfied.
+#define PROM_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
 
 __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");

@@ -606,6 +606,45 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_variant(void* handl
   return PROM_OK;
 }
 
+// bf16 flash attention on device pointers (no reference counterpart: the
+// reference's attention exists only inside its Z-Image block shaders).  The
+// DiT block calls the same launcher; this entry gives the kernel its own
+// parity tests.  Scale 1/sqrt(128) (the block's).
+PROM_REACTOR_API int prometheus_reactor_runtime_attention_bf16_device(void* handle, const uint16_t* q,
+                                                                      const uint16_t* k, const uint16_t* v,
+                                                                      uint16_t* o, uint32_t tokens, uint32_t heads,
+                                                                      uint32_t ld, uint32_t variant,
+                                                                      uint32_t* out_stage, int* out_detail_code) {
+  Runtime* rt = lookup(handle);
+  set_status(out_stage, out_detail_code, PROM_STAGE_NONE, 0);
+  if (rt == nullptr) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_INIT, PROM_INVALID_HANDLE);
+    return PROM_INVALID_HANDLE;
+  }
+  auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const bool ok = q != nullptr && k != nullptr && v != nullptr && o != nullptr && aligned(q) && aligned(k) &&
+                  aligned(v) && aligned(o) && tokens != 0u && heads != 0u && (uint64_t)heads * 128u <= ld &&
+                  ld % 8u == 0u && (uint64_t)tokens * ld * 2u <= 0x7fffffffull && variant <= 1u;
+  if (!ok) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_INIT, PROM_DETAIL_INVALID_ARGUMENT);
+    return PROM_ERROR;
+  }
+  if (!rt->available) {
+    set_status(out_stage, out_detail_code, PROM_STAGE_INIT, rt->init_detail);
+    return PROM_ERROR;
+  }
+  DeviceContext& cx = ctx();
+  std::lock_guard<std::mutex> lock(cx.mu);
+  if (launch_flash_attn_bf16(q, (int)ld, k, (int)ld, v, (int)ld, o, (int)ld, (int)tokens, (int)heads,
+                             1.0f / sqrtf(128.0f), cx.stream, (int)variant) != hipSuccess) {
+    (void)hipGetLastError();
+    set_status(out_stage, out_detail_code, PROM_STAGE_SUBMIT, PROM_DETAIL_HIP_LAUNCH_FAILED);
+    return PROM_ERROR;
+  }
+  set_status(out_stage, out_detail_code, PROM_STAGE_SUBMIT, 0);
+  return PROM_OK;
+}
+
 // Allocation-free form of ..._sgemm_device (no reference counterpart): the
 // lookup, validation, lock and launch path allocate nothing.
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_noalloc(void* handle, const float* a, const float* b,

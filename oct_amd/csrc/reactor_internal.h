@@ -132,6 +132,12 @@ hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint
 // hipErrorNotSupported, launching nothing, when the shape is outside the fused path.
 hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w13, uint16_t* h, int ldh, uint32_t m,
                                    uint32_t f, uint32_t k, hipStream_t stream);
+// bf16 flash attention, head dim 128, full (non-causal): Q/K/V/O [T, ld*] with
+// head h at column 128 h.  variant 0: software-pipelined kernel (80 KiB of
+// dynamic LDS); 1: the serial kernel.  hipErrorInvalidValue for other variants.
+hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v, int ldv,
+                                  uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream,
+                                  int variant);
 // Binary64 FFT of n = 2^k <= 2^20 points (interleaved complex); temp holds n
 // points and is used when n > 4096.  roots comes from fft64_roots(n).
 hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,

@@ -54,6 +54,7 @@ DETAIL_PATH_HIP_MFMA_F32 = 6120
 DETAIL_PATH_HIP_GEMV_F32 = 6121
 DETAIL_PATH_HIP_MFMA_BF16 = 6122
 DETAIL_HIP_UNAVAILABLE = -6905
+DETAIL_INVALID_ARGUMENT = -6906
 DETAIL_SCRATCH_LIMIT = -6930
 DETAIL_SCRATCH_UNAVAILABLE = -6931
 SGEMM_NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -872,6 +873,9 @@ _SIGNATURES = {
                 POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_sgemm_device_noalloc": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
+    "prometheus_reactor_runtime_attention_bf16_device": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
+                POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_gemm_bf16": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_int)]),
     "prometheus_reactor_runtime_gemm_bf16_device": (
@@ -1415,6 +1419,15 @@ class NativeRuntime:
         rc = self.lib.prometheus_reactor_runtime_sgemm_device_variant(self.handle, c_void_p(da), c_void_p(db),
                                                                        c_void_p(dc), m, n, k, tile, k_slices,
                                                                        byref(stage), byref(detail))
+        return rc, CallStatus(stage.value, detail.value)
+
+    def attention_bf16_device(self, dq: int, dk: int, dv: int, do: int, tokens: int, heads: int, ld: int,
+                              variant: int = 0) -> Tuple[int, CallStatus]:
+        """bf16 flash attention on device buffers [tokens, ld]: (rc, stage/detail); does not raise."""
+        stage, detail = c_uint32(0), c_int(0)
+        rc = self.lib.prometheus_reactor_runtime_attention_bf16_device(self.handle, c_void_p(dq), c_void_p(dk),
+                                                                        c_void_p(dv), c_void_p(do), tokens, heads,
+                                                                        ld, variant, byref(stage), byref(detail))
         return rc, CallStatus(stage.value, detail.value)
 
     def sgemm_device_noalloc(self, da: int, db: int, dc: int, m: int, n: int, k: int) -> Tuple[int, CallStatus]:

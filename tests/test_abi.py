@@ -526,3 +526,21 @@ def test_reduction_diagnostics_and_benchmark_without_device():
             assert d.last_detail_code == p.REDUCTION_DETAIL["RUNTIME_UNAVAILABLE"]
     finally:
         rt.close()
+
+
+def test_attention_entry_validates_before_the_device():
+    """prometheus_reactor_runtime_attention_bf16_device: argument checks come
+    first (INIT, PROM_DETAIL_INVALID_ARGUMENT); valid arguments on a runtime
+    without a device stop at INIT with the runtime's unavailability detail."""
+    rt = p.NativeRuntime(test_flags=p.TESTCFG_SKIP_VULKAN_INIT)
+    try:
+        ok = 1 << 20  # an aligned address; nothing is dereferenced on these paths
+        for args in ((ok, ok, ok, ok, 64, 2, 128, 0), (ok, ok, ok, ok, 64, 1, 129, 0), (ok, ok, ok, ok, 0, 1, 128, 0),
+                     (ok, ok, ok, ok, 64, 1, 128, 2), (ok, ok, ok, ok, 64, 0, 128, 0), (ok + 2, ok, ok, ok, 64, 1, 128, 0),
+                     (0, ok, ok, ok, 64, 1, 128, 0), (ok, ok, ok, ok, 1 << 20, 8, 1024, 0)):
+            rc, st = rt.attention_bf16_device(*args)
+            assert rc == p.PROM_ERROR and st.stage == p.STAGE_INIT and st.detail == p.DETAIL_INVALID_ARGUMENT, args
+        rc, st = rt.attention_bf16_device(ok, ok, ok, ok, 64, 1, 128, 0)
+        assert rc == p.PROM_ERROR and st.stage == p.STAGE_INIT and st.detail == p.DETAIL_HIP_UNAVAILABLE
+    finally:
+        rt.close()

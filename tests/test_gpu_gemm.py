@@ -90,7 +90,7 @@ def test_every_variant(gpu_runtime, tile, slices, shape):
     try:
         rc, st = gpu_runtime.sgemm_device_variant(da, db, dc, m, n, k, tile, slices)
         if not possible:
-            assert rc == p.PROM_ERROR and st.detail == -6906
+            assert rc == p.PROM_ERROR and st.detail == p.DETAIL_INVALID_ARGUMENT
             return
         assert rc == p.PROM_OK, (st.stage, st.detail)
         gpu_runtime.synchronize()
@@ -148,14 +148,14 @@ def test_staged_variants_cover_unaligned_shapes_and_direct_ones_refuse(gpu_runti
         for tile in range(7):
             rc, st = gpu_runtime.sgemm_device_variant(da, db, dc, m, n, k, tile, 1)
             if tile >= 3:
-                assert rc == p.PROM_ERROR and st.stage == p.STAGE_INIT and st.detail == -6906, tile
+                assert rc == p.PROM_ERROR and st.stage == p.STAGE_INIT and st.detail == p.DETAIL_INVALID_ARGUMENT, tile
                 continue
             assert rc == p.PROM_OK, (tile, st.detail)
             gpu_runtime.synchronize()
             out = gpu_runtime.download(np.empty((m, n), np.float32), dc)
             assert oracle.normwise_rel_err(out, oracle.matmul_f64(a, b)) <= FP32_NORMWISE, tile
         rc, st = gpu_runtime.sgemm_device_variant(da, db, dc, m, n, k, 7, 1)
-        assert rc == p.PROM_ERROR and st.detail == -6906
+        assert rc == p.PROM_ERROR and st.detail == p.DETAIL_INVALID_ARGUMENT
     finally:
         for d in (da, db, dc):
             gpu_runtime.free(d)
