@@ -60,6 +60,47 @@ __global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ co
   }
 }
 
+// The same product with 16-byte weight loads (W 16-byte aligned, 4D a
+// multiple of 8): a workgroup owns 128 columns, lane c of each 16-lane group
+// 8 consecutive columns, and the 16 groups take every 16th k; every load of a
+// thread is independent, so they are all in flight together.  The 16 partial
+// sums are added in a fixed order.
+__global__ __launch_bounds__(256) void adaln_vec_kernel(const float* __restrict__ cond,
+                                                        const uint16_t* __restrict__ W, const float* __restrict__ b,
+                                                        float* __restrict__ mod, int C, int D) {
+  __shared__ float part[16][129];
+  const int cg = (int)(threadIdx.x & 15);
+  const int kg = (int)(threadIdx.x >> 4);
+  const int j0 = (int)blockIdx.x * 128 + cg * 8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (j0 < 4 * D) {
+#pragma unroll 4
+    for (int k = kg; k < C; k += 16) {
+      const uint4 w = *reinterpret_cast<const uint4*>(W + (size_t)k * 4 * D + j0);
+      const float c = cond[k];
+      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += c * __uint_as_float(wv[i] << 16);
+        acc[2 * i + 1] += c * __uint_as_float(wv[i] & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) part[kg][cg * 8 + i] = acc[i];
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    const int j = (int)blockIdx.x * 128 + (int)threadIdx.x;
+    if (j < 4 * D) {
+      float m = b[j];
+#pragma unroll
+      for (int g = 0; g < 16; ++g) m += part[g][threadIdx.x];
+      const int chunk = j / D;
+      mod[j] = (chunk == 0 || chunk == 2) ? 1.0f + m : tanhf(m);
+    }
+  }
+}
+
 // RoPE table: tab[t][p] = (cos, sin) of coord[t][axis(p)] * theta^(-2*pair/width)
 // for the 64 pairs of a 128-wide head; angles in binary64 (once per token,
 // shared by every head).
@@ -85,41 +126,32 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict
 // Per (token, head): q and k RMSNorm over 128 channels, then RoPE on the
 // interleaved pairs (2p, 2p+1) with the token's (cos, sin) table entry for
 // pair p (zimage/canonical_contract.go:66-87, zimage_main_transformer_canonical.py:124-140).
-// One wave per (token, head); lane l owns pair l.  V is copied to bf16.
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restrict__ qkv, const float2* __restrict__ tab,
+// In place on the QKV projection, bf16 [T, 3D] (Q | K | V per token); V is left
+// as it is.  One wave per (token, head); lane l owns pair l.
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict__ qkv, const float2* __restrict__ tab,
                                                            const float* __restrict__ qn, const float* __restrict__ kn,
-                                                           uint16_t* __restrict__ Q, uint16_t* __restrict__ K,
-                                                           uint16_t* __restrict__ V, int T, int H, float eps) {
+                                                           int T, int H, float eps) {
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
   const int unit = (int)blockIdx.x * 4 + wave;
   if (unit >= T * H) return;
   const int t = unit / H;
   const int h = unit - t * H;
   const int D = H * 128;
-  const float* row = qkv + (size_t)t * 3 * D;
+  uint16_t* row = qkv + (size_t)t * 3 * D;
   const int c0 = h * 128 + 2 * lane;
   const float2 cs2 = tab[(size_t)t * 64 + lane];
   const float cs = cs2.x, sn = cs2.y;
-  const float qw0 = qn[2 * lane], qw1 = qn[2 * lane + 1];
-  const float kw0 = kn[2 * lane], kw1 = kn[2 * lane + 1];
-  {
-    const float e = row[c0], o = row[c0 + 1];
+  uint32_t* qp = reinterpret_cast<uint32_t*>(row + c0);
+  uint32_t* kp = reinterpret_cast<uint32_t*>(row + D + c0);
+  const uint32_t qw = *qp, kw = *kp;
+  auto norm_rope = [&](uint32_t pair, float w0, float w1) {
+    const float e = __uint_as_float(pair << 16), o = __uint_as_float(pair & 0xffff0000u);
     const float inv = 1.0f / sqrtf(wave_sum(e * e + o * o) / 128.0f + eps);
-    const float ne = e * inv * qw0, no = o * inv * qw1;
-    const uint32_t w = (uint32_t)f2bf(ne * cs - no * sn) | ((uint32_t)f2bf(ne * sn + no * cs) << 16);
-    *reinterpret_cast<uint32_t*>(Q + (size_t)t * D + c0) = w;
-  }
-  {
-    const float e = row[D + c0], o = row[D + c0 + 1];
-    const float inv = 1.0f / sqrtf(wave_sum(e * e + o * o) / 128.0f + eps);
-    const float ne = e * inv * kw0, no = o * inv * kw1;
-    const uint32_t w = (uint32_t)f2bf(ne * cs - no * sn) | ((uint32_t)f2bf(ne * sn + no * cs) << 16);
-    *reinterpret_cast<uint32_t*>(K + (size_t)t * D + c0) = w;
-  }
-  {
-    const float e = row[2 * D + c0], o = row[2 * D + c0 + 1];
-    *reinterpret_cast<uint32_t*>(V + (size_t)t * D + c0) = (uint32_t)f2bf(e) | ((uint32_t)f2bf(o) << 16);
-  }
+    const float ne = e * inv * w0, no = o * inv * w1;
+    return (uint32_t)f2bf(ne * cs - no * sn) | ((uint32_t)f2bf(ne * sn + no * cs) << 16);
+  };
+  *qp = norm_rope(qw, qn[2 * lane], qn[2 * lane + 1]);
+  *kp = norm_rope(kw, kn[2 * lane], kn[2 * lane + 1]);
 }
 
 // G [T, 2F] (w1 | w3) -> h [T, F] bf16: silu(g) * u (canonical_reference.go:457-460)
@@ -147,7 +179,7 @@ enum { kWsMod, kWsA, kWsQkv, kWsQ, kWsK, kWsV, kWsO, kWsProj, kWsR, kWsF, kWsG, 
 
 size_t dit_workspace(const PrometheusDitBlockBf16Request* r, size_t off[kWsCount]) {
   const size_t T = r->tokens, D = r->hidden, F = r->ffn_hidden;
-  const size_t sizes[kWsCount] = {4 * D * 4, T * D * 2, T * 3 * D * 4, T * D * 2,     T * D * 2, T * D * 2,
+  const size_t sizes[kWsCount] = {4 * D * 4, T * D * 2, T * 3 * D * 2, 0,             0,         0,
                                   T * D * 2, T * D * 4, T * D * 4,     T * D * 2,     T * 2 * F * 4, T * F * 2,
                                   T * D * 4, T * 64 * 8};
   size_t o = 0;
@@ -185,10 +217,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   const float eps = r->rms_epsilon;
   float* mod = reinterpret_cast<float*>(ws + off[kWsMod]);
   uint16_t* A = reinterpret_cast<uint16_t*>(ws + off[kWsA]);
-  float* qkv = reinterpret_cast<float*>(ws + off[kWsQkv]);
-  uint16_t* Q = reinterpret_cast<uint16_t*>(ws + off[kWsQ]);
-  uint16_t* K = reinterpret_cast<uint16_t*>(ws + off[kWsK]);
-  uint16_t* V = reinterpret_cast<uint16_t*>(ws + off[kWsV]);
+  uint16_t* qkv = reinterpret_cast<uint16_t*>(ws + off[kWsQkv]);  // bf16 [T, 3D]
   uint16_t* O = reinterpret_cast<uint16_t*>(ws + off[kWsO]);
   float* proj = reinterpret_cast<float*>(ws + off[kWsProj]);
   float* R = reinterpret_cast<float*>(ws + off[kWsR]);
@@ -210,18 +239,26 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     ++n;                           \
   } while (0)
   const dim3 row_grid((T + 3) / 4), blk(256);
-  hipLaunchKernelGGL(adaln_kernel, dim3((4 * D + 63) / 64), blk, 0, st, r->condition, r->w_adaln, r->b_adaln, mod, C, D);
+  if ((reinterpret_cast<uintptr_t>(r->w_adaln) & 15u) == 0 && (4 * D) % 8 == 0)
+    hipLaunchKernelGGL(adaln_vec_kernel, dim3((4 * D + 127) / 128), blk, 0, st, r->condition, r->w_adaln, r->b_adaln,
+                       mod, C, D);
+  else
+    hipLaunchKernelGGL(adaln_kernel, dim3((4 * D + 63) / 64), blk, 0, st, r->condition, r->w_adaln, r->b_adaln, mod, C,
+                       D);
   PROM_STEP(hipGetLastError());
   hipLaunchKernelGGL(rope_table_kernel, dim3((T * 64 + 255) / 256), blk, 0, st, r->coordinates, rope, T, r->rope_theta,
                      (int)r->rope_axes[0], (int)r->rope_axes[1]);
   PROM_STEP(hipGetLastError());
   hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, row_grid, blk, 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
   PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, qkv, nullptr, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, Q, K, V,
-                     T, H, eps);
+  // QKV in bf16 (one rounding before the per-head norms), the norms and RoPE
+  // in place, and the attention reading Q, K, V from the same [T, 3D] rows.
+  PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, nullptr, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, T, H,
+                     eps);
   PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_flash_attn_bf16(Q, D, K, D, V, D, O, D, T, H, 1.0f / sqrtf(128.0f), st, 0));
+  PROM_STEP(launch_flash_attn_bf16(qkv, 3 * D, qkv + D, 3 * D, qkv + 2 * D, 3 * D, O, D, T, H, 1.0f / sqrtf(128.0f),
+                                   st, 0));
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, proj, nullptr, D, T, D, D, nullptr, 0, st, nullptr));
   hipLaunchKernelGGL(rows::resid_norm_mod_kernel<uint16_t>, row_grid, blk, 0, st, r->input, proj, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
                      R, Fb, T, D, eps);
