@@ -76,6 +76,18 @@ __device__ __forceinline__ void load_row(const float* __restrict__ src, int D, i
   for (int c = 0; c < kRowChunks; ++c) v[c] = ld4(r, c * 64 + lane);
 }
 
+// The same from a bf16 row (64-bit loads, widened exactly).
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ src, int D, int lane,
+                                         floatx4 (&v)[kRowChunks]) {
+  const __amdgpu_buffer_rsrc_t r = row_rsrc(src, 2 * D);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (uint32_t)(8 * (c * 64 + lane)), 0, 0));
+    v[c] = floatx4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                   __uint_as_float(w.y & 0xffff0000u)};
+  }
+}
+
 __device__ __forceinline__ float sum_sq(const floatx4 (&v)[kRowChunks]) {
   float ss = 0.0f;
 #pragma unroll
@@ -91,21 +103,30 @@ __device__ __forceinline__ void stage_vec(floatx4* dst, const float* src, int d4
     dst[i] = src ? reinterpret_cast<const floatx4*>(src)[i] : floatx4{1.f, 1.f, 1.f, 1.f};
 }
 
+// The norm kernels below run one row per wave, kRows rows per workgroup:
+// the D-vectors (norm weights, adaLN scale and gate, up to 4 x 16 KiB) are
+// staged in LDS once per workgroup.  resid_norm_mod, with four vectors, takes
+// 8 rows (with 4 its vector reads from L2 matched the row data itself,
+// 57 -> 53 us at C5); the two-vector kernels keep 4, which lets more
+// workgroups share a CU (final_resid: 36 us with 4 rows, 43 with 8).
+template <int kRows>
+inline dim3 row_groups(int T) { return dim3((unsigned)((T + kRows - 1) / kRows)); }
+
 // out = RMSNorm(x; w) * scale.
-template <typename OutT>
-__global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ w,
+template <typename OutT, int kRows = 4>
+__global__ __launch_bounds__(64 * kRows) void norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                        const float* __restrict__ scale, OutT* __restrict__ out, int T,
                                                        int D, float eps) {
   __shared__ floatx4 sw[1024], ssc[1024];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = min((int)blockIdx.x * 4 + wave, T - 1);
+  const int t = min((int)blockIdx.x * kRows + wave, T - 1);
   const int d4 = D >> 2;
   floatx4 v[kRowChunks];
   load_row(x + (size_t)t * D, D, lane, v);
   stage_vec(sw, w, d4);
   stage_vec(ssc, scale, d4);
   __syncthreads();
-  if ((int)blockIdx.x * 4 + wave >= T) return;
+  if ((int)blockIdx.x * kRows + wave >= T) return;
   const float inv = 1.0f / sqrtf(sum_sq(v) / (float)D + eps);
   const __amdgpu_buffer_rsrc_t ro = row_rsrc(out + (size_t)t * D, (int)sizeof(OutT) * D);
 #pragma unroll
@@ -121,16 +142,16 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
   }
 }
 
-// r = x + gate * RMSNorm(proj; n2) (fp32 out), f = RMSNorm(r; n3) * scale (OutT).
-template <typename OutT>
-__global__ __launch_bounds__(256) void resid_norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ proj,
+// r = x + gate * RMSNorm(proj; n2) (fp32 out), f = RMSNorm(r; n3) * scale (OutT); proj fp32 or bf16.
+template <typename OutT, int kRows = 8, typename ProjT = float>
+__global__ __launch_bounds__(64 * kRows) void resid_norm_mod_kernel(const float* __restrict__ x, const ProjT* __restrict__ proj,
                                                              const float* __restrict__ n2, const float* __restrict__ gate,
                                                              const float* __restrict__ n3, const float* __restrict__ scale,
                                                              float* __restrict__ r_out, OutT* __restrict__ f_out, int T,
                                                              int D, float eps) {
   __shared__ floatx4 s2[1024], sg[1024], s3[1024], ssc[1024];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = min((int)blockIdx.x * 4 + wave, T - 1);
+  const int t = min((int)blockIdx.x * kRows + wave, T - 1);
   const int d4 = D >> 2;
   floatx4 v[kRowChunks], xv[kRowChunks];
   load_row(proj + (size_t)t * D, D, lane, v);
@@ -140,7 +161,7 @@ __global__ __launch_bounds__(256) void resid_norm_mod_kernel(const float* __rest
   stage_vec(s3, n3, d4);
   stage_vec(ssc, scale, d4);
   __syncthreads();
-  if ((int)blockIdx.x * 4 + wave >= T) return;
+  if ((int)blockIdx.x * kRows + wave >= T) return;
   const float inv = 1.0f / sqrtf(sum_sq(v) / (float)D + eps);
   const __amdgpu_buffer_rsrc_t rr = row_rsrc(r_out + (size_t)t * D, 4 * D);
   float ss2 = 0.0f;
@@ -175,13 +196,14 @@ __global__ __launch_bounds__(256) void resid_norm_mod_kernel(const float* __rest
   }
 }
 
-// out = r + gate * RMSNorm(w2; n4)
-__global__ __launch_bounds__(256) void final_resid_kernel(const float* __restrict__ r, const float* __restrict__ w2,
+// out = r + gate * RMSNorm(w2; n4); w2 fp32 or bf16.
+template <int kRows = 4, typename W2T = float>
+__global__ __launch_bounds__(64 * kRows) void final_resid_kernel(const float* __restrict__ r, const W2T* __restrict__ w2,
                                                           const float* __restrict__ n4, const float* __restrict__ gate,
                                                           float* __restrict__ out, int T, int D, float eps) {
   __shared__ floatx4 s4[1024], sg[1024];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int t = min((int)blockIdx.x * 4 + wave, T - 1);
+  const int t = min((int)blockIdx.x * kRows + wave, T - 1);
   const int d4 = D >> 2;
   floatx4 v[kRowChunks], rv[kRowChunks];
   load_row(w2 + (size_t)t * D, D, lane, v);
@@ -189,7 +211,7 @@ __global__ __launch_bounds__(256) void final_resid_kernel(const float* __restric
   stage_vec(s4, n4, d4);
   stage_vec(sg, gate, d4);
   __syncthreads();
-  if ((int)blockIdx.x * 4 + wave >= T) return;
+  if ((int)blockIdx.x * kRows + wave >= T) return;
   const float inv = 1.0f / sqrtf(sum_sq(v) / (float)D + eps);
   const __amdgpu_buffer_rsrc_t ro = row_rsrc(out + (size_t)t * D, 4 * D);
 #pragma unroll

@@ -12,15 +12,21 @@
 // fp32 accumulation; attention is the flash kernel (attention_bf16.hip); the
 // per-row work between them is fused into four one-pass row kernels (one wave
 // per row, the row held in registers, 128-bit loads):
-//   adaln          m = c @ Wada + b -> modulation vectors       (k split over 4 waves)
+//   adaln          m = c @ Wada + b -> modulation vectors       (16-byte weight loads, k split 16 ways)
 //   rope_table     (cos, sin) per token and pair, binary64 angles
 //   norm_mod       a = RMSNorm(x; n1) * scaleA                   -> bf16
-//   qk_norm_rope   per (token, head): RMSNorm(q), RMSNorm(k), RoPE, V copy -> bf16
+//   (QKV GEMM      -> bf16 [T, 3D])
+//   qk_norm_rope   per (token, head), in place: RMSNorm(q), RMSNorm(k), RoPE
+//                  (the attention reads Q, K, V from the [T, 3D] rows)
+//   (out-projection GEMM -> bf16 proj)
 //   resid_norm_mod r = x + gateA * RMSNorm(proj; n2)             -> fp32
 //                  f = RMSNorm(r; n3) * scaleM                   -> bf16
 //   swiglu         h = silu(g) * u -> bf16, fused into the W1|W3 GEMM epilogue
 //                  (gemm_bf16.hip) when F % 128 == 0 and D % 64 == 0
+//   (W2 GEMM       -> bf16 w2)
 //   final_resid    out = r + gateM * RMSNorm(w2; n4)              -> fp32
+// The bf16 intermediates (qkv, proj, w2) are each normalised before they
+// meet the fp32 residual stream.
 #include <math.h>
 #include <string.h>
 
@@ -219,12 +225,12 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   uint16_t* A = reinterpret_cast<uint16_t*>(ws + off[kWsA]);
   uint16_t* qkv = reinterpret_cast<uint16_t*>(ws + off[kWsQkv]);  // bf16 [T, 3D]
   uint16_t* O = reinterpret_cast<uint16_t*>(ws + off[kWsO]);
-  float* proj = reinterpret_cast<float*>(ws + off[kWsProj]);
+  uint16_t* projb = reinterpret_cast<uint16_t*>(ws + off[kWsProj]);
   float* R = reinterpret_cast<float*>(ws + off[kWsR]);
   uint16_t* Fb = reinterpret_cast<uint16_t*>(ws + off[kWsF]);
   float* G = reinterpret_cast<float*>(ws + off[kWsG]);
   uint16_t* Hb = reinterpret_cast<uint16_t*>(ws + off[kWsH]);
-  float* W2 = reinterpret_cast<float*>(ws + off[kWsW2]);
+  uint16_t* w2b = reinterpret_cast<uint16_t*>(ws + off[kWsW2]);
   float2* rope = reinterpret_cast<float2*>(ws + off[kWsRope]);
   const float* scaleA = mod;
   const float* gateA = mod + D;
@@ -238,7 +244,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     if (e != hipSuccess) return e; \
     ++n;                           \
   } while (0)
-  const dim3 row_grid((T + 3) / 4), blk(256);
+  const dim3 blk(256);
   if ((reinterpret_cast<uintptr_t>(r->w_adaln) & 15u) == 0 && (4 * D) % 8 == 0)
     hipLaunchKernelGGL(adaln_vec_kernel, dim3((4 * D + 127) / 128), blk, 0, st, r->condition, r->w_adaln, r->b_adaln,
                        mod, C, D);
@@ -249,7 +255,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   hipLaunchKernelGGL(rope_table_kernel, dim3((T * 64 + 255) / 256), blk, 0, st, r->coordinates, rope, T, r->rope_theta,
                      (int)r->rope_axes[0], (int)r->rope_axes[1]);
   PROM_STEP(hipGetLastError());
-  hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, row_grid, blk, 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
+  hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, rows::row_groups<4>(T), dim3(256), 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
   PROM_STEP(hipGetLastError());
   // QKV in bf16 (one rounding before the per-head norms), the norms and RoPE
   // in place, and the attention reading Q, K, V from the same [T, 3D] rows.
@@ -259,8 +265,10 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_flash_attn_bf16(qkv, 3 * D, qkv + D, 3 * D, qkv + 2 * D, 3 * D, O, D, T, H, 1.0f / sqrtf(128.0f),
                                    st, 0));
-  PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, proj, nullptr, D, T, D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(rows::resid_norm_mod_kernel<uint16_t>, row_grid, blk, 0, st, r->input, proj, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
+  // The out- and down-projections go to bf16: both are RMS-normalised before
+  // they join the fp32 residual stream.
+  PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, nullptr, projb, D, T, D, D, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL((rows::resid_norm_mod_kernel<uint16_t, 8, uint16_t>), rows::row_groups<8>(T), dim3(512), 0, st, r->input, projb, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
                      R, Fb, T, D, eps);
   PROM_STEP(hipGetLastError());
   // FFN up-projection with SwiGLU fused into the GEMM epilogue when the shape
@@ -275,8 +283,8 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   } else {
     PROM_STEP(fused);
   }
-  PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, W2, nullptr, D, T, D, F, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(rows::final_resid_kernel, row_grid, blk, 0, st, R, W2, r->ffn_norm2, gateM, r->output, T, D, eps);
+  PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, nullptr, w2b, D, T, D, F, nullptr, 0, st, nullptr));
+  hipLaunchKernelGGL((rows::final_resid_kernel<4, uint16_t>), rows::row_groups<4>(T), dim3(256), 0, st, R, w2b, r->ffn_norm2, gateM, r->output, T, D, eps);
   PROM_STEP(hipGetLastError());
 #undef PROM_STEP
   if (launches) *launches = n;

@@ -378,7 +378,7 @@ hipError_t launch_zimage_rope_table(const float* coords, float2* tab, int T, hip
 }
 
 hipError_t launch_zimage_norm(const float* x, const float* w, float* out, int T, int D, float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(rows::norm_mod_kernel<float>, dim3((T + 3) / 4), dim3(256), 0, stream, x, w, (const float*)nullptr,
+  hipLaunchKernelGGL(rows::norm_mod_kernel<float>, rows::row_groups<4>(T), dim3(256), 0, stream, x, w, (const float*)nullptr,
                      out, T, D, eps);
   return hipGetLastError();
 }
@@ -441,7 +441,7 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
   } while (0)
   // stage_events[0] before the first stage, stage_events[i] after stage i (1..13)
   auto mark = [&](int i) { return stage_events ? hipEventRecord(stage_events[i], st) : hipSuccess; };
-  const dim3 row_grid((T + 3) / 4), blk(256);
+  const dim3 blk(256);
   if (first_phase > last_phase || first_phase < 1 || last_phase > 3) return hipErrorInvalidValue;
   if (launches) *launches = 0;
   if (first_phase == 1) {  // adaLN, attention norm, QKV, head norms and RoPE
@@ -452,7 +452,7 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
       PROM_STEP(hipGetLastError());
     }
     if ((e = mark(1)) != hipSuccess) return e;
-    hipLaunchKernelGGL(rows::norm_mod_kernel<float>, row_grid, blk, 0, st, x, w.attn_norm1, scaleA, A, T, D, eps);
+    hipLaunchKernelGGL(rows::norm_mod_kernel<float>, rows::row_groups<4>(T), dim3(256), 0, st, x, w.attn_norm1, scaleA, A, T, D, eps);
     PROM_STEP(hipGetLastError());
     if ((e = mark(2)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(A, D, w.w_qkv, 3 * D, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
@@ -490,7 +490,7 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
     if ((e = mark(7)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(O, D, w.w_out, D, proj, D, T, D, D, nullptr, 0, st, nullptr));
     if ((e = mark(8)) != hipSuccess) return e;
-    hipLaunchKernelGGL(rows::resid_norm_mod_kernel<float>, row_grid, blk, 0, st, x, proj, w.attn_norm2, gateA,
+    hipLaunchKernelGGL(rows::resid_norm_mod_kernel<float>, rows::row_groups<8>(T), dim3(512), 0, st, x, proj, w.attn_norm2, gateA,
                        w.ffn_norm1, scaleM, R, Fm, T, D, eps);
     PROM_STEP(hipGetLastError());
     if ((e = mark(9)) != hipSuccess) return e;
@@ -503,7 +503,7 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
     if ((e = mark(11)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(Hd, F, w.w_2, D, W2, D, T, D, F, nullptr, 0, st, nullptr));
     if ((e = mark(12)) != hipSuccess) return e;
-    hipLaunchKernelGGL(rows::final_resid_kernel, row_grid, blk, 0, st, R, W2, w.ffn_norm2, gateM, out, T, D, eps);
+    hipLaunchKernelGGL(rows::final_resid_kernel<4>, rows::row_groups<4>(T), dim3(256), 0, st, R, W2, w.ffn_norm2, gateM, out, T, D, eps);
     PROM_STEP(hipGetLastError());
     if ((e = mark(13)) != hipSuccess) return e;
   }
