@@ -662,9 +662,9 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_variant(void* handl
    the bf16 flash attention of the DiT block on device pointers, for its own
    parity tests and tuning.  O = softmax(Q K^T / sqrt(128)) V per head, full
    attention; q, k, v, o are bf16 [tokens, ld] with head h at column 128 h,
-   16-byte aligned, ld a multiple of 8 and >= 128 * heads, tokens * ld * 2 <
-   2^31.  variant 0 = the block's kernel (DMA-fed), 1 = the register-staged
-   kernel.  Invalid arguments: PROM_ERROR, stage INIT,
+   16-byte aligned, ld a multiple of 8, >= 128 * heads and < 2^24, tokens *
+   ld * 2 < 2^31.  variant 0 = the block's kernel (DMA-fed), 1 = the
+   register-staged kernel.  Invalid arguments: PROM_ERROR, stage INIT,
    PROM_DETAIL_INVALID_ARGUMENT.  Queued on the runtime's stream. */
 PROM_REACTOR_API int prometheus_reactor_runtime_attention_bf16_device(void* handle, const uint16_t* q,
                                                                       const uint16_t* k, const uint16_t* v,

@@ -20,10 +20,12 @@
 //     built in the same key order by two ds_read_b64_tr_b16 transpose reads;
 //   * softmax runs in the log2 domain: max on raw scores, one FMA and one
 //     v_exp_f32 per score, running max/sum in fp32; O is rescaled only when
-//     some query's maximum grew; masking only on the last, partial tile;
+//     some query's maximum grew (in the DMA-fed kernel only when it grew by
+//     more than 2^8, see kLazyLog2); masking only on the last, partial tile;
 //     P and O go to bf16 with the hardware round-to-nearest-even pair
 //     conversion (VALU work per tile is the bound of this kernel, not MFMA);
-//   * the output tile is staged through LDS for 128-bit coalesced stores.
+//   * the output tile is staged through LDS for 128-bit coalesced stores;
+//   * the 1-D grid runs a head's query blocks on one XCD (block_coords).
 //
 // Two kernels share that design: flash_attn_bf16_dma_kernel (the DiT block's,
 // tiles moved HBM -> LDS by DMA, less VALU work per tile; see its comment)
@@ -49,6 +51,23 @@ constexpr int kKB = 64;     // keys per tile
 constexpr int kKP = kD + 8;   // K row pitch (bf16): 68 words, 16 rows on distinct 16-byte bank groups
 constexpr int kVP = kD + 16;  // V row pitch (bf16): 72 words, 4 consecutive rows on distinct banks
 constexpr float kNegBig = -1.0e30f;
+// Growth of a query's maximum (log2 units) below which the DMA-fed kernel
+// keeps the older maximum as the softmax reference:
+// probabilities then reach 2^8 before O/l normalises them, well inside bf16
+// and fp32 range, and the result is the same softmax.
+constexpr float kLazyLog2 = 8.0f;
+
+// The grid is 1-D over (head, query block) pairs, head-major, renumbered by
+// xcd_pid: an XCD runs the query blocks of one or two heads at a time, so a
+// K/V tile reaches its L2 once per head instead of once per query block (with
+// the blocks of a head spread over all 8 XCDs, each L2 held tiles of about 8
+// heads at once).
+__device__ __forceinline__ void block_coords(int T, int* head, int* qb) {
+  const int nqb = (T + 4 * kQW - 1) / (4 * kQW);
+  const int p = xcd_pid((int)blockIdx.x, (int)gridDim.x);
+  *head = p / nqb;
+  *qb = p - *head * nqb;
+}
 
 __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t* __restrict__ Q,
                                                                  const uint16_t* __restrict__ K,
@@ -63,8 +82,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_kernel(const uint16_t*
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int head = (int)blockIdx.y;
-  const int q0 = (int)blockIdx.x * (4 * kQW) + wave * kQW;
+  int head, qb;
+  block_coords(T, &head, &qb);
+  const int q0 = qb * (4 * kQW) + wave * kQW;
   const int lq = lane & 31;
   const int hi = lane >> 5;  // lane half
   const int qi = q0 + lq;
@@ -270,8 +290,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int head = (int)blockIdx.y;
-  const int q0 = (int)blockIdx.x * (4 * kQW) + wave * kQW;
+  int head, qb;
+  block_coords(T, &head, &qb);
+  const int q0 = qb * (4 * kQW) + wave * kQW;
   const int lq = lane & 31;
   const int hi = lane >> 5;
   const int qi = q0 + lq;
@@ -279,6 +300,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
 
   // HBM -> LDS transfers; the buffer range ends with the head's last row
   // (row T-1, 128 columns), so the rows of the last tile past T read zero.
+  // The entry point bounds T * ld * 2 below 2^31 and ld below 2^24, so the
+  // byte offsets below (at most 63 rows of a tile past row T - 1) fit 32 bits.
   typedef int int4v __attribute__((ext_vector_type(4)));
   auto desc = [](const void* ptr, uint32_t bytes) {
     const unsigned long long a = (unsigned long long)ptr;
@@ -295,10 +318,10 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     // 1 KiB block 4*wave + i of a tile: rows 16*wave + 4i .. +3, lane -> (row, slot)
-    const int row = 16 * wave + 4 * i + (lane >> 4);
-    const int slot = lane & 15;
-    koff[i] = (uint32_t)((row * ldk + 8 * (slot ^ (row & 15))) * 2);
-    voff[i] = (uint32_t)((row * ldv + 8 * (slot ^ (4 * (row & 3)))) * 2);
+    const uint32_t row = (uint32_t)(16 * wave + 4 * i + (lane >> 4));
+    const uint32_t slot = (uint32_t)(lane & 15);
+    koff[i] = (row * (uint32_t)ldk + 8u * (slot ^ (row & 15u))) * 2u;
+    voff[i] = (row * (uint32_t)ldv + 8u * (slot ^ (4u * (row & 3u)))) * 2u;
   }
   auto issue = [&](const int4v& rs, const uint32_t* off, char* st, uint32_t add) {
     const uint32_t base = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)st;
@@ -311,8 +334,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
     }
   };
   auto issue_tile = [&](int j) {
-    issue(rs_k, koff, lds + (j & 1) * kTileB, (uint32_t)(j * kKB * ldk * 2));
-    issue(rs_v, voff, lds + (2 + (j & 1)) * kTileB, (uint32_t)(j * kKB * ldv * 2));
+    issue(rs_k, koff, lds + (j & 1) * kTileB, (uint32_t)j * (uint32_t)(kKB * 2) * (uint32_t)ldk);
+    issue(rs_v, voff, lds + (2 + (j & 1)) * kTileB, (uint32_t)j * (uint32_t)(kKB * 2) * (uint32_t)ldv);
   };
 
   bf16x8 qf[8];
@@ -374,20 +397,24 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
 #pragma unroll
     for (int r = 1; r < 16; ++r) asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mt) : "v"(mt), "v"(s0[r]), "v"(s1[r]));
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt * scale_log2);
-    if (__builtin_amdgcn_read_exec() & __ballot(m_new > m_run)) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    // Lazy rescaling: the reference maximum m_run moves only when the tile's
+    // maximum exceeds it by more than kLazyLog2, so p <= 2^kLazyLog2 and O and
+    // the running sum are rescaled in a handful of tiles, not in most.
+    const float m_cand = fmaxf(m_run, mt * scale_log2);
+    const bool grow = m_cand > m_run + kLazyLog2;
+    if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_cand) : 1.0f;
       l_part *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
     }
-    m_run = m_new;
+    if (grow) m_run = m_cand;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, -m_new));
-      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, -m_new));
+      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, -m_run));
+      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, -m_run));
     }
     // P^T operands (keys of chunk c in the accumulator's order, see
     // flash_attn_bf16_kernel), and their sum two at a time
@@ -461,7 +488,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
 hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v, int ldv,
                                   uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream,
                                   int variant) {
-  const dim3 grid((unsigned)((T + 4 * kQW - 1) / (4 * kQW)), (unsigned)heads);
+  const dim3 grid((unsigned)((T + 4 * kQW - 1) / (4 * kQW) * heads));
   const float scale_log2 = scale * 1.4426950408889634f;
   if (variant == 1) {
     hipLaunchKernelGGL(flash_attn_bf16_kernel, grid, dim3(256), 0, stream, q, k, v, o, T, ldq, ldk, ldv, ldo,

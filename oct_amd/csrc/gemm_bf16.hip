@@ -37,18 +37,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
   return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
 }
 
-// Workgroups are dealt to the 8 XCDs round-robin (workgroup b to XCD b % 8);
-// this gives XCD x the contiguous range of tile ids starting at
-// x * (n / 8) + min(x, n % 8), of n / 8 or n / 8 + 1 ids, for any n, so the
-// tiles an XCD runs together are neighbours in the grouped order below and
-// share their A and B panels in that XCD's L2.  (With the remap applied only
-// when n % 8 == 0, the C5 QKV grid of 765 tiles gave each XCD one A panel and
-// 32 B panels at a time.)
-__device__ __forceinline__ int xcd_pid(int b, int n) {
-  const int x = b & 7, q = n >> 3, r = n & 7;
-  return x * q + min(x, r) + (b >> 3);
-}
-
+// xcd_pid gives each XCD a contiguous range of tile ids, so the tiles an XCD
+// runs together are neighbours in the grouped order below and share their A
+// and B panels in its L2.  (With the remap applied only when n % 8 == 0, the
+// C5 QKV grid of 765 tiles gave each XCD one A panel and 32 B panels at a
+// time.)
 __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int* tn) {
   const int num_tiles = tiles_m * tiles_n;
   const int pid = xcd_pid((int)blockIdx.x, num_tiles);

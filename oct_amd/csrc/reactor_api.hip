@@ -624,7 +624,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_attention_bf16_device(void* hand
   auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   const bool ok = q != nullptr && k != nullptr && v != nullptr && o != nullptr && aligned(q) && aligned(k) &&
                   aligned(v) && aligned(o) && tokens != 0u && heads != 0u && (uint64_t)heads * 128u <= ld &&
-                  ld % 8u == 0u && (uint64_t)tokens * ld * 2u <= 0x7fffffffull && variant <= 1u;
+                  ld % 8u == 0u && ld < (1u << 24) && (uint64_t)tokens * ld * 2u <= 0x7fffffffull && variant <= 1u;
   if (!ok) {
     set_status(out_stage, out_detail_code, PROM_STAGE_INIT, PROM_DETAIL_INVALID_ARGUMENT);
     return PROM_ERROR;

@@ -17,6 +17,16 @@
 
 namespace prom {
 
+// Workgroups of a launch are dealt to the 8 XCDs round-robin (workgroup b to
+// XCD b % 8).  xcd_pid(b, n) renumbers a grid of n workgroups so that XCD x
+// runs the contiguous range of ids starting at x * (n / 8) + min(x, n % 8)
+// (n / 8 or n / 8 + 1 of them, for any n), in increasing order: work items
+// with neighbouring ids share their operands in that XCD's L2.
+__device__ __forceinline__ int xcd_pid(int b, int n) {
+  const int x = b & 7, q = n >> 3, r = n & 7;
+  return x * q + min(x, r) + (b >> 3);
+}
+
 constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
 // Staging slots: 0-3 operand staging, 4 block workspace, 5 block host staging,

@@ -37,15 +37,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kBK = 16;
 constexpr int kGroupM = 8;
 
-// Workgroups are dealt to the 8 XCDs round-robin (workgroup b to XCD b % 8);
-// XCD x takes the contiguous range of tile ids starting at
-// x * (n / 8) + min(x, n % 8) (n / 8 or n / 8 + 1 of them, any n), so the
-// tiles an XCD runs together are neighbours in the grouped order and share
-// their A and B panels in its L2.
+// xcd_pid gives each XCD a contiguous range of tile ids, so the tiles an XCD
+// runs together are neighbours in the grouped order and share their A and B
+// panels in its L2.
 __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int* tn) {
   const int num_tiles = tiles_m * tiles_n;
-  const int b = (int)blockIdx.x;
-  const int pid = (b & 7) * (num_tiles >> 3) + min(b & 7, num_tiles & 7) + (b >> 3);
+  const int pid = xcd_pid((int)blockIdx.x, num_tiles);
   const int per_group = kGroupM * tiles_n;
   const int group = pid / per_group;
   const int first_m = group * kGroupM;

@@ -536,7 +536,7 @@ def test_attention_entry_validates_before_the_device():
     try:
         ok = 1 << 20  # an aligned address; nothing is dereferenced on these paths
         for args in ((ok, ok, ok, ok, 64, 2, 128, 0), (ok, ok, ok, ok, 64, 1, 129, 0), (ok, ok, ok, ok, 0, 1, 128, 0),
-                     (ok, ok, ok, ok, 64, 1, 128, 2), (ok, ok, ok, ok, 64, 0, 128, 0), (ok + 2, ok, ok, ok, 64, 1, 128, 0),
+                     (ok, ok, ok, ok, 64, 1, 128, 2), (ok, ok, ok, ok, 64, 0, 128, 0), (ok, ok, ok, ok, 1, 1, 1 << 24, 0), (ok + 2, ok, ok, ok, 64, 1, 128, 0),
                      (0, ok, ok, ok, 64, 1, 128, 0), (ok, ok, ok, ok, 1 << 20, 8, 1024, 0)):
             rc, st = rt.attention_bf16_device(*args)
             assert rc == p.PROM_ERROR and st.stage == p.STAGE_INIT and st.detail == p.DETAIL_INVALID_ARGUMENT, args
