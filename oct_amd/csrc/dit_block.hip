@@ -16,7 +16,7 @@
 //   rope_table     (cos, sin) per token and pair, binary64 angles
 //   norm_mod       a = RMSNorm(x; n1) * scaleA                   -> bf16
 //   (QKV GEMM      -> bf16 [T, 3D])
-//   qk_norm_rope   per (token, head), in place: RMSNorm(q), RMSNorm(k), RoPE
+//   qk_norm_rope   per token and head, in place: RMSNorm(q), RMSNorm(k), RoPE
 //                  (the attention reads Q, K, V from the [T, 3D] rows)
 //   (out-projection GEMM -> bf16 proj)
 //   resid_norm_mod r = x + gateA * RMSNorm(proj; n2)             -> fp32
@@ -133,31 +133,80 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict
 // interleaved pairs (2p, 2p+1) with the token's (cos, sin) table entry for
 // pair p (zimage/canonical_contract.go:66-87, zimage_main_transformer_canonical.py:124-140).
 // In place on the QKV projection, bf16 [T, 3D] (Q | K | V per token); V is left
-// as it is.  One wave per (token, head); lane l owns pair l.
+// as it is.  One wave per token: lane l takes the 16-byte chunks
+// c = l + 64 j of the token's Q row and of its K row (c < 16 H): head c / 16,
+// channels 8 (c % 16) .. +7, i.e. pairs 4 (l % 16) .. +3 of the head, so the
+// lane's (cos, sin) entries and norm weights are the same for every chunk and
+// are loaded once.  A head's sum of squares is reduced over its 16-lane group.
+// Up to 8 chunks of Q and 8 of K (32 heads) are loaded before any arithmetic.
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict__ qkv, const float2* __restrict__ tab,
                                                            const float* __restrict__ qn, const float* __restrict__ kn,
                                                            int T, int H, float eps) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int kBatch = 8;
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int unit = (int)blockIdx.x * 4 + wave;
-  if (unit >= T * H) return;
-  const int t = unit / H;
-  const int h = unit - t * H;
+  const int t = (int)blockIdx.x * 4 + wave;
+  if (t >= T) return;  // the whole wave
   const int D = H * 128;
+  const int nc = H * 16;
+  const int sub = lane & 15;
   uint16_t* row = qkv + (size_t)t * 3 * D;
-  const int c0 = h * 128 + 2 * lane;
-  const float2 cs2 = tab[(size_t)t * 64 + lane];
-  const float cs = cs2.x, sn = cs2.y;
-  uint32_t* qp = reinterpret_cast<uint32_t*>(row + c0);
-  uint32_t* kp = reinterpret_cast<uint32_t*>(row + D + c0);
-  const uint32_t qw = *qp, kw = *kp;
-  auto norm_rope = [&](uint32_t pair, float w0, float w1) {
-    const float e = __uint_as_float(pair << 16), o = __uint_as_float(pair & 0xffff0000u);
-    const float inv = 1.0f / sqrtf(wave_sum(e * e + o * o) / 128.0f + eps);
-    const float ne = e * inv * w0, no = o * inv * w1;
-    return (uint32_t)f2bf(ne * cs - no * sn) | ((uint32_t)f2bf(ne * sn + no * cs) << 16);
+  float cs[4], sn[4], wq[8], wk[8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float2 e = tab[(size_t)t * 64 + 4 * sub + p];
+    cs[p] = e.x;
+    sn[p] = e.y;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    wq[i] = qn[8 * sub + i];
+    wk[i] = kn[8 * sub + i];
+  }
+  auto norm_rope = [&](u32x4 v, const float* w) __attribute__((always_inline)) {
+    float e[4], o[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      e[p] = __uint_as_float(v[p] << 16);
+      o[p] = __uint_as_float(v[p] & 0xffff0000u);
+      ss += e[p] * e[p] + o[p] * o[p];
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+    u32x4 r;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float ne = e[p] * inv * w[2 * p], no = o[p] * inv * w[2 * p + 1];
+      r[p] = (uint32_t)f2bf(ne * cs[p] - no * sn[p]) | ((uint32_t)f2bf(ne * sn[p] + no * cs[p]) << 16);
+    }
+    return r;
   };
-  *qp = norm_rope(qw, qn[2 * lane], qn[2 * lane + 1]);
-  *kp = norm_rope(kw, kn[2 * lane], kn[2 * lane + 1]);
+  for (int c0 = 0; c0 < nc; c0 += 64 * kBatch) {
+    u32x4 qv[kBatch], kv[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int c = c0 + lane + 64 * j;
+      qv[j] = kv[j] = u32x4{0u, 0u, 0u, 0u};
+      if (c < nc) {
+        qv[j] = *reinterpret_cast<const u32x4*>(row + 8 * c);
+        kv[j] = *reinterpret_cast<const u32x4*>(row + D + 8 * c);
+      }
+    }
+    // c < nc holds for whole 16-lane groups (nc is a multiple of 16), so
+    // every group's reduction sees only its own head
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int c = c0 + lane + 64 * j;
+      const u32x4 qr = norm_rope(qv[j], wq);
+      const u32x4 kr = norm_rope(kv[j], wk);
+      if (c < nc) {
+        *reinterpret_cast<u32x4*>(row + 8 * c) = qr;
+        *reinterpret_cast<u32x4*>(row + D + 8 * c) = kr;
+      }
+    }
+  }
 }
 
 // G [T, 2F] (w1 | w3) -> h [T, F] bf16: silu(g) * u (canonical_reference.go:457-460)
@@ -260,8 +309,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   // QKV in bf16 (one rounding before the per-head norms), the norms and RoPE
   // in place, and the attention reading Q, K, V from the same [T, 3D] rows.
   PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, nullptr, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T * H + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, T, H,
-                     eps);
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, T, H, eps);
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_flash_attn_bf16(qkv, 3 * D, qkv + D, 3 * D, qkv + 2 * D, 3 * D, O, D, T, H, 1.0f / sqrtf(128.0f),
                                    st, 0));
