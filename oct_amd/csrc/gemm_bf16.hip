@@ -636,22 +636,29 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
   };
   const int4v da = desc(A, (uint32_t)((size_t)M * lda * 2));
   const int4v db = desc(B, (uint32_t)((size_t)K * ldb * 2));
-  auto issue = [&](char* stage, int k0) {
-    const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
-    const int sb = __builtin_amdgcn_readfirstlane(k0 * ldb * 2);
+  // Transfer j (0..3) of this wave for the tile at k0: A rows (j even) or B
+  // rows (j odd) of instruction i = j / 2.
+  auto issue_one = [&](char* stage, int k0, int j) __attribute__((always_inline)) {
+    const int i = j >> 1;
+    const int q = wave * 2 + i;
     const uint32_t base = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)stage;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int q = wave * 2 + i;
+    if ((j & 1) == 0) {
+      const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
       const uint32_t la = __builtin_amdgcn_readfirstlane(base + q * 1024);
-      const uint32_t lb = __builtin_amdgcn_readfirstlane(base + 16384 + q * 1024);
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(la), "v"(a_off[i]), "s"(da),
                    "s"(sa)
                    : "memory", "m0");
+    } else {
+      const int sb = __builtin_amdgcn_readfirstlane(k0 * ldb * 2);
+      const uint32_t lb = __builtin_amdgcn_readfirstlane(base + 16384 + q * 1024);
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lb), "v"(b_off[i]), "s"(db),
                    "s"(sb)
                    : "memory", "m0");
     }
+  };
+  auto issue = [&](char* stage, int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) issue_one(stage, k0, j);
   };
 
   const int lrow = lane & 31;
@@ -685,14 +692,6 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
     }
     return f;
   };
-  auto mma = [&](const Frags& f) {
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
-  };
-
   const int k_tiles = K / kBK4;
   // Step t: wait until this wave's transfers of tile t+1 have landed (the
   // kSt-3 tiles after it may stay in flight), barrier (tile t+1 complete for
@@ -708,14 +707,31 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
       PROM_WAIT_VMCNT(0);
   };
   Frags f0;
+  // The tile's 16 MFMAs run in four groups of four, each followed by one of
+  // the wave's four transfers of tile t+kSt-1: issued all at once after the
+  // barrier, the 32 transfers of a workgroup queue at the texture unit and
+  // hold back the MFMAs of the waves that issue them last.
+  auto mma_quarter = [&](const Frags& f, int h) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mi = 2 * h; mi < 2 * h + 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
+  };
   auto step = [&](int t, auto u_c) {
     constexpr int u = decltype(u_c)::value;
     wait_tiles(min(kSt - 3, k_tiles - t - 2));
     stage_barrier();
-    if (t + kSt - 1 < k_tiles) issue(S[(u + kSt - 1) % kSt], (t + kSt - 1) * kBK4);
+    const bool more = t + kSt - 1 < k_tiles;
+    char* const next = S[(u + kSt - 1) % kSt];
+    const int k_next = (t + kSt - 1) * kBK4;
     const Frags f1 = read(S[u], 1);
-    mma(f0);
-    mma(f1);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      mma_quarter(g < 2 ? f0 : f1, g & 1);
+      if (more) issue_one(next, k_next, g);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (t + 1 < k_tiles) f0 = read(S[(u + 1) % kSt], 0);
   };
 #pragma unroll
