@@ -323,19 +323,27 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
     koff[i] = (row * (uint32_t)ldk + 8u * (slot ^ (row & 15u))) * 2u;
     voff[i] = (row * (uint32_t)ldv + 8u * (slot ^ (4u * (row & 3u)))) * 2u;
   }
-  auto issue = [&](const int4v& rs, const uint32_t* off, char* st, uint32_t add) {
+  // Transfer x (0..7) of this wave for tile j: K block x (x < 4) or V block
+  // x - 4, 1 KiB each.
+  auto issue_one = [&](int j, int x) __attribute__((always_inline)) {
+    const bool kx = x < 4;
+    const int i = x & 3;
+    char* st = lds + (kx ? 0 : 2 * kTileB) + (j & 1) * kTileB;
+    const uint32_t add = (uint32_t)j * (uint32_t)(kKB * 2) * (uint32_t)(kx ? ldk : ldv);
     const uint32_t base = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)st;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t la = __builtin_amdgcn_readfirstlane(base + (4 * wave + i) * 1024);
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(off[i] + add),
-                   "s"(rs)
+    const uint32_t la = __builtin_amdgcn_readfirstlane(base + (4 * wave + i) * 1024);
+    if (kx)
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(koff[i] + add),
+                   "s"(rs_k)
                    : "memory", "m0");
-    }
+    else
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff[i] + add),
+                   "s"(rs_v)
+                   : "memory", "m0");
   };
   auto issue_tile = [&](int j) {
-    issue(rs_k, koff, lds + (j & 1) * kTileB, (uint32_t)j * (uint32_t)(kKB * 2) * (uint32_t)ldk);
-    issue(rs_v, voff, lds + (2 + (j & 1)) * kTileB, (uint32_t)j * (uint32_t)(kKB * 2) * (uint32_t)ldv);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) issue_one(j, x);
   };
 
   bf16x8 qf[8];
@@ -371,19 +379,33 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (t + 1 < n_tiles) issue_tile(t + 1);
+    const bool more = t + 1 < n_tiles;
     const char* kst = lds + kStage * kTileB;
     const char* vst = lds + (2 + kStage) * kTileB;
 
-    // S^T for two 32-key blocks (raw scores)
+    // S^T for two 32-key blocks (raw scores).  Each pair of MFMAs is followed
+    // by one of the wave's 8 transfers of tile t+1 (issued together after the
+    // barrier, a workgroup's 32 transfers queue at the texture unit and hold
+    // back the MFMAs of the waves that issue them last).
+    // The K operands are read one step ahead: the transfers' asm statements
+    // (memory clobbers) keep the compiler from hoisting the reads itself.
     floatx16 s0 = {}, s1 = {};
+    auto k_pair = [&](int s, bf16x8& ka, bf16x8& kb) __attribute__((always_inline)) {
+      const int off = ((2 * s + hi) ^ k_swz) << 4;
+      ka = *reinterpret_cast<const bf16x8*>(kst + k_lane + off);
+      kb = *reinterpret_cast<const bf16x8*>(kst + k_lane + 32 * 256 + off);
+    };
+    bf16x8 ka, kb;
+    k_pair(0, ka, kb);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const int off = ((2 * s + hi) ^ k_swz) << 4;
-      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kst + k_lane + off);
-      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(kst + k_lane + 32 * 256 + off);
+      bf16x8 na = ka, nb = kb;
+      if (s + 1 < 8) k_pair(s + 1, na, nb);
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[s], s1, 0, 0, 0);
+      if (more) issue_one(t + 1, s);
+      ka = na;
+      kb = nb;
     }
     if (k0 + kKB > T) {  // the last, partial tile: keys past T get a huge negative score
 #pragma unroll
