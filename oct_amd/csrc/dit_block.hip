@@ -321,7 +321,10 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   PROM_STEP(hipGetLastError());
   // FFN up-projection with SwiGLU fused into the GEMM epilogue when the shape
   // allows (F a multiple of 128, D of 64); otherwise GEMM to fp32, then SwiGLU.
-  const hipError_t fused = launch_gemm_bf16_swiglu(Fb, D, r->w_13, Hb, F, T, F, D, st);
+  // (G, unused on the fused path, takes the K-slice sums of a final partial wave.)
+  uint32_t k13 = 1;
+  const hipError_t fused =
+      launch_gemm_bf16_swiglu(Fb, D, r->w_13, Hb, F, T, F, D, st, G, (size_t)T * 2 * F * sizeof(float), &k13);
   if (fused == hipErrorNotSupported) {
     PROM_STEP(launch_gemm_bf16_ex(Fb, D, r->w_13, 2 * F, G, nullptr, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
     const size_t total = (size_t)T * (F / 4);
@@ -330,6 +333,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     PROM_STEP(hipGetLastError());
   } else {
     PROM_STEP(fused);
+    n += k13 - 1;
   }
   PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, nullptr, w2b, D, T, D, F, nullptr, 0, st, nullptr));
   hipLaunchKernelGGL((rows::final_resid_kernel<4, uint16_t>), rows::row_groups<4>(T), dim3(256), 0, st, R, w2b, r->ffn_norm2, gateM, r->output, T, D, eps);

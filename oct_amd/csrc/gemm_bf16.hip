@@ -222,6 +222,18 @@ constexpr int kBK2 = 64;
 constexpr int kLdsA2 = kBK2 + 8;   // 144-byte A rows
 constexpr int kLdsB2 = kBN2 + 16;  // 544-byte B rows: 4 consecutive rows land on distinct banks
 
+// Tile (tm, tn) of grouped position pid: groups of kGroupM rows of tiles,
+// column-major inside a group.
+__device__ __forceinline__ void pid_tile2(int pid, int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int per_group = kGroupM * tiles_n;
+  const int group = pid / per_group;
+  const int first_m = group * kGroupM;
+  const int group_m = min(tiles_m - first_m, kGroupM);
+  const int in_group = pid - group * per_group;
+  *tm = first_m + in_group % group_m;
+  *tn = in_group / group_m;
+}
+
 __device__ __forceinline__ void map_tile2(int tiles_m, int tiles_n, int* tm, int* tn) {
   const int num_tiles = tiles_m * tiles_n;
   const int pid = xcd_pid((int)blockIdx.x, num_tiles);
@@ -586,11 +598,9 @@ __device__ __forceinline__ void stage_barrier() {
 
 template <bool kSwiGLU, int kSt>
 __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                                                   float* C, int M, int N, int K, int tiles_m, int tiles_n, int lda,
-                                                   int ldb, int ldc, const float* R, int ldr, uint16_t* Cb,
-                                                   char* const (&S)[kSt]) {
-  int tm, tn;
-  map_tile2(tiles_m, tiles_n, &tm, &tn);
+                                                   float* C, int M, int N, int K, int tm, int tn, int kt0,
+                                                   int k_tiles, int lda, int ldb, int ldc, const float* R, int ldr,
+                                                   uint16_t* Cb, float2* part, char* const (&S)[kSt]) {
   const int row0 = tm * kBM2;
   const int col0 = kSwiGLU ? tn * (kBN2 / 2) : tn * kBN2;
   const int tid = (int)threadIdx.x;
@@ -692,7 +702,6 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
     }
     return f;
   };
-  const int k_tiles = K / kBK4;
   // Step t: wait until this wave's transfers of tile t+1 have landed (the
   // kSt-3 tiles after it may stay in flight), barrier (tile t+1 complete for
   // all waves, tile t-1's stage free), issue tile t+kSt-1 into that stage, run
@@ -724,7 +733,7 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
     stage_barrier();
     const bool more = t + kSt - 1 < k_tiles;
     char* const next = S[(u + kSt - 1) % kSt];
-    const int k_next = (t + kSt - 1) * kBK4;
+    const int k_next = (kt0 + t + kSt - 1) * kBK4;
     const Frags f1 = read(S[u], 1);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -736,7 +745,7 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
   };
 #pragma unroll
   for (int j = 0; j < kSt - 1; ++j)
-    if (j < k_tiles) issue(S[j], j * kBK4);
+    if (j < k_tiles) issue(S[j], (kt0 + j) * kBK4);
   wait_tiles(min(kSt - 2, k_tiles - 1));  // tile 0 complete before its first reads
   stage_barrier();
   f0 = read(S[0], 0);
@@ -762,6 +771,19 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
   const int lgrp = hk * 4;
   if constexpr (kSwiGLU) {
     const int col = col0 + wn * 32 + lrow;
+    if (part != nullptr) {
+      // one K slice of a split tile: the raw (gate, up) sums, [256 rows][128 columns]
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const int rl = wm * 128 + mi * 32 + lgrp;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = 8 * (r >> 2) + (r & 3);
+          if (row0 + rl + dr < M) part[(size_t)(rl + dr) * 128 + (col - col0)] = make_float2(acc[mi][0][r], acc[mi][1][r]);
+        }
+      }
+      return;
+    }
     if (col < N) {
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
@@ -814,27 +836,71 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_kernel(const uint16_t* _
   __shared__ __attribute__((aligned(1024))) char S3[kStage4];
   __shared__ __attribute__((aligned(1024))) char S4[kStage4];
   char* const st[5] = {S0, S1, S2, S3, S4};
-  gemm_bf16_dl4_body<false>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, Cb, st);
+  int tm, tn;
+  map_tile2(tiles_m, tiles_n, &tm, &tn);
+  gemm_bf16_dl4_body<false>(A, B, C, M, N, K, tm, tn, 0, K / kBK4, lda, ldb, ldc, R, ldr, Cb, nullptr, st);
 }
 
+// Workgroups b < n_main take whole tiles (pids 0 .. n_main-1, XCD-contiguous);
+// the rest take one of `splits` K slices of the tiles n_main .. (tiles of a
+// final partial wave, split so that they fill it), writing their raw sums to
+// part for swiglu_splitk_kernel.
 __global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_swiglu_kernel(const uint16_t* __restrict__ A,
                                                                      const uint16_t* __restrict__ B, int M, int N,
                                                                      int K, int tiles_m, int tiles_n, int lda, int ldb,
-                                                                     int ldh, uint16_t* H) {
+                                                                     int ldh, uint16_t* H, int n_main, int splits,
+                                                                     float2* part) {
   __shared__ __attribute__((aligned(1024))) char S0[kStage4];
   __shared__ __attribute__((aligned(1024))) char S1[kStage4];
   __shared__ __attribute__((aligned(1024))) char S2[kStage4];
   __shared__ __attribute__((aligned(1024))) char S3[kStage4];
   __shared__ __attribute__((aligned(1024))) char S4[kStage4];
   char* const st[5] = {S0, S1, S2, S3, S4};
-  gemm_bf16_dl4_body<true>(A, B, nullptr, M, N, K, tiles_m, tiles_n, lda, ldb, ldh, nullptr, 0, H, st);
+  const int b = (int)blockIdx.x;
+  const int k_tiles = K / kBK4;
+  int pid = 0, kt0 = 0, kn = k_tiles;
+  float2* dst = nullptr;
+  if (b < n_main) {
+    pid = xcd_pid(b, n_main);
+  } else {
+    const int j = b - n_main;
+    const int s = j % splits;
+    pid = n_main + j / splits;
+    kt0 = s * k_tiles / splits;
+    kn = (s + 1) * k_tiles / splits - kt0;
+    dst = part + (size_t)j * (kBM2 * 128);
+  }
+  int tm, tn;
+  pid_tile2(pid, tiles_m, tiles_n, &tm, &tn);
+  gemm_bf16_dl4_body<true>(A, B, nullptr, M, N, K, tm, tn, kt0, kn, lda, ldb, ldh, nullptr, 0, H, dst, st);
+}
+
+// h = silu(g) * u for the split tiles: (g, u) summed over the K slices in
+// slice order (the same expression and rounding as the GEMM epilogue).
+__global__ __launch_bounds__(256) void swiglu_splitk_kernel(const float2* __restrict__ part, uint16_t* __restrict__ H,
+                                                            int ldh, int M, int tiles_m, int tiles_n, int n_main,
+                                                            int splits) {
+  const int ti = (int)blockIdx.y;
+  const int e = (int)(blockIdx.x * 256 + threadIdx.x);  // element of the 256 x 128 tile
+  const int rl = e >> 7, cl = e & 127;
+  int tm, tn;
+  pid_tile2(n_main + ti, tiles_m, tiles_n, &tm, &tn);
+  const int row = tm * kBM2 + rl;
+  if (row >= M) return;
+  const float2* p = part + (size_t)ti * splits * (kBM2 * 128) + e;
+  float g = p[0].x, u = p[0].y;
+  for (int s = 1; s < splits; ++s) {
+    g += p[(size_t)s * (kBM2 * 128)].x;
+    u += p[(size_t)s * (kBM2 * 128)].y;
+  }
+  H[(size_t)row * ldh + tn * 128 + cl] = f32_to_bf16_rne(g / (1.0f + expf(-g)) * u);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // The four-stage kernel wins once a CU runs more than one tile in turn or the
 // K loop is long (measured on MI355X; see its comment).
-inline bool use_four_stage(int tiles, uint32_t k) { return tiles > 256 || k >= 8192; }
+inline bool use_four_stage(int tiles, uint32_t k) { return tiles >= 256 || k >= 8192; }
 
 }  // namespace
 
@@ -873,7 +939,9 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
 }
 
 hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w13, uint16_t* h, int ldh, uint32_t m,
-                                   uint32_t f, uint32_t k, hipStream_t stream) {
+                                   uint32_t f, uint32_t k, hipStream_t stream, void* part_ws, size_t part_bytes,
+                                   uint32_t* launches) {
+  if (launches) *launches = 1;
   // Fused path conditions: whole 128-column output tiles, K a multiple of the K
   // tile, 16-byte aligned rows, byte offsets below 2^31; otherwise the caller
   // runs the GEMM and the elementwise SwiGLU separately.
@@ -883,10 +951,31 @@ hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w
   const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
   const int tiles_n2 = (int)(f / 128);
   const dim3 grid((unsigned)(tiles_m2 * tiles_n2));
-  if (use_four_stage(tiles_m2 * tiles_n2, k))
-    hipLaunchKernelGGL(gemm_bf16_dl4_swiglu_kernel, grid, dim3(512), 0, stream, a, w13, (int)m, (int)f, (int)k,
-                       tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, h);
-  else if (k % kBK2 == 0)
+  if (use_four_stage(tiles_m2 * tiles_n2, k)) {
+    // One workgroup per CU: the tiles of a final wave that would run at most
+    // half full are split along K into as many slices as fill it (at most 4,
+    // each of 4 K tiles or more), their partial sums going to part_ws.
+    const int total = tiles_m2 * tiles_n2;
+    const int cus = ctx().props.multiProcessorCount > 0 ? ctx().props.multiProcessorCount : 256;
+    const int rem = total % cus;
+    const int splits = rem > 0 ? std::min(cus / rem, 4) : 0;
+    const int k_tiles = (int)(k / kBK4);
+    const size_t need = (size_t)rem * splits * kBM2 * 128 * sizeof(float2);
+    if (total > cus && splits >= 2 && k_tiles >= 4 * splits && part_ws != nullptr && need <= part_bytes) {
+      const int n_main = total - rem;
+      hipLaunchKernelGGL(gemm_bf16_dl4_swiglu_kernel, dim3((unsigned)(n_main + rem * splits)), dim3(512), 0, stream, a,
+                         w13, (int)m, (int)f, (int)k, tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, h, n_main, splits,
+                         reinterpret_cast<float2*>(part_ws));
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(swiglu_splitk_kernel, dim3(kBM2 * 128 / 256, (unsigned)rem), dim3(256), 0, stream,
+                         reinterpret_cast<const float2*>(part_ws), h, ldh, (int)m, tiles_m2, tiles_n2, n_main, splits);
+      if (launches) *launches = 2;
+    } else {
+      hipLaunchKernelGGL(gemm_bf16_dl4_swiglu_kernel, grid, dim3(512), 0, stream, a, w13, (int)m, (int)f, (int)k,
+                         tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, h, total, 1, nullptr);
+    }
+  } else if (k % kBK2 == 0)
     hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<true>, grid, dim3(512), 0, stream, a, w13, nullptr, (int)m, (int)f,
                        (int)k, tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, nullptr, 0, h);
   else

@@ -140,8 +140,13 @@ hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint
                             hipStream_t stream, int* path_detail);
 // h[m, f] (bf16) = silu(a @ w13[:, :f]) * (a @ w13[:, f:]) in one GEMM; returns
 // hipErrorNotSupported, launching nothing, when the shape is outside the fused path.
+// part_ws (part_bytes, may be null) takes the K-slice sums of the tiles of a
+// final partial wave, which are then split along K; their fixed slice order
+// keeps the result deterministic.  *launches (when given) receives the number
+// of kernels queued.
 hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w13, uint16_t* h, int ldh, uint32_t m,
-                                   uint32_t f, uint32_t k, hipStream_t stream);
+                                   uint32_t f, uint32_t k, hipStream_t stream, void* part_ws, size_t part_bytes,
+                                   uint32_t* launches = nullptr);
 // bf16 flash attention, head dim 128, full (non-causal): Q/K/V/O [T, ld*] with
 // head h at column 128 h.  variant 0: software-pipelined kernel (80 KiB of
 // dynamic LDS); 1: the serial kernel.  hipErrorInvalidValue for other variants.
