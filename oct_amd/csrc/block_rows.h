@@ -118,7 +118,7 @@ __global__ __launch_bounds__(64 * kRows) void norm_mod_kernel(const float* __res
                                                        const float* __restrict__ scale, OutT* __restrict__ out, int T,
                                                        int D, float eps) {
   __shared__ floatx4 sw[1024], ssc[1024];
-  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63);
   const int t = min((int)blockIdx.x * kRows + wave, T - 1);
   const int d4 = D >> 2;
   floatx4 v[kRowChunks];
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64 * kRows) void resid_norm_mod_kernel(const float*
                                                              float* __restrict__ r_out, OutT* __restrict__ f_out, int T,
                                                              int D, float eps) {
   __shared__ floatx4 s2[1024], sg[1024], s3[1024], ssc[1024];
-  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63);
   const int t = min((int)blockIdx.x * kRows + wave, T - 1);
   const int d4 = D >> 2;
   floatx4 v[kRowChunks], xv[kRowChunks];
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(64 * kRows) void final_resid_kernel(const float* __
                                                           const float* __restrict__ n4, const float* __restrict__ gate,
                                                           float* __restrict__ out, int T, int D, float eps) {
   __shared__ floatx4 s4[1024], sg[1024];
-  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63);
   const int t = min((int)blockIdx.x * kRows + wave, T - 1);
   const int d4 = D >> 2;
   floatx4 v[kRowChunks], rv[kRowChunks];
