@@ -135,6 +135,35 @@ def test_dit_block_c5_full(gpu_runtime):
     assert np.all(np.isfinite(out))
 
 
+def test_dit_block_swiglu_k_split(gpu_runtime):
+    """The fused W1|W3 GEMM splits along K the tiles of a final wave that would
+    run at most half full (gemm_bf16.hip, launch_gemm_bf16_swiglu): T = 2064
+    gives 9 x 32 = 288 workgroup tiles, 32 past the first 256 (one per CU on
+    MI355X), split 4 ways and summed by a second kernel.  All rows, the split
+    ones included (rows 2048..2063), are checked against the oracle, and the
+    extra launch shows that the split ran."""
+    grid, text, heads, F, C = (32, 64), 16, 4, 4096, 32
+    T = grid[0] * grid[1] + text
+    D = heads * 128
+    x, cond, w = blocks.make_dit_block(21, T, D, F, C)
+    coords = blocks.joint_coordinates(grid[0], grid[1], text)
+    if gpu_runtime.device_diagnostics().compute_units != 256:
+        pytest.skip("the split case is sized for 256 CUs")
+    rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
+    assert rc == p.PROM_OK, (res.stage, res.detail_code)
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads)
+    row_err = np.linalg.norm(out - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    print(f"T={T} normwise rel err {oracle.normwise_rel_err(out, ref):.3e}, worst row {row_err.max():.3e}, "
+          f"split rows worst {row_err[2048:].max():.3e}", flush=True)
+    assert oracle.normwise_rel_err(out, ref) <= BF16_BLOCK
+    assert row_err.max() <= BF16_BLOCK
+    # same block with one 256-row tile row fewer (T = 2048: 256 tiles, no split)
+    x2, cond2, w2 = blocks.make_dit_block(21, 2048, D, F, C)
+    rc2, res2, _ = gpu_runtime.dit_block_bf16(x2, blocks.joint_coordinates(32, 64, 0), cond2, w2, heads=heads)
+    assert rc2 == p.PROM_OK
+    assert res.kernel_launches == res2.kernel_launches + 1
+
+
 @pytest.mark.parametrize("q_heads,head_dim", [(8, 256), (3, 4)])
 def test_decoder_layer_attention_closed_form(gpu_runtime, q_heads, head_dim):
     """T = 2 layer with a closed-form output (head h weights token 1 by
