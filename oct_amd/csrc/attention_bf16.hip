@@ -62,6 +62,19 @@ constexpr float kLazyLog2 = 8.0f;
 // K/V tile reaches its L2 once per head instead of once per query block (with
 // the blocks of a head spread over all 8 XCDs, each L2 held tiles of about 8
 // heads at once).
+// The two 32-lane halves of a wave hold the two key halves of a query's
+// scores: v_permlane32_swap with v as both operands returns, in every lane l,
+// v[l & 31] and v[l | 32] in registers (__shfl_xor(v, 32) is an LDS
+// permute round trip on the critical path of every tile).
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ void block_coords(int T, int* head, int* qb) {
   const int nqb = (T + 4 * kQW - 1) / (4 * kQW);
   const int p = xcd_pid((int)blockIdx.x, (int)gridDim.x);
@@ -418,7 +431,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
     float mt = fmaxf(s0[0], s1[0]);
 #pragma unroll
     for (int r = 1; r < 16; ++r) asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mt) : "v"(mt), "v"(s0[r]), "v"(s1[r]));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = max_halves(mt);
     // Lazy rescaling: the reference maximum m_run moves only when the tile's
     // maximum exceeds it by more than kLazyLog2, so p <= 2^kLazyLog2 and O and
     // the running sum are rescaled in a handful of tiles, not in most.
@@ -479,7 +492,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
   // Normalise and stage the wave's [32 q][128 d] output through LDS (34 KiB
   // from offset 0); the barrier ends every wave's reads of the stages.
   __syncthreads();
-  const float l_run = l_part + __shfl_xor(l_part, 32, 64);
+  const float l_run = sum_halves(l_part);
   uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + wave * (kQW * kKP);
   const float inv_l = 1.0f / l_run;
 #pragma unroll
