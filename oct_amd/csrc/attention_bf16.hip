@@ -62,19 +62,6 @@ constexpr float kLazyLog2 = 8.0f;
 // K/V tile reaches its L2 once per head instead of once per query block (with
 // the blocks of a head spread over all 8 XCDs, each L2 held tiles of about 8
 // heads at once).
-// The two 32-lane halves of a wave hold the two key halves of a query's
-// scores: v_permlane32_swap with v as both operands returns, in every lane l,
-// v[l & 31] and v[l | 32] in registers (__shfl_xor(v, 32) is an LDS
-// permute round trip on the critical path of every tile).
-__device__ __forceinline__ float max_halves(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float sum_halves(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 __device__ __forceinline__ void block_coords(int T, int* head, int* qb) {
   const int nqb = (T + 4 * kQW - 1) / (4 * kQW);
   const int p = xcd_pid((int)blockIdx.x, (int)gridDim.x);

@@ -183,7 +183,7 @@ __device__ __forceinline__ void flash_attn_f32_body(const AttnLaunch& a, char* S
     float mt = s[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = max_halves(mt);
     const float m_new = fmaxf(m_run, mt * a.scale_log2);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // a query with no visible key yet
     float lt = 0.0f;
@@ -192,7 +192,7 @@ __device__ __forceinline__ void flash_attn_f32_body(const AttnLaunch& a, char* S
       s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.scale_log2, -m_use));
       lt += s[r];
     }
-    lt += __shfl_xor(lt, 32, 64);
+    lt = sum_halves(lt);
     if (__builtin_amdgcn_read_exec() & __ballot(m_new > m_run)) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       l_run *= alpha;

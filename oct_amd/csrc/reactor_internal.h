@@ -27,6 +27,19 @@ __device__ __forceinline__ int xcd_pid(int b, int n) {
   return x * q + min(x, r) + (b >> 3);
 }
 
+// max / sum of v over lanes l and l ^ 32 of a wave64 (the attention kernels
+// keep a query's scores in the two 32-lane halves).  v_permlane32_swap with v
+// as both operands returns v[l & 31] and v[l | 32] in every lane l, in
+// registers; __shfl_xor(v, 32) is an LDS permute round trip.
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
 // Staging slots: 0-3 operand staging, 4 block workspace, 5 block host staging,
