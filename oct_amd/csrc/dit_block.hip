@@ -220,10 +220,10 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ G
     const floatx4 g = reinterpret_cast<const floatx4*>(G + t * 2 * F)[i];
     const floatx4 u = reinterpret_cast<const floatx4*>(G + t * 2 * F + F)[i];
     floatx4 o;
-    o.x = g.x / (1.0f + expf(-g.x)) * u.x;
-    o.y = g.y / (1.0f + expf(-g.y)) * u.y;
-    o.z = g.z / (1.0f + expf(-g.z)) * u.z;
-    o.w = g.w / (1.0f + expf(-g.w)) * u.w;
+    o.x = silu_mul(g.x, u.x);
+    o.y = silu_mul(g.y, u.y);
+    o.z = silu_mul(g.z, u.z);
+    o.w = silu_mul(g.w, u.w);
     rows::store4(Hb + t * F + 4 * i, o);
   }
 }

@@ -538,7 +538,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mfma_dl_kernel(const uint16_
           const int row = row0 + wm * 128 + mi * 32 + 8 * (r >> 2) + lgrp + (r & 3);
           if (row < M) {
             const float g = acc[mi][0][r], u = acc[mi][1][r];
-            Cb[(size_t)row * ldc + col] = f32_to_bf16_rne(g / (1.0f + expf(-g)) * u);
+            Cb[(size_t)row * ldc + col] = f32_to_bf16_rne(silu_mul(g, u));
           }
         }
       }
@@ -794,7 +794,7 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
           const int dr = 8 * (r >> 2) + (r & 3);
           if (rb + dr < M) {
             const float g = acc[mi][0][r], u = acc[mi][1][r];
-            hp[(size_t)dr * ldc] = f32_to_bf16_rne(g / (1.0f + expf(-g)) * u);
+            hp[(size_t)dr * ldc] = f32_to_bf16_rne(silu_mul(g, u));
           }
         }
       }
@@ -876,7 +876,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_swiglu_kernel(const uint
 }
 
 // h = silu(g) * u for the split tiles: (g, u) summed over the K slices in
-// slice order (the same expression and rounding as the GEMM epilogue).
+// slice order, then silu_mul as in the GEMM epilogue.
 __global__ __launch_bounds__(256) void swiglu_splitk_kernel(const float2* __restrict__ part, uint16_t* __restrict__ H,
                                                             int ldh, int M, int tiles_m, int tiles_n, int n_main,
                                                             int splits) {
@@ -893,7 +893,7 @@ __global__ __launch_bounds__(256) void swiglu_splitk_kernel(const float2* __rest
     g += p[(size_t)s * (kBM2 * 128)].x;
     u += p[(size_t)s * (kBM2 * 128)].y;
   }
-  H[(size_t)row * ldh + tn * 128 + cl] = f32_to_bf16_rne(g / (1.0f + expf(-g)) * u);
+  H[(size_t)row * ldh + tn * 128 + cl] = f32_to_bf16_rne(silu_mul(g, u));
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

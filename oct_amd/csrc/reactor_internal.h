@@ -40,6 +40,17 @@ __device__ __forceinline__ float sum_halves(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// silu(g) * u = g / (1 + e^-g) * u with the hardware base-2 exponential and
+// reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each, so ~3e-7 relative
+// error before the bf16 rounding of the result); every bf16 SwiGLU of the DiT
+// block uses this form: the fused GEMM epilogues, the K-split sum and the
+// separate elementwise kernel.  e^-g overflows to infinity for g < -88 and
+// the product goes to -0, as silu does.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
 constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
 // Staging slots: 0-3 operand staging, 4 block workspace, 5 block host staging,
