@@ -2163,9 +2163,12 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_session_destroy(v
    created bound to NoiseRefiner 0 for an existing session, retargeted in
    place through NoiseRefiner 1, ContextRefiner 0/1 and MainTransformer 0..29
    (the session's position names the next block), reset for a new evaluation.
-   The PREFETCH profile is not selected here (profile_fallback_reason 1), so
-   prefetch and activate_prefetch report REBIND_FAILED as the reference does
-   without a separate transfer queue. */
+   A session that requests PREFETCH selects it (fallback reason 0: a second
+   HIP stream is always an independent transfer queue) and its owner holds a
+   second weight window: prefetch uploads the next block into it on that
+   stream, from a caller thread other than the one executing, and
+   activate_prefetch swaps it in and advances the position.  Under
+   MINIMUM_MEMORY both report REBIND_FAILED. */
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_owner_create(
     void* handle, const PrometheusNoiseRefinerRebindRequest* request, uint64_t* out_block_id,
     PrometheusModelBlockEvidence* out_evidence);

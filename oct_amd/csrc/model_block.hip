@@ -134,6 +134,28 @@ struct WeightSet {
   uint32_t allocations = 0;
 };
 
+// The PREFETCH profile's second weight window (reactor_vulkan_model_block.c:
+// 4545-4715, PrometheusModelBlock.concept:1310-1485): a full Z-Image weight
+// set filled from pinned host staging on a transfer stream of its own while
+// the runtime stream executes with the active set.  A prefetch holds `mu`
+// (taken after the device context's lock) for its whole transfer and never
+// takes the device context's lock while holding it, so activation, reset and
+// destroy wait for an in-flight transfer by taking `mu`.
+struct PrefetchWindow {
+  std::mutex mu;
+  bool enabled = false;
+  WeightSet set;
+  void* host[2] = {};    // pinned staging, alternated so a memcpy overlaps the previous copy
+  void* dev = nullptr;   // device staging the FP16 widening reads
+  uint64_t staging_bytes = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t copied[2] = {};  // host[k] may be refilled once copied[k] has completed
+  uint32_t state = PROM_MODEL_WEIGHT_WINDOW_EMPTY;
+  uint32_t target_position = 0, family = 0, parameter_set = 0, count = 0;
+  int program = 0;
+  uint64_t aggregate = 0, generation = 0, transfer_ns = 0;
+};
+
 struct ModelBlock {
   bool created = false;
   bool shared = false;  // the compiled-model owner: retargeted through every family
@@ -149,6 +171,9 @@ struct ModelBlock {
   PrometheusModelBlockWeightDeclaration decl[PROM_MODEL_BLOCK_MAX_WEIGHTS] = {};
   // binding
   WeightSet active, candidate;
+  PrefetchWindow* pf = nullptr;  // the owner's second window under PREFETCH (held by ModelState)
+  uint64_t prefetch_bytes = 0;   // device bytes of that window's weight set
+  uint32_t active_window = 0;    // flips at every activated prefetch
   bool binding_valid = false;
   uint32_t binding_phase = 0;  // 0 empty, 3 uploading, 7 failed (binding_state when not valid)
   uint64_t binding_generation = 0, descriptor_generation = 0;
@@ -195,6 +220,7 @@ struct ModelSession {
   bool created = false;
   uint64_t id = 0, lock = 0;
   uint32_t requested_profile = 0, requested_route = 0;
+  uint32_t selected_profile = PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY;  // decided at owner create
   uint32_t selected_route = 0, route_fallback = 0, route_shader = 0;
   float* buf[3] = {};  // image [1024, D], context [32, D], joint [1056, D]
   Stream streams[3];
@@ -214,6 +240,7 @@ struct ModelSession {
 struct ModelState {
   ModelBlock block;
   ModelSession session;
+  PrefetchWindow prefetch;
   uint64_t next_block_id = 1, next_session_id = 1;
 };
 
@@ -284,8 +311,31 @@ void free_set_proof(WeightSet* s) {
   *s = WeightSet{};
 }
 
+// Waits for an in-flight prefetch (its transfer holds pf->mu), then frees the window.
+void release_prefetch(PrefetchWindow* pf) {
+  std::lock_guard<std::mutex> window(pf->mu);
+  if (pf->stream) (void)hipStreamSynchronize(pf->stream);
+  free_set(&pf->set);
+  free_dev(pf->dev);
+  for (int k = 0; k < 2; ++k) {
+    if (pf->host[k]) (void)hipHostFree(pf->host[k]);
+    if (pf->copied[k]) (void)hipEventDestroy(pf->copied[k]);
+    pf->host[k] = nullptr;
+    pf->copied[k] = nullptr;
+  }
+  if (pf->stream) (void)hipStreamDestroy(pf->stream);
+  pf->stream = nullptr;
+  pf->dev = nullptr;
+  pf->staging_bytes = 0;
+  pf->enabled = false;
+  pf->state = PROM_MODEL_WEIGHT_WINDOW_EMPTY;
+  pf->target_position = pf->family = pf->parameter_set = pf->count = 0;
+  pf->aggregate = pf->transfer_ns = 0;
+}
+
 void release_block(ModelBlock* b) {
   if (ctx().available) (void)hipStreamSynchronize(ctx().stream);
+  if (b->pf) release_prefetch(b->pf);
   if (b->program == kProgProof) {
     free_set_proof(&b->active);
     free_set_proof(&b->candidate);
@@ -338,7 +388,7 @@ void fill_evidence(const ModelBlock* b, int32_t detail, PrometheusModelBlockEvid
   ev->struct_size = (uint32_t)sizeof(*ev);
   ev->detail_code = detail;
   if (b == nullptr || !b->created) return;
-  const uint64_t persistent = b->active.bytes + b->candidate.bytes;
+  const uint64_t persistent = b->active.bytes + b->candidate.bytes + b->prefetch_bytes;
   const uint64_t audit = b->audit_alloc_bytes;
   ev->created = 1u;
   ev->weights_uploaded = b->binding_valid ? 1u : 0u;
@@ -364,6 +414,7 @@ void fill_evidence(const ModelBlock* b, int32_t detail, PrometheusModelBlockEvid
   ev->assembly_family = b->family;
   ev->parameter_set = b->parameter_set;
   ev->binding_state = binding_state(b);
+  ev->active_weight_window = b->active_window;
   ev->parameter_set_aggregate_identity = b->aggregate;
   ev->binding_generation = b->binding_generation;
   ev->output_generation = b->output_generation;
@@ -411,7 +462,7 @@ void fill_session_evidence(const ModelSession* s, PrometheusCompiledModelSession
   ev->cold_buffer_allocation_count = s->cold_allocations;
   ev->composition_count = s->compositions;
   ev->requested_execution_profile = s->requested_profile;
-  ev->selected_execution_profile = PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY;
+  ev->selected_execution_profile = s->selected_profile;
   ev->profile_fallback_reason = s->profile_fallback;
   ev->requested_main_attention_route = s->requested_route;
   ev->selected_main_attention_route = s->selected_route;
@@ -1354,6 +1405,64 @@ bool retarget_uploads_match(const ModelBlock* b, const PrometheusModelBlockWeigh
       return false;
   }
   return true;
+}
+
+// The PREFETCH window of a freshly created owner (bound to NoiseRefiner 0, so
+// alloc_set lays out all 13 slots, which also hold any ContextRefiner set):
+// its weight set, two pinned staging buffers and a device staging buffer of
+// the largest weight, a non-blocking stream at the default priority and two
+// events (reactor_vulkan_model_block.c:1730-1741).
+bool alloc_prefetch(ModelBlock* b, PrefetchWindow* pf) {
+  std::lock_guard<std::mutex> window(pf->mu);
+  b->pf = pf;  // release_block frees a partial window
+  pf->staging_bytes = b->staging_bytes;
+  if (!alloc_set(b, &pf->set) || !alloc_dev(b, &pf->dev, pf->staging_bytes) ||
+      hipStreamCreateWithFlags(&pf->stream, hipStreamNonBlocking) != hipSuccess) {
+    pf->stream = nullptr;
+    return false;
+  }
+  for (int k = 0; k < 2; ++k) {
+    if (hipHostMalloc(&pf->host[k], (size_t)pf->staging_bytes, hipHostMallocDefault) != hipSuccess) {
+      pf->host[k] = nullptr;
+      return false;
+    }
+    ++b->cold_allocations;
+    if (hipEventCreateWithFlags(&pf->copied[k], hipEventDisableTiming) != hipSuccess) {
+      pf->copied[k] = nullptr;
+      return false;
+    }
+  }
+  pf->enabled = true;
+  pf->state = PROM_MODEL_WEIGHT_WINDOW_EMPTY;
+  b->prefetch_bytes = pf->set.bytes;
+  b->reusable_bytes += pf->staging_bytes;
+  return true;
+}
+
+// One prefetch transfer (PrometheusModelBlock.concept:1370-1404): weight i is
+// copied into pinned staging, sent to the device staging buffer and widened
+// from FP16 into its slot of the window on the window's stream.  The caller
+// holds pf->mu and not the device context's lock.  Returns 0 or a detail.
+int32_t prefetch_transfer(PrefetchWindow* pf, const Target& t, const PrometheusModelBlockWeightUpload* uploads) {
+  if (hipSetDevice(ctx().device) != hipSuccess) return PROM_MODEL_BLOCK_DETAIL_COMMAND_RECORD_FAILED;
+  for (uint32_t i = 0; i < t.count; ++i) {
+    const int k = (int)(i & 1u);
+    // the copy that last read host[k] (weight i - 2) must have completed
+    if (i >= 2 && hipEventSynchronize(pf->copied[k]) != hipSuccess)
+      return PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
+    const PrometheusModelBlockWeightUpload& u = uploads[i];
+    memcpy(pf->host[k], u.bytes, (size_t)u.byte_count);
+    const SlotShape& sh = kSlots[t.program == kProgContext ? i + 2u : i];
+    float* dst = static_cast<float*>(pf->set.buf[sh.owner]) + sh.col0;
+    if (hipMemcpyAsync(pf->dev, pf->host[k], (size_t)u.byte_count, hipMemcpyHostToDevice, pf->stream) != hipSuccess ||
+        hipEventRecord(pf->copied[k], pf->stream) != hipSuccess ||
+        launch_widen_f16(static_cast<const uint16_t*>(pf->dev), dst, sh.rows, sh.cols, sh.ld, pf->stream) !=
+            hipSuccess) {
+      (void)hipStreamSynchronize(pf->stream);
+      return PROM_MODEL_BLOCK_DETAIL_QUEUE_SUBMIT_FAILED;
+    }
+  }
+  return hipStreamSynchronize(pf->stream) == hipSuccess ? 0 : PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN;
 }
 
 
@@ -2655,9 +2764,13 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_owner_create(
       return PROM_ERROR;
     }
     ModelSession* s = &rt->model->session;
-    // A weight prefetch needs a transfer queue of its own; this library runs
-    // every copy on the runtime stream, so PREFETCH falls back (reason 1).
-    s->profile_fallback = s->requested_profile == PROM_MODEL_EXECUTION_PROFILE_PREFETCH ? 1u : 0u;
+    // reactor_vulkan_model_block.c:4364-4380: PREFETCH needs a transfer queue
+    // independent of compute; a second HIP stream always is one, so the
+    // requested profile is selected without a fallback.
+    s->selected_profile = s->requested_profile == PROM_MODEL_EXECUTION_PROFILE_PREFETCH
+                              ? PROM_MODEL_EXECUTION_PROFILE_PREFETCH
+                              : PROM_MODEL_EXECUTION_PROFILE_MINIMUM_MEMORY;
+    s->profile_fallback = 0u;
     const RouteDecision route = decide_main_route(s->requested_route);  // reactor_vulkan_model_block.c:4381-4408
     s->selected_route = route.selected;
     s->route_fallback = route.fallback;
@@ -2691,6 +2804,13 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_owner_create(
       c.weights[i].byte_count = r->uploads[i].byte_count;
     }
     if (create_block(rt, &c, out_block_id, out_evidence, true) != PROM_OK) return PROM_ERROR;
+    if (s->selected_profile == PROM_MODEL_EXECUTION_PROFILE_PREFETCH &&
+        !alloc_prefetch(&rt->model->block, &rt->model->prefetch)) {
+      release_block(&rt->model->block);
+      *out_block_id = 0;
+      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_RESOURCE_CREATE_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
     if (upload_weights(rt, *out_block_id, r->uploads, 13u, out_evidence) != PROM_OK) {
       release_block(&rt->model->block);
       *out_block_id = 0;
@@ -2755,29 +2875,129 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_retarget(
   });
 }
 
-// reactor_vulkan_model_block.c:4545-4715: only under the PREFETCH profile,
-// which this library does not select (see owner_create).
+// reactor_vulkan_model_block.c:4545-4641: under the PREFETCH profile, uploads
+// the weights of the block the session's position names into the owner's
+// second window.  The transfer runs on the window's stream without the device
+// context's lock, so a caller may execute the active block on another thread
+// meanwhile (tools/prometheus_zimage_bridge/reactor_windows.go:510-531); the
+// evidence of a successful prefetch reports only `created`, because the block's
+// counters belong to that other thread.
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_prefetch(
     void* handle, const PrometheusCompiledModelPrefetchRequest* request, PrometheusModelBlockEvidence* out_evidence) {
-  return with_runtime(handle, out_evidence, [&](Runtime*) -> int {
-    const PrometheusCompiledModelPrefetchRequest* r = request;
-    if (r == nullptr || r->struct_size != sizeof(*r) || r->uploads == nullptr ||
-        r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID) {
-      fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
-      return PROM_ERROR;
-    }
+  Runtime* rt = lookup(handle);
+  const PrometheusCompiledModelPrefetchRequest* r = request;
+  if (rt == nullptr || r == nullptr || r->struct_size != sizeof(*r) || r->uploads == nullptr ||
+      r->lock_identity != PROM_ZIMAGE_TURBO_LOCK_ID) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+    return PROM_ERROR;
+  }
+  std::unique_lock<std::mutex> lock(ctx().mu);
+  ModelState* ms = rt->model;
+  if (ms == nullptr || !ms->block.created || !ms->session.created || ms->session.id != r->session_identity ||
+      ms->session.selected_profile != PROM_MODEL_EXECUTION_PROFILE_PREFETCH || ms->block.pf == nullptr ||
+      !ms->prefetch.enabled) {
     fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
     return PROM_ERROR;
-  });
+  }
+  const uint32_t position = ms->session.retarget_position;
+  Target t;
+  if (position == 0u || !target_at(position, &t) || r->model_local_block_id != t.local ||
+      r->upload_count != t.count || !retarget_uploads_match(&ms->block, r->uploads, t)) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_INVALID_REQUEST, out_evidence);
+    return PROM_ERROR;
+  }
+  PrefetchWindow* pf = &ms->prefetch;
+  // PrometheusModelBlock.concept:1348-1352: a window that holds a prepared set
+  // (or is being filled by another call) is not begun again.
+  std::unique_lock<std::mutex> window(pf->mu, std::try_to_lock);
+  if (!window.owns_lock() || pf->state == PROM_MODEL_WEIGHT_WINDOW_DEVICE_READY) {
+    fill_evidence(nullptr, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+    return PROM_ERROR;
+  }
+  pf->state = PROM_MODEL_WEIGHT_WINDOW_UPLOAD_SUBMITTED;
+  pf->target_position = 0;
+  lock.unlock();  // compute may proceed; destroy, reset and activation wait on pf->mu
+  const uint64_t t0 = wall_ns();
+  const int32_t detail = prefetch_transfer(pf, t, r->uploads);
+  if (detail != 0) {
+    pf->state = PROM_MODEL_WEIGHT_WINDOW_UNCERTAIN;
+    fill_evidence(nullptr, detail, out_evidence);
+    return PROM_ERROR;
+  }
+  pf->transfer_ns = wall_ns() - t0;
+  pf->state = PROM_MODEL_WEIGHT_WINDOW_DEVICE_READY;
+  pf->program = (int)t.program;
+  pf->family = t.family;
+  pf->parameter_set = t.parameter_set;
+  pf->count = t.count;
+  pf->aggregate = t.aggregate;
+  pf->target_position = position;
+  pf->generation += 1;
+  fill_evidence(nullptr, 0, out_evidence);
+  if (out_evidence) out_evidence->created = 1u;
+  return PROM_OK;
 }
 
+// reactor_vulkan_model_block.c:4643-4715: swaps the prepared window in as the
+// owner's active weights when it holds the block the session's position names
+// (waiting for a transfer still in flight), and advances the position.
 PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_activate_prefetch(
     void* handle, uint64_t session_id, PrometheusModelBlockEvidence* out_evidence) {
   return with_runtime(handle, out_evidence, [&](Runtime* rt) -> int {
-    ModelBlock* b = rt->model && rt->model->block.created ? &rt->model->block : nullptr;
-    (void)session_id;
-    fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
-    return PROM_ERROR;
+    ModelState* ms = rt->model;
+    ModelBlock* b = ms && ms->block.created ? &ms->block : nullptr;
+    ModelSession* s = ms ? &ms->session : nullptr;
+    if (b == nullptr || !s->created || s->id != session_id ||
+        s->selected_profile != PROM_MODEL_EXECUTION_PROFILE_PREFETCH || b->pf == nullptr) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    PrefetchWindow* pf = b->pf;
+    std::lock_guard<std::mutex> window(pf->mu);
+    if (pf->target_position != s->retarget_position) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    if (!reap(b)) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_COMPLETION_UNCERTAIN, out_evidence);
+      return PROM_ERROR;
+    }
+    if (pf->state != PROM_MODEL_WEIGHT_WINDOW_DEVICE_READY) {  // PrometheusModelBlock.concept:1406-1409
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_REBIND_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    const Program program = (Program)pf->program;
+    if (b->program != program && !set_program(b, program)) {
+      fill_evidence(b, PROM_MODEL_BLOCK_DETAIL_DESCRIPTOR_UPDATE_FAILED, out_evidence);
+      return PROM_ERROR;
+    }
+    // PrometheusModelBlock.concept:1428-1448: the windows trade places.
+    std::swap(b->active, pf->set);
+    b->family = pf->family;
+    b->parameter_set = pf->parameter_set;
+    b->weight_count = pf->count;
+    b->aggregate = pf->aggregate;
+    b->uploads += pf->count;
+    b->last_memcpy_ns = pf->transfer_ns;
+    b->binding_valid = true;
+    b->binding_phase = PROM_NOISE_REFINER_BINDING_BOUND;
+    b->binding_generation += 1;
+    b->descriptor_generation += 1;
+    b->output_valid = false;
+    b->audit_valid = false;
+    b->resident_input_generation = 0;
+    b->replay_identity = 0;
+    b->prefix_replay = 0;
+    b->active_window ^= 1u;
+    b->last_detail = 0;
+    pf->state = PROM_MODEL_WEIGHT_WINDOW_EMPTY;
+    pf->target_position = 0;
+    pf->count = 0;
+    s->retarget_position += 1;
+    s->active_block_id = b->id;
+    s->binding_generation = b->binding_generation;
+    fill_evidence(b, 0, out_evidence);
+    return PROM_OK;
   });
 }
 
@@ -2791,6 +3011,12 @@ PROM_REACTOR_API int prometheus_reactor_runtime_compiled_model_evaluation_reset(
     if (s == nullptr || b == nullptr || !b->created || !b->shared || s->joint_writing || !reap(b)) {
       fill_session_evidence(nullptr, out_evidence, PROM_MODEL_SESSION_DETAIL_INVALID_REQUEST);
       return PROM_ERROR;
+    }
+    if (b->pf != nullptr) {  // reactor_vulkan_model_block.c:4731-4734: waits for and drops a prefetch
+      std::lock_guard<std::mutex> window(b->pf->mu);
+      b->pf->state = PROM_MODEL_WEIGHT_WINDOW_EMPTY;
+      b->pf->target_position = 0;
+      b->pf->count = 0;
     }
     for (Stream& st : s->streams) st = Stream{st.generation, 0, 0, false};
     s->joint_image_generation = 0;

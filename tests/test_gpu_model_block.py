@@ -12,6 +12,8 @@ FP16 weights and BF16 inputs at the lock's shapes (1024 image, 32 context,
 1056 joint tokens; width 3840, 30 heads, FFN 10240).
 """
 import json
+import threading
+import time
 from pathlib import Path
 
 import numpy as np
@@ -419,13 +421,15 @@ def test_compiled_owner_drives_the_bridge_sequence(model, weights, inputs):
     ContextRefiner 0/1 and MainTransformer layers, then a reset evaluation."""
     x_bits, t_bits, ctx = inputs
     cond = oracle.from_bf16(t_bits).astype(np.float64)
-    rc, sid, sev = model.session_create(profile=2)  # PREFETCH requested
+    rc, sid, sev = model.session_create(profile=1)  # MINIMUM_MEMORY
     assert rc == p.PROM_OK
     rc, oid, ev = model.owner_create(weights["nr0"])
     assert rc == p.PROM_OK and oid != 0, ev.detail_code
     sev = model.session_evidence(sid)[1]
-    assert sev.selected_execution_profile == 1 and sev.profile_fallback_reason == 1
+    assert sev.selected_execution_profile == 1 and sev.profile_fallback_reason == 0
+    # prefetch belongs to the PREFETCH profile only
     assert model.prefetch(sid, 1, weights["nr1"])[1].detail_code == D["REBIND_FAILED"]
+    assert model.activate_prefetch(sid)[1].detail_code == D["REBIND_FAILED"]
     rc, ev = model.noise_refiner_execute(oid, x_bits, t_bits)
     assert rc == p.PROM_OK
     first_nr0 = np.zeros(T_IMG * W, np.float32)
@@ -491,6 +495,170 @@ def test_compiled_owner_drives_the_bridge_sequence(model, weights, inputs):
     assert model.audit_final("noise", oid, ev.output_generation, again)[0] == p.PROM_OK
     np.testing.assert_array_equal(again, first_nr0)
     assert model.destroy(oid) == p.PROM_OK
+    assert model.session_destroy(sid) == p.PROM_OK
+
+
+# ------------------------------------------------------------ PREFETCH profile
+# Device bytes of one fp32 Z-Image weight set (13 slots, w1 and w3 sharing W13).
+SET_BYTES = 4 * (15360 + 256 * 15360 + 128 + W * W + 128 + W * 3 * W + 2 * W + W * 2 * 10240 + 10240 * W + 2 * W)
+CHAIN = [(1, "nr1", mb.ZIMAGE_TENSORS), (0, "cr0", mb.CONTEXT_TENSORS), (1, "cr1", mb.CONTEXT_TENSORS),
+         (0, "main0", mb.ZIMAGE_TENSORS), (1, "nr1", mb.ZIMAGE_TENSORS)]
+
+
+class Advance:
+    """Moves the owner to CHAIN[i]: with prefetch, the upload starts on a
+    second thread (the bridge's goroutine, reactor_windows.go:510-545) before
+    the caller executes the current block and is activated afterwards;
+    otherwise the owner is retargeted in place."""
+
+    def __init__(self, model, sid, weights, prefetch):
+        self.model, self.sid, self.weights, self.prefetch = model, sid, weights, prefetch
+        self.thread, self.result, self.windows = None, None, []
+
+    def start(self, i):
+        if not self.prefetch:
+            return
+        local, name, names = CHAIN[i]
+
+        def run():
+            t0 = time.perf_counter()
+            self.result = self.model.prefetch(self.sid, local, self.weights[name], names), time.perf_counter() - t0
+
+        self.thread = threading.Thread(target=run)
+        self.thread.start()
+
+    def finish(self, i):
+        local, name, names = CHAIN[i]
+        if self.prefetch:
+            self.thread.join(timeout=100)
+            assert not self.thread.is_alive(), "prefetch did not return"
+            (rc, ev), seconds = self.result
+            assert rc == p.PROM_OK and ev.created == 1, (i, ev.detail_code)
+            print(f"prefetch {name}: {seconds * 1e3:.1f} ms on its thread", flush=True)
+            if i == 0:  # a prepared window is not begun again
+                rc, ev = self.model.prefetch(self.sid, local, self.weights[name], names)
+                assert rc == p.PROM_ERROR and ev.detail_code == D["REBIND_FAILED"]
+            t0 = time.perf_counter()
+            rc, ev = self.model.activate_prefetch(self.sid)
+            self.windows.append(ev.active_weight_window)
+        else:
+            t0 = time.perf_counter()
+            rc, ev = self.model.retarget(self.sid, local, self.weights[name], names)
+        print(f"{'activate' if self.prefetch else 'retarget'} {name}: {(time.perf_counter() - t0) * 1e3:.1f} ms "
+              "on the executing thread", flush=True)
+        assert rc == p.PROM_OK, (i, ev.detail_code)
+        assert ev.weight_count == len(names) and ev.output_valid == 0
+        return ev
+
+
+def owner_evaluation(model, sid, oid, weights, inputs, prefetch):
+    """NoiseRefiner 0/1, ContextRefiner 0/1 and MainTransformer layers 0/1 on
+    the owner, which is bound to NoiseRefiner 0 on entry; returns the prepared
+    image, the prepared context and the final joint output."""
+    x_bits, t_bits, ctx = inputs
+    adv = Advance(model, sid, weights, prefetch)
+    adv.start(0)
+    rc, ev = model.noise_refiner_execute(oid, x_bits, t_bits)
+    assert rc == p.PROM_OK, ev.detail_code
+    gen = ev.output_generation
+    adv.finish(0)
+    adv.start(1)
+    rc, ev = model.noise_refiner_resident(oid, gen)
+    assert rc == p.PROM_OK, ev.detail_code
+    rc, sev = model.session_capture(sid, oid, ev.output_generation)
+    assert rc == p.PROM_OK
+    image_gen = sev.prepared_image_generation
+    image = np.zeros(T_IMG * W, np.float32)
+    assert model.audit_final("noise", oid, ev.output_generation, image)[0] == p.PROM_OK
+    adv.finish(1)
+    assert model.session_evidence(sid)[1].active_block_id == oid
+    adv.start(2)
+    rc, ev = model.context_refiner0_execute(oid, ctx)
+    assert rc == p.PROM_OK, ev.detail_code
+    gen = ev.output_generation
+    adv.finish(2)
+    adv.start(3)
+    rc, ev = model.context_refiner_resident(oid, gen)
+    assert rc == p.PROM_OK, ev.detail_code
+    rc, sev = model.session_capture(sid, oid, ev.output_generation)
+    assert rc == p.PROM_OK
+    context_gen = sev.prepared_context_generation
+    context = np.zeros(T_CTX * W, np.float32)
+    assert model.audit_final("context", oid, ev.output_generation, context)[0] == p.PROM_OK
+    adv.finish(3)
+    rc, sev = model.session_compose(sid, image_gen, context_gen)
+    assert rc == p.PROM_OK
+    joint_gen = sev.joint_generation
+    adv.start(4)
+    rc, ev = model.main_transformer_execute(oid, sid, 0, t_bits, image_gen, context_gen, joint_gen, chain=True)
+    assert rc == p.PROM_OK, ev.detail_code
+    ev_layer1 = adv.finish(4)
+    assert ev_layer1.parameter_set == 2 and ev_layer1.assembly_family == p.PROM_MAIN_TRANSFORMER_FAMILY
+    rc, ev = model.main_transformer_execute(oid, sid, 1, t_bits, image_gen, context_gen, joint_gen + 1, chain=True)
+    assert rc == p.PROM_OK, ev.detail_code
+    out = np.zeros(T_JOINT * W, np.float32)
+    assert model.audit_final("main", oid, ev.output_generation, out)[0] == p.PROM_OK
+    if prefetch:  # the two windows alternate at every activation
+        assert adv.windows == [1, 0, 1, 0, 1]
+    return image, context, out
+
+
+def test_compiled_owner_prefetch_profile(model, weights, inputs):
+    """The PREFETCH profile (reactor_vulkan_model_block.c:4364-4380, 4545-4715):
+    every next block is uploaded into the owner's second window on another
+    thread while the current block executes, then activated.  The evaluation
+    equals the one the same session then runs by in-place retargets bit for
+    bit, and its prepared image equals the binary64 NoiseRefiner 0 -> 1 chain."""
+    x_bits, t_bits, ctx = inputs
+    rc, sid, sev = model.session_create(profile=2)
+    assert rc == p.PROM_OK
+    rc, oid, ev = model.owner_create(weights["nr0"])
+    assert rc == p.PROM_OK and oid != 0, ev.detail_code
+    assert ev.persistent_bytes == 2 * SET_BYTES, (ev.persistent_bytes, SET_BYTES)
+    sev = model.session_evidence(sid)[1]
+    assert sev.selected_execution_profile == 2 and sev.profile_fallback_reason == 0
+    # refusals before any transfer: nothing prepared, the wrong block, the wrong session
+    assert model.activate_prefetch(sid)[1].detail_code == D["REBIND_FAILED"]
+    assert model.prefetch(sid, 0, weights["nr1"])[1].detail_code == D["INVALID_REQUEST"]
+    assert model.prefetch(sid, 1, weights["cr0"], mb.CONTEXT_TENSORS)[1].detail_code == D["INVALID_REQUEST"]
+    assert model.prefetch(sid + 1, 1, weights["nr1"])[1].detail_code == D["REBIND_FAILED"]
+
+    image_a, context_a, out_a = owner_evaluation(model, sid, oid, weights, inputs, prefetch=True)
+    cond = oracle.from_bf16(t_bits).astype(np.float64)
+    coords = blocks.image_coordinates(T_IMG)
+    nr0 = blocks.zimage_block_f64(oracle.from_bf16(x_bits).astype(np.float64), coords, weights["nr0"], cond)
+    ref = blocks.zimage_block_f64(nr0, coords, weights["nr1"], cond, rows=ROWS_IMG)
+    err = rel_l2(image_a.reshape(T_IMG, W)[ROWS_IMG], ref)
+    print(f"prefetched NoiseRefiner 0 -> 1 rel L2 {err:.3e}", flush=True)
+    assert err <= BAR
+
+    rc, sev = model.evaluation_reset(sid)
+    assert rc == p.PROM_OK
+    assert model.prefetch(sid, 0, weights["nr0"])[1].detail_code == D["INVALID_REQUEST"]  # position 0 is retargeted
+    rc, ev = model.retarget(sid, 0, weights["nr0"])
+    assert rc == p.PROM_OK
+    image_b, context_b, out_b = owner_evaluation(model, sid, oid, weights, inputs, prefetch=False)
+    np.testing.assert_array_equal(image_a, image_b)
+    np.testing.assert_array_equal(context_a, context_b)
+    np.testing.assert_array_equal(out_a, out_b)
+
+    # a reset drops a prepared window
+    rc, sev = model.evaluation_reset(sid)
+    assert rc == p.PROM_OK
+    assert model.retarget(sid, 0, weights["nr0"])[0] == p.PROM_OK
+    assert model.prefetch(sid, 1, weights["nr1"])[0] == p.PROM_OK
+    assert model.evaluation_reset(sid)[0] == p.PROM_OK
+    assert model.retarget(sid, 0, weights["nr0"])[0] == p.PROM_OK
+    assert model.activate_prefetch(sid)[1].detail_code == D["REBIND_FAILED"]
+    # destroying the owner waits for a transfer in flight on another thread
+    box = {}
+    th = threading.Thread(target=lambda: box.update(r=model.prefetch(sid, 1, weights["nr1"])))
+    th.start()
+    assert model.destroy(oid) == p.PROM_OK
+    th.join(timeout=100)
+    assert not th.is_alive()
+    rc, ev = box["r"]
+    assert (rc, ev.detail_code) in ((p.PROM_OK, 0), (p.PROM_ERROR, D["REBIND_FAILED"])), (rc, ev.detail_code)
     assert model.session_destroy(sid) == p.PROM_OK
 
 
