@@ -372,6 +372,23 @@ constexpr uint32_t kWaveElems = 1024;
 
 __device__ __forceinline__ uint32_t xslot(uint32_t e) { return e ^ ((e >> 4) & 15u); }
 
+// Streaming 16-byte accesses for the passes' data: every element is read once
+// and written once per pass, so neither side is kept in the L2.  With ordinary
+// accesses the dirty lines a pass leaves behind are written back while the
+// next pass runs, which made the first pass 1.7x slower than the second;
+// streaming both sides takes 2^20 points from 33.4 to 28 us.
+typedef double stream_double2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ double2 load_stream(const double2* p) {
+  const stream_double2 v = __builtin_nontemporal_load(reinterpret_cast<const stream_double2*>(p));
+  return make_double2(v.x, v.y);
+}
+
+__device__ __forceinline__ void store_stream(double2* p, double2 v) {
+  const stream_double2 w = {v.x, v.y};
+  __builtin_nontemporal_store(w, reinterpret_cast<stream_double2*>(p));
+}
+
 __device__ __forceinline__ void butterfly(double2& x, double2& y, double2 w) {
 #pragma clang fp contract(off)
   const double2 t = cmul(w, y);
@@ -448,7 +465,7 @@ __device__ __forceinline__ void fft_wave_pass_body(const double2* __restrict__ i
       const uint32_t f = tid + m * kT;
       const uint32_t r = f & ((1u << lgr) - 1u);
       const uint64_t i = f >> lgr;
-      v[m] = kColumns ? in[qwg + r + (i << log2n2)] : in[(qwg << log2n2) + (i << lgg) + r];
+      v[m] = load_stream(in + (kColumns ? qwg + r + (i << log2n2) : (qwg << log2n2) + (i << lgg) + r));
     }
 #pragma unroll
     for (uint32_t u = 0; u < 2; ++u) tw[min(tid + u * kT, tw_last)] = rt[u];
@@ -563,11 +580,11 @@ __device__ __forceinline__ void fft_wave_pass_body(const double2* __restrict__ i
       const uint64_t kk = f & ((1u << lgg) - 1u);
       const uint64_t r = (f >> lgg) & ((1u << lgr) - 1u);
       const uint64_t kg = f >> (lgg + lgr);
-      out[(kg << (log2n2 + lgg)) + ((qwg + r) << lgg) + kk] = smem[oslot1(f)];
+      store_stream(out + (kg << (log2n2 + lgg)) + ((qwg + r) << lgg) + kk, smem[oslot1(f)]);
     } else {
       const uint32_t r = f & ((1u << lgr) - 1u);
       const uint64_t k = f >> lgr;
-      out[qwg + r + (k << log2n1)] = smem[sslot(f)];
+      store_stream(out + qwg + r + (k << log2n1), smem[sslot(f)]);
     }
   }
 }
