@@ -41,9 +41,24 @@ __device__ __forceinline__ floatx4 ld4(__amdgpu_buffer_rsrc_t r, int i) {
   return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(16 * i), 0, 0));
 }
 
+// Sum over the 64 lanes (every lane gets it; call with the whole wave
+// active): four DPP steps within each row of 16 lanes (swap pairs, swap the
+// halves of quads, mirror within 8, mirror within 16), then two lane permutes
+// across the rows, in place of six permutes through the LDS unit (C5
+// resid_norm_mod 47.5 -> 45.5 us).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF,
+                                                                   false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
   return v;
 }
 
