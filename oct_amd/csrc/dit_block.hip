@@ -71,13 +71,12 @@ __global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ co
 // 8 consecutive columns, and the 16 groups take every 16th k; every load of a
 // thread is independent, so they are all in flight together.  The 16 partial
 // sums are added in a fixed order.
-__global__ __launch_bounds__(256) void adaln_vec_kernel(const float* __restrict__ cond,
-                                                        const uint16_t* __restrict__ W, const float* __restrict__ b,
-                                                        float* __restrict__ mod, int C, int D) {
-  __shared__ float part[16][129];
+__device__ __forceinline__ void adaln_vec_block(int blk, const float* __restrict__ cond,
+                                                const uint16_t* __restrict__ W, const float* __restrict__ b,
+                                                float* __restrict__ mod, int C, int D, float (*part)[129]) {
   const int cg = (int)(threadIdx.x & 15);
   const int kg = (int)(threadIdx.x >> 4);
-  const int j0 = (int)blockIdx.x * 128 + cg * 8;
+  const int j0 = blk * 128 + cg * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (j0 < 4 * D) {
 #pragma unroll 4
@@ -96,7 +95,7 @@ __global__ __launch_bounds__(256) void adaln_vec_kernel(const float* __restrict_
   for (int i = 0; i < 8; ++i) part[kg][cg * 8 + i] = acc[i];
   __syncthreads();
   if (threadIdx.x < 128) {
-    const int j = (int)blockIdx.x * 128 + (int)threadIdx.x;
+    const int j = blk * 128 + (int)threadIdx.x;
     if (j < 4 * D) {
       float m = b[j];
 #pragma unroll
@@ -110,9 +109,8 @@ __global__ __launch_bounds__(256) void adaln_vec_kernel(const float* __restrict_
 // RoPE table: tab[t][p] = (cos, sin) of coord[t][axis(p)] * theta^(-2*pair/width)
 // for the 64 pairs of a 128-wide head; angles in binary64 (once per token,
 // shared by every head).
-__global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict__ coords, float2* __restrict__ tab,
-                                                         int T, float theta, int ax0, int ax1) {
-  const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+__device__ __forceinline__ void rope_table_entry(int idx, const float* __restrict__ coords,
+                                                 float2* __restrict__ tab, int T, float theta, int ax0, int ax1) {
   if (idx >= T * 64) return;
   const int t = idx >> 6;
   const int p = idx & 63;
@@ -127,6 +125,28 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict
   const double freq = pow((double)theta, -2.0 * (double)pair / (double)width);
   const double angle = (double)coords[(size_t)t * 3 + axis] * freq;
   tab[idx] = make_float2((float)cos(angle), (float)sin(angle));
+}
+
+__global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict__ coords, float2* __restrict__ tab,
+                                                         int T, float theta, int ax0, int ax1) {
+  rope_table_entry((int)(blockIdx.x * blockDim.x + threadIdx.x), coords, tab, T, theta, ax0, ax1);
+}
+
+// The block's two independent set-up products in one launch (16-byte-aligned
+// adaLN weights): workgroups below n_adaln take 128 adaLN columns each
+// (adaln_vec_block), the rest 256 RoPE-table entries each.  Apart, the two
+// took about 6 us each at C5, one after the other.
+__global__ __launch_bounds__(256) void adaln_rope_kernel(const float* __restrict__ cond,
+                                                         const uint16_t* __restrict__ W, const float* __restrict__ b,
+                                                         float* __restrict__ mod, int C, int D, int n_adaln,
+                                                         const float* __restrict__ coords, float2* __restrict__ tab,
+                                                         int T, float theta, int ax0, int ax1) {
+  __shared__ float part[16][129];
+  const int blk = (int)blockIdx.x;
+  if (blk < n_adaln)
+    adaln_vec_block(blk, cond, W, b, mod, C, D, part);
+  else
+    rope_table_entry((blk - n_adaln) * 256 + (int)threadIdx.x, coords, tab, T, theta, ax0, ax1);
 }
 
 // Per (token, head): q and k RMSNorm over 128 channels, then RoPE on the
@@ -294,16 +314,20 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     ++n;                           \
   } while (0)
   const dim3 blk(256);
-  if ((reinterpret_cast<uintptr_t>(r->w_adaln) & 15u) == 0 && (4 * D) % 8 == 0)
-    hipLaunchKernelGGL(adaln_vec_kernel, dim3((4 * D + 127) / 128), blk, 0, st, r->condition, r->w_adaln, r->b_adaln,
-                       mod, C, D);
-  else
+  if ((reinterpret_cast<uintptr_t>(r->w_adaln) & 15u) == 0 && (4 * D) % 8 == 0) {
+    const int n_adaln = (4 * D + 127) / 128;
+    hipLaunchKernelGGL(adaln_rope_kernel, dim3((unsigned)(n_adaln + (T * 64 + 255) / 256)), blk, 0, st, r->condition,
+                       r->w_adaln, r->b_adaln, mod, C, D, n_adaln, r->coordinates, rope, T, r->rope_theta,
+                       (int)r->rope_axes[0], (int)r->rope_axes[1]);
+    PROM_STEP(hipGetLastError());
+  } else {
     hipLaunchKernelGGL(adaln_kernel, dim3((4 * D + 63) / 64), blk, 0, st, r->condition, r->w_adaln, r->b_adaln, mod, C,
                        D);
-  PROM_STEP(hipGetLastError());
-  hipLaunchKernelGGL(rope_table_kernel, dim3((T * 64 + 255) / 256), blk, 0, st, r->coordinates, rope, T, r->rope_theta,
-                     (int)r->rope_axes[0], (int)r->rope_axes[1]);
-  PROM_STEP(hipGetLastError());
+    PROM_STEP(hipGetLastError());
+    hipLaunchKernelGGL(rope_table_kernel, dim3((T * 64 + 255) / 256), blk, 0, st, r->coordinates, rope, T,
+                       r->rope_theta, (int)r->rope_axes[0], (int)r->rope_axes[1]);
+    PROM_STEP(hipGetLastError());
+  }
   hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, rows::row_groups<4>(T), dim3(256), 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
   PROM_STEP(hipGetLastError());
   // QKV in bf16 (one rounding before the per-head norms), the norms and RoPE
