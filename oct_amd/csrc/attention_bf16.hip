@@ -41,6 +41,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -281,11 +282,21 @@ struct Bf16Pairs {
   bf16x2 v[4];
 };
 
+// kQNormRope: the DiT block's per-head RMSNorm (weights qn, eps) and RoPE
+// (table rope [T][64] of (cos, sin)) are applied to the raw Q rows here, as
+// k_norm_rope_kernel (dit_block.hip) applies them to K, with the same
+// arithmetic: per 8-channel chunk the sum of squares of its four (even, odd)
+// pairs, the 16 chunk sums of the head added pairwise over chunk index bits
+// 3, 2, 1, 0 (bits 3..1 are this lane's own chunks s ^ 4, s ^ 2, s ^ 1; bit 0
+// is the other lane half), then the scaled, rotated pairs rounded to bf16.
+template <bool kQNormRope>
 __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint16_t* __restrict__ Q,
                                                                      const uint16_t* __restrict__ K,
                                                                      const uint16_t* __restrict__ V,
                                                                      uint16_t* __restrict__ O, int T, int ldq,
-                                                                     int ldk, int ldv, int ldo, float scale_log2) {
+                                                                     int ldk, int ldv, int ldo, float scale_log2,
+                                                                     const float2* __restrict__ rope,
+                                                                     const float* __restrict__ qn, float eps) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -354,6 +365,19 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
       u32x4 v = {0u, 0u, 0u, 0u};
       if (qi < T) v = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * hi);
       qf[s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  // Q's RoPE entries (chunk c = 2 s + hi holds channels 8 c .. 8 c + 7 of the
+  // head: 32 contiguous bytes of the 256-byte-aligned table) are loaded here
+  // and used after tile 0's transfers are issued.
+  floatx4 qtab[kQNormRope ? 8 : 1][2];
+  if constexpr (kQNormRope) {
+    const floatx4* trow = reinterpret_cast<const floatx4*>(rope + (size_t)min(qi, T - 1) * 64);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int c = 2 * s + hi;
+      qtab[s][0] = trow[2 * c];
+      qtab[s][1] = trow[2 * c + 1];
     }
   }
 
@@ -467,6 +491,52 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
     }
   };
   issue_tile(0);
+  if constexpr (kQNormRope) {
+    float cs[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
+      float ss = 0.0f;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float e = __uint_as_float(w[p] << 16), o = __uint_as_float(w[p] & 0xffff0000u);
+        ss += e * e + o * o;
+      }
+      cs[s] = ss;
+    }
+    float x[8], y[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) x[s] = cs[s] + cs[s ^ 4];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) y[s] = x[s] + x[s ^ 2];
+    const float z = y[0] + y[1];
+    const float inv = 1.0f / sqrtf(sum_halves(z) / 128.0f + eps);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
+      // weights of chunks 2 s and 2 s + 1: the same addresses in every lane,
+      // held in scalar registers (scalar loads), then the lane half's chunk
+      float wv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float we = qn[16 * s + i], wo = qn[16 * s + 8 + i];
+        asm("" : "+s"(we), "+s"(wo));
+        wv[i] = hi ? wo : we;
+      }
+      const float tv[8] = {qtab[s][0].x, qtab[s][0].y, qtab[s][0].z, qtab[s][0].w,
+                           qtab[s][1].x, qtab[s][1].y, qtab[s][1].z, qtab[s][1].w};
+      u32x4 r;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float e = __uint_as_float(w[p] << 16), o = __uint_as_float(w[p] & 0xffff0000u);
+        const float cs_p = tv[2 * p], sn_p = tv[2 * p + 1];
+        const float ne = e * inv * wv[2 * p], no = o * inv * wv[2 * p + 1];
+        r[p] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(ne * cs_p - no * sn_p)) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(ne * sn_p + no * cs_p)) << 16);
+      }
+      qf[s] = __builtin_bit_cast(bf16x8, r);
+    }
+  }
   const std::integral_constant<int, 0> st0{};
   const std::integral_constant<int, 1> st1{};
   int t = 0;
@@ -520,13 +590,31 @@ hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k,
   if (variant != 0) return hipErrorInvalidValue;
   static bool lds_raised = false;
   if (!lds_raised) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(flash_attn_bf16_dma_kernel),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(flash_attn_bf16_dma_kernel<false>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, kDmaLds);
     if (e != hipSuccess) return e;
     lds_raised = true;
   }
-  hipLaunchKernelGGL(flash_attn_bf16_dma_kernel, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk, ldv, ldo,
-                     scale_log2);
+  hipLaunchKernelGGL(flash_attn_bf16_dma_kernel<false>, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk,
+                     ldv, ldo, scale_log2, nullptr, nullptr, 0.0f);
+  return hipGetLastError();
+}
+
+// The DiT block's attention: the DMA-fed kernel with the per-head RMSNorm
+// (qn, eps) and RoPE (rope, [T][64]) applied to the raw Q rows on load.
+hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v,
+                                            int ldv, uint16_t* o, int ldo, int T, int heads, float scale,
+                                            const float2* rope, const float* qn, float eps, hipStream_t stream) {
+  const dim3 grid((unsigned)((T + 4 * kQW - 1) / (4 * kQW) * heads));
+  static bool lds_raised = false;
+  if (!lds_raised) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(flash_attn_bf16_dma_kernel<true>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kDmaLds);
+    if (e != hipSuccess) return e;
+    lds_raised = true;
+  }
+  hipLaunchKernelGGL(flash_attn_bf16_dma_kernel<true>, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk, ldv,
+                     ldo, scale * 1.4426950408889634f, rope, qn, eps);
   return hipGetLastError();
 }
 

@@ -13,11 +13,12 @@
 // per-row work between them is fused into four one-pass row kernels (one wave
 // per row, the row held in registers, 128-bit loads):
 //   adaln          m = c @ Wada + b -> modulation vectors       (16-byte weight loads, k split 16 ways)
-//   rope_table     (cos, sin) per token and pair, binary64 angles
+//   rope_table     (cos, sin) per token and pair, binary64 angles (one launch with adaln)
 //   norm_mod       a = RMSNorm(x; n1) * scaleA                   -> bf16
 //   (QKV GEMM      -> bf16 [T, 3D])
-//   qk_norm_rope   per token and head, in place: RMSNorm(q), RMSNorm(k), RoPE
-//                  (the attention reads Q, K, V from the [T, 3D] rows)
+//   k_norm_rope    per token and head, in place: RMSNorm(k), RoPE; the
+//                  attention applies RMSNorm(q) and RoPE to Q as it loads it
+//                  and reads Q, K, V from the [T, 3D] rows
 //   (out-projection GEMM -> bf16 proj)
 //   resid_norm_mod r = x + gateA * RMSNorm(proj; n2)             -> fp32
 //                  f = RMSNorm(r; n3) * scaleM                   -> bf16
@@ -149,19 +150,20 @@ __global__ __launch_bounds__(256) void adaln_rope_kernel(const float* __restrict
     rope_table_entry((blk - n_adaln) * 256 + (int)threadIdx.x, coords, tab, T, theta, ax0, ax1);
 }
 
-// Per (token, head): q and k RMSNorm over 128 channels, then RoPE on the
+// Per (token, head): k RMSNorm over 128 channels, then RoPE on the
 // interleaved pairs (2p, 2p+1) with the token's (cos, sin) table entry for
 // pair p (zimage/canonical_contract.go:66-87, zimage_main_transformer_canonical.py:124-140).
-// In place on the QKV projection, bf16 [T, 3D] (Q | K | V per token); V is left
-// as it is.  One wave per token: lane l takes the 16-byte chunks
-// c = l + 64 j of the token's Q row and of its K row (c < 16 H): head c / 16,
-// channels 8 (c % 16) .. +7, i.e. pairs 4 (l % 16) .. +3 of the head, so the
-// lane's (cos, sin) entries and norm weights are the same for every chunk and
-// are loaded once.  A head's sum of squares is reduced over its 16-lane group.
-// Up to 8 chunks of Q and 8 of K (32 heads) are loaded before any arithmetic.
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict__ qkv, const float2* __restrict__ tab,
-                                                           const float* __restrict__ qn, const float* __restrict__ kn,
-                                                           int T, int H, float eps) {
+// In place on the K part of the QKV projection, bf16 [T, 3D] (Q | K | V per
+// token); the attention kernel applies the same norm (q_norm) and RoPE to Q as
+// it loads it (launch_flash_attn_bf16_qnorm_rope), and V is left as it is.
+// One wave per token: lane l takes the 16-byte chunks c = l + 64 j of the
+// token's K row (c < 16 H): head c / 16, channels 8 (c % 16) .. +7, i.e. pairs
+// 4 (l % 16) .. +3 of the head, so the lane's (cos, sin) entries and norm
+// weights are the same for every chunk and are loaded once.  A head's sum of
+// squares is reduced over its 16-lane group.  Up to 8 chunks (32 heads) are
+// loaded before any arithmetic.
+__global__ __launch_bounds__(256) void k_norm_rope_kernel(uint16_t* __restrict__ qkv, const float2* __restrict__ tab,
+                                                          const float* __restrict__ kn, int T, int H, float eps) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   constexpr int kBatch = 8;
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
@@ -170,8 +172,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict_
   const int D = H * 128;
   const int nc = H * 16;
   const int sub = lane & 15;
-  uint16_t* row = qkv + (size_t)t * 3 * D;
-  float cs[4], sn[4], wq[8], wk[8];
+  uint16_t* row = qkv + (size_t)t * 3 * D + D;
+  float cs[4], sn[4], wk[8];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const float2 e = tab[(size_t)t * 64 + 4 * sub + p];
@@ -179,10 +181,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict_
     sn[p] = e.y;
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    wq[i] = qn[8 * sub + i];
-    wk[i] = kn[8 * sub + i];
-  }
+  for (int i = 0; i < 8; ++i) wk[i] = kn[8 * sub + i];
   auto norm_rope = [&](u32x4 v, const float* w) __attribute__((always_inline)) {
     float e[4], o[4];
     float ss = 0.0f;
@@ -204,27 +203,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict_
     return r;
   };
   for (int c0 = 0; c0 < nc; c0 += 64 * kBatch) {
-    u32x4 qv[kBatch], kv[kBatch];
+    u32x4 kv[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int c = c0 + lane + 64 * j;
-      qv[j] = kv[j] = u32x4{0u, 0u, 0u, 0u};
-      if (c < nc) {
-        qv[j] = *reinterpret_cast<const u32x4*>(row + 8 * c);
-        kv[j] = *reinterpret_cast<const u32x4*>(row + D + 8 * c);
-      }
+      kv[j] = u32x4{0u, 0u, 0u, 0u};
+      if (c < nc) kv[j] = *reinterpret_cast<const u32x4*>(row + 8 * c);
     }
     // c < nc holds for whole 16-lane groups (nc is a multiple of 16), so
     // every group's reduction sees only its own head
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int c = c0 + lane + 64 * j;
-      const u32x4 qr = norm_rope(qv[j], wq);
       const u32x4 kr = norm_rope(kv[j], wk);
-      if (c < nc) {
-        *reinterpret_cast<u32x4*>(row + 8 * c) = qr;
-        *reinterpret_cast<u32x4*>(row + D + 8 * c) = kr;
-      }
+      if (c < nc) *reinterpret_cast<u32x4*>(row + 8 * c) = kr;
     }
   }
 }
@@ -330,13 +322,13 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   }
   hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, rows::row_groups<4>(T), dim3(256), 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
   PROM_STEP(hipGetLastError());
-  // QKV in bf16 (one rounding before the per-head norms), the norms and RoPE
-  // in place, and the attention reading Q, K, V from the same [T, 3D] rows.
+  // QKV in bf16 (one rounding before the per-head norms), K's norm and RoPE in
+  // place, Q's inside the attention, which reads Q, K, V from the [T, 3D] rows.
   PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, nullptr, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((T + 3) / 4), blk, 0, st, qkv, rope, r->q_norm, r->k_norm, T, H, eps);
+  hipLaunchKernelGGL(k_norm_rope_kernel, dim3((T + 3) / 4), blk, 0, st, qkv, rope, r->k_norm, T, H, eps);
   PROM_STEP(hipGetLastError());
-  PROM_STEP(launch_flash_attn_bf16(qkv, 3 * D, qkv + D, 3 * D, qkv + 2 * D, 3 * D, O, D, T, H, 1.0f / sqrtf(128.0f),
-                                   st, 0));
+  PROM_STEP(launch_flash_attn_bf16_qnorm_rope(qkv, 3 * D, qkv + D, 3 * D, qkv + 2 * D, 3 * D, O, D, T, H,
+                                              1.0f / sqrtf(128.0f), rope, r->q_norm, eps, st));
   // The out- and down-projections go to bf16: both are RMS-normalised before
   // they join the fp32 residual stream.
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, nullptr, projb, D, T, D, D, nullptr, 0, st, nullptr));

@@ -172,11 +172,18 @@ hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w
                                    uint32_t f, uint32_t k, hipStream_t stream, void* part_ws, size_t part_bytes,
                                    uint32_t* launches = nullptr);
 // bf16 flash attention, head dim 128, full (non-causal): Q/K/V/O [T, ld*] with
-// head h at column 128 h.  variant 0: software-pipelined kernel (80 KiB of
-// dynamic LDS); 1: the serial kernel.  hipErrorInvalidValue for other variants.
+// head h at column 128 h.  variant 0: K/V tiles moved HBM -> LDS by DMA (64 KiB
+// of dynamic LDS); 1: tiles staged through registers.  hipErrorInvalidValue for
+// other variants.
 hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v, int ldv,
                                   uint16_t* o, int ldo, int T, int heads, float scale, hipStream_t stream,
                                   int variant);
+// Variant 0 with the DiT block's per-head RMSNorm (weights qn [128], eps) and
+// RoPE (rope [T][64] (cos, sin) per pair) applied to the raw Q rows as they
+// are loaded, with k_norm_rope_kernel's arithmetic (dit_block.hip).
+hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v,
+                                            int ldv, uint16_t* o, int ldo, int T, int heads, float scale,
+                                            const float2* rope, const float* qn, float eps, hipStream_t stream);
 // Binary64 FFT of n = 2^k <= 2^20 points (interleaved complex); temp holds n
 // points and is used when n > 4096.  roots comes from fft64_roots(n).
 hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,
