@@ -164,6 +164,47 @@ def test_dit_block_swiglu_k_split(gpu_runtime):
     assert res.kernel_launches == res2.kernel_launches + 1
 
 
+def test_dit_block_unaligned_vectors(gpu_runtime):
+    """Device entry with an adaLN weight 2 bytes past a 16-byte boundary (the
+    separate adaLN and RoPE-table kernels instead of their fused launch,
+    dit_block.hip) and q_norm 4 bytes past one (read by the attention kernel's
+    scalar loads), against the binary64 oracle."""
+    rt = gpu_runtime
+    grid, text, heads, F, C = (8, 16), 40, 4, 1024, 64
+    T = grid[0] * grid[1] + text
+    D = heads * 128
+    x, cond, w = blocks.make_dit_block(31, T, D, F, C)
+    coords = blocks.joint_coordinates(grid[0], grid[1], text)
+    f32 = lambda a: np.ascontiguousarray(a, dtype=np.float32)
+    u16 = lambda a: np.ascontiguousarray(a, dtype=np.uint16)
+    arrs = {"input": f32(x), "coordinates": f32(coords), "condition": f32(cond), "b_adaln": f32(w.b_adaln),
+            "attn_norm1": f32(w.attn_norm1), "attn_norm2": f32(w.attn_norm2), "ffn_norm1": f32(w.ffn_norm1),
+            "ffn_norm2": f32(w.ffn_norm2), "k_norm": f32(w.k_norm), "w_qkv": u16(w.w_qkv), "w_out": u16(w.w_out),
+            "w_13": u16(w.w_13), "w_2": u16(w.w_2)}
+    ptrs = {k: rt.upload_new(v) for k, v in arrs.items()}
+    held = list(ptrs.values())
+    base_w = rt.upload_new(np.concatenate([np.zeros(1, np.uint16), u16(w.w_adaln).ravel()]))
+    base_q = rt.upload_new(np.concatenate([np.zeros(1, np.float32), f32(w.q_norm)]))
+    held += [base_w, base_q]
+    ptrs["w_adaln"], ptrs["q_norm"] = base_w + 2, base_q + 4
+    ptrs["output"] = rt.alloc(T * D * 4)
+    held.append(ptrs["output"])
+    try:
+        req = rt.dit_block_request(T, D, heads, F, C, ptrs)
+        res = rt.dit_block_bf16_device(req)
+        rt.synchronize()
+        out = rt.download(np.empty((T, D), np.float32), ptrs["output"])
+    finally:
+        for ptr in held:
+            rt.free(ptr)
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads)
+    err = oracle.normwise_rel_err(out, ref)
+    print(f"unaligned adaLN / q_norm: normwise rel err {err:.3e}, {res.kernel_launches} launches", flush=True)
+    assert err <= BF16_BLOCK
+    rc, res2, _ = rt.dit_block_bf16(x, coords, cond, w, heads=heads)  # aligned: adaLN and RoPE table fused
+    assert rc == p.PROM_OK and res.kernel_launches == res2.kernel_launches + 1
+
+
 @pytest.mark.parametrize("q_heads,head_dim", [(8, 256), (3, 4)])
 def test_decoder_layer_attention_closed_form(gpu_runtime, q_heads, head_dim):
     """T = 2 layer with a closed-form output (head h weights token 1 by
