@@ -492,7 +492,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
   };
   issue_tile(0);
   if constexpr (kQNormRope) {
-    float cs[8];
+    float chunk_ss[8];  // sum of squares of chunk 2 s + hi
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
@@ -502,11 +502,11 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
         const float e = __uint_as_float(w[p] << 16), o = __uint_as_float(w[p] & 0xffff0000u);
         ss += e * e + o * o;
       }
-      cs[s] = ss;
+      chunk_ss[s] = ss;
     }
     float x[8], y[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) x[s] = cs[s] + cs[s ^ 4];
+    for (int s = 0; s < 8; ++s) x[s] = chunk_ss[s] + chunk_ss[s ^ 4];
 #pragma unroll
     for (int s = 0; s < 8; ++s) y[s] = x[s] + x[s ^ 2];
     const float z = y[0] + y[1];
