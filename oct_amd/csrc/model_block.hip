@@ -1444,6 +1444,8 @@ bool alloc_prefetch(ModelBlock* b, PrefetchWindow* pf) {
 // from FP16 into its slot of the window on the window's stream.  The caller
 // holds pf->mu and not the device context's lock.  Returns 0 or a detail.
 int32_t prefetch_transfer(PrefetchWindow* pf, const Target& t, const PrometheusModelBlockWeightUpload* uploads) {
+  // The calling thread may never have used the device: make the library's
+  // device current for it (the library runs on that one device only).
   if (hipSetDevice(ctx().device) != hipSuccess) return PROM_MODEL_BLOCK_DETAIL_COMMAND_RECORD_FAILED;
   for (uint32_t i = 0; i < t.count; ++i) {
     const int k = (int)(i & 1u);
