@@ -121,9 +121,12 @@ __device__ __forceinline__ void stage_vec(floatx4* dst, const float* src, int d4
 // The norm kernels below run one row per wave, kRows rows per workgroup:
 // the D-vectors (norm weights, adaLN scale and gate, up to 4 x 16 KiB) are
 // staged in LDS once per workgroup.  resid_norm_mod, with four vectors, takes
-// 8 rows (with 4 its vector reads from L2 matched the row data itself,
-// 57 -> 53 us at C5); the two-vector kernels keep 4, which lets more
-// workgroups share a CU (final_resid: 36 us with 4 rows, 43 with 8).
+// 8 rows by default (with 4 its vector reads from L2 matched the row data
+// itself, 57 -> 53 us at C5; the bf16 block launches 12); the two-vector
+// kernels keep 4, which lets more workgroups share a CU (final_resid: 36 us
+// with 4 rows, 43 with 8).  Both hold two rows' worth of registers and run
+// 3 waves per SIMD, so the row count sets how many rounds of workgroups a
+// launch takes.
 template <int kRows>
 inline dim3 row_groups(int T) { return dim3((unsigned)((T + kRows - 1) / kRows)); }
 

@@ -332,7 +332,10 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   // The out- and down-projections go to bf16: both are RMS-normalised before
   // they join the fp32 residual stream.
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, nullptr, projb, D, T, D, D, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL((rows::resid_norm_mod_kernel<uint16_t, 8, uint16_t>), rows::row_groups<8>(T), dim3(512), 0, st, r->input, projb, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
+  // 149 VGPRs allow 3 waves per SIMD, so one 12-wave workgroup per CU: 352
+  // workgroups at T = 4224 run in two rounds, where 8-row workgroups (one per
+  // CU as well) took three, the last with 16 (45 -> 37.5 us).
+  hipLaunchKernelGGL((rows::resid_norm_mod_kernel<uint16_t, 12, uint16_t>), rows::row_groups<12>(T), dim3(768), 0, st, r->input, projb, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
                      R, Fb, T, D, eps);
   PROM_STEP(hipGetLastError());
   // FFN up-projection with SwiGLU fused into the GEMM epilogue when the shape
