@@ -84,6 +84,13 @@ __device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, int i, floatx4 v, 
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, h), r, (uint32_t)(8 * i), 0, 0);
 }
 
+// An fp32 chunk as a streaming store (cache-policy operand 2: nt), for fp32
+// rows that no kernel reads soon: they leave no dirty L2 lines for the next
+// kernels to wait on.
+__device__ __forceinline__ void st4_stream(__amdgpu_buffer_rsrc_t r, int i, floatx4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (uint32_t)(16 * i), 0, 2);
+}
+
 // Issues the 16 chunk loads of a row (zero past D) into v.
 __device__ __forceinline__ void load_row(const float* __restrict__ src, int D, int lane, floatx4 (&v)[kRowChunks]) {
   const __amdgpu_buffer_rsrc_t r = row_rsrc(src, 4 * D);
@@ -161,7 +168,8 @@ __global__ __launch_bounds__(64 * kRows) void norm_mod_kernel(const float* __res
 }
 
 // r = x + gate * RMSNorm(proj; n2) (fp32 out), f = RMSNorm(r; n3) * scale (OutT); proj fp32 or bf16.
-template <typename OutT, int kRows = 8, typename ProjT = float>
+// kStream: r is written with streaming stores.
+template <typename OutT, int kRows = 8, typename ProjT = float, bool kStream = false>
 __global__ __launch_bounds__(64 * kRows) void resid_norm_mod_kernel(const float* __restrict__ x, const ProjT* __restrict__ proj,
                                                              const float* __restrict__ n2, const float* __restrict__ gate,
                                                              const float* __restrict__ n3, const float* __restrict__ scale,
@@ -195,7 +203,10 @@ __global__ __launch_bounds__(64 * kRows) void resid_norm_mod_kernel(const float*
     // chunks past D hold garbage vector values: keep them out of the sum
     if (i >= d4) r = floatx4{0.f, 0.f, 0.f, 0.f};
     v[c] = r;
-    st4(rr, i, r, r_out);
+    if constexpr (kStream)
+      st4_stream(rr, i, r);
+    else
+      st4(rr, i, r, r_out);
     ss2 += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
   }
   ss2 = wave_sum(ss2);
@@ -215,7 +226,8 @@ __global__ __launch_bounds__(64 * kRows) void resid_norm_mod_kernel(const float*
 }
 
 // out = r + gate * RMSNorm(w2; n4); w2 fp32 or bf16.
-template <int kRows = 4, typename W2T = float>
+// kStream: out is written with streaming stores.
+template <int kRows = 4, typename W2T = float, bool kStream = false>
 __global__ __launch_bounds__(64 * kRows) void final_resid_kernel(const float* __restrict__ r, const W2T* __restrict__ w2,
                                                           const float* __restrict__ n4, const float* __restrict__ gate,
                                                           float* __restrict__ out, int T, int D, float eps) {
@@ -241,7 +253,10 @@ __global__ __launch_bounds__(64 * kRows) void final_resid_kernel(const float* __
     o.y = rv[c].y + g.y * (v[c].y * inv * w.y);
     o.z = rv[c].z + g.z * (v[c].z * inv * w.z);
     o.w = rv[c].w + g.w * (v[c].w * inv * w.w);
-    st4(ro, i, o, out);
+    if constexpr (kStream)
+      st4_stream(ro, i, o);
+    else
+      st4(ro, i, o, out);
   }
 }
 

@@ -334,8 +334,11 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, nullptr, projb, D, T, D, D, nullptr, 0, st, nullptr));
   // 149 VGPRs allow 3 waves per SIMD, so one 12-wave workgroup per CU: 352
   // workgroups at T = 4224 run in two rounds, where 8-row workgroups (one per
-  // CU as well) took three, the last with 16 (45 -> 37.5 us).
-  hipLaunchKernelGGL((rows::resid_norm_mod_kernel<uint16_t, 12, uint16_t>), rows::row_groups<12>(T), dim3(768), 0, st, r->input, projb, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
+  // CU as well) took three, the last with 16 (45 -> 37.5 us).  R is next read
+  // after the FFN GEMMs and the block output by the next block's first
+  // kernel: both go out as streaming stores (W1|W3 -4 us, the first row
+  // kernel -1.3, this one -1.2).
+  hipLaunchKernelGGL((rows::resid_norm_mod_kernel<uint16_t, 12, uint16_t, true>), rows::row_groups<12>(T), dim3(768), 0, st, r->input, projb, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
                      R, Fb, T, D, eps);
   PROM_STEP(hipGetLastError());
   // FFN up-projection with SwiGLU fused into the GEMM epilogue when the shape
@@ -355,7 +358,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     n += k13 - 1;
   }
   PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, nullptr, w2b, D, T, D, F, nullptr, 0, st, nullptr));
-  hipLaunchKernelGGL((rows::final_resid_kernel<4, uint16_t>), rows::row_groups<4>(T), dim3(256), 0, st, R, w2b, r->ffn_norm2, gateM, r->output, T, D, eps);
+  hipLaunchKernelGGL((rows::final_resid_kernel<4, uint16_t, true>), rows::row_groups<4>(T), dim3(256), 0, st, R, w2b, r->ffn_norm2, gateM, r->output, T, D, eps);
   PROM_STEP(hipGetLastError());
 #undef PROM_STEP
   if (launches) *launches = n;
