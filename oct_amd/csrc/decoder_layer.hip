@@ -110,6 +110,17 @@ __global__ __launch_bounds__(256) void geglu_kernel(const float* __restrict__ G,
   }
 }
 
+// The same with 16-byte accesses (F % 4 == 0, G and A 16-byte aligned): row
+// t = blockIdx.y, four columns per thread, no per-element index division.
+__global__ __launch_bounds__(256) void geglu_vec_kernel(const float4* __restrict__ G, float4* __restrict__ A, int F4) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= F4) return;
+  const size_t t = blockIdx.y;
+  const float4 g = G[t * 2 * F4 + i];
+  const float4 u = G[t * 2 * F4 + F4 + i];
+  A[t * F4 + i] = make_float4(gelu_tanh(g.x) * u.x, gelu_tanh(g.y) * u.y, gelu_tanh(g.z) * u.z, gelu_tanh(g.w) * u.w);
+}
+
 struct LayerShape {
   int T, D, Hq, d, F, nqkv;
   int ldkt() const { return (T + 3) & ~3; }  // K^T row stride: 16-byte rows for the attention's tile transfers
@@ -219,7 +230,12 @@ hipError_t enqueue_layer(const PrometheusDecoderLayerF32Request* r, char* ws, co
   PROM_STEP(launch_sgemm_f32_ex(O, s.Hq * s.d, r->w_o, s.D, h, s.D, s.T, s.D, s.Hq * s.d, r->input, s.D, st, nullptr));
   PROM_STEP(launch_rmsnorm(h, r->ffn_norm_weight, n2, nullptr, s.T, s.D, s.D, r->rms_epsilon, st));
   PROM_STEP(launch_sgemm_f32_ex(n2, s.D, r->w_gate_up, 2 * s.F, G, 2 * s.F, s.T, 2 * s.F, s.D, nullptr, 0, st, nullptr));
-  {
+  if (s.F % 4 == 0 && ((reinterpret_cast<uintptr_t>(G) | reinterpret_cast<uintptr_t>(A)) & 15) == 0 && s.T <= 65535) {
+    const int f4 = s.F / 4;
+    hipLaunchKernelGGL(geglu_vec_kernel, dim3((unsigned)((f4 + 255) / 256), (unsigned)s.T), dim3(256), 0, st,
+                       reinterpret_cast<const float4*>(G), reinterpret_cast<float4*>(A), f4);
+    PROM_STEP(hipGetLastError());
+  } else {
     const size_t total = (size_t)s.T * s.F;
     const unsigned blocks = (unsigned)min((size_t)65536, (total + 255) / 256);
     hipLaunchKernelGGL(geglu_kernel, dim3(blocks), dim3(256), 0, st, G, A, s.T, s.F);

@@ -15,8 +15,10 @@ pytestmark = pytest.mark.gpu
 F32_BLOCK = 1e-3
 
 
+# F = 90 (not a multiple of 4) takes the scalar GeGLU kernel; the others the
+# 16-byte one.
 @pytest.mark.parametrize("T,D,Hq,d,F", [(5, 64, 2, 32, 96), (33, 256, 4, 64, 512), (130, 512, 8, 64, 1024),
-                                        (64, 384, 3, 128, 640)])
+                                        (64, 384, 3, 128, 640), (7, 64, 2, 32, 90)])
 def test_decoder_layer_small_shapes(gpu_runtime, T, D, Hq, d, F):
     x, w = blocks.make_decoder_layer(T + D, T, D, Hq, d, F)
     rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
