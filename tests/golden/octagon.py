@@ -1,7 +1,8 @@
-"""Reader for the Octagon text fixtures: ``Type { Field: [..]  Field: Sub { A: x B: y } }``.
+"""Reader for the Octagon text fixtures: ``Type { Field: [..]  Field: Sub { A: x B: y }  Field: x }``.
 
 Arrays become float64 numpy arrays; scalars inside nested records are keyed
-``Record.Field`` (e.g. ``QNormPair.Even``)."""
+``Record.Field`` (e.g. ``QNormPair.Even``); scalars of the outer record keep
+their own name (e.g. ``Expected``)."""
 import re
 from pathlib import Path
 
@@ -20,4 +21,10 @@ def load(name: str) -> dict:
     for m in re.finditer(r"(\w+):\s*\w+\s*\{([^{}]*)\}", text):
         for s in re.finditer(rf"(\w+):\s*({_NUM})", m.group(2)):
             fields[f"{m.group(1)}.{s.group(1)}"] = float(s.group(2))
+    # outer-record scalars: the body with arrays and nested records removed
+    body = text[text.index("{") + 1:text.rindex("}")]
+    body = re.sub(r"\[[^\]]*\]", "[]", body)
+    body = re.sub(r"\w+\s*\{[^{}]*\}", "{}", body)
+    for s in re.finditer(rf"(\w+):\s*({_NUM})(?![\w.])", body):
+        fields[s.group(1)] = float(s.group(2))
     return fields

@@ -220,3 +220,40 @@ def test_decoder_layer_attention_closed_form(gpu_runtime, q_heads, head_dim):
     want = closed_form_expected(x, qkv, q_heads, head_dim, 1e-6)
     assert oracle.normwise_rel_err(out, want) <= 1e-5
     assert np.max(np.abs(out - want)) <= 1e-5
+
+
+# ------------------------------------------------------------- closed forms
+# tests/closed_forms.py: identical tokens, period-4 channel classes and scaled
+# selection weights make every stage of the block known from four numbers;
+# tests/test_oracle_closed_forms.py shows that each named misreading of the
+# block's wiring misses these outputs by more than ten times the bar.
+@pytest.mark.parametrize("T,heads,F,C,grid,text", [(64, 2, 512, 32, (6, 8), 16), (130, 1, 200, 16, (8, 16), 2),
+                                                   (4224, 30, 10240, 256, (64, 64), 128)])
+def test_dit_block_closed_form(gpu_runtime, T, heads, F, C, grid, text):
+    from tests import closed_forms as cf
+
+    D = heads * 128
+    x, _, cond, w = cf.dit_case(T, heads, F, C)
+    coords = blocks.joint_coordinates(grid[0], grid[1], text)  # uneven scores
+    rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
+    assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)
+    want = cf.dit_expected(T, D)
+    err = oracle.normwise_rel_err(out, want)
+    row_err = np.linalg.norm(out - want, axis=1) / np.linalg.norm(want, axis=1)
+    print(f"DiT closed form T={T} D={D} F={F}: normwise {err:.3e}, worst row {row_err.max():.3e}", flush=True)
+    assert err <= BF16_BLOCK and row_err.max() <= BF16_BLOCK
+
+
+@pytest.mark.parametrize("T,D,Hq,d,F", [(64, 256, 2, 128, 512), (33, 384, 3, 128, 400),
+                                        (512, 2048, 8, 256, 16384)])
+def test_decoder_layer_closed_form(gpu_runtime, T, D, Hq, d, F):
+    from tests import closed_forms as cf
+
+    x, w = cf.decoder_case(T, D, Hq, d, F)
+    rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
+    assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)
+    want = cf.decoder_expected(T, D)
+    err = oracle.normwise_rel_err(out, want)
+    row_err = np.linalg.norm(out - want, axis=1) / np.linalg.norm(want, axis=1)
+    print(f"decoder closed form T={T} D={D} F={F}: normwise {err:.3e}, worst row {row_err.max():.3e}", flush=True)
+    assert err <= F32_BLOCK and row_err.max() <= F32_BLOCK

@@ -281,6 +281,39 @@ def test_context_refiner_chain(model, weights, inputs):
     assert model.destroy(bid) == p.PROM_OK
 
 
+def test_closed_form_refiners(model):
+    """The NoiseRefiner and ContextRefiner on the closed-form weights of
+    tests/closed_forms.py (scaled selections, period-4 channel classes,
+    identical tokens): every row of the output is known from the stage
+    recurrences there, and tests/test_oracle_closed_forms.py shows that each
+    named misreading of the block wiring misses it by more than 0.2."""
+    from tests import closed_forms as cf
+
+    x = np.tile(cf.tile(cf.X, W), (T_IMG, 1)).astype(np.float32)
+    t_bits = oracle.to_bf16(np.random.default_rng(9).standard_normal(256).astype(np.float32))
+    print("closed-form noise refiner: create and upload", flush=True)
+    rc, bid, ev = model.noise_refiner_create(cf.zimage_case(True))
+    assert rc == p.PROM_OK, ev.detail_code
+    rc, ev = model.noise_refiner_execute(bid, oracle.to_bf16(x), t_bits, parameter_set=1)
+    assert rc == p.PROM_OK, ev.detail_code
+    out = np.zeros(T_IMG * W, np.float32)
+    assert model.audit_final("noise", bid, 1, out)[0] == p.PROM_OK
+    err = rel_l2(out.reshape(T_IMG, W), cf.zimage_expected(T_IMG, True))
+    print(f"closed-form noise refiner rel L2 {err:.3e} over all {T_IMG} rows", flush=True)
+    assert err <= BAR
+    assert model.destroy(bid) == p.PROM_OK
+    rc, bid, ev = model.context_refiner_create(cf.zimage_case(False))
+    assert rc == p.PROM_OK, ev.detail_code
+    rc, ev = model.context_refiner0_execute(bid, x[:T_CTX])
+    assert rc == p.PROM_OK, ev.detail_code
+    out = np.zeros(T_CTX * W, np.float32)
+    assert model.audit_final("context", bid, 1, out)[0] == p.PROM_OK
+    err = rel_l2(out.reshape(T_CTX, W), cf.zimage_expected(T_CTX, False))
+    print(f"closed-form context refiner rel L2 {err:.3e}", flush=True)
+    assert err <= BAR
+    assert model.destroy(bid) == p.PROM_OK
+
+
 # ------------------------------------------------------------ session and MainTransformer
 def check_stage_timing(ev):
     """The 13 per-stage GPU timings of a MainTransformer execution tile its
