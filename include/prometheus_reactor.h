@@ -589,6 +589,12 @@ typedef struct PrometheusHipDeviceDiagnostics {
   uint32_t wavefront_size;
   int32_t hip_runtime_version;
   int32_t device_ordinal;
+  /* Device allocations made so far by the library's grow-only staging
+     buffers (operand staging, block workspaces, split-K partials, padded
+     copies), and the bytes they hold now.  Written only when struct_size
+     covers them (a caller's struct that ends at device_ordinal is accepted). */
+  uint64_t staging_allocations;
+  uint64_t staging_bytes;
 } PrometheusHipDeviceDiagnostics;
 PROM_REACTOR_API int prometheus_reactor_runtime_hip_device_diagnostics(void* handle,
                                                                         PrometheusHipDeviceDiagnostics* out_diag);
@@ -626,19 +632,23 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device(void* handle, const
                                                              uint32_t m, uint32_t n, uint32_t k, uint32_t* out_stage,
                                                              int* out_detail_code);
 /* No counterpart in the reference.  For callers that cannot allocate device
-   memory (code under HIP graph capture, tight serving loops, harnesses that
-   forbid hipMalloc): the product of ..._sgemm_device, with the same plan and
-   bit-identical results, that allocates nothing.  The split-K partial slices,
-   the only device memory the SGEMM needs beyond A, B and C, go to a static
-   device array of PROM_SGEMM_NOALLOC_SCRATCH_BYTES (64 MiB, one per GPU, held
-   until the process ends) instead of runtime-allocated staging.  A plan whose
-   partial buffer (PrometheusSgemmPlanInfo.partial_bytes) exceeds the array is
-   rejected: PROM_ERROR, stage TRANSFER_IN, PROM_DETAIL_SCRATCH_LIMIT.  Every
-   call on a GPU shares that GPU's array and leaves the last call's partials in
-   it (nothing in it needs to start at zero: each slice overwrites its part);
-   calls are ordered on the runtime's single stream, and work of two calls
-   that runs concurrently on one GPU (e.g. replayed from a captured graph on
-   another stream) races on the array. */
+   memory (tight serving loops, harnesses that forbid hipMalloc): the product
+   of ..._sgemm_device, with the same plan and bit-identical results, that
+   allocates nothing.  The scratch the plan needs beyond A, B and C (the
+   split-K partial slices, rounded up to 256 bytes, followed by the
+   zero-padded copies of A and B when the plan repacks unaligned operands)
+   goes to a static device array of PROM_SGEMM_NOALLOC_SCRATCH_BYTES (64 MiB,
+   one per GPU, held until the process ends) instead of runtime-allocated
+   staging.  A plan whose PrometheusSgemmPlanInfo.scratch_bytes (exactly that
+   sum) exceeds the array is rejected before anything is queued: PROM_ERROR,
+   stage TRANSFER_IN, PROM_DETAIL_SCRATCH_LIMIT, C untouched.  The work is
+   queued on the library's own stream, like every entry here, so a HIP graph
+   capture that a caller runs on a stream of its own does not record it.
+   Every call on a GPU shares that GPU's array and leaves the last call's
+   contents in it (nothing in it needs to start at zero: each slice and copy
+   overwrites its part); calls are ordered on that one stream, and two
+   processes, or two library copies, running this entry on one GPU race on
+   the array. */
 #define PROM_SGEMM_NOALLOC_SCRATCH_BYTES (64ull << 20)
 PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_device_noalloc(void* handle, const float* a, const float* b,
                                                                      float* c, uint32_t m, uint32_t n, uint32_t k,
@@ -698,6 +708,10 @@ typedef struct PrometheusSgemmPlanInfo {
   uint64_t partial_bytes;   /* split-K partial buffer the plan writes */
   double estimated_us;      /* the plan model's estimate */
   uint64_t repack_bytes;    /* the padded copies of A and B */
+  /* Scratch of ..._sgemm_device_noalloc: partial_bytes rounded up to 256,
+     plus repack_bytes.  Written only when struct_size covers it (a caller's
+     struct that ends at repack_bytes is still accepted). */
+  uint64_t scratch_bytes;
 } PrometheusSgemmPlanInfo;
 PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32_t n, uint32_t k,
                                                    PrometheusSgemmPlanInfo* out_plan);

@@ -93,6 +93,7 @@ struct DeviceContext {
   hipEvent_t op_begin = nullptr, op_end = nullptr;
   void* staging[kStagingSlots] = {};
   size_t staging_bytes[kStagingSlots] = {};
+  uint64_t staging_allocations = 0;  // hipMalloc calls made by staging(), for the diagnostics
   void* fft_roots = nullptr;  // twiddle table in staging slot 7 for length fft_roots_n
   uint32_t fft_roots_n = 0;
   hipDeviceProp_t props{};

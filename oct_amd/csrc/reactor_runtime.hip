@@ -7,6 +7,7 @@
 //                          UNKNOWN, reason VULKAN_UNAVAILABLE, as asserted by
 //                          Marionette/reactor_stub_tests.cpp:164-185)
 //   config struct_size gating  reactor_api.h:1751-1769
+#include <stddef.h>
 #include <string.h>
 #include <time.h>
 
@@ -95,6 +96,7 @@ void* staging(uint32_t slot, size_t bytes) {
   }
   c.staging[slot] = p;
   c.staging_bytes[slot] = rounded;
+  ++c.staging_allocations;
   return p;
 }
 
@@ -216,9 +218,11 @@ PROM_REACTOR_API int prometheus_reactor_runtime_hip_device_diagnostics(void* han
                                                                         PrometheusHipDeviceDiagnostics* out_diag) {
   Runtime* rt = lookup(handle);
   if (rt == nullptr) return PROM_INVALID_HANDLE;
-  if (out_diag == nullptr || out_diag->struct_size < sizeof(PrometheusHipDeviceDiagnostics)) return PROM_ERROR;
+  if (out_diag == nullptr || out_diag->struct_size < offsetof(PrometheusHipDeviceDiagnostics, staging_allocations))
+    return PROM_ERROR;
   const uint32_t size = out_diag->struct_size;
-  memset(out_diag, 0, sizeof(*out_diag));
+  const bool has_staging = size >= sizeof(PrometheusHipDeviceDiagnostics);
+  memset(out_diag, 0, has_staging ? sizeof(*out_diag) : offsetof(PrometheusHipDeviceDiagnostics, staging_allocations));
   out_diag->struct_size = size;
   if (!rt->available) return PROM_ERROR;
   const DeviceContext& c = ctx();
@@ -236,6 +240,11 @@ PROM_REACTOR_API int prometheus_reactor_runtime_hip_device_diagnostics(void* han
   (void)hipRuntimeGetVersion(&runtime_version);
   out_diag->hip_runtime_version = runtime_version;
   out_diag->device_ordinal = c.device;
+  if (has_staging) {
+    std::lock_guard<std::mutex> lock(ctx().mu);
+    out_diag->staging_allocations = c.staging_allocations;
+    for (uint32_t i = 0; i < kStagingSlots; ++i) out_diag->staging_bytes += c.staging_bytes[i];
+  }
   return PROM_OK;
 }
 

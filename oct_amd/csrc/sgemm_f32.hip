@@ -24,6 +24,7 @@
 //     compact block of A rows and B columns.
 #include <algorithm>
 #include <cmath>
+#include <cstddef>
 #include <cstring>
 
 #include "reactor_internal.h"
@@ -1160,6 +1161,12 @@ uint64_t schedule_partial_floats(const SgemmSchedule& s, uint32_t m, uint32_t n)
   return need;
 }
 
+// Floats of scratch the schedule needs in one array: the split-K partials
+// rounded up to 256 bytes, then the padded copies of A and B.
+uint64_t schedule_scratch_floats(const SgemmSchedule& s, uint32_t m, uint32_t n) {
+  return ((schedule_partial_floats(s, m, n) + 63) & ~63ull) + schedule_repack_floats(s, m);
+}
+
 }  // namespace
 
 hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
@@ -1209,7 +1216,7 @@ int launch_sgemm_f32_noalloc(const float* a, const float* b, float* c, uint32_t 
   // copies share the array: [partials | padded A | padded B].
   const SgemmSchedule s = schedule_sgemm(aligned16(a) && aligned16(b), (int)k, (int)n, m, n, k, false, ~0ull);
   const uint64_t part_floats = (schedule_partial_floats(s, m, n) + 63) & ~63ull;
-  if ((part_floats + schedule_repack_floats(s, m)) * sizeof(float) > PROM_SGEMM_NOALLOC_SCRATCH_BYTES)
+  if (schedule_scratch_floats(s, m, n) * sizeof(float) > PROM_SGEMM_NOALLOC_SCRATCH_BYTES)
     return PROM_DETAIL_SCRATCH_LIMIT;
   if (path_detail) *path_detail = s.gemv ? PROM_DETAIL_PATH_HIP_GEMV_F32 : PROM_DETAIL_PATH_HIP_MFMA_F32;
   return run_sgemm_schedule(s, a, (int)k, b, (int)n, c, (int)n, m, n, k, nullptr, 0, part, part + part_floats,
@@ -1253,9 +1260,13 @@ using namespace prom;
 
 extern "C" PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32_t n, uint32_t k,
                                                               PrometheusSgemmPlanInfo* out_plan) {
-  if (out_plan == nullptr || out_plan->struct_size < sizeof(PrometheusSgemmPlanInfo)) return PROM_ERROR;
+  // Callers built before scratch_bytes existed pass the shorter struct; the
+  // tail field is written only when the caller's struct holds it.
+  if (out_plan == nullptr || out_plan->struct_size < offsetof(PrometheusSgemmPlanInfo, scratch_bytes))
+    return PROM_ERROR;
   const uint32_t size = out_plan->struct_size;
-  memset(out_plan, 0, sizeof(*out_plan));
+  const bool has_scratch = size >= sizeof(PrometheusSgemmPlanInfo);
+  memset(out_plan, 0, has_scratch ? sizeof(*out_plan) : offsetof(PrometheusSgemmPlanInfo, scratch_bytes));
   out_plan->struct_size = size;
   if (m == 0u || n == 0u || k == 0u) {
     out_plan->detail_code = PROM_ERROR;
@@ -1293,5 +1304,6 @@ extern "C" PROM_REACTOR_API int prometheus_reactor_sgemm_plan(uint32_t m, uint32
   if (s.repack) out_plan->launches += 2u;
   out_plan->partial_bytes = schedule_partial_floats(s, m, n) * sizeof(float);
   out_plan->estimated_us = s.cost_us;
+  if (has_scratch) out_plan->scratch_bytes = schedule_scratch_floats(s, m, n) * sizeof(float);
   return PROM_OK;
 }

@@ -147,6 +147,7 @@ class PrometheusSgemmPlanInfo(Structure):
         ("partial_bytes", c_uint64),
         ("estimated_us", ctypes.c_double),
         ("repack_bytes", c_uint64),
+        ("scratch_bytes", c_uint64),
     ]
 
 
@@ -164,6 +165,8 @@ class PrometheusHipDeviceDiagnostics(Structure):
         ("wavefront_size", c_uint32),
         ("hip_runtime_version", ctypes.c_int32),
         ("device_ordinal", ctypes.c_int32),
+        ("staging_allocations", c_uint64),
+        ("staging_bytes", c_uint64),
     ]
 
 

@@ -125,3 +125,35 @@ def test_legacy_aliases_forward_to_the_runtime_entries():
     assert lib.prometheus_runtime_destroy(handle) == p.PROM_INVALID_HANDLE
     assert lib.prometheus_runtime_probe(handle, ctypes.byref(caps)) == p.PROM_INVALID_HANDLE
     assert lib.prometheus_runtime_create(None, None) == p.PROM_ERROR
+
+
+def test_scratch_bytes_is_what_the_noalloc_entry_needs():
+    """scratch_bytes = split-K partials rounded up to 256 bytes + the padded
+    copies of A and B: the exact rule of ..._sgemm_device_noalloc, which
+    refuses a plan whose scratch_bytes exceeds its 64 MiB array even when it
+    writes no partials (the repacking plans of large unaligned products)."""
+    for m, n, k in ((4097, 4097, 4097), (1056, 3840, 3841), (1280, 2048, 8192), (513, 1027, 131),
+                    (1056, 2048, 16384), (4096, 4096, 4096), (8192, 1, 4096)):
+        rc, i = _plan(m, n, k)
+        assert rc == p.PROM_OK
+        assert i.scratch_bytes == (i.partial_bytes + 255) // 256 * 256 + i.repack_bytes, (m, n, k)
+    rc, i = _plan(1056, 3840, 3841)
+    assert i.partial_bytes == 0 and i.repacked == 1 and i.scratch_bytes > p.SGEMM_NOALLOC_SCRATCH_BYTES
+    rc, i = _plan(8192, 1, 4096)  # the GEMV needs none
+    assert i.scratch_bytes == 0
+
+
+def test_plan_accepts_the_struct_without_scratch_bytes():
+    """A caller's struct that ends at repack_bytes is still served, and the
+    bytes past it are left alone."""
+    lib = p.shared_library()
+    short = p.PrometheusSgemmPlanInfo.scratch_bytes.offset
+    buf = (ctypes.c_ubyte * ctypes.sizeof(p.PrometheusSgemmPlanInfo))()
+    ctypes.memset(buf, 0xAB, len(buf))
+    info = p.PrometheusSgemmPlanInfo.from_buffer(buf)
+    info.struct_size = short
+    assert lib.prometheus_reactor_sgemm_plan(1056, 3840, 3841, ctypes.byref(info)) == p.PROM_OK
+    assert info.repacked == 1 and info.repack_bytes > 0
+    assert bytes(buf[short:]) == b"\xab" * (len(buf) - short)
+    info.struct_size = short - 1
+    assert lib.prometheus_reactor_sgemm_plan(4, 4, 4, ctypes.byref(info)) == p.PROM_ERROR
