@@ -76,6 +76,43 @@ def build_reactor(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer build of the same
+# sources (the GPU code is built as usual: each -fsanitize= applies to the host
+# pass only).  Load it with $OCT_PROMETHEUS_REACTOR and the clang ASan runtime
+# preloaded; oct_amd/sanitize.py does both and runs the host-logic tests.
+SAN_DIR = PKG_DIR / "_build_san"
+SAN_LIB_PATH = SAN_DIR / "libprometheus_reactor_san.so"
+REACTOR_ENV = "OCT_PROMETHEUS_REACTOR"  # the library override the loader honours
+SAN_FLAGS = ("-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined "
+             "-Xarch_host -fno-sanitize-recover=undefined -Xarch_host -fno-omit-frame-pointer -Xarch_host -g1").split()
+
+
+def build_reactor_sanitized(verbose: bool = False) -> Path:
+    """Compile and link the host-sanitized reactor into oct_amd/_build_san/."""
+    SAN_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC_DIR.glob("*.hip"))
+
+    def compile_one(src: Path) -> Path:
+        obj = SAN_DIR / (src.stem + ".o")
+        cmd = [_hipcc(), *HIPCC_FLAGS, *SAN_FLAGS, "-c", str(src), "-o", str(obj)]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc (sanitized) failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
+        return obj
+
+    workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        objs = list(pool.map(compile_one, sources))
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *SAN_FLAGS, "-o", str(SAN_LIB_PATH),
+           *map(str, objs)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link (sanitized) failed:\n{proc.stdout}\n{proc.stderr}")
+    if verbose:
+        print(f"built {SAN_LIB_PATH}")
+    return SAN_LIB_PATH
+
+
 def build_oracle(verbose: bool = False) -> Path:
     """Compile the CPU oracle (test infrastructure) with its Makefile."""
     proc = subprocess.run(["make", "-s", "-C", str(REPO_DIR / "oracle")], capture_output=True, text=True)
