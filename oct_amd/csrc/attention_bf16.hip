@@ -21,7 +21,10 @@
 //   * softmax runs in the log2 domain: max on raw scores, one FMA and one
 //     v_exp_f32 per score, running max/sum in fp32; O is rescaled only when
 //     some query's maximum grew (in the DMA-fed kernel only when it grew by
-//     more than 2^8, see kLazyLog2); masking only on the last, partial tile;
+//     more than 2^8, see kLazyLog2); masking only on the last, partial tile.
+//     The DiT block's queries and keys are per-head RMS-normalised, which
+//     bounds every score; when the bound allows (kDirectLog2) the kernel
+//     takes p = 2^s with no running maximum at all, one v_exp_f32 per score;
 //     P and O go to bf16 with the hardware round-to-nearest-even pair
 //     conversion (VALU work per tile is the bound of this kernel, not MFMA);
 //   * the output tile is staged through LDS for 128-bit coalesced stores;
@@ -57,6 +60,10 @@ constexpr float kNegBig = -1.0e30f;
 // probabilities then reach 2^8 before O/l normalises them, well inside bf16
 // and fp32 range, and the result is the same softmax.
 constexpr float kLazyLog2 = 8.0f;
+// Largest score magnitude (log2 units) for which the DiT kernel drops the
+// running maximum: with |s| <= 64, p = 2^s and the running sum of up to 2^31
+// keys stay far inside fp32 and bf16 range and never underflow to zero.
+constexpr float kDirectLog2 = 64.0f;
 
 // The grid is 1-D over (head, query block) pairs, head-major, renumbered by
 // xcd_pid: an XCD runs the query blocks of one or two heads at a time, so a
@@ -296,7 +303,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
                                                                      uint16_t* __restrict__ O, int T, int ldq,
                                                                      int ldk, int ldv, int ldo, float scale_log2,
                                                                      const float2* __restrict__ rope,
-                                                                     const float* __restrict__ qn, float eps) {
+                                                                     const float* __restrict__ qn,
+                                                                     const float* __restrict__ kn, float eps) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -381,6 +389,28 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
     }
   }
 
+  // Score bound of the per-head-normalised queries and keys: |q| <= sqrt(128)
+  // max|q_norm|, |k| <= sqrt(128) max|k_norm| (RMSNorm output has RMS <= 1,
+  // RoPE keeps the norm, bf16 rounding grows it by at most 2^-9), so every
+  // score in log2 units is at most 128 max|q_norm| max|k_norm| scale_log2 in
+  // magnitude.  When that is <= kDirectLog2 the softmax needs no running
+  // maximum: p = 2^s directly, and O / sum(p) is the same softmax
+  // (mathematically identical to subtracting the maximum; the probabilities
+  // are rounded to bf16 with the same relative error).  The scale goes into
+  // Q as it is normalised, so a score needs one v_exp_f32 and nothing else.
+  bool direct = false;
+  if constexpr (kQNormRope) {
+    float wq = fmaxf(fabsf(qn[lane]), fabsf(qn[lane + 64]));
+    float wk = fmaxf(fabsf(kn[lane]), fabsf(kn[lane + 64]));
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+      wq = fmaxf(wq, __shfl_xor(wq, sh));
+      wk = fmaxf(wk, __shfl_xor(wk, sh));
+    }
+    const float bound = 128.0f * wq * wk * scale_log2 * 1.01f;
+    direct = __builtin_amdgcn_readfirstlane((int)(bound <= kDirectLog2)) != 0;
+  }
+
   // operand addresses within a stage (bytes)
   const int k_lane = lq * 256;
   const int k_swz = lq & 15;
@@ -395,8 +425,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
 
   // One tile; kStage (0 or 1) is a compile-time constant so that the stage
   // offsets fold into the LDS instructions' offset fields.
-  auto tile = [&](int t, auto stage_c) {
+  auto tile = [&](int t, auto stage_c, auto direct_c) {
     constexpr int kStage = decltype(stage_c)::value;
+    constexpr bool kDirect = decltype(direct_c)::value;
     const int k0 = t * kKB;
     // tile t has landed (this wave's transfers; the barrier covers the
     // others'), and every wave is past tile t-1, whose stages take tile t+1
@@ -439,28 +470,37 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
         if (k0 + 32 + kr >= T) s1[r] = kNegBig;
       }
     }
-    float mt = fmaxf(s0[0], s1[0]);
+    if constexpr (kDirect) {
+      // scores are already in log2 units (the scale is inside Q) and bounded
 #pragma unroll
-    for (int r = 1; r < 16; ++r) asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mt) : "v"(mt), "v"(s0[r]), "v"(s1[r]));
-    mt = max_halves(mt);
-    // Lazy rescaling: the reference maximum m_run moves only when the tile's
-    // maximum exceeds it by more than kLazyLog2, so p <= 2^kLazyLog2 and O and
-    // the running sum are rescaled in a handful of tiles, not in most.
-    const float m_cand = fmaxf(m_run, mt * scale_log2);
-    const bool grow = m_cand > m_run + kLazyLog2;
-    if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_cand) : 1.0f;
-      l_part *= alpha;
+      for (int r = 0; r < 16; ++r) {
+        s0[r] = __builtin_amdgcn_exp2f(s0[r]);
+        s1[r] = __builtin_amdgcn_exp2f(s1[r]);
+      }
+    } else {
+      float mt = fmaxf(s0[0], s1[0]);
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int r = 1; r < 16; ++r) asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mt) : "v"(mt), "v"(s0[r]), "v"(s1[r]));
+      mt = max_halves(mt);
+      // Lazy rescaling: the reference maximum m_run moves only when the tile's
+      // maximum exceeds it by more than kLazyLog2, so p <= 2^kLazyLog2 and O and
+      // the running sum are rescaled in a handful of tiles, not in most.
+      const float m_cand = fmaxf(m_run, mt * scale_log2);
+      const bool grow = m_cand > m_run + kLazyLog2;
+      if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_cand) : 1.0f;
+        l_part *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-    }
-    if (grow) m_run = m_cand;
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, -m_run));
-      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, -m_run));
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      }
+      if (grow) m_run = m_cand;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, -m_run));
+        s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, -m_run));
+      }
     }
     // P^T operands (keys of chunk c in the accumulator's order, see
     // flash_attn_bf16_kernel), and their sum two at a time
@@ -510,7 +550,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
 #pragma unroll
     for (int s = 0; s < 8; ++s) y[s] = x[s] + x[s ^ 2];
     const float z = y[0] + y[1];
-    const float inv = 1.0f / sqrtf(sum_halves(z) / 128.0f + eps);
+    const float inv = 1.0f / sqrtf(sum_halves(z) / 128.0f + eps) * (direct ? scale_log2 : 1.0f);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
@@ -539,12 +579,25 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
   }
   const std::integral_constant<int, 0> st0{};
   const std::integral_constant<int, 1> st1{};
+  // (Peeling the last two tiles out of the loop, so that the steady tiles
+  // carry no branches around their transfers, measured 6 us slower in the C5
+  // block.)
+  const std::integral_constant<bool, false> with_max{};
   int t = 0;
-  for (; t + 1 < n_tiles; t += 2) {
-    tile(t, st0);
-    tile(t + 1, st1);
+  if (kQNormRope && direct) {
+    const std::integral_constant<bool, kQNormRope> no_max{};  // the direct path exists only with the norms
+    for (; t + 1 < n_tiles; t += 2) {
+      tile(t, st0, no_max);
+      tile(t + 1, st1, no_max);
+    }
+    if (t < n_tiles) tile(t, st0, no_max);
+  } else {
+    for (; t + 1 < n_tiles; t += 2) {
+      tile(t, st0, with_max);
+      tile(t + 1, st1, with_max);
+    }
+    if (t < n_tiles) tile(t, st0, with_max);
   }
-  if (t < n_tiles) tile(t, st0);
 
   // Normalise and stage the wave's [32 q][128 d] output through LDS (34 KiB
   // from offset 0); the barrier ends every wave's reads of the stages.
@@ -596,15 +649,17 @@ hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k,
     lds_raised = true;
   }
   hipLaunchKernelGGL(flash_attn_bf16_dma_kernel<false>, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk,
-                     ldv, ldo, scale_log2, nullptr, nullptr, 0.0f);
+                     ldv, ldo, scale_log2, nullptr, nullptr, nullptr, 0.0f);
   return hipGetLastError();
 }
 
 // The DiT block's attention: the DMA-fed kernel with the per-head RMSNorm
-// (qn, eps) and RoPE (rope, [T][64]) applied to the raw Q rows on load.
+// (qn, eps) and RoPE (rope, [T][64]) applied to the raw Q rows on load; K
+// holds rows normalised with kn, whose largest weight bounds the scores.
 hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v,
                                             int ldv, uint16_t* o, int ldo, int T, int heads, float scale,
-                                            const float2* rope, const float* qn, float eps, hipStream_t stream) {
+                                            const float2* rope, const float* qn, const float* kn, float eps,
+                                            hipStream_t stream) {
   const dim3 grid((unsigned)((T + 4 * kQW - 1) / (4 * kQW) * heads));
   static bool lds_raised = false;
   if (!lds_raised) {
@@ -614,7 +669,7 @@ hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const u
     lds_raised = true;
   }
   hipLaunchKernelGGL(flash_attn_bf16_dma_kernel<true>, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk, ldv,
-                     ldo, scale * 1.4426950408889634f, rope, qn, eps);
+                     ldo, scale * 1.4426950408889634f, rope, qn, kn, eps);
   return hipGetLastError();
 }
 

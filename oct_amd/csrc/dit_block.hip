@@ -328,7 +328,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   hipLaunchKernelGGL(k_norm_rope_kernel, dim3((T + 3) / 4), blk, 0, st, qkv, rope, r->k_norm, T, H, eps);
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_flash_attn_bf16_qnorm_rope(qkv, 3 * D, qkv + D, 3 * D, qkv + 2 * D, 3 * D, O, D, T, H,
-                                              1.0f / sqrtf(128.0f), rope, r->q_norm, eps, st));
+                                              1.0f / sqrtf(128.0f), rope, r->q_norm, r->k_norm, eps, st));
   // The out- and down-projections go to bf16: both are RMS-normalised before
   // they join the fp32 residual stream.
   PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, nullptr, projb, D, T, D, D, nullptr, 0, st, nullptr));

@@ -417,20 +417,25 @@ __device__ __forceinline__ uint32_t oslot1(uint32_t f) {
   return f ^ (((x << 2) | (x >> 2)) & 15u) ^ ((f >> 8) & 15u);
 }
 
-template <bool kColumns>
+// The transform size is a template parameter: every shift, mask and LDS slot
+// offset that depends only on it is a compile-time constant, which removed
+// about half of the kernels' integer instructions (at one wave per SIMD each
+// VALU instruction costs the wave its issue slot).
+template <bool kColumns, uint32_t log2n1, uint32_t log2n2>
 __device__ __forceinline__ void fft_wave_pass_body(const double2* __restrict__ in, double2* __restrict__ out,
-                                                   const double2* __restrict__ tables, uint32_t log2l,
-                                                   uint32_t tw_off, uint32_t lo_off, uint32_t hi_count,
-                                                   uint32_t log2n1, uint32_t log2n2) {
+                                                   const double2* __restrict__ tables, uint32_t tw_off,
+                                                   uint32_t lo_off) {
 #pragma clang fp contract(off)
   extern __shared__ double2 smem[];
+  constexpr uint32_t log2l = kColumns ? log2n1 : log2n2;
+  constexpr uint32_t hi_count = 1u << (log2n1 + log2n2 - 10u);
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  const uint32_t L = 1u << log2l;
-  const uint32_t lgr = 12u - log2l;  // log2 of sequences per workgroup
-  const uint32_t lgg = 12u - log2n2;  // log2 of the T tile height G
-  const uint32_t lgs = 10u - log2l;  // log2 of sequences per wave
+  constexpr uint32_t L = 1u << log2l;
+  constexpr uint32_t lgr = 12u - log2l;  // log2 of sequences per workgroup
+  constexpr uint32_t lgg = 12u - log2n2;  // log2 of the T tile height G
+  constexpr uint32_t lgs = 10u - log2l;  // log2 of sequences per wave
   double2* xb = smem + wave * kWaveElems;
   double2* tw = smem + kPassWaves * kWaveElems;
   double2* lo = tw + (L >> 1);
@@ -447,7 +452,7 @@ __device__ __forceinline__ void fft_wave_pass_body(const double2* __restrict__ i
   // the surplus threads load and store the last entry again (same value,
   // same slot).
   constexpr uint32_t kT = kPassWaves * 64;
-  const uint32_t tw_last = (L >> 1) - 1u, hi_last = hi_count - 1u;
+  constexpr uint32_t tw_last = (L >> 1) - 1u, hi_last = hi_count - 1u;
   double2 rt[2], rl[4], rh[4];
 #pragma unroll
   for (uint32_t u = 0; u < 2; ++u) rt[u] = tables[tw_off + min(tid + u * kT, tw_last)];
@@ -483,7 +488,7 @@ __device__ __forceinline__ void fft_wave_pass_body(const double2* __restrict__ i
 
   // phase-1 reads: lane holds positions 16 b .. 16 b + 15 of its sequence s1,
   // i.e. inputs rev(b) + m * L/16 (see fft_reg16_body)
-  const uint32_t lgq = log2l - 4u;
+  constexpr uint32_t lgq = log2l - 4u;
   const uint32_t s1 = lane >> lgq;
   const uint32_t b1 = lane & ((1u << lgq) - 1u);
   const uint32_t base = __brev(b1) >> (32u - lgq);
@@ -591,16 +596,18 @@ __device__ __forceinline__ void fft_wave_pass_body(const double2* __restrict__ i
 
 // Pass 1 (twiddled outputs) and pass 2.  At most two workgroups fit a CU's
 // LDS (104 or 72 KiB each), so the kernels may use 256 VGPRs.
+template <uint32_t kLog2N1, uint32_t kLog2N2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void fft_wave_pass1_kernel(
-    const double2* __restrict__ in, double2* __restrict__ out, const double2* __restrict__ tables, uint32_t log2l,
-    uint32_t tw_off, uint32_t lo_off, uint32_t hi_count, uint32_t log2n1, uint32_t log2n2) {
-  fft_wave_pass_body<true>(in, out, tables, log2l, tw_off, lo_off, hi_count, log2n1, log2n2);
+    const double2* __restrict__ in, double2* __restrict__ out, const double2* __restrict__ tables, uint32_t tw_off,
+    uint32_t lo_off) {
+  fft_wave_pass_body<true, kLog2N1, kLog2N2>(in, out, tables, tw_off, lo_off);
 }
 
+template <uint32_t kLog2N1, uint32_t kLog2N2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void fft_wave_pass2_kernel(
-    const double2* __restrict__ in, double2* __restrict__ out, const double2* __restrict__ tables, uint32_t log2l,
-    uint32_t tw_off, uint32_t lo_off, uint32_t hi_count, uint32_t log2n1, uint32_t log2n2) {
-  fft_wave_pass_body<false>(in, out, tables, log2l, tw_off, lo_off, hi_count, log2n1, log2n2);
+    const double2* __restrict__ in, double2* __restrict__ out, const double2* __restrict__ tables, uint32_t tw_off,
+    uint32_t lo_off) {
+  fft_wave_pass_body<false, kLog2N1, kLog2N2>(in, out, tables, tw_off, lo_off);
 }
 
 uint32_t ilog2(uint32_t v) {
@@ -660,32 +667,50 @@ hipError_t launch_pass(const double2* in, double2* out, const double2* roots, ui
 // One four-step pass of an n = 2^(log2n1 + log2n2) point transform
 // (n in (4096, 2^20], N1 = 2^log2n1 >= N2): n/4096 workgroups of four waves,
 // 1024 elements per wave; post selects pass 1 (columns of x to tiled T).
-hipError_t launch_wave_pass(const double2* in, double2* out, const double2* tables, uint32_t log2n1,
-                            uint32_t log2n2, uint32_t tw_off, uint32_t lo_off, int post, hipStream_t stream) {
-  const uint32_t log2l = post ? log2n1 : log2n2;
-  const uint32_t n = 1u << (log2n1 + log2n2);
-  if (log2n2 < 6 || log2n1 > 10 || log2n1 < log2n2) return hipErrorInvalidValue;
+template <uint32_t kLog2N1, uint32_t kLog2N2>
+hipError_t launch_wave_pass_t(const double2* in, double2* out, const double2* tables, uint32_t tw_off,
+                              uint32_t lo_off, int post, hipStream_t stream) {
+  constexpr uint32_t n = 1u << (kLog2N1 + kLog2N2);
+  constexpr uint32_t log2l_1 = kLog2N1, log2l_2 = kLog2N2;
   static bool lds_raised = false;
   const uint32_t max_elems = kPassWaves * kWaveElems + 512 + 1024 + 1024;
   if (!lds_raised) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_wave_pass1_kernel),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_wave_pass1_kernel<kLog2N1, kLog2N2>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)(max_elems * sizeof(double2)));
     if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_wave_pass2_kernel),
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(fft_wave_pass2_kernel<kLog2N1, kLog2N2>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)(max_elems * sizeof(double2)));
     if (e != hipSuccess) return e;
     lds_raised = true;
   }
-  const uint32_t hi_count = n / 1024;
-  const size_t lds = (kPassWaves * kWaveElems + (1u << log2l) / 2 + (post ? 1024 + hi_count : 0)) * sizeof(double2);
+  constexpr uint32_t hi_count = n / 1024;
+  const size_t lds =
+      (kPassWaves * kWaveElems + (1u << (post ? log2l_1 : log2l_2)) / 2 + (post ? 1024 + hi_count : 0)) *
+      sizeof(double2);
   const dim3 grid(n / (kPassWaves * kWaveElems)), block(64 * kPassWaves);
   if (post)
-    hipLaunchKernelGGL(fft_wave_pass1_kernel, grid, block, lds, stream, in, out, tables, log2l, tw_off, lo_off,
-                       hi_count, log2n1, log2n2);
+    hipLaunchKernelGGL((fft_wave_pass1_kernel<kLog2N1, kLog2N2>), grid, block, lds, stream, in, out, tables, tw_off,
+                       lo_off);
   else
-    hipLaunchKernelGGL(fft_wave_pass2_kernel, grid, block, lds, stream, in, out, tables, log2l, tw_off, lo_off,
-                       hi_count, log2n1, log2n2);
+    hipLaunchKernelGGL((fft_wave_pass2_kernel<kLog2N1, kLog2N2>), grid, block, lds, stream, in, out, tables, tw_off,
+                       lo_off);
   return hipGetLastError();
+}
+
+hipError_t launch_wave_pass(const double2* in, double2* out, const double2* tables, uint32_t log2n1,
+                            uint32_t log2n2, uint32_t tw_off, uint32_t lo_off, int post, hipStream_t stream) {
+  // the split launch_fft64 makes: log2n1 = ceil(log2 n / 2), log2n2 = floor(log2 n / 2)
+  switch (log2n1 * 16u + log2n2) {
+    case 7u * 16u + 6u: return launch_wave_pass_t<7, 6>(in, out, tables, tw_off, lo_off, post, stream);
+    case 7u * 16u + 7u: return launch_wave_pass_t<7, 7>(in, out, tables, tw_off, lo_off, post, stream);
+    case 8u * 16u + 7u: return launch_wave_pass_t<8, 7>(in, out, tables, tw_off, lo_off, post, stream);
+    case 8u * 16u + 8u: return launch_wave_pass_t<8, 8>(in, out, tables, tw_off, lo_off, post, stream);
+    case 9u * 16u + 8u: return launch_wave_pass_t<9, 8>(in, out, tables, tw_off, lo_off, post, stream);
+    case 9u * 16u + 9u: return launch_wave_pass_t<9, 9>(in, out, tables, tw_off, lo_off, post, stream);
+    case 10u * 16u + 9u: return launch_wave_pass_t<10, 9>(in, out, tables, tw_off, lo_off, post, stream);
+    case 10u * 16u + 10u: return launch_wave_pass_t<10, 10>(in, out, tables, tw_off, lo_off, post, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace

@@ -184,7 +184,8 @@ hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k,
 // are loaded, with k_norm_rope_kernel's arithmetic (dit_block.hip).
 hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v,
                                             int ldv, uint16_t* o, int ldo, int T, int heads, float scale,
-                                            const float2* rope, const float* qn, float eps, hipStream_t stream);
+                                            const float2* rope, const float* qn, const float* kn, float eps,
+                                            hipStream_t stream);
 // Binary64 FFT of n = 2^k <= 2^20 points (interleaved complex); temp holds n
 // points and is used when n > 4096.  roots comes from fft64_roots(n).
 hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,

@@ -118,6 +118,27 @@ def test_dit_block_attention_is_not_trivial(gpu_runtime):
     assert oracle.normwise_rel_err(out, ref) <= BF16_BLOCK
 
 
+@pytest.mark.parametrize("qk_gain", [1.0, 6.0])
+def test_dit_block_score_bound_paths(gpu_runtime, qk_gain):
+    """The attention drops the running maximum when the q/k norm weights
+    bound every score by 2^64 (gain 1: 128 * 1.04^2 / sqrt(128) * log2 e ~ 19)
+    and keeps it otherwise (gain 6 on both: ~600).  Strong projections give
+    the scores range; both paths against the oracle."""
+    T, heads, F, C = 200, 2, 256, 16
+    D = heads * 128
+    x, cond, w = blocks.make_dit_block(41, T, D, F, C)
+    w.w_qkv = oracle.to_bf16(oracle.from_bf16(w.w_qkv) * 6)
+    w.q_norm = (w.q_norm * qk_gain).astype(np.float32)
+    w.k_norm = (w.k_norm * qk_gain).astype(np.float32)
+    coords = blocks.joint_coordinates(12, 16, 8)
+    rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
+    assert rc == p.PROM_OK, (res.stage, res.detail_code)
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads)
+    err = oracle.normwise_rel_err(out, ref)
+    print(f"qk gain {qk_gain}: normwise rel err {err:.3e}", flush=True)
+    assert err <= BF16_BLOCK
+
+
 def test_dit_block_c5_full(gpu_runtime):
     """hidden 3840, 30 x 128 heads, FFN 10240, 4096 image + 128 text tokens."""
     grid, text, heads, F, C = (64, 64), 128, 30, 10240, 256
