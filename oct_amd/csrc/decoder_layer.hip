@@ -92,12 +92,6 @@ __global__ __launch_bounds__(256) void causal_softmax_kernel(float* __restrict__
   for (int j = lane; j < width; j += 64) row[j] = j < valid ? expf(row[j] - m) / denom : 0.0f;
 }
 
-__device__ __forceinline__ float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
-}
-
 // G [T, 2F] (gate | up) -> A [T, F]
 __global__ __launch_bounds__(256) void geglu_kernel(const float* __restrict__ G, float* __restrict__ A, int T, int F) {
   const size_t total = (size_t)T * F;
@@ -229,8 +223,22 @@ hipError_t enqueue_layer(const PrometheusDecoderLayerF32Request* r, char* ws, co
   }
   PROM_STEP(launch_sgemm_f32_ex(O, s.Hq * s.d, r->w_o, s.D, h, s.D, s.T, s.D, s.Hq * s.d, r->input, s.D, st, nullptr));
   PROM_STEP(launch_rmsnorm(h, r->ffn_norm_weight, n2, nullptr, s.T, s.D, s.D, r->rms_epsilon, st));
-  PROM_STEP(launch_sgemm_f32_ex(n2, s.D, r->w_gate_up, 2 * s.F, G, 2 * s.F, s.T, 2 * s.F, s.D, nullptr, 0, st, nullptr));
-  if (s.F % 4 == 0 && ((reinterpret_cast<uintptr_t>(G) | reinterpret_cast<uintptr_t>(A)) & 15) == 0 && s.T <= 65535) {
+  // gate|up with GeGLU in the GEMM's epilogue (the [T, 2F] intermediate is
+  // never written); shapes the fused kernel does not take run the GEMM and
+  // the elementwise GeGLU.
+  e = launch_sgemm_f32_geglu(n2, s.D, r->w_gate_up, A, s.F, s.T, s.F, s.D, st);
+  const bool fused = e == hipSuccess;
+  if (fused) {
+    ++n;
+  } else if (e != hipErrorNotSupported) {
+    return e;
+  } else {
+    PROM_STEP(launch_sgemm_f32_ex(n2, s.D, r->w_gate_up, 2 * s.F, G, 2 * s.F, s.T, 2 * s.F, s.D, nullptr, 0, st,
+                                  nullptr));
+  }
+  if (fused) {
+    // the GeGLU ran in the GEMM's epilogue
+  } else if (s.F % 4 == 0 && ((reinterpret_cast<uintptr_t>(G) | reinterpret_cast<uintptr_t>(A)) & 15) == 0 && s.T <= 65535) {
     const int f4 = s.F / 4;
     hipLaunchKernelGGL(geglu_vec_kernel, dim3((unsigned)((f4 + 255) / 256), (unsigned)s.T), dim3(256), 0, st,
                        reinterpret_cast<const float4*>(G), reinterpret_cast<float4*>(A), f4);

@@ -51,6 +51,14 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
+// Tanh-approximate GELU of the fp32 Gemma-style layer's GeGLU (the reference
+// has none; Gemma uses this form): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
+}
+
 constexpr uint64_t kRuntimeMagic = 0x4F43544D49333535ull;  // "OCTMI355"
 constexpr uint32_t kEventSlots = 64;
 // Staging slots: 0-3 operand staging, 4 block workspace, 5 block host staging,
@@ -141,6 +149,14 @@ hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m
 hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
                                uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
                                int* path_detail);
+// H[m, f] = gelu_tanh(A @ W[:, :f]) * (A @ W[:, f:]) for W = [gate | up]
+// ([k, 2f], row pitch 2f): one launch of the 128x128 direct-to-LDS kernel
+// whose tiles take 64 gate and the matching 64 up columns.  Returns
+// hipErrorNotSupported when the shape does not fit it (f % 64, k % 16,
+// 16-byte aligned operands and rows, byte offsets below 2^31); the caller
+// then runs the GEMM and the elementwise GeGLU.
+hipError_t launch_sgemm_f32_geglu(const float* a, int lda, const float* w, float* h, int ldh, uint32_t m, uint32_t f,
+                                  uint32_t k, hipStream_t stream);
 // C_z = A_z @ B_z for z < batch, A_z = a + z*sa etc. (elements); no residual, no split-K.
 // Allocation-free SGEMM: split-K partials in the library's static scratch
 // array.  init_sgemm_scratch(device) runs once per device at set-up (device

@@ -292,11 +292,18 @@ struct DlCfg {
   static constexpr int kStage = kABytes + kBK * kBPitch;
 };
 
-template <int kBN, int kWaves>
+// kGeGLU (128-wide tiles, eight waves only): B is [gate | up] with N gate
+// columns, the tile of column block tn takes gate columns 64 tn .. +63 and the
+// matching up columns, placed so that each wave's two 32-column MFMA blocks
+// are a gate block and its up block (tile columns 0-31 gate, 32-63 up, 64-95
+// gate + 32, 96-127 up + 32); the epilogue stores gelu_tanh(gate) * up, N
+// columns in all.
+template <int kBN, int kWaves, bool kGeGLU = false>
 __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, const float* __restrict__ B, float* C,
                                                   int M, int N, int K, int tiles_m, int tiles_n, int lda, int ldb,
                                                   int ldc, const float* R, int ldr, int k_len, long long sa,
                                                   long long sb, long long sc, char* S0, char* S1) {
+  static_assert(!kGeGLU || (kBN == 128 && kWaves == 8), "the GeGLU tile is the eight-wave 128x128 one");
   using D = DlCfg<kBN>;
   constexpr int kNI = D::kNI;
   constexpr int kRW = 256 / kWaves;                  // rows per wave (waves: kWaves/2 along M, 2 along N)
@@ -313,7 +320,7 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
   int tm, tn;
   map_tile(tiles_m, tiles_n, &tm, &tn);
   const int row0 = tm * 128;
-  const int col0 = tn * kBN;
+  const int col0 = kGeGLU ? tn * (kBN / 2) : tn * kBN;
   size_t a_extent = (size_t)M * lda;
   if (gridDim.y > 1) {
     const int kb = (int)blockIdx.y * k_len;
@@ -353,7 +360,12 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
       const int q = kBI * wave + i;  // rows 2q, 2q+1
       const int kr = 2 * q + (lane >> 5);
       const int c = (lane & 31) ^ (((kr >> 2) & 1) << 3);
-      b_off[i] = (uint32_t)((kr * ldb + col0 + 4 * c) * 4);
+      int gcol = col0 + 4 * c;
+      if constexpr (kGeGLU) {
+        const int seg = c >> 3;  // tile columns 32 seg .. +31
+        gcol = col0 + (seg >> 1) * 32 + 4 * (c & 7) + ((seg & 1) ? N : 0);
+      }
+      b_off[i] = (uint32_t)((kr * ldb + gcol) * 4);
     }
   }
   auto issue = [&](char* stage, int k0) {
@@ -441,6 +453,19 @@ __device__ __forceinline__ void sgemm_f32_dl_body(const float* __restrict__ A, c
   }
   if (kt < k_tiles) compute(S0);  // odd count: the last tile was issued into S0
 
+  if constexpr (kGeGLU) {
+    // acc[0][0]: gate columns col0 + 32 wn + lrow, acc[0][1]: the same up columns
+    const int col = col0 + wn * 32 + lrow;
+    if (col >= N) return;
+    const int rb = row0 + wm * kRW + 4 * h;
+    float* cp = C + (size_t)rb * ldc + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int dr = 8 * (r >> 2) + (r & 3);
+      if (rb + dr < M) cp[(size_t)dr * ldc] = gelu_tanh(acc[0][0][r]) * acc[0][1][r];
+    }
+    return;
+  }
   // Row offsets from the block's first row are wave-uniform (scalar), so only
   // one 64-bit address per block lives in vector registers.
   auto store_block = [&](const floatx16& acc, int mi, int ni) {
@@ -488,6 +513,18 @@ __global__ __launch_bounds__(512, 1) void sgemm_f32_dl128w8_kernel(const float* 
   __shared__ __attribute__((aligned(1024))) char S0[DlCfg<128>::kStage];
   __shared__ __attribute__((aligned(1024))) char S1[DlCfg<128>::kStage];
   sgemm_f32_dl_body<128, 8>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+}
+
+// The gate|up product of the Gemma-style layer with GeGLU in the epilogue
+// (sgemm_f32_dl_body's kGeGLU): C is the [M, N] GeGLU output.
+__global__ __launch_bounds__(512, 1) void sgemm_f32_dl128w8_geglu_kernel(const float* __restrict__ A,
+                                                                         const float* __restrict__ B, float* C,
+                                                                         int M, int N, int K, int tiles_m,
+                                                                         int tiles_n, int lda, int ldb, int ldc) {
+  __shared__ __attribute__((aligned(1024))) char S0[DlCfg<128>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S1[DlCfg<128>::kStage];
+  sgemm_f32_dl_body<128, 8, true>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, nullptr, 0, K, 0, 0, 0, S0,
+                                  S1);
 }
 
 // 64x64 tile for grids that would otherwise leave CUs idle or need a
@@ -1223,6 +1260,19 @@ int launch_sgemm_f32_noalloc(const float* a, const float* b, float* c, uint32_t 
                             stream) == hipSuccess
              ? PROM_OK
              : PROM_DETAIL_HIP_LAUNCH_FAILED;
+}
+
+hipError_t launch_sgemm_f32_geglu(const float* a, int lda, const float* w, float* h, int ldh, uint32_t m, uint32_t f,
+                                  uint32_t k, hipStream_t stream) {
+  if (m == 0 || f == 0 || k == 0) return hipErrorNotSupported;
+  const int ldb = (int)(2 * f);
+  const bool ok = f % 64 == 0 && buffer_path(aligned16(a) && aligned16(w), lda, 0, ldb, 0, m, 2 * f, k, (int)k, 4) &&
+                  ldh % 4 == 0 && aligned16(h);
+  if (!ok) return hipErrorNotSupported;
+  const int tiles_m = (int)((m + 127) / 128), tiles_n = (int)(f / 64);
+  hipLaunchKernelGGL(sgemm_f32_dl128w8_geglu_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, stream, a, w,
+                     h, (int)m, (int)f, (int)k, tiles_m, tiles_n, lda, ldb, ldh);
+  return hipGetLastError();
 }
 
 hipError_t launch_sgemm_f32_variant(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
