@@ -26,6 +26,7 @@
 #include <cmath>
 #include <cstddef>
 #include <cstring>
+#include <type_traits>
 
 #include "reactor_internal.h"
 
@@ -559,13 +560,23 @@ __device__ __forceinline__ int dl64_swz(int r) {
   return kBKs == 32 ? ((r >> 1) & 7) : (r & 15);
 }
 
-template <int kBKs>
+// kSt LDS stages in a ring: the transfers of tile t + kSt - 1 are issued while
+// tile t is computed.  With two stages a tile's transfers are waited for one
+// tile (about 0.8 us of MFMA work at one workgroup per CU) after they are
+// issued, less than the memory latency; the four-stage form, launched when a
+// grid has at most one workgroup per CU and K slices of 2048 or more, keeps
+// three tiles in flight.  The
+// transfers are inline assembly (the compiler then adds no waits of its own
+// before the LDS reads of other stages); explicit vmcnt waits and barriers
+// order each tile.
+template <int kBKs, int kSt>
 __device__ __forceinline__ void sgemm_f32_dl64_body(const float* __restrict__ A, const float* __restrict__ B,
                                                     float* C, int M, int N, int K, int tiles_m, int tiles_n, int lda,
                                                     int ldb, int ldc, const float* R, int ldr, int k_len,
-                                                    long long sa, long long sb, long long sc, char* S0, char* S1) {
+                                                    long long sa, long long sb, long long sc,
+                                                    char* const (&S)[kSt]) {
+  static_assert(kSt >= 2 && kSt <= 4, "two to four stages");
   using Cfg = Dl64Cfg<kBKs>;
-  typedef __attribute__((address_space(3))) void lds_void;
   if (gridDim.z > 1) {
     A += (size_t)blockIdx.z * sa;
     B += (size_t)blockIdx.z * sb;
@@ -591,10 +602,18 @@ __device__ __forceinline__ void sgemm_f32_dl64_body(const float* __restrict__ A,
   const int wm = (wave >> 1) & 1;
   const int wn = wave & 1;
 
-  const __amdgpu_buffer_rsrc_t rsa =
-      __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)(a_extent * 4), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsb =
-      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)((size_t)K * ldb * 4), 0x00020000);
+  typedef int int4v __attribute__((ext_vector_type(4)));
+  auto desc = [](const void* ptr, uint32_t bytes) {
+    const unsigned long long addr = (unsigned long long)ptr;
+    int4v d;
+    d.x = __builtin_amdgcn_readfirstlane((int)(addr & 0xffffffffu));
+    d.y = __builtin_amdgcn_readfirstlane((int)(addr >> 32));
+    d.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    d.w = 0x00020000;
+    return d;
+  };
+  const int4v rsa = desc(A, (uint32_t)(a_extent * 4));
+  const int4v rsb = desc(B, (uint32_t)((size_t)K * ldb * 4));
   // Transfer q (1 KB) of A covers rows 1024q/kRowBytes.., of B k-rows 4q..4q+3;
   // wave w issues q = kXfer*w + i.
   uint32_t a_off[Cfg::kXfer], b_off[Cfg::kXfer];
@@ -612,13 +631,35 @@ __device__ __forceinline__ void sgemm_f32_dl64_body(const float* __restrict__ A,
   auto issue = [&](char* stage, int k0) {
     const int sa_k = __builtin_amdgcn_readfirstlane(k0 * 4);
     const int sb_k = __builtin_amdgcn_readfirstlane(k0 * ldb * 4);
+    const uint32_t base = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)stage;
 #pragma unroll
     for (int i = 0; i < Cfg::kXfer; ++i) {
       const int q = Cfg::kXfer * wave + i;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(stage + q * 1024), 16, a_off[i], sa_k, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_void*)(stage + Cfg::kABytes + q * 1024), 16, b_off[i], sb_k,
-                                               0, 0);
+      const uint32_t la = __builtin_amdgcn_readfirstlane(base + q * 1024);
+      const uint32_t lb = __builtin_amdgcn_readfirstlane(base + Cfg::kABytes + q * 1024);
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(la), "v"(a_off[i]), "s"(rsa),
+                   "s"(sa_k)
+                   : "memory", "m0");
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lb), "v"(b_off[i]), "s"(rsb),
+                   "s"(sb_k)
+                   : "memory", "m0");
     }
+  };
+  // This wave's transfers of a tile: kPerTile; at most `in_flight` later
+  // tiles may stay outstanding.
+  constexpr int kPerTile = 2 * Cfg::kXfer;
+  auto wait_tiles = [&](int in_flight) {
+    if (in_flight >= 2)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPerTile) : "memory");
+    else if (in_flight == 1)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPerTile) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  auto barrier = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
 
   // Operand addresses (bytes within a stage).  Half kh covers k in
@@ -663,31 +704,42 @@ __device__ __forceinline__ void sgemm_f32_dl64_body(const float* __restrict__ A,
     }
     __syncthreads();
   };
-  issue(S0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  int kt = 0;
-  for (; kt + 1 < k_tiles; kt += 2) {
-    issue(S1, (kt + 1) * kBKs);
-    settle_last(S0, kt);
-    compute(S0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (kt + 2 < k_tiles) issue(S0, (kt + 2) * kBKs);
-    settle_last(S1, kt + 1);
-    compute(S1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  // Step t: tile t has landed for this wave (later tiles may stay in flight),
+  // the barrier makes it complete for all waves and frees tile t-1's stage,
+  // which takes tile t + kSt - 1; then tile t is computed.  u = t % kSt is a
+  // compile-time constant (the loop is unrolled by kSt).
+  auto step = [&](int t, auto u_c) {
+    constexpr int u = decltype(u_c)::value;
+    wait_tiles(min(kSt - 2, k_tiles - 1 - t));
+    barrier();
+    if (t + kSt - 1 < k_tiles) issue(S[(u + kSt - 1) % kSt], (t + kSt - 1) * kBKs);
+    settle_last(S[u], t);
+    compute(S[u]);
+  };
+#pragma unroll
+  for (int j = 0; j < kSt - 1; ++j)
+    if (j < k_tiles) issue(S[j], j * kBKs);
+  const std::integral_constant<int, 0> u0{};
+  const std::integral_constant<int, 1> u1{};
+  const std::integral_constant<int, (kSt > 2 ? 2 : 0)> u2{};
+  const std::integral_constant<int, (kSt > 3 ? 3 : 0)> u3{};
+  int t = 0;
+  for (; t + kSt <= k_tiles; t += kSt) {
+    step(t, u0);
+    step(t + 1, u1);
+    if constexpr (kSt > 2) step(t + 2, u2);
+    if constexpr (kSt > 3) step(t + 3, u3);
   }
-  if (kt < k_tiles) {
-    settle_last(S0, kt);
-    compute(S0);
-    __syncthreads();
-  }
+  if (t < k_tiles) step(t, u0);
+  if constexpr (kSt > 2)
+    if (t + 1 < k_tiles) step(t + 1, u1);
+  if constexpr (kSt > 3)
+    if (t + 2 < k_tiles) step(t + 2, u2);
+  __syncthreads();  // every wave is done with the stages
 
   // The kh = 1 waves pass their quadrant's accumulators to the kh = 0 waves
   // (stage 0 is free after the last barrier): 64 lanes x 16 floats per quadrant.
-  float* xchg = reinterpret_cast<float*>(S0) + (wave & 3) * 1024;
+  float* xchg = reinterpret_cast<float*>(S[0]) + (wave & 3) * 1024;
   if (kh == 1) {
 #pragma unroll
     for (int r = 0; r < 16; r += 4)
@@ -726,7 +778,8 @@ __global__ __launch_bounds__(512, 2) void sgemm_f32_dl64_kernel(const float* __r
                                                                 long long sa, long long sb, long long sc) {
   __shared__ __attribute__((aligned(1024))) char S0[Dl64Cfg<32>::kStage];
   __shared__ __attribute__((aligned(1024))) char S1[Dl64Cfg<32>::kStage];
-  sgemm_f32_dl64_body<32>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+  char* const st[2] = {S0, S1};
+  sgemm_f32_dl64_body<32, 2>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, st);
 }
 
 // 64-wide K tiles: twice the MFMA work between barriers and per LDS stage,
@@ -739,7 +792,25 @@ __global__ __launch_bounds__(512, 2) void sgemm_f32_dl64k64_kernel(const float* 
                                                                    long long sc) {
   __shared__ __attribute__((aligned(1024))) char S0[Dl64Cfg<64>::kStage];
   __shared__ __attribute__((aligned(1024))) char S1[Dl64Cfg<64>::kStage];
-  sgemm_f32_dl64_body<64>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, S0, S1);
+  char* const st[2] = {S0, S1};
+  sgemm_f32_dl64_body<64, 2>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, st);
+}
+
+// The four-stage forms, for grids of at most one workgroup per CU (the LDS
+// ring takes 64 and 128 KB).
+template <int kBKs>
+__global__ __launch_bounds__(512, 1) void sgemm_f32_dl64_ring_kernel(const float* __restrict__ A,
+                                                                     const float* __restrict__ B, float* C, int M,
+                                                                     int N, int K, int tiles_m, int tiles_n, int lda,
+                                                                     int ldb, int ldc, const float* R, int ldr,
+                                                                     int k_len, long long sa, long long sb,
+                                                                     long long sc) {
+  __shared__ __attribute__((aligned(1024))) char S0[Dl64Cfg<kBKs>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S1[Dl64Cfg<kBKs>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S2[Dl64Cfg<kBKs>::kStage];
+  __shared__ __attribute__((aligned(1024))) char S3[Dl64Cfg<kBKs>::kStage];
+  char* const st[4] = {S0, S1, S2, S3};
+  sgemm_f32_dl64_body<kBKs, 4>(A, B, C, M, N, K, tiles_m, tiles_n, lda, ldb, ldc, R, ldr, k_len, sa, sb, sc, st);
 }
 
 // dst [rows_d][ld_d] (16-byte rows) = src [rows_s][cols_s] (row stride ld_s,
@@ -1008,16 +1079,30 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
   const int tiles_n = (int)((n + bn - 1) / bn);
   const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)p.splits, batch);
   float* out = split ? partial : c;
+  // A grid that gives every CU at most one workgroup, with a long K loop:
+  // the 64x64 kernels take their four-stage form (C4's 512x2048x2048 output
+  // projection 38.8 -> 36.8 us; at K = 1024, C1, the deeper ring measured
+  // 0.4 us slower, so shorter slices keep two stages).
+  const int cus = ctx().props.multiProcessorCount > 0 ? ctx().props.multiProcessorCount : 256;
+  const bool one_per_cu = (long long)grid.x * grid.y * grid.z <= cus && p.k_len >= 2048;
   const int ldo = split ? (int)n : ldc;
   const float* res = split ? nullptr : residual;
   switch (tile) {
     case 5:
-      hipLaunchKernelGGL(sgemm_f32_dl64_kernel, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n, (int)k, tiles_m,
-                         tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      if (one_per_cu)
+        hipLaunchKernelGGL(sgemm_f32_dl64_ring_kernel<32>, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n,
+                           (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      else
+        hipLaunchKernelGGL(sgemm_f32_dl64_kernel, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+                           tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
       break;
     case 6:
-      hipLaunchKernelGGL(sgemm_f32_dl64k64_kernel, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n, (int)k,
-                         tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      if (one_per_cu)
+        hipLaunchKernelGGL(sgemm_f32_dl64_ring_kernel<64>, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n,
+                           (int)k, tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
+      else
+        hipLaunchKernelGGL(sgemm_f32_dl64k64_kernel, grid, dim3(512), 0, stream, a, b, out, (int)m, (int)n, (int)k,
+                           tiles_m, tiles_n, lda, ldb, ldo, res, ldr, p.k_len, sa, sb, sc);
       break;
     case 3:
       hipLaunchKernelGGL(sgemm_f32_dl256_kernel, grid, dim3(256), 0, stream, a, b, out, (int)m, (int)n, (int)k,
