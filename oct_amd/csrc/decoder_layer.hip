@@ -365,8 +365,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_decoder_layer_f32(void* handle,
   }
   res->stage = PROM_STAGE_TRANSFER_IN;
   for (int i = 0; i < 7; ++i) {
-    if (hipMemcpyAsync(dev + offs[i], srcs[i], sizes[i] * sizeof(float), hipMemcpyHostToDevice, cx.stream) !=
-        hipSuccess) {
+    if (upload_host(dev + offs[i], srcs[i], sizes[i] * sizeof(float), cx.stream) != hipSuccess) {
       res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
       return PROM_ERROR;
     }
@@ -390,7 +389,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_decoder_layer_f32(void* handle,
   }
   (void)hipEventRecord(cx.op_end, cx.stream);
   res->stage = PROM_STAGE_TRANSFER_OUT;
-  if (hipMemcpyAsync(r.output, dr.output, sizes[7] * sizeof(float), hipMemcpyDeviceToHost, cx.stream) != hipSuccess ||
+  if (download_host(r.output, dr.output, sizes[7] * sizeof(float), cx.stream) != hipSuccess ||
       hipStreamSynchronize(cx.stream) != hipSuccess) {
     res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
     return PROM_ERROR;

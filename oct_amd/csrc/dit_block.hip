@@ -472,7 +472,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16(void* handle, con
   }
   res->stage = PROM_STAGE_TRANSFER_IN;
   for (int i = 0; i < 15; ++i) {
-    if (hipMemcpyAsync(dev + offs[i], srcs[i], bytes[i], hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+    if (upload_host(dev + offs[i], srcs[i], bytes[i], cx.stream) != hipSuccess) {
       res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
       return PROM_ERROR;
     }
@@ -504,7 +504,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_dit_block_bf16(void* handle, con
   }
   (void)hipEventRecord(cx.op_end, cx.stream);
   res->stage = PROM_STAGE_TRANSFER_OUT;
-  if (hipMemcpyAsync(r.output, dr.output, bytes[15], hipMemcpyDeviceToHost, cx.stream) != hipSuccess ||
+  if (download_host(r.output, dr.output, bytes[15], cx.stream) != hipSuccess ||
       hipStreamSynchronize(cx.stream) != hipSuccess) {
     res->detail_code = PROM_DETAIL_HIP_COPY_FAILED;
     return PROM_ERROR;

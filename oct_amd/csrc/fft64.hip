@@ -815,7 +815,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_fft64(void* handle, const double
     set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_ALLOCATION_FAILED);
     return PROM_ERROR;
   }
-  if (hipMemcpyAsync(din, input, bytes, hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+  if (upload_host(din, input, bytes, cx.stream) != hipSuccess) {
     (void)hipGetLastError();
     set_status(stage, detail, PROM_STAGE_TRANSFER_IN, PROM_FFT_DETAIL_UPLOAD_FAILED);
     return PROM_ERROR;
@@ -826,7 +826,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_fft64(void* handle, const double
     set_status(stage, detail, PROM_STAGE_SUBMIT, PROM_FFT_DETAIL_DISPATCH_FAILED);
     return PROM_ERROR;
   }
-  if (hipMemcpyAsync(output, dout, bytes, hipMemcpyDeviceToHost, cx.stream) != hipSuccess ||
+  if (download_host(output, dout, bytes, cx.stream) != hipSuccess ||
       hipStreamSynchronize(cx.stream) != hipSuccess) {
     (void)hipGetLastError();
     set_status(stage, detail, PROM_STAGE_TRANSFER_OUT, PROM_FFT_DETAIL_READBACK_FAILED);

@@ -74,8 +74,8 @@ int gemm_host(void* handle, const TIn* a, const TIn* b, float* c, uint32_t m, ui
     set_status(out_stage, out_detail, PROM_STAGE_TRANSFER_IN, PROM_DETAIL_INJECTED_UPLOAD_FAILURE);
     return PROM_ERROR;
   }
-  if (hipMemcpyAsync(da, a, a_bytes, hipMemcpyHostToDevice, cx.stream) != hipSuccess ||
-      hipMemcpyAsync(db, b, b_bytes, hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+  if (upload_host(da, a, a_bytes, cx.stream) != hipSuccess ||
+      upload_host(db, b, b_bytes, cx.stream) != hipSuccess) {
     set_status(out_stage, out_detail, PROM_STAGE_TRANSFER_IN, PROM_DETAIL_HIP_COPY_FAILED);
     return PROM_ERROR;
   }
@@ -97,7 +97,7 @@ int gemm_host(void* handle, const TIn* a, const TIn* b, float* c, uint32_t m, ui
     set_status(out_stage, out_detail, PROM_STAGE_TRANSFER_OUT, PROM_DETAIL_INJECTED_DOWNLOAD_FAILURE);
     return PROM_ERROR;
   }
-  if (hipMemcpyAsync(c, dc, c_bytes, hipMemcpyDeviceToHost, cx.stream) != hipSuccess) {
+  if (download_host(c, dc, c_bytes, cx.stream) != hipSuccess) {
     (void)hipStreamSynchronize(cx.stream);
     set_status(out_stage, out_detail, PROM_STAGE_TRANSFER_OUT, PROM_DETAIL_HIP_COPY_FAILED);
     return PROM_ERROR;
@@ -384,7 +384,7 @@ int reduction_execute_once(void* handle, const PrometheusReductionRequest* reque
     return PROM_ERROR;
   }
   out.stage = PROM_STAGE_TRANSFER_IN;
-  if (hipMemcpyAsync(din, request->input, total * sizeof(float), hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+  if (upload_host(din, request->input, total * sizeof(float), cx.stream) != hipSuccess) {
     out.detail_code = PROM_REDUCTION_DETAIL_RESOURCE_CREATE_FAILED;
     return PROM_ERROR;
   }
@@ -402,8 +402,7 @@ int reduction_execute_once(void* handle, const PrometheusReductionRequest* reque
   }
   (void)hipEventRecord(cx.op_end, cx.stream);
   out.stage = PROM_STAGE_TRANSFER_OUT;
-  if (hipMemcpyAsync(request->output, dout, out_count * sizeof(float), hipMemcpyDeviceToHost, cx.stream) !=
-          hipSuccess ||
+  if (download_host(request->output, dout, out_count * sizeof(float), cx.stream) != hipSuccess ||
       hipStreamSynchronize(cx.stream) != hipSuccess) {
     out.detail_code = PROM_REDUCTION_DETAIL_READBACK_FAILED;
     return PROM_ERROR;
@@ -533,8 +532,8 @@ int rmsnorm_host(Runtime* rt, const RmsArgs& a, uint32_t* stage, int32_t* detail
     return PROM_ERROR;
   }
   *stage = PROM_STAGE_TRANSFER_IN;
-  if (hipMemcpyAsync(din, a.input, in_count * sizeof(float), hipMemcpyHostToDevice, cx.stream) != hipSuccess ||
-      hipMemcpyAsync(dw, a.weight, a.width * sizeof(float), hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+  if (upload_host(din, a.input, in_count * sizeof(float), cx.stream) != hipSuccess ||
+      upload_host(dw, a.weight, a.width * sizeof(float), cx.stream) != hipSuccess) {
     *detail = PROM_DETAIL_HIP_COPY_FAILED;
     return PROM_ERROR;
   }
@@ -547,9 +546,9 @@ int rmsnorm_host(Runtime* rt, const RmsArgs& a, uint32_t* stage, int32_t* detail
   }
   (void)hipEventRecord(cx.op_end, cx.stream);
   *stage = PROM_STAGE_TRANSFER_OUT;
-  if (hipMemcpyAsync(a.output, dout, out_count * sizeof(float), hipMemcpyDeviceToHost, cx.stream) != hipSuccess ||
+  if (download_host(a.output, dout, out_count * sizeof(float), cx.stream) != hipSuccess ||
       (a.inv_rms != nullptr &&
-       hipMemcpyAsync(a.inv_rms, dinv, a.tokens * sizeof(float), hipMemcpyDeviceToHost, cx.stream) != hipSuccess) ||
+       download_host(a.inv_rms, dinv, a.tokens * sizeof(float), cx.stream) != hipSuccess) ||
       hipStreamSynchronize(cx.stream) != hipSuccess) {
     *detail = PROM_DETAIL_HIP_COPY_FAILED;
     return PROM_ERROR;
@@ -771,12 +770,10 @@ PROM_REACTOR_API int prometheus_reactor_runtime_reduction_benchmark(void* handle
     float* din = static_cast<float*>(staging(0, r.input_element_count * sizeof(float)));
     float* dexp = static_cast<float*>(staging(2, out_count * sizeof(float)));
     if (din == nullptr || dexp == nullptr ||
-        hipMemcpyAsync(din, r.input, r.input_element_count * sizeof(float), hipMemcpyHostToDevice, cx.stream) !=
-            hipSuccess ||
+        upload_host(din, r.input, r.input_element_count * sizeof(float), cx.stream) != hipSuccess ||
         launch_row_reduction_check(din, dexp, r.row_count, r.elements_per_row, r.operation, cx.stream) !=
             hipSuccess ||
-        hipMemcpyAsync(expected.data(), dexp, out_count * sizeof(float), hipMemcpyDeviceToHost, cx.stream) !=
-            hipSuccess ||
+        download_host(expected.data(), dexp, out_count * sizeof(float), cx.stream) != hipSuccess ||
         hipStreamSynchronize(cx.stream) != hipSuccess) {
       (void)hipGetLastError();
       res.detail_code = PROM_REDUCTION_DETAIL_READBACK_FAILED;

@@ -114,6 +114,11 @@ bool ensure_device();
 Runtime* lookup(void* handle);
 // Grow-only device staging buffer `slot` of at least `bytes`.
 void* staging(uint32_t slot, size_t bytes);
+// Copies of caller-owned pageable host buffers (host_copy.hip).  upload_host
+// returns once `src` has been read (the device side completes in stream
+// order); download_host returns once `dst` holds the data.
+hipError_t upload_host(void* dst, const void* src, size_t bytes, hipStream_t stream);
+hipError_t download_host(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
 // Unconsumed async tasks of a runtime (READY and FAILED count until consumed
 // or abandoned); the synchronous SGEMM is rejected while this is non-zero.
