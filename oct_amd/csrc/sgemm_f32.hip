@@ -816,23 +816,32 @@ __global__ __launch_bounds__(512, 1) void sgemm_f32_dl64_ring_kernel(const float
 // dst [rows_d][ld_d] (16-byte rows) = src [rows_s][cols_s] (row stride ld_s,
 // any alignment), zero outside: the padded copies through which operands the
 // direct-to-LDS kernels cannot read (ragged k or n, unaligned rows) reach them.
-__global__ __launch_bounds__(256) void pack_pad_kernel(const float* __restrict__ src, int rows_s, int cols_s, int ld_s,
-                                                       float* __restrict__ dst, int rows_d, int ld_d) {
-  const int c4n = ld_d >> 2;
-  const size_t total = (size_t)rows_d * c4n;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int r = (int)(i / c4n);
-    const int c = (int)(i - (size_t)r * c4n) * 4;
-    floatx4 v = {0.f, 0.f, 0.f, 0.f};
-    if (r < rows_s) {
-      const float* sp = src + (size_t)r * ld_s + c;
-      if (c + 0 < cols_s) v.x = sp[0];
-      if (c + 1 < cols_s) v.y = sp[1];
-      if (c + 2 < cols_s) v.z = sp[2];
-      if (c + 3 < cols_s) v.w = sp[3];
-    }
-    reinterpret_cast<floatx4*>(dst + (size_t)r * ld_d)[c >> 2] = v;
+// One launch pads both operands: the first blocks_a workgroups copy A, the
+// rest B, one 16-byte group per thread (rows_d * ld_d / 4 < 2^31: the GEMM
+// admission bounds m*k and k*n below 2^32).
+struct PadJob {
+  const float* src;
+  float* dst;
+  int rows_s, cols_s, ld_s, rows_d, ld_d;
+};
+
+__global__ __launch_bounds__(256) void pack_pad_kernel(PadJob ja, PadJob jb, uint32_t blocks_a) {
+  const bool first = blockIdx.x < blocks_a;
+  const PadJob j = first ? ja : jb;
+  const uint32_t i = (first ? blockIdx.x : blockIdx.x - blocks_a) * 256u + threadIdx.x;
+  const uint32_t c4n = (uint32_t)j.ld_d >> 2;
+  if (i >= (uint32_t)j.rows_d * c4n) return;
+  const int r = (int)(i / c4n);
+  const int c = (int)(i - (uint32_t)r * c4n) * 4;
+  floatx4 v = {0.f, 0.f, 0.f, 0.f};
+  if (r < j.rows_s) {
+    const float* sp = j.src + (size_t)r * j.ld_s + c;
+    if (c + 0 < j.cols_s) v.x = sp[0];
+    if (c + 1 < j.cols_s) v.y = sp[1];
+    if (c + 2 < j.cols_s) v.z = sp[2];
+    if (c + 3 < j.cols_s) v.w = sp[3];
   }
+  reinterpret_cast<floatx4*>(j.dst + (size_t)r * j.ld_d)[c >> 2] = v;
 }
 
 // y[m] = A[m,:] . x : one wave per row, 4 rows per workgroup.  HBM-bound:
@@ -1245,11 +1254,11 @@ hipError_t run_sgemm_schedule(const SgemmSchedule& s, const float* a, int lda, c
     float* pb = packed != nullptr ? packed + (size_t)m * s.k4
                                   : static_cast<float*>(staging(9, (size_t)s.k4 * s.n4 * sizeof(float)));
     if (pa == nullptr || pb == nullptr) return hipErrorOutOfMemory;
-    const size_t na = (size_t)m * (s.k4 / 4), nb = (size_t)s.k4 * (s.n4 / 4);
-    hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)std::min<size_t>(8192, (na + 255) / 256)), dim3(256), 0,
-                       stream, a, (int)m, (int)k, lda, pa, (int)m, (int)s.k4);
-    hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)std::min<size_t>(8192, (nb + 255) / 256)), dim3(256), 0,
-                       stream, b, (int)k, (int)n, ldb, pb, (int)s.k4, (int)s.n4);
+    const PadJob ja{a, pa, (int)m, (int)k, lda, (int)m, (int)s.k4};
+    const PadJob jb{b, pb, (int)k, (int)n, ldb, (int)s.k4, (int)s.n4};
+    const uint32_t blocks_a = (uint32_t)(((uint64_t)m * (s.k4 / 4) + 255) / 256);
+    const uint32_t blocks_b = (uint32_t)(((uint64_t)s.k4 * (s.n4 / 4) + 255) / 256);
+    hipLaunchKernelGGL(pack_pad_kernel, dim3(blocks_a + blocks_b), dim3(256), 0, stream, ja, jb, blocks_a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     a = pa;
