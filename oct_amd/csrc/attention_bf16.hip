@@ -304,7 +304,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
                                                                      int ldk, int ldv, int ldo, float scale_log2,
                                                                      const float2* __restrict__ rope,
                                                                      const float* __restrict__ qn,
-                                                                     const float* __restrict__ kn, float eps) {
+                                                                     const float* __restrict__ kn, float eps,
+                                                                     int o_slice) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -614,6 +615,21 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bf16_dma_kernel(const uint1
     }
   }
   __syncthreads();
+  if (o_slice > 0) {
+    // K-blocked O ([D/32][o_slice][32], for the output GEMM): each store
+    // instruction writes 16 rows of one 32-column slice, 1 KiB contiguous
+    // (lanes 16j .. 16j + 15: chunk j of 16 rows, so each 16-lane LDS read
+    // touches 16 distinct bank groups).
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int row = (lane & 15) + 16 * (u & 1), blk = u >> 1, chunk = lane >> 4;
+      const int q = q0 + row;
+      if (q < T)
+        *reinterpret_cast<u32x4*>(O + ((size_t)(head * 4 + blk) * o_slice + q) * 32 + 8 * chunk) =
+            *reinterpret_cast<const u32x4*>(&stage[row * kKP + 32 * blk + 8 * chunk]);
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int c = lane + 64 * u;
@@ -649,7 +665,7 @@ hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k,
     lds_raised = true;
   }
   hipLaunchKernelGGL(flash_attn_bf16_dma_kernel<false>, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk,
-                     ldv, ldo, scale_log2, nullptr, nullptr, nullptr, 0.0f);
+                     ldv, ldo, scale_log2, nullptr, nullptr, nullptr, 0.0f, 0);
   return hipGetLastError();
 }
 
@@ -659,7 +675,7 @@ hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k,
 hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v,
                                             int ldv, uint16_t* o, int ldo, int T, int heads, float scale,
                                             const float2* rope, const float* qn, const float* kn, float eps,
-                                            hipStream_t stream) {
+                                            hipStream_t stream, int o_slice) {
   const dim3 grid((unsigned)((T + 4 * kQW - 1) / (4 * kQW) * heads));
   static bool lds_raised = false;
   if (!lds_raised) {
@@ -669,7 +685,7 @@ hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const u
     lds_raised = true;
   }
   hipLaunchKernelGGL(flash_attn_bf16_dma_kernel<true>, grid, dim3(256), kDmaLds, stream, q, k, v, o, T, ldq, ldk, ldv,
-                     ldo, scale * 1.4426950408889634f, rope, qn, kn, eps);
+                     ldo, scale * 1.4426950408889634f, rope, qn, kn, eps, o_slice);
   return hipGetLastError();
 }
 

@@ -84,6 +84,17 @@ __device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, int i, floatx4 v, 
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, h), r, (uint32_t)(8 * i), 0, 0);
 }
 
+// Chunk i (4 values, bf16) of row t of a K-blocked matrix [D/32][slice][32]
+// (the layout a following bf16 GEMM reads in whole 128-byte lines); chunks
+// past D are dropped.
+__device__ __forceinline__ void st4_blocked(uint16_t* base, int slice, int t, int i, int d4, floatx4 v) {
+  if (i >= d4) return;
+  const bf16x4 h = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+  *reinterpret_cast<u32x2*>(base + ((size_t)(i >> 3) * slice + t) * 32 + 4 * (i & 7)) = __builtin_bit_cast(u32x2, h);
+}
+
+__device__ __forceinline__ void st4_blocked(float*, int, int, int, int, floatx4) {}  // fp32 outputs stay row-major
+
 // An fp32 chunk as a streaming store (cache-policy operand 2: nt), for fp32
 // rows that no kernel reads soon: they leave no dirty L2 lines for the next
 // kernels to wait on.
@@ -137,11 +148,12 @@ __device__ __forceinline__ void stage_vec(floatx4* dst, const float* src, int d4
 template <int kRows>
 inline dim3 row_groups(int T) { return dim3((unsigned)((T + kRows - 1) / kRows)); }
 
-// out = RMSNorm(x; w) * scale.
+// out = RMSNorm(x; w) * scale; out_slice > 0 (bf16 only): out is K-blocked
+// with that many rows per slice.
 template <typename OutT, int kRows = 4>
 __global__ __launch_bounds__(64 * kRows) void norm_mod_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                        const float* __restrict__ scale, OutT* __restrict__ out, int T,
-                                                       int D, float eps) {
+                                                       int D, float eps, int out_slice) {
   __shared__ floatx4 sw[1024], ssc[1024];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63);
   const int t = min((int)blockIdx.x * kRows + wave, T - 1);
@@ -163,18 +175,22 @@ __global__ __launch_bounds__(64 * kRows) void norm_mod_kernel(const float* __res
     o.y = v[c].y * inv * g.y * sc.y;
     o.z = v[c].z * inv * g.z * sc.z;
     o.w = v[c].w * inv * g.w * sc.w;
-    st4(ro, i, o, out);
+    if (out_slice > 0)
+      st4_blocked(out, out_slice, t, i, d4, o);
+    else
+      st4(ro, i, o, out);
   }
 }
 
 // r = x + gate * RMSNorm(proj; n2) (fp32 out), f = RMSNorm(r; n3) * scale (OutT); proj fp32 or bf16.
-// kStream: r is written with streaming stores.
+// kStream: r is written with streaming stores.  f_slice > 0 (bf16 only): f is
+// K-blocked with that many rows per slice.
 template <typename OutT, int kRows = 8, typename ProjT = float, bool kStream = false>
 __global__ __launch_bounds__(64 * kRows) void resid_norm_mod_kernel(const float* __restrict__ x, const ProjT* __restrict__ proj,
                                                              const float* __restrict__ n2, const float* __restrict__ gate,
                                                              const float* __restrict__ n3, const float* __restrict__ scale,
                                                              float* __restrict__ r_out, OutT* __restrict__ f_out, int T,
-                                                             int D, float eps) {
+                                                             int D, float eps, int f_slice) {
   __shared__ floatx4 s2[1024], sg[1024], s3[1024], ssc[1024];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63);
   const int t = min((int)blockIdx.x * kRows + wave, T - 1);
@@ -221,7 +237,10 @@ __global__ __launch_bounds__(64 * kRows) void resid_norm_mod_kernel(const float*
     o.y = v[c].y * inv2 * w.y * sc.y;
     o.z = v[c].z * inv2 * w.z * sc.z;
     o.w = v[c].w * inv2 * w.w * sc.w;
-    st4(rf, i, o, f_out);
+    if (f_slice > 0)
+      st4_blocked(f_out, f_slice, t, i, d4, o);
+    else
+      st4(rf, i, o, f_out);
   }
 }
 

@@ -244,11 +244,16 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 enum { kWsMod, kWsA, kWsQkv, kWsQ, kWsK, kWsV, kWsO, kWsProj, kWsR, kWsF, kWsG, kWsH, kWsW2, kWsRope, kWsCount };
 
+// Rows of a K-blocked GEMM operand: every slice covers the GEMM's last tile row.
+size_t blocked_rows(size_t T) { return (T + 255) & ~(size_t)255; }
+
 size_t dit_workspace(const PrometheusDitBlockBf16Request* r, size_t off[kWsCount]) {
-  const size_t T = r->tokens, D = r->hidden, F = r->ffn_hidden;
-  const size_t sizes[kWsCount] = {4 * D * 4, T * D * 2, T * 3 * D * 2, 0,             0,         0,
-                                  T * D * 2, T * D * 4, T * D * 4,     T * D * 2,     T * 2 * F * 4, T * F * 2,
-                                  T * D * 4, T * 64 * 8};
+  const size_t T = r->tokens, D = r->hidden, F = r->ffn_hidden, Tb = blocked_rows(T);
+  // A, O, F and H (the bf16 GEMMs' left operands) hold Tb rows so that they
+  // can be K-blocked.
+  const size_t sizes[kWsCount] = {4 * D * 4,  Tb * D * 2, T * 3 * D * 2, 0,             0,          0,
+                                  Tb * D * 2, T * D * 4,  T * D * 4,     Tb * D * 2,    T * 2 * F * 4, Tb * F * 2,
+                                  T * D * 4,  T * 64 * 8};
   size_t o = 0;
   for (int i = 0; i < kWsCount; ++i) {
     off[i] = o;
@@ -320,18 +325,29 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
                        r->rope_theta, (int)r->rope_axes[0], (int)r->rope_axes[1]);
     PROM_STEP(hipGetLastError());
   }
-  hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, rows::row_groups<4>(T), dim3(256), 0, st, r->input, r->attn_norm1, scaleA, A, T, D, eps);
+  // Each GEMM that runs on the four-stage kernel reads its left operand
+  // K-blocked ([K/32][Tb][32]: whole 128-byte lines per transfer, 4096^3
+  // 109 -> 105.5 us), written so by the kernel that produces it; the others
+  // read rows.  The values and their order are the same either way.
+  const int Tb = (int)blocked_rows((size_t)T);
+  const int qkv_slice = gemm_bf16_takes_blocked_a(A, D, r->w_qkv, 3 * D, T, 3 * D, D) ? Tb : 0;
+  const int o_slice = gemm_bf16_takes_blocked_a(O, D, r->w_out, D, T, D, D) ? Tb : 0;
+  const int f_slice = gemm_bf16_swiglu_takes_blocked_a(Fb, D, r->w_13, T, F, D) ? Tb : 0;
+  const int h_slice = f_slice > 0 && gemm_bf16_takes_blocked_a(Hb, F, r->w_2, D, T, D, F) ? Tb : 0;
+  hipLaunchKernelGGL(rows::norm_mod_kernel<uint16_t>, rows::row_groups<4>(T), dim3(256), 0, st, r->input,
+                     r->attn_norm1, scaleA, A, T, D, eps, qkv_slice);
   PROM_STEP(hipGetLastError());
   // QKV in bf16 (one rounding before the per-head norms), K's norm and RoPE in
   // place, Q's inside the attention, which reads Q, K, V from the [T, 3D] rows.
-  PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, nullptr, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
+  PROM_STEP(launch_gemm_bf16_ex(A, D, r->w_qkv, 3 * D, nullptr, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr,
+                                qkv_slice));
   hipLaunchKernelGGL(k_norm_rope_kernel, dim3((T + 3) / 4), blk, 0, st, qkv, rope, r->k_norm, T, H, eps);
   PROM_STEP(hipGetLastError());
   PROM_STEP(launch_flash_attn_bf16_qnorm_rope(qkv, 3 * D, qkv + D, 3 * D, qkv + 2 * D, 3 * D, O, D, T, H,
-                                              1.0f / sqrtf(128.0f), rope, r->q_norm, r->k_norm, eps, st));
+                                              1.0f / sqrtf(128.0f), rope, r->q_norm, r->k_norm, eps, st, o_slice));
   // The out- and down-projections go to bf16: both are RMS-normalised before
   // they join the fp32 residual stream.
-  PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, nullptr, projb, D, T, D, D, nullptr, 0, st, nullptr));
+  PROM_STEP(launch_gemm_bf16_ex(O, D, r->w_out, D, nullptr, projb, D, T, D, D, nullptr, 0, st, nullptr, o_slice));
   // 149 VGPRs allow 3 waves per SIMD, so one 12-wave workgroup per CU: 352
   // workgroups at T = 4224 run in two rounds, where 8-row workgroups (one per
   // CU as well) took three, the last with 16 (45 -> 37.5 us).  R is next read
@@ -339,14 +355,15 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
   // kernel: both go out as streaming stores (W1|W3 -4 us, the first row
   // kernel -1.3, this one -1.2).
   hipLaunchKernelGGL((rows::resid_norm_mod_kernel<uint16_t, 12, uint16_t, true>), rows::row_groups<12>(T), dim3(768), 0, st, r->input, projb, r->attn_norm2, gateA, r->ffn_norm1, scaleM,
-                     R, Fb, T, D, eps);
+                     R, Fb, T, D, eps, f_slice);
   PROM_STEP(hipGetLastError());
   // FFN up-projection with SwiGLU fused into the GEMM epilogue when the shape
   // allows (F a multiple of 128, D of 64); otherwise GEMM to fp32, then SwiGLU.
   // (G, unused on the fused path, takes the K-slice sums of a final partial wave.)
   uint32_t k13 = 1;
   const hipError_t fused =
-      launch_gemm_bf16_swiglu(Fb, D, r->w_13, Hb, F, T, F, D, st, G, (size_t)T * 2 * F * sizeof(float), &k13);
+      launch_gemm_bf16_swiglu(Fb, D, r->w_13, Hb, F, T, F, D, st, G, (size_t)T * 2 * F * sizeof(float), &k13,
+                              f_slice, h_slice);
   if (fused == hipErrorNotSupported) {
     PROM_STEP(launch_gemm_bf16_ex(Fb, D, r->w_13, 2 * F, G, nullptr, 2 * F, T, 2 * F, D, nullptr, 0, st, nullptr));
     const size_t total = (size_t)T * (F / 4);
@@ -357,7 +374,7 @@ hipError_t enqueue_dit(const PrometheusDitBlockBf16Request* r, char* ws, const s
     PROM_STEP(fused);
     n += k13 - 1;
   }
-  PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, nullptr, w2b, D, T, D, F, nullptr, 0, st, nullptr));
+  PROM_STEP(launch_gemm_bf16_ex(Hb, F, r->w_2, D, nullptr, w2b, D, T, D, F, nullptr, 0, st, nullptr, h_slice));
   hipLaunchKernelGGL((rows::final_resid_kernel<4, uint16_t, true>), rows::row_groups<4>(T), dim3(256), 0, st, R, w2b, r->ffn_norm2, gateM, r->output, T, D, eps);
   PROM_STEP(hipGetLastError());
 #undef PROM_STEP

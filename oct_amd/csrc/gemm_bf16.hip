@@ -600,7 +600,8 @@ template <bool kSwiGLU, int kSt>
 __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                    float* C, int M, int N, int K, int tm, int tn, int kt0,
                                                    int k_tiles, int lda, int ldb, int ldc, const float* R, int ldr,
-                                                   uint16_t* Cb, float2* part, char* const (&S)[kSt]) {
+                                                   uint16_t* Cb, float2* part, int a_slice, int h_slice,
+                                                   char* const (&S)[kSt]) {
   const int row0 = tm * kBM2;
   const int col0 = kSwiGLU ? tn * (kBN2 / 2) : tn * kBN2;
   const int tid = (int)threadIdx.x;
@@ -617,7 +618,7 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
     const int q = wave * 2 + i;
     const int r = 16 * q + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 2) & 3);
-    a_off[i] = (uint32_t)(((row0 + r) * lda + 8 * c) * 2);
+    a_off[i] = a_slice > 0 ? (uint32_t)(((row0 + r) * 32 + 8 * c) * 2) : (uint32_t)(((row0 + r) * lda + 8 * c) * 2);
     const int kr = 2 * q + (lane >> 5);
     const int cb = (lane & 31) ^ swz_b(kr);
     int gcol = col0 + 8 * cb;
@@ -644,7 +645,7 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
     d.w = 0x00020000;
     return d;
   };
-  const int4v da = desc(A, (uint32_t)((size_t)M * lda * 2));
+  const int4v da = desc(A, (uint32_t)(a_slice > 0 ? (size_t)K * a_slice * 2 : (size_t)M * lda * 2));
   const int4v db = desc(B, (uint32_t)((size_t)K * ldb * 2));
   // Transfer j (0..3) of this wave for the tile at k0: A rows (j even) or B
   // rows (j odd) of instruction i = j / 2.
@@ -653,7 +654,7 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
     const int q = wave * 2 + i;
     const uint32_t base = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)stage;
     if ((j & 1) == 0) {
-      const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
+      const int sa = __builtin_amdgcn_readfirstlane(a_slice > 0 ? k0 * a_slice * 2 : k0 * 2);
       const uint32_t la = __builtin_amdgcn_readfirstlane(base + q * 1024);
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(la), "v"(a_off[i]), "s"(da),
                    "s"(sa)
@@ -788,13 +789,16 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         const int rb = row0 + wm * 128 + mi * 32 + lgrp;
-        uint16_t* hp = Cb + (size_t)rb * ldc + col;
+        // K-blocked H (h_slice rows per 32-column slice): a row step is 32
+        uint16_t* hp = h_slice > 0 ? Cb + ((size_t)(col >> 5) * h_slice + rb) * 32 + (col & 31)
+                                   : Cb + (size_t)rb * ldc + col;
+        const size_t hstep = h_slice > 0 ? 32 : (size_t)ldc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dr = 8 * (r >> 2) + (r & 3);
           if (rb + dr < M) {
             const float g = acc[mi][0][r], u = acc[mi][1][r];
-            hp[(size_t)dr * ldc] = f32_to_bf16_rne(silu_mul(g, u));
+            hp[(size_t)dr * hstep] = f32_to_bf16_rne(silu_mul(g, u));
           }
         }
       }
@@ -829,7 +833,8 @@ __device__ __forceinline__ void gemm_bf16_dl4_body(const uint16_t* __restrict__ 
 __global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_kernel(const uint16_t* __restrict__ A,
                                                               const uint16_t* __restrict__ B, float* C, int M, int N,
                                                               int K, int tiles_m, int tiles_n, int lda, int ldb,
-                                                              int ldc, const float* R, int ldr, uint16_t* Cb) {
+                                                              int ldc, const float* R, int ldr, uint16_t* Cb,
+                                                              int a_slice) {
   __shared__ __attribute__((aligned(1024))) char S0[kStage4];
   __shared__ __attribute__((aligned(1024))) char S1[kStage4];
   __shared__ __attribute__((aligned(1024))) char S2[kStage4];
@@ -838,7 +843,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_kernel(const uint16_t* _
   char* const st[5] = {S0, S1, S2, S3, S4};
   int tm, tn;
   map_tile2(tiles_m, tiles_n, &tm, &tn);
-  gemm_bf16_dl4_body<false>(A, B, C, M, N, K, tm, tn, 0, K / kBK4, lda, ldb, ldc, R, ldr, Cb, nullptr, st);
+  gemm_bf16_dl4_body<false>(A, B, C, M, N, K, tm, tn, 0, K / kBK4, lda, ldb, ldc, R, ldr, Cb, nullptr, a_slice, 0,
+                            st);
 }
 
 // Workgroups b < n_main take whole tiles (pids 0 .. n_main-1, XCD-contiguous);
@@ -849,7 +855,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_swiglu_kernel(const uint
                                                                      const uint16_t* __restrict__ B, int M, int N,
                                                                      int K, int tiles_m, int tiles_n, int lda, int ldb,
                                                                      int ldh, uint16_t* H, int n_main, int splits,
-                                                                     float2* part) {
+                                                                     float2* part, int a_slice, int h_slice) {
   __shared__ __attribute__((aligned(1024))) char S0[kStage4];
   __shared__ __attribute__((aligned(1024))) char S1[kStage4];
   __shared__ __attribute__((aligned(1024))) char S2[kStage4];
@@ -872,14 +878,15 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_dl4_swiglu_kernel(const uint
   }
   int tm, tn;
   pid_tile2(pid, tiles_m, tiles_n, &tm, &tn);
-  gemm_bf16_dl4_body<true>(A, B, nullptr, M, N, K, tm, tn, kt0, kn, lda, ldb, ldh, nullptr, 0, H, dst, st);
+  gemm_bf16_dl4_body<true>(A, B, nullptr, M, N, K, tm, tn, kt0, kn, lda, ldb, ldh, nullptr, 0, H, dst, a_slice,
+                           h_slice, st);
 }
 
 // h = silu(g) * u for the split tiles: (g, u) summed over the K slices in
 // slice order, then silu_mul as in the GEMM epilogue.
 __global__ __launch_bounds__(256) void swiglu_splitk_kernel(const float2* __restrict__ part, uint16_t* __restrict__ H,
                                                             int ldh, int M, int tiles_m, int tiles_n, int n_main,
-                                                            int splits) {
+                                                            int splits, int h_slice) {
   const int ti = (int)blockIdx.y;
   const int e = (int)(blockIdx.x * 256 + threadIdx.x);  // element of the 256 x 128 tile
   const int rl = e >> 7, cl = e & 127;
@@ -893,7 +900,9 @@ __global__ __launch_bounds__(256) void swiglu_splitk_kernel(const float2* __rest
     g += p[(size_t)s * (kBM2 * 128)].x;
     u += p[(size_t)s * (kBM2 * 128)].y;
   }
-  H[(size_t)row * ldh + tn * 128 + cl] = f32_to_bf16_rne(silu_mul(g, u));
+  const int col = tn * 128 + cl;
+  const size_t at = h_slice > 0 ? ((size_t)(col >> 5) * h_slice + row) * 32 + (col & 31) : (size_t)row * ldh + col;
+  H[at] = f32_to_bf16_rne(silu_mul(g, u));
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -906,19 +915,61 @@ inline bool use_four_stage(int tiles, uint32_t k) { return tiles >= 240 || k >= 
 
 }  // namespace
 
+namespace {
+
+enum class Bf16Path { kFourStage, kTwoStage, kStaged256, kSmall };
+
+// The kernel launch_gemm_bf16_ex runs for a shape and its operands' layout.
+Bf16Path bf16_path(const uint16_t* a, int lda, const uint16_t* b, int ldb, uint32_t m, uint32_t n, uint32_t k,
+                   bool* vec_out) {
+  const bool vec = (k % 8 == 0) && (n % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(a) && aligned16(b);
+  if (vec_out) *vec_out = vec;
+  const int tiles = (int)((m + kBM2 - 1) / kBM2) * (int)((n + kBN2 - 1) / kBN2);
+  if (!vec || tiles < 128) return Bf16Path::kSmall;
+  const bool range = (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * ldb * 2 < (1ull << 31);
+  if (range && k % kBK4 == 0 && use_four_stage(tiles, k)) return Bf16Path::kFourStage;
+  if (range && k % kBK2 == 0) return Bf16Path::kTwoStage;
+  return Bf16Path::kStaged256;
+}
+
+bool swiglu_fused_ok(const uint16_t* a, int lda, const uint16_t* w13, uint32_t m, uint32_t f, uint32_t k) {
+  return f % 128 == 0 && k % kBK4 == 0 && lda % 8 == 0 && aligned16(a) && aligned16(w13) &&
+         (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * 2 * f * 2 < (1ull << 31);
+}
+
+// K-blocked A ([k/32][a_slice][32], a_slice >= m rounded up to 256 rows) keeps
+// every byte offset below 2^31.
+bool blocked_range(int a_slice, uint32_t m, uint32_t k) {
+  return a_slice >= (int)((m + kBM2 - 1) / kBM2 * kBM2) && (size_t)k * a_slice * 2 < (1ull << 31);
+}
+
+}  // namespace
+
+bool gemm_bf16_takes_blocked_a(const uint16_t* a, int lda, const uint16_t* b, int ldb, uint32_t m, uint32_t n,
+                               uint32_t k) {
+  return bf16_path(a, lda, b, ldb, m, n, k, nullptr) == Bf16Path::kFourStage;
+}
+
+bool gemm_bf16_swiglu_takes_blocked_a(const uint16_t* a, int lda, const uint16_t* w13, uint32_t m, uint32_t f,
+                                      uint32_t k) {
+  const int tiles = (int)((m + kBM2 - 1) / kBM2) * (int)(f / 128);
+  return swiglu_fused_ok(a, lda, w13, m, f, k) && use_four_stage(tiles, k);
+}
+
 hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, int ldb, float* c, uint16_t* cb,
                                int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
-                               hipStream_t stream, int* path_detail) {
-  const bool vec = (k % 8 == 0) && (n % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(a) && aligned16(b);
-  const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
-  const int tiles_n2 = (int)((n + kBN2 - 1) / kBN2);
-  if (vec && tiles_m2 * tiles_n2 >= 128) {
+                               hipStream_t stream, int* path_detail, int a_slice) {
+  bool vec = false;
+  const Bf16Path path = bf16_path(a, lda, b, ldb, m, n, k, &vec);
+  if (a_slice > 0 && (path != Bf16Path::kFourStage || !blocked_range(a_slice, m, k))) return hipErrorNotSupported;
+  if (path != Bf16Path::kSmall) {
+    const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
+    const int tiles_n2 = (int)((n + kBN2 - 1) / kBN2);
     const dim3 grid2((unsigned)(tiles_m2 * tiles_n2));
-    const bool range = (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * ldb * 2 < (1ull << 31);
-    if (range && k % kBK4 == 0 && use_four_stage(tiles_m2 * tiles_n2, k))
+    if (path == Bf16Path::kFourStage)
       hipLaunchKernelGGL(gemm_bf16_dl4_kernel, grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n, (int)k, tiles_m2,
-                         tiles_n2, lda, ldb, ldc, residual, ldr, cb);
-    else if (range && k % kBK2 == 0)
+                         tiles_n2, lda, ldb, ldc, residual, ldr, cb, a_slice);
+    else if (path == Bf16Path::kTwoStage)
       hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<false>, grid2, dim3(512), 0, stream, a, b, c, (int)m, (int)n, (int)k,
                          tiles_m2, tiles_n2, lda, ldb, ldc, residual, ldr, cb);
     else
@@ -942,18 +993,21 @@ hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, in
 
 hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w13, uint16_t* h, int ldh, uint32_t m,
                                    uint32_t f, uint32_t k, hipStream_t stream, void* part_ws, size_t part_bytes,
-                                   uint32_t* launches) {
+                                   uint32_t* launches, int a_slice, int h_slice) {
   if (launches) *launches = 1;
   // Fused path conditions: whole 128-column output tiles, K a multiple of the K
   // tile, 16-byte aligned rows, byte offsets below 2^31; otherwise the caller
   // runs the GEMM and the elementwise SwiGLU separately.
-  const bool ok = f % 128 == 0 && k % kBK4 == 0 && lda % 8 == 0 && aligned16(a) && aligned16(w13) &&
-                  (size_t)(m + kBM2) * lda * 2 < (1ull << 31) && (size_t)k * 2 * f * 2 < (1ull << 31);
-  if (!ok) return hipErrorNotSupported;
+  if (!swiglu_fused_ok(a, lda, w13, m, f, k)) return hipErrorNotSupported;
   const int tiles_m2 = (int)((m + kBM2 - 1) / kBM2);
   const int tiles_n2 = (int)(f / 128);
   const dim3 grid((unsigned)(tiles_m2 * tiles_n2));
-  if (use_four_stage(tiles_m2 * tiles_n2, k)) {
+  const bool four = use_four_stage(tiles_m2 * tiles_n2, k);
+  // K-blocked A or H only on the four-stage kernel.
+  if ((a_slice > 0 && (!four || !blocked_range(a_slice, m, k))) ||
+      (h_slice > 0 && (!four || h_slice < tiles_m2 * kBM2 || (size_t)f * h_slice * 2 >= (1ull << 31))))
+    return hipErrorInvalidValue;
+  if (four) {
     // One workgroup per CU: the tiles of a final wave that would run at most
     // half full are split along K into as many slices as fill it (at most 4,
     // each of 4 K tiles or more), their partial sums going to part_ws.
@@ -967,15 +1021,16 @@ hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w
       const int n_main = total - rem;
       hipLaunchKernelGGL(gemm_bf16_dl4_swiglu_kernel, dim3((unsigned)(n_main + rem * splits)), dim3(512), 0, stream, a,
                          w13, (int)m, (int)f, (int)k, tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, h, n_main, splits,
-                         reinterpret_cast<float2*>(part_ws));
+                         reinterpret_cast<float2*>(part_ws), a_slice, h_slice);
       const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(swiglu_splitk_kernel, dim3(kBM2 * 128 / 256, (unsigned)rem), dim3(256), 0, stream,
-                         reinterpret_cast<const float2*>(part_ws), h, ldh, (int)m, tiles_m2, tiles_n2, n_main, splits);
+                         reinterpret_cast<const float2*>(part_ws), h, ldh, (int)m, tiles_m2, tiles_n2, n_main, splits,
+                         h_slice);
       if (launches) *launches = 2;
     } else {
       hipLaunchKernelGGL(gemm_bf16_dl4_swiglu_kernel, grid, dim3(512), 0, stream, a, w13, (int)m, (int)f, (int)k,
-                         tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, h, total, 1, nullptr);
+                         tiles_m2, tiles_n2, lda, (int)(2 * f), ldh, h, total, 1, nullptr, a_slice, h_slice);
     }
   } else if (k % kBK2 == 0)
     hipLaunchKernelGGL(gemm_bf16_mfma_dl_kernel<true>, grid, dim3(512), 0, stream, a, w13, nullptr, (int)m, (int)f,
@@ -987,7 +1042,7 @@ hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w
 
 hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
                             hipStream_t stream, int* path_detail) {
-  return launch_gemm_bf16_ex(a, (int)k, b, (int)n, c, nullptr, (int)n, m, n, k, nullptr, 0, stream, path_detail);
+  return launch_gemm_bf16_ex(a, (int)k, b, (int)n, c, nullptr, (int)n, m, n, k, nullptr, 0, stream, path_detail, 0);
 }
 
 }  // namespace prom

@@ -179,9 +179,23 @@ hipError_t launch_sgemm_f32_variant(const float* a, const float* b, float* c, ui
 hipError_t launch_sgemm_f32_batched(const float* a, int lda, long long sa, const float* b, int ldb, long long sb,
                                     float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
                                     uint32_t batch, hipStream_t stream);
+// K-blocked A: a_slice > 0 says A is stored as [k/32][a_slice][32] (the 32
+// consecutive k of one row are 64 contiguous bytes, rows of a slice adjacent,
+// a_slice >= m rounded up to 256), so every HBM -> LDS transfer of A moves
+// whole 128-byte lines; only the four-stage kernel reads it, and
+// gemm_bf16_takes_blocked_a says whether a shape runs there (with a_slice == 0
+// A is row-major with row stride lda).  hipErrorNotSupported otherwise.
 hipError_t launch_gemm_bf16_ex(const uint16_t* a, int lda, const uint16_t* b, int ldb, float* c, uint16_t* cb,
                                int ldc, uint32_t m, uint32_t n, uint32_t k, const float* residual, int ldr,
-                               hipStream_t stream, int* path_detail);
+                               hipStream_t stream, int* path_detail, int a_slice = 0);
+// True when launch_gemm_bf16_ex runs this shape on the four-stage kernel (a:
+// 16-byte aligned, lda its row-major stride).
+bool gemm_bf16_takes_blocked_a(const uint16_t* a, int lda, const uint16_t* b, int ldb, uint32_t m, uint32_t n,
+                               uint32_t k);
+// The same for the fused SwiGLU GEMM, whose four-stage kernel also writes H
+// K-blocked ([f/32][h_slice][32]) for a following GEMM when h_slice > 0.
+bool gemm_bf16_swiglu_takes_blocked_a(const uint16_t* a, int lda, const uint16_t* w13, uint32_t m, uint32_t f,
+                                      uint32_t k);
 hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint32_t m, uint32_t n, uint32_t k,
                             hipStream_t stream, int* path_detail);
 // h[m, f] (bf16) = silu(a @ w13[:, :f]) * (a @ w13[:, f:]) in one GEMM; returns
@@ -190,9 +204,11 @@ hipError_t launch_gemm_bf16(const uint16_t* a, const uint16_t* b, float* c, uint
 // final partial wave, which are then split along K; their fixed slice order
 // keeps the result deterministic.  *launches (when given) receives the number
 // of kernels queued.
+// a_slice / h_slice > 0 (K-blocked A or H) only where
+// gemm_bf16_swiglu_takes_blocked_a holds; hipErrorInvalidValue otherwise.
 hipError_t launch_gemm_bf16_swiglu(const uint16_t* a, int lda, const uint16_t* w13, uint16_t* h, int ldh, uint32_t m,
                                    uint32_t f, uint32_t k, hipStream_t stream, void* part_ws, size_t part_bytes,
-                                   uint32_t* launches = nullptr);
+                                   uint32_t* launches = nullptr, int a_slice = 0, int h_slice = 0);
 // bf16 flash attention, head dim 128, full (non-causal): Q/K/V/O [T, ld*] with
 // head h at column 128 h.  variant 0: K/V tiles moved HBM -> LDS by DMA (64 KiB
 // of dynamic LDS); 1: tiles staged through registers.  hipErrorInvalidValue for
@@ -202,11 +218,13 @@ hipError_t launch_flash_attn_bf16(const uint16_t* q, int ldq, const uint16_t* k,
                                   int variant);
 // Variant 0 with the DiT block's per-head RMSNorm (weights qn [128], eps) and
 // RoPE (rope [T][64] (cos, sin) per pair) applied to the raw Q rows as they
-// are loaded, with k_norm_rope_kernel's arithmetic (dit_block.hip).
+// are loaded, with k_norm_rope_kernel's arithmetic (dit_block.hip).  o_slice
+// > 0 writes O K-blocked ([128 heads / 32][o_slice][32], o_slice >= T) for a
+// following launch_gemm_bf16_ex with that a_slice; 0 writes rows of stride ldo.
 hipError_t launch_flash_attn_bf16_qnorm_rope(const uint16_t* q, int ldq, const uint16_t* k, int ldk, const uint16_t* v,
                                             int ldv, uint16_t* o, int ldo, int T, int heads, float scale,
                                             const float2* rope, const float* qn, const float* kn, float eps,
-                                            hipStream_t stream);
+                                            hipStream_t stream, int o_slice = 0);
 // Binary64 FFT of n = 2^k <= 2^20 points (interleaved complex); temp holds n
 // points and is used when n > 4096.  roots comes from fft64_roots(n).
 hipError_t launch_fft64(const double2* in, double2* out, double2* temp, const double2* roots, uint32_t n,

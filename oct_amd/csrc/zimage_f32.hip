@@ -431,7 +431,7 @@ hipError_t launch_zimage_rope_table(const float* coords, float2* tab, int T, hip
 
 hipError_t launch_zimage_norm(const float* x, const float* w, float* out, int T, int D, float eps, hipStream_t stream) {
   hipLaunchKernelGGL(rows::norm_mod_kernel<float>, rows::row_groups<4>(T), dim3(256), 0, stream, x, w, (const float*)nullptr,
-                     out, T, D, eps);
+                     out, T, D, eps, 0);
   return hipGetLastError();
 }
 
@@ -508,7 +508,7 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
       PROM_STEP(hipGetLastError());
     }
     if ((e = mark(1)) != hipSuccess) return e;
-    hipLaunchKernelGGL(rows::norm_mod_kernel<float>, rows::row_groups<4>(T), dim3(256), 0, st, x, w.attn_norm1, scaleA, A, T, D, eps);
+    hipLaunchKernelGGL(rows::norm_mod_kernel<float>, rows::row_groups<4>(T), dim3(256), 0, st, x, w.attn_norm1, scaleA, A, T, D, eps, 0);
     PROM_STEP(hipGetLastError());
     if ((e = mark(2)) != hipSuccess) return e;
     PROM_STEP(launch_sgemm_f32_ex(A, D, w.w_qkv, 3 * D, qkv, 3 * D, T, 3 * D, D, nullptr, 0, st, nullptr));
@@ -547,7 +547,7 @@ hipError_t enqueue_zimage_block_f32(const ZImageBlockWeights& w, const float* x,
     PROM_STEP(launch_sgemm_f32_ex(O, D, w.w_out, D, proj, D, T, D, D, nullptr, 0, st, nullptr));
     if ((e = mark(8)) != hipSuccess) return e;
     hipLaunchKernelGGL(rows::resid_norm_mod_kernel<float>, rows::row_groups<8>(T), dim3(512), 0, st, x, proj, w.attn_norm2, gateA,
-                       w.ffn_norm1, scaleM, R, Fm, T, D, eps);
+                       w.ffn_norm1, scaleM, R, Fm, T, D, eps, 0);
     PROM_STEP(hipGetLastError());
     if ((e = mark(9)) != hipSuccess) return e;
   }
