@@ -139,6 +139,25 @@ def test_dit_block_score_bound_paths(gpu_runtime, qk_gain):
     assert err <= BF16_BLOCK
 
 
+def test_dit_block_mixed_operand_layouts(gpu_runtime):
+    """T = 1696: the QKV and W1|W3 GEMMs run on the four-stage kernel and read
+    their left operands K-blocked (written so by the row kernels), while the
+    output and down projections take other kernels and read rows (the
+    attention output and the SwiGLU output stay row-major)."""
+    grid, text, heads, F, C = (40, 40), 96, 30, 10240, 256
+    T = grid[0] * grid[1] + text
+    D = heads * 128
+    x, cond, w = blocks.make_dit_block(13, T, D, F, C)
+    coords = blocks.joint_coordinates(grid[0], grid[1], text)
+    rc, res, out = gpu_runtime.dit_block_bf16(x, coords, cond, w, heads=heads)
+    assert rc == p.PROM_OK, (res.stage, res.detail_code)
+    rows = np.unique(np.linspace(0, T - 1, 48).astype(int))
+    ref = blocks.dit_block_bf16(x, coords, cond, w, heads, rows=rows)
+    err = oracle.normwise_rel_err(out[rows], ref)
+    print(f"T={T}: normwise rel err {err:.3e} over {len(rows)} rows", flush=True)
+    assert err <= BF16_BLOCK
+
+
 def test_dit_block_c5_full(gpu_runtime):
     """hidden 3840, 30 x 128 heads, FFN 10240, 4096 image + 128 text tokens."""
     grid, text, heads, F, C = (64, 64), 128, 30, 10240, 256
