@@ -10,7 +10,9 @@
 // downloads.  Four host threads (the caller and three workers) copy
 // pageable <-> pinned at 70-95 GB/s; the pipelined upload measured 47 GB/s.
 // Copies below kPipeMin bytes, or when pinned memory is unavailable, keep
-// hipMemcpyAsync.  Nothing here changes what is copied, only how.
+// hipMemcpyAsync.  host_memcpy lends the same threads to the async and batch
+// entries' copies between caller buffers and their own pinned staging.
+// Nothing here changes what is copied, only how.
 #include <string.h>
 
 #include <condition_variable>
@@ -139,6 +141,12 @@ Pipe& pipe() {
 }
 
 }  // namespace
+
+void host_memcpy(void* dst, const void* src, size_t bytes) {
+  Pipe& p = pipe();
+  std::lock_guard<std::mutex> g(p.mu);
+  p.pool.copy(static_cast<char*>(dst), static_cast<const char*>(src), bytes);
+}
 
 hipError_t upload_host(void* dst, const void* src, size_t bytes, hipStream_t stream) {
   Pipe& p = pipe();

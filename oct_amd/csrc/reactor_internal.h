@@ -118,6 +118,8 @@ void* staging(uint32_t slot, size_t bytes);
 // returns once `src` has been read (the device side completes in stream
 // order); download_host returns once `dst` holds the data.
 hipError_t upload_host(void* dst, const void* src, size_t bytes, hipStream_t stream);
+// memcpy between host buffers on the same host threads (1 MiB and more).
+void host_memcpy(void* dst, const void* src, size_t bytes);
 hipError_t download_host(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
 // Unconsumed async tasks of a runtime (READY and FAILED count until consumed

@@ -460,8 +460,7 @@ int batch_execute(Runtime* rt, const PrometheusSgemmBatchEntry* entries, uint32_
       float* dc = reinterpret_cast<float*>(arena + off);
       off += align256(cb);
       const uint32_t lane = batch_lane(i, count, planned, flags);
-      if (hipMemcpyAsync(da, e.a, ab, hipMemcpyHostToDevice, cx.stream) != hipSuccess ||
-          hipMemcpyAsync(db, e.b, bb, hipMemcpyHostToDevice, cx.stream) != hipSuccess) {
+      if (upload_host(da, e.a, ab, cx.stream) != hipSuccess || upload_host(db, e.b, bb, cx.stream) != hipSuccess) {
         (void)hipGetLastError();
         failed = true;
         failed_entry = i;
@@ -565,7 +564,7 @@ int batch_execute(Runtime* rt, const PrometheusSgemmBatchEntry* entries, uint32_
   }
   // Ordered commit (reactor_batch.c:538-541).
   for (uint32_t i = 0; i < count; ++i) {
-    memcpy(entries[i].c, reinterpret_cast<const char*>(st->batch_host) + host_offsets[i],
+    host_memcpy(entries[i].c, reinterpret_cast<const char*>(st->batch_host) + host_offsets[i],
            (size_t)entries[i].m * entries[i].n * sizeof(float));
     if (i < 64u) d.m31_commit_order[i] = i;
   }
@@ -677,8 +676,8 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_submit_async(void* handle,
     return PROM_ERROR;
   }
   // The caller's inputs are captured now; the device work runs after return.
-  memcpy(s.host_in, a, ab);
-  memcpy(reinterpret_cast<char*>(s.host_in) + align256(ab), b, bb);
+  host_memcpy(s.host_in, a, ab);
+  host_memcpy(reinterpret_cast<char*>(s.host_in) + align256(ab), b, bb);
   char* dev = static_cast<char*>(s.dev);
   float* da = reinterpret_cast<float*>(dev);
   float* db = reinterpret_cast<float*>(dev + align256(ab));
@@ -838,7 +837,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_sgemm_consume_async(void* handle
     set_status(out_stage, out_detail_code, PROM_STAGE_TRANSFER_OUT, PROM_DETAIL_ASYNC_FAILED);
     return PROM_ERROR;
   }
-  memcpy(c, s->host_out, (size_t)required * sizeof(float));
+  host_memcpy(c, s->host_out, (size_t)required * sizeof(float));
   t->lifecycle = PROM_ASYNC_STATE_CONSUMED;
   s->state = PROM_ASYNC_PHYSICAL_EMPTY;
   rt->successes++;
