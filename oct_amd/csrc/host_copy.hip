@@ -143,15 +143,20 @@ Pipe& pipe() {
 }  // namespace
 
 void host_memcpy(void* dst, const void* src, size_t bytes) {
+  if (bytes < kParallelMin) {
+    memcpy(dst, src, bytes);
+    return;
+  }
   Pipe& p = pipe();
   std::lock_guard<std::mutex> g(p.mu);
   p.pool.copy(static_cast<char*>(dst), static_cast<const char*>(src), bytes);
 }
 
 hipError_t upload_host(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+  if (bytes < kPipeMin) return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream);
   Pipe& p = pipe();
   std::lock_guard<std::mutex> g(p.mu);
-  if (bytes < kPipeMin || !p.init()) return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream);
+  if (!p.init()) return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream);
   const char* s8 = static_cast<const char*>(src);
   char* d8 = static_cast<char*>(dst);
   int s = 0;
@@ -170,12 +175,14 @@ hipError_t upload_host(void* dst, const void* src, size_t bytes, hipStream_t str
 }
 
 hipError_t download_host(void* dst, const void* src, size_t bytes, hipStream_t stream) {
-  Pipe& p = pipe();
-  std::lock_guard<std::mutex> g(p.mu);
-  if (bytes < kPipeMin || !p.init()) {
+  auto direct = [&] {
     const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream);
     return e != hipSuccess ? e : hipStreamSynchronize(stream);
-  }
+  };
+  if (bytes < kPipeMin) return direct();
+  Pipe& p = pipe();
+  std::lock_guard<std::mutex> g(p.mu);
+  if (!p.init()) return direct();
   const char* s8 = static_cast<const char*>(src);
   char* d8 = static_cast<char*>(dst);
   const size_t chunks = (bytes + kPipeChunk - 1) / kPipeChunk;

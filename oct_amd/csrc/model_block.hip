@@ -601,10 +601,10 @@ bool alloc_set(ModelBlock* b, WeightSet* s) {
 hipError_t upload_one(ModelBlock* b, WeightSet* s, uint32_t i, const PrometheusModelBlockWeightUpload& u) {
   hipStream_t st = ctx().stream;
   if (b->program == kProgProof)
-    return hipMemcpyAsync(s->buf[i], u.bytes, (size_t)u.byte_count, hipMemcpyHostToDevice, st);
+    return upload_host(s->buf[i], u.bytes, (size_t)u.byte_count, st);
   const int slot = slot_of(b, i);
   const SlotShape& sh = kSlots[slot];
-  hipError_t e = hipMemcpyAsync(b->staging, u.bytes, (size_t)u.byte_count, hipMemcpyHostToDevice, st);
+  hipError_t e = upload_host(b->staging, u.bytes, (size_t)u.byte_count, st);
   if (e != hipSuccess) return e;
   float* dst = static_cast<float*>(s->buf[sh.owner]) + sh.col0;
   e = launch_widen_f16(static_cast<const uint16_t*>(b->staging), dst, sh.rows, sh.cols, sh.ld, st);
@@ -1038,7 +1038,7 @@ bool copy_out(float* dst, const float* src, size_t rows, size_t cols, size_t src
   hipStream_t st = ctx().stream;
   hipError_t e;
   if (cols == src_ld)
-    e = hipMemcpyAsync(dst, src, rows * cols * 4, hipMemcpyDeviceToHost, st);
+    e = download_host(dst, src, rows * cols * 4, st);
   else
     e = hipMemcpy2DAsync(dst, cols * 4, src, src_ld * 4, cols * 4, rows, hipMemcpyDeviceToHost, st);
   return e == hipSuccess && hipStreamSynchronize(st) == hipSuccess;
@@ -1138,8 +1138,7 @@ int noise_external(Runtime* rt, uint64_t id, const PrometheusNoiseRefiner0Execut
   b->audit_valid = false;
   const uint64_t t0 = wall_ns();
   hipStream_t st = ctx().stream;
-  if (hipMemcpyAsync(b->x_bf16, r->model_input_bf16, (size_t)r->model_input_bytes, hipMemcpyHostToDevice, st) !=
-          hipSuccess ||
+  if (upload_host(b->x_bf16, r->model_input_bf16, (size_t)r->model_input_bytes, st) != hipSuccess ||
       hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st) !=
           hipSuccess ||
       launch_widen_bf16(b->x_bf16, b->x, (size_t)kImageTokens * kWidth, st) != hipSuccess ||
@@ -1548,8 +1547,7 @@ int m1b_execute(Runtime* rt, uint64_t id, const PrometheusModelBlockM1BExecuteRe
   b->resident_input_generation = 0;  // the ingress buffer is also the resident boundary
   const uint64_t t0 = wall_ns();
   hipStream_t st = ctx().stream;
-  if (hipMemcpyAsync(b->x_bf16, r->model_input_bf16, (size_t)r->model_input_bytes, hipMemcpyHostToDevice, st) !=
-          hipSuccess ||
+  if (upload_host(b->x_bf16, r->model_input_bf16, (size_t)r->model_input_bytes, st) != hipSuccess ||
       hipMemcpyAsync(b->cond_bf16, r->timestep_bf16, (size_t)r->timestep_bytes, hipMemcpyHostToDevice, st) !=
           hipSuccess ||
       launch_widen_bf16(b->x_bf16, b->x, (size_t)kImageTokens * kWidth, st) != hipSuccess ||
@@ -2163,7 +2161,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute(void* handle
     }
     hipStream_t st = ctx().stream;
     (void)hipEventRecord(b->ev_begin, st);
-    hipError_t e = hipMemcpyAsync(b->proof_in, r->input, (size_t)bytes, hipMemcpyHostToDevice, st);
+    hipError_t e = upload_host(b->proof_in, r->input, (size_t)bytes, st);
     if (e == hipSuccess) {
       const unsigned blocks = (unsigned)std::min<uint64_t>(4096, (r->element_count + 255) / 256);
       hipLaunchKernelGGL(proof_kernel, dim3(blocks), dim3(256), 0, st, b->proof_in, b->proof_out, r->element_count,
@@ -2189,7 +2187,7 @@ PROM_REACTOR_API int prometheus_reactor_runtime_model_block_execute(void* handle
       fill_evidence(b, b->last_detail, out_evidence);
       return PROM_ERROR;
     }
-    e = hipMemcpyAsync(r->output, b->proof_out, (size_t)b->ext_out, hipMemcpyDeviceToHost, st);
+    e = download_host(r->output, b->proof_out, (size_t)b->ext_out, st);
     if (e == hipSuccess && r->audit_enabled)
       e = hipMemcpyAsync(r->audit_output, b->proof_audit, (size_t)b->declared_audit, hipMemcpyDeviceToHost, st);
     if (e != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
