@@ -71,3 +71,27 @@ def test_alternating_host_calls(gpu_runtime):
         row = x[-1].astype(np.float64)
         e = np.exp(row - row.max())
         assert oracle.normwise_rel_err(y[-1], e / e.sum()) <= 1e-5
+
+
+def test_async_and_batch_copies_equal_device(gpu_runtime):
+    """The async entry's copies into and out of its pinned staging and the
+    batch's uploads (over 4 MiB: the pinned ring) leave the results exactly
+    those of the device entry."""
+    rt = gpu_runtime
+    m, n, k = 1037, 2049, 1531
+    a = oracle.uniform(501, (m, k))
+    b = oracle.uniform(502, (k, n))
+    want = _device_sgemm(rt, a, b)
+    rc, task, _ = rt.submit_async(m, n, k, a, b)
+    assert rc == p.PROM_OK
+    st = rt.wait_async(task)
+    assert st.lifecycle_state == p.ASYNC_READY
+    out = np.empty((m, n), np.float32)
+    rc, _ = rt.consume_async(task, out)
+    assert rc == p.PROM_OK
+    np.testing.assert_array_equal(out, want)
+    a2 = oracle.uniform(503, (m, k))
+    rc, _, outs = rt.sgemm_batch([(a, b), (a2, b)])
+    assert rc == p.PROM_OK
+    np.testing.assert_array_equal(outs[0], want)
+    np.testing.assert_array_equal(outs[1], _device_sgemm(rt, a2, b))
