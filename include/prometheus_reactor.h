@@ -920,8 +920,9 @@ enum {
   PROM_BATCH_FLAG_TEST_DUAL_FAIL_FIRST_TWO = 1u << 22,
   PROM_BATCH_FLAG_TEST_DELAY_ENTRY0 = 1u << 23,
   PROM_BATCH_FLAG_TEST_FAIL_ENTRY_SHIFT = 24u,
-  PROM_BATCH_FLAG_TEST_FAIL_ENTRY_MASK = 0xFFu << 24u,
 };
+/* Above INT_MAX, so a macro: ISO C limits enumerators to int. */
+#define PROM_BATCH_FLAG_TEST_FAIL_ENTRY_MASK 0xFF000000u
 
 /* reactor_api.h:1476-1545 (the values this library reports) */
 enum { PROM_BATCH_PARTITION_ROUND_ROBIN = 1u, PROM_BATCH_PARTITION_CONTIGUOUS = 2u };

@@ -124,7 +124,27 @@ def build_oracle(verbose: bool = False) -> Path:
     return path
 
 
+CBRIDGE_DIR = PKG_DIR / "cbridge"
+CBRIDGE_CHECK = CBRIDGE_DIR / "bridge_check"
+CBRIDGE_FLAGS = ["-std=c11", "-O2", "-Wall", "-Wextra", "-Wpedantic", "-Werror", f"-I{REPO_DIR / 'include'}"]
+
+
+def build_cbridge(verbose: bool = False, out: Path = CBRIDGE_CHECK) -> Path:
+    """Compile the C loader (``cbridge/prom_bridge.c``) with its check program.
+
+    Plain gcc, no HIP: the loader only dlopens the reactor library."""
+    cmd = ["gcc", *CBRIDGE_FLAGS, str(CBRIDGE_DIR / "prom_bridge.c"), str(CBRIDGE_DIR / "bridge_check.c"),
+           "-o", str(out), "-ldl", "-lm"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"C bridge build failed:\n{proc.stdout}\n{proc.stderr}")
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 if __name__ == "__main__":
     build_reactor(verbose=True)
+    build_cbridge(verbose=True)
     build_oracle(verbose=True)
     sys.exit(0)
