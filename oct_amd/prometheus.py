@@ -825,6 +825,18 @@ class ReactorIssue(RuntimeError):
     def __init__(self, code: str, message: str):
         super().__init__(f"{code}: {message}")
         self.code = code
+        self.message = message
+
+
+class StrictExecutionError(ReactorIssue):
+    """strict.go:11-32's error.  Its text is the message alone
+    ("PROMETHEUS requires GPU matrix execution: ..."), as the Go code's
+    fmt.Errorf words it, so an interpreter can print it unchanged."""
+
+    def __init__(self, message: str):
+        RuntimeError.__init__(self, message)
+        self.code = "strict"
+        self.message = message
 
 
 def stage_name(stage: int) -> str:
@@ -1620,15 +1632,15 @@ def run_compiled_matmul_mm_strict(left, right) -> Tuple[list, str]:
     try:
         rt = NativeRuntime()
     except ReactorIssue as exc:
-        raise ReactorIssue("strict", f"PROMETHEUS requires GPU matrix execution: {exc}") from exc
+        raise StrictExecutionError(f"PROMETHEUS requires GPU matrix execution: {exc.message}") from exc
     with rt:
         try:
             rt.require_hardware_gpu()
         except ReactorIssue as exc:
-            raise ReactorIssue("strict", f"PROMETHEUS requires GPU matrix execution: {exc}") from exc
+            raise StrictExecutionError(f"PROMETHEUS requires GPU matrix execution: {exc.message}") from exc
         try:
             out, status = rt.sgemm(m, n, k, a, b)
         except ReactorIssue as exc:
-            raise ReactorIssue("strict", f"PROMETHEUS requires GPU matrix execution: {exc}") from exc
+            raise StrictExecutionError(f"PROMETHEUS requires GPU matrix execution: {exc.message}") from exc
         env = rt.environment()
     return out.reshape(m, n).astype(np.float64).tolist(), env
