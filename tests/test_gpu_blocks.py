@@ -45,6 +45,23 @@ def test_decoder_layer_c4_gemma2b(gpu_runtime):
     np.testing.assert_array_equal(out2[:T // 2], out[:T // 2])
 
 
+@pytest.mark.parametrize("T,D,Hq,F", [(45, 256, 8, 512), (200, 512, 16, 512), (1000, 256, 8, 256)])
+def test_decoder_layer_head_dim_256_shared_kv(gpu_runtime, T, D, Hq, F):
+    """Head dim 256 with the query heads in eights on the one K/V head takes the
+    16-query-wave attention kernel: ragged T (partial key tiles, query rows
+    past T), two head groups, and key splits of one to two tiles, so the
+    combine merges up to 32 splits per token."""
+    d = 256
+    x, w = blocks.make_decoder_layer(T + Hq, T, D, Hq, d, F)
+    rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
+    assert rc == p.PROM_OK and res.output_written == 1, (res.stage, res.detail_code)
+    ref = blocks.decoder_layer_f32(x, w, Hq, d)
+    err = oracle.normwise_rel_err(out, ref)
+    row_err = np.linalg.norm(out - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    print(f"T={T} Hq={Hq}: normwise rel err {err:.3e}, worst row {row_err.max():.3e}", flush=True)
+    assert err <= F32_BLOCK and row_err.max() <= F32_BLOCK
+
+
 def test_decoder_layer_tail_rows(gpu_runtime):
     """Gemma-2B widths at T = 1056: the output projection and the down
     projection (both adding the residual) run their last 32 rows as a second,
