@@ -10,8 +10,10 @@
 // MI355X design: every matrix product is the fp32 MFMA SGEMM
 // (sgemm_f32.hip) on row-major operands with strides:
 //   1 RMSNorm                       x -> n1                        (reduction.hip)
-//   2 QKV projection, fused         n1 @ Wqkv -> qkv [T, (Hq+2)d]
-//   3 RoPE + split                  qkv -> Q [T, Hq*d] (scaled by 1/sqrt d, exact
+//   2 QKV projection, fused         n1 @ Wqkv -> qkv [T, (Hq+2)d], or its K-split
+//                                   slices left unreduced
+//   3 RoPE + split                  qkv (or the slices, added in slice order) ->
+//                                   Q [T, Hq*d] (scaled by 1/sqrt d, exact
 //                                   power of two), K^T [d, T], V [T, d]
 //   4 causal flash attention        Q, K^T, V -> O [T, Hq*d] (attention_f32.hip:
 //     the query heads of a workgroup share each K/V tile; no score matrix;
@@ -24,6 +26,7 @@
 //  10 GeGLU                         gelu_tanh(G[:, :F]) * G[:, F:] -> A [T, F]
 //  11 down projection + residual    h + A @ Wdown -> out
 #include <math.h>
+#include <algorithm>
 #include <string.h>
 
 #include "reactor_internal.h"
@@ -63,6 +66,74 @@ __global__ __launch_bounds__(256) void gemma_rope_split_kernel(const float* __re
     const int t = idx / d;
     const int j = idx - t * d;
     V[(size_t)t * d + j] = qkv[(size_t)t * ldq + (Hq + 1) * d + j];
+  }
+}
+
+// The same split, one token per workgroup, reading the QKV projection as
+// `slices` K-split slices `slab` floats apart (1: the reduced product) and
+// adding them in slice order, as the split-K reduce does.  The token's
+// angles are evaluated once into LDS (half * 8 bytes).
+constexpr int kRopeMaxSlices = 4;
+
+__device__ __forceinline__ float add_slices(const float* __restrict__ P, size_t off, int slices, size_t slab) {
+  float p[kRopeMaxSlices];
+#pragma unroll
+  for (int z = 0; z < kRopeMaxSlices; ++z) p[z] = z < slices ? P[z * slab + off] : 0.0f;
+  float v = p[0];
+#pragma unroll
+  for (int z = 1; z < kRopeMaxSlices; ++z)
+    if (z < slices) v += p[z];
+  return v;
+}
+
+__global__ __launch_bounds__(256) void qkv_rope_split_kernel(const float* __restrict__ P, int ldq, int slices,
+                                                             size_t slab, int Hq, int d, int pos0, float base,
+                                                             float q_scale, float* __restrict__ Q,
+                                                             float* __restrict__ Kt, int ldkt, float* __restrict__ V) {
+  extern __shared__ float2 rope_cs[];  // [half] (cos, sin) of this token
+  const int half = d >> 1;
+  const int t = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
+  for (int i = tid; i < half; i += 256) {
+    // angle = position * base^(-2i/d), evaluated in binary64 then rounded.
+    const double inv_freq = pow((double)base, -2.0 * (double)i / (double)d);
+    const double angle = (double)(pos0 + t) * inv_freq;
+    rope_cs[i] = make_float2((float)cos(angle), (float)sin(angle));
+  }
+  const float* row = P + (size_t)t * ldq;
+  // V and the K pairs need no angle: load them before the barrier.
+  for (int j = tid; j < d; j += 256) V[(size_t)t * d + j] = add_slices(row, (size_t)(Hq + 1) * d + j, slices, slab);
+  __syncthreads();
+  for (int i = tid; i < half; i += 256) {
+    const float k1 = add_slices(row, (size_t)Hq * d + i, slices, slab);
+    const float k2 = add_slices(row, (size_t)Hq * d + i + half, slices, slab);
+    const float c = rope_cs[i].x, sn = rope_cs[i].y;
+    Kt[(size_t)i * ldkt + t] = k1 * c - k2 * sn;
+    Kt[(size_t)(i + half) * ldkt + t] = k2 * c + k1 * sn;
+  }
+  // Q: the pairs (i, i + half) of every head, four per thread per pass.
+  const int qpairs = Hq * half;
+  float* qrow = Q + (size_t)t * Hq * d;
+  for (int e0 = tid; e0 < qpairs; e0 += 4 * 256) {
+    float x1[4], x2[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = min(e0 + 256 * u, qpairs - 1);
+      const int h = e / half;
+      const size_t col = (size_t)h * d + (e - h * half);
+      x1[u] = add_slices(row, col, slices, slab);
+      x2[u] = add_slices(row, col + half, slices, slab);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = e0 + 256 * u;
+      if (e >= qpairs) break;
+      const int h = e / half;
+      const int i = e - h * half;
+      const float c = rope_cs[i].x, sn = rope_cs[i].y;
+      qrow[h * d + i] = (x1[u] * c - x2[u] * sn) * q_scale;
+      qrow[h * d + i + half] = (x2[u] * c + x1[u] * sn) * q_scale;
+    }
   }
 }
 
@@ -122,14 +193,22 @@ struct LayerShape {
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// The RoPE split's LDS (one token's angles) fits.
+bool rope_fused(const LayerShape& s) { return (size_t)s.d / 2 * sizeof(float2) <= 32768; }
+
 // Workspace layout: n1 [T,D] | qkv [T,nqkv] | Q [T,Hq*d] | Kt [d,ldkt] | V [T,d]
 // | attention partials (or S [T*Hq,T]) | O [T,Hq*d] | h [T,D] | n2 [T,D] | G [T,2F] | A [T,F]
 size_t layer_workspace_bytes(const LayerShape& s, size_t offsets[11]) {
   // Slot 5: the key-split partials of the flash attention (often none), or
   // the [T*Hq, T] score matrix of the unfused path for other head dims.
-  const size_t attn_bytes = flash_attn_f32_supported(s.d)
-                                ? flash_attn_f32_partial_bytes(s.T, s.Hq, s.Hq, s.d, 1)
-                                : (size_t)s.T * s.Hq * s.T * sizeof(float);
+  // The QKV projection's unreduced K-split slices live here first: the RoPE
+  // split consumes them before the attention writes its partials.
+  size_t attn_bytes = flash_attn_f32_supported(s.d) ? flash_attn_f32_partial_bytes(s.T, s.Hq, s.Hq, s.d, 1)
+                                                    : (size_t)s.T * s.Hq * s.T * sizeof(float);
+  if (rope_fused(s)) {
+    const int slices = sgemm_f32_unreduced_slices(s.D, s.nqkv, s.T, s.nqkv, s.D, kRopeMaxSlices);
+    if (slices > 1) attn_bytes = std::max(attn_bytes, (size_t)slices * s.T * s.nqkv * sizeof(float));
+  }
   const size_t sizes[11] = {(size_t)s.T * s.D * 4,        (size_t)s.T * s.nqkv * 4, (size_t)s.T * s.Hq * s.d * 4,
                             (size_t)s.d * s.ldkt() * 4,   (size_t)s.T * s.d * 4,    attn_bytes,
                             (size_t)s.T * s.Hq * s.d * 4, (size_t)s.T * s.D * 4,    (size_t)s.T * s.D * 4,
@@ -185,10 +264,22 @@ hipError_t enqueue_layer(const PrometheusDecoderLayerF32Request* r, char* ws, co
     ++n;                            \
   } while (0)
   PROM_STEP(launch_rmsnorm(r->input, r->attn_norm_weight, n1, nullptr, s.T, s.D, s.D, r->rms_epsilon, st));
-  PROM_STEP(launch_sgemm_f32_ex(n1, s.D, r->w_qkv, s.nqkv, qkv, s.nqkv, s.T, s.nqkv, s.D, nullptr, 0, st, nullptr));
-  {
+  const float q_scale = 1.0f / sqrtf((float)s.d);
+  if (rope_fused(s)) {
+    // The QKV projection's K-split slices (if any) go to slot 5 unreduced and
+    // the RoPE split adds them: one launch and one [T, nqkv] round trip fewer.
+    int slices = 1;
+    const size_t slot5 = off[6] - off[5];
+    PROM_STEP(launch_sgemm_f32_unreduced(n1, s.D, r->w_qkv, s.nqkv, qkv, s.nqkv, s.T, s.nqkv, s.D, S,
+                                         slot5 / sizeof(float), kRopeMaxSlices, st, &slices));
+    const float* src = slices > 1 ? S : qkv;
+    hipLaunchKernelGGL(qkv_rope_split_kernel, dim3(s.T), dim3(256), (size_t)s.d / 2 * sizeof(float2), st, src,
+                       s.nqkv, slices, (size_t)s.T * s.nqkv, s.Hq, s.d, (int)r->position_offset, r->rope_base,
+                       q_scale, Q, Kt, s.ldkt(), V);
+    PROM_STEP(hipGetLastError());
+  } else {
+    PROM_STEP(launch_sgemm_f32_ex(n1, s.D, r->w_qkv, s.nqkv, qkv, s.nqkv, s.T, s.nqkv, s.D, nullptr, 0, st, nullptr));
     const int threads = s.T * s.d;  // covers T*d/2 rope pairs and T*d V elements
-    const float q_scale = 1.0f / sqrtf((float)s.d);
     hipLaunchKernelGGL(gemma_rope_split_kernel, dim3((threads + 255) / 256), dim3(256), 0, st, qkv, s.nqkv, s.T, s.Hq,
                        s.d, (int)r->position_offset, r->rope_base, q_scale, Q, Kt, s.ldkt(), V);
     PROM_STEP(hipGetLastError());

@@ -156,6 +156,18 @@ hipError_t launch_sgemm_f32(const float* a, const float* b, float* c, uint32_t m
 hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb, float* c, int ldc, uint32_t m,
                                uint32_t n, uint32_t k, const float* residual, int ldr, hipStream_t stream,
                                int* path_detail);
+// C = A @ B with the K-split slices left unreduced for a consumer that adds
+// them itself: when the product's schedule is one K-split product of at most
+// max_slices slices (no GEMV, padded copies or tail split) and `partial` holds
+// them, slice z goes to partial + z*m*n ([m, n], row pitch n), *slices is set
+// and nothing is written to c; otherwise c is computed in full and *slices is
+// 1.  The slices are those launch_sgemm_f32_ex's reduce would add, in the
+// same plan, so adding them in slice order reproduces its output bit for bit.
+hipError_t launch_sgemm_f32_unreduced(const float* a, int lda, const float* b, int ldb, float* c, int ldc,
+                                      uint32_t m, uint32_t n, uint32_t k, float* partial, size_t partial_floats,
+                                      int max_slices, hipStream_t stream, int* slices);
+// The slices launch_sgemm_f32_unreduced leaves for 16-byte aligned operands (1: none).
+int sgemm_f32_unreduced_slices(int lda, int ldb, uint32_t m, uint32_t n, uint32_t k, int max_slices);
 // H[m, f] = gelu_tanh(A @ W[:, :f]) * (A @ W[:, f:]) for W = [gate | up]
 // ([k, 2f], row pitch 2f): one launch of the 128x128 direct-to-LDS kernel
 // whose tiles take 64 gate and the matching 64 up columns.  Returns

@@ -1077,7 +1077,8 @@ void launch_tile(bool buf, bool vec, dim3 grid, hipStream_t stream, const float*
 // without split) and, when split, the reduce into c (partial: splits*m*n floats).
 hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long sa, const float* b, int ldb,
                           long long sb, float* c, int ldc, long long sc, uint32_t m, uint32_t n, uint32_t k,
-                          uint32_t batch, const float* residual, int ldr, float* partial, hipStream_t stream) {
+                          uint32_t batch, const float* residual, int ldr, float* partial, hipStream_t stream,
+                          bool reduce = true) {
   const bool split = p.splits > 1;
   const bool vec = (k % 4 == 0) && (n % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) && (sa % 4 == 0) &&
                    (sb % 4 == 0) && aligned16(a) && aligned16(b);
@@ -1134,7 +1135,7 @@ hipError_t run_sgemm_plan(const SgemmPlan& p, const float* a, int lda, long long
                            ldo, res, ldr, p.k_len, sa, sb, sc);
       break;
   }
-  if (split) {
+  if (split && reduce) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const bool vec4 = n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && (residual == nullptr || (ldr % 4 == 0 && aligned16(residual)));
@@ -1307,6 +1308,25 @@ hipError_t launch_sgemm_f32_ex(const float* a, int lda, const float* b, int ldb,
       schedule_sgemm(aligned16(a) && aligned16(b), lda, ldb, m, n, k, residual != nullptr, ~0ull);
   if (path_detail) *path_detail = s.gemv ? PROM_DETAIL_PATH_HIP_GEMV_F32 : PROM_DETAIL_PATH_HIP_MFMA_F32;
   return run_sgemm_schedule(s, a, lda, b, ldb, c, ldc, m, n, k, residual, ldr, nullptr, nullptr, stream);
+}
+
+int sgemm_f32_unreduced_slices(int lda, int ldb, uint32_t m, uint32_t n, uint32_t k, int max_slices) {
+  const SgemmSchedule s = schedule_sgemm(true, lda, ldb, m, n, k, false, ~0ull);
+  if (s.gemv || s.repack || s.tail_split || s.plan[0].splits <= 1 || s.plan[0].splits > max_slices) return 1;
+  return s.plan[0].splits;
+}
+
+hipError_t launch_sgemm_f32_unreduced(const float* a, int lda, const float* b, int ldb, float* c, int ldc,
+                                      uint32_t m, uint32_t n, uint32_t k, float* partial, size_t partial_floats,
+                                      int max_slices, hipStream_t stream, int* slices) {
+  *slices = 1;
+  const SgemmSchedule s = schedule_sgemm(aligned16(a) && aligned16(b), lda, ldb, m, n, k, false, ~0ull);
+  if (s.gemv || s.repack || s.tail_split || s.plan[0].splits <= 1 || s.plan[0].splits > max_slices ||
+      partial == nullptr || (uint64_t)s.plan[0].splits * m * n > partial_floats)
+    return run_sgemm_schedule(s, a, lda, b, ldb, c, ldc, m, n, k, nullptr, 0, nullptr, nullptr, stream);
+  *slices = s.plan[0].splits;
+  return run_sgemm_plan(s.plan[0], a, lda, 0, b, ldb, 0, c, ldc, 0, m, n, k, 1, nullptr, 0, partial, stream,
+                        false);
 }
 
 }  // namespace prom
