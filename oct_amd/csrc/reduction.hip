@@ -47,8 +47,10 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   return v;
 }
 
-// Register-resident path: width % 4 == 0, width <= 256 * kChunks.
-template <uint32_t kOp, int kChunks>
+// Register-resident path: width % 4 == 0, width <= 256 * kChunks.  kPreW
+// (RMSNorm of few rows, where each wave's memory latency is the cost): the
+// weight chunks load with the row, before the reduction, instead of after it.
+template <uint32_t kOp, int kChunks, bool kPreW = false>
 __global__ __launch_bounds__(256) void row_resident_kernel(const float* __restrict__ in, const float* __restrict__ w,
                                                            float* __restrict__ out, float* __restrict__ aux,
                                                            uint32_t rows, uint32_t width, float eps) {
@@ -133,6 +135,15 @@ __global__ __launch_bounds__(256) void row_resident_kernel(const float* __restri
       }
     }
   } else {  // RMSNorm
+    const floatx4* w4p = reinterpret_cast<const floatx4*>(w);
+    floatx4 g[kPreW ? kChunks : 1];
+    if constexpr (kPreW) {
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c) {
+        const uint32_t i = (uint32_t)c * 64u + lane;
+        if (i < w4) g[c] = w4p[i];
+      }
+    }
     double acc = 0.0;
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
@@ -145,18 +156,17 @@ __global__ __launch_bounds__(256) void row_resident_kernel(const float* __restri
     acc = wave_sum_f64(acc);
     const float sumsq = (float)acc;
     const float inv = 1.0f / sqrtf(sumsq / (float)width + eps);
-    const floatx4* w4p = reinterpret_cast<const floatx4*>(w);
     floatx4* dst = reinterpret_cast<floatx4*>(out + (size_t)row * width);
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
       const uint32_t i = (uint32_t)c * 64u + lane;
       if (i < w4) {
-        const floatx4 g = w4p[i];
+        const floatx4 gc = kPreW ? g[kPreW ? c : 0] : w4p[i];
         floatx4 o;
-        o.x = v[c].x * inv * g.x;
-        o.y = v[c].y * inv * g.y;
-        o.z = v[c].z * inv * g.z;
-        o.w = v[c].w * inv * g.w;
+        o.x = v[c].x * inv * gc.x;
+        o.y = v[c].y * inv * gc.y;
+        o.z = v[c].z * inv * gc.z;
+        o.w = v[c].w * inv * gc.w;
         dst[i] = o;
       }
     }
@@ -218,7 +228,13 @@ hipError_t dispatch(const float* in, const float* w, float* out, float* aux, uin
   if (resident && width <= 256u * 4u) {
     hipLaunchKernelGGL((row_resident_kernel<kOp, 4>), grid, block, 0, stream, in, w, out, aux, rows, width, eps);
   } else if (resident && width <= 256u * 16u) {
-    hipLaunchKernelGGL((row_resident_kernel<kOp, 16>), grid, block, 0, stream, in, w, out, aux, rows, width, eps);
+    // Few rows (a transformer layer's tokens): one wave per row leaves the
+    // chip mostly idle, so each wave's latency is the cost; preload the weights.
+    if (kOp == kOpRms && rows <= 2048u && width <= 256u * 8u)
+      hipLaunchKernelGGL((row_resident_kernel<kOp, 8, true>), grid, block, 0, stream, in, w, out, aux, rows, width,
+                         eps);
+    else
+      hipLaunchKernelGGL((row_resident_kernel<kOp, 16>), grid, block, 0, stream, in, w, out, aux, rows, width, eps);
   } else {
     hipLaunchKernelGGL((row_stream_kernel<kOp>), grid, block, 0, stream, in, w, out, aux, rows, width, stride, eps);
   }
