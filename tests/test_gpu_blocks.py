@@ -45,12 +45,14 @@ def test_decoder_layer_c4_gemma2b(gpu_runtime):
     np.testing.assert_array_equal(out2[:T // 2], out[:T // 2])
 
 
-@pytest.mark.parametrize("T,D,Hq,F", [(45, 256, 8, 512), (200, 512, 16, 512), (1000, 256, 8, 256)])
+@pytest.mark.parametrize("T,D,Hq,F", [(45, 256, 8, 512), (200, 512, 16, 512), (1000, 256, 8, 256),
+                                      (300, 256, 4, 256), (77, 256, 2, 256)])
 def test_decoder_layer_head_dim_256_shared_kv(gpu_runtime, T, D, Hq, F):
     """Head dim 256 with the query heads in eights on the one K/V head takes the
     16-query-wave attention kernel: ragged T (partial key tiles, query rows
     past T), two head groups, and key splits of one to two tiles, so the
-    combine merges up to 32 splits per token."""
+    combine merges up to 32 splits per token.  Four and two query heads take
+    the four-wave 32-query kernel, its key splits and the same combine."""
     d = 256
     x, w = blocks.make_decoder_layer(T + Hq, T, D, Hq, d, F)
     rc, res, out = gpu_runtime.decoder_layer_f32(x, w, q_heads=Hq, head_dim=d)
