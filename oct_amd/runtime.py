@@ -1,7 +1,10 @@
 """The non-strict SGEMM path of Oct's Prometheus package.
 
-Mirrors ``internal/prometheus/runtime.go:12-376``: ``RunSGEMM``,
-``RunCompiledMatMulMM`` and ``RunStarterCorpus`` over ``runSGEMMWithOutput``.
+Mirrors ``internal/prometheus/runtime.go:12-658``: ``RunSGEMM``,
+``RunCompiledMatMulMM`` and ``RunStarterCorpus`` over ``runSGEMMWithOutput``,
+the async hardware validation ``ValidateAsyncSGEMMOnHardware``, and the
+Octagon reports of both (``WriteOctagonReport``,
+``WriteAsyncValidationOctagon``; the writer is ``oct_amd.octagon``).
 Unlike the strict ``@`` (``run_compiled_matmul_mm_strict`` in
 ``oct_amd.prometheus``), this path always computes the fp32 CPU reference
 first, then runs the reactor and gates its output against that reference with
@@ -24,6 +27,7 @@ from typing import List, Optional, Sequence, Tuple
 
 import numpy as np
 
+from . import octagon
 from . import prometheus as p
 
 # runtime.go:12-15
@@ -67,9 +71,10 @@ class SGEMMRequest:
 
 @dataclass
 class CorrectnessResult:
-    """runtime.go:30-38."""
+    """runtime.go:30-38.  The zero value, as Go's, has not passed: a run that
+    stopped before the gate reports CorrectnessPass false."""
 
-    passed: bool = True
+    passed: bool = False
     max_abs_error: float = 0.0
     max_rel_error: float = 0.0
     failing_count: int = 0
@@ -139,7 +144,7 @@ def compare_against_oracle(expected: np.ndarray, actual: np.ndarray) -> Correctn
     when |e - a| (an fp32 difference) exceeds both the absolute and relative tolerance."""
     e = np.ascontiguousarray(expected, dtype=np.float32).reshape(-1)
     a = np.ascontiguousarray(actual, dtype=np.float32).reshape(-1)
-    res = CorrectnessResult()
+    res = CorrectnessResult(passed=True)
     finite = np.isfinite(e) & np.isfinite(a)
     with np.errstate(over="ignore", invalid="ignore"):
         diff = np.where(finite, e - a, np.float32(0)).astype(np.float32)
@@ -311,3 +316,167 @@ def run_starter_corpus(backend: str) -> List[SGEMMRunResult]:
             exc.runs = runs  # type: ignore[attr-defined]  (the report so far, as the Go code returns it)
             raise
     return runs
+
+
+# ---- Octagon reports (runtime.go:382-432, 497-566) ---------------------------
+def _octagon_failing_index(index: int) -> int:
+    """runtime.go:427-432: no failing element is written as 0."""
+    return 0 if index < 0 else index
+
+
+def _correctness_fields(c: CorrectnessResult) -> list:
+    return [("CorrectnessPass", bool(c.passed)), ("MaxAbsError", float(c.max_abs_error)),
+            ("MaxRelError", float(c.max_rel_error)), ("FailingElementCount", int(c.failing_count)),
+            ("FirstFailingIndex", _octagon_failing_index(int(c.first_failing_index))),
+            ("FirstExpectedValue", float(c.first_expected_value)),
+            ("FirstActualValue", float(c.first_actual_value))]
+
+
+def report_to_octagon(runs: Sequence[SGEMMRunResult]) -> octagon.Record:
+    """runtime.go:386-425 (reportToOctagon): a PrometheusSgemmReport of one
+    PrometheusSgemmRun record per run, fields in the reference's order."""
+    records = []
+    for r in runs:
+        records.append(octagon.Record("PrometheusSgemmRun", [
+            ("BackendRequested", r.requested_backend), ("BackendUsed", r.used_backend),
+            ("M", int(r.shape.m)), ("N", int(r.shape.n)), ("K", int(r.shape.k)),
+            ("Status", str(r.status)), ("DetailCode", int(r.detail_code)), ("DetailName", r.detail_name),
+            *_correctness_fields(r.correctness),
+            ("CPUTimeNs", int(r.cpu_time_ns)), ("VulkanTimeNs", int(r.vulkan_time_ns)), ("VulkanEnv", r.vulkan_env),
+            ("TimingMode", r.timing_mode), ("WallTimeNs", int(r.wall_time_ns)), ("Notes", r.notes)]))
+    return octagon.Record("PrometheusSgemmReport", [("Runs", records)])
+
+
+def write_octagon_report(path: str, runs: Sequence[SGEMMRunResult], prefix: str = "") -> str:
+    """runtime.go:382-384 (WriteOctagonReport)."""
+    return octagon.write(path, report_to_octagon(runs), prefix)
+
+
+_ASYNC_LIFECYCLE = {0: "idle", 1: "submitted", 2: "ready", 3: "failed", 4: "consumed"}
+
+
+def async_lifecycle_name(state: int) -> str:
+    """runtime.go:497-512."""
+    return _ASYNC_LIFECYCLE.get(state, f"state_{state}")
+
+
+@dataclass
+class AsyncValidationResult:
+    """runtime.go:60-81 (AsyncValidationResult), as ValidateAsyncSGEMMOnHardware
+    initialises it (runtime.go:585-596)."""
+
+    shape: Shape
+    requested_backend: str = BACKEND_PROMETHEUS
+    used_backend: str = BACKEND_PROMETHEUS
+    outcome: str = "error(init,-2)"
+    environment: str = "not_applicable"
+    submit_stage: str = "unknown"
+    submit_detail_code: int = 0
+    submit_detail_name: str = "not_applicable"
+    query_lifecycle: str = "idle"
+    query_ready: bool = False
+    query_failed: bool = False
+    query_consumed: bool = False
+    query_outstanding: int = 0
+    query_attempts: int = 0
+    consume_stage: str = "unknown"
+    consume_detail_code: int = 0
+    consume_detail_name: str = "not_applicable"
+    correctness: CorrectnessResult = field(default_factory=CorrectnessResult)
+    wall_time_ns: int = 0
+    notes: str = ""
+
+
+class AsyncValidationError(RuntimeError):
+    """An error return of ValidateAsyncSGEMMOnHardware; ``result`` is the record so far."""
+
+    def __init__(self, message: str, result: AsyncValidationResult):
+        super().__init__(message)
+        self.result = result
+
+
+def validate_async_sgemm_on_hardware(shape: Shape) -> AsyncValidationResult:
+    """runtime.go:585-658 (ValidateAsyncSGEMMOnHardware): one async SGEMM on
+    deterministic operands through submit, up to 2000 queries, consume, and
+    the correctness gate against the fp32 CPU reference.  Without a reactor
+    the result is ``skipped(prometheus_unavailable)`` (no error); a failed
+    step raises AsyncValidationError carrying the record."""
+    res = AsyncValidationResult(shape=shape)
+    a = deterministic_matrix(shape.m, shape.k)
+    b = deterministic_matrix(shape.k, shape.n)
+    reference, _ = _timed_cpu_sgemm(shape.m, shape.n, shape.k, a.reshape(-1), b.reshape(-1))
+    try:
+        rt = new_native_runtime()
+    except p.ReactorIssue as exc:
+        res.used_backend = BACKEND_CPU
+        res.environment = "unavailable"
+        res.outcome = "skipped(prometheus_unavailable)"
+        res.notes = str(exc)
+        return res
+    with rt:
+        res.environment = rt.environment()
+        t0 = time.perf_counter_ns()
+        rc, task, st = rt.submit_async(shape.m, shape.n, shape.k, a, b)
+        res.wall_time_ns = time.perf_counter_ns() - t0
+        res.submit_stage = p.stage_name(st.stage)
+        res.submit_detail_code = st.detail
+        res.submit_detail_name = detail_code_name(st.detail)
+        if rc != p.PROM_OK:
+            res.outcome = f"error({res.submit_stage},{st.detail})"
+            raise AsyncValidationError(f"async submit failed: stage={res.submit_stage} detail={st.detail}", res)
+        last = None
+        for attempt in range(1, 2001):
+            qrc, last = rt.query_async(task)
+            res.query_attempts = attempt
+            if qrc != p.PROM_OK:
+                res.outcome = "error(query,-1)"
+                raise AsyncValidationError(f"async query failed with status {qrc}", res)
+            res.query_lifecycle = async_lifecycle_name(last.lifecycle_state)
+            res.query_ready = bool(last.ready)
+            res.query_failed = bool(last.failed)
+            res.query_consumed = bool(last.consumed)
+            res.query_outstanding = int(last.outstanding_tasks)
+            if last.lifecycle_state in (2, 3):
+                break
+        if last is None or last.lifecycle_state != 2:
+            detail = last.detail_code if last is not None else 0
+            res.outcome = f"error(query,{detail})"
+            res.notes = "async task did not reach ready state"
+            raise AsyncValidationError(f"async task did not reach ready state: lifecycle={res.query_lifecycle} "
+                                       f"detail={detail}", res)
+        out = np.zeros(shape.m * shape.n, dtype=np.float32)
+        crc, cst = rt.consume_async(task, out)
+        res.consume_stage = p.stage_name(cst.stage)
+        res.consume_detail_code = cst.detail
+        res.consume_detail_name = detail_code_name(cst.detail)
+        if crc != p.PROM_OK:
+            res.outcome = f"error({res.consume_stage},{cst.detail})"
+            raise AsyncValidationError(f"async consume failed: stage={res.consume_stage} detail={cst.detail}", res)
+    res.correctness = compare_against_oracle(reference, out)
+    if not res.correctness.passed:
+        res.outcome = "error(correctness,-1)"
+        raise AsyncValidationError("async correctness gate failed", res)
+    res.outcome = "ok"
+    return res
+
+
+def async_validation_to_octagon(r: AsyncValidationResult) -> octagon.Record:
+    """runtime.go:525-566 (asyncValidationToOctagon)."""
+    return octagon.Record("PrometheusAsyncValidation", [
+        ("BackendRequested", r.requested_backend), ("BackendUsed", r.used_backend),
+        ("M", int(r.shape.m)), ("N", int(r.shape.n)), ("K", int(r.shape.k)),
+        ("Outcome", r.outcome), ("Environment", r.environment),
+        ("SubmitStage", r.submit_stage), ("SubmitDetailCode", int(r.submit_detail_code)),
+        ("SubmitDetailName", r.submit_detail_name),
+        ("QueryLifecycle", r.query_lifecycle), ("QueryReady", r.query_ready), ("QueryFailed", r.query_failed),
+        ("QueryConsumed", r.query_consumed), ("QueryOutstanding", int(r.query_outstanding)),
+        ("QueryAttempts", int(r.query_attempts)),
+        ("ConsumeStage", r.consume_stage), ("ConsumeDetailCode", int(r.consume_detail_code)),
+        ("ConsumeDetailName", r.consume_detail_name),
+        *_correctness_fields(r.correctness),
+        ("WallTimeNs", int(r.wall_time_ns)), ("Notes", r.notes)])
+
+
+def write_async_validation_octagon(path: str, result: AsyncValidationResult, prefix: str = "") -> str:
+    """runtime.go:521-523 (WriteAsyncValidationOctagon)."""
+    return octagon.write(path, async_validation_to_octagon(result), prefix)
