@@ -1,0 +1,127 @@
+"""The FFT engine (internal/fft/fft.go:13-258, internal/prometheus/fft.go:1-55)
+on the CPU.
+
+The engine's CPU transform is checked bit for bit against the C restatement
+of fft.go in the oracle (same twiddle formula and libm, every operation
+rounded on its own) and against numpy.fft within fft.go's agreement rule.
+Go's own math.Cos/Sin are not glibc's, so the reference's twiddles may differ
+from these in the last bit; both are within an ulp of the true value, which
+the roots test checks against numpy's (correctly rounded at these angles to
+within an ulp).
+Backend selection is exercised with stand-in backends (instant and exact,
+inaccurate, failing) and with the reactor forced unavailable.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from oct_amd import fft_engine as fe
+from oct_amd import prometheus as p
+
+
+def _values(n, seed=7):
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal(n) + 1j * rng.standard_normal(n)
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 8, 64, 1024, 4096])
+def test_cpu_transform_is_bit_identical_to_the_restated_reference(n):
+    x = _values(n)
+    r = fe.roots(n)
+    np.testing.assert_array_equal(r, oracle.fft64_roots(n))
+    a = -2.0 * np.pi / n * np.arange(n // 2)
+    np.testing.assert_array_max_ulp(r.real, np.cos(a), maxulp=1)
+    np.testing.assert_array_max_ulp(r.imag, np.sin(a), maxulp=1)
+    got = fe.cpu(x)
+    want = oracle.fft64(x)
+    assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
+
+
+@pytest.mark.parametrize("n", [2 ** 14, 2 ** 17])
+def test_cpu_transform_agrees_with_numpy(n):
+    x = _values(n, 3)
+    assert fe.agrees(np.fft.fft(x), fe.cpu(x))
+
+
+def test_validation_texts():
+    with pytest.raises(fe.FFTError, match="^runtime error: FFT requires non-empty input$"):
+        fe.validate(0)
+    with pytest.raises(fe.FFTError, match="^runtime error: FFT requires power-of-two input length$"):
+        fe.validate(12)
+    fe.validate(1)
+
+
+class Instant:
+    """A backend that returns a prepared answer at once."""
+
+    def __init__(self, answer, fail_after=None):
+        self.answer, self.calls, self.fail_after = answer, 0, fail_after
+
+    def transform(self, values):
+        self.calls += 1
+        if self.fail_after is not None and self.calls > self.fail_after:
+            raise fe.FFTError("device lost")
+        return self.answer.copy()
+
+    def close(self):
+        pass
+
+
+def test_strict_without_a_device_is_an_error(monkeypatch):
+    monkeypatch.setenv(p.REACTOR_TEST_FLAGS_ENV_VAR, str(p.TESTCFG_SKIP_VULKAN_INIT))
+    with fe.FFTEngine() as eng:
+        with pytest.raises(fe.FFTError, match="^PROMETHEUS FFT requires GPU execution: "):
+            eng.transform(_values(16), required_gpu=True)
+
+
+def test_automatic_without_a_device_runs_the_cpu_and_says_why(monkeypatch):
+    monkeypatch.setenv(p.REACTOR_TEST_FLAGS_ENV_VAR, str(p.TESTCFG_SKIP_VULKAN_INIT))
+    x = _values(256)
+    with fe.FFTEngine() as eng:
+        out = eng.transform(x, required_gpu=False)
+        m = eng.measurement()
+    np.testing.assert_array_equal(out, fe.cpu(x))
+    assert (m.elements, m.selected) == (256, "cpu") and "probe failed" in m.reason and m.cpu_warm_ns > 0
+
+
+def test_automatic_selects_a_faster_exact_backend_and_falls_back_when_it_fails():
+    x = _values(4096)
+    ref = fe.cpu(x)
+    backend = Instant(ref)
+    with fe.FFTEngine(new_backend=lambda: backend) as eng:
+        out = eng.transform(x, required_gpu=False)
+        m = eng.measurement()
+        assert m.selected == "vulkan-fp64" and m.reason == "warm GPU call exceeds 20 percent speedup margin"
+        assert m.gpu_warm_ns < m.cpu_warm_ns * 4 // 5
+        np.testing.assert_array_equal(out, ref)
+        calls = backend.calls
+        eng.transform(x, required_gpu=False)  # the same length: the selected backend
+        assert backend.calls == calls + 1
+        backend.fail_after = backend.calls
+        out = eng.transform(x, required_gpu=False)
+        m = eng.measurement()
+        assert m.selected == "cpu" and m.reason == "GPU execution failed: device lost"
+        np.testing.assert_array_equal(out, ref)
+
+
+def test_automatic_rejects_an_inaccurate_backend():
+    x = _values(1024)
+    ref = fe.cpu(x)
+    wrong = ref.copy()
+    wrong[5] += 1e-9 * np.max(np.abs(ref))
+    with fe.FFTEngine(new_backend=lambda: Instant(wrong)) as eng:
+        out = eng.transform(x, required_gpu=False)
+        assert eng.measurement().reason == "GPU calibration did not preserve binary64 accuracy"
+    np.testing.assert_array_equal(out, ref)
+
+
+def test_strict_uses_the_backend_and_a_new_length_resets_the_measurement():
+    x = _values(512)
+    ref = fe.cpu(x)
+    with fe.FFTEngine(new_backend=lambda: Instant(ref)) as eng:
+        eng.transform(x, required_gpu=False)
+        assert eng.measurement().elements == 512
+        np.testing.assert_array_equal(eng.transform(_values(256), required_gpu=True), ref)
+        assert eng.measurement().elements == 0

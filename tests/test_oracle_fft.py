@@ -103,6 +103,18 @@ def test_roots_table():
     np.testing.assert_allclose(tw, np.exp(-2j * np.pi * np.arange(n // 2) / n), rtol=0, atol=2e-16)
 
 
+@pytest.mark.parametrize("n", [4096, 1 << 14])
+def test_roots_are_two_libm_calls(n):
+    """The table is cos(a) and sin(a) from two libm calls, as the reactor's
+    host code computes it; at these sizes glibc's sincos differs from them in
+    the last bit for at least one angle, so a build that merges the pair fails."""
+    import math
+
+    step = -2.0 * math.pi / n
+    want = np.array([complex(math.cos(step * j), math.sin(step * j)) for j in range(n // 2)])
+    assert np.array_equal(oracle.fft64_roots(n).view(np.uint64), want.view(np.uint64))
+
+
 def test_agreement_rule_catches_planted_errors():
     rng = np.random.default_rng(5)
     x = rng.standard_normal(256) + 1j * rng.standard_normal(256)
