@@ -21,6 +21,12 @@ hands over to is ``oct_amd.prometheus.run_compiled_matmul_mm_strict``
 The CPU evaluation outside ``PROMETHEUS`` belongs to the caller's interpreter:
 the functions here take it as a callable and never compute a product
 themselves.
+
+The ``FFT`` builtin is routed the same way in both lanes: inside
+``PROMETHEUS`` the engine must run it on the GPU, outside it selects by
+measurement (``oct_amd.fft_engine``).  Unlike a strict product, an FFT
+failure is a recoverable Oct error value, not a terminal runtime error
+(interpret.go:3464-3486, emit_go_runtime.go:715-721).
 """
 from __future__ import annotations
 
@@ -28,6 +34,9 @@ import sys
 from dataclasses import dataclass, field
 from typing import Callable, List, Optional, Sequence, TextIO, Tuple
 
+import numpy as np
+
+from . import fft_engine as fe
 from . import prometheus as p
 from . import runtime as rt
 
@@ -35,15 +44,20 @@ from . import runtime as rt
 VALUE_INT = "Int"
 VALUE_FLOAT = "Float"
 VALUE_MATRIX = "Matrix"
+VALUE_COMPLEX = "Complex"
+VALUE_ARRAY = "Array"
 
 
 @dataclass
 class Value:
-    """A boxed interpreter value: a scalar or a row-major matrix of values."""
+    """A boxed interpreter value: a scalar, a complex number, an array of
+    values or a row-major matrix of values."""
 
     kind: str
     number: float = 0.0
     matrix: Optional["MatrixValue"] = None
+    complex_value: complex = 0j
+    array: Optional[List["Value"]] = None
 
 
 @dataclass
@@ -146,6 +160,45 @@ def eval_prometheus_matmul_call(in_prometheus: bool, type_arguments: Sequence[st
     return multiply(left, right)
 
 
+@dataclass
+class EvalResult:
+    """An evaluation's outcome: a value, or a recoverable Oct error value
+    (the interpreter's ``evalResult{hasError, errorVal}``)."""
+
+    value: Optional[Value] = None
+    error: Optional[str] = None
+
+
+def complex_array(values) -> Value:
+    """A Complex[] value."""
+    return Value(VALUE_ARRAY, array=[Value(VALUE_COMPLEX, complex_value=complex(z)) for z in values])
+
+
+def eval_fft_call(engine: "fe.FFTEngine", in_prometheus: bool, type_arguments: Sequence[str],
+                  arguments: Sequence[Value]) -> EvalResult:
+    """interpret.go:3464-3486 with the argument evaluated, and
+    interpret/fft.go:10-29: the Complex[] argument goes to the engine in
+    binary64, GPU-required inside PROMETHEUS; an engine error (validation,
+    GPU unavailable or failed) becomes a recoverable error value."""
+    if type_arguments:
+        raise StrictDispatchError("runtime invariant violation: FFT does not accept type arguments")
+    if len(arguments) != 1:
+        raise StrictDispatchError("runtime invariant violation: FFT expects 1 argument")
+    argument = arguments[0]
+    if argument.kind != VALUE_ARRAY or argument.array is None:
+        raise StrictDispatchError("runtime invariant violation: FFT expects Complex[] argument")
+    values = np.empty(len(argument.array), dtype=np.complex128)
+    for index, entry in enumerate(argument.array):
+        if entry.kind != VALUE_COMPLEX:
+            raise StrictDispatchError("runtime invariant violation: FFT expects Complex[] input")
+        values[index] = entry.complex_value
+    try:
+        out = engine.transform(values, required_gpu=in_prometheus)
+    except fe.FFTError as exc:
+        return EvalResult(error=str(exc))
+    return EvalResult(value=complex_array(out))
+
+
 # ---- compiler decisions (internal/build) ------------------------------------
 def parse_matrix_elem_type(type_name: str) -> Optional[str]:
     """lower_expr.go:3154-3156: ``Matrix<E>`` -> ``E``, else None."""
@@ -219,3 +272,37 @@ def oct_prometheus_matmul_mm(left: Sequence[Sequence[float]], right: Sequence[Se
     if err is not None:
         raise RuntimeError(f"PrometheusMatMulMM failed: {err}") from err
     return out
+
+
+def lower_fft_call(in_prometheus: bool, argument_types: Sequence[str]) -> Tuple[str, str]:
+    """lower_expr.go:2598-2603 and 3320-3327 for ``FFT(x)``: (callee, result
+    type); the GPU-required callee inside PROMETHEUS."""
+    if len(argument_types) != 1:
+        raise StrictDispatchError(f"function 'FFT' expects 1 arguments, got {len(argument_types)}")
+    if argument_types[0] != "Complex[]":
+        raise StrictDispatchError(f"compiled mode does not yet support builtin FFT for type {argument_types[0]}")
+    return ("FFTGPU" if in_prometheus else "FFT"), "Complex[]"
+
+
+@dataclass
+class ComplexSliceResult:
+    """The compiled program's ``octResult_ComplexSlice``."""
+
+    value: Optional[np.ndarray] = None
+    err: str = ""
+    is_err: bool = False
+
+
+def new_fft_engine() -> "fe.FFTEngine":
+    """internal/prometheus/fft.go:19 (``NewFFTEngine``): the compiled
+    program's one engine, closed when its main returns (emit_go.go:793-794)."""
+    return fe.FFTEngine()
+
+
+def oct_fft(engine: "fe.FFTEngine", values, required_gpu: bool) -> ComplexSliceResult:
+    """emit_go_runtime.go:715-721 (``__octFFT``): the engine's result or its
+    error as a recoverable result value."""
+    try:
+        return ComplexSliceResult(value=engine.transform(values, required_gpu))
+    except fe.FFTError as exc:
+        return ComplexSliceResult(err=str(exc), is_err=True)

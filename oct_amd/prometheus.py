@@ -1120,14 +1120,22 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     raise ReactorIssue("reactor_not_found", "prometheus reactor not found")
 
 
-_SHARED_LIB: Optional[ctypes.CDLL] = None
+_LOADED: dict = {}
 
 
 def shared_library() -> ctypes.CDLL:
-    global _SHARED_LIB
-    if _SHARED_LIB is None:
-        _SHARED_LIB = load_library()
-    return _SHARED_LIB
+    """The reactor that discovery names now.  The reference resolves the path
+    on every runtime open (bridge.go:552-582), so a changed
+    $OCT_PROMETHEUS_REACTOR takes effect at the next open; each path is
+    loaded and bound once per process, as a repeated dlopen of one path
+    returns the same handle."""
+    for cand in discover_reactor_candidates():
+        lib = _LOADED.get(cand)
+        if lib is not None:
+            return lib
+    lib = load_library()
+    _LOADED[lib._oct_path] = lib
+    return lib
 
 
 def _ptr(arr: Optional[np.ndarray]) -> Optional[int]:

@@ -487,7 +487,6 @@ def test_strict_path_raises_without_device(monkeypatch):
 def test_strict_path_missing_library_is_an_error(monkeypatch, tmp_path):
     # Language/Prometheus/unavailable/matrix.octfail: no CPU substitute when the reactor is absent
     monkeypatch.setenv(p.REACTOR_ENV_VAR, str(tmp_path / "missing" / p.LIBRARY_BASENAME))
-    monkeypatch.setattr(p, "_SHARED_LIB", None)
     with pytest.raises(p.ReactorIssue, match="PROMETHEUS requires GPU matrix execution"):
         p.run_compiled_matmul_mm_strict([[1.0]], [[1.0]])
 
