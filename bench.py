@@ -279,7 +279,7 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: A,B ~ U[-1,1] (numpy PCG64 seeds 11,12), fp32 row-major, resident in HBM",
         "config": {"workload": "sgemm_f32 C=A@B M=N=K=4096 row-major (BASELINE configs[1])", "m": n, "n": n, "k": n,
-                   "kernel": "sgemm_f32_dl128w8_kernel (v_mfma_f32_32x32x2_f32, 128x128x16 tiles loaded HBM->LDS directly, 8 waves of 32x64, 5 workgroups per CU)"},
+                   "kernel": "sgemm_f32_dl128w8_kernel (v_mfma_f32_32x32x2_f32, 128x128x16 tiles loaded HBM->LDS directly, 8 waves of 32x64, 3 workgroups per CU)"},
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 3),

@@ -504,7 +504,10 @@ __global__ __launch_bounds__(256, 3) void sgemm_f32_dl256_kernel(const float* __
 
 // 128x128 with eight waves (each 32x64, 50 VGPRs): two waves per SIMD even
 // when the grid gives one workgroup per CU (small and split-K products), and
-// five workgroups per CU (LDS-bound) on large grids.
+// three workgroups per CU on large grids (106 SGPRs, the residual epilogue's
+// row offsets among them, allow seven waves per SIMD).  Two or four
+// workgroups per CU measured the same at 4096^3 (921 us), four 4 % slower
+// at 8192 x 8192 x 2048.
 __global__ __launch_bounds__(512, 1) void sgemm_f32_dl128w8_kernel(const float* __restrict__ A,
                                                                    const float* __restrict__ B, float* C, int M,
                                                                    int N, int K, int tiles_m, int tiles_n, int lda,
