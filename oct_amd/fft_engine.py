@@ -138,7 +138,10 @@ class ReactorFFTBackend:
         try:
             self.runtime.require_hardware_gpu()
             if not hasattr(self.runtime.lib, "prometheus_reactor_runtime_fft64"):
-                raise FFTError("reactor lacks a binary64 FFT adapter")
+                # bridge_dlopen_linux.go:234: dlsym's error (glibc's dlerror wording)
+                path = getattr(self.runtime.lib, "_oct_path", "")
+                raise FFTError(f"dlsym prometheus_reactor_runtime_fft64: {path}: undefined symbol: "
+                               "prometheus_reactor_runtime_fft64")
         except Exception:
             self.runtime.close()
             raise
