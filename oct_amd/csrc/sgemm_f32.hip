@@ -820,31 +820,46 @@ __global__ __launch_bounds__(512, 1) void sgemm_f32_dl64_ring_kernel(const float
 // any alignment), zero outside: the padded copies through which operands the
 // direct-to-LDS kernels cannot read (ragged k or n, unaligned rows) reach them.
 // One launch pads both operands: the first blocks_a workgroups copy A, the
-// rest B, one 16-byte group per thread (rows_d * ld_d / 4 < 2^31: the GEMM
-// admission bounds m*k and k*n below 2^32).
+// rest B.  A workgroup's four waves take four consecutive rows and one
+// 256-float chunk of them (pad_blocks per job); lane l moves floats l, l + 64,
+// l + 128 and l + 192 of the chunk, so each load and store instruction covers
+// 256 contiguous bytes of its row on either side (rows_d * ld_d < 2^32 and
+// the block count < 2^22: the GEMM admission bounds m*k and k*n below 2^32).
 struct PadJob {
   const float* src;
   float* dst;
   int rows_s, cols_s, ld_s, rows_d, ld_d;
 };
 
+constexpr uint32_t kPadChunk = 256;
+
+uint32_t pad_blocks(uint32_t rows_d, uint32_t ld_d) {
+  return ((rows_d + 3u) / 4u) * ((ld_d + kPadChunk - 1u) / kPadChunk);
+}
+
 __global__ __launch_bounds__(256) void pack_pad_kernel(PadJob ja, PadJob jb, uint32_t blocks_a) {
   const bool first = blockIdx.x < blocks_a;
   const PadJob j = first ? ja : jb;
-  const uint32_t i = (first ? blockIdx.x : blockIdx.x - blocks_a) * 256u + threadIdx.x;
-  const uint32_t c4n = (uint32_t)j.ld_d >> 2;
-  if (i >= (uint32_t)j.rows_d * c4n) return;
-  const int r = (int)(i / c4n);
-  const int c = (int)(i - (uint32_t)r * c4n) * 4;
-  floatx4 v = {0.f, 0.f, 0.f, 0.f};
-  if (r < j.rows_s) {
-    const float* sp = j.src + (size_t)r * j.ld_s + c;
-    if (c + 0 < j.cols_s) v.x = sp[0];
-    if (c + 1 < j.cols_s) v.y = sp[1];
-    if (c + 2 < j.cols_s) v.z = sp[2];
-    if (c + 3 < j.cols_s) v.w = sp[3];
+  const uint32_t blk = first ? blockIdx.x : blockIdx.x - blocks_a;
+  const uint32_t chunks = ((uint32_t)j.ld_d + kPadChunk - 1u) / kPadChunk;
+  const uint32_t group = blk / chunks;
+  const int r = (int)(group * 4u + (threadIdx.x >> 6));
+  if (r >= j.rows_d) return;
+  const int c0 = (int)((blk - group * chunks) * kPadChunk + (threadIdx.x & 63u));
+  const bool row_in = r < j.rows_s;
+  const float* sp = j.src + (row_in ? (size_t)r * j.ld_s : 0);
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = c0 + 64 * q;
+    v[q] = (row_in && c < j.cols_s) ? sp[c] : 0.0f;
   }
-  reinterpret_cast<floatx4*>(j.dst + (size_t)r * j.ld_d)[c >> 2] = v;
+  float* dp = j.dst + (size_t)r * j.ld_d;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = c0 + 64 * q;
+    if (c < j.ld_d) dp[c] = v[q];
+  }
 }
 
 // y[m] = A[m,:] . x : one wave per row, 4 rows per workgroup.  HBM-bound:
@@ -1260,8 +1275,8 @@ hipError_t run_sgemm_schedule(const SgemmSchedule& s, const float* a, int lda, c
     if (pa == nullptr || pb == nullptr) return hipErrorOutOfMemory;
     const PadJob ja{a, pa, (int)m, (int)k, lda, (int)m, (int)s.k4};
     const PadJob jb{b, pb, (int)k, (int)n, ldb, (int)s.k4, (int)s.n4};
-    const uint32_t blocks_a = (uint32_t)(((uint64_t)m * (s.k4 / 4) + 255) / 256);
-    const uint32_t blocks_b = (uint32_t)(((uint64_t)s.k4 * (s.n4 / 4) + 255) / 256);
+    const uint32_t blocks_a = pad_blocks(m, s.k4);
+    const uint32_t blocks_b = pad_blocks(s.k4, s.n4);
     hipLaunchKernelGGL(pack_pad_kernel, dim3(blocks_a + blocks_b), dim3(256), 0, stream, ja, jb, blocks_a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
