@@ -72,6 +72,13 @@ enum {
   PROM_TESTCFG_SKIP_VULKAN_INIT = 1u << 7,
   /* An async query observes a failure for every submitted task. */
   PROM_TESTCFG_FAIL_ASYNC_POLL = 1u << 15,
+  /* The recorded work fails to end / to be submitted: the synchronous SGEMM
+     fails at stage SUBMIT with detail -4 (reactor_sgemm.cpp:5071-5078), the
+     binary64 FFT with PROM_FFT_DETAIL_DISPATCH_FAILED
+     (PrometheusFft.concept:171, reactor_concept_fft.cpp:63-70); nothing is
+     queued and no output is written. */
+  PROM_TESTCFG_FAIL_COMMAND_END = 1u << 20,
+  PROM_TESTCFG_FAIL_QUEUE_SUBMIT = 1u << 22,
 };
 
 /* reactor_api.h:227-324 (subset) */

@@ -811,19 +811,32 @@ PROM_REACTOR_API int prometheus_reactor_runtime_fft64(void* handle, const double
   double2* din = static_cast<double2*>(staging(0, bytes));
   double2* dout = static_cast<double2*>(staging(1, bytes));
   double2* dtmp = count > kFftMaxLds ? static_cast<double2*>(staging(3, bytes)) : nullptr;
-  if (roots == nullptr || din == nullptr || dout == nullptr || (count > kFftMaxLds && dtmp == nullptr)) {
+  // Injected faults (reactor_api.h:131-166) in the order the reference's FFT
+  // executor meets them (PrometheusFft.concept:135-176): allocation, upload,
+  // dispatch (a command that fails to end or to be submitted is a dispatch
+  // failure there), readback.  An injected failure writes no output.
+  const uint32_t tf = rt->test_flags;
+  if ((tf & PROM_TESTCFG_FAIL_BUFFER_ALLOC) != 0u || roots == nullptr || din == nullptr || dout == nullptr ||
+      (count > kFftMaxLds && dtmp == nullptr)) {
     set_status(stage, detail, PROM_STAGE_INIT, PROM_FFT_DETAIL_ALLOCATION_FAILED);
     return PROM_ERROR;
   }
-  if (upload_host(din, input, bytes, cx.stream) != hipSuccess) {
+  if ((tf & PROM_TESTCFG_FAIL_UPLOAD) != 0u || upload_host(din, input, bytes, cx.stream) != hipSuccess) {
     (void)hipGetLastError();
+    (void)hipStreamSynchronize(cx.stream);
     set_status(stage, detail, PROM_STAGE_TRANSFER_IN, PROM_FFT_DETAIL_UPLOAD_FAILED);
     return PROM_ERROR;
   }
-  if (launch_fft64(din, dout, dtmp, roots, count, cx.stream) != hipSuccess) {
+  if ((tf & (PROM_TESTCFG_FAIL_DISPATCH | PROM_TESTCFG_FAIL_COMMAND_END | PROM_TESTCFG_FAIL_QUEUE_SUBMIT)) != 0u ||
+      launch_fft64(din, dout, dtmp, roots, count, cx.stream) != hipSuccess) {
     (void)hipGetLastError();
     (void)hipStreamSynchronize(cx.stream);
     set_status(stage, detail, PROM_STAGE_SUBMIT, PROM_FFT_DETAIL_DISPATCH_FAILED);
+    return PROM_ERROR;
+  }
+  if ((tf & PROM_TESTCFG_FAIL_DOWNLOAD) != 0u) {
+    (void)hipStreamSynchronize(cx.stream);
+    set_status(stage, detail, PROM_STAGE_TRANSFER_OUT, PROM_FFT_DETAIL_READBACK_FAILED);
     return PROM_ERROR;
   }
   if (download_host(output, dout, bytes, cx.stream) != hipSuccess ||

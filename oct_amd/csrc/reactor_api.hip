@@ -85,6 +85,11 @@ int gemm_host(void* handle, const TIn* a, const TIn* b, float* c, uint32_t m, ui
     set_status(out_stage, out_detail, PROM_STAGE_SUBMIT, PROM_DETAIL_INJECTED_DISPATCH_FAILURE);
     return PROM_ERROR;
   }
+  if (rt->test_flags & (PROM_TESTCFG_FAIL_COMMAND_END | PROM_TESTCFG_FAIL_QUEUE_SUBMIT)) {
+    (void)hipStreamSynchronize(cx.stream);
+    set_status(out_stage, out_detail, PROM_STAGE_SUBMIT, -4);  // VK_ERROR_DEVICE_LOST, reactor_sgemm.cpp:5071-5078
+    return PROM_ERROR;
+  }
   int path = 0;
   if (launch(da, db, dc, m, n, k, cx.stream, &path) != hipSuccess) {
     (void)hipStreamSynchronize(cx.stream);

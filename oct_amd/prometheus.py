@@ -46,6 +46,8 @@ TESTCFG_FAIL_DISPATCH = 1 << 4
 TESTCFG_FAIL_DOWNLOAD = 1 << 5
 TESTCFG_SKIP_VULKAN_INIT = 1 << 7
 TESTCFG_FAIL_ASYNC_POLL = 1 << 15
+TESTCFG_FAIL_COMMAND_END = 1 << 20
+TESTCFG_FAIL_QUEUE_SUBMIT = 1 << 22
 DETAIL_INJECTED_UPLOAD_FAILURE = -6001
 DETAIL_INJECTED_DISPATCH_FAILURE = -6002
 DETAIL_INJECTED_DOWNLOAD_FAILURE = -6003
