@@ -1195,13 +1195,18 @@ class NativeRuntime:
         return bool(self.caps.available)
 
     def require_hardware_gpu(self) -> None:
-        """fft.go:50-55: strict execution requires a hardware device (backend 2)."""
+        """internal/prometheus/fft.go:50-55: strict execution requires an
+        available hardware device (backend 2), with the reference's error text."""
         if not self.caps.available or self.caps.backend_type != PROM_BACKEND_HARDWARE_GPU:
-            raise ReactorIssue("unavailable", f"hardware GPU unavailable (backend={self.caps.backend_type}, "
-                                              f"reason={self.caps.reason_code})")
+            raise ReactorIssue("unavailable", f"GPU execution requires hardware Vulkan; backend is {self.environment()}")
 
     def environment(self) -> str:
-        return "hardware_gpu_hip" if self.caps.backend_type == PROM_BACKEND_HARDWARE_GPU else "unknown"
+        """bridge.go:518-533, with this library's name for the hardware backend."""
+        if self.caps.backend_type == PROM_BACKEND_HARDWARE_GPU:
+            return "hardware_gpu_hip"
+        if self.caps.backend_type == 3:
+            return "software_vulkan_llvmpipe_or_cpu"
+        return "unknown"
 
     def device_diagnostics(self) -> PrometheusHipDeviceDiagnostics:
         d = PrometheusHipDeviceDiagnostics()

@@ -3,7 +3,10 @@ ReactorIssue path of bridge.go:242-394.
 
 Small stand-in reactor libraries are compiled from C in the test's temporary
 directory so each failure can be forced: no abi symbol, a wrong ABI version,
-a create that fails, a probe that succeeds but no sgemm.  The real library
+a create that fails, a probe that succeeds but no sgemm; the reference's
+own bridge tests (bridge_test.go:8-57: a missing symbol and an ABI mismatch
+reported as structured issues, a stub library that loads and probes) are
+among these cases.  The real library
 with the SKIP_VULKAN_INIT test flag forces the probe-unavailable path on any
 machine, as bridge.go's reactorTestFlagsFromEnv (bridge.go:584-594) passes
 the flag through.

@@ -9,7 +9,9 @@ from these in the last bit; both are within an ulp of the true value, which
 the roots test checks against numpy's (correctly rounded at these angles to
 within an ulp).
 Backend selection is exercised with stand-in backends (instant and exact,
-inaccurate, failing) and with the reactor forced unavailable.
+inaccurate, failing) and with the reactor forced unavailable, and the
+reference's own engine tests (internal/fft/fft_test.go, with a counting
+backend) and admission test (internal/prometheus/fft_test.go) are mirrored.
 """
 from __future__ import annotations
 
@@ -125,3 +127,78 @@ def test_strict_uses_the_backend_and_a_new_length_resets_the_measurement():
         assert eng.measurement().elements == 512
         np.testing.assert_array_equal(eng.transform(_values(256), required_gpu=True), ref)
         assert eng.measurement().elements == 0
+
+
+# ---- the reference's own engine tests (internal/fft/fft_test.go:9-100) ------
+class Counted:
+    """fft_test.go:9-21: a backend that counts calls and closes and returns the
+    CPU transform, or fails with a set error."""
+
+    def __init__(self, err=None):
+        self.calls, self.closed, self.err = 0, 0, err
+
+    def transform(self, values):
+        self.calls += 1
+        if self.err is not None:
+            raise fe.FFTError(self.err)
+        return fe.cpu(values)
+
+    def close(self):
+        self.closed += 1
+
+
+def test_forced_execution_bypasses_calibration_and_propagates_failure():
+    backend = Counted()
+    eng = fe.FFTEngine(new_backend=lambda: backend)
+    eng.transform([1, 2], required_gpu=True)
+    assert backend.calls == 1 and eng.measurement().cpu_warm_ns == 0
+    backend.err = "device lost"
+    with pytest.raises(fe.FFTError, match="device lost"):
+        eng.transform([1, 2], required_gpu=True)
+    eng.close()
+    assert backend.closed == 1
+
+
+def test_automatic_selection_records_measured_calls_and_caches_decision():
+    backend = Counted()
+    with fe.FFTEngine(new_backend=lambda: backend) as eng:
+        eng.transform([1, 2, 3, 4], required_gpu=False)
+        m = eng.measurement()
+        assert m.cpu_warm_ns > 0 and m.gpu_warm_ns > 0 and m.reason
+        calls = backend.calls
+        eng.transform([1, 2, 3, 4], required_gpu=False)
+        assert backend.calls <= calls + 1  # the same shape is not recalibrated
+        eng.transform([1, 2], required_gpu=True)
+        assert eng.measurement().elements == 0  # a forced shape change drops the warm decision
+
+
+def test_automatic_failure_is_inspectable_and_forced_failure_remains_an_error():
+    with fe.FFTEngine(new_backend=lambda: Counted(err="shaderFloat64 unavailable")) as eng:
+        out = eng.transform([1, 2], required_gpu=False)
+        assert out.size == 2 and "shaderFloat64 unavailable" in eng.measurement().reason
+        with pytest.raises(fe.FFTError):
+            eng.transform([1, 2], required_gpu=True)
+
+
+def test_invalid_input_does_not_dispatch():
+    backend = Counted()
+    with fe.FFTEngine(new_backend=lambda: backend) as eng:
+        for values in ([], [1, 2, 3]):
+            with pytest.raises(fe.FFTError):
+                eng.transform(values, required_gpu=True)
+    assert backend.calls == 0
+
+
+def test_strict_gpu_admission_rejects_software_and_unavailable_backends():
+    """internal/prometheus/fft_test.go:5-15."""
+    def runtime_with(available, backend_type):
+        rt = object.__new__(p.NativeRuntime)
+        rt.caps = p.PrometheusCaps(available, backend_type, 0)
+        return rt
+
+    for available, backend_type in ((0, 2), (1, 3), (1, 0)):
+        with pytest.raises(p.ReactorIssue) as err:
+            runtime_with(available, backend_type).require_hardware_gpu()
+        assert err.value.message.startswith("GPU execution requires hardware Vulkan; backend is ")
+    runtime_with(1, 2).require_hardware_gpu()
+    assert runtime_with(1, 3).environment() == "software_vulkan_llvmpipe_or_cpu"
