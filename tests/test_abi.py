@@ -155,6 +155,38 @@ def test_layouts_equal_the_reference_header(tmp_path):
     assert not diff, diff
 
 
+def _constant_values(tmp_path, header: Path, names, tag: str) -> dict:
+    lines = ["#include <stdio.h>", f'#include "{header}"', "int main(void){"]
+    lines += [f'printf("{n} %lld\\n", (long long)({n}));' for n in names]
+    lines.append("return 0;}")
+    src = tmp_path / f"const_{tag}.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / f"const_{tag}"
+    subprocess.run(["gcc", "-std=c11", "-w", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    return dict(line.rsplit(" ", 1) for line in out.splitlines())
+
+
+@pytest.mark.skipif(not REFERENCE_HEADER.exists(), reason="reference tree not present on this machine")
+def test_constants_equal_the_reference_header(tmp_path):
+    """Every enum value and macro this header shares by name with the
+    reference's (status, stage and detail codes, fault-injection bits, limits)
+    has the reference's value, evaluated by the C compiler in both headers."""
+    pattern = re.compile(r"^\s*(PROM_[A-Z0-9_]+)\s*=|^#define\s+(PROM_[A-Z0-9_]+)\s+\S", re.M)
+
+    def names(text):
+        return {a or b for a, b in pattern.findall(text)}
+
+    ours_text = HEADER.read_text()
+    ref_text = REFERENCE_HEADER.read_text()
+    shared = sorted((names(ours_text) & names(ref_text)) - {"PROM_REACTOR_API"})  # the export attribute
+    assert len(shared) > 100
+    ours = _constant_values(tmp_path, HEADER, shared, "ours")
+    ref = _constant_values(tmp_path, REFERENCE_HEADER, shared, "ref")
+    diff = {k: (ours[k], ref[k]) for k in shared if ours[k] != ref[k]}
+    assert not diff, diff
+
+
 def test_ctypes_layouts_match_c_header(tmp_path):
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){"]
     for name, cls in STRUCTS.items():
