@@ -14,8 +14,6 @@ import pytest
 import oracle
 from oct_amd import prometheus as p
 
-pytestmark = pytest.mark.gpu
-
 CASES = [  # gemma4e2b_sgemm_corpus_test.go:44-59
     ("m1_n256_k1536", 1, 256, 1536),
     ("m2_n256_k1536", 2, 256, 1536),
@@ -57,6 +55,7 @@ def test_generators_first_values():
     assert np.all(np.abs(b - (np.array([-63, -34, -5], np.float32) / np.float32(37))) <= 2.0 ** -8)
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("name,m,n,k", CASES, ids=[c[0] for c in CASES])
 def test_small_m_production_corpus(gpu_runtime, name, m, n, k):
     a = deterministic_corpus_fp32(m * k).reshape(m, k)
